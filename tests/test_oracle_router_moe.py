@@ -1,0 +1,215 @@
+"""Pin the oracle's router, activations and MoE layer.
+
+Known answers come from the reference's own tests:
+  * crates/hawking-core/tests/moe_topk_gate_exact_ties_parity.rs:76-155 (planted ties)
+  * crates/hawking-core/src/moe.rs:143-155 (topk_picks_largest)
+  * crates/hawking-core/src/gravity_glm.rs:3664-3667 (topk_desc ties -> lower index)
+The layer itself is checked against its FP64 authority and against closed
+forms (zero experts, identical experts, top_k = n_experts).
+"""
+import numpy as np
+import pytest
+
+
+def _tie_fixture_boundary():
+    logits = np.full(128, -3.0, np.float32)
+    logits[:12] = 5.0
+    logits[20:28] = 1.0
+    logits[40] = 2.0
+    for i in range(50, 128):
+        logits[i] = -1.0 - (i % 17) * 0.01
+    return logits
+
+
+def _tie_fixture_interior():
+    logits = np.full(128, -4.0, np.float32)
+    for rank, idx in enumerate([90, 10, 50, 3, 70]):
+        logits[idx] = 10.0 - rank
+    for idx in (100, 25, 110, 15):
+        logits[idx] = 4.0
+    return logits
+
+
+TIE_CASES = [
+    ("boundary-ties-128x8", _tie_fixture_boundary, 8, list(range(8))),
+    ("interior-ties-128x8", _tie_fixture_interior, 8, [90, 10, 50, 3, 70, 15, 25, 100]),
+    ("all-equal-64x6", lambda: np.full(64, 0.25, np.float32), 6, list(range(6))),
+]
+
+
+@pytest.mark.parametrize("label,make,k,want", TIE_CASES)
+def test_reference_tie_fixtures(oracle, label, make, k, want):
+    logits = make()
+    ids, w = oracle.topk_softmax_batch(logits, 1, logits.size, k)
+    assert ids.tolist() == want, label
+    ids2, w2 = oracle.router_softmax_topk(logits, k)
+    assert ids2.tolist() == want, label
+    assert abs(float(w2.sum()) - 1.0) < 1e-4
+
+
+def test_no_ties_randomish_is_sorted_prefix(oracle):
+    n = 128
+    logits = np.array([((i * 37 + 11) % n) / n * 12.0 - 6.0 for i in range(n)], np.float32)
+    ids, _ = oracle.topk_softmax_batch(logits, 1, n, 8)
+    assert ids.tolist() == np.argsort(-logits.astype(np.float64), kind="stable")[:8].tolist()
+
+
+def test_topk_picks_largest(oracle):
+    ids, w = oracle.router_softmax_topk(np.array([0.1, 5.0, 2.0, 0.5], np.float32), 2)
+    assert ids.tolist() == [1, 2]
+    assert abs(float(w.sum()) - 1.0) < 1e-5
+    # closed form: renormalised softmax over the pair = sigmoid of the logit gap
+    assert abs(float(w[0]) - 1.0 / (1.0 + np.exp(-3.0))) < 1e-6
+
+
+def test_topk_desc_ties_lower_index_and_neg_inf(oracle):
+    v = np.array([1.0, 3.0, 3.0, -np.inf, 2.0, 3.0, -np.inf], np.float32)
+    assert oracle.topk_desc(v, 7).tolist() == [1, 2, 5, 4, 0, 3, 6]
+
+
+def test_router_weights_vs_f64_softmax(oracle):
+    rng = np.random.default_rng(3)
+    logits = (rng.standard_normal(512) * 0.5).astype(np.float32)
+    ids, w = oracle.router_softmax_topk(logits, 10)
+    l64 = logits.astype(np.float64)
+    p = np.exp(l64 - l64.max())
+    p /= p.sum()
+    assert ids.tolist() == np.argsort(-p, kind="stable")[:10].tolist()
+    sel = p[ids] / p[ids].sum()
+    assert np.max(np.abs(w - sel)) < 1e-6
+
+
+def test_router_rejects_nonfinite(oracle):
+    logits = np.zeros(16, np.float32)
+    logits[3] = np.nan
+    with pytest.raises(oracle.OracleError):
+        oracle.router_softmax_topk(logits, 4)
+
+
+def test_noaux_tc_single_group_reduces_to_sorted_corrected_scores(oracle):
+    rng = np.random.default_rng(4)
+    logits = rng.standard_normal(256).astype(np.float32)
+    bias = (rng.standard_normal(256) * 0.01).astype(np.float32)
+    ids, w = oracle.router_noaux_tc(logits, bias, 1, 1, 8, True, 2.5)
+    s = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
+    corr = s + bias
+    assert ids.tolist() == np.argsort(-corr, kind="stable")[:8].tolist()
+    want = s[ids] / (s[ids].sum() + 1e-20) * 2.5
+    assert np.max(np.abs(w - want)) < 1e-6
+
+
+def test_noaux_tc_group_restriction_known_answer(oracle):
+    # 4 groups x 4 experts; group score = sum of its best two corrected scores.
+    # Group 0 has one huge expert but a weak second; groups 1 and 2 win on
+    # their top-2 sums, so expert 0 is excluded although it is the maximum.
+    logits = np.full(16, -6.0, np.float32)
+    logits[0] = 6.0                        # group 0: 0.9975 + ~0.0025
+    logits[4:6] = [2.0, 2.0]               # group 1: 0.88 + 0.88
+    logits[8:10] = [1.0, 1.5]              # group 2: 0.73 + 0.82
+    bias = np.zeros(16, np.float32)
+    ids, w = oracle.router_noaux_tc(logits, bias, 4, 2, 3, False, 1.0)
+    assert ids.tolist() == [4, 5, 9]
+    assert abs(float(w[0]) - 1 / (1 + np.exp(-2.0))) < 1e-7
+
+
+def test_rmsnorm_closed_form(oracle):
+    x = np.array([3.0, 4.0], np.float32)
+    w = np.array([0.0, 1.0], np.float32)
+    out = oracle.rmsnorm_1p(x, w, 1e-6)
+    inv = 1.0 / np.sqrt((9 + 16) / 2 + 1e-6)
+    assert np.allclose(out, [3 * inv, 4 * inv * 2], rtol=1e-6)
+
+
+def test_silu_mul_closed_form(oracle):
+    g = np.array([0.0, 1.0, -2.0], np.float32)
+    u = np.array([5.0, 2.0, 1.0], np.float32)
+    got = oracle.silu_mul(g, u)
+    want = g / (1 + np.exp(-g.astype(np.float64))) * u
+    assert got[0] == 0.0 and np.allclose(got, want, rtol=1e-6)
+
+
+# ------------------------------------------------------------------ MoE layer
+
+def _small_layer(oracle, kind="q4", hidden=256, inter=128, n_experts=16, top_k=4, seed=0,
+                 shared_gate=True, zero_experts=False, identical=False):
+    rng = np.random.default_rng(seed)
+
+    def organ(rows, cols):
+        w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+        if zero_experts:
+            w[:] = 0
+        if kind == "q4":
+            return oracle.Organ.q4(w, 32), w
+        sel = (rng.random(rows * cols // 128) < 0.7).astype(np.uint8)
+        return oracle.Organ.mixed_from(w, sel), w
+
+    experts = []
+    first = None
+    for e in range(n_experts):
+        if identical and first is not None:
+            experts.append(first)
+            continue
+        trip = tuple(organ(*s)[0] for s in [(inter, hidden), (inter, hidden), (hidden, inter)])
+        experts.append(trip)
+        first = first or trip
+    shared = tuple(organ(*s)[0] for s in [(inter, hidden), (inter, hidden), (hidden, inter)])
+    norm_w = (rng.standard_normal(hidden) * 0.1).astype(np.float32)
+    router_w = (rng.standard_normal((n_experts, hidden)) * 0.02).astype(np.float32)
+    gate_w = (rng.standard_normal(hidden) * 0.02).astype(np.float32) if shared_gate else None
+    layer = oracle.MoeLayer(hidden, inter, n_experts, top_k, norm_w, router_w, experts,
+                            shared=shared, shared_gate_w=gate_w)
+    return layer, rng, experts, shared, router_w, norm_w, gate_w
+
+
+@pytest.mark.parametrize("kind", ["q4", "mixed"])
+def test_moe_layer_vs_f64_authority(oracle, kind):
+    layer, rng, *_ = _small_layer(oracle, kind)
+    h = rng.standard_normal(256).astype(np.float32)
+    out, ids, w, xn, logits = layer.forward(h)
+    assert len(set(ids.tolist())) == 4 and abs(float(w.sum()) - 1) < 1e-4
+    ref = layer.forward_f64(h, ids)
+    assert oracle.relative_l2(out, ref) < 2e-6
+    # the residual is carried: the delta is small relative to h but nonzero
+    assert 0 < np.linalg.norm(out - h) < np.linalg.norm(h)
+
+
+def test_moe_layer_route_is_router_of_normed_input(oracle):
+    layer, rng, experts, shared, router_w, norm_w, gate_w = _small_layer(oracle)
+    h = rng.standard_normal(256).astype(np.float32)
+    out, ids, w, xn, logits = layer.forward(h)
+    assert np.array_equal(xn, oracle.rmsnorm_1p(h, norm_w))
+    assert np.array_equal(logits, oracle.gemv_f32(router_w, xn))
+    ids2, w2 = oracle.router_softmax_topk(logits, 4)
+    assert np.array_equal(ids, ids2) and np.array_equal(w, w2)
+
+
+def test_moe_layer_zero_experts_leaves_gated_shared(oracle):
+    layer, rng, experts, shared, router_w, norm_w, gate_w = _small_layer(oracle, zero_experts=True)
+    h = rng.standard_normal(256).astype(np.float32)
+    out, *_ = layer.forward(h)
+    # all routed and shared weights are zero -> every MLP is zero -> out == h exactly
+    assert np.array_equal(out, h)
+
+
+def test_moe_layer_identical_experts_route_invariant(oracle):
+    layer, rng, experts, shared, router_w, norm_w, gate_w = _small_layer(oracle, identical=True)
+    h = rng.standard_normal(256).astype(np.float32)
+    out, ids, w, xn, _ = layer.forward(h)
+    # sum_r w_r * f(xn) with sum w_r = 1 -> f(xn) (+ gated shared), whatever the route
+    ref = layer.forward_f64(h, ids)
+    e = oracle.Organ
+    a = np.empty(128, np.float32)
+    single = np.empty(256, np.float32)
+    import ctypes as C
+    lib = oracle.lib()
+    t = experts[0]
+    lib.hko_mlp(C.byref(t[0].c), C.byref(t[1].c), C.byref(t[2].c), xn.ctypes.data,
+                a.ctypes.data, single.ctypes.data)
+    sh = np.empty(256, np.float32)
+    lib.hko_mlp(C.byref(shared[0].c), C.byref(shared[1].c), C.byref(shared[2].c), xn.ctypes.data,
+                None, sh.ctypes.data)
+    g = 1 / (1 + np.exp(-np.dot(gate_w.astype(np.float64), xn.astype(np.float64))))
+    approx = h.astype(np.float64) + single.astype(np.float64) + g * sh.astype(np.float64)
+    assert oracle.relative_l2(out, approx) < 1e-6
+    assert oracle.relative_l2(out, ref) < 2e-6
+    del e
