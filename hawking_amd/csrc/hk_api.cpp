@@ -1,0 +1,981 @@
+// hk_api.cpp -- host side of the C ABI (include/hawking_hip.h).
+//
+// Validates every argument on the host before any launch, owns device
+// memory for organs and MoE models, and enqueues kernels on the caller's
+// stream.  No entry point falls back to a CPU path.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "hk_internal.h"
+#include "hk_moe.h"
+#include "hk_router.h"
+#include "hk_synth.h"
+
+using hk::OrganView;
+
+struct hk_organ {
+    OrganView view{};
+    void* mem = nullptr;
+    size_t alloc_bytes = 0;
+    size_t packed_bytes = 0;
+};
+
+namespace hk {
+
+int set_error(hk_ctx* ctx, int code, const std::string& msg) {
+    if (ctx) {
+        ctx->last_status = code;
+        ctx->last_error = msg;
+    }
+    return code;
+}
+
+int check_hip(hk_ctx* ctx, hipError_t e, const char* what) {
+    if (e == hipSuccess) return HK_OK;
+    return set_error(ctx, HK_E_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int ensure_scratch(hk_ctx* ctx, size_t bytes, void** out) {
+    if (ctx->scratch_bytes < bytes) {
+        if (ctx->scratch) {
+            hipError_t e = hipDeviceSynchronize();
+            if (e != hipSuccess) return check_hip(ctx, e, "hipDeviceSynchronize (scratch grow)");
+            (void)hipFree(ctx->scratch);
+            ctx->scratch = nullptr;
+            ctx->scratch_bytes = 0;
+        }
+        size_t want = std::max<size_t>(bytes, 1 << 20);
+        hipError_t e = hipMalloc(&ctx->scratch, want);
+        if (e != hipSuccess) return set_error(ctx, HK_E_NOMEM, "scratch allocation failed");
+        ctx->scratch_bytes = want;
+    }
+    *out = ctx->scratch;
+    return HK_OK;
+}
+
+static inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+static inline bool f16_finite(uint16_t b) { return (b & 0x7C00u) != 0x7C00u; }
+
+static int popcount8(uint8_t v) { return __builtin_popcount(v); }
+
+// Section sizes of one organ in the device layout.
+struct Layout {
+    size_t scales = 0, codes = 0, tags = 0, row_tab = 0, q2_scales = 0, q2_codes = 0, dense = 0;
+    size_t total() const {
+        return align256(scales) + align256(codes) + align256(tags) + 2 * align256(row_tab) +
+               align256(q2_scales) + align256(q2_codes) + align256(dense);
+    }
+    size_t packed() const { return scales + codes + tags + q2_scales + q2_codes + dense; }
+};
+
+static int validate_shape(hk_ctx* ctx, int kind, int group, uint32_t rows, uint32_t cols) {
+    if (rows == 0 || cols == 0) return set_error(ctx, HK_E_GEOMETRY, "organ rows and cols must be positive");
+    switch (kind) {
+    case HK_Q4:
+        if (group != 32 && group != 64 && group != 128)
+            return set_error(ctx, HK_E_UNSUPPORTED,
+                             "uniform Q4 group_size=" + std::to_string(group) + " must be 32, 64 or 128");
+        if (cols % (uint32_t)group)
+            return set_error(ctx, HK_E_GEOMETRY, "uniform Q4 requires cols to be a multiple of group_size");
+        return HK_OK;
+    case HK_BIN:
+        if (group != 128) return set_error(ctx, HK_E_UNSUPPORTED, "binary organs use group_size 128");
+        if (cols % 128)
+            return set_error(ctx, HK_E_GEOMETRY,
+                             "binary_group kernel requires cols to be a multiple of group_size");
+        return HK_OK;
+    case HK_MIXED:
+        if (cols % 128) return set_error(ctx, HK_E_GEOMETRY, "mixed organs require cols % 128 == 0");
+        return HK_OK;
+    case HK_F32:
+        if (cols % 4) return set_error(ctx, HK_E_GEOMETRY, "dense organs require cols % 4 == 0");
+        return HK_OK;
+    default:
+        return set_error(ctx, HK_E_UNSUPPORTED, "unknown organ kind " + std::to_string(kind));
+    }
+}
+
+static Layout layout_for(int kind, int group, uint32_t rows, uint32_t cols, uint32_t n_bin,
+                         uint32_t n_q2) {
+    Layout L;
+    const size_t n = (size_t)rows * cols;
+    switch (kind) {
+    case HK_Q4:
+        L.scales = n / (size_t)group * 2;
+        L.codes = n / 2;
+        break;
+    case HK_BIN:
+        L.scales = n / 128 * 2;
+        L.codes = n / 8;
+        break;
+    case HK_MIXED: {
+        const size_t groups = n / 128;
+        L.tags = ((groups + 31) / 32) * 4;
+        L.row_tab = ((size_t)rows + 1) * 4;
+        L.scales = (size_t)n_bin * 2;
+        L.codes = (size_t)n_bin * 16;
+        L.q2_scales = (size_t)n_q2 * 4;
+        L.q2_codes = (size_t)n_q2 * 32;
+        break;
+    }
+    default:
+        L.dense = n * 4;
+    }
+    return L;
+}
+
+// Carves the sections of `L` out of `base` and returns the organ view.
+static OrganView place(int kind, int group, uint32_t rows, uint32_t cols, const Layout& L,
+                       uint8_t* base) {
+    OrganView v{};
+    v.kind = kind;
+    v.group = group;
+    v.rows = rows;
+    v.cols = cols;
+    uint8_t* p = base;
+    v.scales = reinterpret_cast<const uint16_t*>(p);
+    p += align256(L.scales);
+    v.codes = p;
+    p += align256(L.codes);
+    v.tags = p;
+    p += align256(L.tags);
+    v.row_bin = reinterpret_cast<const uint32_t*>(p);
+    p += align256(L.row_tab);
+    v.row_q2 = reinterpret_cast<const uint32_t*>(p);
+    p += align256(L.row_tab);
+    v.q2_scales = reinterpret_cast<const uint16_t*>(p);
+    p += align256(L.q2_scales);
+    v.q2_codes = p;
+    p += align256(L.q2_codes);
+    v.dense = reinterpret_cast<const float*>(p);
+    return v;
+}
+
+// Validates the host canonical source of one organ (geometry, finite scales,
+// mixed tag counts) and returns its layout.
+static int validate_src(hk_ctx* ctx, const hk_organ_src* s, Layout* out) {
+    if (!s) return set_error(ctx, HK_E_INVALID_ARG, "organ source is NULL");
+    int rc = validate_shape(ctx, s->kind, s->group, s->rows, s->cols);
+    if (rc) return rc;
+    const size_t n = (size_t)s->rows * s->cols;
+    if (s->kind == HK_Q4 || s->kind == HK_BIN) {
+        if (!s->scales || !s->codes) return set_error(ctx, HK_E_INVALID_ARG, "organ scales/codes are NULL");
+        const size_t groups = n / (size_t)(s->kind == HK_Q4 ? s->group : 128);
+        for (size_t g = 0; g < groups; ++g)
+            if (!f16_finite(s->scales[g]))
+                return set_error(ctx, HK_E_NONFINITE, "group " + std::to_string(g) + " scale is not a finite FP16");
+    } else if (s->kind == HK_MIXED) {
+        if (!s->tags || (s->n_bin && (!s->scales || !s->codes)) || (s->n_q2 && (!s->q2_scales || !s->q2_codes)))
+            return set_error(ctx, HK_E_INVALID_ARG, "mixed organ streams are NULL");
+        const size_t groups = n / 128;
+        size_t nb = 0;
+        for (size_t b = 0; b < (groups + 7) / 8; ++b) {
+            uint8_t t = s->tags[b];
+            if (b == (groups + 7) / 8 - 1 && (groups & 7)) t &= (uint8_t)((1u << (groups & 7)) - 1);
+            nb += (size_t)popcount8(t);
+        }
+        if (nb != s->n_bin || groups - nb != s->n_q2)
+            return set_error(ctx, HK_E_GEOMETRY, "mixed tag bitmap disagrees with n_bin / n_q2");
+        for (size_t g = 0; g < s->n_bin; ++g)
+            if (!f16_finite(s->scales[g])) return set_error(ctx, HK_E_NONFINITE, "mixed binary scale is not finite");
+        for (size_t g = 0; g < 2 * (size_t)s->n_q2; ++g)
+            if (!f16_finite(s->q2_scales[g])) return set_error(ctx, HK_E_NONFINITE, "mixed Q2 scale is not finite");
+    } else {
+        if (!s->dense) return set_error(ctx, HK_E_INVALID_ARG, "dense organ data is NULL");
+    }
+    *out = layout_for(s->kind, s->group, s->rows, s->cols, s->n_bin, s->n_q2);
+    return HK_OK;
+}
+
+// Copies one validated host organ into device memory at `base` (stream-ordered).
+static int copy_src(hk_ctx* ctx, const hk_organ_src* s, const Layout& L, uint8_t* base,
+                    OrganView* view, hipStream_t st, std::vector<std::vector<uint32_t>>* keep) {
+    OrganView v = place(s->kind, s->group, s->rows, s->cols, L, base);
+    auto cp = [&](const void* dst, const void* src, size_t bytes) -> int {
+        if (!bytes) return HK_OK;
+        return check_hip(ctx, hipMemcpyAsync(const_cast<void*>(dst), src, bytes, hipMemcpyHostToDevice, st),
+                         "hipMemcpyAsync (organ upload)");
+    };
+    int rc = HK_OK;
+    if (s->kind == HK_Q4 || s->kind == HK_BIN) {
+        if ((rc = cp(v.scales, s->scales, L.scales))) return rc;
+        if ((rc = cp(v.codes, s->codes, L.codes))) return rc;
+    } else if (s->kind == HK_MIXED) {
+        const uint32_t gpr = s->cols / 128;
+        std::vector<uint32_t> tags_words(L.tags / 4, 0u);
+        std::memcpy(tags_words.data(), s->tags, ((size_t)s->rows * gpr + 7) / 8);
+        std::vector<uint32_t> tab(2 * ((size_t)s->rows + 1));
+        uint32_t run = 0;
+        for (uint32_t r = 0; r <= s->rows; ++r) {
+            tab[r] = run;
+            tab[s->rows + 1 + r] = r * gpr - run;
+            if (r == s->rows) break;
+            for (uint32_t g = r * gpr; g < (r + 1) * gpr; ++g) run += (s->tags[g >> 3] >> (g & 7u)) & 1u;
+        }
+        if ((rc = cp(v.tags, tags_words.data(), L.tags))) return rc;
+        if ((rc = cp(v.row_bin, tab.data(), L.row_tab))) return rc;
+        if ((rc = cp(v.row_q2, tab.data() + s->rows + 1, L.row_tab))) return rc;
+        if ((rc = cp(v.scales, s->scales, L.scales))) return rc;
+        if ((rc = cp(v.codes, s->codes, L.codes))) return rc;
+        if ((rc = cp(v.q2_scales, s->q2_scales, L.q2_scales))) return rc;
+        if ((rc = cp(v.q2_codes, s->q2_codes, L.q2_codes))) return rc;
+        // the async copies read host staging vectors: keep them alive until sync
+        keep->push_back(std::move(tags_words));
+        keep->push_back(std::move(tab));
+    } else {
+        if ((rc = cp(v.dense, s->dense, L.dense))) return rc;
+    }
+    *view = v;
+    return HK_OK;
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace hk
+
+using namespace hk;
+
+// ====================================================================== context
+
+extern "C" int hk_ctx_create(int device, hk_ctx** out) {
+    if (!out) return HK_E_INVALID_ARG;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return HK_E_HIP;
+    if (device < 0 || device >= n) return HK_E_INVALID_ARG;
+    if (hipSetDevice(device) != hipSuccess) return HK_E_HIP;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return HK_E_HIP;
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return HK_E_UNSUPPORTED;
+    hk_ctx* ctx = new hk_ctx();
+    ctx->device = device;
+    void* st = nullptr;
+    if (hipMalloc(&st, 256) != hipSuccess) {
+        delete ctx;
+        return HK_E_NOMEM;
+    }
+    (void)hipMemset(st, 0, 256);
+    ctx->dev_status = static_cast<uint32_t*>(st);
+    *out = ctx;
+    return HK_OK;
+}
+
+extern "C" void hk_ctx_destroy(hk_ctx* ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    (void)hipDeviceSynchronize();
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->dev_status) (void)hipFree(ctx->dev_status);
+    delete ctx;
+}
+
+extern "C" int hk_last_error(const hk_ctx* ctx, char* buf, size_t len) {
+    if (!ctx || !buf || !len) return HK_E_INVALID_ARG;
+    std::snprintf(buf, len, "%s", ctx->last_error.c_str());
+    return ctx->last_status;
+}
+
+extern "C" const char* hk_version(void) { return "hawking-mi355x 0.1 (gfx950)"; }
+
+extern "C" int hk_device_info(hk_ctx* ctx, char* name, size_t len, int* cu_count, size_t* hbm_bytes) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    hipDeviceProp_t prop;
+    int rc = check_hip(ctx, hipGetDeviceProperties(&prop, ctx->device), "hipGetDeviceProperties");
+    if (rc) return rc;
+    if (name && len) std::snprintf(name, len, "%s (%s)", prop.name, prop.gcnArchName);
+    if (cu_count) *cu_count = prop.multiProcessorCount;
+    if (hbm_bytes) *hbm_bytes = prop.totalGlobalMem;
+    return HK_OK;
+}
+
+extern "C" int hk_check_device_status(hk_ctx* ctx, hk_stream stream, uint32_t* bits) {
+    if (!ctx || !bits) return HK_E_INVALID_ARG;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    uint32_t v = 0;
+    int rc = check_hip(ctx, hipMemcpyAsync(&v, ctx->dev_status, 4, hipMemcpyDeviceToHost, st), "status read");
+    if (rc) return rc;
+    rc = check_hip(ctx, hipStreamSynchronize(st), "hipStreamSynchronize");
+    if (rc) return rc;
+    *bits = v;
+    return check_hip(ctx, hipMemsetAsync(ctx->dev_status, 0, 4, st), "status clear");
+}
+
+// ====================================================================== plumbing
+
+extern "C" int hk_malloc(hk_ctx* ctx, size_t bytes, void** out) {
+    if (!ctx || !out) return HK_E_INVALID_ARG;
+    *out = nullptr;
+    if (bytes == 0) bytes = 256;
+    if (hipMalloc(out, bytes) != hipSuccess)
+        return set_error(ctx, HK_E_NOMEM, "hipMalloc of " + std::to_string(bytes) + " bytes failed");
+    return HK_OK;
+}
+
+extern "C" int hk_free(hk_ctx* ctx, void* ptr) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (!ptr) return HK_OK;
+    return check_hip(ctx, hipFree(ptr), "hipFree");
+}
+
+static int memcpy_kind(hk_ctx* ctx, void* dst, const void* src, size_t bytes, hk_stream s,
+                       hipMemcpyKind kind) {
+    if (!ctx || (bytes && (!dst || !src))) return set_error(ctx, HK_E_INVALID_ARG, "memcpy: NULL pointer");
+    if (!bytes) return HK_OK;
+    return check_hip(ctx, hipMemcpyAsync(dst, src, bytes, kind, static_cast<hipStream_t>(s)), "hipMemcpyAsync");
+}
+
+extern "C" int hk_memcpy_htod(hk_ctx* ctx, void* dst, const void* src, size_t bytes, hk_stream s) {
+    return memcpy_kind(ctx, dst, src, bytes, s, hipMemcpyHostToDevice);
+}
+extern "C" int hk_memcpy_dtoh(hk_ctx* ctx, void* dst, const void* src, size_t bytes, hk_stream s) {
+    return memcpy_kind(ctx, dst, src, bytes, s, hipMemcpyDeviceToHost);
+}
+extern "C" int hk_memcpy_dtod(hk_ctx* ctx, void* dst, const void* src, size_t bytes, hk_stream s) {
+    return memcpy_kind(ctx, dst, src, bytes, s, hipMemcpyDeviceToDevice);
+}
+
+extern "C" int hk_memset(hk_ctx* ctx, void* dst, int value, size_t bytes, hk_stream s) {
+    if (!ctx || (bytes && !dst)) return HK_E_INVALID_ARG;
+    if (!bytes) return HK_OK;
+    return check_hip(ctx, hipMemsetAsync(dst, value, bytes, static_cast<hipStream_t>(s)), "hipMemsetAsync");
+}
+
+extern "C" int hk_stream_create(hk_ctx* ctx, hk_stream* out) {
+    if (!ctx || !out) return HK_E_INVALID_ARG;
+    hipStream_t s;
+    int rc = check_hip(ctx, hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+    if (rc) return rc;
+    *out = s;
+    return HK_OK;
+}
+
+extern "C" int hk_stream_destroy(hk_ctx* ctx, hk_stream s) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (!s) return HK_OK;
+    return check_hip(ctx, hipStreamDestroy(static_cast<hipStream_t>(s)), "hipStreamDestroy");
+}
+
+extern "C" int hk_stream_synchronize(hk_ctx* ctx, hk_stream s) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    return check_hip(ctx, hipStreamSynchronize(static_cast<hipStream_t>(s)), "hipStreamSynchronize");
+}
+
+extern "C" int hk_device_synchronize(hk_ctx* ctx) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    return check_hip(ctx, hipDeviceSynchronize(), "hipDeviceSynchronize");
+}
+
+extern "C" int hk_event_create(hk_ctx* ctx, void** out) {
+    if (!ctx || !out) return HK_E_INVALID_ARG;
+    hipEvent_t e;
+    int rc = check_hip(ctx, hipEventCreate(&e), "hipEventCreate");
+    if (rc) return rc;
+    *out = e;
+    return HK_OK;
+}
+
+extern "C" int hk_event_destroy(hk_ctx* ctx, void* ev) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    return ev ? check_hip(ctx, hipEventDestroy(static_cast<hipEvent_t>(ev)), "hipEventDestroy") : HK_OK;
+}
+
+extern "C" int hk_event_record(hk_ctx* ctx, void* ev, hk_stream s) {
+    if (!ctx || !ev) return HK_E_INVALID_ARG;
+    return check_hip(ctx, hipEventRecord(static_cast<hipEvent_t>(ev), static_cast<hipStream_t>(s)),
+                     "hipEventRecord");
+}
+
+extern "C" int hk_event_elapsed_ms(hk_ctx* ctx, void* a, void* b, float* ms) {
+    if (!ctx || !a || !b || !ms) return HK_E_INVALID_ARG;
+    int rc = check_hip(ctx, hipEventSynchronize(static_cast<hipEvent_t>(b)), "hipEventSynchronize");
+    if (rc) return rc;
+    return check_hip(ctx, hipEventElapsedTime(ms, static_cast<hipEvent_t>(a), static_cast<hipEvent_t>(b)),
+                     "hipEventElapsedTime");
+}
+
+// ====================================================================== organs
+
+extern "C" int hk_organ_upload(hk_ctx* ctx, const hk_organ_src* src, hk_stream stream, hk_organ** out) {
+    if (!ctx || !out) return HK_E_INVALID_ARG;
+    *out = nullptr;
+    Layout L;
+    int rc = validate_src(ctx, src, &L);
+    if (rc) return rc;
+    hk_organ* o = new hk_organ();
+    o->alloc_bytes = L.total();
+    if (hipMalloc(&o->mem, o->alloc_bytes) != hipSuccess) {
+        delete o;
+        return set_error(ctx, HK_E_NOMEM, "organ allocation failed");
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    std::vector<std::vector<uint32_t>> keep;
+    rc = copy_src(ctx, src, L, static_cast<uint8_t*>(o->mem), &o->view, st, &keep);
+    if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "hipStreamSynchronize (organ upload)");
+    if (rc) {
+        (void)hipFree(o->mem);
+        delete o;
+        return rc;
+    }
+    o->packed_bytes = L.packed();
+    *out = o;
+    return HK_OK;
+}
+
+extern "C" int hk_organ_free(hk_ctx* ctx, hk_organ* o) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (!o) return HK_OK;
+    int rc = check_hip(ctx, hipFree(o->mem), "hipFree (organ)");
+    delete o;
+    return rc;
+}
+
+extern "C" int hk_organ_info(const hk_organ* o, int32_t* kind, int32_t* group, uint32_t* rows, uint32_t* cols,
+                             size_t* packed_bytes) {
+    if (!o) return HK_E_INVALID_ARG;
+    if (kind) *kind = o->view.kind;
+    if (group) *group = o->view.group;
+    if (rows) *rows = o->view.rows;
+    if (cols) *cols = o->view.cols;
+    if (packed_bytes) *packed_bytes = o->packed_bytes;
+    return HK_OK;
+}
+
+extern "C" int hk_gemv(hk_ctx* ctx, const hk_organ* o, const float* x, float* y, hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (!o || !x || !y) return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv: NULL organ or vector");
+    if (!aligned16(x) || !aligned16(y)) return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv: x and y must be 16-byte aligned");
+    return check_hip(ctx, launch_gemv(o->view, x, y, static_cast<hipStream_t>(stream)), "gemv launch");
+}
+
+extern "C" int hk_gemv_batch(hk_ctx* ctx, const hk_organ* const* organs, uint32_t n, const float* x,
+                             size_t x_stride, float* y, size_t y_stride, hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (!organs || !x || !y || n == 0) return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv_batch: bad arguments");
+    if (n > 65535) return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv_batch: at most 65535 organs per launch");
+    if (!aligned16(x) || !aligned16(y) || (x_stride % 4) || (y_stride % 4) || (n > 1 && (!x_stride || !y_stride)))
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv_batch: x/y must be 16-byte aligned with strides % 4 == 0");
+    std::vector<OrganView> views(n);
+    for (uint32_t i = 0; i < n; ++i) {
+        if (!organs[i]) return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv_batch: NULL organ");
+        views[i] = organs[i]->view;
+        const OrganView& a = views[0];
+        const OrganView& b = views[i];
+        if (a.kind != b.kind || a.rows != b.rows || a.cols != b.cols || a.group != b.group)
+            return set_error(ctx, HK_E_GEOMETRY, "hk_gemv_batch: organs must share kind and shape");
+    }
+    if (x_stride && x_stride < views[0].cols) return set_error(ctx, HK_E_GEOMETRY, "hk_gemv_batch: x_stride < cols");
+    if (y_stride && y_stride < views[0].rows) return set_error(ctx, HK_E_GEOMETRY, "hk_gemv_batch: y_stride < rows");
+    void* dv = nullptr;
+    int rc = ensure_scratch(ctx, n * sizeof(OrganView), &dv);
+    if (rc) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    rc = check_hip(ctx, hipMemcpyAsync(dv, views.data(), n * sizeof(OrganView), hipMemcpyHostToDevice, st),
+                   "descriptor upload");
+    if (rc) return rc;
+    // the host vector must outlive the copy
+    rc = check_hip(ctx, hipStreamSynchronize(st), "hipStreamSynchronize (descriptor upload)");
+    if (rc) return rc;
+    return check_hip(ctx,
+                     launch_gemv_batch(static_cast<const OrganView*>(dv), n, views[0].kind, views[0].rows,
+                                       views[0].cols, views[0].group, x, x_stride, y, y_stride, st),
+                     "gemv_batch launch");
+}
+
+extern "C" int hk_decode_rows(hk_ctx* ctx, const hk_organ* o, uint32_t row0, uint32_t nrows, float* out,
+                              hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (!o || !out) return set_error(ctx, HK_E_INVALID_ARG, "hk_decode_rows: NULL argument");
+    if ((uint64_t)row0 + nrows > o->view.rows) return set_error(ctx, HK_E_GEOMETRY, "hk_decode_rows: rows out of range");
+    return check_hip(ctx, launch_decode_rows(o->view, row0, nrows, out, static_cast<hipStream_t>(stream)),
+                     "decode launch");
+}
+
+// ====================================================================== packers / generator
+
+static int finish_pack(hk_ctx* ctx, hipStream_t st, uint32_t* bad_dev, hipError_t launch) {
+    int rc = check_hip(ctx, launch, "pack launch");
+    if (rc) return rc;
+    uint32_t bad = 0;
+    rc = check_hip(ctx, hipMemcpyAsync(&bad, bad_dev, 4, hipMemcpyDeviceToHost, st), "pack status read");
+    if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "hipStreamSynchronize (pack)");
+    if (rc) return rc;
+    if (bad) return set_error(ctx, HK_E_NONFINITE, "source tensor contains a non-finite value or scale");
+    return HK_OK;
+}
+
+static int pack_prologue(hk_ctx* ctx, hipStream_t st, uint32_t** bad) {
+    void* p = nullptr;
+    int rc = ensure_scratch(ctx, 256, &p);
+    if (rc) return rc;
+    *bad = static_cast<uint32_t*>(p);
+    return check_hip(ctx, hipMemsetAsync(p, 0, 4, st), "hipMemsetAsync (pack flag)");
+}
+
+extern "C" int hk_pack_q4(hk_ctx* ctx, const float* w, uint32_t rows, uint32_t cols, int32_t group,
+                          uint16_t* scales, uint8_t* codes, hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    int rc = validate_shape(ctx, HK_Q4, group, rows, cols);
+    if (rc) return rc;
+    if (!w || !scales || !codes || !aligned16(codes) || !aligned16(w))
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_pack_q4: NULL or misaligned pointer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    uint32_t* bad;
+    if ((rc = pack_prologue(ctx, st, &bad))) return rc;
+    const size_t groups = (size_t)rows * cols / (size_t)group;
+    return finish_pack(ctx, st, bad, launch_pack_q4(w, groups, group, scales, codes, bad, st));
+}
+
+extern "C" int hk_pack_bin(hk_ctx* ctx, const float* w, uint32_t rows, uint32_t cols, uint16_t* scales,
+                           uint8_t* signs, hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    int rc = validate_shape(ctx, HK_BIN, 128, rows, cols);
+    if (rc) return rc;
+    if (!w || !scales || !signs || !aligned16(signs))
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_pack_bin: NULL or misaligned pointer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    uint32_t* bad;
+    if ((rc = pack_prologue(ctx, st, &bad))) return rc;
+    return finish_pack(ctx, st, bad, launch_pack_bin(w, (size_t)rows * cols / 128, scales, signs, bad, st));
+}
+
+extern "C" int hk_pack_q2(hk_ctx* ctx, const float* w, size_t count, uint16_t* scales, uint8_t* codes,
+                          hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (count == 0 || count % 64) return set_error(ctx, HK_E_GEOMETRY, "hk_pack_q2: count must be a positive multiple of 64");
+    if (!w || !scales || !codes || !aligned16(codes))
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_pack_q2: NULL or misaligned pointer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    uint32_t* bad;
+    int rc;
+    if ((rc = pack_prologue(ctx, st, &bad))) return rc;
+    return finish_pack(ctx, st, bad, launch_pack_q2(w, count / 64, scales, codes, bad, st));
+}
+
+extern "C" uint64_t hk_stream_key(uint64_t seed, uint64_t stream_id) { return hk::stream_key(seed, stream_id); }
+
+extern "C" int hk_synth_normal(hk_ctx* ctx, uint64_t key, uint64_t first, size_t count, float sigma, float* out,
+                               hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (!out) return set_error(ctx, HK_E_INVALID_ARG, "hk_synth_normal: NULL output");
+    if (!count) return HK_OK;
+    return check_hip(ctx, launch_synth_normal(key, first, count, sigma, out, static_cast<hipStream_t>(stream)),
+                     "synth launch");
+}
+
+// ====================================================================== routers
+
+extern "C" int hk_router_softmax_topk(hk_ctx* ctx, const float* logits, uint32_t n_tokens, uint32_t n_experts,
+                                      uint32_t top_k, float tie_eps, int renorm, int32_t* ids, float* weights,
+                                      hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (!logits || !ids || !weights) return set_error(ctx, HK_E_INVALID_ARG, "router: NULL pointer");
+    if (n_tokens == 0 || n_experts == 0 || top_k == 0 || top_k > n_experts)
+        return set_error(ctx, HK_E_INVALID_ARG, "router: need 0 < top_k <= n_experts and n_tokens > 0");
+    if (n_experts > 16384) return set_error(ctx, HK_E_UNSUPPORTED, "router: n_experts above 16384");
+    if (!(tie_eps >= 0.0f) || !std::isfinite(tie_eps)) return set_error(ctx, HK_E_INVALID_ARG, "router: tie_eps must be finite and >= 0");
+    return check_hip(ctx,
+                     launch_softmax_topk(logits, n_tokens, n_experts, top_k, tie_eps, renorm, ids, weights,
+                                         ctx->dev_status, static_cast<hipStream_t>(stream)),
+                     "router launch");
+}
+
+extern "C" int hk_router_noaux_tc(hk_ctx* ctx, const float* logits, const float* bias, uint32_t n_tokens,
+                                  uint32_t n_experts, uint32_t n_group, uint32_t topk_group, uint32_t top_k,
+                                  int norm_topk_prob, float routed_scaling_factor, int32_t* ids, float* weights,
+                                  hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (!logits || !bias || !ids || !weights) return set_error(ctx, HK_E_INVALID_ARG, "noaux_tc: NULL pointer");
+    if (n_tokens == 0 || n_group == 0 || n_experts % n_group || topk_group == 0 || topk_group > n_group ||
+        top_k == 0 || top_k > (n_experts / n_group) * topk_group)
+        return set_error(ctx, HK_E_INVALID_ARG, "noaux_tc: inconsistent group / top-k geometry");
+    if (n_experts > 8192) return set_error(ctx, HK_E_UNSUPPORTED, "noaux_tc: n_experts above 8192");
+    return check_hip(ctx,
+                     launch_noaux_tc(logits, bias, n_tokens, n_experts, n_group, topk_group, top_k, norm_topk_prob,
+                                     routed_scaling_factor, ids, weights, static_cast<hipStream_t>(stream)),
+                     "noaux_tc launch");
+}
+
+// ====================================================================== MoE model
+
+namespace {
+
+constexpr uint32_t PROJ_NORM = 16, PROJ_ROUTER = 17, PROJ_SHARED_GATE = 18, PROJ_COIN = 32;
+constexpr float SIGMA_W = 0.02f, SIGMA_NORM = 0.02f;
+
+struct MoeLayerHost {
+    void* slab = nullptr;
+    size_t slab_bytes = 0;
+    std::vector<OrganView> table;      // (E+1)*3
+    std::vector<size_t> packed;        // per organ, algorithmic bytes
+    OrganView* table_dev = nullptr;
+    float* norm_w = nullptr;
+    float* router_w = nullptr;
+    float* gate_w = nullptr;
+    bool ready = false;
+};
+
+}  // namespace
+
+struct hk_moe_model {
+    hk_moe_config cfg{};
+    hk::MoeDims dims{};
+    std::vector<MoeLayerHost> layers;
+    void* dense = nullptr;   // norm/router/gate weights of all layers
+    void* ws_mem = nullptr;
+    void* tables = nullptr;  // device expert tables of all layers
+    hk::MoeWs ws{};
+    float* hbuf[2] = {nullptr, nullptr};
+};
+
+static size_t dense_per_layer(const hk_moe_config& c) {
+    return align256((size_t)c.hidden * 4) + align256((size_t)c.n_experts * c.hidden * 4) + align256((size_t)c.hidden * 4);
+}
+
+static void organ_shape(const hk_moe_config& c, uint32_t e, uint32_t p, uint32_t* rows, uint32_t* cols) {
+    const uint32_t inter = e == c.n_experts ? c.shared_inter : c.inter;
+    if (p < 2) {
+        *rows = inter;
+        *cols = c.hidden;
+    } else {
+        *rows = c.hidden;
+        *cols = inter;
+    }
+}
+
+extern "C" uint64_t hk_moe_stream_id(uint32_t layer, uint32_t expert, uint32_t proj) {
+    return ((uint64_t)(layer + 1) << 40) | ((uint64_t)expert << 8) | (uint64_t)proj;
+}
+
+extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe_model** out) {
+    if (!ctx || !cfg || !out) return HK_E_INVALID_ARG;
+    *out = nullptr;
+    const hk_moe_config& c = *cfg;
+    if (c.n_layers == 0 || c.hidden == 0 || c.inter == 0 || c.n_experts == 0 || c.top_k == 0 || c.top_k > c.n_experts)
+        return set_error(ctx, HK_E_INVALID_ARG, "moe config: zero dimension or top_k > n_experts");
+    if (c.expert_kind != HK_Q4 && c.expert_kind != HK_MIXED)
+        return set_error(ctx, HK_E_UNSUPPORTED, "moe config: expert_kind must be HK_Q4 or HK_MIXED");
+    if (c.top_k > 64 || c.n_experts > 4096 || c.hidden > 8192 || c.hidden % 128)
+        return set_error(ctx, HK_E_UNSUPPORTED, "moe config: need top_k <= 64, n_experts <= 4096, hidden % 128 == 0, hidden <= 8192");
+    const int grp = c.expert_kind == HK_MIXED ? 128 : c.expert_group;
+    int rc = validate_shape(ctx, c.expert_kind, grp, c.inter, c.hidden);
+    if (!rc) rc = validate_shape(ctx, c.expert_kind, grp, c.hidden, c.inter);
+    if (!rc && c.shared_inter) rc = validate_shape(ctx, c.expert_kind, grp, c.hidden, c.shared_inter);
+    if (rc) return rc;
+    if (!(c.eps > 0.0f) || !std::isfinite(c.eps)) return set_error(ctx, HK_E_INVALID_ARG, "moe config: eps must be positive");
+    const uint32_t imax = std::max(c.inter, c.shared_inter);
+    if ((size_t)(c.top_k + 1) * imax * 4 > 64 * 1024)
+        return set_error(ctx, HK_E_UNSUPPORTED, "moe config: (top_k+1)*intermediate activations exceed 64 KiB of LDS");
+    hk_moe_model* m = new hk_moe_model();
+    m->cfg = c;
+    m->cfg.expert_group = grp;
+    m->dims = hk::MoeDims{c.hidden, c.inter, c.shared_inter, imax, c.n_experts, c.top_k, c.shared_inter ? 1 : 0, c.eps};
+    m->layers.resize(c.n_layers);
+    const size_t dpl = dense_per_layer(c);
+    const size_t tab = align256((size_t)(c.n_experts + 1) * 3 * sizeof(OrganView));
+    const size_t ws = align256((size_t)c.hidden * 4) + align256(((size_t)c.n_experts + 4) * 4) + 256 + 256 + 256 +
+                      align256((size_t)(c.top_k + 1) * imax * 4) + 2 * align256((size_t)c.hidden * 4);
+    if (hipMalloc(&m->dense, dpl * c.n_layers) != hipSuccess || hipMalloc(&m->tables, tab * c.n_layers) != hipSuccess ||
+        hipMalloc(&m->ws_mem, ws) != hipSuccess) {
+        if (m->dense) (void)hipFree(m->dense);
+        if (m->tables) (void)hipFree(m->tables);
+        if (m->ws_mem) (void)hipFree(m->ws_mem);
+        delete m;
+        return set_error(ctx, HK_E_NOMEM, "moe model allocation failed");
+    }
+    (void)hipMemset(m->ws_mem, 0, ws);
+    for (uint32_t l = 0; l < c.n_layers; ++l) {
+        uint8_t* d = static_cast<uint8_t*>(m->dense) + l * dpl;
+        MoeLayerHost& L = m->layers[l];
+        L.norm_w = reinterpret_cast<float*>(d);
+        L.router_w = reinterpret_cast<float*>(d + align256((size_t)c.hidden * 4));
+        L.gate_w = reinterpret_cast<float*>(d + align256((size_t)c.hidden * 4) + align256((size_t)c.n_experts * c.hidden * 4));
+        L.table_dev = reinterpret_cast<OrganView*>(static_cast<uint8_t*>(m->tables) + l * tab);
+        L.table.assign((size_t)(c.n_experts + 1) * 3, OrganView{});
+        L.packed.assign((size_t)(c.n_experts + 1) * 3, 0);
+    }
+    uint8_t* w = static_cast<uint8_t*>(m->ws_mem);
+    m->ws.xn = reinterpret_cast<float*>(w);
+    w += align256((size_t)c.hidden * 4);
+    m->ws.logits = reinterpret_cast<float*>(w);
+    w += align256(((size_t)c.n_experts + 4) * 4);
+    m->ws.ids = reinterpret_cast<int32_t*>(w);
+    w += 256;
+    m->ws.weights = reinterpret_cast<float*>(w);
+    w += 256;
+    m->ws.gate = reinterpret_cast<float*>(w);
+    w += 256;
+    m->ws.act = reinterpret_cast<float*>(w);
+    w += align256((size_t)(c.top_k + 1) * imax * 4);
+    m->hbuf[0] = reinterpret_cast<float*>(w);
+    w += align256((size_t)c.hidden * 4);
+    m->hbuf[1] = reinterpret_cast<float*>(w);
+    m->ws.status = ctx->dev_status;
+    *out = m;
+    return HK_OK;
+}
+
+extern "C" int hk_moe_model_free(hk_ctx* ctx, hk_moe_model* m) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (!m) return HK_OK;
+    (void)hipDeviceSynchronize();
+    for (auto& L : m->layers)
+        if (L.slab) (void)hipFree(L.slab);
+    (void)hipFree(m->dense);
+    (void)hipFree(m->tables);
+    (void)hipFree(m->ws_mem);
+    delete m;
+    return HK_OK;
+}
+
+static int upload_table(hk_ctx* ctx, MoeLayerHost& L, hipStream_t st) {
+    int rc = check_hip(ctx,
+                       hipMemcpyAsync(L.table_dev, L.table.data(), L.table.size() * sizeof(OrganView),
+                                      hipMemcpyHostToDevice, st),
+                       "expert table upload");
+    if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "hipStreamSynchronize (expert table)");
+    return rc;
+}
+
+extern "C" int hk_moe_model_set_layer(hk_ctx* ctx, hk_moe_model* m, uint32_t layer, const hk_moe_layer_src* src,
+                                      hk_stream stream) {
+    if (!ctx || !m || !src) return HK_E_INVALID_ARG;
+    const hk_moe_config& c = m->cfg;
+    if (layer >= c.n_layers) return set_error(ctx, HK_E_INVALID_ARG, "layer index out of range");
+    if (!src->norm_w || !src->router_w || !src->experts || (c.shared_inter && !src->shared) ||
+        (c.shared_gate && c.shared_inter && !src->shared_gate_w))
+        return set_error(ctx, HK_E_INVALID_ARG, "layer source: missing tensor (a missing tensor must raise, not zero-fill)");
+    const uint32_t n_org = (c.n_experts + (c.shared_inter ? 1 : 0)) * 3;
+    std::vector<Layout> lay(n_org);
+    std::vector<const hk_organ_src*> srcs(n_org);
+    size_t total = 0;
+    for (uint32_t i = 0; i < n_org; ++i) {
+        const uint32_t e = i / 3, p = i % 3;
+        const hk_organ_src* s = e < c.n_experts ? &src->experts[i] : &src->shared[p];
+        uint32_t rows, cols;
+        organ_shape(c, e, p, &rows, &cols);
+        if (s->kind != c.expert_kind || s->rows != rows || s->cols != cols ||
+            (c.expert_kind == HK_Q4 && s->group != c.expert_group))
+            return set_error(ctx, HK_E_GEOMETRY,
+                             "expert " + std::to_string(e) + " proj " + std::to_string(p) + " disagrees with the model config");
+        int rc = validate_src(ctx, s, &lay[i]);
+        if (rc) return rc;
+        srcs[i] = s;
+        total += lay[i].total();
+    }
+    MoeLayerHost& L = m->layers[layer];
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (L.slab) {
+        (void)hipStreamSynchronize(st);
+        (void)hipFree(L.slab);
+        L.slab = nullptr;
+        L.ready = false;
+    }
+    if (hipMalloc(&L.slab, total) != hipSuccess) return set_error(ctx, HK_E_NOMEM, "expert slab allocation failed");
+    L.slab_bytes = total;
+    std::vector<std::vector<uint32_t>> keep;
+    uint8_t* p = static_cast<uint8_t*>(L.slab);
+    for (uint32_t i = 0; i < n_org; ++i) {
+        int rc = copy_src(ctx, srcs[i], lay[i], p, &L.table[i], st, &keep);
+        if (rc) return rc;
+        L.packed[i] = lay[i].packed();
+        p += lay[i].total();
+    }
+    int rc = check_hip(ctx, hipMemcpyAsync(L.norm_w, src->norm_w, (size_t)c.hidden * 4, hipMemcpyHostToDevice, st), "norm upload");
+    if (!rc) rc = check_hip(ctx, hipMemcpyAsync(L.router_w, src->router_w, (size_t)c.n_experts * c.hidden * 4,
+                                                hipMemcpyHostToDevice, st), "router upload");
+    if (!rc && src->shared_gate_w)
+        rc = check_hip(ctx, hipMemcpyAsync(L.gate_w, src->shared_gate_w, (size_t)c.hidden * 4, hipMemcpyHostToDevice, st),
+                       "gate upload");
+    if (!rc) rc = upload_table(ctx, L, st);
+    if (rc) return rc;
+    L.ready = true;
+    return HK_OK;
+}
+
+extern "C" int hk_moe_model_fill_synthetic(hk_ctx* ctx, hk_moe_model* m, uint64_t seed, hk_stream stream) {
+    if (!ctx || !m) return HK_E_INVALID_ARG;
+    const hk_moe_config& c = m->cfg;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const uint32_t n_exp = c.n_experts + (c.shared_inter ? 1 : 0);
+    const uint32_t n_org = n_exp * 3;
+    void* jobs_dev = nullptr;
+    void* aux = nullptr;
+    if (hipMalloc(&jobs_dev, (size_t)n_org * sizeof(SynthJob)) != hipSuccess ||
+        hipMalloc(&aux, (size_t)n_org * 4 + 256) != hipSuccess) {
+        if (jobs_dev) (void)hipFree(jobs_dev);
+        return set_error(ctx, HK_E_NOMEM, "synthetic job table allocation failed");
+    }
+    uint32_t* counts = static_cast<uint32_t*>(aux);
+    uint32_t* bad = counts + n_org;
+    int rc = check_hip(ctx, hipMemsetAsync(bad, 0, 4, st), "memset");
+    std::vector<SynthJob> jobs(n_org);
+    std::vector<uint32_t> nbin(n_org, 0);
+    size_t max_groups = 0;
+    for (uint32_t l = 0; l < c.n_layers && !rc; ++l) {
+        MoeLayerHost& L = m->layers[l];
+        // dense tensors
+        SynthJob dj[3] = {};
+        const uint32_t drows[3] = {1, c.n_experts, 1};
+        const uint32_t dproj[3] = {PROJ_NORM, PROJ_ROUTER, PROJ_SHARED_GATE};
+        float* dptr[3] = {L.norm_w, L.router_w, L.gate_w};
+        const float dsig[3] = {SIGMA_NORM, SIGMA_W, SIGMA_W};
+        for (int k = 0; k < 3; ++k) {
+            dj[k].key = hk::stream_key(seed, hk_moe_stream_id(l, 0, dproj[k]));
+            dj[k].sigma = dsig[k];
+            dj[k].rows = drows[k];
+            dj[k].cols = c.hidden;
+            dj[k].dense = dptr[k];
+        }
+        rc = check_hip(ctx, hipMemcpyAsync(jobs_dev, dj, sizeof(dj), hipMemcpyHostToDevice, st), "job upload");
+        if (!rc) rc = check_hip(ctx, launch_synth_jobs(HK_F32, static_cast<SynthJob*>(jobs_dev), 3,
+                                                       (size_t)c.n_experts * c.hidden / 128 + 1, bad, st), "dense synth");
+        if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "sync");
+        if (rc) break;
+        // expert organs: keys and shapes
+        max_groups = 0;
+        for (uint32_t i = 0; i < n_org; ++i) {
+            const uint32_t e = i / 3, p = i % 3;
+            uint32_t rows, cols;
+            organ_shape(c, e, p, &rows, &cols);
+            SynthJob& j = jobs[i];
+            j = SynthJob{};
+            j.key = hk::stream_key(seed, hk_moe_stream_id(l, e, p));
+            j.coin_key = hk::stream_key(seed, hk_moe_stream_id(l, e, PROJ_COIN + p));
+            j.sigma = SIGMA_W;
+            j.group = c.expert_group;
+            j.rows = rows;
+            j.cols = cols;
+            max_groups = std::max(max_groups, (size_t)rows * cols / (size_t)(c.expert_kind == HK_MIXED ? 128 : c.expert_group));
+        }
+        if (c.expert_kind == HK_MIXED) {
+            rc = check_hip(ctx, hipMemcpyAsync(jobs_dev, jobs.data(), n_org * sizeof(SynthJob), hipMemcpyHostToDevice, st), "job upload");
+            if (!rc) rc = check_hip(ctx, hipMemsetAsync(counts, 0, (size_t)n_org * 4, st), "memset");
+            if (!rc) rc = check_hip(ctx, launch_synth_mixed_count(static_cast<SynthJob*>(jobs_dev), n_org, max_groups, counts, st),
+                                    "mixed count");
+            if (!rc) rc = check_hip(ctx, hipMemcpyAsync(nbin.data(), counts, (size_t)n_org * 4, hipMemcpyDeviceToHost, st), "count read");
+            if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "sync");
+            if (rc) break;
+        }
+        std::vector<Layout> lay(n_org);
+        size_t total = 0;
+        for (uint32_t i = 0; i < n_org; ++i) {
+            const SynthJob& j = jobs[i];
+            const uint32_t groups = (uint32_t)((size_t)j.rows * j.cols / 128);
+            lay[i] = layout_for(c.expert_kind, c.expert_group, j.rows, j.cols, nbin[i],
+                                c.expert_kind == HK_MIXED ? groups - nbin[i] : 0);
+            total += lay[i].total();
+        }
+        if (L.slab) {
+            (void)hipStreamSynchronize(st);
+            (void)hipFree(L.slab);
+            L.slab = nullptr;
+        }
+        if (hipMalloc(&L.slab, total) != hipSuccess) {
+            rc = set_error(ctx, HK_E_NOMEM, "expert slab allocation failed (layer " + std::to_string(l) + ")");
+            break;
+        }
+        L.slab_bytes = total;
+        uint8_t* p = static_cast<uint8_t*>(L.slab);
+        for (uint32_t i = 0; i < n_org; ++i) {
+            SynthJob& j = jobs[i];
+            OrganView v = place(c.expert_kind, c.expert_group, j.rows, j.cols, lay[i], p);
+            j.scales = const_cast<uint16_t*>(v.scales);
+            j.codes = const_cast<uint8_t*>(v.codes);
+            j.tags = const_cast<uint8_t*>(v.tags);
+            j.q2_scales = const_cast<uint16_t*>(v.q2_scales);
+            j.q2_codes = const_cast<uint8_t*>(v.q2_codes);
+            j.row_bin = const_cast<uint32_t*>(v.row_bin);
+            j.row_q2 = const_cast<uint32_t*>(v.row_q2);
+            L.table[i] = v;
+            L.packed[i] = lay[i].packed();
+            p += lay[i].total();
+        }
+        rc = check_hip(ctx, hipMemcpyAsync(jobs_dev, jobs.data(), n_org * sizeof(SynthJob), hipMemcpyHostToDevice, st), "job upload");
+        if (!rc) rc = check_hip(ctx, launch_synth_jobs(c.expert_kind, static_cast<SynthJob*>(jobs_dev), n_org, max_groups, bad, st),
+                                "expert synth");
+        if (!rc) rc = upload_table(ctx, L, st);
+        if (!rc) L.ready = true;
+    }
+    uint32_t badv = 0;
+    if (!rc) rc = check_hip(ctx, hipMemcpyAsync(&badv, bad, 4, hipMemcpyDeviceToHost, st), "flag read");
+    if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "sync");
+    (void)hipFree(jobs_dev);
+    (void)hipFree(aux);
+    if (!rc && badv) rc = set_error(ctx, HK_E_NONFINITE, "synthetic pack produced a non-finite scale");
+    return rc;
+}
+
+extern "C" int hk_moe_model_bytes(const hk_moe_model* m, size_t* device_bytes, size_t* dense_bytes_per_layer) {
+    if (!m) return HK_E_INVALID_ARG;
+    size_t dev = 0;
+    for (const auto& L : m->layers) dev += L.slab_bytes;
+    dev += dense_per_layer(m->cfg) * m->cfg.n_layers;
+    if (device_bytes) *device_bytes = dev;
+    if (dense_bytes_per_layer)
+        *dense_bytes_per_layer = (size_t)m->cfg.hidden * 4 * (1 + (m->cfg.shared_gate ? 1 : 0)) +
+                                 (size_t)m->cfg.n_experts * m->cfg.hidden * 4;
+    return HK_OK;
+}
+
+extern "C" int hk_moe_expert_bytes(const hk_moe_model* m, uint32_t layer, uint32_t expert, size_t* bytes) {
+    if (!m || !bytes || layer >= m->cfg.n_layers || expert > m->cfg.n_experts) return HK_E_INVALID_ARG;
+    const MoeLayerHost& L = m->layers[layer];
+    if (expert == m->cfg.n_experts && !m->cfg.shared_inter) return HK_E_INVALID_ARG;
+    *bytes = L.packed[expert * 3] + L.packed[expert * 3 + 1] + L.packed[expert * 3 + 2];
+    return HK_OK;
+}
+
+static int moe_layer_dev(hk_ctx* ctx, hk_moe_model* m, uint32_t layer, MoeLayerDev* out) {
+    if (layer >= m->cfg.n_layers) return set_error(ctx, HK_E_INVALID_ARG, "layer index out of range");
+    MoeLayerHost& L = m->layers[layer];
+    if (!L.ready) return set_error(ctx, HK_E_INVALID_ARG, "layer " + std::to_string(layer) + " has no weights");
+    *out = MoeLayerDev{L.norm_w, L.router_w, (m->cfg.shared_gate && m->cfg.shared_inter) ? L.gate_w : nullptr, L.table_dev};
+    return HK_OK;
+}
+
+extern "C" int hk_moe_decode_layer(hk_ctx* ctx, hk_moe_model* m, uint32_t layer, const float* h_in, float* h_out,
+                                   int32_t* ids, float* weights, hk_stream stream) {
+    if (!ctx || !m) return HK_E_INVALID_ARG;
+    if (!h_in || !h_out || h_in == h_out) return set_error(ctx, HK_E_INVALID_ARG, "moe layer: h_in/h_out NULL or aliased");
+    MoeLayerDev L;
+    int rc = moe_layer_dev(ctx, m, layer, &L);
+    if (rc) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    rc = check_hip(ctx, launch_moe_layer(m->cfg.expert_kind, m->dims, L, h_in, h_out, m->ws, st), "moe layer launch");
+    if (rc) return rc;
+    const size_t kb = (size_t)m->cfg.top_k * 4;
+    if (ids) rc = check_hip(ctx, hipMemcpyAsync(ids, m->ws.ids, kb, hipMemcpyDeviceToDevice, st), "ids copy");
+    if (!rc && weights) rc = check_hip(ctx, hipMemcpyAsync(weights, m->ws.weights, kb, hipMemcpyDeviceToDevice, st), "weights copy");
+    return rc;
+}
+
+extern "C" int hk_moe_decode_stack(hk_ctx* ctx, hk_moe_model* m, const float* h_in, float* h_out, int32_t* ids,
+                                   float* weights, hk_stream stream) {
+    if (!ctx || !m) return HK_E_INVALID_ARG;
+    if (!h_in || !h_out) return set_error(ctx, HK_E_INVALID_ARG, "moe stack: NULL h_in/h_out");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const uint32_t n = m->cfg.n_layers;
+    const size_t kb = (size_t)m->cfg.top_k * 4;
+    const float* cur = h_in;
+    for (uint32_t l = 0; l < n; ++l) {
+        MoeLayerDev L;
+        int rc = moe_layer_dev(ctx, m, l, &L);
+        if (rc) return rc;
+        float* dst = (l == n - 1) ? h_out : m->hbuf[l & 1];
+        rc = check_hip(ctx, launch_moe_layer(m->cfg.expert_kind, m->dims, L, cur, dst, m->ws, st), "moe layer launch");
+        if (!rc && ids) rc = check_hip(ctx, hipMemcpyAsync(ids + (size_t)l * m->cfg.top_k, m->ws.ids, kb, hipMemcpyDeviceToDevice, st), "ids copy");
+        if (!rc && weights)
+            rc = check_hip(ctx, hipMemcpyAsync(weights + (size_t)l * m->cfg.top_k, m->ws.weights, kb, hipMemcpyDeviceToDevice, st),
+                           "weights copy");
+        if (rc) return rc;
+        cur = dst;
+    }
+    return HK_OK;
+}

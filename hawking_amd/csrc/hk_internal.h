@@ -1,0 +1,106 @@
+// hk_internal.h -- shared host/device definitions of the HIP library.
+//
+// Device-side layouts (all little-endian, all device memory owned by the
+// library unless a caller passes its own pointers):
+//
+//   Q4 organ   (kind HK_Q4, group G in {32,64,128}): canonical SoA, as the
+//              reference's HQ30UQ4 body: f16 scales[rows*cols/G] then
+//              u8 codes[rows*cols/2]; element e -> byte e/2, even e in the
+//              low nibble, value (nibble-8)*scale[e/G].
+//   BIN organ  (kind HK_BIN, group 128): HGRAVB01 body: f16 scales[rows*cols/128]
+//              then u8 signs[rows*cols/8], bit (e&7) of byte e>>3, 1 -> +scale.
+//   MIXED      (kind HK_MIXED): tags bitmap (1 = binary, LSB-first over flat
+//              128-groups) + binary section (f16 scale, 16 B signs per group)
+//              + Q2 section (2 f16 scales, 32 B 2-bit codes per group), plus two
+//              u32[rows+1] prefix tables giving each row's first binary and Q2
+//              group, so a row is addressable without a scan.
+//   F32 dense  (kind HK_F32): row-major f32[rows*cols].
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/hawking_hip.h"
+
+namespace hk {
+
+// ------------------------------------------------------------------ device organ view
+
+struct OrganView {
+    int32_t kind;
+    int32_t group;
+    uint32_t rows;
+    uint32_t cols;
+    const uint16_t* scales;     // Q4 / BIN scales, MIXED binary scales
+    const uint8_t* codes;       // Q4 codes, BIN signs, MIXED binary signs
+    const uint8_t* tags;        // MIXED
+    const uint16_t* q2_scales;  // MIXED
+    const uint8_t* q2_codes;    // MIXED
+    const uint32_t* row_bin;    // MIXED, [rows+1]
+    const uint32_t* row_q2;     // MIXED, [rows+1]
+    const float* dense;         // F32
+};
+
+// ------------------------------------------------------------------ device helpers
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, b));
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+}
+
+// Full-wave (64 lanes) sum; every lane gets the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// ------------------------------------------------------------------ host error plumbing
+
+struct Status {
+    int code = HK_OK;
+    std::string msg;
+};
+
+}  // namespace hk
+
+// Context: one per host thread (not thread-safe), bound to one device.
+struct hk_ctx {
+    int device = 0;
+    int last_status = HK_OK;
+    std::string last_error;
+    // Library-owned device scratch reused across calls (grown on demand).
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
+    // Device word that kernels OR error bits into (read by hk_check_device_status).
+    uint32_t* dev_status = nullptr;
+};
+
+namespace hk {
+
+int set_error(hk_ctx* ctx, int code, const std::string& msg);
+int check_hip(hk_ctx* ctx, hipError_t e, const char* what);
+// Grows ctx->scratch to at least `bytes` (device memory, 256-B aligned).
+int ensure_scratch(hk_ctx* ctx, size_t bytes, void** out);
+
+// Kernel launchers (defined in the .hip files); all stream-ordered, no sync.
+hipError_t launch_gemv(const OrganView& o, const float* x, float* y, hipStream_t s);
+hipError_t launch_gemv_batch(const OrganView* organs_dev, uint32_t n, int kind, uint32_t rows,
+                             uint32_t cols, int group, const float* x, size_t x_stride,
+                             float* y, size_t y_stride, hipStream_t s);
+hipError_t launch_decode_rows(const OrganView& o, uint32_t row0, uint32_t nrows, float* out,
+                              hipStream_t s);
+
+}  // namespace hk

@@ -1,0 +1,331 @@
+// hk_pack.hip -- device packers and the synthetic weight generator.
+//
+// Bit-exact with the reference packers: every f32 step is a separate IEEE
+// operation (FP contraction is off for this file), divisions are correctly
+// rounded (__fdiv_rn), f32->f16 is the hardware round-to-nearest-even
+// conversion, rint is roundTiesToEven, and the binary scale is the f64 mean
+// rounded to f32 and then to f16 (two roundings), as in pack_binary_group
+// (crates/hawking-core/src/model/qwen_complete_binary/q80_mixed_decode.rs:185-230).
+#pragma clang fp contract(off)
+
+#include "hk_internal.h"
+#include "hk_synth.h"
+
+namespace hk {
+
+// ------------------------------------------------------------------ one group
+
+// pack_uniform_q4_group64 (qwen80_uniform_q4.rs:190-278), one group of G.
+template <typename Src>
+__device__ void q4_pack_group(const Src& src, int G, uint16_t* scale_out, uint8_t* codes_out,
+                              uint32_t* bad) {
+    float max_abs = 0.0f;
+    for (int i = 0; i < G; ++i) {
+        const float v = src(i);
+        if (!isfinite(v)) *bad = 1u;
+        max_abs = fmaxf(max_abs, fabsf(v));
+    }
+    const uint16_t sb = f32_to_f16_bits(__fdiv_rn(max_abs, 7.0f));
+    if ((sb & 0x7C00u) == 0x7C00u) *bad = 1u;
+    const float rs = f16_bits_to_f32(sb);
+    *scale_out = sb;
+    for (int i = 0; i < G; i += 8) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            int q = 0;
+            if (rs != 0.0f) {
+                float r = rintf(__fdiv_rn(src(i + k), rs));
+                r = fminf(fmaxf(r, -8.0f), 7.0f);
+                q = (int)r;
+            }
+            word |= (uint32_t)(q + 8) << (4 * k);
+        }
+        reinterpret_cast<uint32_t*>(codes_out)[i >> 3] = word;
+    }
+}
+
+// pack_binary_group (q80_mixed_decode.rs:185-230), one group of 128.
+template <typename Src>
+__device__ void bin_pack_group(const Src& src, uint16_t* scale_out, uint8_t* signs_out,
+                               uint32_t* bad) {
+    double sum_abs = 0.0;
+    uint32_t words[4] = {0, 0, 0, 0};
+    for (int i = 0; i < 128; ++i) {
+        const float v = src(i);
+        if (!isfinite(v)) *bad = 1u;
+        sum_abs += (double)fabsf(v);
+        if (v >= 0.0f) words[i >> 5] |= 1u << (i & 31);
+    }
+    const double mean = sum_abs / 128.0;
+    *scale_out = f32_to_f16_bits((float)mean);
+    *reinterpret_cast<uint4*>(signs_out) = make_uint4(words[0], words[1], words[2], words[3]);
+}
+
+// Q2 base stage (ascension_dual_gravity_worker.py:898-911), one group of 64.
+template <typename Src>
+__device__ void q2_pack_group(const Src& src, uint16_t* scale_out, uint8_t* codes_out,
+                              uint32_t* bad) {
+    float max_abs = 0.0f;
+    for (int i = 0; i < 64; ++i) {
+        const float v = src(i);
+        if (!isfinite(v)) *bad = 1u;
+        max_abs = fmaxf(max_abs, fabsf(v));
+    }
+    const uint16_t sb = f32_to_f16_bits(__fdiv_rn(max_abs, 1.5f));
+    const float sf = f16_bits_to_f32(sb);
+    const float denom = sf > 0.0f ? sf : 1.0f;
+    *scale_out = sb;
+    uint32_t words[4] = {0, 0, 0, 0};
+    for (int i = 0; i < 64; ++i) {
+        const float n = __fdiv_rn(src(i), denom);
+        float r = rintf(n + 1.5f);
+        r = fminf(fmaxf(r, 0.0f), 3.0f);
+        words[i >> 4] |= (uint32_t)r << (2 * (i & 15));
+    }
+    *reinterpret_cast<uint4*>(codes_out) = make_uint4(words[0], words[1], words[2], words[3]);
+}
+
+struct BufSrc {
+    const float* p;
+    __device__ float operator()(int i) const { return p[i]; }
+};
+
+struct SynthSrc {
+    uint64_t key;
+    uint64_t base;
+    float sigma;
+    __device__ float operator()(int i) const { return synth_normal(key, base + (uint64_t)i, sigma); }
+};
+
+// ------------------------------------------------------------------ packers over f32 buffers
+
+__global__ void pack_q4_kernel(const float* __restrict__ w, size_t groups, int G,
+                               uint16_t* __restrict__ scales, uint8_t* __restrict__ codes,
+                               uint32_t* bad) {
+    for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < groups;
+         g += (size_t)gridDim.x * blockDim.x) {
+        uint32_t b = 0;
+        q4_pack_group(BufSrc{w + g * G}, G, scales + g, codes + g * (G / 2), &b);
+        if (b) atomicOr(bad, 1u);
+    }
+}
+
+__global__ void pack_bin_kernel(const float* __restrict__ w, size_t groups,
+                                uint16_t* __restrict__ scales, uint8_t* __restrict__ signs,
+                                uint32_t* bad) {
+    for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < groups;
+         g += (size_t)gridDim.x * blockDim.x) {
+        uint32_t b = 0;
+        bin_pack_group(BufSrc{w + g * 128}, scales + g, signs + g * 16, &b);
+        if (b) atomicOr(bad, 1u);
+    }
+}
+
+__global__ void pack_q2_kernel(const float* __restrict__ w, size_t groups,
+                               uint16_t* __restrict__ scales, uint8_t* __restrict__ codes,
+                               uint32_t* bad) {
+    for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < groups;
+         g += (size_t)gridDim.x * blockDim.x) {
+        uint32_t b = 0;
+        q2_pack_group(BufSrc{w + g * 64}, scales + g, codes + g * 16, &b);
+        if (b) atomicOr(bad, 1u);
+    }
+}
+
+__global__ void synth_normal_kernel(uint64_t key, uint64_t first, size_t count, float sigma,
+                                    float* __restrict__ out) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+         i += (size_t)gridDim.x * blockDim.x)
+        out[i] = synth_normal(key, first + i, sigma);
+}
+
+static unsigned grid_for(size_t n, unsigned block) {
+    size_t b = (n + block - 1) / block;
+    if (b > 1u << 20) b = 1u << 20;
+    return (unsigned)(b ? b : 1);
+}
+
+hipError_t launch_pack_q4(const float* w, size_t groups, int G, uint16_t* scales, uint8_t* codes,
+                          uint32_t* bad, hipStream_t s) {
+    hipLaunchKernelGGL(pack_q4_kernel, dim3(grid_for(groups, 256)), dim3(256), 0, s, w, groups, G,
+                       scales, codes, bad);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack_bin(const float* w, size_t groups, uint16_t* scales, uint8_t* signs,
+                           uint32_t* bad, hipStream_t s) {
+    hipLaunchKernelGGL(pack_bin_kernel, dim3(grid_for(groups, 256)), dim3(256), 0, s, w, groups,
+                       scales, signs, bad);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack_q2(const float* w, size_t groups, uint16_t* scales, uint8_t* codes,
+                          uint32_t* bad, hipStream_t s) {
+    hipLaunchKernelGGL(pack_q2_kernel, dim3(grid_for(groups, 256)), dim3(256), 0, s, w, groups,
+                       scales, codes, bad);
+    return hipGetLastError();
+}
+
+hipError_t launch_synth_normal(uint64_t key, uint64_t first, size_t count, float sigma, float* out,
+                               hipStream_t s) {
+    hipLaunchKernelGGL(synth_normal_kernel, dim3(grid_for(count, 256)), dim3(256), 0, s, key, first,
+                       count, sigma, out);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ synthetic organs
+// Generate-and-pack without materialising f32 weights: element e of organ
+// (key) is synth_normal(key, e, sigma), so the host oracle regenerates any
+// single organ bit for bit.
+
+__global__ void synth_pack_q4_kernel(const SynthJob* __restrict__ jobs, uint32_t njobs,
+                                     uint32_t* bad) {
+    const SynthJob j = jobs[blockIdx.y];
+    const size_t groups = (size_t)j.rows * j.cols / (uint32_t)j.group;
+    for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < groups;
+         g += (size_t)gridDim.x * blockDim.x) {
+        uint32_t b = 0;
+        q4_pack_group(SynthSrc{j.key, g * (uint32_t)j.group, j.sigma}, j.group, j.scales + g,
+                      j.codes + g * (uint32_t)(j.group / 2), &b);
+        if (b) atomicOr(bad, 1u);
+    }
+    (void)njobs;
+}
+
+// Mixed, pass 1: tag words (32 flat groups per thread).
+__global__ void synth_mixed_tags_kernel(const SynthJob* __restrict__ jobs) {
+    const SynthJob j = jobs[blockIdx.y];
+    const size_t groups = (size_t)j.rows * j.cols / 128;
+    const size_t words = (groups + 31) / 32;
+    for (size_t w = (size_t)blockIdx.x * blockDim.x + threadIdx.x; w < words;
+         w += (size_t)gridDim.x * blockDim.x) {
+        uint32_t t = 0;
+        for (uint32_t b = 0; b < 32; ++b) {
+            const size_t g = w * 32 + b;
+            if (g < groups && synth_coin(j.coin_key, g)) t |= 1u << b;
+        }
+        reinterpret_cast<uint32_t*>(j.tags)[w] = t;
+    }
+}
+
+// Mixed, pass 2 (one block per organ): per-row prefix counts.
+__global__ void __launch_bounds__(1024) mixed_row_scan_kernel(const SynthJob* __restrict__ jobs) {
+    const SynthJob j = jobs[blockIdx.x];
+    __shared__ uint32_t part[1024];
+    const uint32_t gpr = j.cols / 128;
+    const uint32_t tid = threadIdx.x, nt = blockDim.x;
+    // rows handled by this thread: contiguous chunk
+    const uint32_t per = (j.rows + nt - 1) / nt;
+    const uint32_t r0 = tid * per, r1 = min(j.rows, r0 + per);
+    uint32_t local = 0;
+    for (uint32_t r = r0; r < r1; ++r)
+        for (uint32_t g = r * gpr; g < (r + 1) * gpr; ++g) local += (j.tags[g >> 3] >> (g & 7u)) & 1u;
+    part[tid] = local;
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t run = 0;
+        for (uint32_t t = 0; t < nt; ++t) {
+            const uint32_t v = part[t];
+            part[t] = run;
+            run += v;
+        }
+    }
+    __syncthreads();
+    uint32_t run = part[tid];
+    for (uint32_t r = r0; r < r1; ++r) {
+        j.row_bin[r] = run;
+        j.row_q2[r] = r * gpr - run;
+        for (uint32_t g = r * gpr; g < (r + 1) * gpr; ++g) run += (j.tags[g >> 3] >> (g & 7u)) & 1u;
+    }
+    if (r1 == j.rows && r0 < r1) {
+        j.row_bin[j.rows] = run;
+        j.row_q2[j.rows] = j.rows * gpr - run;
+    }
+    if (j.rows == 0 && tid == 0) {
+        j.row_bin[0] = 0;
+        j.row_q2[0] = 0;
+    }
+}
+
+// Mixed, pass 3: thread per (row, group) generates and packs its group.
+__global__ void synth_mixed_pack_kernel(const SynthJob* __restrict__ jobs, uint32_t* bad) {
+    const SynthJob j = jobs[blockIdx.y];
+    const uint32_t gpr = j.cols / 128;
+    const size_t groups = (size_t)j.rows * gpr;
+    for (size_t fg = (size_t)blockIdx.x * blockDim.x + threadIdx.x; fg < groups;
+         fg += (size_t)gridDim.x * blockDim.x) {
+        const uint32_t r = (uint32_t)(fg / gpr), g = (uint32_t)(fg % gpr);
+        uint32_t nb = 0;
+        for (uint32_t h = r * gpr; h < (uint32_t)fg; ++h) nb += (j.tags[h >> 3] >> (h & 7u)) & 1u;
+        uint32_t b = 0;
+        if ((j.tags[fg >> 3] >> (fg & 7u)) & 1u) {
+            const uint32_t idx = j.row_bin[r] + nb;
+            bin_pack_group(SynthSrc{j.key, fg * 128, j.sigma}, j.scales + idx,
+                           j.codes + (size_t)idx * 16, &b);
+        } else {
+            const uint32_t idx = j.row_q2[r] + (g - nb);
+            q2_pack_group(SynthSrc{j.key, fg * 128, j.sigma}, j.q2_scales + 2 * idx,
+                          j.q2_codes + (size_t)idx * 32, &b);
+            q2_pack_group(SynthSrc{j.key, fg * 128 + 64, j.sigma}, j.q2_scales + 2 * idx + 1,
+                          j.q2_codes + (size_t)idx * 32 + 16, &b);
+        }
+        if (b) atomicOr(bad, 1u);
+    }
+}
+
+// Mixed: count binary groups per organ (for exact allocation).
+__global__ void synth_mixed_count_kernel(const SynthJob* __restrict__ jobs, uint32_t* counts) {
+    const SynthJob j = jobs[blockIdx.y];
+    const size_t groups = (size_t)j.rows * j.cols / 128;
+    uint32_t local = 0;
+    for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < groups;
+         g += (size_t)gridDim.x * blockDim.x)
+        local += synth_coin(j.coin_key, g) ? 1u : 0u;
+    for (int off = 32; off >= 1; off >>= 1) local += __shfl_xor(local, off, 64);
+    if ((threadIdx.x & 63) == 0 && local) atomicAdd(counts + blockIdx.y, local);
+}
+
+__global__ void synth_dense_kernel(const SynthJob* __restrict__ jobs) {
+    const SynthJob j = jobs[blockIdx.y];
+    const size_t n = (size_t)j.rows * j.cols;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        j.dense[i] = synth_normal(j.key, i, j.sigma);
+}
+
+hipError_t launch_synth_jobs(int kind, const SynthJob* jobs_dev, uint32_t njobs,
+                             size_t max_groups, uint32_t* bad, hipStream_t s) {
+    const unsigned bx = (unsigned)((max_groups + 255) / 256 < 4096 ? (max_groups + 255) / 256 : 4096);
+    switch (kind) {
+    case HK_Q4:
+        hipLaunchKernelGGL(synth_pack_q4_kernel, dim3(bx ? bx : 1, njobs), dim3(256), 0, s, jobs_dev,
+                           njobs, bad);
+        break;
+    case HK_MIXED: {
+        const size_t words = (max_groups + 31) / 32;
+        const unsigned tx = (unsigned)((words + 255) / 256 < 4096 ? (words + 255) / 256 : 4096);
+        hipLaunchKernelGGL(synth_mixed_tags_kernel, dim3(tx ? tx : 1, njobs), dim3(256), 0, s, jobs_dev);
+        hipLaunchKernelGGL(mixed_row_scan_kernel, dim3(njobs), dim3(1024), 0, s, jobs_dev);
+        hipLaunchKernelGGL(synth_mixed_pack_kernel, dim3(bx ? bx : 1, njobs), dim3(256), 0, s, jobs_dev,
+                           bad);
+        break;
+    }
+    case HK_F32:
+        hipLaunchKernelGGL(synth_dense_kernel, dim3(bx ? bx : 1, njobs), dim3(256), 0, s, jobs_dev);
+        break;
+    default:
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_synth_mixed_count(const SynthJob* jobs_dev, uint32_t njobs, size_t max_groups,
+                                    uint32_t* counts, hipStream_t s) {
+    const unsigned bx = (unsigned)((max_groups + 255) / 256 < 1024 ? (max_groups + 255) / 256 : 1024);
+    hipLaunchKernelGGL(synth_mixed_count_kernel, dim3(bx ? bx : 1, njobs), dim3(256), 0, s, jobs_dev,
+                       counts);
+    return hipGetLastError();
+}
+
+}  // namespace hk

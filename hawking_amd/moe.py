@@ -1,0 +1,179 @@
+"""Routers and the MoE decode step on the GPU.
+
+Mirrors the reference's routing and MoE-suffix API:
+  * source_qwen80_topk_router (crates/hawking-core/src/model/qwen80_complete_runtime.rs:5970-6025)
+  * topk_softmax_batch        (crates/hawking-core/src/kernels/mod.rs:342-374)
+  * noaux_tc router           (crates/hawking-core/src/gravity_glm.rs:447-500)
+  * moe_suffix                (crates/hawking-core/src/model/qwen80_uniform_q4_hybrid_decode.rs:2615-2757)
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from ._lib import HK_MIXED, HK_Q4, MoeConfig, MoeLayerSrc, OrganSrc
+from .runtime import Context, DeviceArray
+
+
+def _dev(ctx: Context, a) -> DeviceArray:
+    return a if isinstance(a, DeviceArray) else ctx.to_device(np.ascontiguousarray(a, np.float32))
+
+
+def topk_router(ctx: Context, logits, top_k: int, tie_eps: float = 0.0, renorm: bool = True,
+                n_tokens: int = 1):
+    """Softmax top-k on device; returns (ids, weights) as numpy (synchronises)."""
+    ld = _dev(ctx, logits)
+    n_experts = ld.shape[-1] if n_tokens == 1 else ld.shape[-1]
+    ids = ctx.empty(n_tokens * top_k, np.int32)
+    w = ctx.empty(n_tokens * top_k, np.float32)
+    ctx.call("hk_router_softmax_topk", ld.ptr, n_tokens, n_experts, top_k, tie_eps, int(renorm),
+             ids.ptr, w.ptr, ctx.stream)
+    return ids.download().reshape(n_tokens, top_k), w.download().reshape(n_tokens, top_k)
+
+
+def source_qwen80_topk_router(ctx: Context, logits, top_k: int = 10):
+    ids, w = topk_router(ctx, logits, top_k, 0.0, True)
+    return ids[0], w[0]
+
+
+def noaux_tc_router(ctx: Context, logits, bias, n_group: int, topk_group: int, top_k: int,
+                    norm_topk_prob: bool = True, routed_scaling_factor: float = 1.0, n_tokens: int = 1):
+    ld = _dev(ctx, logits)
+    bd = _dev(ctx, bias)
+    n_experts = int(np.prod(ld.shape)) // n_tokens
+    ids = ctx.empty(n_tokens * top_k, np.int32)
+    w = ctx.empty(n_tokens * top_k, np.float32)
+    ctx.call("hk_router_noaux_tc", ld.ptr, bd.ptr, n_tokens, n_experts, n_group, topk_group, top_k,
+             int(norm_topk_prob), routed_scaling_factor, ids.ptr, w.ptr, ctx.stream)
+    return ids.download().reshape(n_tokens, top_k), w.download().reshape(n_tokens, top_k)
+
+
+# stream-id projections (hk_moe_stream_id)
+PROJ_GATE, PROJ_UP, PROJ_DOWN = 0, 1, 2
+PROJ_NORM, PROJ_ROUTER, PROJ_SHARED_GATE, PROJ_COIN = 16, 17, 18, 32
+
+
+def moe_stream_id(layer: int, expert: int, proj: int) -> int:
+    return ((layer + 1) << 40) | (expert << 8) | proj
+
+
+@dataclass
+class MoeShape:
+    n_layers: int = 1
+    hidden: int = 2048
+    inter: int = 512
+    shared_inter: int = 512
+    n_experts: int = 512
+    top_k: int = 10
+    expert_kind: int = HK_Q4
+    expert_group: int = 32
+    shared_gate: bool = True
+    eps: float = 1e-6
+
+
+class MoeModel:
+    """Device-resident MoE stack: per layer RMSNorm(1+w) weight, f32 router,
+    optional shared-expert gate, and the packed expert table."""
+
+    def __init__(self, ctx: Context, shape: MoeShape):
+        self.ctx, self.shape = ctx, shape
+        cfg = MoeConfig(shape.n_layers, shape.hidden, shape.inter, shape.shared_inter, shape.n_experts,
+                        shape.top_k, shape.expert_kind, shape.expert_group, int(shape.shared_gate), shape.eps)
+        h = C.c_void_p()
+        ctx.call("hk_moe_model_create", C.byref(cfg), C.byref(h))
+        self.h = h
+
+    def free(self):
+        if getattr(self, "h", None) and self.h.value and self.ctx.h:
+            self.ctx.L.hk_moe_model_free(self.ctx.h, self.h)
+        self.h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def fill_synthetic(self, seed: int) -> None:
+        self.ctx.call("hk_moe_model_fill_synthetic", self.h, seed, self.ctx.stream)
+
+    def set_layer(self, layer: int, norm_w, router_w, experts, shared=None, shared_gate_w=None) -> None:
+        """experts: list over expert id of (gate, up, down) canonical organ dicts
+        (see organ_src); shared likewise or None."""
+        keep = []
+
+        def arr(a, dt):
+            a = np.ascontiguousarray(a, dt)
+            keep.append(a)
+            return a.ctypes.data
+
+        def src(d) -> OrganSrc:
+            if d["kind"] == HK_Q4:
+                return OrganSrc(kind=HK_Q4, group=d["group"], rows=d["rows"], cols=d["cols"],
+                                scales=arr(d["scales"], np.uint16), codes=arr(d["codes"], np.uint8))
+            return OrganSrc(kind=HK_MIXED, group=128, rows=d["rows"], cols=d["cols"],
+                            tags=arr(d["tags"], np.uint8),
+                            scales=arr(d["bin_scales"], np.uint16) if d["bin_scales"].size else None,
+                            codes=arr(d["bin_signs"], np.uint8) if d["bin_signs"].size else None,
+                            q2_scales=arr(d["q2_scales"], np.uint16) if d["q2_scales"].size else None,
+                            q2_codes=arr(d["q2_codes"], np.uint8) if d["q2_codes"].size else None,
+                            n_bin=d["bin_scales"].size, n_q2=d["q2_scales"].size // 2)
+
+        ex = (OrganSrc * (len(experts) * 3))()
+        for e, trip in enumerate(experts):
+            for j in range(3):
+                ex[e * 3 + j] = src(trip[j])
+        sh = None
+        if shared is not None:
+            sh = (OrganSrc * 3)(*[src(d) for d in shared])
+        L = MoeLayerSrc(arr(norm_w, np.float32), arr(router_w, np.float32),
+                        arr(shared_gate_w, np.float32) if shared_gate_w is not None else None,
+                        C.cast(ex, C.c_void_p), C.cast(sh, C.c_void_p) if sh is not None else None)
+        self.ctx.call("hk_moe_model_set_layer", self.h, layer, C.byref(L), self.ctx.stream)
+
+    def expert_bytes(self, layer: int, expert: int) -> int:
+        b = C.c_size_t()
+        self.ctx.check("hk_moe_expert_bytes", self.ctx.L.hk_moe_expert_bytes(self.h, layer, expert, C.byref(b)))
+        return int(b.value)
+
+    def model_bytes(self) -> tuple[int, int]:
+        a, b = C.c_size_t(), C.c_size_t()
+        self.ctx.check("hk_moe_model_bytes", self.ctx.L.hk_moe_model_bytes(self.h, C.byref(a), C.byref(b)))
+        return int(a.value), int(b.value)
+
+    # -- decode -----------------------------------------------------------------------
+    def decode_layer_device(self, layer: int, h_in: DeviceArray, h_out: DeviceArray,
+                            ids: DeviceArray | None = None, weights: DeviceArray | None = None,
+                            stream=None) -> None:
+        self.ctx.call("hk_moe_decode_layer", self.h, layer, h_in.ptr, h_out.ptr,
+                      ids.ptr if ids is not None else None, weights.ptr if weights is not None else None,
+                      stream if stream is not None else self.ctx.stream)
+
+    def decode_stack_device(self, h_in: DeviceArray, h_out: DeviceArray, ids: DeviceArray | None = None,
+                            weights: DeviceArray | None = None, stream=None) -> None:
+        self.ctx.call("hk_moe_decode_stack", self.h, h_in.ptr, h_out.ptr,
+                      ids.ptr if ids is not None else None, weights.ptr if weights is not None else None,
+                      stream if stream is not None else self.ctx.stream)
+
+    def moe_suffix(self, layer: int, h: np.ndarray):
+        """One layer on numpy input: returns (out, ids, weights)."""
+        hd = self.ctx.to_device(np.ascontiguousarray(h, np.float32))
+        out = self.ctx.empty(self.shape.hidden)
+        ids = self.ctx.empty(self.shape.top_k, np.int32)
+        w = self.ctx.empty(self.shape.top_k, np.float32)
+        self.decode_layer_device(layer, hd, out, ids, w)
+        return out.download(), ids.download(), w.download()
+
+    def forward_token(self, h: np.ndarray):
+        """All layers: returns (out, ids[n_layers, k], weights[n_layers, k])."""
+        s = self.shape
+        hd = self.ctx.to_device(np.ascontiguousarray(h, np.float32))
+        out = self.ctx.empty(s.hidden)
+        ids = self.ctx.empty(s.n_layers * s.top_k, np.int32)
+        w = self.ctx.empty(s.n_layers * s.top_k, np.float32)
+        self.decode_stack_device(hd, out, ids, w)
+        return (out.download(), ids.download().reshape(s.n_layers, s.top_k),
+                w.download().reshape(s.n_layers, s.top_k))

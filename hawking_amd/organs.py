@@ -1,0 +1,184 @@
+"""Packed matvec organs on the GPU, mirroring hawking-core's organ API.
+
+Reference names are kept where the reference has them:
+  * Qwen80Q4PackedTensor.matvec / gather_row
+    (crates/hawking-core/src/model/qwen80_uniform_q4_hybrid_decode.rs:900-1036)
+  * BinaryGroupPacked + binary_group_matvec_f32
+    (crates/hawking-core/src/model/qwen_complete_binary/q80_mixed_decode.rs:48-257)
+  * MixedPackedTensor (q80_mixed_decode.rs:1073-1417)
+Every matvec runs the gfx950 kernels through the C ABI; the inputs are the
+reference's canonical packed bytes, uploaded and repacked once.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from ._lib import HK_BIN, HK_F32, HK_MIXED, HK_Q4, OrganSrc
+from .runtime import Context, DeviceArray
+
+
+def _ptr(a):
+    return None if a is None else np.ascontiguousarray(a).ctypes.data
+
+
+class PackedOrgan:
+    """One packed matrix resident in device memory (library-owned)."""
+
+    kind: int = -1
+
+    def __init__(self, ctx: Context, src: OrganSrc, keep: tuple):
+        self.ctx = ctx
+        h = C.c_void_p()
+        ctx.call("hk_organ_upload", C.byref(src), ctx.stream, C.byref(h))
+        self.h = h
+        self.rows, self.cols, self.group = int(src.rows), int(src.cols), int(src.group)
+        del keep  # host buffers only had to outlive the synchronous upload
+        sz = C.c_size_t()
+        ctx.check("hk_organ_info", ctx.L.hk_organ_info(h, None, None, None, None, C.byref(sz)))
+        self.packed_bytes = int(sz.value)
+
+    def free(self):
+        if getattr(self, "h", None) and self.h.value and self.ctx.h:
+            self.ctx.L.hk_organ_free(self.ctx.h, self.h)
+        self.h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    # -- device-pointer API --------------------------------------------------------
+    def matvec_device(self, x: DeviceArray | C.c_void_p, y: DeviceArray | C.c_void_p, stream=None) -> None:
+        xp = x.ptr if isinstance(x, DeviceArray) else x
+        yp = y.ptr if isinstance(y, DeviceArray) else y
+        self.ctx.call("hk_gemv", self.h, xp, yp, stream if stream is not None else self.ctx.stream)
+
+    def decode_rows_device(self, row0: int, nrows: int, out: DeviceArray, stream=None) -> None:
+        self.ctx.call("hk_decode_rows", self.h, row0, nrows, out.ptr,
+                      stream if stream is not None else self.ctx.stream)
+
+    # -- numpy convenience (uploads, runs, synchronises) -----------------------------
+    def matvec(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        if x.shape != (self.cols,):
+            raise ValueError(f"matvec input {x.shape} != cols {self.cols}")
+        xd = self.ctx.to_device(x)
+        yd = self.ctx.empty(self.rows)
+        self.matvec_device(xd, yd)
+        return yd.download()
+
+    def decode(self, row0: int = 0, nrows: int | None = None) -> np.ndarray:
+        nrows = self.rows - row0 if nrows is None else nrows
+        out = self.ctx.empty((nrows, self.cols))
+        self.decode_rows_device(row0, nrows, out)
+        return out.download()
+
+    def gather_row(self, row: int) -> np.ndarray:
+        return self.decode(row, 1)[0]
+
+
+class Qwen80Q4PackedTensor(PackedOrgan):
+    """Uniform Q4 (HQ30UQ4 semantics), group 32/64/128."""
+
+    kind = HK_Q4
+
+    def __init__(self, ctx: Context, scales: np.ndarray, codes: np.ndarray, rows: int, cols: int,
+                 group: int):
+        scales = np.ascontiguousarray(scales, np.uint16)
+        codes = np.ascontiguousarray(codes, np.uint8)
+        if scales.size != rows * cols // max(group, 1) or codes.size != rows * cols // 2:
+            raise ValueError("Q4 scales/codes sizes disagree with the shape")
+        src = OrganSrc(kind=HK_Q4, group=group, rows=rows, cols=cols, scales=_ptr(scales), codes=_ptr(codes))
+        super().__init__(ctx, src, (scales, codes))
+
+
+class BinaryGroupPacked(PackedOrgan):
+    """Binary sign plane, group 128 (HGRAVB01 body)."""
+
+    kind = HK_BIN
+
+    def __init__(self, ctx: Context, scales: np.ndarray, signs: np.ndarray, rows: int, cols: int):
+        scales = np.ascontiguousarray(scales, np.uint16)
+        signs = np.ascontiguousarray(signs, np.uint8)
+        if scales.size != rows * cols // 128 or signs.size != rows * cols // 8:
+            raise ValueError("binary scales/signs sizes disagree with the shape")
+        src = OrganSrc(kind=HK_BIN, group=128, rows=rows, cols=cols, scales=_ptr(scales), codes=_ptr(signs))
+        super().__init__(ctx, src, (scales, signs))
+
+
+def binary_group_matvec_f32(packed: BinaryGroupPacked, x: np.ndarray) -> np.ndarray:
+    """GPU counterpart of binary_group_matvec_f32 (q80_mixed_decode.rs:245-257)."""
+    return packed.matvec(x)
+
+
+class MixedPackedTensor(PackedOrgan):
+    """Per-128-group binary | Q2 organ from the canonical mixed stream."""
+
+    kind = HK_MIXED
+
+    def __init__(self, ctx: Context, rows: int, cols: int, tags: np.ndarray, bin_scales: np.ndarray,
+                 bin_signs: np.ndarray, q2_scales: np.ndarray, q2_codes: np.ndarray):
+        arrs = [np.ascontiguousarray(a, dt) for a, dt in
+                ((tags, np.uint8), (bin_scales, np.uint16), (bin_signs, np.uint8),
+                 (q2_scales, np.uint16), (q2_codes, np.uint8))]
+        tags, bs, bg, qs, qc = arrs
+        src = OrganSrc(kind=HK_MIXED, group=128, rows=rows, cols=cols, scales=_ptr(bs) if bs.size else None,
+                       codes=_ptr(bg) if bg.size else None, tags=_ptr(tags),
+                       q2_scales=_ptr(qs) if qs.size else None, q2_codes=_ptr(qc) if qc.size else None,
+                       n_bin=bs.size, n_q2=qs.size // 2)
+        super().__init__(ctx, src, tuple(arrs))
+
+
+class DenseF32Organ(PackedOrgan):
+    kind = HK_F32
+
+    def __init__(self, ctx: Context, w: np.ndarray):
+        w = np.ascontiguousarray(w, np.float32)
+        rows, cols = w.shape
+        src = OrganSrc(kind=HK_F32, group=0, rows=rows, cols=cols, dense=_ptr(w))
+        super().__init__(ctx, src, (w,))
+
+
+def gemv_batch(ctx: Context, organs: list[PackedOrgan], x: DeviceArray, x_stride: int, y: DeviceArray,
+               y_stride: int, stream=None) -> None:
+    """y_i = W_i x_i for organs of one kind and shape, in one launch."""
+    arr = (C.c_void_p * len(organs))(*[o.h.value for o in organs])
+    ctx.call("hk_gemv_batch", arr, len(organs), x.ptr, x_stride, y.ptr, y_stride,
+             stream if stream is not None else ctx.stream)
+
+
+# ---------------------------------------------------------------- device packers / generator
+
+def pack_q4_device(ctx: Context, w: DeviceArray, rows: int, cols: int, group: int):
+    scales = ctx.empty(rows * cols // group, np.uint16)
+    codes = ctx.empty(rows * cols // 2, np.uint8)
+    ctx.call("hk_pack_q4", w.ptr, rows, cols, group, scales.ptr, codes.ptr, ctx.stream)
+    return scales, codes
+
+
+def pack_binary_group_device(ctx: Context, w: DeviceArray, rows: int, cols: int):
+    scales = ctx.empty(rows * cols // 128, np.uint16)
+    signs = ctx.empty(rows * cols // 8, np.uint8)
+    ctx.call("hk_pack_bin", w.ptr, rows, cols, scales.ptr, signs.ptr, ctx.stream)
+    return scales, signs
+
+
+def pack_q2_device(ctx: Context, w: DeviceArray, count: int):
+    scales = ctx.empty(count // 64, np.uint16)
+    codes = ctx.empty(count // 4, np.uint8)
+    ctx.call("hk_pack_q2", w.ptr, count, scales.ptr, codes.ptr, ctx.stream)
+    return scales, codes
+
+
+def stream_key(seed: int, stream_id: int) -> int:
+    return int(_lib.lib().hk_stream_key(seed, stream_id))
+
+
+def synth_normal(ctx: Context, key: int, count: int, sigma: float, first: int = 0) -> DeviceArray:
+    out = ctx.empty(count)
+    ctx.call("hk_synth_normal", key, first, count, sigma, out.ptr, ctx.stream)
+    return out

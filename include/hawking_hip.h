@@ -1,0 +1,251 @@
+/*
+ * hawking_hip.h -- C ABI of the MI355X (gfx950) quantized-decode library.
+ *
+ * Drop-in boundary for hawking-core's packed-organ / MoE-step compute seam.
+ * Citations are path:line inside the reference (joshuahickscorp/hawking),
+ * relative to crates/hawking-core/src/.
+ *
+ * Conventions
+ *   - Every entry point returns an int status (HK_OK or an HK_E_* code) and
+ *     records a message retrievable with hk_last_error().  Nothing falls back
+ *     to the CPU: a missing or failing GPU path is an error, never a silent
+ *     substitute (mirrors the fail-closed fallback counters,
+ *     model/qwen80_mixed_hybrid_decode.rs:4694-4699,4728-4733).
+ *   - Compute entry points take DEVICE pointers, enqueue on the given HIP
+ *     stream (hk_stream = hipStream_t; NULL = the null stream) and never
+ *     synchronise, like CommandRecorder ops that record and do not commit
+ *     (backend/mod.rs:36-41, 227-263).  Geometry is validated on the host
+ *     before any launch (the reference kernels silently no-op on bad
+ *     geometry, so its hosts validate first).
+ *   - An hk_ctx is bound to one device and is not thread-safe: one per
+ *     host thread.
+ */
+#ifndef HAWKING_HIP_H
+#define HAWKING_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  The variants of hawking_core::Error (error.rs:3-27) map as
+ * Model -> INVALID_ARG / GEOMETRY / NONFINITE / ROUTE, Metal -> HIP,
+ * Unimplemented -> UNSUPPORTED. */
+#define HK_OK 0
+#define HK_E_INVALID_ARG 1
+#define HK_E_GEOMETRY 2
+#define HK_E_NONFINITE 3
+#define HK_E_HIP 4
+#define HK_E_UNSUPPORTED 5
+#define HK_E_ROUTE 6
+#define HK_E_NOMEM 7
+
+/* Organ kinds: the WeightKind variants the reference's GemvSpec lacks for
+ * these formats (backend/mod.rs:120-137, 145-171). */
+#define HK_Q4 0    /* uniform Q4, group 32/64/128, f16 scale per group */
+#define HK_BIN 1   /* binary sign plane, group 128, f16 mean|w| per group */
+#define HK_MIXED 2 /* per-128-group binary | Q2 (two f16 scales per 64) */
+#define HK_F32 3   /* dense row-major f32 (router, shared-expert gate) */
+
+typedef struct hk_ctx hk_ctx;
+typedef struct hk_organ hk_organ;
+typedef struct hk_moe_model hk_moe_model;
+typedef void* hk_stream;
+
+/* ------------------------------------------------------------------ context */
+
+/* Replaces MetalContext construction (metal/mod.rs:1044). */
+int hk_ctx_create(int device, hk_ctx** out);
+void hk_ctx_destroy(hk_ctx* ctx);
+/* Copies the last error message (NUL-terminated, truncated to len). */
+int hk_last_error(const hk_ctx* ctx, char* buf, size_t len);
+const char* hk_version(void);
+int hk_device_info(hk_ctx* ctx, char* name, size_t len, int* cu_count, size_t* hbm_bytes);
+
+/* ------------------------------------------------ device memory and streams
+ * Plumbing for callers without their own allocator; replaces PinnedBuffer /
+ * new_buffer_with_bytes_checked (metal/mod.rs:2709-2787).  Copies are
+ * stream-ordered; pass the stream and synchronise it before reading. */
+int hk_malloc(hk_ctx* ctx, size_t bytes, void** out);
+int hk_free(hk_ctx* ctx, void* ptr);
+int hk_memcpy_htod(hk_ctx* ctx, void* dst, const void* src, size_t bytes, hk_stream stream);
+int hk_memcpy_dtoh(hk_ctx* ctx, void* dst, const void* src, size_t bytes, hk_stream stream);
+int hk_memcpy_dtod(hk_ctx* ctx, void* dst, const void* src, size_t bytes, hk_stream stream);
+int hk_memset(hk_ctx* ctx, void* dst, int value, size_t bytes, hk_stream stream);
+int hk_stream_create(hk_ctx* ctx, hk_stream* out);
+int hk_stream_destroy(hk_ctx* ctx, hk_stream stream);
+/* The only synchronising calls; TokenCommandBuffer::commit_and_wait (metal/mod.rs:5221). */
+int hk_stream_synchronize(hk_ctx* ctx, hk_stream stream);
+int hk_device_synchronize(hk_ctx* ctx);
+int hk_event_create(hk_ctx* ctx, void** out);
+int hk_event_destroy(hk_ctx* ctx, void* event);
+int hk_event_record(hk_ctx* ctx, void* event, hk_stream stream);
+int hk_event_elapsed_ms(hk_ctx* ctx, void* start, void* stop, float* ms);
+/* Synchronises `stream`, returns and clears the device error bits that
+ * kernels set when they meet invalid data (1 = non-finite input, 2 = invalid
+ * route).  The GPU-side counterpart of the reference's per-op Result
+ * checks, which cannot be returned from stream-ordered launches. */
+int hk_check_device_status(hk_ctx* ctx, hk_stream stream, uint32_t* bits);
+
+/* ------------------------------------------------------------------ organs */
+
+/* One packed matrix in the reference's canonical byte layout (HOST memory).
+ *  HK_Q4:    scales f16[rows*cols/group] || codes u8[rows*cols/2]
+ *            (HQ30UQ4 body, model/qwen_complete_binary/qwen80_uniform_q4.rs:190-278)
+ *  HK_BIN:   scales f16[rows*cols/128] || signs u8[rows*cols/8]
+ *            (HGRAVB01 body, model/qwen_complete_binary/q80_mixed_decode.rs:185-230)
+ *  HK_MIXED: tags u8[ceil(groups/8)], bin_scales f16[n_bin], bin_signs u8[16*n_bin],
+ *            q2_scales f16[2*n_q2], q2_codes u8[32*n_q2] (build-defined stream)
+ *  HK_F32:   dense f32[rows*cols]
+ * Requires cols % group == 0 (row-aligned groups). */
+typedef struct hk_organ_src {
+    int32_t kind;
+    int32_t group;
+    uint32_t rows;
+    uint32_t cols;
+    const uint16_t* scales;
+    const uint8_t* codes;
+    const uint8_t* tags;
+    const uint16_t* q2_scales;
+    const uint8_t* q2_codes;
+    uint32_t n_bin;
+    uint32_t n_q2;
+    const float* dense;
+} hk_organ_src;
+
+/* Upload + load-time repack of one organ into library-owned device memory.
+ * Replaces Qwen80Q4PackedTensor / MixedPackedTensor::from_codec_payload binds
+ * (model/qwen80_uniform_q4_hybrid_decode.rs:957; q80_mixed_decode.rs:1336)
+ * and the no-copy bind of payload windows.  Validates geometry and finiteness
+ * of every scale.  Synchronous with respect to `stream`'s prior work. */
+int hk_organ_upload(hk_ctx* ctx, const hk_organ_src* src, hk_stream stream, hk_organ** out);
+int hk_organ_free(hk_ctx* ctx, hk_organ* organ);
+int hk_organ_info(const hk_organ* organ, int32_t* kind, int32_t* group, uint32_t* rows,
+                  uint32_t* cols, size_t* packed_bytes);
+
+/* y[rows] = W x[cols], f32 in and out (device pointers).
+ * Replaces BackendGemv::gemv (backend/mod.rs:270-291) for the packed kinds and
+ * the Q4/binary matvec kernels (shaders/qwen_uniform_q4.metal:183-272,
+ * shaders/q80_mixed_decode.metal:701-741).  Numerics: within 2e-5 relative L2
+ * of Qwen80Q4PackedTensor::matvec / binary_group_matvec_f32. */
+int hk_gemv(hk_ctx* ctx, const hk_organ* organ, const float* x, float* y, hk_stream stream);
+
+/* n organs of one kind and shape in ONE launch: y_i = W_i x_i with
+ * x_i = x + i*x_stride, y_i = y + i*y_stride (element strides).  The batched
+ * form of matvec_batch (gravity_glm.rs:515-548) / the routed wave. */
+int hk_gemv_batch(hk_ctx* ctx, const hk_organ* const* organs, uint32_t n, const float* x,
+                  size_t x_stride, float* y, size_t y_stride, hk_stream stream);
+
+/* Bit-exact decode probe: out[nrows*cols] = decoded weights of rows
+ * [row0, row0+nrows).  Replaces qwen_uniform_q4_decode_vector
+ * (shaders/qwen_uniform_q4.metal:627) and gather_row
+ * (model/qwen80_uniform_q4_hybrid_decode.rs:900-911). */
+int hk_decode_rows(hk_ctx* ctx, const hk_organ* organ, uint32_t row0, uint32_t nrows,
+                   float* out, hk_stream stream);
+
+/* ------------------------------------------- device packers and generator
+ * Bit-exact with the reference packers on the same f32 input (device
+ * pointers in and out). */
+/* pack_uniform_q4_group64 (qwen80_uniform_q4.rs:190-278), group 32/64/128. */
+int hk_pack_q4(hk_ctx* ctx, const float* w, uint32_t rows, uint32_t cols, int32_t group,
+               uint16_t* scales, uint8_t* codes, hk_stream stream);
+/* pack_binary_group (q80_mixed_decode.rs:185-230), group 128. */
+int hk_pack_bin(hk_ctx* ctx, const float* w, uint32_t rows, uint32_t cols, uint16_t* scales,
+                uint8_t* signs, hk_stream stream);
+/* Q2 base stage of _additive_residual_codec
+ * (lab/operators/ascension_dual_gravity_worker.py:898-911), group 64. */
+int hk_pack_q2(hk_ctx* ctx, const float* w, size_t count, uint16_t* scales, uint8_t* codes,
+               hk_stream stream);
+/* Synthetic N(0, sigma): counter-based SplitMix64 words -> Irwin-Hall(12),
+ * integer-exact so host and device draws agree bit for bit.  No reference
+ * counterpart (the reference's synthetic inputs are deterministic_matrix /
+ * deterministic_input, q80_mixed_decode.rs:631-647). */
+uint64_t hk_stream_key(uint64_t seed, uint64_t stream_id);
+int hk_synth_normal(hk_ctx* ctx, uint64_t key, uint64_t first, size_t count, float sigma,
+                    float* out, hk_stream stream);
+
+/* ------------------------------------------------------------------ routers */
+
+/* Per token: softmax over n_experts logits, top_k by strict '>' (lowest index
+ * on exact ties; tie_eps > 0 = HAWKING_DS_ROUTE_TIE_EPS window), renormalised
+ * by the selected sum.  ids/weights stay on the device.
+ * source_qwen80_topk_router (model/qwen80_complete_runtime.rs:5970-6025),
+ * moe_topk_gate (shaders/moe.metal:118-305, kernels/mod.rs:12721-12790).
+ * renorm = 0 gives topk_softmax_batch (kernels/mod.rs:342-374). */
+int hk_router_softmax_topk(hk_ctx* ctx, const float* logits, uint32_t n_tokens,
+                           uint32_t n_experts, uint32_t top_k, float tie_eps, int renorm,
+                           int32_t* ids, float* weights, hk_stream stream);
+/* noaux_tc (gravity_glm.rs:447-500): select on sigmoid(logit)+bias inside the
+ * top topk_group groups (group score = sum of its best two), weight with the
+ * uncorrected sigmoid, optional renorm (+1e-20), times routed_scaling_factor. */
+int hk_router_noaux_tc(hk_ctx* ctx, const float* logits, const float* bias, uint32_t n_tokens,
+                       uint32_t n_experts, uint32_t n_group, uint32_t topk_group, uint32_t top_k,
+                       int norm_topk_prob, float routed_scaling_factor, int32_t* ids,
+                       float* weights, hk_stream stream);
+
+/* ------------------------------------------------------------------ MoE step */
+
+typedef struct hk_moe_config {
+    uint32_t n_layers;
+    uint32_t hidden;
+    uint32_t inter;          /* routed expert intermediate */
+    uint32_t shared_inter;   /* 0 = no shared expert */
+    uint32_t n_experts;
+    uint32_t top_k;
+    int32_t expert_kind;     /* HK_Q4 or HK_MIXED */
+    int32_t expert_group;    /* Q4 group (32/64/128); 128 for mixed */
+    int32_t shared_gate;     /* 1 = sigmoid(wg . xn) gate on the shared expert */
+    float eps;               /* RMSNorm epsilon */
+} hk_moe_config;
+
+/* Host-side canonical weights of one layer (HOST pointers).
+ * experts: n_experts*3 organ sources (gate, up, down per expert). */
+typedef struct hk_moe_layer_src {
+    const float* norm_w;         /* [hidden], applied as (1 + w) */
+    const float* router_w;       /* [n_experts x hidden] f32 */
+    const float* shared_gate_w;  /* [hidden] or NULL */
+    const hk_organ_src* experts; /* [n_experts*3] */
+    const hk_organ_src* shared;  /* [3] or NULL */
+} hk_moe_layer_src;
+
+/* Expert table + per-layer dense weights in device memory: each expert's
+ * gate|up|down laid out contiguously (Qwen80DeviceExpertTriplet,
+ * model/qwen80_device_expert_table.rs:116-156). */
+int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe_model** out);
+int hk_moe_model_free(hk_ctx* ctx, hk_moe_model* model);
+int hk_moe_model_set_layer(hk_ctx* ctx, hk_moe_model* model, uint32_t layer,
+                           const hk_moe_layer_src* src, hk_stream stream);
+/* Generate every layer on the device with the synthetic generator (layer l,
+ * expert e, projection p draw stream hk_moe_stream_id(l, e, p)). */
+int hk_moe_model_fill_synthetic(hk_ctx* ctx, hk_moe_model* model, uint64_t seed,
+                                hk_stream stream);
+/* stream id = ((layer+1) << 40) | (expert << 8) | proj; proj 0/1/2 = gate/up/down,
+ * 16 = norm weight, 17 = router, 18 = shared-expert gate, 32+p = mixed coins of proj p;
+ * expert n_experts = the shared expert. */
+uint64_t hk_moe_stream_id(uint32_t layer, uint32_t expert, uint32_t proj);
+/* Device bytes held by the model; dense (norm + router + gate) bytes read per layer. */
+int hk_moe_model_bytes(const hk_moe_model* model, size_t* device_bytes, size_t* dense_bytes_per_layer);
+/* Packed (algorithmic) bytes of one expert's gate+up+down; expert n_experts = shared. */
+int hk_moe_expert_bytes(const hk_moe_model* model, uint32_t layer, uint32_t expert, size_t* bytes);
+
+/* One moe_suffix layer at batch 1 on device data, no host round trip:
+ * xn = RMSNorm(1+w)(h); logits = Wr xn; route = softmax top-k renorm;
+ * out = h + sum_r w_r mlp_r(xn) (route order) + g * mlp_shared(xn).
+ * (model/qwen80_uniform_q4_hybrid_decode.rs:2615-2757,
+ *  run_qwen80_routed_expert_table model/qwen80_device_expert_table.rs:1204-1247,
+ *  routed_wave_fused model/qwen80_mixed_hybrid_decode.rs:1962-2078.)
+ * ids/weights (device, top_k each) may be NULL. */
+int hk_moe_decode_layer(hk_ctx* ctx, hk_moe_model* model, uint32_t layer, const float* h_in,
+                        float* h_out, int32_t* ids, float* weights, hk_stream stream);
+/* All layers for one token: h_{l+1} = moe_layer_l(h_l) (forward_token's MoE
+ * suffixes, model/qwen80_mixed_hybrid_decode.rs:4682-4736, without the
+ * attention mixers).  ids/weights may be NULL or [n_layers*top_k]. */
+int hk_moe_decode_stack(hk_ctx* ctx, hk_moe_model* model, const float* h_in, float* h_out,
+                        int32_t* ids, float* weights, hk_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HAWKING_HIP_H */

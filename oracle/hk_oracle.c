@@ -149,6 +149,10 @@ int hko_mixed_coin(uint64_t coin_key, uint64_t group) {
     return u < 3006477107u;
 }
 
+void hko_fill_coins(uint64_t coin_key, size_t groups, uint8_t* out) {
+    for (size_t g = 0; g < groups; ++g) out[g] = (uint8_t)hko_mixed_coin(coin_key, (uint64_t)g);
+}
+
 /* ------------------------------------------------------------------------ */
 /* Q4 uniform                                                                */
 /* ------------------------------------------------------------------------ */

@@ -52,6 +52,7 @@ float hko_normal(uint64_t key, uint64_t index, float sigma);
 void hko_fill_normal(uint64_t key, size_t count, float sigma, float* out);
 /* 1 when the 128-group `group` (flat index) of a mixed tensor is binary. */
 int hko_mixed_coin(uint64_t coin_key, uint64_t group);
+void hko_fill_coins(uint64_t coin_key, size_t groups, uint8_t* out);
 
 /* ---- Q4 uniform (HQ30UQ4 semantics, SoA: f16 scales[groups] || codes[groups*G/2]).
  * Packer: pack_uniform_q4_group64 (qwen80_uniform_q4.rs:190-278) with G in {32,64,128};

@@ -48,6 +48,7 @@ def _declare(L: C.CDLL) -> None:
         "hko_normal": (C.c_float, [C.c_uint64, C.c_uint64, C.c_float]),
         "hko_fill_normal": (None, [C.c_uint64, _sz, C.c_float, _p]),
         "hko_mixed_coin": (C.c_int, [C.c_uint64, C.c_uint64]),
+        "hko_fill_coins": (None, [C.c_uint64, _sz, _p]),
         "hko_q4_pack": (C.c_int, [_p, _sz, _sz, C.c_int, _p, _p]),
         "hko_q4_decode": (C.c_int, [_p, _p, _sz, _sz, C.c_int, _p]),
         "hko_q4_matvec": (C.c_int, [_p, _p, _sz, _sz, C.c_int, _p, _p]),
@@ -141,8 +142,9 @@ def normal(key: int, count: int, sigma: float) -> np.ndarray:
 
 
 def mixed_coins(coin_key: int, groups: int) -> np.ndarray:
-    f = lib().hko_mixed_coin
-    return np.array([f(coin_key, g) for g in range(groups)], np.uint8)
+    out = np.empty(groups, np.uint8)
+    lib().hko_fill_coins(coin_key, groups, _ptr(out))
+    return out
 
 
 # ---- Q4 ------------------------------------------------------------------------

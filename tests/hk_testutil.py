@@ -1,0 +1,93 @@
+"""Shared helpers for the parity tests: the synthetic model definition seen
+from the oracle side.
+
+The product generates weights on the device from (seed, stream id); these
+helpers regenerate any single tensor on the host with the oracle's copy of
+the generator so that the CPU oracle runs on bit-identical inputs.
+Stream ids: ((layer+1) << 40) | (expert << 8) | proj, proj 0/1/2 =
+gate/up/down, 16 = RMSNorm weight, 17 = router, 18 = shared-expert gate,
+32+p = mixed-format coins of projection p; expert n_experts = shared expert.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+SEED = 0x48415752  # "HAWR"
+SIGMA_W = 0.02
+SIGMA_NORM = 0.02
+PROJ_NORM, PROJ_ROUTER, PROJ_SHARED_GATE, PROJ_COIN = 16, 17, 18, 32
+HK_Q4, HK_BIN, HK_MIXED, HK_F32 = 0, 1, 2, 3
+
+
+def stream_id(layer: int, expert: int, proj: int) -> int:
+    return ((layer + 1) << 40) | (expert << 8) | proj
+
+
+def organ_shape(shape, expert: int, proj: int):
+    inter = shape.shared_inter if expert == shape.n_experts else shape.inter
+    return (inter, shape.hidden) if proj < 2 else (shape.hidden, inter)
+
+
+def weights(oracle, seed, layer, expert, proj, rows, cols, sigma=SIGMA_W):
+    key = oracle.stream_key(seed, stream_id(layer, expert, proj))
+    return oracle.normal(key, rows * cols, sigma).reshape(rows, cols)
+
+
+def coins(oracle, seed, layer, expert, proj, groups):
+    return oracle.mixed_coins(oracle.stream_key(seed, stream_id(layer, expert, PROJ_COIN + proj)), groups)
+
+
+def oracle_organ(oracle, seed, shape, layer, expert, proj):
+    rows, cols = organ_shape(shape, expert, proj)
+    w = weights(oracle, seed, layer, expert, proj, rows, cols)
+    if shape.expert_kind == HK_Q4:
+        return oracle.Organ.q4(w, shape.expert_group)
+    sel = coins(oracle, seed, layer, expert, proj, rows * cols // 128)
+    return oracle.Organ.mixed_from(w, sel)
+
+
+def dense(oracle, seed, shape, layer):
+    H, E = shape.hidden, shape.n_experts
+    norm = oracle.normal(oracle.stream_key(seed, stream_id(layer, 0, PROJ_NORM)), H, SIGMA_NORM)
+    router = oracle.normal(oracle.stream_key(seed, stream_id(layer, 0, PROJ_ROUTER)), E * H, SIGMA_W).reshape(E, H)
+    gate = oracle.normal(oracle.stream_key(seed, stream_id(layer, 0, PROJ_SHARED_GATE)), H, SIGMA_W)
+    return norm, router, gate
+
+
+def oracle_layer(oracle, seed, shape, layer, h):
+    """Oracle moe_suffix for one synthetic layer, generating only the routed
+    experts (plus the shared one).  Returns (layer_obj, out, ids, weights)."""
+    norm, router, gate = dense(oracle, seed, shape, layer)
+    xn = oracle.rmsnorm_1p(h, norm, shape.eps)
+    logits = oracle.gemv_f32(router, xn)
+    ids, _ = oracle.router_softmax_topk(logits, shape.top_k)
+    experts = [None] * shape.n_experts
+    for e in ids.tolist():
+        experts[e] = tuple(oracle_organ(oracle, seed, shape, layer, e, p) for p in range(3))
+    shared = None
+    if shape.shared_inter:
+        shared = tuple(oracle_organ(oracle, seed, shape, layer, shape.n_experts, p) for p in range(3))
+    L = oracle.MoeLayer(shape.hidden, shape.inter, shape.n_experts, shape.top_k, norm, router, experts,
+                        shared=shared, shared_gate_w=gate if (shape.shared_gate and shape.shared_inter) else None,
+                        eps=shape.eps)
+    out, ids2, w, xn2, logits2 = L.forward(h)
+    assert np.array_equal(ids, ids2)
+    return L, out, ids2, w, logits2
+
+
+def router_margin_ok(logits: np.ndarray, k: int, rel: float = 1e-4) -> bool:
+    """Survey router margin rule: the f64 gap between the k-th and (k+1)-th
+    score must be >= rel * max|score| for ids to be compared bit-exactly."""
+    l64 = np.sort(logits.astype(np.float64))[::-1]
+    if k >= l64.size:
+        return True
+    return (l64[k - 1] - l64[k]) >= rel * np.max(np.abs(l64))
+
+
+def organ_dict(o) -> dict:
+    """Canonical organ arrays of an oracle Organ, for MoeModel.set_layer."""
+    if o.kind == HK_Q4:
+        return {"kind": HK_Q4, "group": o.group, "rows": o.rows, "cols": o.cols, "scales": o.scales, "codes": o.codes}
+    m = o.mixed
+    return {"kind": HK_MIXED, "rows": o.rows, "cols": o.cols, "tags": m.tags, "bin_scales": m.bin_scales,
+            "bin_signs": m.bin_signs, "q2_scales": m.q2_scales, "q2_codes": m.q2_codes}

@@ -1,0 +1,200 @@
+"""GPU parity of the routers and the MoE decode step against the CPU oracle.
+
+Router ids must match exactly (planted ties from the reference's
+moe_topk_gate_exact_ties_parity.rs, and random logits under the router
+margin rule); weights within 1e-6 abs; layer outputs within 2e-5 rel-L2 of
+the oracle's moe_suffix and of the FP64 authority.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from tests import hk_testutil as U
+from tests.test_oracle_router_moe import TIE_CASES
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-5
+
+
+def say(*a):
+    print("[gpu-case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from hawking_amd.runtime import Context
+    return Context(0)
+
+
+# ------------------------------------------------------------------ routers
+
+@pytest.mark.parametrize("label,make,k,want", TIE_CASES)
+def test_router_exact_tie_fixtures(ctx, oracle, label, make, k, want):
+    from hawking_amd.moe import topk_router
+    logits = make()
+    say("router ties", label)
+    ids, w = topk_router(ctx, logits, k, renorm=False)
+    sids, sw = oracle.topk_softmax_batch(logits, 1, logits.size, k)
+    assert ids[0].tolist() == want == sids.tolist()
+    assert np.max(np.abs(w[0] - sw)) <= 1e-5
+    ids, w = topk_router(ctx, logits, k, renorm=True)
+    rids, rw = oracle.router_softmax_topk(logits, k)
+    assert ids[0].tolist() == rids.tolist()
+    assert np.max(np.abs(w[0] - rw)) <= 1e-6
+
+
+def test_router_random_batch_under_margin_rule(ctx, oracle):
+    from hawking_amd.moe import topk_router
+    rng = np.random.default_rng(5)
+    n_tok, E, k = 64, 512, 10
+    logits = (rng.standard_normal((n_tok, E)) * 0.7).astype(np.float32)
+    say("router batch", n_tok, E, k)
+    ids, w = topk_router(ctx, logits, k, n_tokens=n_tok)
+    checked = 0
+    for t in range(n_tok):
+        if not U.router_margin_ok(logits[t], k):
+            continue
+        rids, rw = oracle.router_softmax_topk(logits[t], k)
+        assert ids[t].tolist() == rids.tolist()
+        assert np.max(np.abs(w[t] - rw)) <= 1e-6
+        checked += 1
+    assert checked > n_tok // 2
+
+
+def test_router_tie_eps_window_is_serial_rule(ctx, oracle):
+    from hawking_amd.moe import topk_router
+    logits = np.full(32, -2.0, np.float32)
+    logits[[3, 9, 17]] = [1.0, 1.0 + 1e-4, 1.0 + 3e-4]
+    eps = 2e-5
+    say("router tie_eps")
+    ids, w = topk_router(ctx, logits, 3, tie_eps=eps)
+    rids, rw = oracle.router_softmax_topk(logits, 3, eps)
+    assert ids[0].tolist() == rids.tolist()
+
+
+def test_noaux_tc_matches_oracle(ctx, oracle):
+    from hawking_amd.moe import noaux_tc_router
+    rng = np.random.default_rng(6)
+    n_tok, E = 32, 256
+    logits = rng.standard_normal((n_tok, E)).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.01).astype(np.float32)
+    for (ng, tg) in [(1, 1), (8, 4)]:
+        say("noaux_tc", ng, tg)
+        ids, w = noaux_tc_router(ctx, logits, bias, ng, tg, 8, True, 2.5, n_tokens=n_tok)
+        for t in range(n_tok):
+            rids, rw = oracle.router_noaux_tc(logits[t], bias, ng, tg, 8, True, 2.5)
+            assert ids[t].tolist() == rids.tolist()
+            assert np.max(np.abs(w[t] - rw)) <= 1e-5
+
+
+def test_router_rejects_bad_geometry(ctx):
+    from hawking_amd._lib import HK_E_INVALID_ARG, HawkingError
+    from hawking_amd.moe import topk_router
+    with pytest.raises(HawkingError) as e:
+        topk_router(ctx, np.zeros(8, np.float32), 9)
+    assert e.value.code == HK_E_INVALID_ARG
+
+
+def test_router_flags_nonfinite_logits(ctx):
+    from hawking_amd.moe import topk_router
+    ctx.device_status()  # clear
+    logits = np.zeros(16, np.float32)
+    logits[4] = np.inf
+    topk_router(ctx, logits, 2)
+    assert ctx.device_status() & 1
+
+
+# ------------------------------------------------------------------ MoE layer
+
+def _small_model(ctx, oracle, kind):
+    from hawking_amd.moe import MoeModel, MoeShape
+    shape = MoeShape(n_layers=1, hidden=256, inter=128, shared_inter=128, n_experts=16, top_k=4,
+                     expert_kind=kind, expert_group=32 if kind == U.HK_Q4 else 128)
+    seed = 99
+    experts = [tuple(U.oracle_organ(oracle, seed, shape, 0, e, p) for p in range(3)) for e in range(16)]
+    shared = tuple(U.oracle_organ(oracle, seed, shape, 0, 16, p) for p in range(3))
+    norm, router, gate = U.dense(oracle, seed, shape, 0)
+    L = oracle.MoeLayer(256, 128, 16, 4, norm, router, experts, shared=shared, shared_gate_w=gate)
+    m = MoeModel(ctx, shape)
+    m.set_layer(0, norm, router, [tuple(U.organ_dict(o) for o in t) for t in experts],
+                shared=[U.organ_dict(o) for o in shared], shared_gate_w=gate)
+    return m, L, shape
+
+
+@pytest.mark.parametrize("kind", [U.HK_Q4, U.HK_MIXED])
+def test_small_layer_uploaded_from_oracle(ctx, oracle, kind):
+    say("small layer", kind)
+    m, L, shape = _small_model(ctx, oracle, kind)
+    rng = np.random.default_rng(kind)
+    for trial in range(4):
+        h = rng.standard_normal(256).astype(np.float32)
+        out, ids, w = m.moe_suffix(0, h)
+        rout, rids, rw, _, logits = L.forward(h)
+        if U.router_margin_ok(logits, 4):
+            assert ids.tolist() == rids.tolist()
+            assert np.max(np.abs(w - rw)) <= 1e-6
+        assert oracle.relative_l2(out, rout) < TOL
+        assert oracle.relative_l2(out, L.forward_f64(h, ids)) < TOL
+
+
+@pytest.mark.parametrize("kind", [U.HK_Q4, U.HK_MIXED])
+def test_synthetic_layer_matches_oracle_regeneration(ctx, oracle, kind):
+    """Device-generated weights == oracle-regenerated weights, end to end."""
+    from hawking_amd.moe import MoeModel, MoeShape
+    shape = MoeShape(n_layers=2, hidden=512, inter=256, shared_inter=256, n_experts=64, top_k=6,
+                     expert_kind=kind, expert_group=32 if kind == U.HK_Q4 else 128)
+    say("synthetic layer", kind)
+    m = MoeModel(ctx, shape)
+    m.fill_synthetic(U.SEED)
+    h = oracle.normal(oracle.stream_key(U.SEED, 0xF00D), 512, 1.0)
+    for layer in range(2):
+        out, ids, w = m.moe_suffix(layer, h)
+        L, rout, rids, rw, logits = U.oracle_layer(oracle, U.SEED, shape, layer, h)
+        assert U.router_margin_ok(logits, shape.top_k)
+        assert ids.tolist() == rids.tolist()
+        assert np.max(np.abs(w - rw)) <= 1e-6
+        assert oracle.relative_l2(out, rout) < TOL
+        assert oracle.relative_l2(out, L.forward_f64(h, ids)) < TOL
+        for e in ids.tolist()[:2]:
+            o = U.oracle_organ(oracle, U.SEED, shape, layer, e, 0)
+            want = (o.scales.nbytes + o.codes.nbytes) if kind == U.HK_Q4 else o.mixed.nbytes()
+            assert m.expert_bytes(layer, e) >= want
+
+
+def test_config3_qwen3next_layer_full_size(ctx, oracle):
+    """Config 3: hidden 2048, 512 experts x inter 512 (Q4 G32) + shared, top-10."""
+    from hawking_amd.moe import MoeModel, MoeShape
+    shape = MoeShape(n_layers=1, hidden=2048, inter=512, shared_inter=512, n_experts=512, top_k=10,
+                     expert_kind=U.HK_Q4, expert_group=32)
+    say("config3 full layer")
+    m = MoeModel(ctx, shape)
+    m.fill_synthetic(U.SEED)
+    h = oracle.normal(oracle.stream_key(U.SEED, 0xC3), 2048, 1.0)
+    out, ids, w = m.moe_suffix(0, h)
+    L, rout, rids, rw, logits = U.oracle_layer(oracle, U.SEED, shape, 0, h)
+    assert U.router_margin_ok(logits, 10)
+    assert ids.tolist() == rids.tolist()
+    assert np.max(np.abs(w - rw)) <= 1e-6
+    assert oracle.relative_l2(out, rout) < TOL
+    assert oracle.relative_l2(out, L.forward_f64(h, ids)) < TOL
+
+
+def test_stack_matches_oracle_layer_by_layer(ctx, oracle):
+    """Config 4 geometry (mixed <=1.5 BPW, Qwen3-Next layer) over 3 layers."""
+    from hawking_amd.moe import MoeModel, MoeShape
+    shape = MoeShape(n_layers=3, hidden=2048, inter=512, shared_inter=512, n_experts=512, top_k=10,
+                     expert_kind=U.HK_MIXED, expert_group=128)
+    say("config4 geometry, 3 layers")
+    m = MoeModel(ctx, shape)
+    m.fill_synthetic(U.SEED)
+    h0 = oracle.normal(oracle.stream_key(U.SEED, 0xC4), 2048, 1.0)
+    out, ids, w = m.forward_token(h0)
+    h = h0
+    for layer in range(3):
+        L, h_next, rids, rw, logits = U.oracle_layer(oracle, U.SEED, shape, layer, h)
+        assert U.router_margin_ok(logits, 10), f"near-tie at layer {layer}"
+        assert ids[layer].tolist() == rids.tolist()
+        h = h_next
+    assert oracle.relative_l2(out, h) < TOL

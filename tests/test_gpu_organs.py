@@ -1,0 +1,224 @@
+"""GPU parity of the packed organs against the CPU oracle (through the C ABI).
+
+Bars: the generator, the device packers and the decode probe are bit-exact;
+matvec outputs are within 2e-5 relative L2 of the oracle's serial f32 path
+and of the FP64 authority.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from tests import hk_testutil as U
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-5
+
+
+def say(*a):
+    print("[gpu-case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from hawking_amd.runtime import Context
+    return Context(0)
+
+
+# ------------------------------------------------------------------ generator / packers
+
+def test_generator_is_bit_identical_to_oracle(ctx, oracle):
+    from hawking_amd import organs
+    for sid, n, sigma in [(1, 100003, 0.02), (U.stream_id(3, 7, 1), 4096, 1.0)]:
+        say("synth_normal", sid, n, sigma)
+        key = oracle.stream_key(U.SEED, sid)
+        assert organs.stream_key(U.SEED, sid) == key
+        got = organs.synth_normal(ctx, key, n, sigma).download()
+        assert np.array_equal(got.view(np.uint32), oracle.normal(key, n, sigma).view(np.uint32))
+
+
+def _edge_weights(rng, rows, cols):
+    w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    w[0, :] = 0.0                                  # all-zero groups
+    w[1, :32] = np.arange(32, dtype=np.float32) - 16  # exact ties at x.5 after scaling
+    w[1, 32:64] = 1e-7                             # f16-subnormal scales
+    w[2, ::3] = -0.0
+    return w
+
+
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_device_q4_packer_bit_exact(ctx, oracle, group):
+    from hawking_amd import organs
+    rng = np.random.default_rng(group)
+    w = _edge_weights(rng, 64, 512)
+    say("pack_q4", w.shape, group)
+    s, c = organs.pack_q4_device(ctx, ctx.to_device(w), 64, 512, group)
+    rs, rc = oracle.q4_pack(w, group)
+    assert np.array_equal(s.download(), rs) and np.array_equal(c.download(), rc)
+
+
+def test_device_binary_packer_bit_exact(ctx, oracle):
+    from hawking_amd import organs
+    rng = np.random.default_rng(7)
+    w = _edge_weights(rng, 32, 1024)
+    v0 = np.float32(2.0**-14 * (1 + 2.0**-11))   # double-rounding case
+    w[3, :128] = v0
+    w[3, 0] = np.nextafter(v0, np.float32(1))
+    say("pack_bin", w.shape)
+    s, g = organs.pack_binary_group_device(ctx, ctx.to_device(w), 32, 1024)
+    rs, rg = oracle.bin_pack(w)
+    assert np.array_equal(s.download(), rs) and np.array_equal(g.download(), rg)
+
+
+def test_device_q2_packer_bit_exact(ctx, oracle):
+    from hawking_amd import organs
+    rng = np.random.default_rng(8)
+    w = _edge_weights(rng, 16, 512).reshape(-1)
+    w[4096:4160] = np.linspace(-1.5, 1.5, 64, dtype=np.float32)
+    say("pack_q2", w.size)
+    s, c = organs.pack_q2_device(ctx, ctx.to_device(w), w.size)
+    rs, rc = oracle.q2_pack(w)
+    assert np.array_equal(s.download(), rs) and np.array_equal(c.download(), rc)
+
+
+def test_device_packer_rejects_nonfinite(ctx):
+    from hawking_amd import organs
+    from hawking_amd._lib import HK_E_NONFINITE, HawkingError
+    w = np.zeros((4, 128), np.float32)
+    w[2, 5] = np.nan
+    with pytest.raises(HawkingError) as e:
+        organs.pack_q4_device(ctx, ctx.to_device(w), 4, 128, 32)
+    assert e.value.code == HK_E_NONFINITE
+
+
+# ------------------------------------------------------------------ organs
+
+def _q4(ctx, oracle, w, group):
+    from hawking_amd.organs import Qwen80Q4PackedTensor
+    s, c = oracle.q4_pack(w, group)
+    return Qwen80Q4PackedTensor(ctx, s, c, w.shape[0], w.shape[1], group), (s, c)
+
+
+def _bin(ctx, oracle, w):
+    from hawking_amd.organs import BinaryGroupPacked
+    s, g = oracle.bin_pack(w)
+    return BinaryGroupPacked(ctx, s, g, w.shape[0], w.shape[1]), (s, g)
+
+
+def _mixed(ctx, oracle, w, sel):
+    from hawking_amd.organs import MixedPackedTensor
+    m = oracle.mixed_pack(w, sel)
+    return MixedPackedTensor(ctx, w.shape[0], w.shape[1], m.tags, m.bin_scales, m.bin_signs, m.q2_scales,
+                             m.q2_codes), m
+
+
+def test_config1_q4_512x2048_g32(ctx, oracle):
+    key = oracle.stream_key(U.SEED, 0xC1)
+    w = oracle.normal(key, 512 * 2048, 0.02).reshape(512, 2048)
+    x = oracle.normal(oracle.stream_key(U.SEED, 0xC1 + 1), 2048, 1.0)
+    say("config1 q4 512x2048 g32")
+    organ, (s, c) = _q4(ctx, oracle, w, 32)
+    assert organ.packed_bytes == 589_824
+    assert np.array_equal(organ.decode(), oracle.q4_decode(s, c, 512, 2048, 32))
+    y = organ.matvec(x)
+    yo = oracle.q4_matvec(s, c, 512, 2048, 32, x)
+    y64 = oracle.q4_matvec_f64(s, c, 512, 2048, 32, x)
+    assert oracle.relative_l2(y, yo) < TOL
+    assert oracle.relative_l2(y, y64) < TOL
+
+
+@pytest.mark.parametrize("shape", [(512, 2048), (2048, 512)])
+def test_config2_binary(ctx, oracle, shape):
+    rows, cols = shape
+    w = oracle.normal(oracle.stream_key(U.SEED, 0xC2 + rows), rows * cols, 0.02).reshape(rows, cols)
+    x = oracle.normal(oracle.stream_key(U.SEED, 0xC2 + rows + 1), cols, 1.0)
+    say("config2 binary", shape)
+    organ, (s, g) = _bin(ctx, oracle, w)
+    assert organ.packed_bytes == 147_456
+    assert np.array_equal(organ.decode(), oracle.bin_decode(s, g, rows, cols))
+    y = organ.matvec(x)
+    assert oracle.relative_l2(y, oracle.bin_matvec(s, g, rows, cols, x)) < TOL
+    assert oracle.relative_l2(y, oracle.bin_matvec_f64(s, g, rows, cols, x)) < TOL
+
+
+@pytest.mark.parametrize("shape", [(512, 2048), (2048, 512), (13, 384)])
+def test_mixed_organ(ctx, oracle, shape):
+    rows, cols = shape
+    w = oracle.normal(oracle.stream_key(U.SEED, 0xC4 + rows), rows * cols, 0.02).reshape(rows, cols)
+    sel = oracle.mixed_coins(oracle.stream_key(U.SEED, 0xC4 + rows + 7), rows * cols // 128)
+    x = oracle.normal(oracle.stream_key(U.SEED, 0xC4 + rows + 1), cols, 1.0)
+    say("mixed organ", shape)
+    organ, m = _mixed(ctx, oracle, w, sel)
+    assert np.array_equal(organ.decode(), oracle.mixed_decode(m))
+    y = organ.matvec(x)
+    assert oracle.relative_l2(y, oracle.mixed_matvec(m, x)) < TOL
+    assert oracle.relative_l2(y, oracle.mixed_matvec_f64(m, x)) < TOL
+
+
+@pytest.mark.parametrize("group,shape", [(64, (96, 1024)), (128, (7, 256)), (32, (1, 7168))])
+def test_q4_other_groups_and_ragged_rows(ctx, oracle, group, shape):
+    rows, cols = shape
+    rng = np.random.default_rng(rows * cols + group)
+    w = (rng.standard_normal(shape) * 0.02).astype(np.float32)
+    x = rng.standard_normal(cols).astype(np.float32)
+    say("q4", group, shape)
+    organ, (s, c) = _q4(ctx, oracle, w, group)
+    assert np.array_equal(organ.gather_row(rows - 1), oracle.q4_decode(s, c, rows, cols, group)[rows - 1])
+    assert oracle.relative_l2(organ.matvec(x), oracle.q4_matvec_f64(s, c, rows, cols, group, x)) < TOL
+
+
+def test_reference_deterministic_inputs(ctx, oracle):
+    # deterministic_matrix(512, 2048, 1) / deterministic_input(2048): the inputs of the
+    # reference's organ benchmark (examples/ascension_qwen80_matvec_geometry_sweep.rs).
+    w = oracle.deterministic_matrix(512, 2048, 1)
+    x = oracle.deterministic_input(2048)
+    say("reference deterministic inputs")
+    organ, (s, g) = _bin(ctx, oracle, w)
+    assert oracle.relative_l2(organ.matvec(x), oracle.bin_matvec(s, g, 512, 2048, x)) < TOL
+    organ, (s, c) = _q4(ctx, oracle, w, 64)
+    assert oracle.relative_l2(organ.matvec(x), oracle.q4_matvec(s, c, 512, 2048, 64, x)) < TOL
+
+
+def test_gemv_batch_matches_single(ctx, oracle):
+    from hawking_amd.organs import gemv_batch
+    rng = np.random.default_rng(21)
+    n, rows, cols = 6, 512, 2048
+    organs, refs = [], []
+    xs = rng.standard_normal((n, cols)).astype(np.float32)
+    for i in range(n):
+        w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+        o, (s, g) = _bin(ctx, oracle, w)
+        organs.append(o)
+        refs.append(oracle.bin_matvec(s, g, rows, cols, xs[i]))
+    say("gemv_batch", n)
+    xd = ctx.to_device(xs)
+    yd = ctx.empty((n, rows))
+    gemv_batch(ctx, organs, xd, cols, yd, rows)
+    y = yd.download()
+    for i in range(n):
+        assert oracle.relative_l2(y[i], refs[i]) < TOL
+
+
+def test_zero_input_gives_exact_zero(ctx, oracle):
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal((64, 512)) * 0.02).astype(np.float32)
+    organ, _ = _q4(ctx, oracle, w, 32)
+    assert np.all(organ.matvec(np.zeros(512, np.float32)) == 0.0)
+
+
+def test_upload_validation_errors(ctx, oracle):
+    from hawking_amd._lib import HK_E_GEOMETRY, HK_E_NONFINITE, HK_E_UNSUPPORTED, HawkingError
+    from hawking_amd.organs import BinaryGroupPacked, Qwen80Q4PackedTensor
+    s, c = oracle.q4_pack(np.ones((4, 96), np.float32), 32)
+    with pytest.raises(HawkingError) as e:
+        Qwen80Q4PackedTensor(ctx, s[: 4 * 96 // 48], c, 4, 96, 48)
+    assert e.value.code == HK_E_UNSUPPORTED
+    bad = s.copy()
+    bad[3] = 0x7C00                               # +inf scale
+    with pytest.raises(HawkingError) as e:
+        Qwen80Q4PackedTensor(ctx, bad, c, 4, 96, 32)
+    assert e.value.code == HK_E_NONFINITE
+    with pytest.raises(HawkingError) as e:
+        BinaryGroupPacked(ctx, np.zeros(3, np.uint16), np.zeros(4 * 96 // 8, np.uint8), 4, 96)
+    assert e.value.code == HK_E_GEOMETRY
