@@ -71,6 +71,11 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev
     const uint32_t slot = blockIdx.y;
     const bool shared = slot >= d.K;
     const uint32_t e = shared ? d.E : (uint32_t)ws.ids[slot];
+    if (e > d.E || (!shared && e == d.E)) {
+        // invalid route (non-finite logits): flag it and touch no expert
+        if (threadIdx.x == 0) atomicOr(ws.status, HK_DEVERR_ROUTE);
+        return;
+    }
     const OrganView& g = L.table[e * 3 + 0];
     const OrganView& u = L.table[e * 3 + 1];
     const int lane = threadIdx.x & 63;
@@ -94,7 +99,9 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDims d, MoeLayerDev L,
     if (row >= d.H) return;
     float combined = 0.0f;
     for (uint32_t r = 0; r < d.K; ++r) {
-        const OrganView& dn = L.table[(uint32_t)ws.ids[r] * 3 + 2];
+        const uint32_t e = (uint32_t)ws.ids[r];
+        if (e >= d.E) continue;  // flagged by the gate/up kernel
+        const OrganView& dn = L.table[e * 3 + 2];
         const float y = wave_sum(row_dot_partial<KIND>(dn, row, act + (size_t)r * d.Imax, lane));
         combined += y * ws.weights[r];
     }
