@@ -1,0 +1,266 @@
+"""Benchmark of the quantized decode hot path on one MI355X.
+
+Headline (BASELINE.json metric, configs[1]): the binary sign-plane organ
+(512x2048, 1 bit/weight + f16 mean|w| per 128) streamed over many distinct
+organs in ONE launch, working set > 1 GB (so the 256 MB MALL cannot serve
+repeats), inputs resident in HBM.  A "step" is one launch over all organs.
+
+Also reported (the same JSON line, "extra"): Q4 (config 1) and mixed streamed
+GB/s, the binary down shape (2048x512), single-organ latency, the config-3
+MoE layer and the config-4 48-layer mixed token in microseconds at batch 1.
+
+The CPU baseline is the oracle's serial restatement of
+binary_group_matvec_f32 (crates/hawking-core/src/model/qwen_complete_binary/
+q80_mixed_decode.rs:245-257) on a bounded sample of the same organs, one
+thread, timed on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+SEED = 0x48415752
+HK_Q4, HK_BIN, HK_MIXED, HK_F32 = 0, 1, 2, 3
+WORKLOADS = {
+    # name: (kind, group, rows, cols, n_organs)
+    "binary_512x2048": (HK_BIN, 128, 512, 2048, 8192),
+    "binary_2048x512": (HK_BIN, 128, 2048, 512, 8192),
+    "q4g32_512x2048": (HK_Q4, 32, 512, 2048, 2048),
+    "mixed_512x2048": (HK_MIXED, 128, 512, 2048, 6144),
+}
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def organ_stream_id(workload: str, i: int) -> int:
+    return (0xBE << 48) | (sorted(WORKLOADS).index(workload) << 40) | i
+
+
+def build_stream(ctx, name: str, n_organs: int | None = None):
+    from hawking_amd import organs
+    kind, group, rows, cols, n = WORKLOADS[name]
+    n = n_organs or n
+    orgs = []
+    for i in range(n):
+        sid = organ_stream_id(name, i)
+        orgs.append(organs.SyntheticOrgan(ctx, kind, rows, cols, organs.stream_key(SEED, sid),
+                                          organs.stream_key(SEED, sid ^ (1 << 47)), group=group))
+    oset = organs.OrganSet(ctx, orgs)
+    x = ctx.empty((n, cols))
+    from hawking_amd.organs import stream_key
+    ctx.call("hk_synth_normal", stream_key(SEED, 0xBE0001), 0, n * cols, 1.0, x.ptr, ctx.stream)
+    y = ctx.empty((n, rows))
+    alg_bytes = oset.packed_bytes + n * (rows + cols) * 4
+    return oset, x, y, alg_bytes
+
+
+def time_launches(ctx, fn, steps: int, warmup: int) -> float:
+    """Average ms per call of fn() over `steps` calls, HIP events on ctx.stream."""
+    for _ in range(warmup):
+        fn()
+    ctx.synchronize()
+    e0, e1 = ctx.event(), ctx.event()
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    ctx.synchronize()
+    return e0.elapsed_ms(e1) / steps
+
+
+def streamed(ctx, name, steps, warmup, n_organs=None):
+    oset, x, y, nbytes = build_stream(ctx, name, n_organs)
+    kind, group, rows, cols, _ = WORKLOADS[name]
+    ms = time_launches(ctx, lambda: oset.gemv(x, cols, y, rows), steps, warmup)
+    return {"ms": ms, "bytes": nbytes, "gbps": nbytes / (ms * 1e-3) / 1e9, "organs": len(oset.organs),
+            "packed_bytes_per_organ": oset.packed_bytes / len(oset.organs)}, (oset, x, y)
+
+
+def single_organ_us(ctx, steps=200):
+    from hawking_amd import organs
+    o = organs.SyntheticOrgan(ctx, HK_BIN, 512, 2048, organs.stream_key(SEED, 0xBE0002))
+    x = ctx.empty(2048)
+    ctx.call("hk_synth_normal", organs.stream_key(SEED, 0xBE0003), 0, 2048, 1.0, x.ptr, ctx.stream)
+    y = ctx.empty(512)
+    return time_launches(ctx, lambda: o.matvec_device(x, y), steps, 20) * 1e3
+
+
+def moe_bench(ctx, shape, steps, warmup, n_inputs=16):
+    """Decode `steps` tokens cycling over n_inputs distinct hidden vectors
+    (distinct routings, so the MALL does not serve repeated experts)."""
+    from hawking_amd.moe import MoeModel
+    from hawking_amd.organs import stream_key
+    t0 = time.time()
+    m = MoeModel(ctx, shape)
+    m.fill_synthetic(SEED)
+    ctx.synchronize()
+    gen_s = time.time() - t0
+    H, L, K = shape.hidden, shape.n_layers, shape.top_k
+    hs = ctx.empty((n_inputs, H))
+    ctx.call("hk_synth_normal", stream_key(SEED, 0xBE0004), 0, n_inputs * H, 1.0, hs.ptr, ctx.stream)
+    out = ctx.empty(H)
+    ids = ctx.empty((n_inputs, L, K), np.int32)
+    state = {"i": 0}
+
+    def step():
+        i = state["i"] % n_inputs
+        state["i"] += 1
+        m.decode_stack_device(hs.offset(i * H), out, ids.offset(i * L * K), None)
+
+    ms = time_launches(ctx, step, steps, warmup)
+    # algorithmic bytes per token from the routes actually taken
+    routes = ids.download()
+    dev_bytes, dense_per_layer = m.model_bytes()
+    per_tok = []
+    for t in range(n_inputs):
+        b = 0
+        for layer in range(L):
+            b += dense_per_layer + 2 * H * 4
+            for e in routes[t, layer]:
+                b += m.expert_bytes(layer, int(e))
+            if shape.shared_inter:
+                b += m.expert_bytes(layer, shape.n_experts)
+        per_tok.append(b)
+    tok_bytes = float(np.mean(per_tok))
+    return {"us_per_token": ms * 1e3, "bytes_per_token": tok_bytes, "gbps": tok_bytes / (ms * 1e-3) / 1e9,
+            "model_device_bytes": dev_bytes, "gen_seconds": round(gen_s, 2), "layers": L}
+
+
+def cpu_baseline(budget_s: float = 12.0, n_distinct: int = 64):
+    """Oracle binary matvec (serial f32, one thread) over the first n_distinct
+    organs of the headline workload, cycled until budget_s of matvec time."""
+    from oracle import hk_oracle as oracle
+    kind, group, rows, cols, _ = WORKLOADS["binary_512x2048"]
+    per_organ = 147_456 + (rows + cols) * 4
+    xkey = oracle.stream_key(SEED, 0xBE0001)
+    organs = []
+    for i in range(n_distinct):
+        sid = organ_stream_id("binary_512x2048", i)
+        w = oracle.normal(oracle.stream_key(SEED, sid), rows * cols, 0.02).reshape(rows, cols)
+        s, g = oracle.bin_pack(w)
+        organs.append((s, g, oracle.normal(xkey, cols, 1.0, first=i * cols)))
+    done, t_total = 0, 0.0
+    while t_total < budget_s:
+        s, g, x = organs[done % n_distinct]
+        t0 = time.perf_counter()
+        oracle.bin_matvec(s, g, rows, cols, x)
+        t_total += time.perf_counter() - t0
+        done += 1
+    return {"value": round(done * per_organ / t_total / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{done} matvecs cycling over {n_distinct} distinct binary 512x2048 organs of the headline "
+                      f"workload (9.4 MB, cache-resident on the CPU): the oracle's serial f32 restatement of "
+                      f"binary_group_matvec_f32 (gcc -O2 -ffp-contract=off), 1 thread, {t_total:.1f} s"}
+
+
+def spot_check(ctx, oset, x, y, n_check=4):
+    """GPU output of the first organs of the timed set vs the oracle."""
+    from oracle import hk_oracle as oracle
+    kind, group, rows, cols, _ = WORKLOADS["binary_512x2048"]
+    yg = y.download()
+    xs = x.download()
+    worst = 0.0
+    for i in range(n_check):
+        sid = organ_stream_id("binary_512x2048", i)
+        w = oracle.normal(oracle.stream_key(SEED, sid), rows * cols, 0.02).reshape(rows, cols)
+        s, g = oracle.bin_pack(w)
+        xi = oracle.normal(oracle.stream_key(SEED, 0xBE0001), cols, 1.0, first=i * cols)
+        assert np.array_equal(xi, xs[i]), "device input generator disagrees with the oracle"
+        worst = max(worst, oracle.relative_l2(yg[i], oracle.bin_matvec(s, g, rows, cols, xs[i])))
+    return worst
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only-main", action="store_true", help="headline kernel only (for profiling)")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-moe", action="store_true")
+    ap.add_argument("--moe-layers", type=int, default=48)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
+              "(this build has no multi-GPU path; see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    from hawking_amd.runtime import Context
+    ctx = Context(0)
+    info = ctx.device_info()
+    log("device", info)
+
+    main_name = "binary_512x2048"
+    log("headline", main_name)
+    head, (oset, x, y) = streamed(ctx, main_name, args.steps, args.warmup)
+    log("headline", {k: (round(v, 4) if isinstance(v, float) else v) for k, v in head.items()})
+    extra = {}
+    rel = None
+    if not args.only_main:
+        rel = spot_check(ctx, oset, x, y)
+        log("spot-check rel_l2", rel)
+        del oset, x, y
+        for name in ("binary_2048x512", "q4g32_512x2048", "mixed_512x2048"):
+            r, bufs = streamed(ctx, name, args.steps, args.warmup)
+            del bufs
+            extra[name] = {"gbps": round(r["gbps"], 1), "frac_hbm": round(r["gbps"] / HBM_PEAK_GBPS, 4),
+                           "us_per_launch": round(r["ms"] * 1e3, 1), "organs": r["organs"],
+                           "packed_bytes_per_organ": round(r["packed_bytes_per_organ"], 1)}
+            log(name, extra[name])
+        extra["single_organ_binary_512x2048_us"] = round(single_organ_us(ctx), 2)
+        log("single organ us", extra["single_organ_binary_512x2048_us"])
+        if not args.no_moe:
+            from hawking_amd.moe import MoeShape
+            c3 = MoeShape(n_layers=1, hidden=2048, inter=512, shared_inter=512, n_experts=512, top_k=10,
+                          expert_kind=HK_Q4, expert_group=32)
+            r = moe_bench(ctx, c3, max(args.steps, 20), args.warmup)
+            extra["moe_layer_c3_q4"] = {k: (round(v, 2) if isinstance(v, float) else v) for k, v in r.items()}
+            log("c3", extra["moe_layer_c3_q4"])
+            c4 = MoeShape(n_layers=args.moe_layers, hidden=2048, inter=512, shared_inter=512, n_experts=512,
+                          top_k=10, expert_kind=HK_MIXED, expert_group=128)
+            r = moe_bench(ctx, c4, max(args.steps, 20), args.warmup)
+            extra["moe_token_c4_mixed"] = {k: (round(v, 2) if isinstance(v, float) else v) for k, v in r.items()}
+            log("c4", extra["moe_token_c4_mixed"])
+    cpu = None if (args.no_cpu or args.only_main) else cpu_baseline()
+    if cpu:
+        log("cpu", cpu)
+
+    line = {
+        "metric": "packed-matvec GB/s (% HBM peak); MoE decode µs/token at batch 1",
+        "value": round(head["gbps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (counter-based N(0,0.02) weights packed on device, N(0,1) inputs)",
+        "config": {"workload": f"config2 binary sign-plane organ 512x2048 (group 128, f16 mean|w|), "
+                               f"{head['organs']} distinct organs streamed per launch, batch 1 per organ",
+                   "organs_per_step": head["organs"], "bytes_per_step": head["bytes"],
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(head["gbps"], 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(head["gbps"] / HBM_PEAK_GBPS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "parity_spot_check_rel_l2": rel,
+        "extra": extra,
+        "device": info["name"],
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

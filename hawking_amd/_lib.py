@@ -86,6 +86,10 @@ PROTOTYPES = {
     "hk_gemv": (C.c_int, [_p, _p, _p, _p, _p]),
     "hk_gemv_batch": (C.c_int, [_p, C.POINTER(_p), _u32, _p, _sz, _p, _sz, _p]),
     "hk_decode_rows": (C.c_int, [_p, _p, _u32, _u32, _p, _p]),
+    "hk_organ_set_create": (C.c_int, [_p, C.POINTER(_p), _u32, C.POINTER(_p)]),
+    "hk_organ_set_free": (C.c_int, [_p, _p]),
+    "hk_gemv_set": (C.c_int, [_p, _p, _p, _sz, _p, _sz, _p]),
+    "hk_organ_synthetic": (C.c_int, [_p, _i32, _i32, _u32, _u32, _u64, _u64, C.c_float, _p, C.POINTER(_p)]),
     "hk_pack_q4": (C.c_int, [_p, _p, _u32, _u32, _i32, _p, _p, _p]),
     "hk_pack_bin": (C.c_int, [_p, _p, _u32, _u32, _p, _p, _p]),
     "hk_pack_q2": (C.c_int, [_p, _p, _sz, _p, _p, _p]),

@@ -488,6 +488,132 @@ extern "C" int hk_gemv_batch(hk_ctx* ctx, const hk_organ* const* organs, uint32_
                      "gemv_batch launch");
 }
 
+struct hk_organ_set {
+    OrganView* dev = nullptr;
+    uint32_t n = 0;
+    OrganView first{};
+};
+
+extern "C" int hk_organ_set_create(hk_ctx* ctx, const hk_organ* const* organs, uint32_t n, hk_organ_set** out) {
+    if (!ctx || !out) return HK_E_INVALID_ARG;
+    *out = nullptr;
+    if (!organs || n == 0) return set_error(ctx, HK_E_INVALID_ARG, "organ set: no organs");
+    if (n > 65535) return set_error(ctx, HK_E_INVALID_ARG, "organ set: at most 65535 organs");
+    std::vector<OrganView> views(n);
+    for (uint32_t i = 0; i < n; ++i) {
+        if (!organs[i]) return set_error(ctx, HK_E_INVALID_ARG, "organ set: NULL organ");
+        views[i] = organs[i]->view;
+        if (views[i].kind != views[0].kind || views[i].rows != views[0].rows || views[i].cols != views[0].cols ||
+            views[i].group != views[0].group)
+            return set_error(ctx, HK_E_GEOMETRY, "organ set: organs must share kind and shape");
+    }
+    hk_organ_set* set = new hk_organ_set();
+    if (hipMalloc(&set->dev, n * sizeof(OrganView)) != hipSuccess) {
+        delete set;
+        return set_error(ctx, HK_E_NOMEM, "organ set allocation failed");
+    }
+    int rc = check_hip(ctx, hipMemcpy(set->dev, views.data(), n * sizeof(OrganView), hipMemcpyHostToDevice),
+                       "organ set upload");
+    if (rc) {
+        (void)hipFree(set->dev);
+        delete set;
+        return rc;
+    }
+    set->n = n;
+    set->first = views[0];
+    *out = set;
+    return HK_OK;
+}
+
+extern "C" int hk_organ_set_free(hk_ctx* ctx, hk_organ_set* set) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (!set) return HK_OK;
+    int rc = check_hip(ctx, hipFree(set->dev), "hipFree (organ set)");
+    delete set;
+    return rc;
+}
+
+extern "C" int hk_gemv_set(hk_ctx* ctx, const hk_organ_set* set, const float* x, size_t x_stride, float* y,
+                           size_t y_stride, hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (!set || !x || !y) return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv_set: NULL argument");
+    if (!aligned16(x) || !aligned16(y) || (x_stride % 4) || (y_stride % 4) ||
+        (set->n > 1 && (x_stride < set->first.cols || y_stride < set->first.rows)))
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv_set: bad alignment or strides");
+    const OrganView& f = set->first;
+    return check_hip(ctx,
+                     launch_gemv_batch(set->dev, set->n, f.kind, f.rows, f.cols, f.group, x, x_stride, y, y_stride,
+                                       static_cast<hipStream_t>(stream)),
+                     "gemv_set launch");
+}
+
+extern "C" int hk_organ_synthetic(hk_ctx* ctx, int32_t kind, int32_t group, uint32_t rows, uint32_t cols, uint64_t key,
+                                  uint64_t coin_key, float sigma, hk_stream stream, hk_organ** out) {
+    if (!ctx || !out) return HK_E_INVALID_ARG;
+    *out = nullptr;
+    if (kind == HK_BIN) group = 128;
+    if (kind == HK_MIXED) group = 128;
+    int rc = validate_shape(ctx, kind, group, rows, cols);
+    if (rc) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    void* tmp = nullptr;
+    if (hipMalloc(&tmp, sizeof(SynthJob) + 256) != hipSuccess) return set_error(ctx, HK_E_NOMEM, "job allocation failed");
+    SynthJob* jd = static_cast<SynthJob*>(tmp);
+    uint32_t* aux = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(tmp) + sizeof(SynthJob) + 64);
+    SynthJob j{};
+    j.key = key;
+    j.coin_key = coin_key;
+    j.sigma = sigma;
+    j.group = group;
+    j.rows = rows;
+    j.cols = cols;
+    const size_t groups = (size_t)rows * cols / (size_t)(kind == HK_F32 ? 128 : group);
+    uint32_t nbin = 0;
+    rc = check_hip(ctx, hipMemsetAsync(aux, 0, 8, st), "memset");
+    if (!rc && kind == HK_MIXED) {
+        rc = check_hip(ctx, hipMemcpyAsync(jd, &j, sizeof(j), hipMemcpyHostToDevice, st), "job upload");
+        if (!rc) rc = check_hip(ctx, launch_synth_mixed_count(jd, 1, groups, aux + 1, st), "count");
+        if (!rc) rc = check_hip(ctx, hipMemcpyAsync(&nbin, aux + 1, 4, hipMemcpyDeviceToHost, st), "count read");
+        if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "sync");
+    }
+    hk_organ* o = nullptr;
+    if (!rc) {
+        const Layout L = layout_for(kind, group, rows, cols, nbin, kind == HK_MIXED ? (uint32_t)(groups - nbin) : 0);
+        o = new hk_organ();
+        o->alloc_bytes = L.total();
+        o->packed_bytes = L.packed();
+        if (hipMalloc(&o->mem, o->alloc_bytes) != hipSuccess) {
+            rc = set_error(ctx, HK_E_NOMEM, "organ allocation failed");
+        } else {
+            o->view = place(kind, group, rows, cols, L, static_cast<uint8_t*>(o->mem));
+            j.scales = const_cast<uint16_t*>(o->view.scales);
+            j.codes = const_cast<uint8_t*>(o->view.codes);
+            j.tags = const_cast<uint8_t*>(o->view.tags);
+            j.q2_scales = const_cast<uint16_t*>(o->view.q2_scales);
+            j.q2_codes = const_cast<uint8_t*>(o->view.q2_codes);
+            j.row_bin = const_cast<uint32_t*>(o->view.row_bin);
+            j.row_q2 = const_cast<uint32_t*>(o->view.row_q2);
+            j.dense = const_cast<float*>(o->view.dense);
+            rc = check_hip(ctx, hipMemcpyAsync(jd, &j, sizeof(j), hipMemcpyHostToDevice, st), "job upload");
+            if (!rc) rc = check_hip(ctx, launch_synth_jobs(kind, jd, 1, groups, aux, st), "synth organ");
+            uint32_t bad = 0;
+            if (!rc) rc = check_hip(ctx, hipMemcpyAsync(&bad, aux, 4, hipMemcpyDeviceToHost, st), "flag read");
+            if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "sync");
+            if (!rc && bad) rc = set_error(ctx, HK_E_NONFINITE, "synthetic organ has a non-finite scale");
+        }
+    }
+    (void)hipFree(tmp);
+    if (rc) {
+        if (o) {
+            if (o->mem) (void)hipFree(o->mem);
+            delete o;
+        }
+        return rc;
+    }
+    *out = o;
+    return HK_OK;
+}
+
 extern "C" int hk_decode_rows(hk_ctx* ctx, const hk_organ* o, uint32_t row0, uint32_t nrows, float* out,
                               hk_stream stream) {
     if (!ctx) return HK_E_INVALID_ARG;

@@ -193,6 +193,17 @@ __global__ void synth_pack_q4_kernel(const SynthJob* __restrict__ jobs, uint32_t
     (void)njobs;
 }
 
+__global__ void synth_pack_bin_kernel(const SynthJob* __restrict__ jobs, uint32_t* bad) {
+    const SynthJob j = jobs[blockIdx.y];
+    const size_t groups = (size_t)j.rows * j.cols / 128;
+    for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < groups;
+         g += (size_t)gridDim.x * blockDim.x) {
+        uint32_t b = 0;
+        bin_pack_group(SynthSrc{j.key, g * 128, j.sigma}, j.scales + g, j.codes + g * 16, &b);
+        if (b) atomicOr(bad, 1u);
+    }
+}
+
 // Mixed, pass 1: tag words (32 flat groups per thread).
 __global__ void synth_mixed_tags_kernel(const SynthJob* __restrict__ jobs) {
     const SynthJob j = jobs[blockIdx.y];
@@ -301,6 +312,9 @@ hipError_t launch_synth_jobs(int kind, const SynthJob* jobs_dev, uint32_t njobs,
     case HK_Q4:
         hipLaunchKernelGGL(synth_pack_q4_kernel, dim3(bx ? bx : 1, njobs), dim3(256), 0, s, jobs_dev,
                            njobs, bad);
+        break;
+    case HK_BIN:
+        hipLaunchKernelGGL(synth_pack_bin_kernel, dim3(bx ? bx : 1, njobs), dim3(256), 0, s, jobs_dev, bad);
         break;
     case HK_MIXED: {
         const size_t words = (max_groups + 31) / 32;

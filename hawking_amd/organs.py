@@ -143,6 +143,55 @@ class DenseF32Organ(PackedOrgan):
         super().__init__(ctx, src, (w,))
 
 
+class SyntheticOrgan(PackedOrgan):
+    """An organ generated and packed on the device from the synthetic
+    generator (weights N(0, sigma) from `key`, mixed coins from `coin_key`)."""
+
+    def __init__(self, ctx: Context, kind: int, rows: int, cols: int, key: int, coin_key: int = 0,
+                 group: int = 128, sigma: float = 0.02):
+        self.ctx = ctx
+        self.kind = kind
+        h = C.c_void_p()
+        ctx.call("hk_organ_synthetic", kind, group, rows, cols, key, coin_key, sigma, ctx.stream, C.byref(h))
+        self.h = h
+        self.rows, self.cols, self.group = rows, cols, group
+        sz = C.c_size_t()
+        ctx.check("hk_organ_info", ctx.L.hk_organ_info(h, None, None, None, None, C.byref(sz)))
+        self.packed_bytes = int(sz.value)
+
+
+class OrganSet:
+    """Organs of one kind and shape with a device-resident descriptor table:
+    `gemv` runs y_i = W_i x_i for all of them in one launch, no host sync."""
+
+    def __init__(self, ctx: Context, organs: list[PackedOrgan]):
+        self.ctx, self.organs = ctx, list(organs)
+        arr = (C.c_void_p * len(organs))(*[o.h.value for o in organs])
+        h = C.c_void_p()
+        ctx.call("hk_organ_set_create", arr, len(organs), C.byref(h))
+        self.h = h
+        self.rows, self.cols = organs[0].rows, organs[0].cols
+
+    def gemv(self, x: DeviceArray, x_stride: int, y: DeviceArray, y_stride: int, stream=None) -> None:
+        self.ctx.call("hk_gemv_set", self.h, x.ptr, x_stride, y.ptr, y_stride,
+                      stream if stream is not None else self.ctx.stream)
+
+    @property
+    def packed_bytes(self) -> int:
+        return sum(o.packed_bytes for o in self.organs)
+
+    def free(self):
+        if getattr(self, "h", None) and self.h.value and self.ctx.h:
+            self.ctx.L.hk_organ_set_free(self.ctx.h, self.h)
+        self.h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 def gemv_batch(ctx: Context, organs: list[PackedOrgan], x: DeviceArray, x_stride: int, y: DeviceArray,
                y_stride: int, stream=None) -> None:
     """y_i = W_i x_i for organs of one kind and shape, in one launch."""

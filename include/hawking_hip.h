@@ -138,6 +138,16 @@ int hk_gemv(hk_ctx* ctx, const hk_organ* organ, const float* x, float* y, hk_str
 int hk_gemv_batch(hk_ctx* ctx, const hk_organ* const* organs, uint32_t n, const float* x,
                   size_t x_stride, float* y, size_t y_stride, hk_stream stream);
 
+/* A fixed set of organs of one kind and shape whose device descriptor table
+ * is uploaded once, so hk_gemv_set launches with no host synchronisation
+ * (the persistent form of the routed wave / matvec_batch). */
+typedef struct hk_organ_set hk_organ_set;
+int hk_organ_set_create(hk_ctx* ctx, const hk_organ* const* organs, uint32_t n, hk_organ_set** out);
+int hk_organ_set_free(hk_ctx* ctx, hk_organ_set* set);
+/* y_i = W_i x_i for every organ of the set in ONE launch (strides as hk_gemv_batch). */
+int hk_gemv_set(hk_ctx* ctx, const hk_organ_set* set, const float* x, size_t x_stride, float* y,
+                size_t y_stride, hk_stream stream);
+
 /* Bit-exact decode probe: out[nrows*cols] = decoded weights of rows
  * [row0, row0+nrows).  Replaces qwen_uniform_q4_decode_vector
  * (shaders/qwen_uniform_q4.metal:627) and gather_row
@@ -165,6 +175,12 @@ int hk_pack_q2(hk_ctx* ctx, const float* w, size_t count, uint16_t* scales, uint
 uint64_t hk_stream_key(uint64_t seed, uint64_t stream_id);
 int hk_synth_normal(hk_ctx* ctx, uint64_t key, uint64_t first, size_t count, float sigma,
                     float* out, hk_stream stream);
+
+/* One organ generated and packed on the device: weights synth_normal(key, e, sigma)
+ * in row-major order, mixed coins from coin_key (as the MoE synthetic fill). */
+int hk_organ_synthetic(hk_ctx* ctx, int32_t kind, int32_t group, uint32_t rows, uint32_t cols,
+                       uint64_t key, uint64_t coin_key, float sigma, hk_stream stream,
+                       hk_organ** out);
 
 /* ------------------------------------------------------------------ routers */
 

@@ -143,6 +143,10 @@ void hko_fill_normal(uint64_t key, size_t count, float sigma, float* out) {
     for (size_t i = 0; i < count; ++i) out[i] = hko_normal(key, (uint64_t)i, sigma);
 }
 
+void hko_fill_normal_from(uint64_t key, uint64_t first, size_t count, float sigma, float* out) {
+    for (size_t i = 0; i < count; ++i) out[i] = hko_normal(key, first + (uint64_t)i, sigma);
+}
+
 /* p(binary) = 0.7: threshold floor(0.7 * 2^32). */
 int hko_mixed_coin(uint64_t coin_key, uint64_t group) {
     uint32_t u = (uint32_t)(stream_word(coin_key, group) >> 32);

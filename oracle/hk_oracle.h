@@ -50,6 +50,8 @@ void hko_deterministic_input(size_t cols, float* out);
 uint64_t hko_stream_key(uint64_t seed, uint64_t stream);
 float hko_normal(uint64_t key, uint64_t index, float sigma);
 void hko_fill_normal(uint64_t key, size_t count, float sigma, float* out);
+/* elements [first, first+count) of the stream */
+void hko_fill_normal_from(uint64_t key, uint64_t first, size_t count, float sigma, float* out);
 /* 1 when the 128-group `group` (flat index) of a mixed tensor is binary. */
 int hko_mixed_coin(uint64_t coin_key, uint64_t group);
 void hko_fill_coins(uint64_t coin_key, size_t groups, uint8_t* out);

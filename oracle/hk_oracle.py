@@ -47,6 +47,7 @@ def _declare(L: C.CDLL) -> None:
         "hko_stream_key": (C.c_uint64, [C.c_uint64, C.c_uint64]),
         "hko_normal": (C.c_float, [C.c_uint64, C.c_uint64, C.c_float]),
         "hko_fill_normal": (None, [C.c_uint64, _sz, C.c_float, _p]),
+        "hko_fill_normal_from": (None, [C.c_uint64, C.c_uint64, _sz, C.c_float, _p]),
         "hko_mixed_coin": (C.c_int, [C.c_uint64, C.c_uint64]),
         "hko_fill_coins": (None, [C.c_uint64, _sz, _p]),
         "hko_q4_pack": (C.c_int, [_p, _sz, _sz, C.c_int, _p, _p]),
@@ -135,9 +136,9 @@ def stream_key(seed: int, stream: int) -> int:
     return lib().hko_stream_key(seed, stream)
 
 
-def normal(key: int, count: int, sigma: float) -> np.ndarray:
+def normal(key: int, count: int, sigma: float, first: int = 0) -> np.ndarray:
     out = np.empty(count, np.float32)
-    lib().hko_fill_normal(key, count, sigma, _ptr(out))
+    lib().hko_fill_normal_from(key, first, count, sigma, _ptr(out))
     return out
 
 
