@@ -18,6 +18,13 @@ from ._lib import HK_MIXED, HK_Q4, MoeConfig, MoeLayerSrc, OrganSrc
 from .runtime import Context, DeviceArray
 
 
+def _pp(a):
+    """Device pointer of a DeviceArray, a raw c_void_p, or None."""
+    if a is None:
+        return None
+    return a.ptr if isinstance(a, DeviceArray) else a
+
+
 def _dev(ctx: Context, a) -> DeviceArray:
     return a if isinstance(a, DeviceArray) else ctx.to_device(np.ascontiguousarray(a, np.float32))
 
@@ -148,14 +155,14 @@ class MoeModel:
     def decode_layer_device(self, layer: int, h_in: DeviceArray, h_out: DeviceArray,
                             ids: DeviceArray | None = None, weights: DeviceArray | None = None,
                             stream=None) -> None:
-        self.ctx.call("hk_moe_decode_layer", self.h, layer, h_in.ptr, h_out.ptr,
-                      ids.ptr if ids is not None else None, weights.ptr if weights is not None else None,
+        self.ctx.call("hk_moe_decode_layer", self.h, layer, _pp(h_in), _pp(h_out),
+                      _pp(ids), _pp(weights),
                       stream if stream is not None else self.ctx.stream)
 
     def decode_stack_device(self, h_in: DeviceArray, h_out: DeviceArray, ids: DeviceArray | None = None,
                             weights: DeviceArray | None = None, stream=None) -> None:
-        self.ctx.call("hk_moe_decode_stack", self.h, h_in.ptr, h_out.ptr,
-                      ids.ptr if ids is not None else None, weights.ptr if weights is not None else None,
+        self.ctx.call("hk_moe_decode_stack", self.h, _pp(h_in), _pp(h_out),
+                      _pp(ids), _pp(weights),
                       stream if stream is not None else self.ctx.stream)
 
     def moe_suffix(self, layer: int, h: np.ndarray):
