@@ -17,10 +17,11 @@
 #include "hk_router.h"
 #include "hk_synth.h"
 
-using hk::OrganView;
+using hk::CanonView;
 
 struct hk_organ {
-    OrganView view{};
+    hk::OrganView view{};
+    void* view_dev = nullptr;  // device copy of `view` for single-organ launches
     void* mem = nullptr;
     size_t alloc_bytes = 0;
     size_t packed_bytes = 0;
@@ -132,9 +133,9 @@ static Layout layout_for(int kind, int group, uint32_t rows, uint32_t cols, uint
 }
 
 // Carves the sections of `L` out of `base` and returns the organ view.
-static OrganView place(int kind, int group, uint32_t rows, uint32_t cols, const Layout& L,
+static CanonView place(int kind, int group, uint32_t rows, uint32_t cols, const Layout& L,
                        uint8_t* base) {
-    OrganView v{};
+    CanonView v{};
     v.kind = kind;
     v.group = group;
     v.rows = rows;
@@ -196,8 +197,8 @@ static int validate_src(hk_ctx* ctx, const hk_organ_src* s, Layout* out) {
 
 // Copies one validated host organ into device memory at `base` (stream-ordered).
 static int copy_src(hk_ctx* ctx, const hk_organ_src* s, const Layout& L, uint8_t* base,
-                    OrganView* view, hipStream_t st, std::vector<std::vector<uint32_t>>* keep) {
-    OrganView v = place(s->kind, s->group, s->rows, s->cols, L, base);
+                    CanonView* view, hipStream_t st, std::vector<std::vector<uint32_t>>* keep) {
+    CanonView v = place(s->kind, s->group, s->rows, s->cols, L, base);
     auto cp = [&](const void* dst, const void* src, size_t bytes) -> int {
         if (!bytes) return HK_OK;
         return check_hip(ctx, hipMemcpyAsync(const_cast<void*>(dst), src, bytes, hipMemcpyHostToDevice, st),
@@ -401,6 +402,37 @@ extern "C" int hk_event_elapsed_ms(hk_ctx* ctx, void* a, void* b, float* ms) {
 }
 
 // ====================================================================== organs
+// Organs are staged in the canonical layout (host upload or device
+// generation), then repacked once into the tiled layout the kernels read.
+
+static int repack_into_organ(hk_ctx* ctx, const CanonView& canon, uint32_t n_bin, uint32_t n_q2, hipStream_t st,
+                             hk_organ** out) {
+    hk_organ* o = new hk_organ();
+    o->alloc_bytes = tiled_bytes(canon.kind, canon.group, canon.rows, canon.cols, n_bin, n_q2, &o->packed_bytes);
+    if (hipMalloc(&o->mem, o->alloc_bytes) != hipSuccess) {
+        delete o;
+        return set_error(ctx, HK_E_NOMEM, "organ allocation failed");
+    }
+    o->view = tiled_place(canon.kind, canon.group, canon.rows, canon.cols, n_bin, n_q2, static_cast<uint8_t*>(o->mem));
+    int rc = HK_OK;
+    if (canon.kind == HK_F32) {
+        rc = check_hip(ctx, hipMemcpyAsync(const_cast<float*>(o->view.dense), canon.dense,
+                                           (size_t)canon.rows * canon.cols * 4, hipMemcpyDeviceToDevice, st),
+                       "dense copy");
+    } else {
+        void* scratch = nullptr;
+        rc = ensure_scratch(ctx, 8 * ((size_t)o->view.n_tiles * o->view.steps + 1), &scratch);
+        if (!rc) rc = check_hip(ctx, launch_repack(canon, o->view, scratch, st), "repack launch");
+    }
+    if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "hipStreamSynchronize (repack)");
+    if (rc) {
+        (void)hipFree(o->mem);
+        delete o;
+        return rc;
+    }
+    *out = o;
+    return HK_OK;
+}
 
 extern "C" int hk_organ_upload(hk_ctx* ctx, const hk_organ_src* src, hk_stream stream, hk_organ** out) {
     if (!ctx || !out) return HK_E_INVALID_ARG;
@@ -408,30 +440,23 @@ extern "C" int hk_organ_upload(hk_ctx* ctx, const hk_organ_src* src, hk_stream s
     Layout L;
     int rc = validate_src(ctx, src, &L);
     if (rc) return rc;
-    hk_organ* o = new hk_organ();
-    o->alloc_bytes = L.total();
-    if (hipMalloc(&o->mem, o->alloc_bytes) != hipSuccess) {
-        delete o;
-        return set_error(ctx, HK_E_NOMEM, "organ allocation failed");
-    }
+    void* stage = nullptr;
+    if (hipMalloc(&stage, L.total()) != hipSuccess) return set_error(ctx, HK_E_NOMEM, "staging allocation failed");
     hipStream_t st = static_cast<hipStream_t>(stream);
     std::vector<std::vector<uint32_t>> keep;
-    rc = copy_src(ctx, src, L, static_cast<uint8_t*>(o->mem), &o->view, st, &keep);
-    if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "hipStreamSynchronize (organ upload)");
-    if (rc) {
-        (void)hipFree(o->mem);
-        delete o;
-        return rc;
-    }
-    o->packed_bytes = L.packed();
-    *out = o;
-    return HK_OK;
+    CanonView canon{};
+    rc = copy_src(ctx, src, L, static_cast<uint8_t*>(stage), &canon, st, &keep);
+    if (!rc) rc = repack_into_organ(ctx, canon, src->n_bin, src->n_q2, st, out);
+    (void)hipStreamSynchronize(st);
+    (void)hipFree(stage);
+    return rc;
 }
 
 extern "C" int hk_organ_free(hk_ctx* ctx, hk_organ* o) {
     if (!ctx) return HK_E_INVALID_ARG;
     if (!o) return HK_OK;
     int rc = check_hip(ctx, hipFree(o->mem), "hipFree (organ)");
+    if (o->view_dev) (void)hipFree(o->view_dev);
     delete o;
     return rc;
 }
@@ -447,45 +472,32 @@ extern "C" int hk_organ_info(const hk_organ* o, int32_t* kind, int32_t* group, u
     return HK_OK;
 }
 
-extern "C" int hk_gemv(hk_ctx* ctx, const hk_organ* o, const float* x, float* y, hk_stream stream) {
-    if (!ctx) return HK_E_INVALID_ARG;
-    if (!o || !x || !y) return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv: NULL organ or vector");
-    if (!aligned16(x) || !aligned16(y)) return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv: x and y must be 16-byte aligned");
-    return check_hip(ctx, launch_gemv(o->view, x, y, static_cast<hipStream_t>(stream)), "gemv launch");
+static int check_vectors(hk_ctx* ctx, const char* fn, const float* x, size_t x_stride, const float* y,
+                         size_t y_stride, uint32_t n, const OrganView& f) {
+    if (!x || !y) return set_error(ctx, HK_E_INVALID_ARG, std::string(fn) + ": NULL vector");
+    if (!aligned16(x) || !aligned16(y) || (x_stride % 4) || (y_stride % 4))
+        return set_error(ctx, HK_E_INVALID_ARG, std::string(fn) + ": x/y must be 16-byte aligned with strides % 4 == 0");
+    if (n > 1 && (x_stride < f.cols || y_stride < f.rows))
+        return set_error(ctx, HK_E_GEOMETRY, std::string(fn) + ": strides smaller than the organ shape");
+    return HK_OK;
 }
 
-extern "C" int hk_gemv_batch(hk_ctx* ctx, const hk_organ* const* organs, uint32_t n, const float* x,
-                             size_t x_stride, float* y, size_t y_stride, hk_stream stream) {
+extern "C" int hk_gemv(hk_ctx* ctx, const hk_organ* o, const float* x, float* y, hk_stream stream) {
     if (!ctx) return HK_E_INVALID_ARG;
-    if (!organs || !x || !y || n == 0) return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv_batch: bad arguments");
-    if (n > 65535) return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv_batch: at most 65535 organs per launch");
-    if (!aligned16(x) || !aligned16(y) || (x_stride % 4) || (y_stride % 4) || (n > 1 && (!x_stride || !y_stride)))
-        return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv_batch: x/y must be 16-byte aligned with strides % 4 == 0");
-    std::vector<OrganView> views(n);
-    for (uint32_t i = 0; i < n; ++i) {
-        if (!organs[i]) return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv_batch: NULL organ");
-        views[i] = organs[i]->view;
-        const OrganView& a = views[0];
-        const OrganView& b = views[i];
-        if (a.kind != b.kind || a.rows != b.rows || a.cols != b.cols || a.group != b.group)
-            return set_error(ctx, HK_E_GEOMETRY, "hk_gemv_batch: organs must share kind and shape");
-    }
-    if (x_stride && x_stride < views[0].cols) return set_error(ctx, HK_E_GEOMETRY, "hk_gemv_batch: x_stride < cols");
-    if (y_stride && y_stride < views[0].rows) return set_error(ctx, HK_E_GEOMETRY, "hk_gemv_batch: y_stride < rows");
-    void* dv = nullptr;
-    int rc = ensure_scratch(ctx, n * sizeof(OrganView), &dv);
+    if (!o) return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv: NULL organ");
+    int rc = check_vectors(ctx, "hk_gemv", x, 0, y, 0, 1, o->view);
     if (rc) return rc;
+    // the single-organ descriptor lives in the organ's own scratch slot
     hipStream_t st = static_cast<hipStream_t>(stream);
-    rc = check_hip(ctx, hipMemcpyAsync(dv, views.data(), n * sizeof(OrganView), hipMemcpyHostToDevice, st),
-                   "descriptor upload");
-    if (rc) return rc;
-    // the host vector must outlive the copy
-    rc = check_hip(ctx, hipStreamSynchronize(st), "hipStreamSynchronize (descriptor upload)");
-    if (rc) return rc;
-    return check_hip(ctx,
-                     launch_gemv_batch(static_cast<const OrganView*>(dv), n, views[0].kind, views[0].rows,
-                                       views[0].cols, views[0].group, x, x_stride, y, y_stride, st),
-                     "gemv_batch launch");
+    if (!o->view_dev) {
+        hk_organ* m = const_cast<hk_organ*>(o);
+        if (hipMalloc(&m->view_dev, sizeof(OrganView)) != hipSuccess)
+            return set_error(ctx, HK_E_NOMEM, "descriptor allocation failed");
+        rc = check_hip(ctx, hipMemcpy(m->view_dev, &m->view, sizeof(OrganView), hipMemcpyHostToDevice), "descriptor upload");
+        if (rc) return rc;
+    }
+    return check_hip(ctx, launch_gemv_tiled(static_cast<const OrganView*>(o->view_dev), 1, o->view, x, 0, y, 0, st),
+                     "gemv launch");
 }
 
 struct hk_organ_set {
@@ -536,23 +548,32 @@ extern "C" int hk_organ_set_free(hk_ctx* ctx, hk_organ_set* set) {
 extern "C" int hk_gemv_set(hk_ctx* ctx, const hk_organ_set* set, const float* x, size_t x_stride, float* y,
                            size_t y_stride, hk_stream stream) {
     if (!ctx) return HK_E_INVALID_ARG;
-    if (!set || !x || !y) return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv_set: NULL argument");
-    if (!aligned16(x) || !aligned16(y) || (x_stride % 4) || (y_stride % 4) ||
-        (set->n > 1 && (x_stride < set->first.cols || y_stride < set->first.rows)))
-        return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv_set: bad alignment or strides");
-    const OrganView& f = set->first;
+    if (!set) return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv_set: NULL set");
+    int rc = check_vectors(ctx, "hk_gemv_set", x, x_stride, y, y_stride, set->n, set->first);
+    if (rc) return rc;
     return check_hip(ctx,
-                     launch_gemv_batch(set->dev, set->n, f.kind, f.rows, f.cols, f.group, x, x_stride, y, y_stride,
+                     launch_gemv_tiled(set->dev, set->n, set->first, x, x_stride, y, y_stride,
                                        static_cast<hipStream_t>(stream)),
                      "gemv_set launch");
+}
+
+extern "C" int hk_gemv_batch(hk_ctx* ctx, const hk_organ* const* organs, uint32_t n, const float* x,
+                             size_t x_stride, float* y, size_t y_stride, hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    hk_organ_set* set = nullptr;
+    int rc = hk_organ_set_create(ctx, organs, n, &set);
+    if (rc) return rc;
+    rc = hk_gemv_set(ctx, set, x, x_stride, y, y_stride, stream);
+    if (!rc) rc = check_hip(ctx, hipStreamSynchronize(static_cast<hipStream_t>(stream)), "hipStreamSynchronize");
+    int rc2 = hk_organ_set_free(ctx, set);
+    return rc ? rc : rc2;
 }
 
 extern "C" int hk_organ_synthetic(hk_ctx* ctx, int32_t kind, int32_t group, uint32_t rows, uint32_t cols, uint64_t key,
                                   uint64_t coin_key, float sigma, hk_stream stream, hk_organ** out) {
     if (!ctx || !out) return HK_E_INVALID_ARG;
     *out = nullptr;
-    if (kind == HK_BIN) group = 128;
-    if (kind == HK_MIXED) group = 128;
+    if (kind == HK_BIN || kind == HK_MIXED) group = 128;
     int rc = validate_shape(ctx, kind, group, rows, cols);
     if (rc) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -576,24 +597,23 @@ extern "C" int hk_organ_synthetic(hk_ctx* ctx, int32_t kind, int32_t group, uint
         if (!rc) rc = check_hip(ctx, hipMemcpyAsync(&nbin, aux + 1, 4, hipMemcpyDeviceToHost, st), "count read");
         if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "sync");
     }
-    hk_organ* o = nullptr;
+    const uint32_t nq2 = kind == HK_MIXED ? (uint32_t)(groups - nbin) : 0;
+    void* stage = nullptr;
+    CanonView canon{};
     if (!rc) {
-        const Layout L = layout_for(kind, group, rows, cols, nbin, kind == HK_MIXED ? (uint32_t)(groups - nbin) : 0);
-        o = new hk_organ();
-        o->alloc_bytes = L.total();
-        o->packed_bytes = L.packed();
-        if (hipMalloc(&o->mem, o->alloc_bytes) != hipSuccess) {
-            rc = set_error(ctx, HK_E_NOMEM, "organ allocation failed");
+        const Layout L = layout_for(kind, group, rows, cols, nbin, nq2);
+        if (hipMalloc(&stage, L.total()) != hipSuccess) {
+            rc = set_error(ctx, HK_E_NOMEM, "staging allocation failed");
         } else {
-            o->view = place(kind, group, rows, cols, L, static_cast<uint8_t*>(o->mem));
-            j.scales = const_cast<uint16_t*>(o->view.scales);
-            j.codes = const_cast<uint8_t*>(o->view.codes);
-            j.tags = const_cast<uint8_t*>(o->view.tags);
-            j.q2_scales = const_cast<uint16_t*>(o->view.q2_scales);
-            j.q2_codes = const_cast<uint8_t*>(o->view.q2_codes);
-            j.row_bin = const_cast<uint32_t*>(o->view.row_bin);
-            j.row_q2 = const_cast<uint32_t*>(o->view.row_q2);
-            j.dense = const_cast<float*>(o->view.dense);
+            canon = place(kind, group, rows, cols, L, static_cast<uint8_t*>(stage));
+            j.scales = const_cast<uint16_t*>(canon.scales);
+            j.codes = const_cast<uint8_t*>(canon.codes);
+            j.tags = const_cast<uint8_t*>(canon.tags);
+            j.q2_scales = const_cast<uint16_t*>(canon.q2_scales);
+            j.q2_codes = const_cast<uint8_t*>(canon.q2_codes);
+            j.row_bin = const_cast<uint32_t*>(canon.row_bin);
+            j.row_q2 = const_cast<uint32_t*>(canon.row_q2);
+            j.dense = const_cast<float*>(canon.dense);
             rc = check_hip(ctx, hipMemcpyAsync(jd, &j, sizeof(j), hipMemcpyHostToDevice, st), "job upload");
             if (!rc) rc = check_hip(ctx, launch_synth_jobs(kind, jd, 1, groups, aux, st), "synth organ");
             uint32_t bad = 0;
@@ -602,16 +622,11 @@ extern "C" int hk_organ_synthetic(hk_ctx* ctx, int32_t kind, int32_t group, uint
             if (!rc && bad) rc = set_error(ctx, HK_E_NONFINITE, "synthetic organ has a non-finite scale");
         }
     }
+    if (!rc) rc = repack_into_organ(ctx, canon, nbin, nq2, st, out);
+    (void)hipStreamSynchronize(st);
+    if (stage) (void)hipFree(stage);
     (void)hipFree(tmp);
-    if (rc) {
-        if (o) {
-            if (o->mem) (void)hipFree(o->mem);
-            delete o;
-        }
-        return rc;
-    }
-    *out = o;
-    return HK_OK;
+    return rc;
 }
 
 extern "C" int hk_decode_rows(hk_ctx* ctx, const hk_organ* o, uint32_t row0, uint32_t nrows, float* out,
@@ -738,9 +753,9 @@ constexpr float SIGMA_W = 0.02f, SIGMA_NORM = 0.02f;
 struct MoeLayerHost {
     void* slab = nullptr;
     size_t slab_bytes = 0;
-    std::vector<OrganView> table;      // (E+1)*3
+    std::vector<CanonView> table;      // (E+1)*3
     std::vector<size_t> packed;        // per organ, algorithmic bytes
-    OrganView* table_dev = nullptr;
+    CanonView* table_dev = nullptr;
     float* norm_w = nullptr;
     float* router_w = nullptr;
     float* gate_w = nullptr;
@@ -804,7 +819,7 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
     m->dims = hk::MoeDims{c.hidden, c.inter, c.shared_inter, imax, c.n_experts, c.top_k, c.shared_inter ? 1 : 0, c.eps};
     m->layers.resize(c.n_layers);
     const size_t dpl = dense_per_layer(c);
-    const size_t tab = align256((size_t)(c.n_experts + 1) * 3 * sizeof(OrganView));
+    const size_t tab = align256((size_t)(c.n_experts + 1) * 3 * sizeof(CanonView));
     const size_t ws = align256((size_t)c.hidden * 4) + align256(((size_t)c.n_experts + 4) * 4) + 256 + 256 + 256 +
                       align256((size_t)(c.top_k + 1) * imax * 4) + 2 * align256((size_t)c.hidden * 4);
     if (hipMalloc(&m->dense, dpl * c.n_layers) != hipSuccess || hipMalloc(&m->tables, tab * c.n_layers) != hipSuccess ||
@@ -822,8 +837,8 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
         L.norm_w = reinterpret_cast<float*>(d);
         L.router_w = reinterpret_cast<float*>(d + align256((size_t)c.hidden * 4));
         L.gate_w = reinterpret_cast<float*>(d + align256((size_t)c.hidden * 4) + align256((size_t)c.n_experts * c.hidden * 4));
-        L.table_dev = reinterpret_cast<OrganView*>(static_cast<uint8_t*>(m->tables) + l * tab);
-        L.table.assign((size_t)(c.n_experts + 1) * 3, OrganView{});
+        L.table_dev = reinterpret_cast<CanonView*>(static_cast<uint8_t*>(m->tables) + l * tab);
+        L.table.assign((size_t)(c.n_experts + 1) * 3, CanonView{});
         L.packed.assign((size_t)(c.n_experts + 1) * 3, 0);
     }
     uint8_t* w = static_cast<uint8_t*>(m->ws_mem);
@@ -862,7 +877,7 @@ extern "C" int hk_moe_model_free(hk_ctx* ctx, hk_moe_model* m) {
 
 static int upload_table(hk_ctx* ctx, MoeLayerHost& L, hipStream_t st) {
     int rc = check_hip(ctx,
-                       hipMemcpyAsync(L.table_dev, L.table.data(), L.table.size() * sizeof(OrganView),
+                       hipMemcpyAsync(L.table_dev, L.table.data(), L.table.size() * sizeof(CanonView),
                                       hipMemcpyHostToDevice, st),
                        "expert table upload");
     if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "hipStreamSynchronize (expert table)");
@@ -1011,7 +1026,7 @@ extern "C" int hk_moe_model_fill_synthetic(hk_ctx* ctx, hk_moe_model* m, uint64_
         uint8_t* p = static_cast<uint8_t*>(L.slab);
         for (uint32_t i = 0; i < n_org; ++i) {
             SynthJob& j = jobs[i];
-            OrganView v = place(c.expert_kind, c.expert_group, j.rows, j.cols, lay[i], p);
+            CanonView v = place(c.expert_kind, c.expert_group, j.rows, j.cols, lay[i], p);
             j.scales = const_cast<uint16_t*>(v.scales);
             j.codes = const_cast<uint8_t*>(v.codes);
             j.tags = const_cast<uint8_t*>(v.tags);

@@ -27,9 +27,11 @@
 
 namespace hk {
 
-// ------------------------------------------------------------------ device organ view
+// ------------------------------------------------------------------ device organ views
 
-struct OrganView {
+// An organ in the canonical (reference) byte layout described above; the
+// load-time repack reads it, and the MoE model stores experts in it.
+struct CanonView {
     int32_t kind;
     int32_t group;
     uint32_t rows;
@@ -42,6 +44,20 @@ struct OrganView {
     const uint32_t* row_bin;    // MIXED, [rows+1]
     const uint32_t* row_q2;     // MIXED, [rows+1]
     const float* dense;         // F32
+};
+
+// An organ in the wavefront-tiled layout (hk_tile.h) the GEMV kernels read.
+struct OrganView {
+    int32_t kind;
+    int32_t group;
+    uint32_t rows;
+    uint32_t cols;
+    uint32_t n_tiles;           // ceil(rows / 16)
+    uint32_t steps;             // 1 KiB wave loads per tile
+    const uint8_t* data;        // signs / codes / mixed items
+    const uint16_t* scales;
+    const uint4* hdr;           // MIXED per-(tile, step) headers
+    const float* dense;         // F32 (row-major, not tiled)
 };
 
 // ------------------------------------------------------------------ device helpers
@@ -96,11 +112,18 @@ int check_hip(hk_ctx* ctx, hipError_t e, const char* what);
 int ensure_scratch(hk_ctx* ctx, size_t bytes, void** out);
 
 // Kernel launchers (defined in the .hip files); all stream-ordered, no sync.
-hipError_t launch_gemv(const OrganView& o, const float* x, float* y, hipStream_t s);
-hipError_t launch_gemv_batch(const OrganView* organs_dev, uint32_t n, int kind, uint32_t rows,
-                             uint32_t cols, int group, const float* x, size_t x_stride,
-                             float* y, size_t y_stride, hipStream_t s);
+// GEMV over n organs of one kind/shape (descriptor table in device memory).
+hipError_t launch_gemv_tiled(const OrganView* organs_dev, uint32_t n, const OrganView& shape,
+                             const float* x, size_t x_stride, float* y, size_t y_stride,
+                             hipStream_t s);
 hipError_t launch_decode_rows(const OrganView& o, uint32_t row0, uint32_t nrows, float* out,
                               hipStream_t s);
+// Canonical -> tiled repack of one organ; `scratch` holds >= 8*(n_tiles*steps+1) bytes.
+hipError_t launch_repack(const CanonView& src, const OrganView& dst, void* scratch, hipStream_t s);
+// Device bytes of the tiled layout (sections 256-B aligned); mixed needs n_bin/n_q2.
+size_t tiled_bytes(int kind, int group, uint32_t rows, uint32_t cols, uint32_t n_bin, uint32_t n_q2,
+                   size_t* packed_bytes);
+OrganView tiled_place(int kind, int group, uint32_t rows, uint32_t cols, uint32_t n_bin, uint32_t n_q2,
+                      uint8_t* base);
 
 }  // namespace hk

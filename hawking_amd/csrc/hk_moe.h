@@ -22,7 +22,7 @@ struct MoeLayerDev {
     const float* norm_w;
     const float* router_w;
     const float* gate_w;   // shared-expert gate, may be null
-    const OrganView* table;
+    const CanonView* table;
 };
 
 // Per-model device workspace.

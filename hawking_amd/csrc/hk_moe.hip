@@ -39,7 +39,7 @@ __global__ void __launch_bounds__(256) moe_router_kernel(MoeDims d, MoeLayerDev 
     __syncthreads();
     const int lane = threadIdx.x & 63;
     const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    OrganView o{};
+    CanonView o{};
     o.kind = HK_F32;
     o.cols = d.H;
     if (row < d.E) {
@@ -76,8 +76,8 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev
         if (threadIdx.x == 0) atomicOr(ws.status, HK_DEVERR_ROUTE);
         return;
     }
-    const OrganView& g = L.table[e * 3 + 0];
-    const OrganView& u = L.table[e * 3 + 1];
+    const CanonView& g = L.table[e * 3 + 0];
+    const CanonView& u = L.table[e * 3 + 1];
     const int lane = threadIdx.x & 63;
     const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= g.rows) return;
@@ -101,12 +101,12 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDims d, MoeLayerDev L,
     for (uint32_t r = 0; r < d.K; ++r) {
         const uint32_t e = (uint32_t)ws.ids[r];
         if (e >= d.E) continue;  // flagged by the gate/up kernel
-        const OrganView& dn = L.table[e * 3 + 2];
+        const CanonView& dn = L.table[e * 3 + 2];
         const float y = wave_sum(row_dot_partial<KIND>(dn, row, act + (size_t)r * d.Imax, lane));
         combined += y * ws.weights[r];
     }
     if (d.has_shared) {
-        const OrganView& dn = L.table[d.E * 3 + 2];
+        const CanonView& dn = L.table[d.E * 3 + 2];
         const float y = wave_sum(row_dot_partial<KIND>(dn, row, act + (size_t)d.K * d.Imax, lane));
         combined += y * ws.gate[1];
     }

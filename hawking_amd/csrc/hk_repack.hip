@@ -1,0 +1,228 @@
+// hk_repack.hip -- load-time repack of canonical organs into the wavefront-
+// tiled layout (hk_tile.h), and the bit-exact decode probe over that layout.
+#include "hk_internal.h"
+#include "hk_tile.h"
+
+namespace hk {
+
+static inline size_t a256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+size_t tiled_bytes(int kind, int group, uint32_t rows, uint32_t cols, uint32_t n_bin, uint32_t n_q2,
+                   size_t* packed_bytes) {
+    const size_t nt = n_tiles_for(rows), S = n_steps_for(kind, cols), n = (size_t)rows * cols;
+    size_t data = 0, scales = 0, hdr = 0, dense = 0, packed = 0;
+    switch (kind) {
+    case HK_BIN:
+        data = nt * S * 1024;
+        scales = nt * 64 * S * 2 + 16;
+        packed = n / 8 + n / 128 * 2;
+        break;
+    case HK_Q4:
+        data = nt * S * 1024;
+        scales = nt * 64 * S * 2 + 16;
+        packed = n / 2 + n / (size_t)group * 2;
+        break;
+    case HK_MIXED: {
+        const size_t items = nt * S * 64, pad = items - (size_t)n_bin - n_q2;
+        data = ((size_t)n_bin + pad) * 16 + (size_t)n_q2 * 32;
+        scales = ((size_t)n_bin + pad + 2 * (size_t)n_q2) * 2 + 16;
+        hdr = nt * S * 16;
+        packed = (n / 128 + 7) / 8 + (size_t)n_bin * 18 + (size_t)n_q2 * 36;
+        break;
+    }
+    default:
+        dense = n * 4;
+        packed = n * 4;
+    }
+    if (packed_bytes) *packed_bytes = packed;
+    return a256(data) + a256(scales) + a256(hdr) + a256(dense);
+}
+
+OrganView tiled_place(int kind, int group, uint32_t rows, uint32_t cols, uint32_t n_bin, uint32_t n_q2,
+                      uint8_t* base) {
+    OrganView v{};
+    v.kind = kind;
+    v.group = group;
+    v.rows = rows;
+    v.cols = cols;
+    v.n_tiles = n_tiles_for(rows);
+    v.steps = kind == HK_F32 ? 0 : n_steps_for(kind, cols);
+    const size_t nt = v.n_tiles, S = v.steps, n = (size_t)rows * cols;
+    size_t data = 0, scales = 0, hdr = 0;
+    if (kind == HK_BIN || kind == HK_Q4) {
+        data = nt * S * 1024;
+        scales = nt * 64 * S * 2 + 16;
+    } else if (kind == HK_MIXED) {
+        const size_t items = nt * S * 64, pad = items - (size_t)n_bin - n_q2;
+        data = ((size_t)n_bin + pad) * 16 + (size_t)n_q2 * 32;
+        scales = ((size_t)n_bin + pad + 2 * (size_t)n_q2) * 2 + 16;
+        hdr = nt * S * 16;
+    }
+    uint8_t* p = base;
+    v.data = p;
+    p += a256(data);
+    v.scales = reinterpret_cast<const uint16_t*>(p);
+    p += a256(scales);
+    v.hdr = reinterpret_cast<const uint4*>(p);
+    p += a256(hdr);
+    v.dense = reinterpret_cast<const float*>(p);
+    (void)n;
+    return v;
+}
+
+// ------------------------------------------------------------------ BIN / Q4
+
+// One thread per (tile, step, lane) item: copy its 16 bytes and its scale.
+__global__ void repack_fixed_kernel(CanonView src, OrganView dst) {
+    const size_t total = (size_t)dst.n_tiles * dst.steps * 64;
+    for (size_t it = (size_t)blockIdx.x * blockDim.x + threadIdx.x; it < total;
+         it += (size_t)gridDim.x * blockDim.x) {
+        const uint32_t l = (uint32_t)(it & 63), ts = (uint32_t)(it >> 6);
+        const uint32_t T = ts / dst.steps, t = ts % dst.steps, n = l & 15u, q = l >> 4;
+        const uint32_t r = T * 16u + n;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        uint16_t s = 0;
+        if (src.kind == HK_BIN) {
+            const uint32_t g = 4u * t + q;
+            if (r < src.rows && g < src.cols / 128u) {
+                v = *reinterpret_cast<const uint4*>(src.codes + (size_t)r * (src.cols / 8u) + 16u * g);
+                s = src.scales[(size_t)r * (src.cols / 128u) + g];
+            }
+        } else {
+            const uint32_t c = 4u * t + q;
+            if (r < src.rows && c < src.cols / 32u) {
+                const size_t e = (size_t)r * src.cols + 32u * c;
+                v = *reinterpret_cast<const uint4*>(src.codes + e / 2);
+                s = src.scales[e / (uint32_t)src.group];
+            }
+        }
+        *reinterpret_cast<uint4*>(const_cast<uint8_t*>(dst.data) + (size_t)ts * 1024u + 16u * l) = v;
+        const_cast<uint16_t*>(dst.scales)[((size_t)T * 64u + l) * dst.steps + t] = s;
+    }
+}
+
+// ------------------------------------------------------------------ MIXED
+
+__device__ inline bool canon_is_q2(const CanonView& s, uint32_t r, uint32_t g, bool* valid) {
+    *valid = r < s.rows && g < s.cols / 128u;
+    if (!*valid) return false;
+    const uint32_t fg = r * (s.cols / 128u) + g;
+    return !((s.tags[fg >> 3] >> (fg & 7u)) & 1u);
+}
+
+// Pass 1: one thread per (tile, step) block: Q2 mask and count.
+__global__ void repack_mixed_mask_kernel(CanonView src, OrganView dst, uint32_t* counts) {
+    const uint32_t nb = dst.n_tiles * dst.steps;
+    for (uint32_t b = blockIdx.x * blockDim.x + threadIdx.x; b < nb; b += gridDim.x * blockDim.x) {
+        const uint32_t T = b / dst.steps, t = b % dst.steps;
+        uint64_t mask = 0;
+        for (uint32_t l = 0; l < 64; ++l) {
+            bool valid;
+            if (canon_is_q2(src, T * 16u + (l & 15u), 4u * t + (l >> 4), &valid)) mask |= 1ull << l;
+        }
+        uint4* h = const_cast<uint4*>(dst.hdr) + b;
+        h->x = (uint32_t)mask;
+        h->y = (uint32_t)(mask >> 32);
+        counts[b] = __popcll(mask);
+    }
+}
+
+// Pass 2 (one block): exclusive prefix of Q2 counts -> data / scale offsets.
+__global__ void repack_mixed_offsets_kernel(OrganView dst, const uint32_t* counts) {
+    if (threadIdx.x != 0) return;
+    const uint32_t nb = dst.n_tiles * dst.steps;
+    uint32_t q2 = 0;
+    for (uint32_t b = 0; b < nb; ++b) {
+        uint4* h = const_cast<uint4*>(dst.hdr) + b;
+        h->z = 16u * (64u * b + q2);
+        h->w = 64u * b + q2;
+        q2 += counts[b];
+    }
+}
+
+// Pass 3: one thread per item: copy binary signs, or reorder Q2 codes.
+__global__ void repack_mixed_items_kernel(CanonView src, OrganView dst) {
+    const size_t total = (size_t)dst.n_tiles * dst.steps * 64;
+    const uint32_t gpr = src.cols / 128u;
+    for (size_t it = (size_t)blockIdx.x * blockDim.x + threadIdx.x; it < total;
+         it += (size_t)gridDim.x * blockDim.x) {
+        const uint32_t l = (uint32_t)(it & 63), b = (uint32_t)(it >> 6);
+        const uint32_t T = b / dst.steps, t = b % dst.steps, r = T * 16u + (l & 15u), g = 4u * t + (l >> 4);
+        const uint4 h = dst.hdr[b];
+        const uint64_t mask = (uint64_t)h.x | ((uint64_t)h.y << 32);
+        const uint32_t below = __popcll(mask & ((1ull << l) - 1ull));
+        uint8_t* item = const_cast<uint8_t*>(dst.data) + h.z + 16u * (l + below);
+        uint16_t* sc = const_cast<uint16_t*>(dst.scales) + h.w + l + below;
+        bool valid;
+        const bool q2 = canon_is_q2(src, r, g, &valid);
+        if (!valid) {
+            *reinterpret_cast<uint4*>(item) = make_uint4(0, 0, 0, 0);
+            sc[0] = 0;
+            continue;
+        }
+        const uint32_t fg = r * gpr + g;
+        uint32_t nbin = 0;
+        for (uint32_t k = r * gpr; k < fg; ++k) nbin += (src.tags[k >> 3] >> (k & 7u)) & 1u;
+        if (!q2) {
+            const uint32_t idx = src.row_bin[r] + nbin;
+            *reinterpret_cast<uint4*>(item) = *reinterpret_cast<const uint4*>(src.codes + (size_t)idx * 16u);
+            sc[0] = src.scales[idx];
+        } else {
+            const uint32_t idx = src.row_q2[r] + (g - nbin);
+            const uint8_t* cs = src.q2_codes + (size_t)idx * 32u;
+            uint32_t w[8];
+            for (uint32_t a = 0; a < 8; ++a) {
+                uint32_t word = 0;
+                for (uint32_t j = 0; j < 4; ++j)
+                    for (uint32_t u = 0; u < 4; ++u) {
+                        const uint32_t e = mixed_q2_col(a, j, u);
+                        const uint32_t code = (cs[e >> 2] >> (2u * (e & 3u))) & 3u;
+                        word |= code << (8u * j + 2u * u);
+                    }
+                w[a] = word;
+            }
+            reinterpret_cast<uint4*>(item)[0] = make_uint4(w[0], w[1], w[2], w[3]);
+            reinterpret_cast<uint4*>(item)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+            sc[0] = src.q2_scales[2u * idx];
+            sc[1] = src.q2_scales[2u * idx + 1u];
+        }
+    }
+}
+
+static unsigned grid1(size_t n) {
+    size_t b = (n + 255) / 256;
+    return (unsigned)(b == 0 ? 1 : (b > 65536 ? 65536 : b));
+}
+
+hipError_t launch_repack(const CanonView& src, const OrganView& dst, void* scratch, hipStream_t s) {
+    const size_t items = (size_t)dst.n_tiles * dst.steps * 64;
+    if (src.kind == HK_BIN || src.kind == HK_Q4) {
+        hipLaunchKernelGGL(repack_fixed_kernel, dim3(grid1(items)), dim3(256), 0, s, src, dst);
+    } else if (src.kind == HK_MIXED) {
+        uint32_t* counts = static_cast<uint32_t*>(scratch);
+        hipLaunchKernelGGL(repack_mixed_mask_kernel, dim3(grid1(items / 64)), dim3(256), 0, s, src, dst, counts);
+        hipLaunchKernelGGL(repack_mixed_offsets_kernel, dim3(1), dim3(64), 0, s, dst, counts);
+        hipLaunchKernelGGL(repack_mixed_items_kernel, dim3(grid1(items)), dim3(256), 0, s, src, dst);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ decode probe
+
+__global__ void decode_tiled_kernel(OrganView o, uint32_t row0, uint32_t nrows, float* __restrict__ out) {
+    const size_t total = (size_t)nrows * o.cols;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x)
+        out[i] = tiled_weight(o, row0 + (uint32_t)(i / o.cols), (uint32_t)(i % o.cols));
+}
+
+hipError_t launch_decode_rows(const OrganView& o, uint32_t row0, uint32_t nrows, float* out, hipStream_t s) {
+    const size_t total = (size_t)nrows * o.cols;
+    if (!total) return hipSuccess;
+    hipLaunchKernelGGL(decode_tiled_kernel, dim3(grid1(total)), dim3(256), 0, s, o, row0, nrows, out);
+    return hipGetLastError();
+}
+
+}  // namespace hk

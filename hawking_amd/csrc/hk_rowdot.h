@@ -72,12 +72,12 @@ __device__ __forceinline__ uint32_t mixed_bin_before(const uint8_t* __restrict__
 }
 
 template <int KIND>
-__device__ __forceinline__ float row_dot_partial(const OrganView& o, uint32_t row,
+__device__ __forceinline__ float row_dot_partial(const CanonView& o, uint32_t row,
                                                  const float* __restrict__ x, int lane,
                                                  int width = 64);
 
 template <>
-__device__ __forceinline__ float row_dot_partial<HK_Q4>(const OrganView& o, uint32_t row,
+__device__ __forceinline__ float row_dot_partial<HK_Q4>(const CanonView& o, uint32_t row,
                                                         const float* __restrict__ x, int lane,
                                                         int width) {
     const uint32_t chunks = o.cols >> 5;
@@ -92,7 +92,7 @@ __device__ __forceinline__ float row_dot_partial<HK_Q4>(const OrganView& o, uint
 }
 
 template <>
-__device__ __forceinline__ float row_dot_partial<HK_BIN>(const OrganView& o, uint32_t row,
+__device__ __forceinline__ float row_dot_partial<HK_BIN>(const CanonView& o, uint32_t row,
                                                          const float* __restrict__ x, int lane,
                                                          int width) {
     const uint32_t chunks = o.cols >> 5;
@@ -107,7 +107,7 @@ __device__ __forceinline__ float row_dot_partial<HK_BIN>(const OrganView& o, uin
 }
 
 template <>
-__device__ __forceinline__ float row_dot_partial<HK_MIXED>(const OrganView& o, uint32_t row,
+__device__ __forceinline__ float row_dot_partial<HK_MIXED>(const CanonView& o, uint32_t row,
                                                            const float* __restrict__ x, int lane,
                                                            int width) {
     const uint32_t chunks = o.cols >> 5;
@@ -131,7 +131,7 @@ __device__ __forceinline__ float row_dot_partial<HK_MIXED>(const OrganView& o, u
 }
 
 template <>
-__device__ __forceinline__ float row_dot_partial<HK_F32>(const OrganView& o, uint32_t row,
+__device__ __forceinline__ float row_dot_partial<HK_F32>(const CanonView& o, uint32_t row,
                                                          const float* __restrict__ x, int lane,
                                                          int width) {
     const uint32_t chunks = o.cols >> 2;
@@ -149,7 +149,7 @@ __device__ __forceinline__ float row_dot_partial<HK_F32>(const OrganView& o, uin
 }
 
 // Decoded weight (r, c), bit-exact with the reference decoders.
-__device__ __forceinline__ float decode_weight(const OrganView& o, uint32_t r, uint32_t c) {
+__device__ __forceinline__ float decode_weight(const CanonView& o, uint32_t r, uint32_t c) {
     const size_t e = (size_t)r * o.cols + c;
     switch (o.kind) {
     case HK_Q4: {

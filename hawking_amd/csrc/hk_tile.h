@@ -1,0 +1,80 @@
+// hk_tile.h -- the wavefront-tiled device layout of packed organs.
+//
+// Rows are grouped in tiles of 16 (one MFMA N block); a tile is consumed in
+// "steps", and one step is exactly one 1 KiB wave load: lane l of the wave
+// (n = l % 16 = row in the tile, q = l / 16 = column slot) reads 16 bytes at
+// offset 16*l.  Rows and columns are zero-padded to whole tiles and steps
+// (zero scales contribute exactly 0).
+//
+//   BIN   step = 512 columns; lane (n,q) holds the 16 sign bytes of row n,
+//         128-group 4t+q (bit i of byte j = column 8j+i, 1 = +scale).
+//         scales: [tile][lane][step] f16.
+//   Q4    step = 128 columns; lane (n,q) holds the 16 code bytes of row n,
+//         32-column chunk 4t+q (byte b: column 2b in the low nibble, 2b+1 in
+//         the high nibble, value (nibble-8)*scale).
+//         scales: [tile][lane][step] f16, the scale of the chunk's group
+//         (duplicated per chunk when group > 32).
+//   MIXED step = 512 columns; item (n,q) is row n, 128-group 4t+q, either
+//         binary (16 B of signs, one f16 scale) or Q2 (32 B of 2-bit codes,
+//         two f16 scales for columns 0-63 and 64-127).  Per (tile, step) a
+//         16-byte header {q2mask.lo, q2mask.hi, data_off, scale_off}: item l
+//         starts at data_off + 16*(l + popcount(q2mask below l)) bytes and its
+//         scales at scale_off + (l + popcount(q2mask below l)) u16s.
+//         Q2 code order inside an item (so one shift pattern decodes both
+//         kinds): dword a (0..3) byte j holds, in 2-bit fields u = 0..3, the
+//         codes of columns 32a + 8j + 2u; dword 4+a byte j holds columns
+//         32a + 8j + 2u + 1.
+#pragma once
+
+#include "hk_internal.h"
+
+namespace hk {
+
+constexpr uint32_t TILE_ROWS = 16;
+
+__host__ __device__ inline uint32_t tile_step_cols(int kind) { return kind == HK_Q4 ? 128u : 512u; }
+__host__ __device__ inline uint32_t n_tiles_for(uint32_t rows) { return (rows + TILE_ROWS - 1) / TILE_ROWS; }
+__host__ __device__ inline uint32_t n_steps_for(int kind, uint32_t cols) {
+    const uint32_t sc = tile_step_cols(kind);
+    return (cols + sc - 1) / sc;
+}
+
+// Column (within the 128-group) of field u of byte j of dword a of a Q2 item.
+__host__ __device__ inline uint32_t mixed_q2_col(uint32_t a, uint32_t j, uint32_t u) {
+    return 32u * (a & 3u) + 8u * j + 2u * u + (a >> 2);
+}
+
+// Decoded weight (r, c) of a tiled organ, bit-exact with the reference
+// decoders: (nibble-8)*scale, +-scale, (code-1.5)*scale.
+__device__ inline float tiled_weight(const OrganView& o, uint32_t r, uint32_t c) {
+    const uint32_t T = r / TILE_ROWS, n = r % TILE_ROWS;
+    if (o.kind == HK_F32) return o.dense[(size_t)r * o.cols + c];
+    if (o.kind == HK_Q4) {
+        const uint32_t chunk = c >> 5, t = chunk >> 2, q = chunk & 3u, l = n + 16u * q, w = c & 31u;
+        const uint8_t b = o.data[((size_t)T * o.steps + t) * 1024u + 16u * l + (w >> 1)];
+        const int nib = (w & 1u) ? (b >> 4) : (b & 0xF);
+        const float s = f16_bits_to_f32(o.scales[((size_t)T * 64u + l) * o.steps + t]);
+        return (float)(nib - 8) * s;
+    }
+    const uint32_t g = c >> 7, t = g >> 2, q = g & 3u, l = n + 16u * q, i = c & 127u;
+    if (o.kind == HK_BIN) {
+        const uint8_t b = o.data[((size_t)T * o.steps + t) * 1024u + 16u * l + (i >> 3)];
+        const float s = f16_bits_to_f32(o.scales[((size_t)T * 64u + l) * o.steps + t]);
+        return ((b >> (i & 7u)) & 1u) ? s : -s;
+    }
+    const uint4 h = o.hdr[(size_t)T * o.steps + t];
+    const uint64_t mask = (uint64_t)h.x | ((uint64_t)h.y << 32);
+    const uint32_t below = __popcll(mask & ((1ull << l) - 1ull));
+    const uint8_t* item = o.data + h.z + 16u * (l + below);
+    const uint16_t* sc = o.scales + h.w + l + below;
+    if (!((mask >> l) & 1ull)) {
+        const float s = f16_bits_to_f32(sc[0]);
+        return ((item[i >> 3] >> (i & 7u)) & 1u) ? s : -s;
+    }
+    // invert mixed_q2_col: column i -> (a, j, u)
+    const uint32_t a = ((i >> 5) & 3u) | ((i & 1u) << 2), j = (i >> 3) & 3u, u = (i >> 1) & 3u;
+    const uint32_t code = (item[4u * a + j] >> (2u * u)) & 3u;
+    return ((float)code - 1.5f) * f16_bits_to_f32(sc[i >> 6]);
+}
+
+}  // namespace hk
