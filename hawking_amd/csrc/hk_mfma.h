@@ -1,0 +1,303 @@
+// hk_mfma.h -- the int8 matrix-core GEMV engine for packed organs (device).
+//
+// Batch-1 GEMV is bandwidth bound, but decoding 1-bit or 4-bit weights to
+// floats costs at least one VALU op per weight, more than the VALU can issue
+// at HBM speed for binary weights (8 weights per byte).  So the decode is
+// moved into v_mfma_i32_16x16x64_i8:
+//
+//   * x is converted once per workgroup to a fixed-point integer
+//     X = rint(x * 2^E) (|X| <= 2^23), and X * 2^k is split into four signed
+//     base-256 "limbs".  The MFMA A operand (16 x 64) holds, in row
+//     m = 4*slot + limb, the limbs of the columns that lane-group `slot` of the
+//     B operand covers (zero elsewhere), so one MFMA yields exact int32 partial
+//     sums for 4 column groups x 4 limbs of 16 weight rows.
+//   * The B operand (64 x 16) comes straight from the packed bytes with one AND
+//     per 4 weights: a binary bit plane s is bytes & (0x01 << s) = bit * 2^s, a
+//     Q4 nibble plane is bytes & 0x0F, a Q2 field is bytes & (0x03 << 2u); the
+//     power of two is folded into the A limbs (X * 2^(7-s) etc.).
+//   * Per (row, group) the four int32 limbs are combined in f32, the zero
+//     point is removed with the group's sum of X (binary: sum (2b-1) X =
+//     2 sum bX - sum X; Q4: sum (n-8) X; Q2: sum (c-1.5) X) and the f16 group
+//     scale is applied; y = 2^-E * sum over groups.
+//   * A tiles live in LDS in compact form: per tile 16 lanes x 16 B of limbs
+//     plus a 16-byte zero block (stride 272 B); a lane whose row slot differs
+//     from its column slot reads the zero block through a per-lane constant
+//     offset, so the operand fetch is one ds_read_b128 with no VALU work.  One
+//     A fetch feeds R row tiles.
+// Weights arrive in the tiled layout of hk_tile.h.  Numerics: the only
+// roundings are X (2^-24 of max|x|), the f32 limb combine and the f32
+// accumulation over groups; rel-L2 vs the serial f32 reference is ~1e-7.
+#pragma once
+
+#include "hk_internal.h"
+#include "hk_tile.h"
+
+namespace hk {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4i mfma_i8(const v4i& a, const v4i& b, const v4i& c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+template <int KIND>
+struct Kcfg;
+template <>
+struct Kcfg<HK_BIN> {
+    static constexpr int P = 8, STEP_COLS = 512, DATA = 16;
+};
+template <>
+struct Kcfg<HK_Q4> {
+    static constexpr int P = 2, STEP_COLS = 128, DATA = 16;
+};
+template <>
+struct Kcfg<HK_MIXED> {
+    static constexpr int P = 8, STEP_COLS = 512, DATA = 32;
+};
+
+constexpr int A_TILE_STRIDE = 272;  // 256 B of active-lane limbs + 16 B of zeros
+
+// LDS bytes needed by prepare_x for an organ with `steps` steps.
+template <int KIND>
+__host__ __device__ constexpr size_t x_lds_bytes(uint32_t steps) {
+    return (size_t)steps * Kcfg<KIND>::P * A_TILE_STRIDE + (size_t)steps * Kcfg<KIND>::STEP_COLS / 32 * 4;
+}
+
+__device__ __forceinline__ float combine_limbs(const v4i& c) {
+    return (float)c[0] + 256.0f * (float)c[1] + 65536.0f * (float)c[2] + 16777216.0f * (float)c[3];
+}
+
+__device__ __forceinline__ int32_t fixed_x(const float* __restrict__ x, uint32_t c, uint32_t cols, int E) {
+    return c < cols ? __float2int_rn(ldexpf(x[c], E)) : 0;
+}
+
+// Value Y of A byte i (0..15) for step t, MFMA mu, column slot q.
+template <int KIND>
+__device__ __forceinline__ int32_t a_value(const float* __restrict__ x, uint32_t cols, int E, int t, int mu, int q,
+                                           int i) {
+    if constexpr (KIND == HK_BIN) {
+        const int32_t v = fixed_x(x, (uint32_t)(t * 512 + q * 128 + 8 * i + mu), cols, E);
+        return mu < 7 ? (v << (7 - mu)) : -v;
+    } else if constexpr (KIND == HK_Q4) {
+        return fixed_x(x, (uint32_t)(t * 128 + q * 32 + 2 * i + mu), cols, E);
+    } else {
+        const int h = mu >> 2, u = mu & 3, r = i >> 2, j = i & 3;
+        const int a = r < 2 ? 2 * h + r : 2 * h + 2 + r;
+        const int32_t v =
+            fixed_x(x, (uint32_t)(t * 512 + q * 128) + mixed_q2_col((uint32_t)a, (uint32_t)j, (uint32_t)u), cols, E);
+        return v << (u < 3 ? 6 - 2 * u : 6);
+    }
+}
+
+__device__ __forceinline__ float block_max_abs(const float* __restrict__ x, uint32_t n, float* red) {
+    float m = 0.0f;
+    for (uint32_t c = threadIdx.x; c < n; c += blockDim.x) m = fmaxf(m, fabsf(x[c]));
+    m = wave_max(m);
+    const int nw = (int)(blockDim.x >> 6);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    float r = red[0];
+    for (int w = 1; w < nw; ++w) r = fmaxf(r, red[w]);
+    return r;
+}
+
+// All threads of the block: A tiles and per-32-column sums of X into `lds`
+// (x_lds_bytes<KIND>(steps) bytes).  Returns E; non-finite x sets E's flag.
+// Ends with __syncthreads().
+template <int KIND>
+__device__ int prepare_x(const float* __restrict__ x, uint32_t cols, uint32_t steps, uint8_t* lds, float* red,
+                         bool* nonfinite) {
+    constexpr int P = Kcfg<KIND>::P, SC = Kcfg<KIND>::STEP_COLS;
+    float m = block_max_abs(x, cols, red);
+    *nonfinite = !isfinite(m);
+    if (*nonfinite) m = 0.0f;
+    int e2 = 0;
+    if (m > 0.0f) (void)frexpf(m, &e2);
+    const int E = m > 0.0f ? 23 - e2 : 0;
+    const int ntau = (int)steps * P;
+    uint32_t* A = reinterpret_cast<uint32_t*>(lds);
+    float* SX = reinterpret_cast<float*>(lds + (size_t)ntau * A_TILE_STRIDE);
+    // zero blocks
+    for (int i = threadIdx.x; i < ntau * 4; i += blockDim.x) A[(i >> 2) * (A_TILE_STRIDE / 4) + 64 + (i & 3)] = 0u;
+    // unit = (tau, slot q, dword d): 4 A bytes -> 4 lanes' dwords via a byte transpose
+    for (int u = threadIdx.x; u < ntau * 16; u += blockDim.x) {
+        const int d = u & 3, q = (u >> 2) & 3, tau = u >> 4;
+        const int t = tau / P, mu = tau % P;
+        uint32_t z[4];
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb)
+            z[jb] = ((uint32_t)a_value<KIND>(x, cols, E, t, mu, q, 4 * d + jb) + 0x80808080u) ^ 0x80808080u;
+#pragma unroll
+        for (int L = 0; L < 4; ++L) {
+            // v_perm: selector 0..3 = byte of the second operand, 4..7 = byte of the first, 0x0c = 0
+            const uint32_t lo = __builtin_amdgcn_perm(z[1], z[0], 0x0c0c0400u | (uint32_t)L | ((uint32_t)L << 8));
+            const uint32_t hi = __builtin_amdgcn_perm(z[3], z[2], 0x04000c0cu | ((uint32_t)L << 16) | ((uint32_t)L << 24));
+            A[tau * (A_TILE_STRIDE / 4) + (4 * q + L) * 4 + d] = lo | hi;
+        }
+    }
+    // per-32-column sums: 8 columns per thread, 4 consecutive lanes per block
+    const uint32_t kcols = steps * (uint32_t)SC;
+    for (uint32_t c0 = threadIdx.x * 8u; c0 < kcols; c0 += blockDim.x * 8u) {
+        int32_t s = 0;
+#pragma unroll
+        for (uint32_t k = 0; k < 8; ++k) s += fixed_x(x, c0 + k, cols, E);
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        if ((threadIdx.x & 3u) == 0) SX[c0 / 32u] = (float)s;
+    }
+    __syncthreads();
+    return E;
+}
+
+// Per-lane byte offset of this lane's A operand inside a tile.
+__device__ __forceinline__ uint32_t a_lane_offset(int lane) {
+    return (((lane & 15) >> 2) == (lane >> 4)) ? (uint32_t)(lane & 15) * 16u : 256u;
+}
+
+__device__ __forceinline__ v4i lds_a(const uint8_t* lds, uint32_t tau, uint32_t off) {
+    return *reinterpret_cast<const v4i*>(lds + tau * A_TILE_STRIDE + off);
+}
+
+// One step of R row tiles, as fetched from memory: the weight bytes and scales
+// each lane needs (row lane%16 of tile T[r], column slot lane/16).
+template <int KIND, int R>
+struct Frag;
+template <int R>
+struct Frag<HK_BIN, R> {
+    uint4 v[R];
+    float s[R];
+};
+template <int R>
+struct Frag<HK_Q4, R> {
+    uint4 v[R];
+    float s[R];
+};
+template <int R>
+struct Frag<HK_MIXED, R> {
+    uint32_t V[R][8];
+    float s0[R], s1[R];
+    bool q2[R];
+};
+
+// Issue the loads of step t for tiles T[0..R-1] (tiles r >= nvalid alias T[0]).
+template <int KIND, int R>
+__device__ __forceinline__ void fetch_step(const OrganView& o, const uint32_t* T, int nvalid, uint32_t t, int lane,
+                                           Frag<KIND, R>& f) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t Tr = r < nvalid ? T[r] : T[0];
+        if constexpr (KIND == HK_BIN || KIND == HK_Q4) {
+            f.v[r] = *reinterpret_cast<const uint4*>(o.data + ((size_t)Tr * o.steps + t) * 1024u + 16u * lane);
+            f.s[r] = f16_bits_to_f32(o.scales[((size_t)Tr * 64u + lane) * o.steps + t]);
+        } else {
+            const uint4 h = o.hdr[(size_t)Tr * o.steps + t];
+            const uint32_t below = __builtin_amdgcn_mbcnt_hi(h.y, __builtin_amdgcn_mbcnt_lo(h.x, 0u));
+            const bool isq2 = ((lane < 32 ? (h.x >> lane) : (h.y >> (lane - 32))) & 1u) != 0;
+            const uint8_t* p = o.data + h.z + 16u * ((uint32_t)lane + below);
+            const uint4 va = *reinterpret_cast<const uint4*>(p);
+            const uint4 vb = *reinterpret_cast<const uint4*>(p + (isq2 ? 16 : 0));
+            f.V[r][0] = va.x;
+            f.V[r][1] = va.y;
+            f.V[r][2] = va.z;
+            f.V[r][3] = va.w;
+            f.V[r][4] = vb.x;
+            f.V[r][5] = vb.y;
+            f.V[r][6] = vb.z;
+            f.V[r][7] = vb.w;
+            const uint16_t* spp = o.scales + h.w + (uint32_t)lane + below;
+            f.s0[r] = f16_bits_to_f32(spp[0]);
+            f.s1[r] = f16_bits_to_f32(spp[isq2 ? 1 : 0]);
+            f.q2[r] = isq2;
+        }
+    }
+}
+
+// Consume one fetched step: acc[r] += this lane's partial dot, in units of
+// 2^-E.  Tiles r >= nvalid are computed on aliased data and discarded.
+template <int KIND, int R>
+__device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t, int nvalid, const uint8_t* lds,
+                                             uint32_t aoff, const float* SX, int q, float* acc) {
+    v4i c[R];
+    if constexpr (KIND == HK_BIN) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) c[r] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            const v4i a = lds_a(lds, t * 8 + p, aoff);
+            const uint32_t m = 0x01010101u << p;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const v4i b = {(int)(f.v[r].x & m), (int)(f.v[r].y & m), (int)(f.v[r].z & m), (int)(f.v[r].w & m)};
+                c[r] = mfma_i8(a, b, c[r]);
+            }
+        }
+        const float sx = (SX[16 * t + 4 * q] + SX[16 * t + 4 * q + 1]) + (SX[16 * t + 4 * q + 2] + SX[16 * t + 4 * q + 3]);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (r < nvalid) acc[r] += f.s[r] * (combine_limbs(c[r]) * (1.0f / 64.0f) - sx);
+    } else if constexpr (KIND == HK_Q4) {
+        const uint32_t m = 0x0F0F0F0Fu;
+        const v4i alo = lds_a(lds, t * 2, aoff), ahi = lds_a(lds, t * 2 + 1, aoff);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const v4i lo = {(int)(f.v[r].x & m), (int)(f.v[r].y & m), (int)(f.v[r].z & m), (int)(f.v[r].w & m)};
+            const v4i hi = {(int)((f.v[r].x >> 4) & m), (int)((f.v[r].y >> 4) & m), (int)((f.v[r].z >> 4) & m),
+                            (int)((f.v[r].w >> 4) & m)};
+            c[r] = mfma_i8(alo, lo, v4i{0, 0, 0, 0});
+            c[r] = mfma_i8(ahi, hi, c[r]);
+        }
+        const float sx = SX[4 * t + q];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (r < nvalid) acc[r] += f.s[r] * (combine_limbs(c[r]) - 8.0f * sx);
+    } else {
+        uint32_t V[R][8];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t sh = f.q2[r] ? 0u : 1u;  // binary: odd columns are the signs >> 1
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                V[r][k] = f.V[r][k];
+                V[r][k + 4] = f.V[r][k + 4] >> sh;
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) c[r] = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const v4i a = lds_a(lds, t * 8 + h * 4 + u, aoff);
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const uint32_t bm = f.q2[r] ? 0x03030303u : 0x01010101u;
+                    v4i b;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const int ai = k < 2 ? 2 * h + k : 2 * h + 2 + k;
+                        b[k] = (int)(u < 3 ? (V[r][ai] & (bm << (2 * u))) : ((V[r][ai] >> 6) & bm));
+                    }
+                    c[r] = mfma_i8(a, b, c[r]);
+                }
+            }
+            const float sx = SX[16 * t + 4 * q + 2 * h] + SX[16 * t + 4 * q + 2 * h + 1];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                if (r >= nvalid) continue;
+                const float alpha = f.q2[r] ? (1.0f / 64.0f) : (2.0f / 64.0f);
+                const float beta = f.q2[r] ? 1.5f : 1.0f;
+                acc[r] += (h ? f.s1[r] : f.s0[r]) * (combine_limbs(c[r]) * alpha - beta * sx);
+            }
+        }
+    }
+}
+
+// Sum the four column-slot partials of a tile: every lane gets its row's total.
+__device__ __forceinline__ float tile_row_sum(float v) {
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+}  // namespace hk
