@@ -189,6 +189,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--moe-layers", type=int, default=48)
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="run one device-to-device copy of this size first (PMC byte-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
@@ -199,6 +201,14 @@ def main():
     ctx = Context(0)
     info = ctx.device_info()
     log("device", info)
+    if args.calib_copy_mb:
+        nb = args.calib_copy_mb << 20
+        src, dst = ctx.empty(nb, np.uint8), ctx.empty(nb, np.uint8)
+        ctx.call("hk_memset", src.ptr, 1, nb, ctx.stream)
+        ctx.call("hk_memcpy_dtod", dst.ptr, src.ptr, nb, ctx.stream)
+        ctx.synchronize()
+        log("calibration copy bytes", nb)
+        del src, dst
 
     main_name = "binary_512x2048"
     log("headline", main_name)

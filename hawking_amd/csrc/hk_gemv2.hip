@@ -34,7 +34,9 @@ __device__ __forceinline__ void store_group(const float* acc, const uint32_t* T,
     }
 }
 
-template <int KIND, int R>
+// D-deep software pipeline: D fetched steps are in flight while one is
+// consumed; slot d of the rotating buffer holds item it+d.
+template <int KIND, int R, int D>
 __global__ void __launch_bounds__(256)
 gemv_tiled_kernel(const OrganView* __restrict__ organs, const float* __restrict__ xall, size_t x_stride,
                   float* __restrict__ yall, size_t y_stride, uint32_t tiles_per_wg, uint32_t* status) {
@@ -49,13 +51,16 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, const float* __restrict_
     WaveItems W{t0 + wave * R, 4u * R, t1, o.steps, 0};
     W.n = W.g0 < t1 ? ((t1 - W.g0 + W.gstride - 1) / W.gstride) * o.steps : 0;
 
-    // first weight loads go out before the x preparation
-    Frag<KIND, R> fa, fb;
-    uint32_t Ta[R], Tb[R], ta = 0, tb = 0;
-    int na = 0, nb = 0;
-    if (W.n) {
-        W.at(0, Ta, R, &na, &ta);
-        fetch_step<KIND, R>(o, Ta, na, ta, lane, fa);
+    // the first D steps' weight loads go out before the x preparation
+    Frag<KIND, R> f[D];
+    uint32_t T[D][R], ts[D];
+    int nv[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        if ((uint32_t)d < W.n) {
+            W.at((uint32_t)d, T[d], R, &nv[d], &ts[d]);
+            fetch_step<KIND, R>(o, T[d], nv[d], ts[d], lane, f[d]);
+        }
     }
     bool bad = false;
     const int E = prepare_x<KIND>(x, o.cols, o.steps, lds, red, &bad);
@@ -66,27 +71,21 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, const float* __restrict_
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-    for (uint32_t it = 0; it < W.n; it += 2) {
-        if (it + 1 < W.n) {
-            W.at(it + 1, Tb, R, &nb, &tb);
-            fetch_step<KIND, R>(o, Tb, nb, tb, lane, fb);
-        }
-        compute_step<KIND, R>(fa, ta, na, lds, aoff, SX, q, acc);
-        if (ta + 1 == o.steps) {
-            store_group<R>(acc, Ta, na, o.rows, E, lane, y);
+    for (uint32_t it = 0; it < W.n; it += D) {
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-        }
-        if (it + 1 >= W.n) break;
-        if (it + 2 < W.n) {
-            W.at(it + 2, Ta, R, &na, &ta);
-            fetch_step<KIND, R>(o, Ta, na, ta, lane, fa);
-        }
-        compute_step<KIND, R>(fb, tb, nb, lds, aoff, SX, q, acc);
-        if (tb + 1 == o.steps) {
-            store_group<R>(acc, Tb, nb, o.rows, E, lane, y);
+        for (int d = 0; d < D; ++d) {
+            if (it + d >= W.n) break;
+            compute_step<KIND, R>(f[d], ts[d], nv[d], lds, aoff, SX, q, acc);
+            if (ts[d] + 1 == o.steps) {
+                store_group<R>(acc, T[d], nv[d], o.rows, E, lane, y);
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+                for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+            }
+            const uint32_t nx = it + D + d;
+            if (nx < W.n) {
+                W.at(nx, T[d], R, &nv[d], &ts[d]);
+                fetch_step<KIND, R>(o, T[d], nv[d], ts[d], lane, f[d]);
+            }
         }
     }
 }
@@ -110,12 +109,13 @@ __global__ void __launch_bounds__(256) gemv_f32_kernel(const OrganView* __restri
     if (lane == 0) yall[(size_t)blockIdx.y * y_stride + row] = acc;
 }
 
-template <int KIND, int R>
+template <int KIND, int R, int D>
 static hipError_t launch_kind(const OrganView* organs, uint32_t n, const OrganView& sh, const float* x,
                               size_t xs, float* y, size_t ys, uint32_t tpw, hipStream_t s) {
     const dim3 grid((sh.n_tiles + tpw - 1) / tpw, n);
     const size_t lds = x_lds_bytes<KIND>(sh.steps);
-    hipLaunchKernelGGL((gemv_tiled_kernel<KIND, R>), grid, dim3(256), lds, s, organs, x, xs, y, ys, tpw, nullptr);
+    hipLaunchKernelGGL((gemv_tiled_kernel<KIND, R, D>), grid, dim3(256), lds, s, organs, x, xs, y, ys, tpw,
+                       nullptr);
     return hipGetLastError();
 }
 
@@ -123,10 +123,11 @@ template <int KIND>
 static hipError_t launch_r(const OrganView* organs, uint32_t n, const OrganView& sh, const float* x, size_t xs,
                            float* y, size_t ys, hipStream_t s) {
     const uint64_t tiles = (uint64_t)n * sh.n_tiles;
-    if (tiles >= 16384) return launch_kind<KIND, 4>(organs, n, sh, x, xs, y, ys, 32, s);
-    if (tiles >= 4096) return launch_kind<KIND, 2>(organs, n, sh, x, xs, y, ys, 8, s);
+    constexpr int DB = KIND == HK_MIXED ? 3 : 4;
+    if (tiles >= 16384) return launch_kind<KIND, 2, DB>(organs, n, sh, x, xs, y, ys, 32, s);
+    if (tiles >= 4096) return launch_kind<KIND, 2, 2>(organs, n, sh, x, xs, y, ys, 8, s);
     const uint32_t tpw = (uint64_t)n * ((sh.n_tiles + 3) / 4) >= 256 ? 4 : 1;
-    return launch_kind<KIND, 1>(organs, n, sh, x, xs, y, ys, tpw, s);
+    return launch_kind<KIND, 1, 2>(organs, n, sh, x, xs, y, ys, tpw, s);
 }
 
 hipError_t launch_gemv_tiled(const OrganView* organs_dev, uint32_t n, const OrganView& sh, const float* x,
