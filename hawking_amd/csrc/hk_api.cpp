@@ -16,6 +16,7 @@
 #include "hk_moe.h"
 #include "hk_router.h"
 #include "hk_synth.h"
+#include "hk_tile.h"
 
 using hk::CanonView;
 
@@ -719,7 +720,7 @@ extern "C" int hk_router_softmax_topk(hk_ctx* ctx, const float* logits, uint32_t
     if (!logits || !ids || !weights) return set_error(ctx, HK_E_INVALID_ARG, "router: NULL pointer");
     if (n_tokens == 0 || n_experts == 0 || top_k == 0 || top_k > n_experts)
         return set_error(ctx, HK_E_INVALID_ARG, "router: need 0 < top_k <= n_experts and n_tokens > 0");
-    if (n_experts > 16384) return set_error(ctx, HK_E_UNSUPPORTED, "router: n_experts above 16384");
+    if (n_experts > 8192 || top_k > 64) return set_error(ctx, HK_E_UNSUPPORTED, "router: n_experts above 8192 or top_k above 64");
     if (!(tie_eps >= 0.0f) || !std::isfinite(tie_eps)) return set_error(ctx, HK_E_INVALID_ARG, "router: tie_eps must be finite and >= 0");
     return check_hip(ctx,
                      launch_softmax_topk(logits, n_tokens, n_experts, top_k, tie_eps, renorm, ids, weights,
@@ -736,7 +737,7 @@ extern "C" int hk_router_noaux_tc(hk_ctx* ctx, const float* logits, const float*
     if (n_tokens == 0 || n_group == 0 || n_experts % n_group || topk_group == 0 || topk_group > n_group ||
         top_k == 0 || top_k > (n_experts / n_group) * topk_group)
         return set_error(ctx, HK_E_INVALID_ARG, "noaux_tc: inconsistent group / top-k geometry");
-    if (n_experts > 8192) return set_error(ctx, HK_E_UNSUPPORTED, "noaux_tc: n_experts above 8192");
+    if (n_experts > 8192 || top_k > 64) return set_error(ctx, HK_E_UNSUPPORTED, "noaux_tc: n_experts above 8192 or top_k above 64");
     return check_hip(ctx,
                      launch_noaux_tc(logits, bias, n_tokens, n_experts, n_group, topk_group, top_k, norm_topk_prob,
                                      routed_scaling_factor, ids, weights, static_cast<hipStream_t>(stream)),
@@ -744,18 +745,23 @@ extern "C" int hk_router_noaux_tc(hk_ctx* ctx, const float* logits, const float*
 }
 
 // ====================================================================== MoE model
+// Expert organs are staged in the canonical layout (host upload or device
+// generation) and repacked per layer into one slab of tiled organs; a device
+// table of their views is indexed on the device by the route ids.
 
 namespace {
 
 constexpr uint32_t PROJ_NORM = 16, PROJ_ROUTER = 17, PROJ_SHARED_GATE = 18, PROJ_COIN = 32;
 constexpr float SIGMA_W = 0.02f, SIGMA_NORM = 0.02f;
+constexpr size_t MOE_LDS_LIMIT = 64 * 1024;
+constexpr uint32_t MOE_MAX_SLOTS = 16;
 
 struct MoeLayerHost {
     void* slab = nullptr;
     size_t slab_bytes = 0;
-    std::vector<CanonView> table;      // (E+1)*3
-    std::vector<size_t> packed;        // per organ, algorithmic bytes
-    CanonView* table_dev = nullptr;
+    std::vector<OrganView> table;  // (E+1)*3
+    std::vector<size_t> packed;    // per organ, algorithmic bytes
+    OrganView* table_dev = nullptr;
     float* norm_w = nullptr;
     float* router_w = nullptr;
     float* gate_w = nullptr;
@@ -802,8 +808,10 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
         return set_error(ctx, HK_E_INVALID_ARG, "moe config: zero dimension or top_k > n_experts");
     if (c.expert_kind != HK_Q4 && c.expert_kind != HK_MIXED)
         return set_error(ctx, HK_E_UNSUPPORTED, "moe config: expert_kind must be HK_Q4 or HK_MIXED");
-    if (c.top_k > 64 || c.n_experts > 4096 || c.hidden > 8192 || c.hidden % 128)
-        return set_error(ctx, HK_E_UNSUPPORTED, "moe config: need top_k <= 64, n_experts <= 4096, hidden % 128 == 0, hidden <= 8192");
+    const uint32_t slots = c.top_k + (c.shared_inter ? 1u : 0u);
+    if (slots > MOE_MAX_SLOTS || c.n_experts > 4096 || c.hidden > 8192 || c.hidden % 128)
+        return set_error(ctx, HK_E_UNSUPPORTED,
+                         "moe config: need top_k (+1 shared) <= 16, n_experts <= 4096, hidden % 128 == 0, hidden <= 8192");
     const int grp = c.expert_kind == HK_MIXED ? 128 : c.expert_group;
     int rc = validate_shape(ctx, c.expert_kind, grp, c.inter, c.hidden);
     if (!rc) rc = validate_shape(ctx, c.expert_kind, grp, c.hidden, c.inter);
@@ -811,17 +819,20 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
     if (rc) return rc;
     if (!(c.eps > 0.0f) || !std::isfinite(c.eps)) return set_error(ctx, HK_E_INVALID_ARG, "moe config: eps must be positive");
     const uint32_t imax = std::max(c.inter, c.shared_inter);
-    if ((size_t)(c.top_k + 1) * imax * 4 > 64 * 1024)
-        return set_error(ctx, HK_E_UNSUPPORTED, "moe config: (top_k+1)*intermediate activations exceed 64 KiB of LDS");
+    if (moe_gate_up_lds_bytes(c.expert_kind, c.hidden) > MOE_LDS_LIMIT ||
+        moe_down_lds_bytes(c.expert_kind, imax, slots) > MOE_LDS_LIMIT)
+        return set_error(ctx, HK_E_UNSUPPORTED, "moe config: x images of hidden / intermediate exceed 64 KiB of LDS");
     hk_moe_model* m = new hk_moe_model();
     m->cfg = c;
     m->cfg.expert_group = grp;
     m->dims = hk::MoeDims{c.hidden, c.inter, c.shared_inter, imax, c.n_experts, c.top_k, c.shared_inter ? 1 : 0, c.eps};
     m->layers.resize(c.n_layers);
     const size_t dpl = dense_per_layer(c);
-    const size_t tab = align256((size_t)(c.n_experts + 1) * 3 * sizeof(CanonView));
-    const size_t ws = align256((size_t)c.hidden * 4) + align256(((size_t)c.n_experts + 4) * 4) + 256 + 256 + 256 +
-                      align256((size_t)(c.top_k + 1) * imax * 4) + 2 * align256((size_t)c.hidden * 4);
+    const size_t tab = align256((size_t)(c.n_experts + 1) * 3 * sizeof(OrganView));
+    const size_t img = align256(moe_img_bytes(c.expert_kind, c.hidden));
+    const size_t sel = align256((size_t)slots * 3 * sizeof(OrganView));
+    const size_t ws = align256(((size_t)c.n_experts + 4) * 4) + 4 * 256 + align256((size_t)slots * imax * 4) + img + 256 +
+                      sel + 2 * align256((size_t)c.hidden * 4);
     if (hipMalloc(&m->dense, dpl * c.n_layers) != hipSuccess || hipMalloc(&m->tables, tab * c.n_layers) != hipSuccess ||
         hipMalloc(&m->ws_mem, ws) != hipSuccess) {
         if (m->dense) (void)hipFree(m->dense);
@@ -830,20 +841,25 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
         delete m;
         return set_error(ctx, HK_E_NOMEM, "moe model allocation failed");
     }
-    (void)hipMemset(m->ws_mem, 0, ws);
+    // zero tables (layers without weights select nothing) and the workspace
+    if (hipMemset(m->tables, 0, tab * c.n_layers) != hipSuccess || hipMemset(m->ws_mem, 0, ws) != hipSuccess) {
+        (void)hipFree(m->dense);
+        (void)hipFree(m->tables);
+        (void)hipFree(m->ws_mem);
+        delete m;
+        return set_error(ctx, HK_E_HIP, "moe model initialisation failed");
+    }
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         uint8_t* d = static_cast<uint8_t*>(m->dense) + l * dpl;
         MoeLayerHost& L = m->layers[l];
         L.norm_w = reinterpret_cast<float*>(d);
         L.router_w = reinterpret_cast<float*>(d + align256((size_t)c.hidden * 4));
         L.gate_w = reinterpret_cast<float*>(d + align256((size_t)c.hidden * 4) + align256((size_t)c.n_experts * c.hidden * 4));
-        L.table_dev = reinterpret_cast<CanonView*>(static_cast<uint8_t*>(m->tables) + l * tab);
-        L.table.assign((size_t)(c.n_experts + 1) * 3, CanonView{});
+        L.table_dev = reinterpret_cast<OrganView*>(static_cast<uint8_t*>(m->tables) + l * tab);
+        L.table.assign((size_t)(c.n_experts + 1) * 3, OrganView{});
         L.packed.assign((size_t)(c.n_experts + 1) * 3, 0);
     }
     uint8_t* w = static_cast<uint8_t*>(m->ws_mem);
-    m->ws.xn = reinterpret_cast<float*>(w);
-    w += align256((size_t)c.hidden * 4);
     m->ws.logits = reinterpret_cast<float*>(w);
     w += align256(((size_t)c.n_experts + 4) * 4);
     m->ws.ids = reinterpret_cast<int32_t*>(w);
@@ -852,8 +868,15 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
     w += 256;
     m->ws.gate = reinterpret_cast<float*>(w);
     w += 256;
+    m->ws.img_e = reinterpret_cast<int32_t*>(w);
+    w += 256;
     m->ws.act = reinterpret_cast<float*>(w);
-    w += align256((size_t)(c.top_k + 1) * imax * 4);
+    w += align256((size_t)slots * imax * 4);
+    m->ws.img = w;
+    w += img;
+    w += 256;
+    m->ws.sel = reinterpret_cast<OrganView*>(w);
+    w += sel;
     m->hbuf[0] = reinterpret_cast<float*>(w);
     w += align256((size_t)c.hidden * 4);
     m->hbuf[1] = reinterpret_cast<float*>(w);
@@ -875,12 +898,57 @@ extern "C" int hk_moe_model_free(hk_ctx* ctx, hk_moe_model* m) {
     return HK_OK;
 }
 
-static int upload_table(hk_ctx* ctx, MoeLayerHost& L, hipStream_t st) {
-    int rc = check_hip(ctx,
-                       hipMemcpyAsync(L.table_dev, L.table.data(), L.table.size() * sizeof(CanonView),
-                                      hipMemcpyHostToDevice, st),
-                       "expert table upload");
-    if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "hipStreamSynchronize (expert table)");
+// Repacks one layer's staged canonical organs (canon[i], mixed binary-group
+// counts nbin[i]) into a fresh slab of tiled organs and uploads the layer's
+// device table.  Synchronises `st`.
+static int repack_layer(hk_ctx* ctx, MoeLayerHost& L, const std::vector<CanonView>& canon,
+                        const std::vector<uint32_t>& nbin, hipStream_t st) {
+    const size_t n_org = canon.size();
+    const int kind = canon[0].kind;
+    std::vector<size_t> bytes(n_org);
+    std::vector<uint32_t> nq2(n_org, 0);
+    size_t total = 0, words = 0, max_items = 0;
+    for (size_t i = 0; i < n_org; ++i) {
+        const CanonView& v = canon[i];
+        const uint32_t nb = kind == HK_MIXED ? nbin[i] : 0;
+        if (kind == HK_MIXED) nq2[i] = (uint32_t)((size_t)v.rows * v.cols / 128) - nb;
+        bytes[i] = tiled_bytes(kind, v.group, v.rows, v.cols, nb, nq2[i], &L.packed[i]);
+        total += bytes[i];
+        const size_t blocks = (size_t)n_tiles_for(v.rows) * n_steps_for(kind, v.cols);
+        words += blocks;
+        max_items = std::max(max_items, blocks * 64);
+    }
+    if (L.slab) {
+        (void)hipStreamSynchronize(st);
+        (void)hipFree(L.slab);
+        L.slab = nullptr;
+        L.slab_bytes = 0;
+    }
+    L.ready = false;
+    if (hipMalloc(&L.slab, total) != hipSuccess) return set_error(ctx, HK_E_NOMEM, "expert slab allocation failed");
+    L.slab_bytes = total;
+    void* aux = nullptr;
+    const size_t jobs_bytes = align256(n_org * sizeof(RepackJob));
+    if (hipMalloc(&aux, jobs_bytes + words * 4 + 256) != hipSuccess) return set_error(ctx, HK_E_NOMEM, "repack job allocation failed");
+    std::vector<RepackJob> jobs(n_org);
+    uint8_t* p = static_cast<uint8_t*>(L.slab);
+    uint32_t* counts = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(aux) + jobs_bytes);
+    for (size_t i = 0; i < n_org; ++i) {
+        const CanonView& v = canon[i];
+        L.table[i] = tiled_place(kind, v.group, v.rows, v.cols, kind == HK_MIXED ? nbin[i] : 0, nq2[i], p);
+        jobs[i] = RepackJob{v, L.table[i], counts};
+        counts += (size_t)L.table[i].n_tiles * L.table[i].steps;
+        p += bytes[i];
+    }
+    int rc = check_hip(ctx, hipMemcpyAsync(aux, jobs.data(), n_org * sizeof(RepackJob), hipMemcpyHostToDevice, st),
+                       "repack job upload");
+    if (!rc) rc = check_hip(ctx, launch_repack_batch(kind, static_cast<RepackJob*>(aux), (uint32_t)n_org, max_items, st),
+                            "expert repack");
+    if (!rc) rc = check_hip(ctx, hipMemcpyAsync(L.table_dev, L.table.data(), L.table.size() * sizeof(OrganView),
+                                                hipMemcpyHostToDevice, st),
+                            "expert table upload");
+    if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "hipStreamSynchronize (expert repack)");
+    (void)hipFree(aux);
     return rc;
 }
 
@@ -912,29 +980,29 @@ extern "C" int hk_moe_model_set_layer(hk_ctx* ctx, hk_moe_model* m, uint32_t lay
     }
     MoeLayerHost& L = m->layers[layer];
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (L.slab) {
-        (void)hipStreamSynchronize(st);
-        (void)hipFree(L.slab);
-        L.slab = nullptr;
-        L.ready = false;
-    }
-    if (hipMalloc(&L.slab, total) != hipSuccess) return set_error(ctx, HK_E_NOMEM, "expert slab allocation failed");
-    L.slab_bytes = total;
+    void* stage = nullptr;
+    if (hipMalloc(&stage, total) != hipSuccess) return set_error(ctx, HK_E_NOMEM, "expert staging allocation failed");
     std::vector<std::vector<uint32_t>> keep;
-    uint8_t* p = static_cast<uint8_t*>(L.slab);
-    for (uint32_t i = 0; i < n_org; ++i) {
-        int rc = copy_src(ctx, srcs[i], lay[i], p, &L.table[i], st, &keep);
-        if (rc) return rc;
-        L.packed[i] = lay[i].packed();
+    std::vector<CanonView> canon(n_org);
+    std::vector<uint32_t> nbin(n_org, 0);
+    uint8_t* p = static_cast<uint8_t*>(stage);
+    int rc = HK_OK;
+    for (uint32_t i = 0; i < n_org && !rc; ++i) {
+        rc = copy_src(ctx, srcs[i], lay[i], p, &canon[i], st, &keep);
+        nbin[i] = srcs[i]->n_bin;
         p += lay[i].total();
     }
-    int rc = check_hip(ctx, hipMemcpyAsync(L.norm_w, src->norm_w, (size_t)c.hidden * 4, hipMemcpyHostToDevice, st), "norm upload");
+    if (!rc) rc = repack_layer(ctx, L, canon, nbin, st);
+    (void)hipStreamSynchronize(st);
+    (void)hipFree(stage);
+    if (rc) return rc;
+    rc = check_hip(ctx, hipMemcpyAsync(L.norm_w, src->norm_w, (size_t)c.hidden * 4, hipMemcpyHostToDevice, st), "norm upload");
     if (!rc) rc = check_hip(ctx, hipMemcpyAsync(L.router_w, src->router_w, (size_t)c.n_experts * c.hidden * 4,
                                                 hipMemcpyHostToDevice, st), "router upload");
     if (!rc && src->shared_gate_w)
         rc = check_hip(ctx, hipMemcpyAsync(L.gate_w, src->shared_gate_w, (size_t)c.hidden * 4, hipMemcpyHostToDevice, st),
                        "gate upload");
-    if (!rc) rc = upload_table(ctx, L, st);
+    if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "hipStreamSynchronize (layer upload)");
     if (rc) return rc;
     L.ready = true;
     return HK_OK;
@@ -958,7 +1026,9 @@ extern "C" int hk_moe_model_fill_synthetic(hk_ctx* ctx, hk_moe_model* m, uint64_
     int rc = check_hip(ctx, hipMemsetAsync(bad, 0, 4, st), "memset");
     std::vector<SynthJob> jobs(n_org);
     std::vector<uint32_t> nbin(n_org, 0);
-    size_t max_groups = 0;
+    std::vector<CanonView> canon(n_org);
+    void* stage = nullptr;
+    size_t stage_bytes = 0;
     for (uint32_t l = 0; l < c.n_layers && !rc; ++l) {
         MoeLayerHost& L = m->layers[l];
         // dense tensors
@@ -980,7 +1050,7 @@ extern "C" int hk_moe_model_fill_synthetic(hk_ctx* ctx, hk_moe_model* m, uint64_
         if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "sync");
         if (rc) break;
         // expert organs: keys and shapes
-        max_groups = 0;
+        size_t max_groups = 0;
         for (uint32_t i = 0; i < n_org; ++i) {
             const uint32_t e = i / 3, p = i % 3;
             uint32_t rows, cols;
@@ -1004,6 +1074,7 @@ extern "C" int hk_moe_model_fill_synthetic(hk_ctx* ctx, hk_moe_model* m, uint64_
             if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "sync");
             if (rc) break;
         }
+        // canonical staging for this layer
         std::vector<Layout> lay(n_org);
         size_t total = 0;
         for (uint32_t i = 0; i < n_org; ++i) {
@@ -1013,17 +1084,17 @@ extern "C" int hk_moe_model_fill_synthetic(hk_ctx* ctx, hk_moe_model* m, uint64_
                                 c.expert_kind == HK_MIXED ? groups - nbin[i] : 0);
             total += lay[i].total();
         }
-        if (L.slab) {
-            (void)hipStreamSynchronize(st);
-            (void)hipFree(L.slab);
-            L.slab = nullptr;
+        if (total > stage_bytes) {
+            if (stage) (void)hipFree(stage);
+            stage = nullptr;
+            stage_bytes = 0;
+            if (hipMalloc(&stage, total) != hipSuccess) {
+                rc = set_error(ctx, HK_E_NOMEM, "expert staging allocation failed (layer " + std::to_string(l) + ")");
+                break;
+            }
+            stage_bytes = total;
         }
-        if (hipMalloc(&L.slab, total) != hipSuccess) {
-            rc = set_error(ctx, HK_E_NOMEM, "expert slab allocation failed (layer " + std::to_string(l) + ")");
-            break;
-        }
-        L.slab_bytes = total;
-        uint8_t* p = static_cast<uint8_t*>(L.slab);
+        uint8_t* p = static_cast<uint8_t*>(stage);
         for (uint32_t i = 0; i < n_org; ++i) {
             SynthJob& j = jobs[i];
             CanonView v = place(c.expert_kind, c.expert_group, j.rows, j.cols, lay[i], p);
@@ -1034,19 +1105,20 @@ extern "C" int hk_moe_model_fill_synthetic(hk_ctx* ctx, hk_moe_model* m, uint64_
             j.q2_codes = const_cast<uint8_t*>(v.q2_codes);
             j.row_bin = const_cast<uint32_t*>(v.row_bin);
             j.row_q2 = const_cast<uint32_t*>(v.row_q2);
-            L.table[i] = v;
-            L.packed[i] = lay[i].packed();
+            canon[i] = v;
             p += lay[i].total();
         }
         rc = check_hip(ctx, hipMemcpyAsync(jobs_dev, jobs.data(), n_org * sizeof(SynthJob), hipMemcpyHostToDevice, st), "job upload");
         if (!rc) rc = check_hip(ctx, launch_synth_jobs(c.expert_kind, static_cast<SynthJob*>(jobs_dev), n_org, max_groups, bad, st),
                                 "expert synth");
-        if (!rc) rc = upload_table(ctx, L, st);
+        if (!rc) rc = repack_layer(ctx, L, canon, nbin, st);
         if (!rc) L.ready = true;
     }
     uint32_t badv = 0;
     if (!rc) rc = check_hip(ctx, hipMemcpyAsync(&badv, bad, 4, hipMemcpyDeviceToHost, st), "flag read");
     if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "sync");
+    (void)hipStreamSynchronize(st);
+    if (stage) (void)hipFree(stage);
     (void)hipFree(jobs_dev);
     (void)hipFree(aux);
     if (!rc && badv) rc = set_error(ctx, HK_E_NONFINITE, "synthetic pack produced a non-finite scale");
@@ -1085,36 +1157,34 @@ extern "C" int hk_moe_decode_layer(hk_ctx* ctx, hk_moe_model* m, uint32_t layer,
                                    int32_t* ids, float* weights, hk_stream stream) {
     if (!ctx || !m) return HK_E_INVALID_ARG;
     if (!h_in || !h_out || h_in == h_out) return set_error(ctx, HK_E_INVALID_ARG, "moe layer: h_in/h_out NULL or aliased");
+    if (!aligned16(h_in) || !aligned16(h_out)) return set_error(ctx, HK_E_INVALID_ARG, "moe layer: h_in/h_out must be 16-byte aligned");
     MoeLayerDev L;
     int rc = moe_layer_dev(ctx, m, layer, &L);
     if (rc) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    rc = check_hip(ctx, launch_moe_layer(m->cfg.expert_kind, m->dims, L, h_in, h_out, m->ws, st), "moe layer launch");
-    if (rc) return rc;
-    const size_t kb = (size_t)m->cfg.top_k * 4;
-    if (ids) rc = check_hip(ctx, hipMemcpyAsync(ids, m->ws.ids, kb, hipMemcpyDeviceToDevice, st), "ids copy");
-    if (!rc && weights) rc = check_hip(ctx, hipMemcpyAsync(weights, m->ws.weights, kb, hipMemcpyDeviceToDevice, st), "weights copy");
-    return rc;
+    return check_hip(ctx, launch_moe_layer(m->cfg.expert_kind, m->dims, L, h_in, h_out, m->ws, ids, weights, st),
+                     "moe layer launch");
 }
 
 extern "C" int hk_moe_decode_stack(hk_ctx* ctx, hk_moe_model* m, const float* h_in, float* h_out, int32_t* ids,
                                    float* weights, hk_stream stream) {
     if (!ctx || !m) return HK_E_INVALID_ARG;
     if (!h_in || !h_out) return set_error(ctx, HK_E_INVALID_ARG, "moe stack: NULL h_in/h_out");
+    if (!aligned16(h_in) || !aligned16(h_out)) return set_error(ctx, HK_E_INVALID_ARG, "moe stack: h_in/h_out must be 16-byte aligned");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const uint32_t n = m->cfg.n_layers;
-    const size_t kb = (size_t)m->cfg.top_k * 4;
+    const uint32_t n = m->cfg.n_layers, K = m->cfg.top_k;
+    for (uint32_t l = 0; l < n; ++l)
+        if (!m->layers[l].ready) return set_error(ctx, HK_E_INVALID_ARG, "layer " + std::to_string(l) + " has no weights");
     const float* cur = h_in;
     for (uint32_t l = 0; l < n; ++l) {
         MoeLayerDev L;
         int rc = moe_layer_dev(ctx, m, l, &L);
         if (rc) return rc;
         float* dst = (l == n - 1) ? h_out : m->hbuf[l & 1];
-        rc = check_hip(ctx, launch_moe_layer(m->cfg.expert_kind, m->dims, L, cur, dst, m->ws, st), "moe layer launch");
-        if (!rc && ids) rc = check_hip(ctx, hipMemcpyAsync(ids + (size_t)l * m->cfg.top_k, m->ws.ids, kb, hipMemcpyDeviceToDevice, st), "ids copy");
-        if (!rc && weights)
-            rc = check_hip(ctx, hipMemcpyAsync(weights + (size_t)l * m->cfg.top_k, m->ws.weights, kb, hipMemcpyDeviceToDevice, st),
-                           "weights copy");
+        rc = check_hip(ctx,
+                       launch_moe_layer(m->cfg.expert_kind, m->dims, L, cur, dst, m->ws, ids ? ids + (size_t)l * K : nullptr,
+                                        weights ? weights + (size_t)l * K : nullptr, st),
+                       "moe layer launch");
         if (rc) return rc;
         cur = dst;
     }

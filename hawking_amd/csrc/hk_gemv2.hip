@@ -63,9 +63,9 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, const float* __restrict_
         }
     }
     bool bad = false;
-    const int E = prepare_x<KIND>(x, o.cols, o.steps, lds, red, &bad);
+    const int E = prepare_x<KIND>(BlockTeam{}, x, o.cols, o.steps, lds, red, &bad);
     if (bad && threadIdx.x == 0 && status) atomicOr(status, 1u);
-    const uint32_t aoff = a_lane_offset(lane);
+    const ImageA A{lds, a_lane_offset(lane)};
     const float* SX = reinterpret_cast<const float*>(lds + (size_t)o.steps * Kcfg<KIND>::P * A_TILE_STRIDE);
 
     float acc[R];
@@ -75,7 +75,7 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, const float* __restrict_
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             if (it + d >= W.n) break;
-            compute_step<KIND, R>(f[d], ts[d], nv[d], lds, aoff, SX, q, acc);
+            compute_step<KIND, R>(f[d], ts[d], nv[d], A, SX, q, acc);
             if (ts[d] + 1 == o.steps) {
                 store_group<R>(acc, T[d], nv[d], o.rows, E, lane, y);
 #pragma unroll

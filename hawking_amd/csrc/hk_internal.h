@@ -70,17 +70,45 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
 }
 
+// Wave-wide reductions on the DPP network (VALU lane moves, no LDS round
+// trips): an inclusive scan within each 16-lane row (row_shr 1, 2, 4, 8),
+// then row_bcast:15 / row_bcast:31 fold the rows into lane 63, which is
+// broadcast.  Lanes whose DPP source is outside the row keep the identity.
+// All 64 lanes must be active.
+constexpr int DPP_ROW_SHR1 = 0x111, DPP_ROW_SHR2 = 0x112, DPP_ROW_SHR4 = 0x114, DPP_ROW_SHR8 = 0x118;
+constexpr int DPP_ROW_BCAST15 = 0x142, DPP_ROW_BCAST31 = 0x143;
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_i32(int identity, int v) {
+    return __builtin_amdgcn_update_dpp(identity, v, CTRL, ROW_MASK, 0xF, false);
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f32(float identity, float v) {
+    return __builtin_bit_cast(float, dpp_i32<CTRL, ROW_MASK>(__builtin_bit_cast(int, identity), __builtin_bit_cast(int, v)));
+}
+__device__ __forceinline__ float lane63_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 // Full-wave (64 lanes) sum; every lane gets the total.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+    v += dpp_f32<DPP_ROW_SHR1, 0xF>(0.0f, v);
+    v += dpp_f32<DPP_ROW_SHR2, 0xF>(0.0f, v);
+    v += dpp_f32<DPP_ROW_SHR4, 0xF>(0.0f, v);
+    v += dpp_f32<DPP_ROW_SHR8, 0xF>(0.0f, v);
+    v += dpp_f32<DPP_ROW_BCAST15, 0xA>(0.0f, v);
+    v += dpp_f32<DPP_ROW_BCAST31, 0xC>(0.0f, v);
+    return lane63_f32(v);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
+    v = fmaxf(v, dpp_f32<DPP_ROW_SHR1, 0xF>(-INFINITY, v));
+    v = fmaxf(v, dpp_f32<DPP_ROW_SHR2, 0xF>(-INFINITY, v));
+    v = fmaxf(v, dpp_f32<DPP_ROW_SHR4, 0xF>(-INFINITY, v));
+    v = fmaxf(v, dpp_f32<DPP_ROW_SHR8, 0xF>(-INFINITY, v));
+    v = fmaxf(v, dpp_f32<DPP_ROW_BCAST15, 0xA>(-INFINITY, v));
+    v = fmaxf(v, dpp_f32<DPP_ROW_BCAST31, 0xC>(-INFINITY, v));
+    return lane63_f32(v);
 }
 
 // ------------------------------------------------------------------ host error plumbing
@@ -120,6 +148,15 @@ hipError_t launch_decode_rows(const OrganView& o, uint32_t row0, uint32_t nrows,
                               hipStream_t s);
 // Canonical -> tiled repack of one organ; `scratch` holds >= 8*(n_tiles*steps+1) bytes.
 hipError_t launch_repack(const CanonView& src, const OrganView& dst, void* scratch, hipStream_t s);
+// The same for n organs of one kind (job table in device memory; mixed jobs
+// carry a count array of n_tiles*steps words each).  max_items = the largest
+// n_tiles*steps*64 of the jobs.
+struct RepackJob {
+    CanonView src;
+    OrganView dst;
+    uint32_t* counts;
+};
+hipError_t launch_repack_batch(int kind, const RepackJob* jobs_dev, uint32_t n, size_t max_items, hipStream_t s);
 // Device bytes of the tiled layout (sections 256-B aligned); mixed needs n_bin/n_q2.
 size_t tiled_bytes(int kind, int group, uint32_t rows, uint32_t cols, uint32_t n_bin, uint32_t n_q2,
                    size_t* packed_bytes);

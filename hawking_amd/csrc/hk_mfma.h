@@ -102,14 +102,37 @@ __device__ __forceinline__ float block_max_abs(const float* __restrict__ x, uint
     return r;
 }
 
-// All threads of the block: A tiles and per-32-column sums of X into `lds`
-// (x_lds_bytes<KIND>(steps) bytes).  Returns E; non-finite x sets E's flag.
-// Ends with __syncthreads().
-template <int KIND>
-__device__ int prepare_x(const float* __restrict__ x, uint32_t cols, uint32_t steps, uint8_t* lds, float* red,
-                         bool* nonfinite) {
+// The threads that build one x image together: the whole block, or one wave
+// building an image of its own (no block barrier).
+struct BlockTeam {
+    __device__ uint32_t idx() const { return threadIdx.x; }
+    __device__ uint32_t size() const { return blockDim.x; }
+    __device__ float max_abs(const float* __restrict__ x, uint32_t n, float* red) const {
+        return block_max_abs(x, n, red);
+    }
+    __device__ void sync() const { __syncthreads(); }
+};
+struct WaveTeam {
+    uint32_t lane;
+    __device__ uint32_t idx() const { return lane; }
+    __device__ uint32_t size() const { return 64u; }
+    __device__ float max_abs(const float* __restrict__ x, uint32_t n, float*) const {
+        float m = 0.0f;
+        for (uint32_t c = lane; c < n; c += 64u) m = fmaxf(m, fabsf(x[c]));
+        return wave_max(m);
+    }
+    __device__ void sync() const {}
+};
+
+// The x image: A tiles and per-32-column sums of X written to `lds`
+// (x_lds_bytes<KIND>(steps) bytes; any address space), built by `team`.
+// Returns E; non-finite x sets the flag.  A block team ends with
+// __syncthreads(); a wave team leaves ordering to the caller.
+template <int KIND, class Team>
+__device__ int prepare_x(const Team& team, const float* __restrict__ x, uint32_t cols, uint32_t steps, uint8_t* lds,
+                         float* red, bool* nonfinite) {
     constexpr int P = Kcfg<KIND>::P, SC = Kcfg<KIND>::STEP_COLS;
-    float m = block_max_abs(x, cols, red);
+    float m = team.max_abs(x, cols, red);
     *nonfinite = !isfinite(m);
     if (*nonfinite) m = 0.0f;
     int e2 = 0;
@@ -118,10 +141,11 @@ __device__ int prepare_x(const float* __restrict__ x, uint32_t cols, uint32_t st
     const int ntau = (int)steps * P;
     uint32_t* A = reinterpret_cast<uint32_t*>(lds);
     float* SX = reinterpret_cast<float*>(lds + (size_t)ntau * A_TILE_STRIDE);
+    const int ti = (int)team.idx(), ts = (int)team.size();
     // zero blocks
-    for (int i = threadIdx.x; i < ntau * 4; i += blockDim.x) A[(i >> 2) * (A_TILE_STRIDE / 4) + 64 + (i & 3)] = 0u;
+    for (int i = ti; i < ntau * 4; i += ts) A[(i >> 2) * (A_TILE_STRIDE / 4) + 64 + (i & 3)] = 0u;
     // unit = (tau, slot q, dword d): 4 A bytes -> 4 lanes' dwords via a byte transpose
-    for (int u = threadIdx.x; u < ntau * 16; u += blockDim.x) {
+    for (int u = ti; u < ntau * 16; u += ts) {
         const int d = u & 3, q = (u >> 2) & 3, tau = u >> 4;
         const int t = tau / P, mu = tau % P;
         uint32_t z[4];
@@ -138,15 +162,15 @@ __device__ int prepare_x(const float* __restrict__ x, uint32_t cols, uint32_t st
     }
     // per-32-column sums: 8 columns per thread, 4 consecutive lanes per block
     const uint32_t kcols = steps * (uint32_t)SC;
-    for (uint32_t c0 = threadIdx.x * 8u; c0 < kcols; c0 += blockDim.x * 8u) {
+    for (uint32_t c0 = (uint32_t)ti * 8u; c0 < kcols; c0 += (uint32_t)ts * 8u) {
         int32_t s = 0;
 #pragma unroll
         for (uint32_t k = 0; k < 8; ++k) s += fixed_x(x, c0 + k, cols, E);
         s += __shfl_xor(s, 1, 64);
         s += __shfl_xor(s, 2, 64);
-        if ((threadIdx.x & 3u) == 0) SX[c0 / 32u] = (float)s;
+        if ((ti & 3) == 0) SX[c0 / 32u] = (float)s;
     }
-    __syncthreads();
+    team.sync();
     return E;
 }
 
@@ -158,6 +182,13 @@ __device__ __forceinline__ uint32_t a_lane_offset(int lane) {
 __device__ __forceinline__ v4i lds_a(const uint8_t* lds, uint32_t tau, uint32_t off) {
     return *reinterpret_cast<const v4i*>(lds + tau * A_TILE_STRIDE + off);
 }
+
+// A-operand source: an x image (in LDS) and this lane's offset into each tile.
+struct ImageA {
+    const uint8_t* img;
+    uint32_t aoff;
+    __device__ __forceinline__ v4i operator()(uint32_t tau) const { return lds_a(img, tau, aoff); }
+};
 
 // One step of R row tiles, as fetched from memory: the weight bytes and scales
 // each lane needs (row lane%16 of tile T[r], column slot lane/16).
@@ -180,51 +211,56 @@ struct Frag<HK_MIXED, R> {
     bool q2[R];
 };
 
+// Issue the loads of step t of tile T of organ o into slot r of f.
+template <int KIND, int R>
+__device__ __forceinline__ void fetch_one(const OrganView& o, uint32_t T, uint32_t t, int lane, Frag<KIND, R>& f,
+                                          int r) {
+    if constexpr (KIND == HK_BIN || KIND == HK_Q4) {
+        f.v[r] = *reinterpret_cast<const uint4*>(o.data + ((size_t)T * o.steps + t) * 1024u + 16u * lane);
+        f.s[r] = f16_bits_to_f32(o.scales[((size_t)T * 64u + lane) * o.steps + t]);
+    } else {
+        const uint4 h = o.hdr[(size_t)T * o.steps + t];
+        const uint32_t below = __builtin_amdgcn_mbcnt_hi(h.y, __builtin_amdgcn_mbcnt_lo(h.x, 0u));
+        const bool isq2 = ((lane < 32 ? (h.x >> lane) : (h.y >> (lane - 32))) & 1u) != 0;
+        const uint8_t* p = o.data + h.z + 16u * ((uint32_t)lane + below);
+        const uint4 va = *reinterpret_cast<const uint4*>(p);
+        const uint4 vb = *reinterpret_cast<const uint4*>(p + (isq2 ? 16 : 0));
+        f.V[r][0] = va.x;
+        f.V[r][1] = va.y;
+        f.V[r][2] = va.z;
+        f.V[r][3] = va.w;
+        f.V[r][4] = vb.x;
+        f.V[r][5] = vb.y;
+        f.V[r][6] = vb.z;
+        f.V[r][7] = vb.w;
+        const uint16_t* spp = o.scales + h.w + (uint32_t)lane + below;
+        f.s0[r] = f16_bits_to_f32(spp[0]);
+        f.s1[r] = f16_bits_to_f32(spp[isq2 ? 1 : 0]);
+        f.q2[r] = isq2;
+    }
+}
+
 // Issue the loads of step t for tiles T[0..R-1] (tiles r >= nvalid alias T[0]).
 template <int KIND, int R>
 __device__ __forceinline__ void fetch_step(const OrganView& o, const uint32_t* T, int nvalid, uint32_t t, int lane,
                                            Frag<KIND, R>& f) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const uint32_t Tr = r < nvalid ? T[r] : T[0];
-        if constexpr (KIND == HK_BIN || KIND == HK_Q4) {
-            f.v[r] = *reinterpret_cast<const uint4*>(o.data + ((size_t)Tr * o.steps + t) * 1024u + 16u * lane);
-            f.s[r] = f16_bits_to_f32(o.scales[((size_t)Tr * 64u + lane) * o.steps + t]);
-        } else {
-            const uint4 h = o.hdr[(size_t)Tr * o.steps + t];
-            const uint32_t below = __builtin_amdgcn_mbcnt_hi(h.y, __builtin_amdgcn_mbcnt_lo(h.x, 0u));
-            const bool isq2 = ((lane < 32 ? (h.x >> lane) : (h.y >> (lane - 32))) & 1u) != 0;
-            const uint8_t* p = o.data + h.z + 16u * ((uint32_t)lane + below);
-            const uint4 va = *reinterpret_cast<const uint4*>(p);
-            const uint4 vb = *reinterpret_cast<const uint4*>(p + (isq2 ? 16 : 0));
-            f.V[r][0] = va.x;
-            f.V[r][1] = va.y;
-            f.V[r][2] = va.z;
-            f.V[r][3] = va.w;
-            f.V[r][4] = vb.x;
-            f.V[r][5] = vb.y;
-            f.V[r][6] = vb.z;
-            f.V[r][7] = vb.w;
-            const uint16_t* spp = o.scales + h.w + (uint32_t)lane + below;
-            f.s0[r] = f16_bits_to_f32(spp[0]);
-            f.s1[r] = f16_bits_to_f32(spp[isq2 ? 1 : 0]);
-            f.q2[r] = isq2;
-        }
-    }
+    for (int r = 0; r < R; ++r) fetch_one<KIND, R>(o, r < nvalid ? T[r] : T[0], t, lane, f, r);
 }
 
 // Consume one fetched step: acc[r] += this lane's partial dot, in units of
 // 2^-E.  Tiles r >= nvalid are computed on aliased data and discarded.
-template <int KIND, int R>
-__device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t, int nvalid, const uint8_t* lds,
-                                             uint32_t aoff, const float* SX, int q, float* acc) {
+// A(tau) yields this lane's A operand of x-image tile tau.
+template <int KIND, int R, class ASrc>
+__device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t, int nvalid, const ASrc& A,
+                                             const float* SX, int q, float* acc) {
     v4i c[R];
     if constexpr (KIND == HK_BIN) {
 #pragma unroll
         for (int r = 0; r < R; ++r) c[r] = v4i{0, 0, 0, 0};
 #pragma unroll
         for (int p = 0; p < 8; ++p) {
-            const v4i a = lds_a(lds, t * 8 + p, aoff);
+            const v4i a = A(t * 8 + p);
             const uint32_t m = 0x01010101u << p;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
@@ -238,7 +274,7 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
             if (r < nvalid) acc[r] += f.s[r] * (combine_limbs(c[r]) * (1.0f / 64.0f) - sx);
     } else if constexpr (KIND == HK_Q4) {
         const uint32_t m = 0x0F0F0F0Fu;
-        const v4i alo = lds_a(lds, t * 2, aoff), ahi = lds_a(lds, t * 2 + 1, aoff);
+        const v4i alo = A(t * 2), ahi = A(t * 2 + 1);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const v4i lo = {(int)(f.v[r].x & m), (int)(f.v[r].y & m), (int)(f.v[r].z & m), (int)(f.v[r].w & m)};
@@ -268,7 +304,7 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
             for (int r = 0; r < R; ++r) c[r] = v4i{0, 0, 0, 0};
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const v4i a = lds_a(lds, t * 8 + h * 4 + u, aoff);
+                const v4i a = A(t * 8 + h * 4 + u);
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     const uint32_t bm = f.q2[r] ? 0x03030303u : 0x01010101u;

@@ -16,27 +16,35 @@ struct MoeDims {
     float eps;
 };
 
-// One layer's device weights; table holds (E+1)*3 organ views:
+// One layer's device weights; table holds (E+1)*3 tiled organ views:
 // [expert*3 + {0: gate, 1: up, 2: down}], expert E = shared expert.
 struct MoeLayerDev {
     const float* norm_w;
     const float* router_w;
     const float* gate_w;   // shared-expert gate, may be null
-    const CanonView* table;
+    const OrganView* table;
 };
 
 // Per-model device workspace.
 struct MoeWs {
-    float* xn;        // [H]
-    float* logits;    // [E]
-    int32_t* ids;     // [K]
-    float* weights;   // [K]
-    float* gate;      // [2]: shared-gate logit, shared-gate value
-    float* act;       // [(K+1) * Imax]
-    uint32_t* status; // device error bits
+    float* logits;     // [E]
+    int32_t* ids;      // [K]
+    float* weights;    // [K]
+    float* gate;       // [2]: shared-gate logit, shared-gate value
+    float* act;        // [(K+1) * Imax]
+    uint8_t* img;      // x image of RMSNorm(h) for the gate/up organs
+    int32_t* img_e;    // [1]: its exponent E
+    OrganView* sel;    // [(K+1)*3]: the organs of the selected experts, slot order
+    uint32_t* status;  // device error bits
 };
 
+// Bytes of the gate/up x image and of the down kernel's LDS.
+size_t moe_img_bytes(int kind, uint32_t H);
+size_t moe_down_lds_bytes(int kind, uint32_t Imax, uint32_t slots);
+size_t moe_gate_up_lds_bytes(int kind, uint32_t H);
+
+// ids_out / w_out (device, top_k each) may be null.
 hipError_t launch_moe_layer(int kind, const MoeDims& d, const MoeLayerDev& L, const float* h_in,
-                            float* h_out, const MoeWs& ws, hipStream_t s);
+                            float* h_out, const MoeWs& ws, int32_t* ids_out, float* w_out, hipStream_t s);
 
 }  // namespace hk

@@ -1,139 +1,303 @@
 // hk_moe.hip -- one MoE decode layer (moe_suffix) at batch 1 on device data.
 //
-// Four stream-ordered launches, no host round trip; the routed expert ids
-// are read from device memory by the expert kernels
+// Three stream-ordered launches, no host round trip; expert weights live in
+// the tiled layout and every packed dot runs on the int8 matrix-core engine
+// (hk_mfma.h).  The routed expert ids never leave the device
 // (run_qwen80_routed_expert_table,
 //  crates/hawking-core/src/model/qwen80_device_expert_table.rs:1204-1247):
-//   1. router:  xn = RMSNorm(1+w)(h) (recomputed per block, block 0 stores it);
-//               logits = Wr xn; shared-gate logit = wg . xn
-//   2. top-k:   softmax, top-k, renormalise; gate = sigmoid(gate logit)
-//   3. gate/up: act[slot] = silu(gate_e xn) * (up_e xn) for the K routed
-//               slots and the shared expert (SwiGLU fused)
-//   4. down:    out = h + sum_r w_r (down_r act_r)  (route order)
-//                       + gate * (down_shared act_shared)
+//   1. route:   every block recomputes xn = RMSNorm(1+w)(h) in LDS; blocks
+//               0..ceil(E/4)-1 compute the router logits (one row per wave),
+//               the last block computes the shared-gate logit and the x image
+//               of xn (fixed-point limb tiles, built once per layer).  The
+//               block that finishes last runs softmax / top-k / renormalise
+//               and writes the organ views of the selected experts in slot
+//               order (slot K = the shared expert).
+//   2. gate/up: one workgroup per (16-row tile, slot); its 4 waves split the
+//               columns, both organs share each x-image fetch, and the
+//               epilogue applies SwiGLU: act = silu(gate.xn) * (up.xn).
+//   3. down:    one workgroup per 16-row output tile, one wave per slot; each
+//               wave builds the x image of its slot's activations, and the
+//               block combines out = h + sum_r w_r y_r (route order)
+//               + gate * y_shared  (moe_suffix,
+//               model/qwen80_uniform_q4_hybrid_decode.rs:2615-2757).
 #include "hk_internal.h"
+#include "hk_mfma.h"
 #include "hk_moe.h"
 #include "hk_router_dev.h"
-#include "hk_rowdot.h"
 
 namespace hk {
 
-__device__ __forceinline__ float block_inv_rms(const float* __restrict__ h, uint32_t H, float eps,
-                                               float* red) {
-    float ss = 0.f;
-    for (uint32_t c = threadIdx.x; c < H; c += blockDim.x) ss += h[c] * h[c];
-    ss = block_sum(ss, red);
-    return 1.0f / sqrtf(ss / (float)H + eps);
+size_t moe_img_bytes(int kind, uint32_t H) {
+    const uint32_t S = n_steps_for(kind, H);
+    return kind == HK_Q4 ? x_lds_bytes<HK_Q4>(S) : x_lds_bytes<HK_MIXED>(S);
 }
 
-__global__ void __launch_bounds__(256) moe_router_kernel(MoeDims d, MoeLayerDev L,
-                                                         const float* __restrict__ h, MoeWs ws) {
-    extern __shared__ __align__(16) float xn[];
+size_t moe_gate_up_lds_bytes(int kind, uint32_t H) { return moe_img_bytes(kind, H) + 4 * 32 * sizeof(float); }
+
+size_t moe_down_lds_bytes(int kind, uint32_t Imax, uint32_t slots) {
+    return (size_t)slots * (moe_img_bytes(kind, Imax) + 16 * sizeof(float) + (size_t)Imax * sizeof(float));
+}
+
+// Float4s of h (per thread) and of a router row (per lane) held in registers:
+// every global load of the route kernel is issued before its first reduction.
+constexpr int H_PRE = 8;    // 256 threads x 8 float4 = hidden <= 8192
+constexpr int ROW_PRE = 8;  // 64 lanes x 8 float4 = 2048 columns, the rest streamed
+
+__device__ __forceinline__ float dot4(const float4& a, const float4& b) {
+    return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+}
+
+template <int KIND>
+__global__ void __launch_bounds__(256) moe_route_kernel(MoeDims d, MoeLayerDev L, const float* __restrict__ h,
+                                                        MoeWs ws) {
+    extern __shared__ __align__(16) float xn[];  // [H]
     __shared__ float red[4];
-    const float inv = block_inv_rms(h, d.H, d.eps, red);
-    for (uint32_t c = threadIdx.x; c < d.H; c += blockDim.x) {
-        const float v = h[c] * inv * (1.0f + L.norm_w[c]);
-        xn[c] = v;
-        if (blockIdx.x == 0) ws.xn[c] = v;
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t nrb = (d.E + 3u) / 4u, n4 = d.H / 4u;
+    // this wave's weight row: a router row, or the shared-expert gate (last block, wave 0)
+    const float* wrow = nullptr;
+    if (blockIdx.x < nrb) {
+        const uint32_t row = blockIdx.x * 4u + wave;
+        if (row < d.E) wrow = L.router_w + (size_t)row * d.H;
+    } else if (wave == 0) {
+        wrow = L.gate_w;
+    }
+    const float4* w4 = reinterpret_cast<const float4*>(wrow);
+    float4 wv[ROW_PRE];
+#pragma unroll
+    for (int k = 0; k < ROW_PRE; ++k) {
+        const uint32_t j = (uint32_t)lane + 64u * k;
+        wv[k] = (wrow && j < n4) ? w4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const float4* h4 = reinterpret_cast<const float4*>(h);
+    const float4* g4 = reinterpret_cast<const float4*>(L.norm_w);
+    float4 hv[H_PRE], gv[H_PRE];
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < H_PRE; ++k) {
+        const uint32_t j = threadIdx.x + 256u * k;
+        hv[k] = j < n4 ? h4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        gv[k] = j < n4 ? g4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int k = 0; k < H_PRE; ++k) ss += dot4(hv[k], hv[k]);
+    // xn = RMSNorm(1+w)(h) = h * (mean(h^2) + eps)^-1/2 * (1 + w)
+    const float inv = 1.0f / sqrtf(block_sum(ss, red) / (float)d.H + d.eps);
+    float4* x4 = reinterpret_cast<float4*>(xn);
+#pragma unroll
+    for (int k = 0; k < H_PRE; ++k) {
+        const uint32_t j = threadIdx.x + 256u * k;
+        if (j < n4)
+            x4[j] = make_float4(hv[k].x * inv * (1.0f + gv[k].x), hv[k].y * inv * (1.0f + gv[k].y),
+                                hv[k].z * inv * (1.0f + gv[k].z), hv[k].w * inv * (1.0f + gv[k].w));
     }
     __syncthreads();
-    const int lane = threadIdx.x & 63;
-    const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    CanonView o{};
-    o.kind = HK_F32;
-    o.cols = d.H;
-    if (row < d.E) {
-        o.rows = d.E;
-        o.dense = L.router_w;
-        const float acc = wave_sum(row_dot_partial<HK_F32>(o, row, xn, lane));
-        if (lane == 0) ws.logits[row] = acc;
-    } else if (row == d.E && L.gate_w) {
-        o.rows = 1;
-        o.dense = L.gate_w;
-        const float acc = wave_sum(row_dot_partial<HK_F32>(o, 0, xn, lane));
-        if (lane == 0) ws.gate[0] = acc;
+    if (wrow) {
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < ROW_PRE; ++k) {
+            const uint32_t j = (uint32_t)lane + 64u * k;
+            if (j < n4) acc += dot4(wv[k], x4[j]);
+        }
+        for (uint32_t j = (uint32_t)lane + 64u * ROW_PRE; j < n4; j += 64u) acc += dot4(w4[j], x4[j]);
+        acc = wave_sum(acc);
+        if (lane == 0) {
+            if (blockIdx.x < nrb)
+                ws.logits[blockIdx.x * 4u + wave] = acc;
+            else
+                ws.gate[0] = acc;
+        }
+    }
+    if (blockIdx.x == nrb) {
+        // the x image of xn for every gate/up organ of this layer
+        bool bad = false;
+        const int E = prepare_x<KIND>(BlockTeam{}, xn, d.H, n_steps_for(KIND, d.H), ws.img, red, &bad);
+        if (threadIdx.x == 0) {
+            ws.img_e[0] = E;
+            if (bad) atomicOr(ws.status, HK_DEVERR_NONFINITE);
+        }
     }
 }
 
-__global__ void __launch_bounds__(256) moe_topk_kernel(MoeDims d, int has_gate, MoeWs ws) {
-    extern __shared__ float p[];
-    __shared__ float redf[4];
-    __shared__ ArgBest reda[4];
-    softmax_topk_block(ws.logits, d.E, d.K, 0.0f, 1, p, ws.ids, ws.weights, ws.status, redf, reda);
-    if (threadIdx.x == 0) ws.gate[1] = has_gate ? 1.0f / (1.0f + expf(-ws.gate[0])) : 1.0f;
+// Softmax, top-k, renormalise (source_qwen80_topk_router) in one wave, the
+// shared-expert gate value, and the organ views of the selected experts in
+// slot order.
+template <int NPL>
+__global__ void __launch_bounds__(64) moe_topk_kernel(MoeDims d, MoeLayerDev L, MoeWs ws, int32_t* ids_out,
+                                                      float* w_out) {
+    const int lane = threadIdx.x & 63;
+    const ArgBest mine = softmax_topk_wave<NPL>(ws.logits, d.E, d.K, 1, ws.ids, ws.weights, ws.status);
+    if (lane == 0) ws.gate[1] = L.gate_w ? 1.0f / (1.0f + expf(-ws.gate[0])) : 1.0f;
+    if ((uint32_t)lane < d.K) {
+        if (ids_out) ids_out[lane] = mine.i;
+        if (w_out) w_out[lane] = mine.v;
+    }
+    // lane i writes sel[i]: slot i/3, projection i%3 (slots * 3 <= 48 < 64)
+    const uint32_t slots = d.K + (d.has_shared ? 1u : 0u);
+    const uint32_t i = (uint32_t)lane, slot = i / 3u, pj = i % 3u;
+    const int32_t id = __shfl(mine.i, (int)min(slot, 63u), 64);
+    if (i < slots * 3u) {
+        uint32_t e = d.E;
+        if (slot < d.K) e = (id >= 0 && (uint32_t)id < d.E) ? (uint32_t)id : 0xFFFFFFFFu;
+        // word copy (a struct assignment here goes through scratch memory);
+        // an invalid route selects no organ (all-zero view: n_tiles = 0)
+        static_assert(sizeof(OrganView) % 8 == 0, "OrganView is copied in 8-byte words");
+        const bool ok = e != 0xFFFFFFFFu;
+        const uint64_t* from = reinterpret_cast<const uint64_t*>(L.table + (ok ? e * 3u + pj : 0u));
+        uint64_t* to = reinterpret_cast<uint64_t*>(ws.sel + i);
+#pragma unroll
+        for (uint32_t k = 0; k < sizeof(OrganView) / 8; ++k) to[k] = ok ? from[k] : 0ull;
+        if (!ok && pj == 0) atomicOr(ws.status, HK_DEVERR_ROUTE);
+    }
+}
+
+template <int KIND, int D>
+__global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeWs ws) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const uint32_t slot = blockIdx.y, T = blockIdx.x;
+    const OrganView g = ws.sel[slot * 3u + 0u];
+    if (T >= g.n_tiles) return;
+    const OrganView u = ws.sel[slot * 3u + 1u];
+    const int lane = threadIdx.x & 63, q = lane >> 4;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t S = g.steps, per = (S + 3u) / 4u;
+    const uint32_t s0 = min(wave * per, S), n = min(s0 + per, S) - s0;
+    Frag<KIND, 2> f[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+        if ((uint32_t)k < n) {
+            fetch_one<KIND, 2>(g, T, s0 + k, lane, f[k], 0);
+            fetch_one<KIND, 2>(u, T, s0 + k, lane, f[k], 1);
+        }
+    }
+    // the x image built by the route kernel, into LDS
+    const uint32_t ib = (uint32_t)x_lds_bytes<KIND>(S);
+    for (uint32_t o = threadIdx.x * 16u; o < ib; o += blockDim.x * 16u)
+        *reinterpret_cast<uint4*>(lds + o) = *reinterpret_cast<const uint4*>(ws.img + o);
+    __syncthreads();
+    const int E = ws.img_e[0];
+    const ImageA A{lds, a_lane_offset(lane)};
+    const float* SX = reinterpret_cast<const float*>(lds + (size_t)S * Kcfg<KIND>::P * A_TILE_STRIDE);
+    float acc[2] = {0.0f, 0.0f};
+    for (uint32_t it = 0; it < n; it += D) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            if (it + k >= n) break;
+            compute_step<KIND, 2>(f[k], s0 + it + k, 2, A, SX, q, acc);
+            const uint32_t nx = it + D + k;
+            if (nx < n) {
+                fetch_one<KIND, 2>(g, T, s0 + nx, lane, f[k], 0);
+                fetch_one<KIND, 2>(u, T, s0 + nx, lane, f[k], 1);
+            }
+        }
+    }
+    float* part = reinterpret_cast<float*>(lds + ib);  // [wave][gate 16 | up 16]
+    const float gs = tile_row_sum(acc[0]), us = tile_row_sum(acc[1]);
+    if (lane < 16) {
+        part[wave * 32u + lane] = gs;
+        part[wave * 32u + 16u + lane] = us;
+    }
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        float gv = 0.f, uv = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            gv += part[w * 32 + threadIdx.x];
+            uv += part[w * 32 + 16 + threadIdx.x];
+        }
+        gv = ldexpf(gv, -E);
+        uv = ldexpf(uv, -E);
+        const uint32_t row = T * 16u + threadIdx.x;
+        if (row < g.rows) ws.act[(size_t)slot * d.Imax + row] = (gv / (1.0f + expf(-gv))) * uv;
+    }
+}
+
+template <int KIND, int D>
+__global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, const float* __restrict__ h_in,
+                                                        float* __restrict__ h_out, MoeWs ws, uint32_t img_stride) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const uint32_t T = blockIdx.x, slots = blockDim.x >> 6;
+    const uint32_t slot = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, q = lane >> 4;
+    const OrganView o = ws.sel[slot * 3u + 2u];
+    const bool active = T < o.n_tiles;
+    const uint32_t S = active ? o.steps : 0u;
+    Frag<KIND, 1> f[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+        if ((uint32_t)k < S) fetch_one<KIND, 1>(o, T, (uint32_t)k, lane, f[k], 0);
+    const float wgt = !active ? 0.0f : (slot < d.K ? ws.weights[slot] : ws.gate[1]);
+    // this slot's activations: staged in LDS with one batch of loads, then
+    // turned into an x image of the slot's own
+    uint8_t* img = lds + (size_t)slot * img_stride;
+    float* xs = reinterpret_cast<float*>(lds + (size_t)slots * (img_stride + 64u)) + (size_t)slot * d.Imax;
+    if (active) {
+        const float4* a4 = reinterpret_cast<const float4*>(ws.act + (size_t)slot * d.Imax);
+        for (uint32_t j = (uint32_t)lane; j < o.cols / 4u; j += 64u) reinterpret_cast<float4*>(xs)[j] = a4[j];
+    }
+    __syncthreads();
+    int E = 0;
+    if (active) {
+        bool bad = false;
+        E = prepare_x<KIND>(WaveTeam{(uint32_t)lane}, xs, o.cols, S, img, nullptr, &bad);
+        if (bad && lane == 0) atomicOr(ws.status, HK_DEVERR_NONFINITE);
+    }
+    __syncthreads();
+    const ImageA A{img, a_lane_offset(lane)};
+    const float* SX = reinterpret_cast<const float*>(img + (size_t)S * Kcfg<KIND>::P * A_TILE_STRIDE);
+    float acc[1] = {0.0f};
+    for (uint32_t it = 0; it < S; it += D) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            if (it + k >= S) break;
+            compute_step<KIND, 1>(f[k], it + k, 1, A, SX, q, acc);
+            const uint32_t nx = it + D + k;
+            if (nx < S) fetch_one<KIND, 1>(o, T, nx, lane, f[k], 0);
+        }
+    }
+    float* part = reinterpret_cast<float*>(lds + (size_t)slots * img_stride);  // [slots][16]
+    const float y = tile_row_sum(acc[0]);
+    if (lane < 16) part[slot * 16u + lane] = active ? ldexpf(y, -E) * wgt : 0.0f;
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        // combined += out_r * w_r in route order, then += gate * shared; out = h + combined
+        float comb = 0.0f;
+        for (uint32_t r = 0; r < slots; ++r) comb += part[r * 16u + threadIdx.x];
+        const uint32_t row = T * 16u + threadIdx.x;
+        if (row < d.H) h_out[row] = h_in[row] + comb;
+    }
 }
 
 template <int KIND>
-__global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev L, MoeWs ws) {
-    extern __shared__ __align__(16) float xn[];
-    for (uint32_t c = threadIdx.x; c < d.H; c += blockDim.x) xn[c] = ws.xn[c];
-    __syncthreads();
-    const uint32_t slot = blockIdx.y;
-    const bool shared = slot >= d.K;
-    const uint32_t e = shared ? d.E : (uint32_t)ws.ids[slot];
-    if (e > d.E || (!shared && e == d.E)) {
-        // invalid route (non-finite logits): flag it and touch no expert
-        if (threadIdx.x == 0) atomicOr(ws.status, HK_DEVERR_ROUTE);
-        return;
-    }
-    const CanonView& g = L.table[e * 3 + 0];
-    const CanonView& u = L.table[e * 3 + 1];
-    const int lane = threadIdx.x & 63;
-    const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= g.rows) return;
-    const float gv = wave_sum(row_dot_partial<KIND>(g, row, xn, lane));
-    const float uv = wave_sum(row_dot_partial<KIND>(u, row, xn, lane));
-    if (lane == 0) ws.act[(size_t)slot * d.Imax + row] = (gv / (1.0f + expf(-gv))) * uv;
-}
-
-template <int KIND>
-__global__ void __launch_bounds__(256) moe_down_kernel(MoeDims d, MoeLayerDev L,
-                                                       const float* __restrict__ h_in,
-                                                       float* __restrict__ h_out, MoeWs ws) {
-    extern __shared__ __align__(16) float act[];
+static hipError_t launch_layer(const MoeDims& d, const MoeLayerDev& L, const float* h_in, float* h_out,
+                               const MoeWs& ws, int32_t* ids_out, float* w_out, hipStream_t s) {
+    const uint32_t nrb = (d.E + 3u) / 4u;
     const uint32_t slots = d.K + (d.has_shared ? 1u : 0u);
-    for (uint32_t i = threadIdx.x; i < slots * d.Imax; i += blockDim.x) act[i] = ws.act[i];
-    __syncthreads();
-    const int lane = threadIdx.x & 63;
-    const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= d.H) return;
-    float combined = 0.0f;
-    for (uint32_t r = 0; r < d.K; ++r) {
-        const uint32_t e = (uint32_t)ws.ids[r];
-        if (e >= d.E) continue;  // flagged by the gate/up kernel
-        const CanonView& dn = L.table[e * 3 + 2];
-        const float y = wave_sum(row_dot_partial<KIND>(dn, row, act + (size_t)r * d.Imax, lane));
-        combined += y * ws.weights[r];
-    }
-    if (d.has_shared) {
-        const CanonView& dn = L.table[d.E * 3 + 2];
-        const float y = wave_sum(row_dot_partial<KIND>(dn, row, act + (size_t)d.K * d.Imax, lane));
-        combined += y * ws.gate[1];
-    }
-    if (lane == 0) h_out[row] = h_in[row] + combined;
-}
-
-hipError_t launch_moe_layer(int kind, const MoeDims& d, const MoeLayerDev& L, const float* h_in,
-                            float* h_out, const MoeWs& ws, hipStream_t s) {
-    const size_t xn_bytes = (size_t)d.H * sizeof(float);
-    hipLaunchKernelGGL(moe_router_kernel, dim3((d.E + 1 + 3) / 4), dim3(256), xn_bytes, s, d, L, h_in, ws);
-    hipLaunchKernelGGL(moe_topk_kernel, dim3(1), dim3(256), (size_t)d.E * sizeof(float), s, d,
-                       L.gate_w != nullptr ? 1 : 0, ws);
-    const uint32_t slots = d.K + (d.has_shared ? 1u : 0u);
-    const dim3 gu((d.Imax + 3) / 4, slots);
-    const size_t act_bytes = (size_t)slots * d.Imax * sizeof(float);
-    if (kind == HK_Q4) {
-        hipLaunchKernelGGL(moe_gate_up_kernel<HK_Q4>, gu, dim3(256), xn_bytes, s, d, L, ws);
-        hipLaunchKernelGGL(moe_down_kernel<HK_Q4>, dim3((d.H + 3) / 4), dim3(256), act_bytes, s, d, L,
-                           h_in, h_out, ws);
-    } else if (kind == HK_MIXED) {
-        hipLaunchKernelGGL(moe_gate_up_kernel<HK_MIXED>, gu, dim3(256), xn_bytes, s, d, L, ws);
-        hipLaunchKernelGGL(moe_down_kernel<HK_MIXED>, dim3((d.H + 3) / 4), dim3(256), act_bytes, s, d, L,
-                           h_in, h_out, ws);
-    } else {
-        return hipErrorInvalidValue;
-    }
+    const uint32_t gu_tiles = n_tiles_for(d.has_shared ? max(d.I, d.SI) : d.I);
+    const uint32_t img_stride = (uint32_t)moe_img_bytes(KIND, d.Imax);
+    hipLaunchKernelGGL(moe_route_kernel<KIND>, dim3(nrb + 1u), dim3(256), (size_t)d.H * sizeof(float), s, d, L, h_in,
+                       ws);
+    if (d.E <= 512)
+        hipLaunchKernelGGL(moe_topk_kernel<8>, dim3(1), dim3(64), 0, s, d, L, ws, ids_out, w_out);
+    else if (d.E <= 1024)
+        hipLaunchKernelGGL(moe_topk_kernel<16>, dim3(1), dim3(64), 0, s, d, L, ws, ids_out, w_out);
+    else if (d.E <= 2048)
+        hipLaunchKernelGGL(moe_topk_kernel<32>, dim3(1), dim3(64), 0, s, d, L, ws, ids_out, w_out);
+    else
+        hipLaunchKernelGGL(moe_topk_kernel<64>, dim3(1), dim3(64), 0, s, d, L, ws, ids_out, w_out);
+    hipLaunchKernelGGL((moe_gate_up_kernel<KIND, 4>), dim3(gu_tiles, slots), dim3(256),
+                       moe_gate_up_lds_bytes(KIND, d.H), s, d, ws);
+    hipLaunchKernelGGL((moe_down_kernel<KIND, 4>), dim3(n_tiles_for(d.H)), dim3(64u * slots),
+                       moe_down_lds_bytes(KIND, d.Imax, slots), s, d, h_in, h_out, ws, img_stride);
     return hipGetLastError();
+}
+
+hipError_t launch_moe_layer(int kind, const MoeDims& d, const MoeLayerDev& L, const float* h_in, float* h_out,
+                            const MoeWs& ws, int32_t* ids_out, float* w_out, hipStream_t s) {
+    if (kind == HK_Q4) return launch_layer<HK_Q4>(d, L, h_in, h_out, ws, ids_out, w_out, s);
+    if (kind == HK_MIXED) return launch_layer<HK_MIXED>(d, L, h_in, h_out, ws, ids_out, w_out, s);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace hk

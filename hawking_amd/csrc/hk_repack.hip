@@ -1,5 +1,7 @@
 // hk_repack.hip -- load-time repack of canonical organs into the wavefront-
 // tiled layout (hk_tile.h), and the bit-exact decode probe over that layout.
+#include <algorithm>
+
 #include "hk_internal.h"
 #include "hk_tile.h"
 
@@ -73,7 +75,7 @@ OrganView tiled_place(int kind, int group, uint32_t rows, uint32_t cols, uint32_
 // ------------------------------------------------------------------ BIN / Q4
 
 // One thread per (tile, step, lane) item: copy its 16 bytes and its scale.
-__global__ void repack_fixed_kernel(CanonView src, OrganView dst) {
+__device__ void repack_fixed_body(const CanonView& src, const OrganView& dst) {
     const size_t total = (size_t)dst.n_tiles * dst.steps * 64;
     for (size_t it = (size_t)blockIdx.x * blockDim.x + threadIdx.x; it < total;
          it += (size_t)gridDim.x * blockDim.x) {
@@ -111,7 +113,7 @@ __device__ inline bool canon_is_q2(const CanonView& s, uint32_t r, uint32_t g, b
 }
 
 // Pass 1: one thread per (tile, step) block: Q2 mask and count.
-__global__ void repack_mixed_mask_kernel(CanonView src, OrganView dst, uint32_t* counts) {
+__device__ void repack_mixed_mask_body(const CanonView& src, const OrganView& dst, uint32_t* counts) {
     const uint32_t nb = dst.n_tiles * dst.steps;
     for (uint32_t b = blockIdx.x * blockDim.x + threadIdx.x; b < nb; b += gridDim.x * blockDim.x) {
         const uint32_t T = b / dst.steps, t = b % dst.steps;
@@ -127,9 +129,9 @@ __global__ void repack_mixed_mask_kernel(CanonView src, OrganView dst, uint32_t*
     }
 }
 
-// Pass 2 (one block): exclusive prefix of Q2 counts -> data / scale offsets.
-__global__ void repack_mixed_offsets_kernel(OrganView dst, const uint32_t* counts) {
-    if (threadIdx.x != 0) return;
+// Pass 2 (one thread per organ): exclusive prefix of Q2 counts -> data /
+// scale offsets.
+__device__ void repack_mixed_offsets_body(const OrganView& dst, const uint32_t* counts) {
     const uint32_t nb = dst.n_tiles * dst.steps;
     uint32_t q2 = 0;
     for (uint32_t b = 0; b < nb; ++b) {
@@ -141,7 +143,7 @@ __global__ void repack_mixed_offsets_kernel(OrganView dst, const uint32_t* count
 }
 
 // Pass 3: one thread per item: copy binary signs, or reorder Q2 codes.
-__global__ void repack_mixed_items_kernel(CanonView src, OrganView dst) {
+__device__ void repack_mixed_items_body(const CanonView& src, const OrganView& dst) {
     const size_t total = (size_t)dst.n_tiles * dst.steps * 64;
     const uint32_t gpr = src.cols / 128u;
     for (size_t it = (size_t)blockIdx.x * blockDim.x + threadIdx.x; it < total;
@@ -194,6 +196,30 @@ static unsigned grid1(size_t n) {
     return (unsigned)(b == 0 ? 1 : (b > 65536 ? 65536 : b));
 }
 
+// Single organ (arguments by value) and batched (blockIdx.y = job) forms.
+__global__ void repack_fixed_kernel(CanonView src, OrganView dst) { repack_fixed_body(src, dst); }
+__global__ void repack_mixed_mask_kernel(CanonView src, OrganView dst, uint32_t* counts) {
+    repack_mixed_mask_body(src, dst, counts);
+}
+__global__ void repack_mixed_offsets_kernel(OrganView dst, const uint32_t* counts) {
+    if (threadIdx.x == 0) repack_mixed_offsets_body(dst, counts);
+}
+__global__ void repack_mixed_items_kernel(CanonView src, OrganView dst) { repack_mixed_items_body(src, dst); }
+
+__global__ void repack_fixed_batch_kernel(const RepackJob* __restrict__ jobs) {
+    repack_fixed_body(jobs[blockIdx.y].src, jobs[blockIdx.y].dst);
+}
+__global__ void repack_mixed_mask_batch_kernel(const RepackJob* __restrict__ jobs) {
+    repack_mixed_mask_body(jobs[blockIdx.y].src, jobs[blockIdx.y].dst, jobs[blockIdx.y].counts);
+}
+__global__ void repack_mixed_offsets_batch_kernel(const RepackJob* __restrict__ jobs, uint32_t n) {
+    const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j < n) repack_mixed_offsets_body(jobs[j].dst, jobs[j].counts);
+}
+__global__ void repack_mixed_items_batch_kernel(const RepackJob* __restrict__ jobs) {
+    repack_mixed_items_body(jobs[blockIdx.y].src, jobs[blockIdx.y].dst);
+}
+
 hipError_t launch_repack(const CanonView& src, const OrganView& dst, void* scratch, hipStream_t s) {
     const size_t items = (size_t)dst.n_tiles * dst.steps * 64;
     if (src.kind == HK_BIN || src.kind == HK_Q4) {
@@ -203,6 +229,23 @@ hipError_t launch_repack(const CanonView& src, const OrganView& dst, void* scrat
         hipLaunchKernelGGL(repack_mixed_mask_kernel, dim3(grid1(items / 64)), dim3(256), 0, s, src, dst, counts);
         hipLaunchKernelGGL(repack_mixed_offsets_kernel, dim3(1), dim3(64), 0, s, dst, counts);
         hipLaunchKernelGGL(repack_mixed_items_kernel, dim3(grid1(items)), dim3(256), 0, s, src, dst);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_repack_batch(int kind, const RepackJob* jobs_dev, uint32_t n, size_t max_items, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    if (n > 65535) return hipErrorInvalidValue;
+    const unsigned gx = std::min(grid1(max_items), 1024u);
+    if (kind == HK_BIN || kind == HK_Q4) {
+        hipLaunchKernelGGL(repack_fixed_batch_kernel, dim3(gx, n), dim3(256), 0, s, jobs_dev);
+    } else if (kind == HK_MIXED) {
+        hipLaunchKernelGGL(repack_mixed_mask_batch_kernel, dim3(std::min(grid1(max_items / 64), 1024u), n), dim3(256),
+                           0, s, jobs_dev);
+        hipLaunchKernelGGL(repack_mixed_offsets_batch_kernel, dim3((n + 63) / 64), dim3(64), 0, s, jobs_dev, n);
+        hipLaunchKernelGGL(repack_mixed_items_batch_kernel, dim3(gx, n), dim3(256), 0, s, jobs_dev);
     } else {
         return hipErrorInvalidValue;
     }

@@ -23,9 +23,11 @@ __global__ void __launch_bounds__(256) softmax_topk_kernel(const float* __restri
     extern __shared__ float p[];
     __shared__ float redf[4];
     __shared__ ArgBest reda[4];
+    __shared__ int32_t sel_i[HK_TOPK_MAX];
+    __shared__ float sel_v[HK_TOPK_MAX];
     const size_t t = blockIdx.x;
     softmax_topk_block(logits + t * n, n, k, tie_eps, renorm, p, ids + t * k, weights + t * k, status,
-                       redf, reda);
+                       redf, reda, sel_i, sel_v);
 }
 
 // noaux_tc (gravity_glm.rs:447-500) for one token.
@@ -41,6 +43,8 @@ __global__ void __launch_bounds__(256) noaux_tc_kernel(const float* __restrict__
     float* gscore = smem + 2 * n;        // n_group
     uint8_t* allowed = reinterpret_cast<uint8_t*>(smem + 2 * n + n_group);  // n_group
     __shared__ ArgBest reda[4];
+    __shared__ int32_t sel_i[HK_TOPK_MAX];
+    __shared__ float sel_v[HK_TOPK_MAX];
     const size_t t = blockIdx.x;
     const float* lg = logits + t * n;
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
@@ -93,21 +97,25 @@ __global__ void __launch_bounds__(256) noaux_tc_kernel(const float* __restrict__
         }
         const ArgBest b = block_argmax(a, reda);
         if (threadIdx.x == 0) {
-            ids[t * k + r] = b.i;
-            weights[t * k + r] = score[b.i];
+            sel_i[r] = b.i;
+            sel_v[r] = score[b.i];
             corr[b.i] = __builtin_nanf("");
         }
         __syncthreads();
     }
     if (threadIdx.x == 0) {
-        float* w = weights + t * k;
         if (norm) {
             float total = -0.0f;
-            for (uint32_t r = 0; r < k; ++r) total += w[r];
+            for (uint32_t r = 0; r < k; ++r) total += sel_v[r];
             total = total + 1e-20f;
-            for (uint32_t r = 0; r < k; ++r) w[r] = w[r] / total;
+            for (uint32_t r = 0; r < k; ++r) sel_v[r] = sel_v[r] / total;
         }
-        for (uint32_t r = 0; r < k; ++r) w[r] = w[r] * scaling;
+        for (uint32_t r = 0; r < k; ++r) sel_v[r] = sel_v[r] * scaling;
+    }
+    __syncthreads();
+    for (uint32_t r = threadIdx.x; r < k; r += blockDim.x) {
+        ids[t * k + r] = sel_i[r];
+        weights[t * k + r] = sel_v[r];
     }
 }
 

@@ -16,18 +16,29 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
     return v > bv || (v == bv && i < bi);
 }
 
+__device__ __forceinline__ void take_better(ArgBest& a, float ov, int oi) {
+    const bool t = (oi >= 0) & ((a.i < 0) | (ov > a.v) | ((ov == a.v) & (oi < a.i)));
+    a.v = t ? ov : a.v;
+    a.i = t ? oi : a.i;
+}
+
+// Wave-wide lexicographic argmax (value desc, index asc) over candidates with
+// i >= 0 (i = -1 is "none"), on the DPP network; every lane gets lane 63's
+// result.  All 64 lanes must be active.
+__device__ __forceinline__ ArgBest wave_argbest(ArgBest a) {
+    take_better(a, dpp_f32<DPP_ROW_SHR1, 0xF>(-INFINITY, a.v), dpp_i32<DPP_ROW_SHR1, 0xF>(-1, a.i));
+    take_better(a, dpp_f32<DPP_ROW_SHR2, 0xF>(-INFINITY, a.v), dpp_i32<DPP_ROW_SHR2, 0xF>(-1, a.i));
+    take_better(a, dpp_f32<DPP_ROW_SHR4, 0xF>(-INFINITY, a.v), dpp_i32<DPP_ROW_SHR4, 0xF>(-1, a.i));
+    take_better(a, dpp_f32<DPP_ROW_SHR8, 0xF>(-INFINITY, a.v), dpp_i32<DPP_ROW_SHR8, 0xF>(-1, a.i));
+    take_better(a, dpp_f32<DPP_ROW_BCAST15, 0xA>(-INFINITY, a.v), dpp_i32<DPP_ROW_BCAST15, 0xA>(-1, a.i));
+    take_better(a, dpp_f32<DPP_ROW_BCAST31, 0xC>(-INFINITY, a.v), dpp_i32<DPP_ROW_BCAST31, 0xC>(-1, a.i));
+    return ArgBest{lane63_f32(a.v), __builtin_amdgcn_readlane(a.i, 63)};
+}
+
 // Block-wide lexicographic argmax over candidates with i >= 0; i = -1 is "none".
 __device__ ArgBest block_argmax(ArgBest a, ArgBest* lds) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(a.v, off, 64);
-        const int oi = __shfl_xor(a.i, off, 64);
-        if (oi >= 0 && (a.i < 0 || better(ov, oi, a.v, a.i))) {
-            a.v = ov;
-            a.i = oi;
-        }
-    }
+    a = wave_argbest(a);
     if (lane == 0) lds[wave] = a;
     __syncthreads();
     ArgBest b = lds[0];
@@ -61,12 +72,19 @@ __device__ float block_max(float v, float* lds) {
     return t;
 }
 
-// Softmax top-k over one token's logits, p and taken in LDS.  renorm = 1:
-// source_qwen80_topk_router (divide by the sum, renormalise by the selected
-// sum); renorm = 0: topk_softmax_batch (multiply by 1/sum, raw probs).
+// Largest top_k the device routers select (per-token selections are staged
+// in LDS and written out once).
+constexpr uint32_t HK_TOPK_MAX = 64;
+
+// Softmax top-k over one token's logits, p in LDS, the k selections staged in
+// sel_i / sel_v (LDS, HK_TOPK_MAX each) and written to ids_out / w_out at the
+// end.  renorm = 1: source_qwen80_topk_router (divide by the sum, renormalise
+// by the selected sum); renorm = 0: topk_softmax_batch (multiply by 1/sum,
+// raw probs).
 __device__ void softmax_topk_block(const float* __restrict__ logits, uint32_t n, uint32_t k,
                                    float tie_eps, int renorm, float* p, int32_t* ids_out,
-                                   float* w_out, uint32_t* status, float* redf, ArgBest* reda) {
+                                   float* w_out, uint32_t* status, float* redf, ArgBest* reda,
+                                   int32_t* sel_i, float* sel_v) {
     float m = -INFINITY;
     uint32_t bad = 0;
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
@@ -100,8 +118,8 @@ __device__ void softmax_topk_block(const float* __restrict__ logits, uint32_t n,
                         bv = v;
                     }
                 }
-                ids_out[r] = (int32_t)bi;
-                w_out[r] = bv;
+                sel_i[r] = (int32_t)bi;
+                sel_v[r] = bv;
                 p[bi] = -INFINITY;
             }
         }
@@ -117,8 +135,8 @@ __device__ void softmax_topk_block(const float* __restrict__ logits, uint32_t n,
             }
             const ArgBest b = block_argmax(a, reda);
             if (threadIdx.x == 0) {
-                ids_out[r] = b.i;
-                w_out[r] = b.v;
+                sel_i[r] = b.i;
+                sel_v[r] = b.v;
                 if (b.i >= 0) p[b.i] = -INFINITY;
             }
             __syncthreads();
@@ -127,10 +145,113 @@ __device__ void softmax_topk_block(const float* __restrict__ logits, uint32_t n,
     __syncthreads();
     if (threadIdx.x == 0 && renorm) {
         float sel = -0.0f;
-        for (uint32_t r = 0; r < k; ++r) sel += w_out[r];
-        for (uint32_t r = 0; r < k; ++r) w_out[r] = w_out[r] / sel;
+        for (uint32_t r = 0; r < k; ++r) sel += sel_v[r];
+        for (uint32_t r = 0; r < k; ++r) sel_v[r] = sel_v[r] / sel;
     }
     __syncthreads();
+    for (uint32_t r = threadIdx.x; r < k; r += blockDim.x) {
+        ids_out[r] = sel_i[r];
+        w_out[r] = sel_v[r];
+    }
+}
+
+// Selection key of a softmax probability p >= 0 at index i: high word =
+// bits(p) + 1 (non-negative floats order like their bit patterns), low word =
+// ~i (the lower index wins a tie), so the (value desc, index asc) order is
+// the unsigned order of the keys; 0 = taken / absent.
+__device__ __forceinline__ uint64_t prob_key(float p, uint32_t i) {
+    return ((uint64_t)(__builtin_bit_cast(uint32_t, p) + 1u) << 32) | (uint64_t)(~i);
+}
+
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+    const int lo = dpp_i32<CTRL, ROW_MASK>(0, (int)(uint32_t)v);
+    const int hi = dpp_i32<CTRL, ROW_MASK>(0, (int)(uint32_t)(v >> 32));
+    return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+
+// Wave-wide max of 64-bit keys on the DPP network; every lane gets it.
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
+    k = umax64(k, dpp_u64<DPP_ROW_SHR1, 0xF>(k));
+    k = umax64(k, dpp_u64<DPP_ROW_SHR2, 0xF>(k));
+    k = umax64(k, dpp_u64<DPP_ROW_SHR4, 0xF>(k));
+    k = umax64(k, dpp_u64<DPP_ROW_SHR8, 0xF>(k));
+    k = umax64(k, dpp_u64<DPP_ROW_BCAST15, 0xA>(k));
+    k = umax64(k, dpp_u64<DPP_ROW_BCAST31, 0xC>(k));
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), 63);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// The tie_eps == 0 selection of softmax_topk_block for one wave (blockDim 64,
+// n <= 64 * NPL) without barriers or LDS: lane l holds the keys of
+// p[l + 64 j] in registers, a round takes the wave-wide max key on the DPP
+// network and only the lane that owned the winner recomputes its best.  Same
+// result as the block form for finite logits.  Returns, in lane r < k, the
+// r-th selection (id, weight); ids_out / w_out get all k.
+template <int NPL>
+__device__ ArgBest softmax_topk_wave(const float* __restrict__ logits, uint32_t n, uint32_t k, int renorm,
+                                     int32_t* ids_out, float* w_out, uint32_t* status) {
+    const int lane = threadIdx.x & 63;
+    float p[NPL];
+    float m = -INFINITY;
+    uint32_t bad = 0;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+        const uint32_t i = (uint32_t)lane + 64u * j;
+        p[j] = i < n ? logits[i] : -INFINITY;
+        if (i < n && !isfinite(p[j])) bad = 1;
+        m = fmaxf(m, p[j]);
+    }
+    if (bad && status) atomicOr(status, HK_DEVERR_NONFINITE);
+    m = wave_max(m);
+    float local = 0.f;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+        if ((uint32_t)lane + 64u * j < n) {
+            p[j] = expf(p[j] - m);
+            local += p[j];
+        }
+    }
+    const float sum = wave_sum(local);
+    const float inv = 1.0f / sum;
+    uint64_t key[NPL];
+    uint64_t best = 0;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+        const uint32_t i = (uint32_t)lane + 64u * j;
+        key[j] = i < n ? prob_key(renorm ? p[j] / sum : p[j] * inv, i) : 0ull;
+        best = umax64(best, key[j]);
+    }
+    ArgBest mine{0.0f, -1};
+    for (uint32_t r = 0; r < k; ++r) {
+        const uint64_t w = wave_max_key(best);
+        const uint32_t wi = ~(uint32_t)w;
+        if ((uint32_t)lane == r) {
+            mine.i = w ? (int)wi : -1;
+            mine.v = __builtin_bit_cast(float, (uint32_t)(w >> 32) - 1u);
+        }
+        if (w && (wi & 63u) == (uint32_t)lane) {
+            best = 0;
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) {
+                key[j] = key[j] == w ? 0ull : key[j];
+                best = umax64(best, key[j]);
+            }
+        }
+    }
+    if (renorm) {
+        float sel = -0.0f;
+        for (uint32_t r = 0; r < k; ++r) sel += __shfl(mine.v, (int)r, 64);
+        mine.v = mine.v / sel;
+    }
+    if ((uint32_t)lane < k) {
+        ids_out[lane] = mine.i;
+        w_out[lane] = mine.v;
+    }
+    return mine;
 }
 
 }  // namespace hk

@@ -189,13 +189,15 @@ int hk_organ_synthetic(hk_ctx* ctx, int32_t kind, int32_t group, uint32_t rows, 
  * by the selected sum.  ids/weights stay on the device.
  * source_qwen80_topk_router (model/qwen80_complete_runtime.rs:5970-6025),
  * moe_topk_gate (shaders/moe.metal:118-305, kernels/mod.rs:12721-12790).
- * renorm = 0 gives topk_softmax_batch (kernels/mod.rs:342-374). */
+ * renorm = 0 gives topk_softmax_batch (kernels/mod.rs:342-374).
+ * Limits: n_experts <= 8192, top_k <= 64 (HK_E_UNSUPPORTED beyond). */
 int hk_router_softmax_topk(hk_ctx* ctx, const float* logits, uint32_t n_tokens,
                            uint32_t n_experts, uint32_t top_k, float tie_eps, int renorm,
                            int32_t* ids, float* weights, hk_stream stream);
 /* noaux_tc (gravity_glm.rs:447-500): select on sigmoid(logit)+bias inside the
  * top topk_group groups (group score = sum of its best two), weight with the
- * uncorrected sigmoid, optional renorm (+1e-20), times routed_scaling_factor. */
+ * uncorrected sigmoid, optional renorm (+1e-20), times routed_scaling_factor.
+ * Limits: n_experts <= 8192, top_k <= 64. */
 int hk_router_noaux_tc(hk_ctx* ctx, const float* logits, const float* bias, uint32_t n_tokens,
                        uint32_t n_experts, uint32_t n_group, uint32_t topk_group, uint32_t top_k,
                        int norm_topk_prob, float routed_scaling_factor, int32_t* ids,

@@ -92,9 +92,13 @@ def test_noaux_tc_matches_oracle(ctx, oracle):
 def test_router_rejects_bad_geometry(ctx):
     from hawking_amd._lib import HK_E_INVALID_ARG, HawkingError
     from hawking_amd.moe import topk_router
+    from hawking_amd._lib import HK_E_UNSUPPORTED
     with pytest.raises(HawkingError) as e:
         topk_router(ctx, np.zeros(8, np.float32), 9)
     assert e.value.code == HK_E_INVALID_ARG
+    with pytest.raises(HawkingError) as e:
+        topk_router(ctx, np.zeros(128, np.float32), 65)
+    assert e.value.code == HK_E_UNSUPPORTED
 
 
 def test_router_flags_nonfinite_logits(ctx):
@@ -161,6 +165,66 @@ def test_synthetic_layer_matches_oracle_regeneration(ctx, oracle, kind):
             o = U.oracle_organ(oracle, U.SEED, shape, layer, e, 0)
             want = (o.scales.nbytes + o.codes.nbytes) if kind == U.HK_Q4 else o.mixed.nbytes()
             assert m.expert_bytes(layer, e) >= want
+
+
+VARIANTS = [
+    # (label, kind, group, inter, shared_inter, shared_gate)
+    ("q4-g64-wide-shared", U.HK_Q4, 64, 128, 256, True),
+    ("q4-g128-no-shared", U.HK_Q4, 128, 256, 0, False),
+    ("mixed-shared-no-gate", U.HK_MIXED, 128, 256, 256, False),
+    ("mixed-inter384-narrow-shared", U.HK_MIXED, 128, 384, 128, True),
+]
+
+
+@pytest.mark.parametrize("label,kind,group,inter,shared_inter,shared_gate", VARIANTS)
+def test_synthetic_layer_variants(ctx, oracle, label, kind, group, inter, shared_inter, shared_gate):
+    """Group sizes, no shared expert, a shared expert of another width, an
+    ungated shared expert, and an intermediate that is not a whole number of
+    512-column steps."""
+    from hawking_amd.moe import MoeModel, MoeShape
+    shape = MoeShape(n_layers=1, hidden=512, inter=inter, shared_inter=shared_inter, n_experts=32, top_k=5,
+                     expert_kind=kind, expert_group=group, shared_gate=shared_gate)
+    say("layer variant", label)
+    m = MoeModel(ctx, shape)
+    m.fill_synthetic(U.SEED + 7)
+    ctx.device_status()  # clear
+    checked = 0
+    for trial in range(3):
+        h = oracle.normal(oracle.stream_key(U.SEED, 0xBEEF + trial), 512, 1.0)
+        out, ids, w = m.moe_suffix(0, h)
+        L, rout, rids, rw, logits = U.oracle_layer(oracle, U.SEED + 7, shape, 0, h)
+        if not U.router_margin_ok(logits, shape.top_k):
+            continue
+        checked += 1
+        assert ids.tolist() == rids.tolist()
+        assert np.max(np.abs(w - rw)) <= 1e-6
+        assert oracle.relative_l2(out, rout) < TOL
+        assert oracle.relative_l2(out, L.forward_f64(h, ids)) < TOL
+    assert checked >= 1
+    assert ctx.device_status() == 0
+
+
+def test_layer_flags_nonfinite_hidden_state(ctx, oracle):
+    """A NaN in h is latched in the device status word; every kernel still
+    ends normally and the next clean call is exact again."""
+    from hawking_amd.moe import MoeModel, MoeShape
+    shape = MoeShape(n_layers=1, hidden=256, inter=128, shared_inter=128, n_experts=16, top_k=4,
+                     expert_kind=U.HK_Q4, expert_group=32)
+    say("non-finite hidden state")
+    m = MoeModel(ctx, shape)
+    m.fill_synthetic(U.SEED)
+    ctx.device_status()  # clear
+    h = np.ones(256, np.float32)
+    h[3] = np.nan
+    m.moe_suffix(0, h)
+    assert ctx.device_status() != 0
+    h = oracle.normal(oracle.stream_key(U.SEED, 0xAB), 256, 1.0)
+    out, ids, w = m.moe_suffix(0, h)
+    L, rout, rids, rw, logits = U.oracle_layer(oracle, U.SEED, shape, 0, h)
+    assert ctx.device_status() == 0
+    if U.router_margin_ok(logits, shape.top_k):
+        assert ids.tolist() == rids.tolist()
+    assert oracle.relative_l2(out, L.forward_f64(h, ids)) < TOL
 
 
 def test_config3_qwen3next_layer_full_size(ctx, oracle):
