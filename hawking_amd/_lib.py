@@ -21,6 +21,7 @@ HK_E_ROUTE = 6
 HK_E_NOMEM = 7
 
 HK_Q4, HK_BIN, HK_MIXED, HK_F32 = 0, 1, 2, 3
+HK_ROUTER_SOFTMAX, HK_ROUTER_NOAUX_TC = 0, 1
 
 STATUS_NAMES = {
     HK_OK: "HK_OK", HK_E_INVALID_ARG: "HK_E_INVALID_ARG", HK_E_GEOMETRY: "HK_E_GEOMETRY",
@@ -47,13 +48,15 @@ class MoeConfig(C.Structure):
     _fields_ = [
         ("n_layers", _u32), ("hidden", _u32), ("inter", _u32), ("shared_inter", _u32),
         ("n_experts", _u32), ("top_k", _u32), ("expert_kind", _i32), ("expert_group", _i32),
-        ("shared_gate", _i32), ("eps", C.c_float),
+        ("shared_gate", _i32), ("eps", C.c_float), ("router", _i32), ("n_group", _u32), ("topk_group", _u32),
+        ("norm_topk_prob", _i32), ("routed_scaling_factor", C.c_float),
     ]
 
 
 class MoeLayerSrc(C.Structure):
     _fields_ = [
         ("norm_w", _p), ("router_w", _p), ("shared_gate_w", _p), ("experts", _p), ("shared", _p),
+        ("router_bias", _p),
     ]
 
 
@@ -107,6 +110,7 @@ PROTOTYPES = {
     "hk_moe_expert_bytes": (C.c_int, [_p, _u32, _u32, C.POINTER(_sz)]),
     "hk_moe_decode_layer": (C.c_int, [_p, _p, _u32, _p, _p, _p, _p, _p]),
     "hk_moe_decode_stack": (C.c_int, [_p, _p, _p, _p, _p, _p, _p]),
+    "hk_moe_forward_batch": (C.c_int, [_p, _p, _u32, _p, _u32, _p, _p, _p, _p]),
 }
 
 _lib: C.CDLL | None = None

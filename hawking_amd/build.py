@@ -27,7 +27,8 @@ CFLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{os.path.join(ROOT, 'include')}",
 ]
-SOURCES = ["hk_api.cpp", "hk_gemv2.hip", "hk_repack.hip", "hk_pack.hip", "hk_router.hip", "hk_moe.hip"]
+SOURCES = ["hk_api.cpp", "hk_gemv2.hip", "hk_repack.hip", "hk_pack.hip", "hk_router.hip", "hk_moe.hip",
+           "hk_moe_batch.hip"]
 
 
 def _compile(src: str) -> str:

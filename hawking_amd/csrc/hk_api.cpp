@@ -751,8 +751,8 @@ extern "C" int hk_router_noaux_tc(hk_ctx* ctx, const float* logits, const float*
 
 namespace {
 
-constexpr uint32_t PROJ_NORM = 16, PROJ_ROUTER = 17, PROJ_SHARED_GATE = 18, PROJ_COIN = 32;
-constexpr float SIGMA_W = 0.02f, SIGMA_NORM = 0.02f;
+constexpr uint32_t PROJ_NORM = 16, PROJ_ROUTER = 17, PROJ_SHARED_GATE = 18, PROJ_BIAS = 19, PROJ_COIN = 32;
+constexpr float SIGMA_W = 0.02f, SIGMA_NORM = 0.02f, SIGMA_BIAS = 0.01f;
 constexpr size_t MOE_LDS_LIMIT = 64 * 1024;
 constexpr uint32_t MOE_MAX_SLOTS = 16;
 
@@ -765,6 +765,7 @@ struct MoeLayerHost {
     float* norm_w = nullptr;
     float* router_w = nullptr;
     float* gate_w = nullptr;
+    float* bias = nullptr;
     bool ready = false;
 };
 
@@ -779,10 +780,16 @@ struct hk_moe_model {
     void* tables = nullptr;  // device expert tables of all layers
     hk::MoeWs ws{};
     float* hbuf[2] = {nullptr, nullptr};
+    // batched (noaux_tc) workspace, grown on demand to bws_tokens tokens
+    void* bws_mem = nullptr;
+    uint32_t bws_tokens = 0;
+    hk::MoeBatchWs bws{};
 };
 
+// Per layer: norm weight [H], router [E x H], shared-expert gate [H], router bias [E].
 static size_t dense_per_layer(const hk_moe_config& c) {
-    return align256((size_t)c.hidden * 4) + align256((size_t)c.n_experts * c.hidden * 4) + align256((size_t)c.hidden * 4);
+    return align256((size_t)c.hidden * 4) + align256((size_t)c.n_experts * c.hidden * 4) + align256((size_t)c.hidden * 4) +
+           align256((size_t)c.n_experts * 4);
 }
 
 static void organ_shape(const hk_moe_config& c, uint32_t e, uint32_t p, uint32_t* rows, uint32_t* cols) {
@@ -812,6 +819,18 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
     if (slots > MOE_MAX_SLOTS || c.n_experts > 4096 || c.hidden > 8192 || c.hidden % 128)
         return set_error(ctx, HK_E_UNSUPPORTED,
                          "moe config: need top_k (+1 shared) <= 16, n_experts <= 4096, hidden % 128 == 0, hidden <= 8192");
+    if (c.router != HK_ROUTER_SOFTMAX && c.router != HK_ROUTER_NOAUX_TC)
+        return set_error(ctx, HK_E_UNSUPPORTED, "moe config: router must be HK_ROUTER_SOFTMAX or HK_ROUTER_NOAUX_TC");
+    if (c.router == HK_ROUTER_NOAUX_TC) {
+        if (c.n_group == 0 || c.n_group > 64 || c.n_experts % c.n_group || c.topk_group == 0 || c.topk_group > c.n_group ||
+            c.top_k > (c.n_experts / c.n_group) * c.topk_group)
+            return set_error(ctx, HK_E_INVALID_ARG, "moe config: inconsistent noaux_tc group / top-k geometry");
+        if (!std::isfinite(c.routed_scaling_factor))
+            return set_error(ctx, HK_E_INVALID_ARG, "moe config: routed_scaling_factor must be finite");
+        if (c.expert_kind != HK_Q4 || c.shared_gate || c.n_experts > hk::MOE_BATCH_MAX_EXPERTS)
+            return set_error(ctx, HK_E_UNSUPPORTED,
+                             "moe config: the noaux_tc block needs Q4 experts, no shared gate, n_experts <= 512");
+    }
     const int grp = c.expert_kind == HK_MIXED ? 128 : c.expert_group;
     int rc = validate_shape(ctx, c.expert_kind, grp, c.inter, c.hidden);
     if (!rc) rc = validate_shape(ctx, c.expert_kind, grp, c.hidden, c.inter);
@@ -819,8 +838,8 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
     if (rc) return rc;
     if (!(c.eps > 0.0f) || !std::isfinite(c.eps)) return set_error(ctx, HK_E_INVALID_ARG, "moe config: eps must be positive");
     const uint32_t imax = std::max(c.inter, c.shared_inter);
-    if (moe_gate_up_lds_bytes(c.expert_kind, c.hidden) > MOE_LDS_LIMIT ||
-        moe_down_lds_bytes(c.expert_kind, imax, slots) > MOE_LDS_LIMIT)
+    if (c.router == HK_ROUTER_SOFTMAX && (moe_gate_up_lds_bytes(c.expert_kind, c.hidden) > MOE_LDS_LIMIT ||
+                                          moe_down_lds_bytes(c.expert_kind, imax, slots) > MOE_LDS_LIMIT))
         return set_error(ctx, HK_E_UNSUPPORTED, "moe config: x images of hidden / intermediate exceed 64 KiB of LDS");
     hk_moe_model* m = new hk_moe_model();
     m->cfg = c;
@@ -855,6 +874,7 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
         L.norm_w = reinterpret_cast<float*>(d);
         L.router_w = reinterpret_cast<float*>(d + align256((size_t)c.hidden * 4));
         L.gate_w = reinterpret_cast<float*>(d + align256((size_t)c.hidden * 4) + align256((size_t)c.n_experts * c.hidden * 4));
+        L.bias = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(L.gate_w) + align256((size_t)c.hidden * 4));
         L.table_dev = reinterpret_cast<OrganView*>(static_cast<uint8_t*>(m->tables) + l * tab);
         L.table.assign((size_t)(c.n_experts + 1) * 3, OrganView{});
         L.packed.assign((size_t)(c.n_experts + 1) * 3, 0);
@@ -894,6 +914,7 @@ extern "C" int hk_moe_model_free(hk_ctx* ctx, hk_moe_model* m) {
     (void)hipFree(m->dense);
     (void)hipFree(m->tables);
     (void)hipFree(m->ws_mem);
+    if (m->bws_mem) (void)hipFree(m->bws_mem);
     delete m;
     return HK_OK;
 }
@@ -958,7 +979,7 @@ extern "C" int hk_moe_model_set_layer(hk_ctx* ctx, hk_moe_model* m, uint32_t lay
     const hk_moe_config& c = m->cfg;
     if (layer >= c.n_layers) return set_error(ctx, HK_E_INVALID_ARG, "layer index out of range");
     if (!src->norm_w || !src->router_w || !src->experts || (c.shared_inter && !src->shared) ||
-        (c.shared_gate && c.shared_inter && !src->shared_gate_w))
+        (c.shared_gate && c.shared_inter && !src->shared_gate_w) || (c.router == HK_ROUTER_NOAUX_TC && !src->router_bias))
         return set_error(ctx, HK_E_INVALID_ARG, "layer source: missing tensor (a missing tensor must raise, not zero-fill)");
     const uint32_t n_org = (c.n_experts + (c.shared_inter ? 1 : 0)) * 3;
     std::vector<Layout> lay(n_org);
@@ -1002,6 +1023,9 @@ extern "C" int hk_moe_model_set_layer(hk_ctx* ctx, hk_moe_model* m, uint32_t lay
     if (!rc && src->shared_gate_w)
         rc = check_hip(ctx, hipMemcpyAsync(L.gate_w, src->shared_gate_w, (size_t)c.hidden * 4, hipMemcpyHostToDevice, st),
                        "gate upload");
+    if (!rc && src->router_bias)
+        rc = check_hip(ctx, hipMemcpyAsync(L.bias, src->router_bias, (size_t)c.n_experts * 4, hipMemcpyHostToDevice, st),
+                       "router bias upload");
     if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "hipStreamSynchronize (layer upload)");
     if (rc) return rc;
     L.ready = true;
@@ -1016,7 +1040,7 @@ extern "C" int hk_moe_model_fill_synthetic(hk_ctx* ctx, hk_moe_model* m, uint64_
     const uint32_t n_org = n_exp * 3;
     void* jobs_dev = nullptr;
     void* aux = nullptr;
-    if (hipMalloc(&jobs_dev, (size_t)n_org * sizeof(SynthJob)) != hipSuccess ||
+    if (hipMalloc(&jobs_dev, (size_t)std::max(n_org, 4u) * sizeof(SynthJob)) != hipSuccess ||
         hipMalloc(&aux, (size_t)n_org * 4 + 256) != hipSuccess) {
         if (jobs_dev) (void)hipFree(jobs_dev);
         return set_error(ctx, HK_E_NOMEM, "synthetic job table allocation failed");
@@ -1032,20 +1056,21 @@ extern "C" int hk_moe_model_fill_synthetic(hk_ctx* ctx, hk_moe_model* m, uint64_
     for (uint32_t l = 0; l < c.n_layers && !rc; ++l) {
         MoeLayerHost& L = m->layers[l];
         // dense tensors
-        SynthJob dj[3] = {};
-        const uint32_t drows[3] = {1, c.n_experts, 1};
-        const uint32_t dproj[3] = {PROJ_NORM, PROJ_ROUTER, PROJ_SHARED_GATE};
-        float* dptr[3] = {L.norm_w, L.router_w, L.gate_w};
-        const float dsig[3] = {SIGMA_NORM, SIGMA_W, SIGMA_W};
-        for (int k = 0; k < 3; ++k) {
+        SynthJob dj[4] = {};
+        const uint32_t drows[4] = {1, c.n_experts, 1, 1};
+        const uint32_t dcols[4] = {c.hidden, c.hidden, c.hidden, c.n_experts};
+        const uint32_t dproj[4] = {PROJ_NORM, PROJ_ROUTER, PROJ_SHARED_GATE, PROJ_BIAS};
+        float* dptr[4] = {L.norm_w, L.router_w, L.gate_w, L.bias};
+        const float dsig[4] = {SIGMA_NORM, SIGMA_W, SIGMA_W, SIGMA_BIAS};
+        for (int k = 0; k < 4; ++k) {
             dj[k].key = hk::stream_key(seed, hk_moe_stream_id(l, 0, dproj[k]));
             dj[k].sigma = dsig[k];
             dj[k].rows = drows[k];
-            dj[k].cols = c.hidden;
+            dj[k].cols = dcols[k];
             dj[k].dense = dptr[k];
         }
         rc = check_hip(ctx, hipMemcpyAsync(jobs_dev, dj, sizeof(dj), hipMemcpyHostToDevice, st), "job upload");
-        if (!rc) rc = check_hip(ctx, launch_synth_jobs(HK_F32, static_cast<SynthJob*>(jobs_dev), 3,
+        if (!rc) rc = check_hip(ctx, launch_synth_jobs(HK_F32, static_cast<SynthJob*>(jobs_dev), 4,
                                                        (size_t)c.n_experts * c.hidden / 128 + 1, bad, st), "dense synth");
         if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "sync");
         if (rc) break;
@@ -1156,6 +1181,8 @@ static int moe_layer_dev(hk_ctx* ctx, hk_moe_model* m, uint32_t layer, MoeLayerD
 extern "C" int hk_moe_decode_layer(hk_ctx* ctx, hk_moe_model* m, uint32_t layer, const float* h_in, float* h_out,
                                    int32_t* ids, float* weights, hk_stream stream) {
     if (!ctx || !m) return HK_E_INVALID_ARG;
+    if (m->cfg.router != HK_ROUTER_SOFTMAX)
+        return set_error(ctx, HK_E_UNSUPPORTED, "moe layer: the decode path routes with HK_ROUTER_SOFTMAX");
     if (!h_in || !h_out || h_in == h_out) return set_error(ctx, HK_E_INVALID_ARG, "moe layer: h_in/h_out NULL or aliased");
     if (!aligned16(h_in) || !aligned16(h_out)) return set_error(ctx, HK_E_INVALID_ARG, "moe layer: h_in/h_out must be 16-byte aligned");
     MoeLayerDev L;
@@ -1169,6 +1196,8 @@ extern "C" int hk_moe_decode_layer(hk_ctx* ctx, hk_moe_model* m, uint32_t layer,
 extern "C" int hk_moe_decode_stack(hk_ctx* ctx, hk_moe_model* m, const float* h_in, float* h_out, int32_t* ids,
                                    float* weights, hk_stream stream) {
     if (!ctx || !m) return HK_E_INVALID_ARG;
+    if (m->cfg.router != HK_ROUTER_SOFTMAX)
+        return set_error(ctx, HK_E_UNSUPPORTED, "moe stack: the decode path routes with HK_ROUTER_SOFTMAX");
     if (!h_in || !h_out) return set_error(ctx, HK_E_INVALID_ARG, "moe stack: NULL h_in/h_out");
     if (!aligned16(h_in) || !aligned16(h_out)) return set_error(ctx, HK_E_INVALID_ARG, "moe stack: h_in/h_out must be 16-byte aligned");
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -1189,4 +1218,99 @@ extern "C" int hk_moe_decode_stack(hk_ctx* ctx, hk_moe_model* m, const float* h_
         cur = dst;
     }
     return HK_OK;
+}
+
+// Grows the batched workspace to hold `T` tokens (synchronising the device
+// before freeing a smaller one).
+static int ensure_batch_ws(hk_ctx* ctx, hk_moe_model* m, uint32_t T) {
+    if (m->bws_mem && m->bws_tokens >= T) return HK_OK;
+    const hk_moe_config& c = m->cfg;
+    T = std::max(T, std::min(32u, hk::MOE_BATCH_MAX_TOKENS));
+    const uint32_t imax = std::max(c.inter, c.shared_inter), K = c.top_k, E = c.n_experts;
+    const uint32_t S = (c.hidden + hk::MOE_BATCH_ROUTER_COLS - 1) / hk::MOE_BATCH_ROUTER_COLS;
+    const size_t pairs = (size_t)T * K + (c.shared_inter ? T : 0);
+    const size_t xs = align256(moe_batch_img_bytes(c.hidden)), as = align256(moe_batch_img_bytes(imax));
+    const size_t sz[] = {
+        (size_t)T * c.hidden * 4,          // x32
+        (size_t)T * xs,                    // ximg
+        (size_t)T * 4,                     // ximg_e
+        (size_t)S * T * E * 4,             // part
+        (size_t)T * K * 4,                 // ids
+        (size_t)T * K * 4,                 // w
+        (size_t)T * K * 4,                 // order
+        ((size_t)E + 1) * 16,              // active
+        4,                                 // n_active
+        pairs * 4,                         // members
+        pairs * imax * 4,                  // act
+        pairs * as,                        // aimg
+        pairs * 4,                         // aimg_e
+        pairs * c.hidden * 4,              // ybuf
+    };
+    size_t total = 0;
+    for (size_t b : sz) total += align256(b);
+    if (m->bws_mem) {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(m->bws_mem);
+        m->bws_mem = nullptr;
+        m->bws_tokens = 0;
+    }
+    if (hipMalloc(&m->bws_mem, total) != hipSuccess) return set_error(ctx, HK_E_NOMEM, "batched MoE workspace allocation failed");
+    uint8_t* p = static_cast<uint8_t*>(m->bws_mem);
+    void* ptr[sizeof(sz) / sizeof(sz[0])];
+    for (size_t i = 0; i < sizeof(sz) / sizeof(sz[0]); ++i) {
+        ptr[i] = p;
+        p += align256(sz[i]);
+    }
+    hk::MoeBatchWs& w = m->bws;
+    w.x32 = static_cast<float*>(ptr[0]);
+    w.ximg = static_cast<uint8_t*>(ptr[1]);
+    w.ximg_e = static_cast<int32_t*>(ptr[2]);
+    w.part = static_cast<float*>(ptr[3]);
+    w.ids = static_cast<int32_t*>(ptr[4]);
+    w.w = static_cast<float*>(ptr[5]);
+    w.order = static_cast<int32_t*>(ptr[6]);
+    w.active = static_cast<uint4*>(ptr[7]);
+    w.n_active = static_cast<uint32_t*>(ptr[8]);
+    w.members = static_cast<uint32_t*>(ptr[9]);
+    w.act = static_cast<float*>(ptr[10]);
+    w.aimg = static_cast<uint8_t*>(ptr[11]);
+    w.aimg_e = static_cast<int32_t*>(ptr[12]);
+    w.ybuf = static_cast<float*>(ptr[13]);
+    w.ximg_stride = (uint32_t)xs;
+    w.aimg_stride = (uint32_t)as;
+    w.status = ctx->dev_status;
+    m->bws_tokens = T;
+    return HK_OK;
+}
+
+extern "C" int hk_moe_forward_batch(hk_ctx* ctx, hk_moe_model* m, uint32_t layer, const uint16_t* x_bf16,
+                                    uint32_t n_tokens, float* y, int32_t* ids, float* weights, hk_stream stream) {
+    if (!ctx || !m) return HK_E_INVALID_ARG;
+    const hk_moe_config& c = m->cfg;
+    if (c.router != HK_ROUTER_NOAUX_TC)
+        return set_error(ctx, HK_E_UNSUPPORTED, "moe batch: the batched block routes with HK_ROUTER_NOAUX_TC");
+    if (n_tokens == 0 || n_tokens > hk::MOE_BATCH_MAX_TOKENS)
+        return set_error(ctx, HK_E_INVALID_ARG, "moe batch: n_tokens must be in [1, 64]");
+    if (!x_bf16 || !y || !aligned16(y)) return set_error(ctx, HK_E_INVALID_ARG, "moe batch: NULL x/y or misaligned y");
+    MoeLayerDev L;
+    int rc = moe_layer_dev(ctx, m, layer, &L);
+    if (rc) return rc;
+    if ((rc = ensure_batch_ws(ctx, m, n_tokens))) return rc;
+    hk::MoeBatchDims d{};
+    d.T = n_tokens;
+    d.H = c.hidden;
+    d.I = c.inter;
+    d.SI = c.shared_inter;
+    d.Imax = std::max(c.inter, c.shared_inter);
+    d.E = c.n_experts;
+    d.K = c.top_k;
+    d.n_group = c.n_group;
+    d.topk_group = c.topk_group;
+    d.norm_topk_prob = c.norm_topk_prob;
+    d.scaling = c.routed_scaling_factor;
+    d.S = (c.hidden + hk::MOE_BATCH_ROUTER_COLS - 1) / hk::MOE_BATCH_ROUTER_COLS;
+    return check_hip(ctx,
+                     launch_moe_batch(d, L, m->layers[layer].bias, x_bf16, y, m->bws, ids, weights,
+                                      static_cast<hipStream_t>(stream)),
+                     "moe batch launch");
 }

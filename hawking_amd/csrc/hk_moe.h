@@ -47,4 +47,47 @@ size_t moe_gate_up_lds_bytes(int kind, uint32_t H);
 hipError_t launch_moe_layer(int kind, const MoeDims& d, const MoeLayerDev& L, const float* h_in,
                             float* h_out, const MoeWs& ws, int32_t* ids_out, float* w_out, hipStream_t s);
 
+// ------------------------------------------------------------------ batched (noaux_tc) block
+
+constexpr uint32_t MOE_BATCH_MAX_TOKENS = 64;
+constexpr uint32_t MOE_BATCH_MAX_EXPERTS = 512;
+constexpr uint32_t MOE_BATCH_ROUTER_COLS = 1024;  // router columns per split-K workgroup
+
+struct MoeBatchDims {
+    uint32_t T;         // tokens
+    uint32_t H, I, SI;  // hidden, routed / shared intermediate (SI 0 = none)
+    uint32_t Imax;
+    uint32_t E, K;
+    uint32_t n_group, topk_group;
+    int32_t norm_topk_prob;
+    float scaling;
+    uint32_t S;         // router split-K partials
+};
+
+// A routed (token, slot) pair is p = t*K + r; the shared expert's pair for
+// token t is T*K + t.  active[a] = {expert, first member, members}; entry 0 is
+// the shared expert (if any), then the routed experts in ascending id.
+struct MoeBatchWs {
+    float* x32;          // [T x H]
+    uint8_t* ximg;       // [T] x images of x (stride ximg_stride)
+    int32_t* ximg_e;     // [T]
+    float* part;         // [S x T x E] router partials
+    int32_t* ids;        // [T x K] route order
+    float* w;            // [T x K]
+    int32_t* order;      // [T x K] slots of each token in ascending expert id
+    uint4* active;       // [E + 1]
+    uint32_t* n_active;  // [1]
+    uint32_t* members;   // [T*K + T] pair ids, grouped by active expert
+    float* act;          // [pairs x Imax]
+    uint8_t* aimg;       // [pairs] x images of the activations (stride aimg_stride)
+    int32_t* aimg_e;     // [pairs]
+    float* ybuf;         // [pairs x H] weighted expert outputs
+    uint32_t ximg_stride, aimg_stride;
+    uint32_t* status;
+};
+
+size_t moe_batch_img_bytes(uint32_t cols);  // Q4 x image of `cols` columns
+hipError_t launch_moe_batch(const MoeBatchDims& d, const MoeLayerDev& L, const float* bias, const uint16_t* x_bf16,
+                            float* y, const MoeBatchWs& ws, int32_t* ids_out, float* w_out, hipStream_t s);
+
 }  // namespace hk

@@ -79,6 +79,21 @@ class MoeShape:
     expert_group: int = 32
     shared_gate: bool = True
     eps: float = 1e-6
+    router: int = 0             # HK_ROUTER_SOFTMAX (decode path) or HK_ROUTER_NOAUX_TC (batched block)
+    n_group: int = 1            # noaux_tc
+    topk_group: int = 1
+    norm_topk_prob: bool = True
+    routed_scaling_factor: float = 1.0
+
+    @classmethod
+    def deepseek_v3(cls, n_layers=1, n_group=1, topk_group=1, **kw):
+        """The DeepSeek-V3-shaped batched block: hidden 7168, 256 experts x 2048
+        (Q4 G32) + 1 shared, top-8 noaux_tc (norm, x2.5)."""
+        base = dict(n_layers=n_layers, hidden=7168, inter=2048, shared_inter=2048, n_experts=256, top_k=8,
+                    expert_kind=HK_Q4, expert_group=32, shared_gate=False, router=1, n_group=n_group,
+                    topk_group=topk_group, norm_topk_prob=True, routed_scaling_factor=2.5)
+        base.update(kw)
+        return cls(**base)
 
 
 class MoeModel:
@@ -88,7 +103,9 @@ class MoeModel:
     def __init__(self, ctx: Context, shape: MoeShape):
         self.ctx, self.shape = ctx, shape
         cfg = MoeConfig(shape.n_layers, shape.hidden, shape.inter, shape.shared_inter, shape.n_experts,
-                        shape.top_k, shape.expert_kind, shape.expert_group, int(shape.shared_gate), shape.eps)
+                        shape.top_k, shape.expert_kind, shape.expert_group, int(shape.shared_gate), shape.eps,
+                        shape.router, shape.n_group, shape.topk_group, int(shape.norm_topk_prob),
+                        shape.routed_scaling_factor)
         h = C.c_void_p()
         ctx.call("hk_moe_model_create", C.byref(cfg), C.byref(h))
         self.h = h
@@ -107,7 +124,8 @@ class MoeModel:
     def fill_synthetic(self, seed: int) -> None:
         self.ctx.call("hk_moe_model_fill_synthetic", self.h, seed, self.ctx.stream)
 
-    def set_layer(self, layer: int, norm_w, router_w, experts, shared=None, shared_gate_w=None) -> None:
+    def set_layer(self, layer: int, norm_w, router_w, experts, shared=None, shared_gate_w=None,
+                  router_bias=None) -> None:
         """experts: list over expert id of (gate, up, down) canonical organ dicts
         (see organ_src); shared likewise or None."""
         keep = []
@@ -138,7 +156,8 @@ class MoeModel:
             sh = (OrganSrc * 3)(*[src(d) for d in shared])
         L = MoeLayerSrc(arr(norm_w, np.float32), arr(router_w, np.float32),
                         arr(shared_gate_w, np.float32) if shared_gate_w is not None else None,
-                        C.cast(ex, C.c_void_p), C.cast(sh, C.c_void_p) if sh is not None else None)
+                        C.cast(ex, C.c_void_p), C.cast(sh, C.c_void_p) if sh is not None else None,
+                        arr(router_bias, np.float32) if router_bias is not None else None)
         self.ctx.call("hk_moe_model_set_layer", self.h, layer, C.byref(L), self.ctx.stream)
 
     def expert_bytes(self, layer: int, expert: int) -> int:
@@ -184,3 +203,22 @@ class MoeModel:
         self.decode_stack_device(hd, out, ids, w)
         return (out.download(), ids.download().reshape(s.n_layers, s.top_k),
                 w.download().reshape(s.n_layers, s.top_k))
+
+    # -- batched noaux_tc block ------------------------------------------------------
+    def forward_batch_device(self, layer: int, x_bf16: DeviceArray, n_tokens: int, y: DeviceArray,
+                             ids: DeviceArray | None = None, weights: DeviceArray | None = None, stream=None) -> None:
+        self.ctx.call("hk_moe_forward_batch", self.h, layer, _pp(x_bf16), n_tokens, _pp(y), _pp(ids), _pp(weights),
+                      stream if stream is not None else self.ctx.stream)
+
+    def routed_moe(self, layer: int, x_bf16: np.ndarray):
+        """routed_moe for a batch: x_bf16 uint16 [T, hidden] (bf16 bits).
+        Returns (y [T, hidden] f32, ids [T, top_k], weights [T, top_k])."""
+        s = self.shape
+        x_bf16 = np.ascontiguousarray(x_bf16, np.uint16)
+        T = x_bf16.shape[0]
+        xd = self.ctx.to_device(x_bf16)
+        y = self.ctx.empty((T, s.hidden))
+        ids = self.ctx.empty((T, s.top_k), np.int32)
+        w = self.ctx.empty((T, s.top_k), np.float32)
+        self.forward_batch_device(layer, xd, T, y, ids, w)
+        return y.download(), ids.download(), w.download()

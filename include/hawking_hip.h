@@ -205,6 +205,10 @@ int hk_router_noaux_tc(hk_ctx* ctx, const float* logits, const float* bias, uint
 
 /* ------------------------------------------------------------------ MoE step */
 
+/* Router kinds of an MoE model. */
+#define HK_ROUTER_SOFTMAX 0  /* softmax, top-k, renormalise (source_qwen80_topk_router) */
+#define HK_ROUTER_NOAUX_TC 1 /* sigmoid + bias, group-limited top-k (gravity_glm.rs:447-500) */
+
 typedef struct hk_moe_config {
     uint32_t n_layers;
     uint32_t hidden;
@@ -216,16 +220,22 @@ typedef struct hk_moe_config {
     int32_t expert_group;    /* Q4 group (32/64/128); 128 for mixed */
     int32_t shared_gate;     /* 1 = sigmoid(wg . xn) gate on the shared expert */
     float eps;               /* RMSNorm epsilon */
+    int32_t router;          /* HK_ROUTER_SOFTMAX (decode path) or HK_ROUTER_NOAUX_TC (batched path) */
+    uint32_t n_group;        /* noaux_tc: expert groups (n_experts % n_group == 0) */
+    uint32_t topk_group;     /* noaux_tc: groups kept */
+    int32_t norm_topk_prob;  /* noaux_tc: renormalise the selected scores (+1e-20) */
+    float routed_scaling_factor; /* noaux_tc: factor on the routed weights */
 } hk_moe_config;
 
 /* Host-side canonical weights of one layer (HOST pointers).
  * experts: n_experts*3 organ sources (gate, up, down per expert). */
 typedef struct hk_moe_layer_src {
-    const float* norm_w;         /* [hidden], applied as (1 + w) */
+    const float* norm_w;         /* [hidden], applied as (1 + w) (decode path) */
     const float* router_w;       /* [n_experts x hidden] f32 */
     const float* shared_gate_w;  /* [hidden] or NULL */
     const hk_organ_src* experts; /* [n_experts*3] */
     const hk_organ_src* shared;  /* [3] or NULL */
+    const float* router_bias;    /* [n_experts] e_score_correction_bias (noaux_tc), else NULL */
 } hk_moe_layer_src;
 
 /* Expert table + per-layer dense weights in device memory: each expert's
@@ -240,15 +250,16 @@ int hk_moe_model_set_layer(hk_ctx* ctx, hk_moe_model* model, uint32_t layer,
 int hk_moe_model_fill_synthetic(hk_ctx* ctx, hk_moe_model* model, uint64_t seed,
                                 hk_stream stream);
 /* stream id = ((layer+1) << 40) | (expert << 8) | proj; proj 0/1/2 = gate/up/down,
- * 16 = norm weight, 17 = router, 18 = shared-expert gate, 32+p = mixed coins of proj p;
- * expert n_experts = the shared expert. */
+ * 16 = norm weight, 17 = router, 18 = shared-expert gate, 19 = router bias (N(0, 0.01)),
+ * 32+p = mixed coins of proj p; expert n_experts = the shared expert. */
 uint64_t hk_moe_stream_id(uint32_t layer, uint32_t expert, uint32_t proj);
 /* Device bytes held by the model; dense (norm + router + gate) bytes read per layer. */
 int hk_moe_model_bytes(const hk_moe_model* model, size_t* device_bytes, size_t* dense_bytes_per_layer);
 /* Packed (algorithmic) bytes of one expert's gate+up+down; expert n_experts = shared. */
 int hk_moe_expert_bytes(const hk_moe_model* model, uint32_t layer, uint32_t expert, size_t* bytes);
 
-/* One moe_suffix layer at batch 1 on device data, no host round trip:
+/* One moe_suffix layer at batch 1 on device data, no host round trip
+ * (router == HK_ROUTER_SOFTMAX):
  * xn = RMSNorm(1+w)(h); logits = Wr xn; route = softmax top-k renorm;
  * out = h + sum_r w_r mlp_r(xn) (route order) + g * mlp_shared(xn).
  * (model/qwen80_uniform_q4_hybrid_decode.rs:2615-2757,
@@ -262,6 +273,19 @@ int hk_moe_decode_layer(hk_ctx* ctx, hk_moe_model* model, uint32_t layer, const 
  * attention mixers).  ids/weights may be NULL or [n_layers*top_k]. */
 int hk_moe_decode_stack(hk_ctx* ctx, hk_moe_model* model, const float* h_in, float* h_out,
                         int32_t* ids, float* weights, hk_stream stream);
+
+/* The noaux_tc MoE block for a batch of tokens (routed_moe, gravity_glm.rs:550-600,
+ * with batched_mlp :515-548): per token t, logits = Wr x_t; route = noaux_tc;
+ * y_t = sum over the routed experts in ascending id of w_e mlp_e(x_t), then
+ * + mlp_shared(x_t).  x is the block input (no norm, no residual), bf16
+ * [n_tokens x hidden] (device); y f32 [n_tokens x hidden] (device); ids/weights
+ * [n_tokens x top_k] (device, route order) may be NULL.  Each active expert's
+ * weights are streamed once for all of its tokens (grouped expert GEMM).
+ * Requires router == HK_ROUTER_NOAUX_TC, expert_kind == HK_Q4, no shared gate,
+ * n_tokens <= 64, n_experts <= 512.  The workspace for n_tokens is allocated
+ * on first use (not graph-capturable until then). */
+int hk_moe_forward_batch(hk_ctx* ctx, hk_moe_model* model, uint32_t layer, const uint16_t* x_bf16,
+                         uint32_t n_tokens, float* y, int32_t* ids, float* weights, hk_stream stream);
 
 #ifdef __cplusplus
 }

@@ -876,6 +876,96 @@ done:
     return rc;
 }
 
+/* routed_moe, src/gravity_glm.rs:550-600: the router (:447-500), the
+ * per-expert dense_mlp of batched_mlp (:503-548, experts are independent, so
+ * one at a time here), routed accumulated in ascending expert id
+ * (`order.sort_by_key(|&s| indices[s])`, then `*r += o * w`), then the shared
+ * expert added with weight 1. */
+int hko_noaux_moe_forward(const hko_noaux_moe* M, const float* x, float* out, int32_t* ids_out,
+                          float* weights_out, float* logits_out) {
+    size_t H = M->hidden, E = M->n_experts, K = M->top_k;
+    int rc = HKO_E_INVALID_ARG;
+    float* logits = (float*)malloc(E * sizeof(float));
+    float* eout = (float*)malloc(H * sizeof(float));
+    float* shared = (float*)malloc(H * sizeof(float));
+    int32_t* ids = (int32_t*)malloc(K * sizeof(int32_t));
+    float* wts = (float*)malloc(K * sizeof(float));
+    size_t* order = (size_t*)malloc(K * sizeof(size_t));
+    if (!logits || !eout || !shared || !ids || !wts || !order) goto done;
+    hko_gemv_f32(M->router_w, E, H, x, logits);
+    rc = hko_router_noaux_tc(logits, M->bias, E, M->n_group, M->topk_group, K, M->norm_topk_prob,
+                             M->routed_scaling_factor, ids, wts);
+    if (rc != HKO_OK) goto done;
+    /* stable sort of the slots by expert id (ids are distinct) */
+    for (size_t s = 0; s < K; ++s) order[s] = s;
+    for (size_t s = 1; s < K; ++s) {
+        size_t v = order[s], j = s;
+        while (j > 0 && ids[order[j - 1]] > ids[v]) {
+            order[j] = order[j - 1];
+            --j;
+        }
+        order[j] = v;
+    }
+    for (size_t i = 0; i < H; ++i) out[i] = 0.0f;
+    for (size_t s = 0; s < K; ++s) {
+        size_t slot = order[s];
+        const hko_organ* ex = M->experts + (size_t)ids[slot] * 3;
+        if ((rc = hko_mlp(&ex[0], &ex[1], &ex[2], x, NULL, eout)) != HKO_OK) goto done;
+        for (size_t i = 0; i < H; ++i) out[i] += eout[i] * wts[slot];
+    }
+    if (M->shared) {
+        if ((rc = hko_mlp(&M->shared[0], &M->shared[1], &M->shared[2], x, NULL, shared)) != HKO_OK) goto done;
+        for (size_t i = 0; i < H; ++i) out[i] += shared[i];
+    }
+    for (size_t i = 0; i < H; ++i) {
+        if (!isfinite(out[i])) {
+            rc = HKO_E_NONFINITE;
+            goto done;
+        }
+    }
+    if (ids_out) memcpy(ids_out, ids, K * sizeof(int32_t));
+    if (weights_out) memcpy(weights_out, wts, K * sizeof(float));
+    if (logits_out) memcpy(logits_out, logits, E * sizeof(float));
+    rc = HKO_OK;
+done:
+    free(logits); free(eout); free(shared); free(ids); free(wts); free(order);
+    return rc;
+}
+
+int hko_noaux_moe_forward_f64(const hko_noaux_moe* M, const double* x, const int32_t* ids, double* out) {
+    size_t H = M->hidden, E = M->n_experts, K = M->top_k;
+    int rc = HKO_E_INVALID_ARG;
+    double* eout = (double*)malloc(H * sizeof(double));
+    double* w = (double*)malloc(K * sizeof(double));
+    if (!eout || !w) goto done;
+    double total = 0.0;
+    for (size_t r = 0; r < K; ++r) {
+        if (ids[r] < 0 || (size_t)ids[r] >= E) goto done;
+        double acc = 0.0;
+        for (size_t i = 0; i < H; ++i) acc += (double)M->router_w[(size_t)ids[r] * H + i] * x[i];
+        w[r] = 1.0 / (1.0 + exp(-acc));
+        total += w[r];
+    }
+    for (size_t r = 0; r < K; ++r) {
+        if (M->norm_topk_prob) w[r] /= total + 1e-20;
+        w[r] *= (double)M->routed_scaling_factor;
+    }
+    for (size_t i = 0; i < H; ++i) out[i] = 0.0;
+    for (size_t r = 0; r < K; ++r) {
+        if ((rc = mlp_f64(M->experts + (size_t)ids[r] * 3, x, eout)) != HKO_OK) goto done;
+        for (size_t i = 0; i < H; ++i) out[i] += eout[i] * w[r];
+    }
+    if (M->shared) {
+        if ((rc = mlp_f64(M->shared, x, eout)) != HKO_OK) goto done;
+        for (size_t i = 0; i < H; ++i) out[i] += eout[i];
+    }
+    rc = HKO_OK;
+done:
+    free(eout);
+    free(w);
+    return rc;
+}
+
 /* relative_l2, src/numeric_parity.rs:323-337. */
 double hko_relative_l2_f64ref(const float* candidate, const double* reference, size_t n) {
     double num = 0.0, den = 0.0;

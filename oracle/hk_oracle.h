@@ -167,6 +167,25 @@ int hko_moe_layer_forward(const hko_moe_layer* L, const float* h, float* out,
 int hko_moe_layer_forward_f64(const hko_moe_layer* L, const double* h, const int32_t* ids,
                               const float* weights, double* out);
 
+/* ---- noaux_tc MoE block (src/gravity_glm.rs:447-600, routed_moe) ---- */
+typedef struct hko_noaux_moe {
+    size_t hidden, n_experts, top_k, n_group, topk_group;
+    int norm_topk_prob;
+    float routed_scaling_factor;
+    const float* router_w;    /* [n_experts x hidden] f32 */
+    const float* bias;        /* [n_experts] e_score_correction_bias */
+    const hko_organ* experts; /* [n_experts * 3]: gate, up, down per expert */
+    const hko_organ* shared;  /* [3] or NULL */
+} hko_noaux_moe;
+/* One token: out = sum over the routed experts in ascending id of w_e*mlp_e(x),
+ * then + mlp_shared(x) (weight 1).  x is the block input (no norm, no residual).
+ * ids/weights (top_k, route order) and logits may be NULL. */
+int hko_noaux_moe_forward(const hko_noaux_moe* M, const float* x, float* out, int32_t* ids, float* weights,
+                          float* logits);
+/* FP64 authority for one token given its route ids: sigmoid scores, renorm and
+ * scaling, every MLP and the combine in f64. */
+int hko_noaux_moe_forward_f64(const hko_noaux_moe* M, const double* x, const int32_t* ids, double* out);
+
 /* ---- numeric contract (src/numeric_parity.rs:79-118, 323-358) ---- */
 double hko_relative_l2_f32(const float* candidate, const float* reference, size_t n);
 double hko_relative_l2_f64ref(const float* candidate, const double* reference, size_t n);

@@ -77,6 +77,8 @@ def _declare(L: C.CDLL) -> None:
         "hko_mlp": (C.c_int, [_p, _p, _p, _p, _p, _p]),
         "hko_moe_layer_forward": (C.c_int, [_p, _p, _p, _p, _p, _p, _p]),
         "hko_moe_layer_forward_f64": (C.c_int, [_p, _p, _p, _p, _p]),
+        "hko_noaux_moe_forward": (C.c_int, [_p, _p, _p, _p, _p, _p]),
+        "hko_noaux_moe_forward_f64": (C.c_int, [_p, _p, _p, _p]),
         "hko_relative_l2_f32": (C.c_double, [_p, _p, _sz]),
         "hko_relative_l2_f64ref": (C.c_double, [_p, _p, _sz]),
     }
@@ -483,4 +485,56 @@ class MoeLayer:
         out = np.empty(self.hidden, np.float64)
         _check("hko_moe_layer_forward_f64",
                lib().hko_moe_layer_forward_f64(C.byref(self.c), _ptr(h), _ptr(ids), None, _ptr(out)))
+        return out
+
+
+class _NoauxMoe(C.Structure):
+    _fields_ = [
+        ("hidden", _sz), ("n_experts", _sz), ("top_k", _sz), ("n_group", _sz), ("topk_group", _sz),
+        ("norm_topk_prob", C.c_int), ("routed_scaling_factor", C.c_float),
+        ("router_w", _p), ("bias", _p), ("experts", _p), ("shared", _p),
+    ]
+
+
+class NoauxMoe:
+    """Oracle view of one noaux_tc MoE block (gravity_glm.rs routed_moe).  experts:
+    list of (gate, up, down) Organs indexed by expert id; entries may be None for
+    experts the caller knows are unused."""
+
+    def __init__(self, hidden, n_experts, top_k, n_group, topk_group, norm_topk_prob, scaling,
+                 router_w, bias, experts, shared=None):
+        self.router_w = np.ascontiguousarray(router_w, np.float32)
+        self.bias = np.ascontiguousarray(bias, np.float32)
+        self._experts, self._shared = experts, shared
+        arr = (_Organ * (n_experts * 3))()
+        for e, trip in enumerate(experts):
+            if trip is None:
+                continue
+            for j in range(3):
+                arr[e * 3 + j] = trip[j].c
+        self._arr = arr
+        sh = (_Organ * 3)(shared[0].c, shared[1].c, shared[2].c) if shared is not None else None
+        self._sh = sh
+        self.c = _NoauxMoe(hidden, n_experts, top_k, n_group, topk_group, int(norm_topk_prob), scaling,
+                           _ptr(self.router_w), _ptr(self.bias), C.cast(arr, _p),
+                           C.cast(sh, _p) if sh is not None else None)
+        self.hidden, self.n_experts, self.top_k = hidden, n_experts, top_k
+
+    def forward(self, x):
+        """Returns (out, ids, weights, logits) for one token."""
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty(self.hidden, np.float32)
+        ids = np.empty(self.top_k, np.int32)
+        wts = np.empty(self.top_k, np.float32)
+        logits = np.empty(self.n_experts, np.float32)
+        _check("hko_noaux_moe_forward",
+               lib().hko_noaux_moe_forward(C.byref(self.c), _ptr(x), _ptr(out), _ptr(ids), _ptr(wts), _ptr(logits)))
+        return out, ids, wts, logits
+
+    def forward_f64(self, x, ids):
+        x = np.ascontiguousarray(x, np.float64)
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.empty(self.hidden, np.float64)
+        _check("hko_noaux_moe_forward_f64",
+               lib().hko_noaux_moe_forward_f64(C.byref(self.c), _ptr(x), _ptr(ids), _ptr(out)))
         return out

@@ -6,7 +6,8 @@ helpers regenerate any single tensor on the host with the oracle's copy of
 the generator so that the CPU oracle runs on bit-identical inputs.
 Stream ids: ((layer+1) << 40) | (expert << 8) | proj, proj 0/1/2 =
 gate/up/down, 16 = RMSNorm weight, 17 = router, 18 = shared-expert gate,
-32+p = mixed-format coins of projection p; expert n_experts = shared expert.
+19 = router bias (noaux_tc), 32+p = mixed-format coins of projection p;
+expert n_experts = shared expert.
 """
 from __future__ import annotations
 
@@ -15,7 +16,8 @@ import numpy as np
 SEED = 0x48415752  # "HAWR"
 SIGMA_W = 0.02
 SIGMA_NORM = 0.02
-PROJ_NORM, PROJ_ROUTER, PROJ_SHARED_GATE, PROJ_COIN = 16, 17, 18, 32
+SIGMA_BIAS = 0.01
+PROJ_NORM, PROJ_ROUTER, PROJ_SHARED_GATE, PROJ_BIAS, PROJ_COIN = 16, 17, 18, 19, 32
 HK_Q4, HK_BIN, HK_MIXED, HK_F32 = 0, 1, 2, 3
 
 
@@ -91,3 +93,56 @@ def organ_dict(o) -> dict:
     m = o.mixed
     return {"kind": HK_MIXED, "rows": o.rows, "cols": o.cols, "tags": m.tags, "bin_scales": m.bin_scales,
             "bin_signs": m.bin_signs, "q2_scales": m.q2_scales, "q2_codes": m.q2_codes}
+
+
+def router_bias(oracle, seed, shape, layer):
+    return oracle.normal(oracle.stream_key(seed, stream_id(layer, 0, PROJ_BIAS)), shape.n_experts, SIGMA_BIAS)
+
+
+def to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """f32 -> bf16 bit patterns, round to nearest even (finite inputs)."""
+    b = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def noaux_margin_ok(logits, bias, n_group, topk_group, k, rel=1e-4) -> bool:
+    """Router margin rule for noaux_tc, in f64: the chosen groups and the k-th /
+    (k+1)-th candidate must be separated by >= rel * max|value|."""
+    s = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
+    c = s + bias.astype(np.float64)
+    per = c.size // n_group
+    gs = np.array([np.sort(c[g * per:(g + 1) * per])[::-1][:2].sum() for g in range(n_group)])
+    if topk_group < n_group:
+        o = np.sort(gs)[::-1]
+        if o[topk_group - 1] - o[topk_group] < rel * np.max(np.abs(o)):
+            return False
+    chosen = np.argsort(-gs, kind="stable")[:topk_group]
+    cand = np.sort(np.concatenate([c[g * per:(g + 1) * per] for g in chosen]))[::-1]
+    if k < cand.size and cand[k - 1] - cand[k] < rel * np.max(np.abs(cand)):
+        return False
+    return True
+
+
+def oracle_noaux(oracle, seed, shape, layer, x):
+    """Oracle routed_moe for one synthetic token x (f32), generating only the
+    routed experts and the shared one.  Returns (block, out, ids, weights, logits)."""
+    _, router, _ = dense(oracle, seed, shape, layer)
+    bias = router_bias(oracle, seed, shape, layer)
+    logits = oracle.gemv_f32(router, x)
+    ids, _ = oracle.router_noaux_tc(logits, bias, shape.n_group, shape.topk_group, shape.top_k,
+                                    shape.norm_topk_prob, shape.routed_scaling_factor)
+    experts = [None] * shape.n_experts
+    for e in ids.tolist():
+        experts[e] = tuple(oracle_organ(oracle, seed, shape, layer, e, p) for p in range(3))
+    shared = None
+    if shape.shared_inter:
+        shared = tuple(oracle_organ(oracle, seed, shape, layer, shape.n_experts, p) for p in range(3))
+    M = oracle.NoauxMoe(shape.hidden, shape.n_experts, shape.top_k, shape.n_group, shape.topk_group,
+                        shape.norm_topk_prob, shape.routed_scaling_factor, router, bias, experts, shared)
+    out, ids2, w, logits2 = M.forward(x)
+    assert np.array_equal(ids, ids2)
+    return M, out, ids2, w, logits2

@@ -213,3 +213,104 @@ def test_moe_layer_identical_experts_route_invariant(oracle):
     assert oracle.relative_l2(out, approx) < 1e-6
     assert oracle.relative_l2(out, ref) < 2e-6
     del e
+
+
+# ------------------------------------------------------------------ noaux_tc MoE block (routed_moe)
+
+def _small_noaux(oracle, hidden=256, inter=128, n_experts=32, top_k=4, n_group=4, topk_group=2, seed=1,
+                 norm=True, scaling=2.5, zero_experts=False, identical=False):
+    rng = np.random.default_rng(seed)
+
+    def organ(rows, cols, zero=False):
+        w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+        if zero:
+            w[:] = 0
+        return oracle.Organ.q4(w, 32)
+
+    experts, first = [], None
+    for e in range(n_experts):
+        if identical and first is not None:
+            experts.append(first)
+            continue
+        trip = tuple(organ(*s, zero=zero_experts) for s in [(inter, hidden), (inter, hidden), (hidden, inter)])
+        experts.append(trip)
+        first = first or trip
+    shared = tuple(organ(*s) for s in [(inter, hidden), (inter, hidden), (hidden, inter)])
+    router_w = (rng.standard_normal((n_experts, hidden)) * 0.02).astype(np.float32)
+    bias = (rng.standard_normal(n_experts) * 0.01).astype(np.float32)
+    m = oracle.NoauxMoe(hidden, n_experts, top_k, n_group, topk_group, norm, scaling, router_w, bias,
+                        experts, shared)
+    return m, rng, experts, shared, router_w, bias
+
+
+def _mlp(oracle, trip, x):
+    import ctypes as C
+    out = np.empty(trip[2].rows, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    rc = oracle.lib().hko_mlp(C.byref(trip[0].c), C.byref(trip[1].c), C.byref(trip[2].c), x.ctypes.data, None,
+                              out.ctypes.data)
+    assert rc == 0
+    return out
+
+
+@pytest.mark.parametrize("norm,scaling", [(True, 2.5), (False, 1.0)])
+def test_noaux_moe_vs_f64_authority(oracle, norm, scaling):
+    m, rng, *_ = _small_noaux(oracle, norm=norm, scaling=scaling)
+    for _ in range(3):
+        x = rng.standard_normal(256).astype(np.float32)
+        out, ids, w, logits = m.forward(x)
+        assert len(set(ids.tolist())) == 4
+        if norm:
+            assert abs(float(w.sum()) / scaling - 1) < 1e-5
+        assert oracle.relative_l2(out, m.forward_f64(x, ids)) < 2e-6
+
+
+def test_noaux_moe_route_is_noaux_tc_of_router_logits(oracle):
+    m, rng, experts, shared, router_w, bias = _small_noaux(oracle)
+    x = rng.standard_normal(256).astype(np.float32)
+    out, ids, w, logits = m.forward(x)
+    assert np.array_equal(logits, oracle.gemv_f32(router_w, x))
+    ids2, w2 = oracle.router_noaux_tc(logits, bias, 4, 2, 4, True, 2.5)
+    assert np.array_equal(ids, ids2) and np.array_equal(w, w2)
+
+
+def test_noaux_moe_combines_in_ascending_expert_order(oracle):
+    """routed accumulates o*w over the experts sorted by id, then adds the
+    shared output: rebuilt from per-expert MLPs in that order it is bit-exact,
+    while the route order gives a different rounding on some input."""
+    m, rng, experts, shared, *_ = _small_noaux(oracle)
+    differs = False
+    for _ in range(8):
+        x = rng.standard_normal(256).astype(np.float32)
+        out, ids, w, _ = m.forward(x)
+        outs = {int(e): _mlp(oracle, experts[int(e)], x) for e in ids}
+        asc = np.zeros(256, np.float32)
+        for s in sorted(range(4), key=lambda s: int(ids[s])):
+            asc += outs[int(ids[s])] * w[s]
+        asc += _mlp(oracle, shared, x)
+        assert np.array_equal(out, asc)
+        route = np.zeros(256, np.float32)
+        for s in range(4):
+            route += outs[int(ids[s])] * w[s]
+        route += _mlp(oracle, shared, x)
+        differs |= not np.array_equal(out, route)
+    assert differs
+
+
+def test_noaux_moe_zero_experts_is_shared_only(oracle):
+    m, rng, experts, shared, *_ = _small_noaux(oracle, zero_experts=True)
+    x = rng.standard_normal(256).astype(np.float32)
+    out, *_ = m.forward(x)
+    # every routed MLP is exactly zero: routed = 0, out = 0 + mlp_shared(x) exactly
+    sh = _mlp(oracle, shared, x)
+    assert np.any(sh != 0) and np.array_equal(out, sh)
+
+
+def test_noaux_moe_identical_experts_scale_by_routed_factor(oracle):
+    m, rng, experts, shared, *_ = _small_noaux(oracle, identical=True, norm=True, scaling=2.5)
+    x = rng.standard_normal(256).astype(np.float32)
+    out, ids, w, _ = m.forward(x)
+    f = _mlp(oracle, experts[0], x).astype(np.float64)
+    sh = _mlp(oracle, shared, x).astype(np.float64)
+    # sum_r w_r f(x) with sum_r w_r = 2.5 (renormalised, then scaled) -> 2.5 f(x) + shared
+    assert oracle.relative_l2(out, 2.5 * f + sh) < 1e-6
