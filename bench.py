@@ -137,6 +137,49 @@ def moe_bench(ctx, shape, steps, warmup, n_inputs=16):
             "model_device_bytes": dev_bytes, "gen_seconds": round(gen_s, 2), "layers": L}
 
 
+def moe_batch_bench(ctx, steps, warmup, n_batches=8, T=32):
+    """Config 5: the DeepSeek-V3-shaped noaux_tc block on batches of T bf16
+    tokens, cycling over n_batches distinct batches (distinct routings)."""
+    from hawking_amd.moe import MoeModel, MoeShape
+    from hawking_amd.organs import stream_key
+    shape = MoeShape.deepseek_v3()
+    t0 = time.time()
+    m = MoeModel(ctx, shape)
+    m.fill_synthetic(SEED)
+    ctx.synchronize()
+    gen_s = time.time() - t0
+    H, K = shape.hidden, shape.top_k
+    xf = ctx.empty((n_batches, T, H))
+    ctx.call("hk_synth_normal", stream_key(SEED, 0xC5C5), 0, n_batches * T * H, 1.0, xf.ptr, ctx.stream)
+    x32 = xf.download()
+    b = x32.view(np.uint32).astype(np.uint64)
+    xb = ctx.to_device(((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16))  # bf16, round to nearest even
+    y = ctx.empty((T, H))
+    ids = ctx.empty((n_batches, T, K), np.int32)
+    state = {"i": 0}
+
+    def step():
+        i = state["i"] % n_batches
+        state["i"] += 1
+        m.forward_batch_device(0, xb.offset(i * T * H), T, y, ids.offset(i * T * K), None)
+
+    ms = time_launches(ctx, step, steps, warmup)
+    routes = ids.download()
+    dev_bytes, dense_per_layer = m.model_bytes()
+    router_bytes = shape.n_experts * H * 4 + shape.n_experts * 4
+    shared_bytes = m.expert_bytes(0, shape.n_experts)
+    per_batch, active = [], []
+    for bi in range(n_batches):
+        experts = sorted(set(int(e) for e in routes[bi].ravel()))
+        active.append(len(experts))
+        per_batch.append(router_bytes + sum(m.expert_bytes(0, e) for e in experts) + shared_bytes + T * H * (2 + 4))
+    nbytes = float(np.mean(per_batch))
+    return {"us_per_step": ms * 1e3, "tokens_per_step": T, "tokens_per_s": T / (ms * 1e-3),
+            "bytes_per_step": nbytes, "gbps": nbytes / (ms * 1e-3) / 1e9,
+            "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, "active_experts_mean": float(np.mean(active)),
+            "model_device_bytes": dev_bytes, "gen_seconds": round(gen_s, 2)}
+
+
 def cpu_baseline(budget_s: float = 12.0, n_distinct: int = 64):
     """Oracle binary matvec (serial f32, one thread) over the first n_distinct
     organs of the headline workload, cycled until budget_s of matvec time."""
@@ -241,6 +284,9 @@ def main():
             r = moe_bench(ctx, c4, max(args.steps, 20), args.warmup)
             extra["moe_token_c4_mixed"] = {k: (round(v, 2) if isinstance(v, float) else v) for k, v in r.items()}
             log("c4", extra["moe_token_c4_mixed"])
+            r = moe_batch_bench(ctx, max(args.steps, 10), args.warmup)
+            extra["moe_batch_c5_dsv3"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+            log("c5", extra["moe_batch_c5_dsv3"])
     cpu = None if (args.no_cpu or args.only_main) else cpu_baseline()
     if cpu:
         log("cpu", cpu)

@@ -217,7 +217,7 @@ __device__ __forceinline__ void fetch_one(const OrganView& o, uint32_t T, uint32
                                           int r) {
     if constexpr (KIND == HK_BIN || KIND == HK_Q4) {
         f.v[r] = *reinterpret_cast<const uint4*>(o.data + ((size_t)T * o.steps + t) * 1024u + 16u * lane);
-        f.s[r] = f16_bits_to_f32(o.scales[((size_t)T * 64u + lane) * o.steps + t]);
+        f.s[r] = f16_bits_to_f32(o.scales[((size_t)T * o.steps + t) * 64u + lane]);
     } else {
         const uint4 h = o.hdr[(size_t)T * o.steps + t];
         const uint32_t below = __builtin_amdgcn_mbcnt_hi(h.y, __builtin_amdgcn_mbcnt_lo(h.x, 0u));

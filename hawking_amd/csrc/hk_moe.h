@@ -51,7 +51,7 @@ hipError_t launch_moe_layer(int kind, const MoeDims& d, const MoeLayerDev& L, co
 
 constexpr uint32_t MOE_BATCH_MAX_TOKENS = 64;
 constexpr uint32_t MOE_BATCH_MAX_EXPERTS = 512;
-constexpr uint32_t MOE_BATCH_ROUTER_COLS = 1024;  // router columns per split-K workgroup
+constexpr uint32_t MOE_BATCH_ROUTER_COLS = 256;  // router columns per split-K workgroup
 
 struct MoeBatchDims {
     uint32_t T;         // tokens

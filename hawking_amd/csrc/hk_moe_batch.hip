@@ -2,18 +2,23 @@
 // (routed_moe, crates/hawking-core/src/gravity_glm.rs:550-600, with
 // batched_mlp :515-548): every active expert's weights are streamed from HBM
 // once for all of the tokens routed to it (a grouped expert GEMM on the int8
-// matrix-core engine of hk_mfma.h, up to MOE_TB tokens per weight fetch).
+// matrix-core engine of hk_mfma.h: every weight fetch serves all the member
+// tokens whose x images are in LDS).
 //
 //   1. xprep:    x (bf16) -> f32 rows and the fixed-point x image of each token
-//   2. router:   logits partials, split-K over 1024-column slices (f32)
-//   3. route:    one block: per token (one wave each) the noaux_tc route
-//                (gravity_glm.rs:447-500) on the DPP network, then the tokens
-//                grouped by expert (shared expert first, then ascending id)
-//   4. gate/up:  per (active expert, 16-row tile): SwiGLU activations of every
-//                member token; 4 waves split the columns
-//   5. act image: the x image of every (token, expert) activation row
-//   6. down:     per (active expert, 16-row tile): w * (down . act) per member
-//   7. combine:  y_t = sum over t's experts in ascending id, then + shared
+//   2. router:   logits partials, split-K over 256-column slices (f32, router
+//                rows and x staged in LDS)
+//   3. route:    one wave per token: the noaux_tc route (gravity_glm.rs:447-500)
+//                on the DPP network
+//   4. group:    one block: the (token, slot) pairs grouped by expert (shared
+//                expert first, then ascending id) and each token's slots in
+//                ascending expert id
+//   5. gate/up:  per (active expert, 8 row tiles): the member tokens' x images
+//                in LDS, each wave runs two gate+up tile pairs over all columns
+//                and applies SwiGLU
+//   6. act image: the x image of every (token, expert) activation row
+//   7. down:     per (active expert, 8 row tiles): w * (down . act) per member
+//   8. combine:  y_t = sum over t's experts in ascending id, then + shared
 #include "hk_internal.h"
 #include "hk_mfma.h"
 #include "hk_moe.h"
@@ -21,7 +26,8 @@
 
 namespace hk {
 
-constexpr int MOE_TB = 4;  // member tokens per weight fetch
+constexpr int MOE_TILES_PER_ITEM = 8;  // row tiles per workgroup item (2 per wave)
+constexpr uint32_t RT_ROWS = 32, RT_COLS = 128, RT_SLICE = MOE_BATCH_ROUTER_COLS;  // router tiling
 
 size_t moe_batch_img_bytes(uint32_t cols) { return x_lds_bytes<HK_Q4>(n_steps_for(HK_Q4, cols)); }
 
@@ -83,148 +89,186 @@ __global__ void __launch_bounds__(256) moe_batch_xprep_kernel(MoeBatchDims d, co
 
 // ------------------------------------------------------------------ 2. router (split-K)
 
-// part[s][t][e] = sum over columns [1024 s, 1024 (s+1)) of W[e][k] x[t][k];
-// thread (row r = tid / 32, token tt = tid % 32), x staged in LDS as [k][t].
+// part[s][t][e] = sum over columns [256 s, 256 (s+1)) of W[e][k] x[t][k] for a
+// block of 32 router rows; thread (row r = tid / 8, tokens 4 (tid % 8) .. +3),
+// router rows and x staged in LDS 128 columns at a time.
 __global__ void __launch_bounds__(256) moe_batch_router_kernel(MoeBatchDims d, const float* __restrict__ W,
                                                                MoeBatchWs ws) {
-    __shared__ float xs[256 * 33];
-    const uint32_t tt = threadIdx.x & 31u;
-    const uint32_t r = blockIdx.x * 8u + (threadIdx.x >> 5), s = blockIdx.y;
-    const uint32_t k0 = s * MOE_BATCH_ROUTER_COLS, k1 = min(k0 + MOE_BATCH_ROUTER_COLS, d.H);
-    const bool row_ok = r < d.E;
-    const float* wr = W + (size_t)(row_ok ? r : 0u) * d.H;
+    __shared__ float wsh[RT_ROWS][RT_COLS + 1];
+    __shared__ __align__(16) float xsh[RT_COLS][32];
+    const uint32_t rr = threadIdx.x >> 3, tg = threadIdx.x & 7u;
+    const uint32_t r0 = blockIdx.x * RT_ROWS, s = blockIdx.y;
+    const uint32_t k0 = s * RT_SLICE, k1 = min(k0 + RT_SLICE, d.H);
     for (uint32_t tb = 0; tb < d.T; tb += 32u) {
-        float acc = 0.f;
-        for (uint32_t kc = k0; kc < k1; kc += 256u) {
-            const uint32_t kn = min(256u, k1 - kc);
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (uint32_t kc = k0; kc < k1; kc += RT_COLS) {
+            const uint32_t kn = min(RT_COLS, k1 - kc);
             __syncthreads();
-            for (uint32_t idx = threadIdx.x; idx < 32u * 256u; idx += blockDim.x) {
-                const uint32_t t = idx >> 8, k = idx & 255u;
-                xs[k * 33u + t] = (tb + t < d.T && k < kn) ? ws.x32[(size_t)(tb + t) * d.H + kc + k] : 0.f;
+            for (uint32_t idx = threadIdx.x; idx < RT_ROWS * RT_COLS / 4u; idx += blockDim.x) {
+                const uint32_t row = idx / (RT_COLS / 4u), k = 4u * (idx % (RT_COLS / 4u));
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (r0 + row < d.E && k < kn) v = *reinterpret_cast<const float4*>(W + (size_t)(r0 + row) * d.H + kc + k);
+                wsh[row][k] = v.x;
+                wsh[row][k + 1] = v.y;
+                wsh[row][k + 2] = v.z;
+                wsh[row][k + 3] = v.w;
+            }
+            for (uint32_t idx = threadIdx.x; idx < 32u * RT_COLS / 4u; idx += blockDim.x) {
+                const uint32_t t = idx / (RT_COLS / 4u), k = 4u * (idx % (RT_COLS / 4u));
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (tb + t < d.T && k < kn) v = *reinterpret_cast<const float4*>(ws.x32 + (size_t)(tb + t) * d.H + kc + k);
+                xsh[k][t] = v.x;
+                xsh[k + 1][t] = v.y;
+                xsh[k + 2][t] = v.z;
+                xsh[k + 3][t] = v.w;
             }
             __syncthreads();
-            if (row_ok) {
-                for (uint32_t k = 0; k < kn; k += 4u) {
-                    const float4 w4 = *reinterpret_cast<const float4*>(wr + kc + k);
-                    acc += w4.x * xs[k * 33u + tt] + w4.y * xs[(k + 1u) * 33u + tt] + w4.z * xs[(k + 2u) * 33u + tt] +
-                           w4.w * xs[(k + 3u) * 33u + tt];
-                }
+            for (uint32_t k = 0; k < kn; ++k) {
+                const float w = wsh[rr][k];
+                const float4 x = *reinterpret_cast<const float4*>(&xsh[k][4u * tg]);
+                acc[0] += w * x.x;
+                acc[1] += w * x.y;
+                acc[2] += w * x.z;
+                acc[3] += w * x.w;
             }
         }
-        if (row_ok && tb + tt < d.T) ws.part[((size_t)s * d.T + tb + tt) * d.E + r] = acc;
+        const uint32_t r = r0 + rr;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            const uint32_t t = tb + 4u * tg + i;
+            if (r < d.E && t < d.T) ws.part[((size_t)s * d.T + t) * d.E + r] = acc[i];
+        }
     }
 }
 
-// ------------------------------------------------------------------ 3. route + group
+// ------------------------------------------------------------------ 3. route (one wave per token)
 
-__global__ void __launch_bounds__(1024) moe_batch_route_kernel(MoeBatchDims d, const float* __restrict__ bias,
-                                                               MoeBatchWs ws, int32_t* ids_out, float* w_out) {
+__device__ __forceinline__ float key_value(uint64_t k) {
+    const uint32_t o = (uint32_t)(k >> 32);
+    return __builtin_bit_cast(float, (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
+}
+
+__global__ void __launch_bounds__(64) moe_batch_route_kernel(MoeBatchDims d, const float* __restrict__ bias,
+                                                             MoeBatchWs ws, int32_t* ids_out, float* w_out) {
     constexpr int NPL = MOE_BATCH_MAX_EXPERTS / 64;
-    constexpr uint32_t MAXP = MOE_BATCH_MAX_TOKENS * 16;
-    __shared__ float corr[16][MOE_BATCH_MAX_EXPERTS];
-    __shared__ int32_t sids[MAXP];
-    __shared__ float sw[MAXP];
-    __shared__ uint32_t cnt[MOE_BATCH_MAX_EXPERTS], fill[MOE_BATCH_MAX_EXPERTS], start[MOE_BATCH_MAX_EXPERTS];
+    __shared__ int32_t sel_i[16];
+    __shared__ float sel_w[16];
     const int lane = threadIdx.x & 63;
-    const uint32_t wave = threadIdx.x >> 6;
-    const uint32_t E = d.E, K = d.K, per = d.E / d.n_group;
-    for (uint32_t e = threadIdx.x; e < E; e += blockDim.x) {
-        cnt[e] = 0;
-        fill[e] = 0;
-    }
-    // ---- noaux_tc per token, one wave per token
-    for (uint32_t t = wave; t < d.T; t += 16u) {
-        float sc[NPL], cv[NPL];
-        uint32_t bad = 0;
+    const uint32_t t = blockIdx.x, E = d.E, K = d.K, per = d.E / d.n_group;
+    float sc[NPL], cv[NPL];
+    uint32_t bad = 0;
 #pragma unroll
-        for (int j = 0; j < NPL; ++j) {
-            const uint32_t i = (uint32_t)lane + 64u * j;
-            sc[j] = 0.f;
-            cv[j] = -INFINITY;
-            if (i < E) {
-                float l = 0.f;
-                for (uint32_t s = 0; s < d.S; ++s) l += ws.part[((size_t)s * d.T + t) * E + i];
-                if (!isfinite(l)) bad = 1;
-                sc[j] = 1.0f / (1.0f + expf(-l));
-                cv[j] = sc[j] + bias[i];
-                corr[wave][i] = cv[j];
-            }
+    for (int j = 0; j < NPL; ++j) {
+        const uint32_t i = (uint32_t)lane + 64u * j;
+        sc[j] = 0.f;
+        cv[j] = -INFINITY;
+        if (i < E) {
+            float l = 0.f;
+            for (uint32_t s = 0; s < d.S; ++s) l += ws.part[((size_t)s * d.T + t) * E + i];
+            if (!isfinite(l)) bad = 1;
+            sc[j] = 1.0f / (1.0f + expf(-l));
+            cv[j] = sc[j] + bias[i];
         }
-        if (bad) atomicOr(ws.status, HK_DEVERR_NONFINITE);
-        wave_lds_sync();
-        // group strength = sum of its best two corrected scores (topk_desc order)
+    }
+    if (bad) atomicOr(ws.status, HK_DEVERR_NONFINITE);
+    // group strength = sum of its best two corrected scores, in topk_desc order
+    uint64_t chosen = 1;
+    if (d.topk_group < d.n_group) {
         uint64_t gkey = 0;
-        if ((uint32_t)lane < d.n_group) {
-            const float* sl = corr[wave] + (size_t)lane * per;
-            uint32_t b0 = 0;
-            for (uint32_t i = 1; i < per; ++i)
-                if (sl[i] > sl[b0]) b0 = i;
-            float gs = -0.0f + sl[b0];
-            if (per >= 2) {
-                uint32_t b1 = b0 == 0 ? 1u : 0u;
-                for (uint32_t i = 0; i < per; ++i)
-                    if (i != b0 && (sl[i] > sl[b1] || (sl[i] == sl[b1] && i < b1))) b1 = i;
-                gs = gs + sl[b1];
+        for (uint32_t g = 0; g < d.n_group; ++g) {
+            uint64_t k1 = 0;
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) {
+                const uint32_t i = (uint32_t)lane + 64u * j;
+                const uint64_t k = (i < E && i / per == g) ? order_key(cv[j], i) : 0ull;
+                k1 = k > k1 ? k : k1;
             }
-            gkey = order_key(gs, (uint32_t)lane);
+            const uint64_t b0 = wave_max_key(k1);
+            float gs = -0.0f + key_value(b0);
+            if (per >= 2) {
+                uint64_t k2 = 0;
+#pragma unroll
+                for (int j = 0; j < NPL; ++j) {
+                    const uint32_t i = (uint32_t)lane + 64u * j;
+                    const uint64_t k = (i < E && i / per == g) ? order_key(cv[j], i) : 0ull;
+                    k2 = (k != b0 && k > k2) ? k : k2;
+                }
+                gs = gs + key_value(wave_max_key(k2));
+            }
+            if ((uint32_t)lane == g) gkey = order_key(gs, g);
         }
-        uint64_t chosen = 0;
+        chosen = 0;
         for (uint32_t c = 0; c < d.topk_group; ++c) {
             const uint64_t w = wave_max_key(gkey);
             const uint32_t g = ~(uint32_t)w;
             chosen |= 1ull << g;
             if ((uint32_t)lane == g) gkey = 0;
         }
-        // only experts inside a chosen group compete (others at -inf)
-        uint64_t key[NPL];
-        uint64_t best = 0;
+    } else {
+        chosen = d.n_group >= 64 ? ~0ull : ((1ull << d.n_group) - 1ull);
+    }
+    // only experts inside a chosen group compete (the others at -inf)
+    uint64_t key[NPL];
+    uint64_t best = 0;
 #pragma unroll
-        for (int j = 0; j < NPL; ++j) {
-            const uint32_t i = (uint32_t)lane + 64u * j;
-            key[j] = i < E ? order_key(((chosen >> (i / per)) & 1ull) ? cv[j] : -INFINITY, i) : 0ull;
-            best = key[j] > best ? key[j] : best;
-        }
-        for (uint32_t r = 0; r < K; ++r) {
-            const uint64_t w = wave_max_key(best);
-            const uint32_t id = ~(uint32_t)w;
-            if ((id & 63u) == (uint32_t)lane) {
-                float s_id = 0.f;
-                best = 0;
+    for (int j = 0; j < NPL; ++j) {
+        const uint32_t i = (uint32_t)lane + 64u * j;
+        key[j] = i < E ? order_key(((chosen >> (i / per)) & 1ull) ? cv[j] : -INFINITY, i) : 0ull;
+        best = key[j] > best ? key[j] : best;
+    }
+    for (uint32_t r = 0; r < K; ++r) {
+        const uint64_t w = wave_max_key(best);
+        const uint32_t id = ~(uint32_t)w;
+        if ((id & 63u) == (uint32_t)lane) {
+            float s_id = 0.f;
+            best = 0;
 #pragma unroll
-                for (int j = 0; j < NPL; ++j) {
-                    if ((uint32_t)j == (id >> 6)) {
-                        s_id = sc[j];
-                        key[j] = 0;
-                    }
-                    best = key[j] > best ? key[j] : best;
+            for (int j = 0; j < NPL; ++j) {
+                if ((uint32_t)j == (id >> 6)) {
+                    s_id = sc[j];
+                    key[j] = 0;
                 }
-                sids[t * K + r] = (int32_t)id;
-                sw[t * K + r] = s_id;  // weights are the uncorrected scores
+                best = key[j] > best ? key[j] : best;
             }
-        }
-        wave_lds_sync();
-        if (lane == 0) {
-            float total = -0.0f;
-            for (uint32_t r = 0; r < K; ++r) total += sw[t * K + r];
-            total = total + 1e-20f;
-            for (uint32_t r = 0; r < K; ++r) {
-                float v = sw[t * K + r];
-                if (d.norm_topk_prob) v = v / total;
-                sw[t * K + r] = v * d.scaling;
-            }
-        }
-        wave_lds_sync();
-        if ((uint32_t)lane < K) {
-            const uint32_t p = t * K + (uint32_t)lane;
-            ws.ids[p] = sids[p];
-            ws.w[p] = sw[p];
-            if (ids_out) ids_out[p] = sids[p];
-            if (w_out) w_out[p] = sw[p];
+            sel_i[r] = (int32_t)id;
+            sel_w[r] = s_id;  // weights are the uncorrected scores
         }
     }
+    wave_lds_sync();
+    if (lane == 0) {
+        float total = -0.0f;
+        for (uint32_t r = 0; r < K; ++r) total += sel_w[r];
+        total = total + 1e-20f;
+        for (uint32_t r = 0; r < K; ++r) {
+            float v = sel_w[r];
+            if (d.norm_topk_prob) v = v / total;
+            sel_w[r] = v * d.scaling;
+        }
+    }
+    wave_lds_sync();
+    if ((uint32_t)lane < K) {
+        const uint32_t p = t * K + (uint32_t)lane;
+        ws.ids[p] = sel_i[lane];
+        ws.w[p] = sel_w[lane];
+        if (ids_out) ids_out[p] = sel_i[lane];
+        if (w_out) w_out[p] = sel_w[lane];
+    }
+}
+
+// ------------------------------------------------------------------ 4. group
+
+__global__ void __launch_bounds__(1024) moe_batch_group_kernel(MoeBatchDims d, MoeBatchWs ws) {
+    constexpr int NPL = MOE_BATCH_MAX_EXPERTS / 64;
+    __shared__ int32_t sids[MOE_BATCH_MAX_TOKENS * 16];
+    __shared__ uint32_t cnt[MOE_BATCH_MAX_EXPERTS], fill[MOE_BATCH_MAX_EXPERTS], start[MOE_BATCH_MAX_EXPERTS];
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = threadIdx.x >> 6, E = d.E, K = d.K, np = d.T * d.K, has_shared = d.SI ? 1u : 0u;
+    for (uint32_t e = threadIdx.x; e < E; e += blockDim.x) {
+        cnt[e] = 0;
+        fill[e] = 0;
+    }
+    for (uint32_t p = threadIdx.x; p < np; p += blockDim.x) sids[p] = ws.ids[p];
     __syncthreads();
-    // ---- group the (token, slot) pairs by expert
-    const uint32_t np = d.T * K, has_shared = d.SI ? 1u : 0u;
     for (uint32_t p = threadIdx.x; p < np; p += blockDim.x) atomicAdd(&cnt[(uint32_t)sids[p]], 1u);
     __syncthreads();
     if (wave == 0) {
@@ -261,137 +305,170 @@ __global__ void __launch_bounds__(1024) moe_batch_route_kernel(MoeBatchDims d, c
     }
     if (has_shared)
         for (uint32_t t = threadIdx.x; t < d.T; t += blockDim.x) ws.members[t] = np + t;
-    // each token's slots in ascending expert id (the combine order)
-    for (uint32_t t = threadIdx.x; t < d.T; t += blockDim.x) {
-        int32_t o[16];
-        for (uint32_t r = 0; r < K; ++r) {
-            uint32_t j = r;
-            while (j > 0 && sids[t * K + (uint32_t)o[j - 1]] > sids[t * K + r]) {
-                o[j] = o[j - 1];
-                --j;
-            }
-            o[j] = (int32_t)r;
-        }
-        for (uint32_t r = 0; r < K; ++r) ws.order[t * K + r] = o[r];
+    // each token's slots in ascending expert id (ids of a token are distinct)
+    for (uint32_t p = threadIdx.x; p < np; p += blockDim.x) {
+        const uint32_t t = p / K, r = p % K;
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < K; ++j) rank += sids[t * K + j] < sids[p] ? 1u : 0u;
+        ws.order[t * K + rank] = (int32_t)r;
     }
 }
 
-// ------------------------------------------------------------------ 4. gate/up (grouped)
+// ------------------------------------------------------------------ grouped tile worker
 
-// One fetched step of the gate and up tiles plus the A operands and column
-// sums of up to MOE_TB member tokens.
-struct GuStep {
-    Frag<HK_Q4, 2> f;
-    v4i alo[MOE_TB], ahi[MOE_TB];
-    float sx[MOE_TB];
+// acc[j][r] += this lane's partial dot of weight tile r (tile Tr[r] of organ
+// r's data/scales, S column steps) with member token j's x image in LDS
+// (img + j*img_bytes), over all S steps with a D-deep weight pipeline.
+template <int R, int TB, int D>
+__device__ __forceinline__ void tiles_x_tokens(const uint8_t* const* base_d, const uint16_t* const* base_s, uint32_t S,
+                                               const uint8_t* img, uint32_t img_bytes, uint32_t nm, uint32_t aoff,
+                                               int q, float (*acc)[R]) {
+    Frag<HK_Q4, R> f[D];
+    auto fetch = [&](uint32_t t, Frag<HK_Q4, R>& fr) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            fr.v[r] = *reinterpret_cast<const uint4*>(base_d[r] + (size_t)t * 1024u);
+            fr.s[r] = f16_bits_to_f32(base_s[r][(size_t)t * 64u]);
+        }
+    };
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+        if ((uint32_t)k < S) fetch((uint32_t)k, f[k]);
+    const float* SX0 = reinterpret_cast<const float*>(img + (size_t)S * 2u * A_TILE_STRIDE);
+    for (uint32_t it = 0; it < S; it += D) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            const uint32_t t = it + (uint32_t)k;
+            if (t >= S) break;
+            v4i alo[TB], ahi[TB];
+            float sx[TB];
+#pragma unroll
+            for (int j = 0; j < TB; ++j) {
+                if ((uint32_t)j < nm) {
+                    const uint8_t* ij = img + (size_t)j * img_bytes;
+                    alo[j] = lds_a(ij, 2u * t, aoff);
+                    ahi[j] = lds_a(ij, 2u * t + 1u, aoff);
+                    sx[j] = reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(SX0) + (size_t)j * img_bytes)[4u * t + (uint32_t)q];
+                }
+            }
+            const uint32_t m = 0x0F0F0F0Fu;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const v4i lo = {(int)(f[k].v[r].x & m), (int)(f[k].v[r].y & m), (int)(f[k].v[r].z & m),
+                                (int)(f[k].v[r].w & m)};
+                const v4i hi = {(int)((f[k].v[r].x >> 4) & m), (int)((f[k].v[r].y >> 4) & m),
+                                (int)((f[k].v[r].z >> 4) & m), (int)((f[k].v[r].w >> 4) & m)};
+#pragma unroll
+                for (int j = 0; j < TB; ++j) {
+                    if ((uint32_t)j < nm) {
+                        v4i c = mfma_i8(alo[j], lo, v4i{0, 0, 0, 0});
+                        c = mfma_i8(ahi[j], hi, c);
+                        acc[j][r] += f[k].s[r] * (combine_limbs(c) - 8.0f * sx[j]);
+                    }
+                }
+            }
+            if (t + D < S) fetch(t + D, f[k]);
+        }
+    }
+}
+
+// Copies the x images of nm member tokens into LDS (all threads of the block).
+__device__ __forceinline__ void stage_images(uint8_t* lds, const uint8_t* src, uint32_t stride, const uint32_t* idx,
+                                             uint32_t nm, uint32_t img_bytes) {
+    for (uint32_t o = threadIdx.x * 16u; o < nm * img_bytes; o += blockDim.x * 16u) {
+        const uint32_t j = o / img_bytes, off = o % img_bytes;
+        *reinterpret_cast<uint4*>(lds + o) = *reinterpret_cast<const uint4*>(src + (size_t)idx[j] * stride + off);
+    }
+}
+
+// Work items of a grouped kernel: (active expert a, tile group tg, member
+// groups [m_lo, m_hi) of TB tokens).  The shared expert (active entry 0) has
+// every token as a member, so each of its member groups is an item of its
+// own, listed first and tile-group-major (its weights are then re-read from
+// L2 / MALL by neighbouring items); a routed expert's item covers all of its
+// members (rarely more than one group).
+struct ItemMap {
+    uint32_t gpe, ngs, extra, n_items;
+    __device__ ItemMap(const MoeBatchDims& d, uint32_t gpe_, uint32_t n_active, uint32_t TB) : gpe(gpe_) {
+        ngs = d.SI ? (d.T + TB - 1) / TB : 0u;
+        extra = ngs > 1 ? gpe * (ngs - 1) : 0u;
+        n_items = extra + n_active * gpe;
+    }
+    __device__ void at(uint32_t item, uint32_t* a, uint32_t* tg, uint32_t* m_lo, uint32_t* m_hi) const {
+        if (item < extra) {
+            *a = 0;
+            *tg = item / (ngs - 1);
+            *m_lo = 1u + item % (ngs - 1);
+            *m_hi = *m_lo + 1u;
+            return;
+        }
+        const uint32_t i = item - extra;
+        *a = i / gpe;
+        *tg = i % gpe;
+        *m_lo = 0;
+        *m_hi = (*a == 0 && ngs) ? 1u : 0xFFFFFFFFu;
+    }
 };
 
-__device__ __forceinline__ void gu_fetch(const OrganView& g, const OrganView& u, uint32_t T, uint32_t t, int lane,
-                                         uint32_t aoff, int q, const uint8_t* const* img, uint32_t steps_x, uint32_t nm,
-                                         GuStep& st) {
-    fetch_one<HK_Q4, 2>(g, T, t, lane, st.f, 0);
-    fetch_one<HK_Q4, 2>(u, T, t, lane, st.f, 1);
-#pragma unroll
-    for (int j = 0; j < MOE_TB; ++j) {
-        if ((uint32_t)j < nm) {
-            const uint8_t* ib = img[j] + (size_t)t * 2u * A_TILE_STRIDE + aoff;
-            st.alo[j] = *reinterpret_cast<const v4i*>(ib);
-            st.ahi[j] = *reinterpret_cast<const v4i*>(ib + A_TILE_STRIDE);
-            st.sx[j] = reinterpret_cast<const float*>(img[j] + (size_t)steps_x * 2u * A_TILE_STRIDE)[4u * t + (uint32_t)q];
-        }
-    }
-}
+// ------------------------------------------------------------------ 5. gate/up (grouped)
 
-template <int R>
-__device__ __forceinline__ void q4_tokens(const Frag<HK_Q4, R>& f, const v4i* alo, const v4i* ahi, const float* sx,
-                                          uint32_t nm, float (*acc)[R]) {
-    const uint32_t m = 0x0F0F0F0Fu;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const v4i lo = {(int)(f.v[r].x & m), (int)(f.v[r].y & m), (int)(f.v[r].z & m), (int)(f.v[r].w & m)};
-        const v4i hi = {(int)((f.v[r].x >> 4) & m), (int)((f.v[r].y >> 4) & m), (int)((f.v[r].z >> 4) & m),
-                        (int)((f.v[r].w >> 4) & m)};
-#pragma unroll
-        for (int j = 0; j < MOE_TB; ++j) {
-            if ((uint32_t)j < nm) {
-                v4i c = mfma_i8(alo[j], lo, v4i{0, 0, 0, 0});
-                c = mfma_i8(ahi[j], hi, c);
-                acc[j][r] += f.s[r] * (combine_limbs(c) - 8.0f * sx[j]);
-            }
-        }
-    }
-}
-
-template <int D>
+template <int TB, int D>
 __global__ void __launch_bounds__(256) moe_batch_gate_up_kernel(MoeBatchDims d, const OrganView* __restrict__ table,
                                                                 MoeBatchWs ws) {
-    __shared__ float part[4][MOE_TB][2][16];
+    extern __shared__ __align__(16) uint8_t lds[];  // TB x images of H columns
     const int lane = threadIdx.x & 63, q = lane >> 4;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t aoff = a_lane_offset(lane);
-    const uint32_t tiles = n_tiles_for(max(d.I, d.SI));
-    const uint32_t steps_x = n_steps_for(HK_Q4, d.H);
-    const uint32_t n_items = __builtin_amdgcn_readfirstlane(*ws.n_active) * tiles;
-    for (uint32_t item = blockIdx.x; item < n_items; item += gridDim.x) {
-        const uint32_t a = item / tiles, T = item % tiles;
+    const uint32_t tiles = n_tiles_for(max(d.I, d.SI)), gpe = (tiles + MOE_TILES_PER_ITEM - 1) / MOE_TILES_PER_ITEM;
+    const uint32_t S = n_steps_for(HK_Q4, d.H);
+    const uint32_t img_bytes = (uint32_t)x_lds_bytes<HK_Q4>(S);
+    const ItemMap im(d, gpe, __builtin_amdgcn_readfirstlane(*ws.n_active), TB);
+    for (uint32_t item = blockIdx.x; item < im.n_items; item += gridDim.x) {
+        uint32_t a, tg, mg_lo, mg_hi;
+        im.at(item, &a, &tg, &mg_lo, &mg_hi);
         const uint4 ent = ws.active[a];
-        const OrganView g = table[ent.x * 3u + 0u];
-        if (T >= g.n_tiles) continue;
-        const OrganView u = table[ent.x * 3u + 1u];
-        const uint32_t S = g.steps, per = (S + 3u) / 4u;
-        const uint32_t s0 = min(wave * per, S), ns = min(s0 + per, S) - s0;
-        for (uint32_t m0 = 0; m0 < ent.z; m0 += MOE_TB) {
-            const uint32_t nm = min((uint32_t)MOE_TB, ent.z - m0);
-            uint32_t pair[MOE_TB];
-            const uint8_t* img[MOE_TB];
+        const OrganView g = table[ent.x * 3u + 0u], u = table[ent.x * 3u + 1u];
+        if (tg * MOE_TILES_PER_ITEM >= g.n_tiles) continue;
+        // this wave's two tiles (the second aliases the first past the end)
+        const uint32_t T0 = tg * MOE_TILES_PER_ITEM + 2u * wave, T1 = T0 + 1u;
+        const bool v0 = T0 < g.n_tiles, v1 = T1 < g.n_tiles;
+        const uint32_t T1c = v1 ? T1 : T0;
+        const uint8_t* bd[4] = {g.data + ((size_t)T0 * S) * 1024u + 16u * lane, u.data + ((size_t)T0 * S) * 1024u + 16u * lane,
+                                g.data + ((size_t)T1c * S) * 1024u + 16u * lane, u.data + ((size_t)T1c * S) * 1024u + 16u * lane};
+        const uint16_t* bs[4] = {g.scales + (size_t)T0 * S * 64u + lane, u.scales + (size_t)T0 * S * 64u + lane,
+                                 g.scales + (size_t)T1c * S * 64u + lane, u.scales + (size_t)T1c * S * 64u + lane};
+        const uint32_t m_end = mg_hi == 0xFFFFFFFFu ? ent.z : min(ent.z, mg_hi * (uint32_t)TB);
+        for (uint32_t m0 = mg_lo * TB; m0 < m_end; m0 += TB) {
+            const uint32_t nm = min((uint32_t)TB, ent.z - m0);
+            uint32_t pair[TB], tok[TB];
 #pragma unroll
-            for (int j = 0; j < MOE_TB; ++j) {
+            for (int j = 0; j < TB; ++j) {
                 pair[j] = ws.members[ent.y + m0 + min((uint32_t)j, nm - 1u)];
-                img[j] = ws.ximg + (size_t)pair_token(d, pair[j]) * ws.ximg_stride;
-            }
-            GuStep st[D];
-#pragma unroll
-            for (int k = 0; k < D; ++k)
-                if ((uint32_t)k < ns) gu_fetch(g, u, T, s0 + k, lane, aoff, q, img, steps_x, nm, st[k]);
-            float acc[MOE_TB][2] = {};
-            for (uint32_t it = 0; it < ns; it += D) {
-#pragma unroll
-                for (int k = 0; k < D; ++k) {
-                    if (it + k >= ns) break;
-                    q4_tokens<2>(st[k].f, st[k].alo, st[k].ahi, st[k].sx, nm, acc);
-                    const uint32_t nx = it + D + k;
-                    if (nx < ns) gu_fetch(g, u, T, s0 + nx, lane, aoff, q, img, steps_x, nm, st[k]);
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < MOE_TB; ++j) {
-                const float gs = tile_row_sum(acc[j][0]), us = tile_row_sum(acc[j][1]);
-                if (lane < 16) {
-                    part[wave][j][0][lane] = gs;
-                    part[wave][j][1][lane] = us;
-                }
+                tok[j] = pair_token(d, pair[j]);
             }
             __syncthreads();
-            if (threadIdx.x < 16u * nm) {
-                const uint32_t j = threadIdx.x >> 4, row = threadIdx.x & 15u;
-                float gv = 0.f, uv = 0.f;
-#pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    gv += part[w][j][0][row];
-                    uv += part[w][j][1][row];
-                }
-                const int E = ws.ximg_e[pair_token(d, pair[j])];
-                gv = ldexpf(gv, -E);
-                uv = ldexpf(uv, -E);
-                const uint32_t orow = T * 16u + row;
-                if (orow < g.rows) ws.act[(size_t)pair[j] * d.Imax + orow] = (gv / (1.0f + expf(-gv))) * uv;
-            }
+            stage_images(lds, ws.ximg, ws.ximg_stride, tok, nm, img_bytes);
             __syncthreads();
+            if (!v0) continue;
+            float acc[TB][4] = {};
+            tiles_x_tokens<4, TB, D>(bd, bs, S, lds, img_bytes, nm, aoff, q, acc);
+#pragma unroll
+            for (int j = 0; j < TB; ++j) {
+                if ((uint32_t)j >= nm) break;
+                const int E = ws.ximg_e[tok[j]];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float gs = ldexpf(tile_row_sum(acc[j][2 * h]), -E), us = ldexpf(tile_row_sum(acc[j][2 * h + 1]), -E);
+                    const uint32_t row = (h ? T1 : T0) * 16u + (uint32_t)(lane & 15);
+                    if (lane < 16 && (h ? v1 : v0) && row < g.rows)
+                        ws.act[(size_t)pair[j] * d.Imax + row] = (gs / (1.0f + expf(-gs))) * us;
+                }
+            }
         }
     }
 }
 
-// ------------------------------------------------------------------ 5. activation images
+// ------------------------------------------------------------------ 6. activation images
 
 __global__ void __launch_bounds__(256) moe_batch_act_image_kernel(MoeBatchDims d, MoeBatchWs ws) {
     extern __shared__ __align__(16) float xs[];  // [Imax]
@@ -410,88 +487,58 @@ __global__ void __launch_bounds__(256) moe_batch_act_image_kernel(MoeBatchDims d
     }
 }
 
-// ------------------------------------------------------------------ 6. down (grouped)
+// ------------------------------------------------------------------ 7. down (grouped)
 
-struct DnStep {
-    Frag<HK_Q4, 1> f;
-    v4i alo[MOE_TB], ahi[MOE_TB];
-    float sx[MOE_TB];
-};
-
-__device__ __forceinline__ void dn_fetch(const OrganView& o, uint32_t T, uint32_t t, int lane, uint32_t aoff, int q,
-                                         const uint8_t* const* img, uint32_t steps_x, uint32_t nm, DnStep& st) {
-    fetch_one<HK_Q4, 1>(o, T, t, lane, st.f, 0);
-#pragma unroll
-    for (int j = 0; j < MOE_TB; ++j) {
-        if ((uint32_t)j < nm) {
-            const uint8_t* ib = img[j] + (size_t)t * 2u * A_TILE_STRIDE + aoff;
-            st.alo[j] = *reinterpret_cast<const v4i*>(ib);
-            st.ahi[j] = *reinterpret_cast<const v4i*>(ib + A_TILE_STRIDE);
-            st.sx[j] = reinterpret_cast<const float*>(img[j] + (size_t)steps_x * 2u * A_TILE_STRIDE)[4u * t + (uint32_t)q];
-        }
-    }
-}
-
-template <int D>
+template <int TB, int D>
 __global__ void __launch_bounds__(256) moe_batch_down_kernel(MoeBatchDims d, const OrganView* __restrict__ table,
                                                              MoeBatchWs ws) {
-    __shared__ float part[4][MOE_TB][16];
+    extern __shared__ __align__(16) uint8_t lds[];  // TB activation images
     const int lane = threadIdx.x & 63, q = lane >> 4;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t aoff = a_lane_offset(lane);
-    const uint32_t tiles = n_tiles_for(d.H);
-    const uint32_t n_items = __builtin_amdgcn_readfirstlane(*ws.n_active) * tiles;
+    const uint32_t tiles = n_tiles_for(d.H), gpe = (tiles + MOE_TILES_PER_ITEM - 1) / MOE_TILES_PER_ITEM;
+    const ItemMap im(d, gpe, __builtin_amdgcn_readfirstlane(*ws.n_active), TB);
     const uint32_t np = d.T * d.K;
-    for (uint32_t item = blockIdx.x; item < n_items; item += gridDim.x) {
-        const uint32_t a = item / tiles, T = item % tiles;
+    for (uint32_t item = blockIdx.x; item < im.n_items; item += gridDim.x) {
+        uint32_t a, tg, mg_lo, mg_hi;
+        im.at(item, &a, &tg, &mg_lo, &mg_hi);
         const uint4 ent = ws.active[a];
         const OrganView o = table[ent.x * 3u + 2u];
-        const uint32_t S = o.steps, per = (S + 3u) / 4u;
-        const uint32_t s0 = min(wave * per, S), ns = min(s0 + per, S) - s0;
-        const uint32_t steps_x = S;  // the activation image has the down organ's column steps
-        for (uint32_t m0 = 0; m0 < ent.z; m0 += MOE_TB) {
-            const uint32_t nm = min((uint32_t)MOE_TB, ent.z - m0);
-            uint32_t pair[MOE_TB];
-            const uint8_t* img[MOE_TB];
+        const uint32_t S = o.steps, img_bytes = (uint32_t)x_lds_bytes<HK_Q4>(S);
+        const uint32_t T0 = tg * MOE_TILES_PER_ITEM + 2u * wave, T1 = T0 + 1u;
+        const bool v0 = T0 < o.n_tiles, v1 = T1 < o.n_tiles;
+        const uint32_t T1c = v1 ? T1 : T0;
+        const uint8_t* bd[2] = {o.data + ((size_t)T0 * S) * 1024u + 16u * lane, o.data + ((size_t)T1c * S) * 1024u + 16u * lane};
+        const uint16_t* bs[2] = {o.scales + (size_t)T0 * S * 64u + lane, o.scales + (size_t)T1c * S * 64u + lane};
+        const uint32_t m_end = mg_hi == 0xFFFFFFFFu ? ent.z : min(ent.z, mg_hi * (uint32_t)TB);
+        for (uint32_t m0 = mg_lo * TB; m0 < m_end; m0 += TB) {
+            const uint32_t nm = min((uint32_t)TB, ent.z - m0);
+            uint32_t pair[TB];
 #pragma unroll
-            for (int j = 0; j < MOE_TB; ++j) {
-                pair[j] = ws.members[ent.y + m0 + min((uint32_t)j, nm - 1u)];
-                img[j] = ws.aimg + (size_t)pair[j] * ws.aimg_stride;
-            }
-            DnStep st[D];
+            for (int j = 0; j < TB; ++j) pair[j] = ws.members[ent.y + m0 + min((uint32_t)j, nm - 1u)];
+            __syncthreads();
+            stage_images(lds, ws.aimg, ws.aimg_stride, pair, nm, img_bytes);
+            __syncthreads();
+            if (!v0) continue;
+            float acc[TB][2] = {};
+            tiles_x_tokens<2, TB, D>(bd, bs, S, lds, img_bytes, nm, aoff, q, acc);
 #pragma unroll
-            for (int k = 0; k < D; ++k)
-                if ((uint32_t)k < ns) dn_fetch(o, T, s0 + k, lane, aoff, q, img, steps_x, nm, st[k]);
-            float acc[MOE_TB][1] = {};
-            for (uint32_t it = 0; it < ns; it += D) {
+            for (int j = 0; j < TB; ++j) {
+                if ((uint32_t)j >= nm) break;
+                const int E = ws.aimg_e[pair[j]];
+                const float w = pair[j] < np ? ws.w[pair[j]] : 1.0f;
 #pragma unroll
-                for (int k = 0; k < D; ++k) {
-                    if (it + k >= ns) break;
-                    q4_tokens<1>(st[k].f, st[k].alo, st[k].ahi, st[k].sx, nm, acc);
-                    const uint32_t nx = it + D + k;
-                    if (nx < ns) dn_fetch(o, T, s0 + nx, lane, aoff, q, img, steps_x, nm, st[k]);
+                for (int h = 0; h < 2; ++h) {
+                    const float y = ldexpf(tile_row_sum(acc[j][h]), -E);
+                    const uint32_t row = (h ? T1 : T0) * 16u + (uint32_t)(lane & 15);
+                    if (lane < 16 && (h ? v1 : v0) && row < d.H) ws.ybuf[(size_t)pair[j] * d.H + row] = y * w;
                 }
             }
-#pragma unroll
-            for (int j = 0; j < MOE_TB; ++j) {
-                const float ys = tile_row_sum(acc[j][0]);
-                if (lane < 16) part[wave][j][lane] = ys;
-            }
-            __syncthreads();
-            if (threadIdx.x < 16u * nm) {
-                const uint32_t j = threadIdx.x >> 4, row = threadIdx.x & 15u;
-                const float y = ldexpf(part[0][j][row] + part[1][j][row] + part[2][j][row] + part[3][j][row],
-                                       -ws.aimg_e[pair[j]]);
-                const float w = pair[j] < np ? ws.w[pair[j]] : 1.0f;
-                const uint32_t orow = T * 16u + row;
-                if (orow < d.H) ws.ybuf[(size_t)pair[j] * d.H + orow] = y * w;
-            }
-            __syncthreads();
         }
     }
 }
 
-// ------------------------------------------------------------------ 7. combine
+// ------------------------------------------------------------------ 8. combine
 
 __global__ void __launch_bounds__(256) moe_batch_combine_kernel(MoeBatchDims d, MoeBatchWs ws, float* __restrict__ y) {
     const uint32_t t = blockIdx.x, row = blockIdx.y * blockDim.x + threadIdx.x;
@@ -503,17 +550,38 @@ __global__ void __launch_bounds__(256) moe_batch_combine_kernel(MoeBatchDims d, 
     y[(size_t)t * d.H + row] = acc;
 }
 
+// Token images per member group that fit the 64 KiB LDS budget.
+static uint32_t tokens_per_group(uint32_t img_bytes, uint32_t cap) {
+    return min(cap, (uint32_t)(65536u / img_bytes));
+}
+
 hipError_t launch_moe_batch(const MoeBatchDims& d, const MoeLayerDev& L, const float* bias, const uint16_t* x_bf16,
                             float* y, const MoeBatchWs& ws, int32_t* ids_out, float* w_out, hipStream_t s) {
     const uint32_t pairs = d.T * d.K + (d.SI ? d.T : 0u);
     const uint32_t max_active = min(d.E, d.T * d.K) + (d.SI ? 1u : 0u);
-    const uint32_t gu_items = max_active * n_tiles_for(max(d.I, d.SI)), dn_items = max_active * n_tiles_for(d.H);
+    const uint32_t gpe_gu = (n_tiles_for(max(d.I, d.SI)) + MOE_TILES_PER_ITEM - 1) / MOE_TILES_PER_ITEM;
+    const uint32_t gpe_dn = (n_tiles_for(d.H) + MOE_TILES_PER_ITEM - 1) / MOE_TILES_PER_ITEM;
+    const uint32_t gu_items = (max_active + (d.SI ? d.T : 0u)) * gpe_gu, dn_items = (max_active + (d.SI ? d.T : 0u)) * gpe_dn;
+    const uint32_t ximg = (uint32_t)moe_batch_img_bytes(d.H), aimg = (uint32_t)moe_batch_img_bytes(d.Imax);
+    const uint32_t tb_gu = tokens_per_group(ximg, 2u), tb_dn = tokens_per_group(aimg, 4u);
+    if (tb_gu == 0 || tb_dn == 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL(moe_batch_xprep_kernel, dim3(d.T), dim3(256), (size_t)d.H * sizeof(float), s, d, x_bf16, ws);
-    hipLaunchKernelGGL(moe_batch_router_kernel, dim3((d.E + 7u) / 8u, d.S), dim3(256), 0, s, d, L.router_w, ws);
-    hipLaunchKernelGGL(moe_batch_route_kernel, dim3(1), dim3(1024), 0, s, d, bias, ws, ids_out, w_out);
-    hipLaunchKernelGGL(moe_batch_gate_up_kernel<2>, dim3(min(gu_items, 1024u)), dim3(256), 0, s, d, L.table, ws);
+    hipLaunchKernelGGL(moe_batch_router_kernel, dim3((d.E + RT_ROWS - 1) / RT_ROWS, d.S), dim3(256), 0, s, d, L.router_w,
+                       ws);
+    hipLaunchKernelGGL(moe_batch_route_kernel, dim3(d.T), dim3(64), 0, s, d, bias, ws, ids_out, w_out);
+    hipLaunchKernelGGL(moe_batch_group_kernel, dim3(1), dim3(1024), 0, s, d, ws);
+    const dim3 ggu(min(gu_items, 1024u)), gdn(min(dn_items, 2048u));
+    if (tb_gu >= 2)
+        hipLaunchKernelGGL((moe_batch_gate_up_kernel<2, 4>), ggu, dim3(256), (size_t)2 * ximg, s, d, L.table, ws);
+    else
+        hipLaunchKernelGGL((moe_batch_gate_up_kernel<1, 4>), ggu, dim3(256), (size_t)ximg, s, d, L.table, ws);
     hipLaunchKernelGGL(moe_batch_act_image_kernel, dim3(pairs), dim3(256), (size_t)d.Imax * sizeof(float), s, d, ws);
-    hipLaunchKernelGGL(moe_batch_down_kernel<2>, dim3(min(dn_items, 1024u)), dim3(256), 0, s, d, L.table, ws);
+    if (tb_dn >= 4)
+        hipLaunchKernelGGL((moe_batch_down_kernel<4, 4>), gdn, dim3(256), (size_t)4 * aimg, s, d, L.table, ws);
+    else if (tb_dn >= 2)
+        hipLaunchKernelGGL((moe_batch_down_kernel<2, 4>), gdn, dim3(256), (size_t)2 * aimg, s, d, L.table, ws);
+    else
+        hipLaunchKernelGGL((moe_batch_down_kernel<1, 4>), gdn, dim3(256), (size_t)aimg, s, d, L.table, ws);
     hipLaunchKernelGGL(moe_batch_combine_kernel, dim3(d.T, (d.H + 255u) / 256u), dim3(256), 0, s, d, ws, y);
     return hipGetLastError();
 }

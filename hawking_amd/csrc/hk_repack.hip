@@ -99,7 +99,7 @@ __device__ void repack_fixed_body(const CanonView& src, const OrganView& dst) {
             }
         }
         *reinterpret_cast<uint4*>(const_cast<uint8_t*>(dst.data) + (size_t)ts * 1024u + 16u * l) = v;
-        const_cast<uint16_t*>(dst.scales)[((size_t)T * 64u + l) * dst.steps + t] = s;
+        const_cast<uint16_t*>(dst.scales)[(size_t)ts * 64u + l] = s;
     }
 }
 

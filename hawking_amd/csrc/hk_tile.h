@@ -8,11 +8,11 @@
 //
 //   BIN   step = 512 columns; lane (n,q) holds the 16 sign bytes of row n,
 //         128-group 4t+q (bit i of byte j = column 8j+i, 1 = +scale).
-//         scales: [tile][lane][step] f16.
+//         scales: [tile][step][lane] f16 (one 128-byte line per step).
 //   Q4    step = 128 columns; lane (n,q) holds the 16 code bytes of row n,
 //         32-column chunk 4t+q (byte b: column 2b in the low nibble, 2b+1 in
 //         the high nibble, value (nibble-8)*scale).
-//         scales: [tile][lane][step] f16, the scale of the chunk's group
+//         scales: [tile][step][lane] f16, the scale of the chunk's group
 //         (duplicated per chunk when group > 32).
 //   MIXED step = 512 columns; item (n,q) is row n, 128-group 4t+q, either
 //         binary (16 B of signs, one f16 scale) or Q2 (32 B of 2-bit codes,
@@ -53,13 +53,13 @@ __device__ inline float tiled_weight(const OrganView& o, uint32_t r, uint32_t c)
         const uint32_t chunk = c >> 5, t = chunk >> 2, q = chunk & 3u, l = n + 16u * q, w = c & 31u;
         const uint8_t b = o.data[((size_t)T * o.steps + t) * 1024u + 16u * l + (w >> 1)];
         const int nib = (w & 1u) ? (b >> 4) : (b & 0xF);
-        const float s = f16_bits_to_f32(o.scales[((size_t)T * 64u + l) * o.steps + t]);
+        const float s = f16_bits_to_f32(o.scales[((size_t)T * o.steps + t) * 64u + l]);
         return (float)(nib - 8) * s;
     }
     const uint32_t g = c >> 7, t = g >> 2, q = g & 3u, l = n + 16u * q, i = c & 127u;
     if (o.kind == HK_BIN) {
         const uint8_t b = o.data[((size_t)T * o.steps + t) * 1024u + 16u * l + (i >> 3)];
-        const float s = f16_bits_to_f32(o.scales[((size_t)T * 64u + l) * o.steps + t]);
+        const float s = f16_bits_to_f32(o.scales[((size_t)T * o.steps + t) * 64u + l]);
         return ((b >> (i & 7u)) & 1u) ? s : -s;
     }
     const uint4 h = o.hdr[(size_t)T * o.steps + t];
