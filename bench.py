@@ -137,6 +137,22 @@ def moe_bench(ctx, shape, steps, warmup, n_inputs=16):
             "model_device_bytes": dev_bytes, "gen_seconds": round(gen_s, 2), "layers": L}
 
 
+def measured_traffic(workload: str):
+    """HBM bytes per launch of the headline kernel from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (each counter scaled by what it reads for a
+    512 MiB device copy); None if no summary for this workload is present."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        f"gemv_{workload}_streamed.pmc.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        pmc = json.load(f)
+    if pmc.get("workload") != workload:
+        return None
+    return int(round((pmc["fetch_size_kib_per_dispatch"] * pmc["fetch_factor"] +
+                      pmc["write_size_kib_per_dispatch"] * pmc["write_factor"]) * 1024))
+
+
 def moe_batch_bench(ctx, steps, warmup, n_batches=8, T=32):
     """Config 5: the DeepSeek-V3-shaped noaux_tc block on batches of T bf16
     tokens, cycling over n_batches distinct batches (distinct routings)."""
@@ -309,7 +325,7 @@ def main():
                    "organs_per_step": head["organs"], "bytes_per_step": head["bytes"],
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(head["gbps"], 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(head["gbps"] / HBM_PEAK_GBPS, 4), "traffic": None},
+                     "frac": round(head["gbps"] / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(main_name)},
         "cpu_baseline": cpu,
         "parity_spot_check_rel_l2": rel,
         "extra": extra,
