@@ -22,26 +22,33 @@ struct WaveItems {
     }
 };
 
+// Row totals of a finished group of R tiles into the workgroup's LDS row
+// buffer (unscaled; tiles r >= nvalid alias T[0] and are skipped).
 template <int R>
-__device__ __forceinline__ void store_group(const float* acc, const uint32_t* T, int nvalid, uint32_t rows, int E,
-                                            int lane, float* __restrict__ y) {
+__device__ __forceinline__ void flush_group(float* acc, const uint32_t* T, int nvalid, uint32_t t0, int lane,
+                                            float* ysh) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        if (r >= nvalid) break;
         const float v = tile_row_sum(acc[r]);
-        const uint32_t row = T[r] * 16u + (uint32_t)(lane & 15);
-        if (lane < 16 && row < rows) y[row] = ldexpf(v, -E);
+        if (r < nvalid && lane < 16) ysh[(T[r] - t0) * 16u + (uint32_t)lane] = v;
+        acc[r] = 0.0f;
     }
 }
 
+constexpr uint32_t GEMV_MAX_TILES_PER_WG = 32;
+
 // D-deep software pipeline: D fetched steps are in flight while one is
-// consumed; slot d of the rotating buffer holds item it+d.
+// consumed; slot d of the rotating buffer holds item it+d.  The loop body is
+// branch-free in memory operations (refetches are unconditional, past the end
+// they re-read the last item; y goes out through LDS after the loop) so the
+// compiler can wait for exactly the slot being consumed.
 template <int KIND, int R, int D>
 __global__ void __launch_bounds__(256)
 gemv_tiled_kernel(const OrganView* __restrict__ organs, const float* __restrict__ xall, size_t x_stride,
                   float* __restrict__ yall, size_t y_stride, uint32_t tiles_per_wg, uint32_t* status) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float red[4];
+    __shared__ float ysh[GEMV_MAX_TILES_PER_WG * 16];
     const OrganView o = organs[blockIdx.y];
     const float* __restrict__ x = xall + (size_t)blockIdx.y * x_stride;
     float* __restrict__ y = yall + (size_t)blockIdx.y * y_stride;
@@ -50,15 +57,16 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, const float* __restrict_
     const uint32_t t0 = blockIdx.x * tiles_per_wg, t1 = min(t0 + tiles_per_wg, o.n_tiles);
     WaveItems W{t0 + wave * R, 4u * R, t1, o.steps, 0};
     W.n = W.g0 < t1 ? ((t1 - W.g0 + W.gstride - 1) / W.gstride) * o.steps : 0;
+    const uint32_t last = W.n ? W.n - 1u : 0u;
 
     // the first D steps' weight loads go out before the x preparation
     Frag<KIND, R> f[D];
     uint32_t T[D][R], ts[D];
     int nv[D];
+    if (W.n) {
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-        if ((uint32_t)d < W.n) {
-            W.at((uint32_t)d, T[d], R, &nv[d], &ts[d]);
+        for (int d = 0; d < D; ++d) {
+            W.at(min((uint32_t)d, last), T[d], R, &nv[d], &ts[d]);
             fetch_step<KIND, R>(o, T[d], nv[d], ts[d], lane, f[d]);
         }
     }
@@ -71,22 +79,27 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, const float* __restrict_
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-    for (uint32_t it = 0; it < W.n; it += D) {
+    uint32_t it = 0;
+    for (; it + D <= W.n; it += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            if (it + d >= W.n) break;
             compute_step<KIND, R>(f[d], ts[d], nv[d], A, SX, q, acc);
-            if (ts[d] + 1 == o.steps) {
-                store_group<R>(acc, T[d], nv[d], o.rows, E, lane, y);
-#pragma unroll
-                for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-            }
-            const uint32_t nx = it + D + d;
-            if (nx < W.n) {
-                W.at(nx, T[d], R, &nv[d], &ts[d]);
-                fetch_step<KIND, R>(o, T[d], nv[d], ts[d], lane, f[d]);
-            }
+            if (ts[d] + 1 == o.steps) flush_group<R>(acc, T[d], nv[d], t0, lane, ysh);
+            W.at(min(it + D + d, last), T[d], R, &nv[d], &ts[d]);
+            fetch_step<KIND, R>(o, T[d], nv[d], ts[d], lane, f[d]);
         }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        if (it + d >= W.n) break;
+        compute_step<KIND, R>(f[d], ts[d], nv[d], A, SX, q, acc);
+        if (ts[d] + 1 == o.steps) flush_group<R>(acc, T[d], nv[d], t0, lane, ysh);
+    }
+    __syncthreads();
+    const uint32_t nrows = (t1 > t0 ? t1 - t0 : 0u) * 16u;
+    for (uint32_t i = threadIdx.x; i < nrows; i += blockDim.x) {
+        const uint32_t row = t0 * 16u + i;
+        if (row < o.rows) y[row] = ldexpf(ysh[i], -E);
     }
 }
 

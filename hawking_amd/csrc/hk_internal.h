@@ -62,6 +62,25 @@ struct OrganView {
 
 // ------------------------------------------------------------------ device helpers
 
+// Loads through a global-address-space pointer.  Pointers read out of
+// descriptor structs are generic to the compiler, which then emits flat loads;
+// a flat load counts in both vmcnt and lgkmcnt, so every later LDS wait also
+// waits for it and a software prefetch pipeline collapses to depth one.
+template <class T>
+__device__ __forceinline__ T ldg(const T* p) {
+    return *(const __attribute__((address_space(1))) T*)(p);
+}
+typedef unsigned int hk_u32x4 __attribute__((ext_vector_type(4)));
+typedef float hk_f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ldg(const uint4* p) {
+    const hk_u32x4 v = *(const __attribute__((address_space(1))) hk_u32x4*)(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float4 ldg(const float4* p) {
+    const hk_f32x4 v = *(const __attribute__((address_space(1))) hk_f32x4*)(p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
     return static_cast<float>(__builtin_bit_cast(_Float16, b));
 }

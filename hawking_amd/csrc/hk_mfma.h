@@ -194,20 +194,22 @@ struct ImageA {
 // each lane needs (row lane%16 of tile T[r], column slot lane/16).
 template <int KIND, int R>
 struct Frag;
+// Scales stay raw f16 bits until the step is consumed: converting at fetch
+// time would wait for the load there and collapse the prefetch pipeline.
 template <int R>
 struct Frag<HK_BIN, R> {
     uint4 v[R];
-    float s[R];
+    uint16_t s[R];
 };
 template <int R>
 struct Frag<HK_Q4, R> {
     uint4 v[R];
-    float s[R];
+    uint16_t s[R];
 };
 template <int R>
 struct Frag<HK_MIXED, R> {
     uint32_t V[R][8];
-    float s0[R], s1[R];
+    uint16_t s0[R], s1[R];
     bool q2[R];
 };
 
@@ -216,15 +218,15 @@ template <int KIND, int R>
 __device__ __forceinline__ void fetch_one(const OrganView& o, uint32_t T, uint32_t t, int lane, Frag<KIND, R>& f,
                                           int r) {
     if constexpr (KIND == HK_BIN || KIND == HK_Q4) {
-        f.v[r] = *reinterpret_cast<const uint4*>(o.data + ((size_t)T * o.steps + t) * 1024u + 16u * lane);
-        f.s[r] = f16_bits_to_f32(o.scales[((size_t)T * o.steps + t) * 64u + lane]);
+        f.v[r] = ldg(reinterpret_cast<const uint4*>(o.data + ((size_t)T * o.steps + t) * 1024u + 16u * lane));
+        f.s[r] = ldg(o.scales + ((size_t)T * o.steps + t) * 64u + lane);
     } else {
-        const uint4 h = o.hdr[(size_t)T * o.steps + t];
+        const uint4 h = ldg(o.hdr + (size_t)T * o.steps + t);
         const uint32_t below = __builtin_amdgcn_mbcnt_hi(h.y, __builtin_amdgcn_mbcnt_lo(h.x, 0u));
         const bool isq2 = ((lane < 32 ? (h.x >> lane) : (h.y >> (lane - 32))) & 1u) != 0;
         const uint8_t* p = o.data + h.z + 16u * ((uint32_t)lane + below);
-        const uint4 va = *reinterpret_cast<const uint4*>(p);
-        const uint4 vb = *reinterpret_cast<const uint4*>(p + (isq2 ? 16 : 0));
+        const uint4 va = ldg(reinterpret_cast<const uint4*>(p));
+        const uint4 vb = ldg(reinterpret_cast<const uint4*>(p + (isq2 ? 16 : 0)));
         f.V[r][0] = va.x;
         f.V[r][1] = va.y;
         f.V[r][2] = va.z;
@@ -234,8 +236,8 @@ __device__ __forceinline__ void fetch_one(const OrganView& o, uint32_t T, uint32
         f.V[r][6] = vb.z;
         f.V[r][7] = vb.w;
         const uint16_t* spp = o.scales + h.w + (uint32_t)lane + below;
-        f.s0[r] = f16_bits_to_f32(spp[0]);
-        f.s1[r] = f16_bits_to_f32(spp[isq2 ? 1 : 0]);
+        f.s0[r] = ldg(spp);
+        f.s1[r] = ldg(spp + (isq2 ? 1 : 0));
         f.q2[r] = isq2;
     }
 }
@@ -271,7 +273,7 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
         const float sx = (SX[16 * t + 4 * q] + SX[16 * t + 4 * q + 1]) + (SX[16 * t + 4 * q + 2] + SX[16 * t + 4 * q + 3]);
 #pragma unroll
         for (int r = 0; r < R; ++r)
-            if (r < nvalid) acc[r] += f.s[r] * (combine_limbs(c[r]) * (1.0f / 64.0f) - sx);
+            if (r < nvalid) acc[r] += f16_bits_to_f32(f.s[r]) * (combine_limbs(c[r]) * (1.0f / 64.0f) - sx);
     } else if constexpr (KIND == HK_Q4) {
         const uint32_t m = 0x0F0F0F0Fu;
         const v4i alo = A(t * 2), ahi = A(t * 2 + 1);
@@ -286,7 +288,7 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
         const float sx = SX[4 * t + q];
 #pragma unroll
         for (int r = 0; r < R; ++r)
-            if (r < nvalid) acc[r] += f.s[r] * (combine_limbs(c[r]) - 8.0f * sx);
+            if (r < nvalid) acc[r] += f16_bits_to_f32(f.s[r]) * (combine_limbs(c[r]) - 8.0f * sx);
     } else {
         uint32_t V[R][8];
 #pragma unroll
@@ -323,7 +325,7 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
                 if (r >= nvalid) continue;
                 const float alpha = f.q2[r] ? (1.0f / 64.0f) : (2.0f / 64.0f);
                 const float beta = f.q2[r] ? 1.5f : 1.0f;
-                acc[r] += (h ? f.s1[r] : f.s0[r]) * (combine_limbs(c[r]) * alpha - beta * sx);
+                acc[r] += f16_bits_to_f32(h ? f.s1[r] : f.s0[r]) * (combine_limbs(c[r]) * alpha - beta * sx);
             }
         }
     }

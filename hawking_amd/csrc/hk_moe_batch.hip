@@ -327,48 +327,57 @@ __device__ __forceinline__ void tiles_x_tokens(const uint8_t* const* base_d, con
     auto fetch = [&](uint32_t t, Frag<HK_Q4, R>& fr) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            fr.v[r] = *reinterpret_cast<const uint4*>(base_d[r] + (size_t)t * 1024u);
-            fr.s[r] = f16_bits_to_f32(base_s[r][(size_t)t * 64u]);
+            fr.v[r] = ldg(reinterpret_cast<const uint4*>(base_d[r] + (size_t)t * 1024u));
+            fr.s[r] = ldg(base_s[r] + (size_t)t * 64u);
         }
     };
-#pragma unroll
-    for (int k = 0; k < D; ++k)
-        if ((uint32_t)k < S) fetch((uint32_t)k, f[k]);
     const float* SX0 = reinterpret_cast<const float*>(img + (size_t)S * 2u * A_TILE_STRIDE);
-    for (uint32_t it = 0; it < S; it += D) {
+    auto consume = [&](const Frag<HK_Q4, R>& fr, uint32_t t) {
+        v4i alo[TB], ahi[TB];
+        float sx[TB];
 #pragma unroll
-        for (int k = 0; k < D; ++k) {
-            const uint32_t t = it + (uint32_t)k;
-            if (t >= S) break;
-            v4i alo[TB], ahi[TB];
-            float sx[TB];
+        for (int j = 0; j < TB; ++j) {
+            if ((uint32_t)j < nm) {
+                const uint8_t* ij = img + (size_t)j * img_bytes;
+                alo[j] = lds_a(ij, 2u * t, aoff);
+                ahi[j] = lds_a(ij, 2u * t + 1u, aoff);
+                sx[j] = reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(SX0) + (size_t)j * img_bytes)[4u * t + (uint32_t)q];
+            }
+        }
+        const uint32_t m = 0x0F0F0F0Fu;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const v4i lo = {(int)(fr.v[r].x & m), (int)(fr.v[r].y & m), (int)(fr.v[r].z & m), (int)(fr.v[r].w & m)};
+            const v4i hi = {(int)((fr.v[r].x >> 4) & m), (int)((fr.v[r].y >> 4) & m), (int)((fr.v[r].z >> 4) & m),
+                            (int)((fr.v[r].w >> 4) & m)};
+            const float sc = f16_bits_to_f32(fr.s[r]);
 #pragma unroll
             for (int j = 0; j < TB; ++j) {
                 if ((uint32_t)j < nm) {
-                    const uint8_t* ij = img + (size_t)j * img_bytes;
-                    alo[j] = lds_a(ij, 2u * t, aoff);
-                    ahi[j] = lds_a(ij, 2u * t + 1u, aoff);
-                    sx[j] = reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(SX0) + (size_t)j * img_bytes)[4u * t + (uint32_t)q];
+                    v4i c = mfma_i8(alo[j], lo, v4i{0, 0, 0, 0});
+                    c = mfma_i8(ahi[j], hi, c);
+                    acc[j][r] += sc * (combine_limbs(c) - 8.0f * sx[j]);
                 }
             }
-            const uint32_t m = 0x0F0F0F0Fu;
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const v4i lo = {(int)(f[k].v[r].x & m), (int)(f[k].v[r].y & m), (int)(f[k].v[r].z & m),
-                                (int)(f[k].v[r].w & m)};
-                const v4i hi = {(int)((f[k].v[r].x >> 4) & m), (int)((f[k].v[r].y >> 4) & m),
-                                (int)((f[k].v[r].z >> 4) & m), (int)((f[k].v[r].w >> 4) & m)};
-#pragma unroll
-                for (int j = 0; j < TB; ++j) {
-                    if ((uint32_t)j < nm) {
-                        v4i c = mfma_i8(alo[j], lo, v4i{0, 0, 0, 0});
-                        c = mfma_i8(ahi[j], hi, c);
-                        acc[j][r] += f[k].s[r] * (combine_limbs(c) - 8.0f * sx[j]);
-                    }
-                }
-            }
-            if (t + D < S) fetch(t + D, f[k]);
         }
+    };
+    // branch-free pipeline (refetches past the end re-read the last step), so
+    // each consume waits only for its own slot's loads
+    const uint32_t last = S - 1u;
+#pragma unroll
+    for (int k = 0; k < D; ++k) fetch(min((uint32_t)k, last), f[k]);
+    uint32_t it = 0;
+    for (; it + D <= S; it += D) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            consume(f[k], it + (uint32_t)k);
+            fetch(min(it + D + (uint32_t)k, last), f[k]);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+        if (it + (uint32_t)k >= S) break;
+        consume(f[k], it + (uint32_t)k);
     }
 }
 
