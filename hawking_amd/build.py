@@ -3,7 +3,8 @@
 `python -m hawking_amd.build` compiles every source under hawking_amd/csrc
 with hipcc for gfx950 and links one shared library exporting the C ABI of
 include/hawking_hip.h.  Packed-FP32 instruction selection is disabled
-(-packed-fp32-ops) for all device code.
+(-packed-fp32-ops) for all device code, and MFMA accumulators live in
+ordinary VGPRs (-amdgpu-mfma-vgpr-form).
 """
 from __future__ import annotations
 
@@ -25,6 +26,9 @@ CFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Werror",
     "-Wno-unused-command-line-argument",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in ordinary VGPRs: the epilogues read them directly instead
+    # of copying each accumulator out of the AGPR file first
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{os.path.join(ROOT, 'include')}",
 ]
 SOURCES = ["hk_api.cpp", "hk_gemv2.hip", "hk_repack.hip", "hk_pack.hip", "hk_router.hip", "hk_moe.hip",

@@ -104,6 +104,13 @@ static int validate_shape(hk_ctx* ctx, int kind, int group, uint32_t rows, uint3
     }
 }
 
+// The GEMV keeps one organ's x image (and a quantization window) in LDS.
+static int validate_gemv_cols(hk_ctx* ctx, int kind, uint32_t cols) {
+    if (kind == HK_F32 || gemv_lds_bytes(kind, cols) <= GEMV_LDS_LIMIT) return HK_OK;
+    return set_error(ctx, HK_E_GEOMETRY, "organ cols=" + std::to_string(cols) +
+                                             " exceeds the GEMV's LDS x image (at most ~12000 columns)");
+}
+
 static Layout layout_for(int kind, int group, uint32_t rows, uint32_t cols, uint32_t n_bin,
                          uint32_t n_q2) {
     Layout L;
@@ -165,6 +172,7 @@ static CanonView place(int kind, int group, uint32_t rows, uint32_t cols, const 
 static int validate_src(hk_ctx* ctx, const hk_organ_src* s, Layout* out) {
     if (!s) return set_error(ctx, HK_E_INVALID_ARG, "organ source is NULL");
     int rc = validate_shape(ctx, s->kind, s->group, s->rows, s->cols);
+    if (!rc) rc = validate_gemv_cols(ctx, s->kind, s->cols);
     if (rc) return rc;
     const size_t n = (size_t)s->rows * s->cols;
     if (s->kind == HK_Q4 || s->kind == HK_BIN) {
@@ -472,7 +480,6 @@ extern "C" int hk_organ_info(const hk_organ* o, int32_t* kind, int32_t* group, u
     if (packed_bytes) *packed_bytes = o->packed_bytes;
     return HK_OK;
 }
-
 static int check_vectors(hk_ctx* ctx, const char* fn, const float* x, size_t x_stride, const float* y,
                          size_t y_stride, uint32_t n, const OrganView& f) {
     if (!x || !y) return set_error(ctx, HK_E_INVALID_ARG, std::string(fn) + ": NULL vector");
@@ -576,6 +583,7 @@ extern "C" int hk_organ_synthetic(hk_ctx* ctx, int32_t kind, int32_t group, uint
     *out = nullptr;
     if (kind == HK_BIN || kind == HK_MIXED) group = 128;
     int rc = validate_shape(ctx, kind, group, rows, cols);
+    if (!rc) rc = validate_gemv_cols(ctx, kind, cols);
     if (rc) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
     void* tmp = nullptr;

@@ -1,8 +1,9 @@
 // hk_gemv2.hip -- GEMV over sets of packed organs on the int8 matrix cores
 // (engine in hk_mfma.h), plus the dense f32 GEMV used for the router.
 //
-// Grid: (workgroups per organ, organs).  A workgroup of 4 waves prepares the
-// x limbs once in LDS, then each wave walks groups of R consecutive row tiles
+// Grid: (workgroups per organ, organs).  A workgroup of 4 waves loads x once
+// (ahead of its first weight loads), builds the x image in LDS, then each wave
+// walks groups of R consecutive row tiles
 // (16 rows each) of its slice of the organ; one LDS operand fetch feeds the R
 // tiles' MFMAs and the next step's weight loads are in flight while the
 // current step computes.
@@ -42,7 +43,7 @@ constexpr uint32_t GEMV_MAX_TILES_PER_WG = 32;
 // branch-free in memory operations (refetches are unconditional, past the end
 // they re-read the last item; y goes out through LDS after the loop) so the
 // compiler can wait for exactly the slot being consumed.
-template <int KIND, int R, int D>
+template <int KIND, int R, int D, int NC>
 __global__ void __launch_bounds__(256)
 gemv_tiled_kernel(const OrganView* __restrict__ organs, const float* __restrict__ xall, size_t x_stride,
                   float* __restrict__ yall, size_t y_stride, uint32_t tiles_per_wg, uint32_t* status) {
@@ -59,19 +60,25 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, const float* __restrict_
     W.n = W.g0 < t1 ? ((t1 - W.g0 + W.gstride - 1) / W.gstride) * o.steps : 0;
     const uint32_t last = W.n ? W.n - 1u : 0u;
 
-    // the first D steps' weight loads go out before the x preparation
+    // x first, then the first D steps' weight loads, all before the image build
+    XChunks<NC> xc;
+    load_x<NC>(BlockTeam{}, x, o.cols, xc);
     Frag<KIND, R> f[D];
     uint32_t T[D][R], ts[D];
     int nv[D];
-    if (W.n) {
+    {
+        // unconditional, so the x wait below counts exactly these loads; a
+        // wave without items re-reads the workgroup's first tile
+        const WaveItems P = W.n ? W : WaveItems{t0, 4u * R, t0 + 1u, o.steps, 1u};
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            W.at(min((uint32_t)d, last), T[d], R, &nv[d], &ts[d]);
+            P.at(min((uint32_t)d, last), T[d], R, &nv[d], &ts[d]);
             fetch_step<KIND, R>(o, T[d], nv[d], ts[d], lane, f[d]);
         }
     }
     bool bad = false;
-    const int E = prepare_x<KIND>(BlockTeam{}, x, o.cols, o.steps, lds, red, &bad);
+    float* xq = reinterpret_cast<float*>(lds + x_lds_bytes<KIND>(o.steps));
+    const int E = x_image<KIND, NC>(BlockTeam{}, xc, x, o.cols, o.steps, lds, xq, 0u, red, &bad);
     if (bad && threadIdx.x == 0 && status) atomicOr(status, 1u);
     const ImageA A{lds, a_lane_offset(lane)};
     const float* SX = reinterpret_cast<const float*>(lds + (size_t)o.steps * Kcfg<KIND>::P * A_TILE_STRIDE);
@@ -83,7 +90,7 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, const float* __restrict_
     for (; it + D <= W.n; it += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            compute_step<KIND, R>(f[d], ts[d], nv[d], A, SX, q, acc);
+            compute_step<KIND, R>(f[d], ts[d], A, SX, q, acc);
             if (ts[d] + 1 == o.steps) flush_group<R>(acc, T[d], nv[d], t0, lane, ysh);
             W.at(min(it + D + d, last), T[d], R, &nv[d], &ts[d]);
             fetch_step<KIND, R>(o, T[d], nv[d], ts[d], lane, f[d]);
@@ -92,7 +99,7 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, const float* __restrict_
 #pragma unroll
     for (int d = 0; d < D; ++d) {
         if (it + d >= W.n) break;
-        compute_step<KIND, R>(f[d], ts[d], nv[d], A, SX, q, acc);
+        compute_step<KIND, R>(f[d], ts[d], A, SX, q, acc);
         if (ts[d] + 1 == o.steps) flush_group<R>(acc, T[d], nv[d], t0, lane, ysh);
     }
     __syncthreads();
@@ -122,13 +129,26 @@ __global__ void __launch_bounds__(256) gemv_f32_kernel(const OrganView* __restri
     if (lane == 0) yall[(size_t)blockIdx.y * y_stride + row] = acc;
 }
 
+size_t gemv_lds_bytes(int kind, uint32_t cols) {
+    const uint32_t S = n_steps_for(kind, cols), kc = S * tile_step_cols(kind);
+    const size_t img = kind == HK_Q4 ? x_lds_bytes<HK_Q4>(S) : kind == HK_BIN ? x_lds_bytes<HK_BIN>(S) : x_lds_bytes<HK_MIXED>(S);
+    return img + (size_t)min(kc, 2048u) * sizeof(float);
+}
+
 template <int KIND, int R, int D>
 static hipError_t launch_kind(const OrganView* organs, uint32_t n, const OrganView& sh, const float* x,
                               size_t xs, float* y, size_t ys, uint32_t tpw, hipStream_t s) {
     const dim3 grid((sh.n_tiles + tpw - 1) / tpw, n);
-    const size_t lds = x_lds_bytes<KIND>(sh.steps);
-    hipLaunchKernelGGL((gemv_tiled_kernel<KIND, R, D>), grid, dim3(256), lds, s, organs, x, xs, y, ys, tpw,
-                       nullptr);
+    // image + one quantization window (2048 columns); x chunks held in
+    // registers: one per thread up to 2048 columns, else four
+    const uint32_t kc = x_image_cols<KIND>(sh.steps);
+    const size_t lds = gemv_lds_bytes(sh.kind, sh.cols);
+    if (kc <= 2048u)
+        hipLaunchKernelGGL((gemv_tiled_kernel<KIND, R, D, 1>), grid, dim3(256), lds, s, organs, x, xs, y, ys, tpw,
+                           nullptr);
+    else
+        hipLaunchKernelGGL((gemv_tiled_kernel<KIND, R, D, 4>), grid, dim3(256), lds, s, organs, x, xs, y, ys, tpw,
+                           nullptr);
     return hipGetLastError();
 }
 

@@ -160,6 +160,9 @@ int ensure_scratch(hk_ctx* ctx, size_t bytes, void** out);
 
 // Kernel launchers (defined in the .hip files); all stream-ordered, no sync.
 // GEMV over n organs of one kind/shape (descriptor table in device memory).
+// Dynamic LDS of the GEMV kernel for a packed organ of `cols` columns.
+size_t gemv_lds_bytes(int kind, uint32_t cols);
+constexpr size_t GEMV_LDS_LIMIT = 60 * 1024;
 hipError_t launch_gemv_tiled(const OrganView* organs_dev, uint32_t n, const OrganView& shape,
                              const float* x, size_t x_stride, float* y, size_t y_stride,
                              hipStream_t s);

@@ -14,8 +14,12 @@
 //   * The B operand (64 x 16) comes straight from the packed bytes with one AND
 //     per 4 weights: a binary bit plane s is bytes & (0x01 << s) = bit * 2^s, a
 //     Q4 nibble plane is bytes & 0x0F, a Q2 field is bytes & (0x03 << 2u); the
-//     power of two is folded into the A limbs (X * 2^(7-s) etc.).
-//   * Per (row, group) the four int32 limbs are combined in f32, the zero
+//     power of two is folded into the A limbs (X * 2^(7-s) etc.).  Binary plane
+//     7 is the raw signed byte (no AND): its A row is -X7 and every lower
+//     plane's A row carries +X7, which cancels the lower bits the raw byte
+//     brings in (sum_s<7 (X_s 2^(7-s) + X7) 2^s b_s - X7 byte = 128 sum X_s b_s).
+//   * Per (row, group) the four int32 limbs are combined (pairs exactly in
+//     int32, then one f32 fma), the zero
 //     point is removed with the group's sum of X (binary: sum (2b-1) X =
 //     2 sum bX - sum X; Q4: sum (n-8) X; Q2: sum (c-1.5) X) and the f16 group
 //     scale is applied; y = 2^-E * sum over groups.
@@ -42,64 +46,61 @@ __device__ __forceinline__ v4i mfma_i8(const v4i& a, const v4i& b, const v4i& c)
 
 template <int KIND>
 struct Kcfg;
+// P = A tiles per step, SXG = columns per x-sum (the zero-point granularity a
+// lane needs per step: one binary group, one Q4 group of 32, one Q2 half-group).
 template <>
 struct Kcfg<HK_BIN> {
-    static constexpr int P = 8, STEP_COLS = 512, DATA = 16;
+    static constexpr int P = 8, STEP_COLS = 512, DATA = 16, SXG = 128;
 };
 template <>
 struct Kcfg<HK_Q4> {
-    static constexpr int P = 2, STEP_COLS = 128, DATA = 16;
+    static constexpr int P = 2, STEP_COLS = 128, DATA = 16, SXG = 32;
 };
 template <>
 struct Kcfg<HK_MIXED> {
-    static constexpr int P = 8, STEP_COLS = 512, DATA = 32;
+    static constexpr int P = 8, STEP_COLS = 512, DATA = 32, SXG = 64;
 };
 
 constexpr int A_TILE_STRIDE = 272;  // 256 B of active-lane limbs + 16 B of zeros
 
-// LDS bytes needed by prepare_x for an organ with `steps` steps.
+// Bytes of the x image of an organ with `steps` steps: the A tiles, then the
+// per-SXG-column sums of X (as f32).
 template <int KIND>
 __host__ __device__ constexpr size_t x_lds_bytes(uint32_t steps) {
-    return (size_t)steps * Kcfg<KIND>::P * A_TILE_STRIDE + (size_t)steps * Kcfg<KIND>::STEP_COLS / 32 * 4;
+    return (size_t)steps * Kcfg<KIND>::P * A_TILE_STRIDE + (size_t)steps * (Kcfg<KIND>::STEP_COLS / Kcfg<KIND>::SXG) * 4;
 }
-
-__device__ __forceinline__ float combine_limbs(const v4i& c) {
-    return (float)c[0] + 256.0f * (float)c[1] + 65536.0f * (float)c[2] + 16777216.0f * (float)c[3];
-}
-
-__device__ __forceinline__ int32_t fixed_x(const float* __restrict__ x, uint32_t c, uint32_t cols, int E) {
-    return c < cols ? __float2int_rn(ldexpf(x[c], E)) : 0;
-}
-
-// Value Y of A byte i (0..15) for step t, MFMA mu, column slot q.
+// Columns of the image: cols rounded up to whole steps.
 template <int KIND>
-__device__ __forceinline__ int32_t a_value(const float* __restrict__ x, uint32_t cols, int E, int t, int mu, int q,
-                                           int i) {
+__host__ __device__ constexpr uint32_t x_image_cols(uint32_t steps) {
+    return steps * (uint32_t)Kcfg<KIND>::STEP_COLS;
+}
+
+// c[0] + 2^8 c[1] + 2^16 c[2] + 2^24 c[3].  Every limb sum is below 2^21 in
+// magnitude (at most 128 products of a limb byte and a B byte, each <= 2^14),
+// so each pair combines exactly in int32 before the one f32 rounding.
+__device__ __forceinline__ float combine_limbs(const v4i& c) {
+    const int lo = c[0] + c[1] * 256, hi = c[2] + c[3] * 256;
+    return __builtin_fmaf((float)hi, 65536.0f, (float)lo);
+}
+
+// Value of A byte i (0..15) for step t, MFMA mu, column slot q, from the
+// quantized x (X as exact integer-valued floats, zero past cols).
+template <int KIND>
+__device__ __forceinline__ int32_t a_value(const float* xq, int t, int mu, int q, int i) {
+    auto X = [&](uint32_t c) { return (int32_t)xq[c]; };
     if constexpr (KIND == HK_BIN) {
-        const int32_t v = fixed_x(x, (uint32_t)(t * 512 + q * 128 + 8 * i + mu), cols, E);
-        return mu < 7 ? (v << (7 - mu)) : -v;
+        const uint32_t c0 = (uint32_t)(t * 512 + q * 128 + 8 * i);
+        const int32_t v7 = X(c0 + 7u);
+        if (mu == 7) return -v7;
+        return X(c0 + (uint32_t)mu) * (1 << (7 - mu)) + v7;
     } else if constexpr (KIND == HK_Q4) {
-        return fixed_x(x, (uint32_t)(t * 128 + q * 32 + 2 * i + mu), cols, E);
+        return X((uint32_t)(t * 128 + q * 32 + 2 * i + mu));
     } else {
         const int h = mu >> 2, u = mu & 3, r = i >> 2, j = i & 3;
         const int a = r < 2 ? 2 * h + r : 2 * h + 2 + r;
-        const int32_t v =
-            fixed_x(x, (uint32_t)(t * 512 + q * 128) + mixed_q2_col((uint32_t)a, (uint32_t)j, (uint32_t)u), cols, E);
-        return v << (u < 3 ? 6 - 2 * u : 6);
+        const int32_t v = X((uint32_t)(t * 512 + q * 128) + mixed_q2_col((uint32_t)a, (uint32_t)j, (uint32_t)u));
+        return v * (1 << (u < 3 ? 6 - 2 * u : 6));
     }
-}
-
-__device__ __forceinline__ float block_max_abs(const float* __restrict__ x, uint32_t n, float* red) {
-    float m = 0.0f;
-    for (uint32_t c = threadIdx.x; c < n; c += blockDim.x) m = fmaxf(m, fabsf(x[c]));
-    m = wave_max(m);
-    const int nw = (int)(blockDim.x >> 6);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-    __syncthreads();
-    float r = red[0];
-    for (int w = 1; w < nw; ++w) r = fmaxf(r, red[w]);
-    return r;
 }
 
 // The threads that build one x image together: the whole block, or one wave
@@ -107,8 +108,15 @@ __device__ __forceinline__ float block_max_abs(const float* __restrict__ x, uint
 struct BlockTeam {
     __device__ uint32_t idx() const { return threadIdx.x; }
     __device__ uint32_t size() const { return blockDim.x; }
-    __device__ float max_abs(const float* __restrict__ x, uint32_t n, float* red) const {
-        return block_max_abs(x, n, red);
+    __device__ float reduce_max(float m, float* red) const {
+        m = wave_max(m);
+        const int nw = (int)(blockDim.x >> 6);
+        __syncthreads();
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+        __syncthreads();
+        float r = red[0];
+        for (int w = 1; w < nw; ++w) r = fmaxf(r, red[w]);
+        return r;
     }
     __device__ void sync() const { __syncthreads(); }
 };
@@ -116,61 +124,140 @@ struct WaveTeam {
     uint32_t lane;
     __device__ uint32_t idx() const { return lane; }
     __device__ uint32_t size() const { return 64u; }
-    __device__ float max_abs(const float* __restrict__ x, uint32_t n, float*) const {
-        float m = 0.0f;
-        for (uint32_t c = lane; c < n; c += 64u) m = fmaxf(m, fabsf(x[c]));
-        return wave_max(m);
-    }
+    __device__ float reduce_max(float m, float*) const { return wave_max(m); }
     __device__ void sync() const {}
 };
 
-// The x image: A tiles and per-32-column sums of X written to `lds`
-// (x_lds_bytes<KIND>(steps) bytes; any address space), built by `team`.
-// Returns E; non-finite x sets the flag.  A block team ends with
-// __syncthreads(); a wave team leaves ordering to the caller.
-template <int KIND, class Team>
-__device__ int prepare_x(const Team& team, const float* __restrict__ x, uint32_t cols, uint32_t steps, uint8_t* lds,
-                         float* red, bool* nonfinite) {
-    constexpr int P = Kcfg<KIND>::P, SC = Kcfg<KIND>::STEP_COLS;
-    float m = team.max_abs(x, cols, red);
-    *nonfinite = !isfinite(m);
-    if (*nonfinite) m = 0.0f;
+// x is consumed in chunks of 8 consecutive columns: team member m owns chunks
+// m, m + size, m + 2 size, ...  The first NC of them are loaded into
+// registers by load_x, which a kernel issues before its weight prefetch so
+// that waiting for x does not wait for the weights; later chunks are read
+// from x again when needed.  Requires cols % 8 == 0 and a 16-byte aligned x.
+template <int NC>
+struct XChunks {
+    float4 v[NC][2];
+};
+
+__device__ __forceinline__ void load_chunk(const float* x, uint32_t c0, uint32_t cols, float4* v) {
+    if (c0 < cols) {
+        v[0] = *reinterpret_cast<const float4*>(x + c0);
+        v[1] = *reinterpret_cast<const float4*>(x + c0 + 4);
+    } else {
+        v[0] = v[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+}
+
+template <int NC, class Team>
+__device__ __forceinline__ void load_x(const Team& team, const float* x, uint32_t cols, XChunks<NC>& xc) {
+#pragma unroll
+    for (int j = 0; j < NC; ++j) load_chunk(x, 8u * (team.idx() + (uint32_t)j * team.size()), cols, xc.v[j]);
+}
+
+__device__ __forceinline__ float max_abs8(const float4* v) {
+    return fmaxf(fmaxf(fmaxf(fabsf(v[0].x), fabsf(v[0].y)), fmaxf(fabsf(v[0].z), fabsf(v[0].w))),
+                 fmaxf(fmaxf(fabsf(v[1].x), fabsf(v[1].y)), fmaxf(fabsf(v[1].z), fabsf(v[1].w))));
+}
+
+__device__ __forceinline__ int32_t quantize8(const float4* v, int E, float* f) {
+    const float in[8] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w};
+    int32_t s = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        f[k] = rintf(ldexpf(in[k], E));
+        s += (int32_t)f[k];
+    }
+    return s;
+}
+
+// The x image: fixed-point x (E = 23 - exponent of max|x|; 0 for x = 0 or
+// non-finite x, which sets the flag), X = rint(x 2^E), and from it the A tiles
+// and the per-SXG-column sums of X, written to img (x_lds_bytes<KIND>(steps)
+// bytes, any address space).  Returns E.
+//
+// The image columns (cols rounded up to whole steps, zero past cols) go in
+// rounds of 8 * team size columns: each member quantizes its chunk of the
+// round into the LDS window xq + j * xq_stride (exact integer-valued floats),
+// then the team builds the round's steps from the window.  xq_stride = 0
+// reuses one window of min(image columns, 8 * team size) floats; with
+// xq_stride = 8 * team size and xq == x (x staged in LDS with room for the
+// image columns) x is quantized in place, every chunk being read and
+// rewritten by its owner only.  8 * team size must be a multiple of the
+// step's columns.  Ends with team.sync().
+template <int KIND, int NC, class Team>
+__device__ int x_image(const Team& team, const XChunks<NC>& xc, const float* x, uint32_t cols, uint32_t steps,
+                       uint8_t* img, float* xq, uint32_t xq_stride, float* red, bool* nonfinite) {
+    constexpr int P = Kcfg<KIND>::P, SC = Kcfg<KIND>::STEP_COLS, NL = Kcfg<KIND>::SXG / 8;
+    const uint32_t me = team.idx(), ts = team.size();
+    const uint32_t nch = steps * (uint32_t)SC / 8u, wcols = 8u * ts, rounds = (nch + ts - 1u) / ts;
+    float* SX = reinterpret_cast<float*>(img + (size_t)steps * P * A_TILE_STRIDE);
+    uint32_t* A = reinterpret_cast<uint32_t*>(img);
+
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) m = fmaxf(m, max_abs8(xc.v[j]));
+    for (uint32_t j = NC; j < rounds; ++j) {
+        float4 v[2];
+        load_chunk(x, 8u * (me + j * ts), cols, v);
+        m = fmaxf(m, max_abs8(v));
+    }
+    m = team.reduce_max(m, red);
+    const bool bad = !isfinite(m);
+    *nonfinite = bad;
     int e2 = 0;
-    if (m > 0.0f) (void)frexpf(m, &e2);
-    const int E = m > 0.0f ? 23 - e2 : 0;
-    const int ntau = (int)steps * P;
-    uint32_t* A = reinterpret_cast<uint32_t*>(lds);
-    float* SX = reinterpret_cast<float*>(lds + (size_t)ntau * A_TILE_STRIDE);
-    const int ti = (int)team.idx(), ts = (int)team.size();
-    // zero blocks
-    for (int i = ti; i < ntau * 4; i += ts) A[(i >> 2) * (A_TILE_STRIDE / 4) + 64 + (i & 3)] = 0u;
-    // unit = (tau, slot q, dword d): 4 A bytes -> 4 lanes' dwords via a byte transpose
-    for (int u = ti; u < ntau * 16; u += ts) {
-        const int d = u & 3, q = (u >> 2) & 3, tau = u >> 4;
-        const int t = tau / P, mu = tau % P;
-        uint32_t z[4];
+    if (!bad && m > 0.0f) (void)frexpf(m, &e2);
+    const int E = (!bad && m > 0.0f) ? 23 - e2 : 0;
+
+    for (int i = (int)me; i < (int)steps * P * 4; i += (int)ts) A[(i >> 2) * (A_TILE_STRIDE / 4) + 64 + (i & 3)] = 0u;
+
+    auto round = [&](uint32_t j, float4* v) {
+        float* w = xq + j * xq_stride;
+        const uint32_t ch = me + j * ts;
+        if (ch < nch) {
+            if (bad) v[0] = v[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            float f[8];
+            int32_t s = quantize8(v, E, f);
+            float4* o = reinterpret_cast<float4*>(w + 8u * me);
+            o[0] = make_float4(f[0], f[1], f[2], f[3]);
+            o[1] = make_float4(f[4], f[5], f[6], f[7]);
+            // a sum's NL chunks belong to NL consecutive members, all active together
 #pragma unroll
-        for (int jb = 0; jb < 4; ++jb)
-            z[jb] = ((uint32_t)a_value<KIND>(x, cols, E, t, mu, q, 4 * d + jb) + 0x80808080u) ^ 0x80808080u;
-#pragma unroll
-        for (int L = 0; L < 4; ++L) {
-            // v_perm: selector 0..3 = byte of the second operand, 4..7 = byte of the first, 0x0c = 0
-            const uint32_t lo = __builtin_amdgcn_perm(z[1], z[0], 0x0c0c0400u | (uint32_t)L | ((uint32_t)L << 8));
-            const uint32_t hi = __builtin_amdgcn_perm(z[3], z[2], 0x04000c0cu | ((uint32_t)L << 16) | ((uint32_t)L << 24));
-            A[tau * (A_TILE_STRIDE / 4) + (4 * q + L) * 4 + d] = lo | hi;
+            for (int k = 1; k < NL; k <<= 1) s += __shfl_xor(s, k, 64);
+            if ((me & (uint32_t)(NL - 1)) == 0) SX[ch / (uint32_t)NL] = (float)s;
         }
-    }
-    // per-32-column sums: 8 columns per thread, 4 consecutive lanes per block
-    const uint32_t kcols = steps * (uint32_t)SC;
-    for (uint32_t c0 = (uint32_t)ti * 8u; c0 < kcols; c0 += (uint32_t)ts * 8u) {
-        int32_t s = 0;
+        team.sync();
+        // this round's steps; unit = (tau, slot q, dword d): 4 A bytes -> 4
+        // lanes' dwords via a byte transpose
+        const uint32_t t0 = j * (wcols / (uint32_t)SC), t1 = min(t0 + wcols / (uint32_t)SC, steps);
+        const int nunits = (int)(t1 - t0) * P * 16;
+        for (int u = (int)me; u < nunits; u += (int)ts) {
+            const int d = u & 3, q = (u >> 2) & 3, tl = u >> 4;
+            const int t = tl / P, mu = tl % P;
+            uint32_t z[4];
 #pragma unroll
-        for (uint32_t k = 0; k < 8; ++k) s += fixed_x(x, c0 + k, cols, E);
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
-        if ((ti & 3) == 0) SX[c0 / 32u] = (float)s;
+            for (int jb = 0; jb < 4; ++jb)
+                z[jb] = ((uint32_t)a_value<KIND>(w, t, mu, q, 4 * d + jb) + 0x80808080u) ^ 0x80808080u;
+            const uint32_t tau = t0 * (uint32_t)P + (uint32_t)tl;
+#pragma unroll
+            for (int L = 0; L < 4; ++L) {
+                // v_perm: selector 0..3 = byte of the second operand, 4..7 = byte of the first, 0x0c = 0
+                const uint32_t lo = __builtin_amdgcn_perm(z[1], z[0], 0x0c0c0400u | (uint32_t)L | ((uint32_t)L << 8));
+                const uint32_t hi = __builtin_amdgcn_perm(z[3], z[2], 0x04000c0cu | ((uint32_t)L << 16) | ((uint32_t)L << 24));
+                A[tau * (A_TILE_STRIDE / 4) + (4 * q + L) * 4 + d] = lo | hi;
+            }
+        }
+        team.sync();
+    };
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        if ((uint32_t)j >= rounds) break;
+        float4 v[2] = {xc.v[j][0], xc.v[j][1]};
+        round((uint32_t)j, v);
     }
-    team.sync();
+    for (uint32_t j = NC; j < rounds; ++j) {
+        float4 v[2];
+        load_chunk(x, 8u * (me + j * ts), cols, v);
+        round(j, v);
+    }
     return E;
 }
 
@@ -251,11 +338,11 @@ __device__ __forceinline__ void fetch_step(const OrganView& o, const uint32_t* T
 }
 
 // Consume one fetched step: acc[r] += this lane's partial dot, in units of
-// 2^-E.  Tiles r >= nvalid are computed on aliased data and discarded.
+// 2^-E (slots fetched for aliased tiles accumulate junk the caller drops).
 // A(tau) yields this lane's A operand of x-image tile tau.
 template <int KIND, int R, class ASrc>
-__device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t, int nvalid, const ASrc& A,
-                                             const float* SX, int q, float* acc) {
+__device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t, const ASrc& A, const float* SX,
+                                             int q, float* acc) {
     v4i c[R];
     if constexpr (KIND == HK_BIN) {
 #pragma unroll
@@ -263,17 +350,17 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
 #pragma unroll
         for (int p = 0; p < 8; ++p) {
             const v4i a = A(t * 8 + p);
-            const uint32_t m = 0x01010101u << p;
+            const uint32_t m = p < 7 ? 0x01010101u << p : 0xFFFFFFFFu;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const v4i b = {(int)(f.v[r].x & m), (int)(f.v[r].y & m), (int)(f.v[r].z & m), (int)(f.v[r].w & m)};
+                const v4i b = p < 7 ? v4i{(int)(f.v[r].x & m), (int)(f.v[r].y & m), (int)(f.v[r].z & m), (int)(f.v[r].w & m)}
+                                    : v4i{(int)f.v[r].x, (int)f.v[r].y, (int)f.v[r].z, (int)f.v[r].w};
                 c[r] = mfma_i8(a, b, c[r]);
             }
         }
-        const float sx = (SX[16 * t + 4 * q] + SX[16 * t + 4 * q + 1]) + (SX[16 * t + 4 * q + 2] + SX[16 * t + 4 * q + 3]);
+        const float sx = SX[4 * t + q];
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (r < nvalid) acc[r] += f16_bits_to_f32(f.s[r]) * (combine_limbs(c[r]) * (1.0f / 64.0f) - sx);
+        for (int r = 0; r < R; ++r) acc[r] += f16_bits_to_f32(f.s[r]) * (combine_limbs(c[r]) * (1.0f / 64.0f) - sx);
     } else if constexpr (KIND == HK_Q4) {
         const uint32_t m = 0x0F0F0F0Fu;
         const v4i alo = A(t * 2), ahi = A(t * 2 + 1);
@@ -287,8 +374,7 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
         }
         const float sx = SX[4 * t + q];
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (r < nvalid) acc[r] += f16_bits_to_f32(f.s[r]) * (combine_limbs(c[r]) - 8.0f * sx);
+        for (int r = 0; r < R; ++r) acc[r] += f16_bits_to_f32(f.s[r]) * (combine_limbs(c[r]) - 8.0f * sx);
     } else {
         uint32_t V[R][8];
 #pragma unroll
@@ -319,10 +405,9 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
                     c[r] = mfma_i8(a, b, c[r]);
                 }
             }
-            const float sx = SX[16 * t + 4 * q + 2 * h] + SX[16 * t + 4 * q + 2 * h + 1];
+            const float sx = SX[8 * t + 2 * q + h];
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                if (r >= nvalid) continue;
                 const float alpha = f.q2[r] ? (1.0f / 64.0f) : (2.0f / 64.0f);
                 const float beta = f.q2[r] ? 1.5f : 1.0f;
                 acc[r] += f16_bits_to_f32(h ? f.s1[r] : f.s0[r]) * (combine_limbs(c[r]) * alpha - beta * sx);

@@ -34,8 +34,11 @@ size_t moe_img_bytes(int kind, uint32_t H) {
 
 size_t moe_gate_up_lds_bytes(int kind, uint32_t H) { return moe_img_bytes(kind, H) + 4 * 32 * sizeof(float); }
 
+// Floats of x staging for an image of `cols` columns (cols rounded up to whole steps).
+static uint32_t stage_floats(int kind, uint32_t cols) { return n_steps_for(kind, cols) * tile_step_cols(kind); }
+
 size_t moe_down_lds_bytes(int kind, uint32_t Imax, uint32_t slots) {
-    return (size_t)slots * (moe_img_bytes(kind, Imax) + 16 * sizeof(float) + (size_t)Imax * sizeof(float));
+    return (size_t)slots * (moe_img_bytes(kind, Imax) + 16 * sizeof(float) + (size_t)stage_floats(kind, Imax) * sizeof(float));
 }
 
 // Float4s of h (per thread) and of a router row (per lane) held in registers:
@@ -50,7 +53,7 @@ __device__ __forceinline__ float dot4(const float4& a, const float4& b) {
 template <int KIND>
 __global__ void __launch_bounds__(256) moe_route_kernel(MoeDims d, MoeLayerDev L, const float* __restrict__ h,
                                                         MoeWs ws) {
-    extern __shared__ __align__(16) float xn[];  // [H]
+    extern __shared__ __align__(16) float xn[];  // [H rounded up to whole steps]
     __shared__ float red[4];
     const int lane = threadIdx.x & 63;
     const uint32_t wave = threadIdx.x >> 6;
@@ -110,9 +113,12 @@ __global__ void __launch_bounds__(256) moe_route_kernel(MoeDims d, MoeLayerDev L
         }
     }
     if (blockIdx.x == nrb) {
-        // the x image of xn for every gate/up organ of this layer
+        // the x image of xn for every gate/up organ of this layer (xn quantized in place)
         bool bad = false;
-        const int E = prepare_x<KIND>(BlockTeam{}, xn, d.H, n_steps_for(KIND, d.H), ws.img, red, &bad);
+        const uint32_t S = n_steps_for(KIND, d.H);
+        XChunks<1> xc;
+        load_x<1>(BlockTeam{}, xn, d.H, xc);
+        const int E = x_image<KIND, 1>(BlockTeam{}, xc, xn, d.H, S, ws.img, xn, 8u * blockDim.x, red, &bad);
         if (threadIdx.x == 0) {
             ws.img_e[0] = E;
             if (bad) atomicOr(ws.status, HK_DEVERR_NONFINITE);
@@ -184,7 +190,7 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeWs ws) {
 #pragma unroll
         for (int k = 0; k < D; ++k) {
             if (it + k >= n) break;
-            compute_step<KIND, 2>(f[k], s0 + it + k, 2, A, SX, q, acc);
+            compute_step<KIND, 2>(f[k], s0 + it + k, A, SX, q, acc);
             const uint32_t nx = it + D + k;
             if (nx < n) {
                 fetch_one<KIND, 2>(g, T, s0 + nx, lane, f[k], 0);
@@ -231,7 +237,8 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, const float* 
     // this slot's activations: staged in LDS with one batch of loads, then
     // turned into an x image of the slot's own
     uint8_t* img = lds + (size_t)slot * img_stride;
-    float* xs = reinterpret_cast<float*>(lds + (size_t)slots * (img_stride + 64u)) + (size_t)slot * d.Imax;
+    const uint32_t kst = x_image_cols<KIND>(n_steps_for(KIND, d.Imax));
+    float* xs = reinterpret_cast<float*>(lds + (size_t)slots * (img_stride + 64u)) + (size_t)slot * kst;
     if (active) {
         const float4* a4 = reinterpret_cast<const float4*>(ws.act + (size_t)slot * d.Imax);
         for (uint32_t j = (uint32_t)lane; j < o.cols / 4u; j += 64u) reinterpret_cast<float4*>(xs)[j] = a4[j];
@@ -240,7 +247,10 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, const float* 
     int E = 0;
     if (active) {
         bool bad = false;
-        E = prepare_x<KIND>(WaveTeam{(uint32_t)lane}, xs, o.cols, S, img, nullptr, &bad);
+        const WaveTeam team{(uint32_t)lane};
+        XChunks<1> xc;
+        load_x<1>(team, xs, o.cols, xc);
+        E = x_image<KIND, 1>(team, xc, xs, o.cols, S, img, xs, 8u * 64u, nullptr, &bad);
         if (bad && lane == 0) atomicOr(ws.status, HK_DEVERR_NONFINITE);
     }
     __syncthreads();
@@ -251,7 +261,7 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, const float* 
 #pragma unroll
         for (int k = 0; k < D; ++k) {
             if (it + k >= S) break;
-            compute_step<KIND, 1>(f[k], it + k, 1, A, SX, q, acc);
+            compute_step<KIND, 1>(f[k], it + k, A, SX, q, acc);
             const uint32_t nx = it + D + k;
             if (nx < S) fetch_one<KIND, 1>(o, T, nx, lane, f[k], 0);
         }
@@ -276,8 +286,8 @@ static hipError_t launch_layer(const MoeDims& d, const MoeLayerDev& L, const flo
     const uint32_t slots = d.K + (d.has_shared ? 1u : 0u);
     const uint32_t gu_tiles = n_tiles_for(d.has_shared ? max(d.I, d.SI) : d.I);
     const uint32_t img_stride = (uint32_t)moe_img_bytes(KIND, d.Imax);
-    hipLaunchKernelGGL(moe_route_kernel<KIND>, dim3(nrb + 1u), dim3(256), (size_t)d.H * sizeof(float), s, d, L, h_in,
-                       ws);
+    hipLaunchKernelGGL(moe_route_kernel<KIND>, dim3(nrb + 1u), dim3(256), (size_t)stage_floats(KIND, d.H) * sizeof(float),
+                       s, d, L, h_in, ws);
     if (d.E <= 512)
         hipLaunchKernelGGL(moe_topk_kernel<8>, dim3(1), dim3(64), 0, s, d, L, ws, ids_out, w_out);
     else if (d.E <= 1024)

@@ -67,9 +67,21 @@ __device__ __forceinline__ uint32_t pair_token(const MoeBatchDims& d, uint32_t p
 
 // ------------------------------------------------------------------ 1. x prep
 
+// Floats of LDS x staging for `cols` columns (rounded up to whole Q4 steps).
+static uint32_t q4_stage_floats(uint32_t cols) { return n_steps_for(HK_Q4, cols) * tile_step_cols(HK_Q4); }
+
+// The Q4 x image of xs (LDS, >= q4_stage_floats(cols) floats, quantized in
+// place) into img (global), by the whole block.
+__device__ int x_image_in_place(float* xs, uint32_t cols, uint8_t* img, float* red, bool* bad) {
+    const uint32_t S = n_steps_for(HK_Q4, cols);
+    XChunks<1> xc;
+    load_x<1>(BlockTeam{}, xs, cols, xc);
+    return x_image<HK_Q4, 1>(BlockTeam{}, xc, xs, cols, S, img, xs, 8u * blockDim.x, red, bad);
+}
+
 __global__ void __launch_bounds__(256) moe_batch_xprep_kernel(MoeBatchDims d, const uint16_t* __restrict__ xb,
                                                               MoeBatchWs ws) {
-    extern __shared__ __align__(16) float xs[];  // [H]
+    extern __shared__ __align__(16) float xs[];  // [H rounded up to whole steps]
     __shared__ float red[4];
     const uint32_t t = blockIdx.x;
     for (uint32_t c = threadIdx.x; c < d.H; c += blockDim.x) {
@@ -79,8 +91,7 @@ __global__ void __launch_bounds__(256) moe_batch_xprep_kernel(MoeBatchDims d, co
     }
     __syncthreads();
     bool bad = false;
-    const int E = prepare_x<HK_Q4>(BlockTeam{}, xs, d.H, n_steps_for(HK_Q4, d.H), ws.ximg + (size_t)t * ws.ximg_stride,
-                                   red, &bad);
+    const int E = x_image_in_place(xs, d.H, ws.ximg + (size_t)t * ws.ximg_stride, red, &bad);
     if (threadIdx.x == 0) {
         ws.ximg_e[t] = E;
         if (bad) atomicOr(ws.status, HK_DEVERR_NONFINITE);
@@ -480,7 +491,7 @@ __global__ void __launch_bounds__(256) moe_batch_gate_up_kernel(MoeBatchDims d, 
 // ------------------------------------------------------------------ 6. activation images
 
 __global__ void __launch_bounds__(256) moe_batch_act_image_kernel(MoeBatchDims d, MoeBatchWs ws) {
-    extern __shared__ __align__(16) float xs[];  // [Imax]
+    extern __shared__ __align__(16) float xs[];  // [Imax rounded up to whole steps]
     __shared__ float red[4];
     const uint32_t p = blockIdx.x;
     const uint32_t cols = p < d.T * d.K ? d.I : d.SI;
@@ -488,8 +499,7 @@ __global__ void __launch_bounds__(256) moe_batch_act_image_kernel(MoeBatchDims d
     for (uint32_t j = threadIdx.x; j < cols / 4u; j += blockDim.x) reinterpret_cast<float4*>(xs)[j] = a4[j];
     __syncthreads();
     bool bad = false;
-    const int E = prepare_x<HK_Q4>(BlockTeam{}, xs, cols, n_steps_for(HK_Q4, cols), ws.aimg + (size_t)p * ws.aimg_stride,
-                                   red, &bad);
+    const int E = x_image_in_place(xs, cols, ws.aimg + (size_t)p * ws.aimg_stride, red, &bad);
     if (threadIdx.x == 0) {
         ws.aimg_e[p] = E;
         if (bad) atomicOr(ws.status, HK_DEVERR_NONFINITE);
@@ -574,7 +584,8 @@ hipError_t launch_moe_batch(const MoeBatchDims& d, const MoeLayerDev& L, const f
     const uint32_t ximg = (uint32_t)moe_batch_img_bytes(d.H), aimg = (uint32_t)moe_batch_img_bytes(d.Imax);
     const uint32_t tb_gu = tokens_per_group(ximg, 2u), tb_dn = tokens_per_group(aimg, 4u);
     if (tb_gu == 0 || tb_dn == 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(moe_batch_xprep_kernel, dim3(d.T), dim3(256), (size_t)d.H * sizeof(float), s, d, x_bf16, ws);
+    hipLaunchKernelGGL(moe_batch_xprep_kernel, dim3(d.T), dim3(256), (size_t)q4_stage_floats(d.H) * sizeof(float), s, d,
+                       x_bf16, ws);
     hipLaunchKernelGGL(moe_batch_router_kernel, dim3((d.E + RT_ROWS - 1) / RT_ROWS, d.S), dim3(256), 0, s, d, L.router_w,
                        ws);
     hipLaunchKernelGGL(moe_batch_route_kernel, dim3(d.T), dim3(64), 0, s, d, bias, ws, ids_out, w_out);
@@ -584,7 +595,8 @@ hipError_t launch_moe_batch(const MoeBatchDims& d, const MoeLayerDev& L, const f
         hipLaunchKernelGGL((moe_batch_gate_up_kernel<2, 4>), ggu, dim3(256), (size_t)2 * ximg, s, d, L.table, ws);
     else
         hipLaunchKernelGGL((moe_batch_gate_up_kernel<1, 4>), ggu, dim3(256), (size_t)ximg, s, d, L.table, ws);
-    hipLaunchKernelGGL(moe_batch_act_image_kernel, dim3(pairs), dim3(256), (size_t)d.Imax * sizeof(float), s, d, ws);
+    hipLaunchKernelGGL(moe_batch_act_image_kernel, dim3(pairs), dim3(256), (size_t)q4_stage_floats(d.Imax) * sizeof(float),
+                       s, d, ws);
     if (tb_dn >= 4)
         hipLaunchKernelGGL((moe_batch_down_kernel<4, 4>), gdn, dim3(256), (size_t)4 * aimg, s, d, L.table, ws);
     else if (tb_dn >= 2)
