@@ -4,6 +4,9 @@ Headline (BASELINE.json metric, configs[1]): the binary sign-plane organ
 (512x2048, 1 bit/weight + f16 mean|w| per 128) streamed over many distinct
 organs in ONE launch, working set > 1 GB (so the 256 MB MALL cannot serve
 repeats), inputs resident in HBM.  A "step" is one launch over all organs.
+Every timed loop is preceded by about 0.2 s of untimed launches of the same
+work (the GPU clocks ramp up over the first milliseconds of activity), then
+the W warmup steps, then exactly K timed steps between HIP events.
 
 Also reported (the same JSON line, "extra"): Q4 (config 1) and mixed streamed
 GB/s, the binary down shape (2048x512), single-organ latency, the config-3
@@ -65,8 +68,14 @@ def build_stream(ctx, name: str, n_organs: int | None = None):
     return oset, x, y, alg_bytes
 
 
-def time_launches(ctx, fn, steps: int, warmup: int) -> float:
-    """Average ms per call of fn() over `steps` calls, HIP events on ctx.stream."""
+def time_launches(ctx, fn, steps: int, warmup: int, ramp_s: float = 0.2) -> float:
+    """Average ms per call of fn() over `steps` calls, HIP events on ctx.stream,
+    after ramp_s seconds of untimed calls and `warmup` more."""
+    t_end = time.perf_counter() + ramp_s
+    while time.perf_counter() < t_end:
+        for _ in range(8):
+            fn()
+        ctx.synchronize()
     for _ in range(warmup):
         fn()
     ctx.synchronize()

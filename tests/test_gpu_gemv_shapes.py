@@ -1,0 +1,95 @@
+"""GEMV over organ sets in every launch shape the dispatcher picks, and x
+images of several quantization rounds, against the oracle (through the C ABI).
+
+The dispatcher sizes the launch by the set's total row tiles: >= 16384 tiles
+(the streamed shapes of the benchmark: binary 4 tiles per wave group, 3 steps
+in flight, 16 or 32 tiles per workgroup; Q4 and mixed 2 / 3 / 16), >= 4096
+(2 / 2 / 8) and below (1 / 2 / 4 or 1).  The x image is built 2048 columns per
+round; organs wider than 2048 columns take several rounds, and beyond 8192
+columns the later rounds re-read x.  Organs are generated on the device; the
+oracle regenerates the ones it checks (first, middle, last) bit-identically.
+Bar: 2e-5 relative L2 against the oracle's serial f32 matvec.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from tests import hk_testutil as U
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-5
+HK_Q4, HK_BIN, HK_MIXED = U.HK_Q4, U.HK_BIN, U.HK_MIXED
+
+
+def say(*a):
+    print("[gpu-case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from hawking_amd.runtime import Context
+    return Context(0)
+
+
+def _keys(oracle, tag, i):
+    sid = (0x5E7 << 40) | (tag << 24) | i
+    return oracle.stream_key(U.SEED, sid), oracle.stream_key(U.SEED, sid ^ (1 << 39))
+
+
+def _oracle_matvec(oracle, kind, group, rows, cols, key, coin_key, x):
+    w = oracle.normal(key, rows * cols, U.SIGMA_W).reshape(rows, cols)
+    if kind == HK_BIN:
+        s, g = oracle.bin_pack(w)
+        return oracle.bin_matvec(s, g, rows, cols, x)
+    if kind == HK_Q4:
+        s, c = oracle.q4_pack(w, group)
+        return oracle.q4_matvec(s, c, rows, cols, group, x)
+    m = oracle.mixed_pack(w, oracle.mixed_coins(coin_key, rows * cols // 128))
+    return oracle.mixed_matvec(m, x)
+
+
+CASES = [
+    # label, kind, group, rows, cols, n organs
+    ("bin streamed 16/wg", HK_BIN, 128, 512, 2048, 512),
+    ("bin streamed 32/wg", HK_BIN, 128, 2048, 512, 128),
+    ("q4 streamed", HK_Q4, 32, 512, 2048, 512),
+    ("mixed streamed", HK_MIXED, 128, 512, 2048, 512),
+    ("bin mid", HK_BIN, 128, 512, 2048, 128),
+    ("mixed mid ragged", HK_MIXED, 128, 500, 1024, 140),
+    ("q4 small", HK_Q4, 64, 96, 1024, 5),
+    ("bin 3 rounds", HK_BIN, 128, 48, 6144, 3),
+    ("bin 5 rounds (re-read)", HK_BIN, 128, 40, 10240, 2),
+    ("mixed 4 rounds", HK_MIXED, 128, 33, 7168, 2),
+    ("q4 5 rounds (re-read)", HK_Q4, 128, 24, 9216, 2),
+]
+
+
+@pytest.mark.parametrize("label,kind,group,rows,cols,n", CASES, ids=[c[0] for c in CASES])
+def test_organ_set_launch_shapes(ctx, oracle, label, kind, group, rows, cols, n):
+    from hawking_amd import organs
+    say(label, kind, group, rows, cols, n)
+    tag = CASES.index((label, kind, group, rows, cols, n))
+    keys = [_keys(oracle, tag, i) for i in range(n)]
+    orgs = [organs.SyntheticOrgan(ctx, kind, rows, cols, k, ck, group=group) for k, ck in keys]
+    oset = organs.OrganSet(ctx, orgs)
+    rng = np.random.default_rng(1000 + tag)
+    xs = rng.standard_normal((n, cols)).astype(np.float32)
+    ys = (rows + 3) // 4 * 4                       # y rows 16-byte aligned
+    y = ctx.empty((n, ys))
+    oset.gemv(ctx.to_device(xs), cols, y, ys)
+    yg = y.download()[:, :rows]
+    for i in sorted({0, n // 2, n - 1}):
+        k, ck = keys[i]
+        ref = _oracle_matvec(oracle, kind, group, rows, cols, k, ck, xs[i])
+        err = oracle.relative_l2(yg[i], ref)
+        assert err < TOL, (label, i, err)
+
+
+def test_organ_wider_than_lds_image_is_rejected(ctx):
+    from hawking_amd import organs
+    from hawking_amd._lib import HK_E_GEOMETRY, HawkingError
+    with pytest.raises(HawkingError) as e:
+        organs.SyntheticOrgan(ctx, HK_BIN, 16, 16384, 1, 2)
+    assert e.value.code == HK_E_GEOMETRY
