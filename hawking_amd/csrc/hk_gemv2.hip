@@ -37,6 +37,17 @@ __device__ __forceinline__ void flush_group(float* acc, const uint32_t* T, int n
 }
 
 constexpr uint32_t GEMV_MAX_TILES_PER_WG = 32;
+// Mixed step headers staged per workgroup: tiles x steps <= 32 x 24.
+constexpr int GEMV_HDR_PER_THREAD = 3;
+constexpr uint32_t GEMV_MAX_MIXED_STEPS = GEMV_HDR_PER_THREAD * 256 / GEMV_MAX_TILES_PER_WG;
+
+// Dynamic LDS: x image, one quantization window (2048 columns), then (mixed)
+// the headers of the workgroup's tiles.
+template <int KIND>
+__host__ __device__ constexpr size_t gemv_hdr_offset(uint32_t steps) {
+    return x_lds_bytes<KIND>(steps) + (size_t)(steps * (uint32_t)Kcfg<KIND>::STEP_COLS < 2048u
+                                                   ? steps * (uint32_t)Kcfg<KIND>::STEP_COLS : 2048u) * sizeof(float);
+}
 
 // D-deep software pipeline: D fetched steps are in flight while one is
 // consumed; slot d of the rotating buffer holds item it+d.  The loop body is
@@ -60,9 +71,20 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, const float* __restrict_
     W.n = W.g0 < t1 ? ((t1 - W.g0 + W.gstride - 1) / W.gstride) * o.steps : 0;
     const uint32_t last = W.n ? W.n - 1u : 0u;
 
-    // x first, then the first D steps' weight loads, all before the image build
+    // x first, then (mixed) this workgroup's step headers, then the first D
+    // steps' weight loads, all before the image build
     XChunks<NC> xc;
     load_x<NC>(BlockTeam{}, x, o.cols, xc);
+    const uint32_t nh = (t1 - t0) * o.steps;
+    uint4 hreg[GEMV_HDR_PER_THREAD];
+    uint4* hsh = reinterpret_cast<uint4*>(lds + gemv_hdr_offset<KIND>(o.steps));
+    if constexpr (KIND == HK_MIXED) {
+#pragma unroll
+        for (int k = 0; k < GEMV_HDR_PER_THREAD; ++k) {
+            const uint32_t i = threadIdx.x + 256u * k;
+            if (i < nh) hreg[k] = ldg(o.hdr + (size_t)t0 * o.steps + i);
+        }
+    }
     Frag<KIND, R> f[D];
     uint32_t T[D][R], ts[D];
     int nv[D];
@@ -74,6 +96,13 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, const float* __restrict_
         for (int d = 0; d < D; ++d) {
             P.at(min((uint32_t)d, last), T[d], R, &nv[d], &ts[d]);
             fetch_step<KIND, R>(o, T[d], nv[d], ts[d], lane, f[d]);
+        }
+    }
+    if constexpr (KIND == HK_MIXED) {
+#pragma unroll
+        for (int k = 0; k < GEMV_HDR_PER_THREAD; ++k) {
+            const uint32_t i = threadIdx.x + 256u * k;
+            if (i < nh) hsh[i] = hreg[k];
         }
     }
     bool bad = false;
@@ -93,7 +122,17 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, const float* __restrict_
             compute_step<KIND, R>(f[d], ts[d], A, SX, q, acc);
             if (ts[d] + 1 == o.steps) flush_group<R>(acc, T[d], nv[d], t0, lane, ysh);
             W.at(min(it + D + d, last), T[d], R, &nv[d], &ts[d]);
-            fetch_step<KIND, R>(o, T[d], nv[d], ts[d], lane, f[d]);
+            if constexpr (KIND == HK_MIXED) {
+                // headers from LDS: the data loads wait for an LDS read, not
+                // for every load in flight before them
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const uint32_t Tr = r < nv[d] ? T[d][r] : T[d][0];
+                    fetch_mixed<R>(o, hsh[(Tr - t0) * o.steps + ts[d]], lane, f[d], r);
+                }
+            } else {
+                fetch_step<KIND, R>(o, T[d], nv[d], ts[d], lane, f[d]);
+            }
         }
     }
 #pragma unroll
@@ -130,9 +169,11 @@ __global__ void __launch_bounds__(256) gemv_f32_kernel(const OrganView* __restri
 }
 
 size_t gemv_lds_bytes(int kind, uint32_t cols) {
-    const uint32_t S = n_steps_for(kind, cols), kc = S * tile_step_cols(kind);
-    const size_t img = kind == HK_Q4 ? x_lds_bytes<HK_Q4>(S) : kind == HK_BIN ? x_lds_bytes<HK_BIN>(S) : x_lds_bytes<HK_MIXED>(S);
-    return img + (size_t)min(kc, 2048u) * sizeof(float);
+    const uint32_t S = n_steps_for(kind, cols);
+    if (kind == HK_Q4) return gemv_hdr_offset<HK_Q4>(S);
+    if (kind == HK_BIN) return gemv_hdr_offset<HK_BIN>(S);
+    if (S > GEMV_MAX_MIXED_STEPS) return SIZE_MAX;
+    return gemv_hdr_offset<HK_MIXED>(S) + (size_t)GEMV_MAX_TILES_PER_WG * S * sizeof(uint4);
 }
 
 template <int KIND, int R, int D>
@@ -142,7 +183,7 @@ static hipError_t launch_kind(const OrganView* organs, uint32_t n, const OrganVi
     // image + one quantization window (2048 columns); x chunks held in
     // registers: one per thread up to 2048 columns, else four
     const uint32_t kc = x_image_cols<KIND>(sh.steps);
-    const size_t lds = gemv_lds_bytes(sh.kind, sh.cols);
+    const size_t lds = gemv_hdr_offset<KIND>(sh.steps) + (KIND == HK_MIXED ? (size_t)tpw * sh.steps * sizeof(uint4) : 0);
     if (kc <= 2048u)
         hipLaunchKernelGGL((gemv_tiled_kernel<KIND, R, D, 1>), grid, dim3(256), lds, s, organs, x, xs, y, ys, tpw,
                            nullptr);

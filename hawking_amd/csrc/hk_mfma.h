@@ -300,7 +300,30 @@ struct Frag<HK_MIXED, R> {
     bool q2[R];
 };
 
-// Issue the loads of step t of tile T of organ o into slot r of f.
+// Issue the loads of a mixed step with header h into slot r of f.
+template <int R>
+__device__ __forceinline__ void fetch_mixed(const OrganView& o, const uint4& h, int lane, Frag<HK_MIXED, R>& f, int r) {
+    const uint32_t below = __builtin_amdgcn_mbcnt_hi(h.y, __builtin_amdgcn_mbcnt_lo(h.x, 0u));
+    const bool isq2 = ((lane < 32 ? (h.x >> lane) : (h.y >> (lane - 32))) & 1u) != 0;
+    const uint8_t* p = o.data + h.z + 16u * ((uint32_t)lane + below);
+    const uint4 va = ldg(reinterpret_cast<const uint4*>(p));
+    const uint4 vb = ldg(reinterpret_cast<const uint4*>(p + (isq2 ? 16 : 0)));
+    f.V[r][0] = va.x;
+    f.V[r][1] = va.y;
+    f.V[r][2] = va.z;
+    f.V[r][3] = va.w;
+    f.V[r][4] = vb.x;
+    f.V[r][5] = vb.y;
+    f.V[r][6] = vb.z;
+    f.V[r][7] = vb.w;
+    const uint16_t* spp = o.scales + h.w + (uint32_t)lane + below;
+    f.s0[r] = ldg(spp);
+    f.s1[r] = ldg(spp + (isq2 ? 1 : 0));
+    f.q2[r] = isq2;
+}
+
+// Issue the loads of step t of tile T of organ o into slot r of f (a mixed
+// step first loads its header, and its data loads wait for it).
 template <int KIND, int R>
 __device__ __forceinline__ void fetch_one(const OrganView& o, uint32_t T, uint32_t t, int lane, Frag<KIND, R>& f,
                                           int r) {
@@ -308,24 +331,7 @@ __device__ __forceinline__ void fetch_one(const OrganView& o, uint32_t T, uint32
         f.v[r] = ldg(reinterpret_cast<const uint4*>(o.data + ((size_t)T * o.steps + t) * 1024u + 16u * lane));
         f.s[r] = ldg(o.scales + ((size_t)T * o.steps + t) * 64u + lane);
     } else {
-        const uint4 h = ldg(o.hdr + (size_t)T * o.steps + t);
-        const uint32_t below = __builtin_amdgcn_mbcnt_hi(h.y, __builtin_amdgcn_mbcnt_lo(h.x, 0u));
-        const bool isq2 = ((lane < 32 ? (h.x >> lane) : (h.y >> (lane - 32))) & 1u) != 0;
-        const uint8_t* p = o.data + h.z + 16u * ((uint32_t)lane + below);
-        const uint4 va = ldg(reinterpret_cast<const uint4*>(p));
-        const uint4 vb = ldg(reinterpret_cast<const uint4*>(p + (isq2 ? 16 : 0)));
-        f.V[r][0] = va.x;
-        f.V[r][1] = va.y;
-        f.V[r][2] = va.z;
-        f.V[r][3] = va.w;
-        f.V[r][4] = vb.x;
-        f.V[r][5] = vb.y;
-        f.V[r][6] = vb.z;
-        f.V[r][7] = vb.w;
-        const uint16_t* spp = o.scales + h.w + (uint32_t)lane + below;
-        f.s0[r] = ldg(spp);
-        f.s1[r] = ldg(spp + (isq2 ? 1 : 0));
-        f.q2[r] = isq2;
+        fetch_mixed<R>(o, ldg(o.hdr + (size_t)T * o.steps + t), lane, f, r);
     }
 }
 
