@@ -194,16 +194,22 @@ static hipError_t launch_kind(const OrganView* organs, uint32_t n, const OrganVi
 }
 
 // Launch shape (R tiles per wave group, D steps in flight, tiles per
-// workgroup) by kind and size, from sweeps over the streamed workloads: a
-// workgroup of about 32-64 KiB of binary weights, R = 2 where a wave's
-// fragments are large (mixed) or the steps many (Q4).
+// workgroup) by kind and size, from sweeps over the streamed workloads:
+// binary 4-tile groups over 16 tiles when the organ has >= 4 steps, else
+// 2-tile groups over 32; Q4 2 over 16; mixed (large fragments) 1 over 16.
 template <int KIND>
 static hipError_t launch_r(const OrganView* organs, uint32_t n, const OrganView& sh, const float* x, size_t xs,
                            float* y, size_t ys, hipStream_t s) {
     const uint64_t tiles = (uint64_t)n * sh.n_tiles;
     if (tiles >= 16384) {
-        if constexpr (KIND == HK_BIN) return launch_kind<KIND, 4, 3>(organs, n, sh, x, xs, y, ys, sh.steps >= 4 ? 16 : 32, s);
-        else return launch_kind<KIND, 2, 3>(organs, n, sh, x, xs, y, ys, 16, s);
+        if constexpr (KIND == HK_BIN) {
+            if (sh.steps >= 4) return launch_kind<KIND, 4, 3>(organs, n, sh, x, xs, y, ys, 16, s);
+            return launch_kind<KIND, 2, 3>(organs, n, sh, x, xs, y, ys, 32, s);
+        } else if constexpr (KIND == HK_Q4) {
+            return launch_kind<KIND, 2, 3>(organs, n, sh, x, xs, y, ys, 16, s);
+        } else {
+            return launch_kind<KIND, 1, 3>(organs, n, sh, x, xs, y, ys, 16, s);
+        }
     }
     if (tiles >= 4096) return launch_kind<KIND, 2, 2>(organs, n, sh, x, xs, y, ys, 8, s);
     const uint32_t tpw = (uint64_t)n * ((sh.n_tiles + 3) / 4) >= 256 ? 4 : 1;

@@ -2,9 +2,10 @@
 images of several quantization rounds, against the oracle (through the C ABI).
 
 The dispatcher sizes the launch by the set's total row tiles: >= 16384 tiles
-(the streamed shapes of the benchmark: binary 4 tiles per wave group, 3 steps
-in flight, 16 or 32 tiles per workgroup; Q4 and mixed 2 / 3 / 16), >= 4096
-(2 / 2 / 8) and below (1 / 2 / 4 or 1).  The x image is built 2048 columns per
+(the streamed shapes of the benchmark, as tiles per wave group / steps in
+flight / tiles per workgroup: binary 4 / 3 / 16 with >= 4 steps, else
+2 / 3 / 32; Q4 2 / 3 / 16; mixed 1 / 3 / 16), >= 4096 (2 / 2 / 8) and below
+(1 / 2 / 4 or 1).  The x image is built 2048 columns per
 round; organs wider than 2048 columns take several rounds, and beyond 8192
 columns the later rounds re-read x.  Organs are generated on the device; the
 oracle regenerates the ones it checks (first, middle, last) bit-identically.
@@ -56,6 +57,7 @@ CASES = [
     ("bin streamed 32/wg", HK_BIN, 128, 2048, 512, 128),
     ("q4 streamed", HK_Q4, 32, 512, 2048, 512),
     ("mixed streamed", HK_MIXED, 128, 512, 2048, 512),
+    ("bin streamed 2-tile", HK_BIN, 128, 1024, 1536, 256),
     ("bin mid", HK_BIN, 128, 512, 2048, 128),
     ("mixed mid ragged", HK_MIXED, 128, 500, 1024, 140),
     ("q4 small", HK_Q4, 64, 96, 1024, 5),
