@@ -54,19 +54,32 @@ __host__ __device__ constexpr size_t gemv_hdr_offset(uint32_t steps) {
 // branch-free in memory operations (refetches are unconditional, past the end
 // they re-read the last item; y goes out through LDS after the loop) so the
 // compiler can wait for exactly the slot being consumed.
+// Workgroup -> (organ, part).  Workgroups are dispatched to the 8 XCDs round
+// robin by linear id, so ids 8 apart share an XCD and its L2: each run of
+// 8 * parts ids covers 8 organs with id % 8 selecting the organ, and all
+// parts of an organ (which read the same x) land on one XCD.
+__device__ __forceinline__ void organ_part(uint32_t L, uint32_t parts, uint32_t n, uint32_t* organ, uint32_t* part) {
+    const uint32_t c = L / (8u * parts), r = L % (8u * parts), g = min(8u, n - 8u * c);
+    *organ = 8u * c + r % g;
+    *part = r / g;
+}
+
 template <int KIND, int R, int D, int NC>
 __global__ void __launch_bounds__(256)
-gemv_tiled_kernel(const OrganView* __restrict__ organs, const float* __restrict__ xall, size_t x_stride,
-                  float* __restrict__ yall, size_t y_stride, uint32_t tiles_per_wg, uint32_t* status) {
+gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const float* __restrict__ xall,
+                  size_t x_stride, float* __restrict__ yall, size_t y_stride, uint32_t tiles_per_wg, uint32_t parts,
+                  uint32_t* status) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float red[4];
     __shared__ float ysh[GEMV_MAX_TILES_PER_WG * 16];
-    const OrganView o = organs[blockIdx.y];
-    const float* __restrict__ x = xall + (size_t)blockIdx.y * x_stride;
-    float* __restrict__ y = yall + (size_t)blockIdx.y * y_stride;
+    uint32_t oi, part;
+    organ_part(blockIdx.x, parts, n_organs, &oi, &part);
+    const OrganView o = organs[oi];
+    const float* __restrict__ x = xall + (size_t)oi * x_stride;
+    float* __restrict__ y = yall + (size_t)oi * y_stride;
     const int lane = threadIdx.x & 63, q = lane >> 4;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t t0 = blockIdx.x * tiles_per_wg, t1 = min(t0 + tiles_per_wg, o.n_tiles);
+    const uint32_t t0 = part * tiles_per_wg, t1 = min(t0 + tiles_per_wg, o.n_tiles);
     WaveItems W{t0 + wave * R, 4u * R, t1, o.steps, 0};
     W.n = W.g0 < t1 ? ((t1 - W.g0 + W.gstride - 1) / W.gstride) * o.steps : 0;
     const uint32_t last = W.n ? W.n - 1u : 0u;
@@ -179,17 +192,18 @@ size_t gemv_lds_bytes(int kind, uint32_t cols) {
 template <int KIND, int R, int D>
 static hipError_t launch_kind(const OrganView* organs, uint32_t n, const OrganView& sh, const float* x,
                               size_t xs, float* y, size_t ys, uint32_t tpw, hipStream_t s) {
-    const dim3 grid((sh.n_tiles + tpw - 1) / tpw, n);
+    const uint32_t parts = (sh.n_tiles + tpw - 1) / tpw;
+    const dim3 grid(parts * n);
     // image + one quantization window (2048 columns); x chunks held in
     // registers: one per thread up to 2048 columns, else four
     const uint32_t kc = x_image_cols<KIND>(sh.steps);
     const size_t lds = gemv_hdr_offset<KIND>(sh.steps) + (KIND == HK_MIXED ? (size_t)tpw * sh.steps * sizeof(uint4) : 0);
     if (kc <= 2048u)
-        hipLaunchKernelGGL((gemv_tiled_kernel<KIND, R, D, 1>), grid, dim3(256), lds, s, organs, x, xs, y, ys, tpw,
-                           nullptr);
+        hipLaunchKernelGGL((gemv_tiled_kernel<KIND, R, D, 1>), grid, dim3(256), lds, s, organs, n, x, xs, y, ys, tpw,
+                           parts, nullptr);
     else
-        hipLaunchKernelGGL((gemv_tiled_kernel<KIND, R, D, 4>), grid, dim3(256), lds, s, organs, x, xs, y, ys, tpw,
-                           nullptr);
+        hipLaunchKernelGGL((gemv_tiled_kernel<KIND, R, D, 4>), grid, dim3(256), lds, s, organs, n, x, xs, y, ys, tpw,
+                           parts, nullptr);
     return hipGetLastError();
 }
 
