@@ -8,13 +8,12 @@
 //   1. route:   every block recomputes xn = RMSNorm(1+w)(h) in LDS; blocks
 //               0..ceil(E/4)-1 compute the router logits (one row per wave),
 //               the last block computes the shared-gate logit and the x image
-//               of xn (fixed-point limb tiles, built once per layer).  The
-//               block that finishes last runs softmax / top-k / renormalise
-//               and writes the organ views of the selected experts in slot
-//               order (slot K = the shared expert).
-//   2. gate/up: one workgroup per (16-row tile, slot); its 4 waves split the
-//               columns, both organs share each x-image fetch, and the
-//               epilogue applies SwiGLU: act = silu(gate.xn) * (up.xn).
+//               of xn (fixed-point limb tiles, built once per layer).
+//   2. gate/up: one workgroup per (16-row tile, slot); each runs softmax /
+//               top-k / renormalise over the logits itself to find its
+//               slot's expert (slot K = the shared expert), then its 4 waves
+//               split the columns, both organs share each x-image fetch, and
+//               the epilogue applies SwiGLU: act = silu(gate.xn) * (up.xn).
 //   3. down:    one workgroup per 16-row output tile, one wave per slot; each
 //               wave builds the x image of its slot's activations, and the
 //               block combines out = h + sum_r w_r y_r (route order)
@@ -126,47 +125,49 @@ __global__ void __launch_bounds__(256) moe_route_kernel(MoeDims d, MoeLayerDev L
     }
 }
 
-// Softmax, top-k, renormalise (source_qwen80_topk_router) in one wave, the
-// shared-expert gate value, and the organ views of the selected experts in
-// slot order.
-template <int NPL>
-__global__ void __launch_bounds__(64) moe_topk_kernel(MoeDims d, MoeLayerDev L, MoeWs ws, int32_t* ids_out,
-                                                      float* w_out) {
-    const int lane = threadIdx.x & 63;
-    const ArgBest mine = softmax_topk_wave<NPL>(ws.logits, d.E, d.K, 1, ws.ids, ws.weights, ws.status);
-    if (lane == 0) ws.gate[1] = L.gate_w ? 1.0f / (1.0f + expf(-ws.gate[0])) : 1.0f;
-    if ((uint32_t)lane < d.K) {
-        if (ids_out) ids_out[lane] = mine.i;
-        if (w_out) w_out[lane] = mine.v;
-    }
-    // lane i writes sel[i]: slot i/3, projection i%3 (slots * 3 <= 48 < 64)
-    const uint32_t slots = d.K + (d.has_shared ? 1u : 0u);
-    const uint32_t i = (uint32_t)lane, slot = i / 3u, pj = i % 3u;
-    const int32_t id = __shfl(mine.i, (int)min(slot, 63u), 64);
-    if (i < slots * 3u) {
-        uint32_t e = d.E;
-        if (slot < d.K) e = (id >= 0 && (uint32_t)id < d.E) ? (uint32_t)id : 0xFFFFFFFFu;
-        // word copy (a struct assignment here goes through scratch memory);
-        // an invalid route selects no organ (all-zero view: n_tiles = 0)
-        static_assert(sizeof(OrganView) % 8 == 0, "OrganView is copied in 8-byte words");
-        const bool ok = e != 0xFFFFFFFFu;
-        const uint64_t* from = reinterpret_cast<const uint64_t*>(L.table + (ok ? e * 3u + pj : 0u));
-        uint64_t* to = reinterpret_cast<uint64_t*>(ws.sel + i);
-#pragma unroll
-        for (uint32_t k = 0; k < sizeof(OrganView) / 8; ++k) to[k] = ok ? from[k] : 0ull;
-        if (!ok && pj == 0) atomicOr(ws.status, HK_DEVERR_ROUTE);
-    }
-}
-
-template <int KIND, int D>
-__global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeWs ws) {
+// Gate/up of one (16-row tile, slot).  Every workgroup of a routed slot first
+// ranks the router logits itself (softmax, top-k, renormalise:
+// source_qwen80_topk_router, one wave, 64-bit keys on the DPP network) and
+// takes its slot's expert; this costs about a microsecond per workgroup and
+// saves a launch.  Tile 0 of each slot publishes the slot's down organ (and
+// slot 0 the route and the shared-gate value) for the down kernel.
+template <int KIND, int D, int NPL>
+__global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev L, MoeWs ws, int32_t* ids_out,
+                                                          float* w_out) {
     extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ int32_t sel_id;
     const uint32_t slot = blockIdx.y, T = blockIdx.x;
-    const OrganView g = ws.sel[slot * 3u + 0u];
-    if (T >= g.n_tiles) return;
-    const OrganView u = ws.sel[slot * 3u + 1u];
     const int lane = threadIdx.x & 63, q = lane >> 4;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool lead = T == 0;
+    if (slot < d.K) {
+        if (wave == 0) {
+            const bool pub = lead && slot == 0;
+            const ArgBest mine = softmax_topk_wave<NPL>(ws.logits, d.E, d.K, 1, pub ? ws.ids : nullptr,
+                                                        pub ? ws.weights : nullptr, pub ? ws.status : nullptr);
+            if (pub && (uint32_t)lane < d.K) {
+                if (ids_out) ids_out[lane] = mine.i;
+                if (w_out) w_out[lane] = mine.v;
+            }
+            if (pub && lane == 0) ws.gate[1] = L.gate_w ? 1.0f / (1.0f + expf(-ws.gate[0])) : 1.0f;
+            if ((uint32_t)lane == slot) sel_id = mine.i;
+        }
+        __syncthreads();
+    }
+    const int32_t id = slot < d.K ? sel_id : (int32_t)d.E;
+    // an invalid route selects no organ (all-zero down view: n_tiles = 0)
+    const bool ok = slot >= d.K || (id >= 0 && (uint32_t)id < d.E);
+    if (lead && threadIdx.x < sizeof(OrganView) / 8) {
+        // word copy (a struct assignment here goes through scratch memory)
+        static_assert(sizeof(OrganView) % 8 == 0, "OrganView is copied in 8-byte words");
+        const uint64_t* from = reinterpret_cast<const uint64_t*>(L.table + (ok ? (uint32_t)id * 3u + 2u : 0u));
+        reinterpret_cast<uint64_t*>(ws.sel + slot * 3u + 2u)[threadIdx.x] = ok ? from[threadIdx.x] : 0ull;
+        if (!ok && threadIdx.x == 0) atomicOr(ws.status, HK_DEVERR_ROUTE);
+    }
+    if (!ok) return;
+    const OrganView g = L.table[(uint32_t)id * 3u + 0u];
+    if (T >= g.n_tiles) return;
+    const OrganView u = L.table[(uint32_t)id * 3u + 1u];
     const uint32_t S = g.steps, per = (S + 3u) / 4u;
     const uint32_t s0 = min(wave * per, S), n = min(s0 + per, S) - s0;
     Frag<KIND, 2> f[D];
@@ -288,16 +289,16 @@ static hipError_t launch_layer(const MoeDims& d, const MoeLayerDev& L, const flo
     const uint32_t img_stride = (uint32_t)moe_img_bytes(KIND, d.Imax);
     hipLaunchKernelGGL(moe_route_kernel<KIND>, dim3(nrb + 1u), dim3(256), (size_t)stage_floats(KIND, d.H) * sizeof(float),
                        s, d, L, h_in, ws);
+    const dim3 gg(gu_tiles, slots);
+    const size_t gl = moe_gate_up_lds_bytes(KIND, d.H);
     if (d.E <= 512)
-        hipLaunchKernelGGL(moe_topk_kernel<8>, dim3(1), dim3(64), 0, s, d, L, ws, ids_out, w_out);
+        hipLaunchKernelGGL((moe_gate_up_kernel<KIND, 4, 8>), gg, dim3(256), gl, s, d, L, ws, ids_out, w_out);
     else if (d.E <= 1024)
-        hipLaunchKernelGGL(moe_topk_kernel<16>, dim3(1), dim3(64), 0, s, d, L, ws, ids_out, w_out);
+        hipLaunchKernelGGL((moe_gate_up_kernel<KIND, 4, 16>), gg, dim3(256), gl, s, d, L, ws, ids_out, w_out);
     else if (d.E <= 2048)
-        hipLaunchKernelGGL(moe_topk_kernel<32>, dim3(1), dim3(64), 0, s, d, L, ws, ids_out, w_out);
+        hipLaunchKernelGGL((moe_gate_up_kernel<KIND, 4, 32>), gg, dim3(256), gl, s, d, L, ws, ids_out, w_out);
     else
-        hipLaunchKernelGGL(moe_topk_kernel<64>, dim3(1), dim3(64), 0, s, d, L, ws, ids_out, w_out);
-    hipLaunchKernelGGL((moe_gate_up_kernel<KIND, 4>), dim3(gu_tiles, slots), dim3(256),
-                       moe_gate_up_lds_bytes(KIND, d.H), s, d, ws);
+        hipLaunchKernelGGL((moe_gate_up_kernel<KIND, 4, 64>), gg, dim3(256), gl, s, d, L, ws, ids_out, w_out);
     hipLaunchKernelGGL((moe_down_kernel<KIND, 4>), dim3(n_tiles_for(d.H)), dim3(64u * slots),
                        moe_down_lds_bytes(KIND, d.Imax, slots), s, d, h_in, h_out, ws, img_stride);
     return hipGetLastError();

@@ -248,8 +248,8 @@ __device__ ArgBest softmax_topk_wave(const float* __restrict__ logits, uint32_t 
         mine.v = mine.v / sel;
     }
     if ((uint32_t)lane < k) {
-        ids_out[lane] = mine.i;
-        w_out[lane] = mine.v;
+        if (ids_out) ids_out[lane] = mine.i;
+        if (w_out) w_out[lane] = mine.v;
     }
     return mine;
 }
