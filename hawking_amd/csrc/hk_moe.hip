@@ -127,36 +127,41 @@ __global__ void __launch_bounds__(256) moe_route_kernel(MoeDims d, MoeLayerDev L
 
 // Gate/up of one (16-row tile, slot).  Every workgroup of a routed slot first
 // ranks the router logits itself (softmax, top-k, renormalise:
-// source_qwen80_topk_router, one wave, 64-bit keys on the DPP network) and
-// takes its slot's expert; this costs about a microsecond per workgroup and
-// saves a launch.  Tile 0 of each slot publishes the slot's down organ (and
-// slot 0 the route and the shared-gate value) for the down kernel.
+// source_qwen80_topk_router; one wave, about 2 us) while its other waves copy
+// the layer's x image into LDS, and takes its slot's expert; this saves a
+// launch.  Tile 0 of each slot publishes the slot's down organ (and slot 0
+// the route and the shared-gate value) for the down kernel.
 template <int KIND, int D, int NPL>
 __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev L, MoeWs ws, int32_t* ids_out,
                                                           float* w_out) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ int32_t sel_id;
+    __shared__ TopkLds tk;
     const uint32_t slot = blockIdx.y, T = blockIdx.x;
     const int lane = threadIdx.x & 63, q = lane >> 4;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const bool lead = T == 0;
-    if (slot < d.K) {
-        if (wave == 0) {
-            const bool pub = lead && slot == 0;
-            const ArgBest mine = softmax_topk_wave<NPL>(ws.logits, d.E, d.K, 1, pub ? ws.ids : nullptr,
-                                                        pub ? ws.weights : nullptr, pub ? ws.status : nullptr);
-            if (pub && (uint32_t)lane < d.K) {
-                if (ids_out) ids_out[lane] = mine.i;
-                if (w_out) w_out[lane] = mine.v;
-            }
-            if (pub && lane == 0) ws.gate[1] = L.gate_w ? 1.0f / (1.0f + expf(-ws.gate[0])) : 1.0f;
-            if ((uint32_t)lane == slot) sel_id = mine.i;
+    const bool lead = T == 0, routed = slot < d.K;
+    const uint32_t S = n_steps_for(KIND, d.H), ib = (uint32_t)x_lds_bytes<KIND>(S);
+    if (routed && wave == 0) {
+        const bool pub = lead && slot == 0;
+        const ArgBest mine = softmax_topk_wave<NPL>(ws.logits, d.E, d.K, 1, pub ? ws.ids : nullptr,
+                                                    pub ? ws.weights : nullptr, pub ? ws.status : nullptr, &tk);
+        if (pub && (uint32_t)lane < d.K) {
+            if (ids_out) ids_out[lane] = mine.i;
+            if (w_out) w_out[lane] = mine.v;
         }
-        __syncthreads();
+        if (pub && lane == 0) ws.gate[1] = L.gate_w ? 1.0f / (1.0f + expf(-ws.gate[0])) : 1.0f;
+        if ((uint32_t)lane == slot) sel_id = mine.i;
+    } else {
+        // the x image built by the route kernel, into LDS
+        const uint32_t t0 = routed ? 64u : 0u;
+        for (uint32_t o = (threadIdx.x - t0) * 16u; o < ib; o += (blockDim.x - t0) * 16u)
+            *reinterpret_cast<uint4*>(lds + o) = *reinterpret_cast<const uint4*>(ws.img + o);
     }
-    const int32_t id = slot < d.K ? sel_id : (int32_t)d.E;
+    __syncthreads();
+    const int32_t id = routed ? sel_id : (int32_t)d.E;
     // an invalid route selects no organ (all-zero down view: n_tiles = 0)
-    const bool ok = slot >= d.K || (id >= 0 && (uint32_t)id < d.E);
+    const bool ok = !routed || (id >= 0 && (uint32_t)id < d.E);
     if (lead && threadIdx.x < sizeof(OrganView) / 8) {
         // word copy (a struct assignment here goes through scratch memory)
         static_assert(sizeof(OrganView) % 8 == 0, "OrganView is copied in 8-byte words");
@@ -168,7 +173,7 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev
     const OrganView g = L.table[(uint32_t)id * 3u + 0u];
     if (T >= g.n_tiles) return;
     const OrganView u = L.table[(uint32_t)id * 3u + 1u];
-    const uint32_t S = g.steps, per = (S + 3u) / 4u;
+    const uint32_t per = (S + 3u) / 4u;
     const uint32_t s0 = min(wave * per, S), n = min(s0 + per, S) - s0;
     Frag<KIND, 2> f[D];
 #pragma unroll
@@ -178,11 +183,6 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev
             fetch_one<KIND, 2>(u, T, s0 + k, lane, f[k], 1);
         }
     }
-    // the x image built by the route kernel, into LDS
-    const uint32_t ib = (uint32_t)x_lds_bytes<KIND>(S);
-    for (uint32_t o = threadIdx.x * 16u; o < ib; o += blockDim.x * 16u)
-        *reinterpret_cast<uint4*>(lds + o) = *reinterpret_cast<const uint4*>(ws.img + o);
-    __syncthreads();
     const int E = ws.img_e[0];
     const ImageA A{lds, a_lane_offset(lane)};
     const float* SX = reinterpret_cast<const float*>(lds + (size_t)S * Kcfg<KIND>::P * A_TILE_STRIDE);

@@ -185,15 +185,41 @@ __device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
     return ((uint64_t)hi << 32) | lo;
 }
 
-// The tie_eps == 0 selection of softmax_topk_block for one wave (blockDim 64,
-// n <= 64 * NPL) without barriers or LDS: lane l holds the keys of
-// p[l + 64 j] in registers, a round takes the wave-wide max key on the DPP
-// network and only the lane that owned the winner recomputes its best.  Same
-// result as the block form for finite logits.  Returns, in lane r < k, the
-// r-th selection (id, weight); ids_out / w_out get all k.
+__device__ __forceinline__ uint32_t wave_incl_sum_u32(uint32_t v) {
+    v += (uint32_t)dpp_i32<DPP_ROW_SHR1, 0xF>(0, (int)v);
+    v += (uint32_t)dpp_i32<DPP_ROW_SHR2, 0xF>(0, (int)v);
+    v += (uint32_t)dpp_i32<DPP_ROW_SHR4, 0xF>(0, (int)v);
+    v += (uint32_t)dpp_i32<DPP_ROW_SHR8, 0xF>(0, (int)v);
+    v += (uint32_t)dpp_i32<DPP_ROW_BCAST15, 0xA>(0, (int)v);
+    v += (uint32_t)dpp_i32<DPP_ROW_BCAST31, 0xC>(0, (int)v);
+    return v;
+}
+
+// LDS a wave's top-k selection works in (HK_TOPK_MAX candidates and slots).
+struct TopkLds {
+    uint64_t cand[64];
+    int32_t sel_i[HK_TOPK_MAX];
+    float sel_v[HK_TOPK_MAX];
+};
+
+// The tie_eps == 0 selection of softmax_topk_block for one wave (all 64 lanes,
+// n <= 64 * NPL, k <= 64); same result as the block form for finite logits.
+// Lane l holds p[l + 64 j].  The order is (q desc, index asc) with
+// q = p / sum (renorm = 1) or p * (1/sum), on 64-bit keys: high word
+// bits(q) + 1, low word ~index.
+//   1. tau = the k-th largest lane-best p, to 16 bits (a bitwise ballot
+//      count), is a lower bound of the k-th largest p; every p >= tau
+//      (1 - 2^-20) is a candidate -- the relaxation keeps any element whose
+//      rounded quotient could tie a selected one.
+//   2. The candidates (usually k..2k) are compacted into LDS; each forms its
+//      quotient and key, and its rank is the number of larger keys; ranks < k
+//      are the selection, in order.
+// With more than 64 candidates (flat distributions) it falls back to k
+// rounds of a wave-wide key max.  Returns, in lane r < k, the r-th selection
+// (id, weight); ids_out / w_out (if not null) get all k.
 template <int NPL>
 __device__ ArgBest softmax_topk_wave(const float* __restrict__ logits, uint32_t n, uint32_t k, int renorm,
-                                     int32_t* ids_out, float* w_out, uint32_t* status) {
+                                     int32_t* ids_out, float* w_out, uint32_t* status, TopkLds* t) {
     const int lane = threadIdx.x & 63;
     float p[NPL];
     float m = -INFINITY;
@@ -208,37 +234,80 @@ __device__ ArgBest softmax_topk_wave(const float* __restrict__ logits, uint32_t 
     if (bad && status) atomicOr(status, HK_DEVERR_NONFINITE);
     m = wave_max(m);
     float local = 0.f;
+    uint32_t bv = 0;
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
-        if ((uint32_t)lane + 64u * j < n) {
-            p[j] = expf(p[j] - m);
-            local += p[j];
-        }
+        p[j] = (uint32_t)lane + 64u * j < n ? expf(p[j] - m) : 0.0f;
+        local += p[j];
+        bv = max(bv, __builtin_bit_cast(uint32_t, p[j]));
     }
     const float sum = wave_sum(local);
     const float inv = 1.0f / sum;
-    uint64_t key[NPL];
-    uint64_t best = 0;
+    const uint32_t kk = min(k, 64u);
+    uint32_t tau = 0;
 #pragma unroll
-    for (int j = 0; j < NPL; ++j) {
-        const uint32_t i = (uint32_t)lane + 64u * j;
-        key[j] = i < n ? prob_key(renorm ? p[j] / sum : p[j] * inv, i) : 0ull;
-        best = umax64(best, key[j]);
+    for (int b = 30; b >= 15; --b) {
+        const uint32_t c = tau | (1u << b);
+        if ((uint32_t)__popcll(__ballot(bv >= c)) >= kk) tau = c;
     }
-    ArgBest mine{0.0f, -1};
-    for (uint32_t r = 0; r < k; ++r) {
-        const uint64_t w = wave_max_key(best);
-        const uint32_t wi = ~(uint32_t)w;
-        if ((uint32_t)lane == r) {
-            mine.i = w ? (int)wi : -1;
-            mine.v = __builtin_bit_cast(float, (uint32_t)(w >> 32) - 1u);
-        }
-        if (w && (wi & 63u) == (uint32_t)lane) {
-            best = 0;
+    const float tf = __builtin_bit_cast(float, tau) * (1.0f - 0x1p-20f);
+    uint32_t cnt = 0;
 #pragma unroll
-            for (int j = 0; j < NPL; ++j) {
-                key[j] = key[j] == w ? 0ull : key[j];
-                best = umax64(best, key[j]);
+    for (int j = 0; j < NPL; ++j) cnt += ((uint32_t)lane + 64u * j < n && p[j] >= tf) ? 1u : 0u;
+    const uint32_t incl = wave_incl_sum_u32(cnt);
+    const uint32_t C = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+    ArgBest mine{0.0f, -1};
+    if (C <= 64u) {
+        uint32_t o = incl - cnt;
+#pragma unroll
+        for (int j = 0; j < NPL; ++j)
+            if ((uint32_t)lane + 64u * j < n && p[j] >= tf)
+                t->cand[o++] = ((uint64_t)__builtin_bit_cast(uint32_t, p[j]) << 32) | (uint64_t)((uint32_t)lane + 64u * j);
+        __builtin_amdgcn_wave_barrier();
+        uint64_t me = 0;
+        if ((uint32_t)lane < C) {
+            const uint64_t c = t->cand[lane];
+            const float pv = __builtin_bit_cast(float, (uint32_t)(c >> 32));
+            const float q = renorm ? pv / sum : pv * inv;
+            me = ((uint64_t)(__builtin_bit_cast(uint32_t, q) + 1u) << 32) | (uint64_t)(~(uint32_t)c);
+        }
+        __builtin_amdgcn_wave_barrier();
+        if ((uint32_t)lane < C) t->cand[lane] = me;
+        __builtin_amdgcn_wave_barrier();
+        uint32_t rank = 0;
+        for (uint32_t u = 0; u < C; ++u) rank += t->cand[u] > me ? 1u : 0u;
+        if ((uint32_t)lane < C && rank < k) {
+            t->sel_i[rank] = (int32_t)~(uint32_t)me;
+            t->sel_v[rank] = __builtin_bit_cast(float, (uint32_t)(me >> 32) - 1u);
+        }
+        __builtin_amdgcn_wave_barrier();
+        if ((uint32_t)lane < k) {
+            mine.i = t->sel_i[lane];
+            mine.v = t->sel_v[lane];
+        }
+    } else {
+        uint64_t key[NPL];
+        uint64_t best = 0;
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) {
+            const uint32_t i = (uint32_t)lane + 64u * j;
+            key[j] = i < n ? prob_key(renorm ? p[j] / sum : p[j] * inv, i) : 0ull;
+            best = umax64(best, key[j]);
+        }
+        for (uint32_t r = 0; r < k; ++r) {
+            const uint64_t w = wave_max_key(best);
+            const uint32_t wi = ~(uint32_t)w;
+            if ((uint32_t)lane == r) {
+                mine.i = w ? (int)wi : -1;
+                mine.v = __builtin_bit_cast(float, (uint32_t)(w >> 32) - 1u);
+            }
+            if (w && (wi & 63u) == (uint32_t)lane) {
+                best = 0;
+#pragma unroll
+                for (int j = 0; j < NPL; ++j) {
+                    key[j] = key[j] == w ? 0ull : key[j];
+                    best = umax64(best, key[j]);
+                }
             }
         }
     }

@@ -143,6 +143,46 @@ def test_small_layer_uploaded_from_oracle(ctx, oracle, kind):
         assert oracle.relative_l2(out, L.forward_f64(h, ids)) < TOL
 
 
+def test_decode_router_exact_ties_and_flat_logits(ctx, oracle):
+    """The decode top-k (threshold + rank, k-round fallback past 64
+    candidates) on exact ties: duplicated router rows give equal logits,
+    ranked by index; all-zero router rows give 128 equal probabilities (the
+    fallback), so the route is experts 0..k-1 with weight 1/k each."""
+    from hawking_amd.moe import MoeModel, MoeShape
+    E, K = 128, 8
+    shape = MoeShape(n_layers=1, hidden=256, inter=128, shared_inter=128, n_experts=E, top_k=K,
+                     expert_kind=U.HK_Q4, expert_group=32)
+    seed = 77
+    experts = [tuple(U.oracle_organ(oracle, seed, shape, 0, e, p) for p in range(3)) for e in range(E)]
+    shared = tuple(U.oracle_organ(oracle, seed, shape, 0, E, p) for p in range(3))
+    norm, router, gate = U.dense(oracle, seed, shape, 0)
+    h = oracle.normal(oracle.stream_key(U.SEED, 0x71E), 256, 1.0)
+    logits = oracle.MoeLayer(256, 128, E, K, norm, router, experts, shared=shared, shared_gate_w=gate).forward(h)[4]
+    top = int(np.argmax(logits))
+    tied = router.copy()
+    for e in (5, 40, 77, 100):      # four equal logits, twice the largest
+        tied[e] = 2.0 * router[top]
+    for e in (9, 10):               # two more equal ones
+        tied[e] = 1.5 * router[top]
+    m = MoeModel(ctx, shape)
+    for label, R in (("tied rows", tied), ("flat", np.zeros_like(router))):
+        say("decode router", label)
+        m.set_layer(0, norm, R, [tuple(U.organ_dict(o) for o in t) for t in experts],
+                    shared=[U.organ_dict(o) for o in shared], shared_gate_w=gate)
+        L = oracle.MoeLayer(256, 128, E, K, norm, R, experts, shared=shared, shared_gate_w=gate)
+        out, ids, w = m.moe_suffix(0, h)
+        rout, rids, rw, _, logits = L.forward(h)
+        assert ids.tolist() == rids.tolist(), label
+        assert np.max(np.abs(w - rw)) <= 1e-6
+        assert oracle.relative_l2(out, rout) < TOL
+        if label == "flat":
+            assert ids.tolist() == list(range(K))
+            assert np.allclose(w, 1.0 / K, rtol=0, atol=1e-7)
+        else:
+            pos = [ids.tolist().index(e) for e in (5, 40, 77, 100)]
+            assert pos == sorted(pos)
+
+
 @pytest.mark.parametrize("kind", [U.HK_Q4, U.HK_MIXED])
 def test_synthetic_layer_matches_oracle_regeneration(ctx, oracle, kind):
     """Device-generated weights == oracle-regenerated weights, end to end."""
