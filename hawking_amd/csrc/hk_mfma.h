@@ -183,12 +183,20 @@ __device__ __forceinline__ int32_t quantize8(const float4* v, int E, float* f) {
 // image columns) x is quantized in place, every chunk being read and
 // rewritten by its owner only.  8 * team size must be a multiple of the
 // step's columns.  Ends with team.sync().
+//
+// [tb, te) limits the build to those steps (E still comes from all of x), so
+// several teams can build parts of one image; xq then stands for image column
+// tb * step columns, and the register chunks are used only when tb = 0.
 template <int KIND, int NC, class Team>
 __device__ int x_image(const Team& team, const XChunks<NC>& xc, const float* x, uint32_t cols, uint32_t steps,
-                       uint8_t* img, float* xq, uint32_t xq_stride, float* red, bool* nonfinite) {
+                       uint8_t* img, float* xq, uint32_t xq_stride, float* red, bool* nonfinite, uint32_t tb = 0,
+                       uint32_t te = 0xFFFFFFFFu) {
     constexpr int P = Kcfg<KIND>::P, SC = Kcfg<KIND>::STEP_COLS, NL = Kcfg<KIND>::SXG / 8;
     const uint32_t me = team.idx(), ts = team.size();
     const uint32_t nch = steps * (uint32_t)SC / 8u, wcols = 8u * ts, rounds = (nch + ts - 1u) / ts;
+    te = min(te, steps);
+    const uint32_t cb = tb * (uint32_t)SC / 8u, ce = te * (uint32_t)SC / 8u;
+    const uint32_t prounds = ce > cb ? (ce - cb + ts - 1u) / ts : 0u;
     float* SX = reinterpret_cast<float*>(img + (size_t)steps * P * A_TILE_STRIDE);
     uint32_t* A = reinterpret_cast<uint32_t*>(img);
 
@@ -207,12 +215,13 @@ __device__ int x_image(const Team& team, const XChunks<NC>& xc, const float* x, 
     if (!bad && m > 0.0f) (void)frexpf(m, &e2);
     const int E = (!bad && m > 0.0f) ? 23 - e2 : 0;
 
-    for (int i = (int)me; i < (int)steps * P * 4; i += (int)ts) A[(i >> 2) * (A_TILE_STRIDE / 4) + 64 + (i & 3)] = 0u;
+    for (int i = (int)(tb * P * 4 + me); i < (int)te * P * 4; i += (int)ts)
+        A[(i >> 2) * (A_TILE_STRIDE / 4) + 64 + (i & 3)] = 0u;
 
     auto round = [&](uint32_t j, float4* v) {
         float* w = xq + j * xq_stride;
-        const uint32_t ch = me + j * ts;
-        if (ch < nch) {
+        const uint32_t ch = cb + me + j * ts;
+        if (ch < ce) {
             if (bad) v[0] = v[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             float f[8];
             int32_t s = quantize8(v, E, f);
@@ -227,7 +236,7 @@ __device__ int x_image(const Team& team, const XChunks<NC>& xc, const float* x, 
         team.sync();
         // this round's steps; unit = (tau, slot q, dword d): 4 A bytes -> 4
         // lanes' dwords via a byte transpose
-        const uint32_t t0 = j * (wcols / (uint32_t)SC), t1 = min(t0 + wcols / (uint32_t)SC, steps);
+        const uint32_t t0 = tb + j * (wcols / (uint32_t)SC), t1 = min(t0 + wcols / (uint32_t)SC, te);
         const int nunits = (int)(t1 - t0) * P * 16;
         for (int u = (int)me; u < nunits; u += (int)ts) {
             const int d = u & 3, q = (u >> 2) & 3, tl = u >> 4;
@@ -247,15 +256,16 @@ __device__ int x_image(const Team& team, const XChunks<NC>& xc, const float* x, 
         }
         team.sync();
     };
+    const uint32_t jr = tb == 0 ? (uint32_t)NC : 0u;  // rounds served from the register chunks
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
-        if ((uint32_t)j >= rounds) break;
+        if ((uint32_t)j >= min(jr, prounds)) break;
         float4 v[2] = {xc.v[j][0], xc.v[j][1]};
         round((uint32_t)j, v);
     }
-    for (uint32_t j = NC; j < rounds; ++j) {
+    for (uint32_t j = min(jr, prounds); j < prounds; ++j) {
         float4 v[2];
-        load_chunk(x, 8u * (me + j * ts), cols, v);
+        load_chunk(x, 8u * (cb + me + j * ts), cols, v);
         round(j, v);
     }
     return E;

@@ -7,8 +7,9 @@
 //  crates/hawking-core/src/model/qwen80_device_expert_table.rs:1204-1247):
 //   1. route:   every block recomputes xn = RMSNorm(1+w)(h) in LDS; blocks
 //               0..ceil(E/4)-1 compute the router logits (one row per wave),
-//               the last block computes the shared-gate logit and the x image
-//               of xn (fixed-point limb tiles, built once per layer).
+//               the next block also the shared-gate logit, and the blocks
+//               from there build the x image of xn (fixed-point limb tiles,
+//               once per layer), 512 columns each.
 //   2. gate/up: one workgroup per (16-row tile, slot); each runs softmax /
 //               top-k / renormalise over the logits itself to find its
 //               slot's expert (slot K = the shared expert), then its 4 waves
@@ -62,7 +63,7 @@ __global__ void __launch_bounds__(256) moe_route_kernel(MoeDims d, MoeLayerDev L
     if (blockIdx.x < nrb) {
         const uint32_t row = blockIdx.x * 4u + wave;
         if (row < d.E) wrow = L.router_w + (size_t)row * d.H;
-    } else if (wave == 0) {
+    } else if (blockIdx.x == nrb && wave == 0) {
         wrow = L.gate_w;
     }
     const float4* w4 = reinterpret_cast<const float4*>(wrow);
@@ -111,15 +112,17 @@ __global__ void __launch_bounds__(256) moe_route_kernel(MoeDims d, MoeLayerDev L
                 ws.gate[0] = acc;
         }
     }
-    if (blockIdx.x == nrb) {
-        // the x image of xn for every gate/up organ of this layer (xn quantized in place)
+    if (blockIdx.x >= nrb) {
+        // the x image of xn for every gate/up organ of this layer, 512 columns
+        // per block (xn quantized in place)
         bool bad = false;
-        const uint32_t S = n_steps_for(KIND, d.H);
+        const uint32_t S = n_steps_for(KIND, d.H), spb = 512u / tile_step_cols(KIND), tb = (blockIdx.x - nrb) * spb;
         XChunks<1> xc;
         load_x<1>(BlockTeam{}, xn, d.H, xc);
-        const int E = x_image<KIND, 1>(BlockTeam{}, xc, xn, d.H, S, ws.img, xn, 8u * blockDim.x, red, &bad);
+        const int E = x_image<KIND, 1>(BlockTeam{}, xc, xn, d.H, S, ws.img, xn + tb * tile_step_cols(KIND),
+                                       8u * blockDim.x, red, &bad, tb, tb + spb);
         if (threadIdx.x == 0) {
-            ws.img_e[0] = E;
+            if (blockIdx.x == nrb) ws.img_e[0] = E;
             if (bad) atomicOr(ws.status, HK_DEVERR_NONFINITE);
         }
     }
@@ -287,7 +290,8 @@ static hipError_t launch_layer(const MoeDims& d, const MoeLayerDev& L, const flo
     const uint32_t slots = d.K + (d.has_shared ? 1u : 0u);
     const uint32_t gu_tiles = n_tiles_for(d.has_shared ? max(d.I, d.SI) : d.I);
     const uint32_t img_stride = (uint32_t)moe_img_bytes(KIND, d.Imax);
-    hipLaunchKernelGGL(moe_route_kernel<KIND>, dim3(nrb + 1u), dim3(256), (size_t)stage_floats(KIND, d.H) * sizeof(float),
+    const uint32_t nib = (d.H + 511u) / 512u;  // image blocks, 512 columns each
+    hipLaunchKernelGGL(moe_route_kernel<KIND>, dim3(nrb + nib), dim3(256), (size_t)stage_floats(KIND, d.H) * sizeof(float),
                        s, d, L, h_in, ws);
     const dim3 gg(gu_tiles, slots);
     const size_t gl = moe_gate_up_lds_bytes(KIND, d.H);
