@@ -1299,7 +1299,8 @@ extern "C" int hk_moe_forward_batch(hk_ctx* ctx, hk_moe_model* m, uint32_t layer
         return set_error(ctx, HK_E_UNSUPPORTED, "moe batch: the batched block routes with HK_ROUTER_NOAUX_TC");
     if (n_tokens == 0 || n_tokens > hk::MOE_BATCH_MAX_TOKENS)
         return set_error(ctx, HK_E_INVALID_ARG, "moe batch: n_tokens must be in [1, 64]");
-    if (!x_bf16 || !y || !aligned16(y)) return set_error(ctx, HK_E_INVALID_ARG, "moe batch: NULL x/y or misaligned y");
+    if (!x_bf16 || !y || !aligned16(x_bf16) || !aligned16(y))
+        return set_error(ctx, HK_E_INVALID_ARG, "moe batch: NULL x/y, or x/y not 16-byte aligned");
     MoeLayerDev L;
     int rc = moe_layer_dev(ctx, m, layer, &L);
     if (rc) return rc;

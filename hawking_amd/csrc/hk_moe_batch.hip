@@ -26,7 +26,6 @@
 
 namespace hk {
 
-constexpr int MOE_TILES_PER_ITEM = 8;  // row tiles per workgroup item (2 per wave)
 constexpr uint32_t RT_ROWS = 32, RT_COLS = 128, RT_SLICE = MOE_BATCH_ROUTER_COLS;  // router tiling
 
 size_t moe_batch_img_bytes(uint32_t cols) { return x_lds_bytes<HK_Q4>(n_steps_for(HK_Q4, cols)); }
@@ -70,30 +69,63 @@ __device__ __forceinline__ uint32_t pair_token(const MoeBatchDims& d, uint32_t p
 // Floats of LDS x staging for `cols` columns (rounded up to whole Q4 steps).
 static uint32_t q4_stage_floats(uint32_t cols) { return n_steps_for(HK_Q4, cols) * tile_step_cols(HK_Q4); }
 
-// The Q4 x image of xs (LDS, >= q4_stage_floats(cols) floats, quantized in
-// place) into img (global), by the whole block.
-__device__ int x_image_in_place(float* xs, uint32_t cols, uint8_t* img, float* red, bool* bad) {
+// Image parts of 512 columns (4 Q4 steps): a token's image is built by
+// ceil(cols / 512) blocks, each computing E from all of x.
+constexpr uint32_t XPART_COLS = 512, XPART_STEPS = XPART_COLS / 128u;
+
+// Steps [tb, tb + XPART_STEPS) of the Q4 x image of xs (LDS, >=
+// q4_stage_floats(cols) floats, those columns quantized in place) into img
+// (global), by the whole block.
+__device__ int x_image_in_place(float* xs, uint32_t cols, uint8_t* img, float* red, bool* bad, uint32_t tb) {
     const uint32_t S = n_steps_for(HK_Q4, cols);
     XChunks<1> xc;
     load_x<1>(BlockTeam{}, xs, cols, xc);
-    return x_image<HK_Q4, 1>(BlockTeam{}, xc, xs, cols, S, img, xs, 8u * blockDim.x, red, bad);
+    return x_image<HK_Q4, 1>(BlockTeam{}, xc, xs, cols, S, img, xs + tb * 128u, 8u * blockDim.x, red, bad, tb,
+                             tb + XPART_STEPS);
 }
 
 __global__ void __launch_bounds__(256) moe_batch_xprep_kernel(MoeBatchDims d, const uint16_t* __restrict__ xb,
                                                               MoeBatchWs ws) {
     extern __shared__ __align__(16) float xs[];  // [H rounded up to whole steps]
     __shared__ float red[4];
-    const uint32_t t = blockIdx.x;
-    for (uint32_t c = threadIdx.x; c < d.H; c += blockDim.x) {
-        const float v = bf16_to_f32(xb[(size_t)t * d.H + c]);
-        xs[c] = v;
-        ws.x32[(size_t)t * d.H + c] = v;
+    const uint32_t t = blockIdx.x, part = blockIdx.y;
+    {
+        // 8 bf16 per thread and piece, 4 pieces in flight (hidden <= 8192)
+        const uint4* src = reinterpret_cast<const uint4*>(xb + (size_t)t * d.H);
+        const uint32_t n8 = d.H / 8u;
+        uint4 v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t k = threadIdx.x + (uint32_t)i * blockDim.x;
+            if (k < n8) v[i] = ldg(src + k);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t k = threadIdx.x + (uint32_t)i * blockDim.x;
+            if (k < n8) {
+                const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+                float f[8];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    f[2 * q] = bf16_to_f32((uint16_t)(w[q] & 0xFFFFu));
+                    f[2 * q + 1] = bf16_to_f32((uint16_t)(w[q] >> 16));
+                }
+                float4* o = reinterpret_cast<float4*>(xs + 8u * k);
+                o[0] = make_float4(f[0], f[1], f[2], f[3]);
+                o[1] = make_float4(f[4], f[5], f[6], f[7]);
+                if (8u * k / XPART_COLS == part) {
+                    float4* g = reinterpret_cast<float4*>(ws.x32 + (size_t)t * d.H + 8u * k);
+                    g[0] = o[0];
+                    g[1] = o[1];
+                }
+            }
+        }
     }
     __syncthreads();
     bool bad = false;
-    const int E = x_image_in_place(xs, d.H, ws.ximg + (size_t)t * ws.ximg_stride, red, &bad);
+    const int E = x_image_in_place(xs, d.H, ws.ximg + (size_t)t * ws.ximg_stride, red, &bad, part * XPART_STEPS);
     if (threadIdx.x == 0) {
-        ws.ximg_e[t] = E;
+        if (part == 0) ws.ximg_e[t] = E;
         if (bad) atomicOr(ws.status, HK_DEVERR_NONFINITE);
     }
 }
@@ -102,10 +134,11 @@ __global__ void __launch_bounds__(256) moe_batch_xprep_kernel(MoeBatchDims d, co
 
 // part[s][t][e] = sum over columns [256 s, 256 (s+1)) of W[e][k] x[t][k] for a
 // block of 32 router rows; thread (row r = tid / 8, tokens 4 (tid % 8) .. +3),
-// router rows and x staged in LDS 128 columns at a time.
+// router rows and x staged in LDS 128 columns at a time (hidden % 128 == 0).
+// The inner loop reads 4 columns of its row and 4 x rows per step, 16 FMAs.
 __global__ void __launch_bounds__(256) moe_batch_router_kernel(MoeBatchDims d, const float* __restrict__ W,
                                                                MoeBatchWs ws) {
-    __shared__ float wsh[RT_ROWS][RT_COLS + 1];
+    __shared__ __align__(16) float wsh[RT_ROWS][RT_COLS + 4];
     __shared__ __align__(16) float xsh[RT_COLS][32];
     const uint32_t rr = threadIdx.x >> 3, tg = threadIdx.x & 7u;
     const uint32_t r0 = blockIdx.x * RT_ROWS, s = blockIdx.y;
@@ -114,33 +147,44 @@ __global__ void __launch_bounds__(256) moe_batch_router_kernel(MoeBatchDims d, c
         float acc[4] = {0.f, 0.f, 0.f, 0.f};
         for (uint32_t kc = k0; kc < k1; kc += RT_COLS) {
             const uint32_t kn = min(RT_COLS, k1 - kc);
-            __syncthreads();
-            for (uint32_t idx = threadIdx.x; idx < RT_ROWS * RT_COLS / 4u; idx += blockDim.x) {
+            // every thread's loads of the chunk (4 row pieces, 4 x pieces) in flight, then the stores
+            constexpr uint32_t NP = RT_ROWS * RT_COLS / 4u / 256u;
+            static_assert(NP * 256u == 32u * RT_COLS / 4u, "x and W chunks have the same piece count");
+            float4 wv[NP], xv[NP];
+#pragma unroll
+            for (uint32_t i = 0; i < NP; ++i) {
+                const uint32_t idx = threadIdx.x + 256u * i;
                 const uint32_t row = idx / (RT_COLS / 4u), k = 4u * (idx % (RT_COLS / 4u));
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (r0 + row < d.E && k < kn) v = *reinterpret_cast<const float4*>(W + (size_t)(r0 + row) * d.H + kc + k);
-                wsh[row][k] = v.x;
-                wsh[row][k + 1] = v.y;
-                wsh[row][k + 2] = v.z;
-                wsh[row][k + 3] = v.w;
-            }
-            for (uint32_t idx = threadIdx.x; idx < 32u * RT_COLS / 4u; idx += blockDim.x) {
-                const uint32_t t = idx / (RT_COLS / 4u), k = 4u * (idx % (RT_COLS / 4u));
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (tb + t < d.T && k < kn) v = *reinterpret_cast<const float4*>(ws.x32 + (size_t)(tb + t) * d.H + kc + k);
-                xsh[k][t] = v.x;
-                xsh[k + 1][t] = v.y;
-                xsh[k + 2][t] = v.z;
-                xsh[k + 3][t] = v.w;
+                wv[i] = (r0 + row < d.E && k < kn) ? ldg(reinterpret_cast<const float4*>(W + (size_t)(r0 + row) * d.H + kc + k))
+                                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+                xv[i] = (tb + row < d.T && k < kn)
+                            ? ldg(reinterpret_cast<const float4*>(ws.x32 + (size_t)(tb + row) * d.H + kc + k))
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
             }
             __syncthreads();
-            for (uint32_t k = 0; k < kn; ++k) {
-                const float w = wsh[rr][k];
-                const float4 x = *reinterpret_cast<const float4*>(&xsh[k][4u * tg]);
-                acc[0] += w * x.x;
-                acc[1] += w * x.y;
-                acc[2] += w * x.z;
-                acc[3] += w * x.w;
+#pragma unroll
+            for (uint32_t i = 0; i < NP; ++i) {
+                const uint32_t idx = threadIdx.x + 256u * i;
+                const uint32_t row = idx / (RT_COLS / 4u), k = 4u * (idx % (RT_COLS / 4u));
+                *reinterpret_cast<float4*>(&wsh[row][k]) = wv[i];
+                xsh[k][row] = xv[i].x;
+                xsh[k + 1][row] = xv[i].y;
+                xsh[k + 2][row] = xv[i].z;
+                xsh[k + 3][row] = xv[i].w;
+            }
+            __syncthreads();
+#pragma unroll 4
+            for (uint32_t k = 0; k < kn; k += 4) {
+                const float4 w = *reinterpret_cast<const float4*>(&wsh[rr][k]);
+                const float wk[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (uint32_t i = 0; i < 4; ++i) {
+                    const float4 x = *reinterpret_cast<const float4*>(&xsh[k + i][4u * tg]);
+                    acc[0] += wk[i] * x.x;
+                    acc[1] += wk[i] * x.y;
+                    acc[2] += wk[i] * x.z;
+                    acc[3] += wk[i] * x.w;
+                }
             }
         }
         const uint32_t r = r0 + rr;
@@ -159,13 +203,31 @@ __device__ __forceinline__ float key_value(uint64_t k) {
     return __builtin_bit_cast(float, (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
 }
 
-__global__ void __launch_bounds__(64) moe_batch_route_kernel(MoeBatchDims d, const float* __restrict__ bias,
-                                                             MoeBatchWs ws, int32_t* ids_out, float* w_out) {
+// The block first sums each expert's split-K partials (in split order, every
+// load of a thread in flight at once) into LDS; one wave then selects.
+constexpr uint32_t MOE_ROUTER_MAX_SPLITS = 8192 / MOE_BATCH_ROUTER_COLS;
+
+__global__ void __launch_bounds__(256) moe_batch_route_kernel(MoeBatchDims d, const float* __restrict__ bias,
+                                                              MoeBatchWs ws, int32_t* ids_out, float* w_out) {
     constexpr int NPL = MOE_BATCH_MAX_EXPERTS / 64;
+    __shared__ float lg[MOE_BATCH_MAX_EXPERTS];
     __shared__ int32_t sel_i[16];
     __shared__ float sel_w[16];
     const int lane = threadIdx.x & 63;
     const uint32_t t = blockIdx.x, E = d.E, K = d.K, per = d.E / d.n_group;
+    for (uint32_t e = threadIdx.x; e < E; e += blockDim.x) {
+        float pv[MOE_ROUTER_MAX_SPLITS];
+#pragma unroll
+        for (uint32_t s = 0; s < MOE_ROUTER_MAX_SPLITS; ++s)
+            pv[s] = s < d.S ? ws.part[((size_t)s * d.T + t) * E + e] : 0.0f;
+        float l = 0.f;
+#pragma unroll
+        for (uint32_t s = 0; s < MOE_ROUTER_MAX_SPLITS; ++s)
+            if (s < d.S) l += pv[s];
+        lg[e] = l;
+    }
+    __syncthreads();
+    if (threadIdx.x >= 64) return;
     float sc[NPL], cv[NPL];
     uint32_t bad = 0;
 #pragma unroll
@@ -174,8 +236,7 @@ __global__ void __launch_bounds__(64) moe_batch_route_kernel(MoeBatchDims d, con
         sc[j] = 0.f;
         cv[j] = -INFINITY;
         if (i < E) {
-            float l = 0.f;
-            for (uint32_t s = 0; s < d.S; ++s) l += ws.part[((size_t)s * d.T + t) * E + i];
+            const float l = lg[i];
             if (!isfinite(l)) bad = 1;
             sc[j] = 1.0f / (1.0f + expf(-l));
             cv[j] = sc[j] + bias[i];
@@ -392,12 +453,34 @@ __device__ __forceinline__ void tiles_x_tokens(const uint8_t* const* base_d, con
     }
 }
 
-// Copies the x images of nm member tokens into LDS (all threads of the block).
+// Copies the x images of nm <= TB member tokens (rows idx[] of src) into LDS
+// (all threads of the block): per pass every thread loads PT pieces of each
+// image before its first store (the image index is a compile-time loop
+// variable, so no per-piece table lookup).
+template <int TB, int PT>
 __device__ __forceinline__ void stage_images(uint8_t* lds, const uint8_t* src, uint32_t stride, const uint32_t* idx,
                                              uint32_t nm, uint32_t img_bytes) {
-    for (uint32_t o = threadIdx.x * 16u; o < nm * img_bytes; o += blockDim.x * 16u) {
-        const uint32_t j = o / img_bytes, off = o % img_bytes;
-        *reinterpret_cast<uint4*>(lds + o) = *reinterpret_cast<const uint4*>(src + (size_t)idx[j] * stride + off);
+    const uint32_t n16 = img_bytes / 16u, nt = blockDim.x;
+    for (uint32_t b = 0; b < n16; b += PT * nt) {
+        uint4 v[TB][PT];
+#pragma unroll
+        for (int j = 0; j < TB; ++j) {
+            const uint4* sj = reinterpret_cast<const uint4*>(src + (size_t)idx[j] * stride);
+#pragma unroll
+            for (int i = 0; i < PT; ++i) {
+                const uint32_t k = b + threadIdx.x + (uint32_t)i * nt;
+                if ((uint32_t)j < nm && k < n16) v[j][i] = ldg(sj + k);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < TB; ++j) {
+            uint4* dj = reinterpret_cast<uint4*>(lds + (size_t)j * img_bytes);
+#pragma unroll
+            for (int i = 0; i < PT; ++i) {
+                const uint32_t k = b + threadIdx.x + (uint32_t)i * nt;
+                if ((uint32_t)j < nm && k < n16) dj[k] = v[j][i];
+            }
+        }
     }
 }
 
@@ -432,14 +515,16 @@ struct ItemMap {
 
 // ------------------------------------------------------------------ 5. gate/up (grouped)
 
-template <int TB, int D>
-__global__ void __launch_bounds__(256) moe_batch_gate_up_kernel(MoeBatchDims d, const OrganView* __restrict__ table,
-                                                                MoeBatchWs ws) {
+// An item covers TPI row tiles; a workgroup of TPI / TPW waves, each wave
+// runs TPW row tiles (gate and up of each) for the item's member tokens.
+template <int TB, int D, int TPW, int TPI>
+__global__ void __launch_bounds__(64 * TPI / TPW)
+moe_batch_gate_up_kernel(MoeBatchDims d, const OrganView* __restrict__ table, MoeBatchWs ws) {
     extern __shared__ __align__(16) uint8_t lds[];  // TB x images of H columns
     const int lane = threadIdx.x & 63, q = lane >> 4;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t aoff = a_lane_offset(lane);
-    const uint32_t tiles = n_tiles_for(max(d.I, d.SI)), gpe = (tiles + MOE_TILES_PER_ITEM - 1) / MOE_TILES_PER_ITEM;
+    const uint32_t tiles = n_tiles_for(max(d.I, d.SI)), gpe = (tiles + TPI - 1) / TPI;
     const uint32_t S = n_steps_for(HK_Q4, d.H);
     const uint32_t img_bytes = (uint32_t)x_lds_bytes<HK_Q4>(S);
     const ItemMap im(d, gpe, __builtin_amdgcn_readfirstlane(*ws.n_active), TB);
@@ -448,15 +533,21 @@ __global__ void __launch_bounds__(256) moe_batch_gate_up_kernel(MoeBatchDims d, 
         im.at(item, &a, &tg, &mg_lo, &mg_hi);
         const uint4 ent = ws.active[a];
         const OrganView g = table[ent.x * 3u + 0u], u = table[ent.x * 3u + 1u];
-        if (tg * MOE_TILES_PER_ITEM >= g.n_tiles) continue;
-        // this wave's two tiles (the second aliases the first past the end)
-        const uint32_t T0 = tg * MOE_TILES_PER_ITEM + 2u * wave, T1 = T0 + 1u;
-        const bool v0 = T0 < g.n_tiles, v1 = T1 < g.n_tiles;
-        const uint32_t T1c = v1 ? T1 : T0;
-        const uint8_t* bd[4] = {g.data + ((size_t)T0 * S) * 1024u + 16u * lane, u.data + ((size_t)T0 * S) * 1024u + 16u * lane,
-                                g.data + ((size_t)T1c * S) * 1024u + 16u * lane, u.data + ((size_t)T1c * S) * 1024u + 16u * lane};
-        const uint16_t* bs[4] = {g.scales + (size_t)T0 * S * 64u + lane, u.scales + (size_t)T0 * S * 64u + lane,
-                                 g.scales + (size_t)T1c * S * 64u + lane, u.scales + (size_t)T1c * S * 64u + lane};
+        if (tg * TPI >= g.n_tiles) continue;
+        // this wave's tiles (past the end they alias the first)
+        const uint32_t Tb = tg * TPI + TPW * wave;
+        bool vw[TPW];
+        const uint8_t* bd[2 * TPW];
+        const uint16_t* bs[2 * TPW];
+#pragma unroll
+        for (int h = 0; h < TPW; ++h) {
+            vw[h] = Tb + h < g.n_tiles;
+            const size_t Tc = vw[h] ? Tb + h : Tb;
+            bd[2 * h] = g.data + Tc * S * 1024u + 16u * lane;
+            bd[2 * h + 1] = u.data + Tc * S * 1024u + 16u * lane;
+            bs[2 * h] = g.scales + Tc * S * 64u + lane;
+            bs[2 * h + 1] = u.scales + Tc * S * 64u + lane;
+        }
         const uint32_t m_end = mg_hi == 0xFFFFFFFFu ? ent.z : min(ent.z, mg_hi * (uint32_t)TB);
         for (uint32_t m0 = mg_lo * TB; m0 < m_end; m0 += TB) {
             const uint32_t nm = min((uint32_t)TB, ent.z - m0);
@@ -467,20 +558,20 @@ __global__ void __launch_bounds__(256) moe_batch_gate_up_kernel(MoeBatchDims d, 
                 tok[j] = pair_token(d, pair[j]);
             }
             __syncthreads();
-            stage_images(lds, ws.ximg, ws.ximg_stride, tok, nm, img_bytes);
+            stage_images<TB, 4>(lds, ws.ximg, ws.ximg_stride, tok, nm, img_bytes);
             __syncthreads();
-            if (!v0) continue;
-            float acc[TB][4] = {};
-            tiles_x_tokens<4, TB, D>(bd, bs, S, lds, img_bytes, nm, aoff, q, acc);
+            if (!vw[0]) continue;
+            float acc[TB][2 * TPW] = {};
+            tiles_x_tokens<2 * TPW, TB, D>(bd, bs, S, lds, img_bytes, nm, aoff, q, acc);
 #pragma unroll
             for (int j = 0; j < TB; ++j) {
                 if ((uint32_t)j >= nm) break;
                 const int E = ws.ximg_e[tok[j]];
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
+                for (int h = 0; h < TPW; ++h) {
                     const float gs = ldexpf(tile_row_sum(acc[j][2 * h]), -E), us = ldexpf(tile_row_sum(acc[j][2 * h + 1]), -E);
-                    const uint32_t row = (h ? T1 : T0) * 16u + (uint32_t)(lane & 15);
-                    if (lane < 16 && (h ? v1 : v0) && row < g.rows)
+                    const uint32_t row = (Tb + h) * 16u + (uint32_t)(lane & 15);
+                    if (lane < 16 && vw[h] && row < g.rows)
                         ws.act[(size_t)pair[j] * d.Imax + row] = (gs / (1.0f + expf(-gs))) * us;
                 }
             }
@@ -495,27 +586,27 @@ __global__ void __launch_bounds__(256) moe_batch_act_image_kernel(MoeBatchDims d
     __shared__ float red[4];
     const uint32_t p = blockIdx.x;
     const uint32_t cols = p < d.T * d.K ? d.I : d.SI;
-    const float4* a4 = reinterpret_cast<const float4*>(ws.act + (size_t)p * d.Imax);
-    for (uint32_t j = threadIdx.x; j < cols / 4u; j += blockDim.x) reinterpret_cast<float4*>(xs)[j] = a4[j];
+    copy16_to_lds<4>(reinterpret_cast<uint4*>(xs), reinterpret_cast<const uint4*>(ws.act + (size_t)p * d.Imax), cols / 4u,
+                     threadIdx.x, blockDim.x);
     __syncthreads();
     bool bad = false;
-    const int E = x_image_in_place(xs, cols, ws.aimg + (size_t)p * ws.aimg_stride, red, &bad);
+    const int E = x_image_in_place(xs, cols, ws.aimg + (size_t)p * ws.aimg_stride, red, &bad, blockIdx.y * XPART_STEPS);
     if (threadIdx.x == 0) {
-        ws.aimg_e[p] = E;
+        if (blockIdx.y == 0) ws.aimg_e[p] = E;
         if (bad) atomicOr(ws.status, HK_DEVERR_NONFINITE);
     }
 }
 
 // ------------------------------------------------------------------ 7. down (grouped)
 
-template <int TB, int D>
-__global__ void __launch_bounds__(256) moe_batch_down_kernel(MoeBatchDims d, const OrganView* __restrict__ table,
-                                                             MoeBatchWs ws) {
+template <int TB, int D, int TPW, int TPI>
+__global__ void __launch_bounds__(64 * TPI / TPW)
+moe_batch_down_kernel(MoeBatchDims d, const OrganView* __restrict__ table, MoeBatchWs ws) {
     extern __shared__ __align__(16) uint8_t lds[];  // TB activation images
     const int lane = threadIdx.x & 63, q = lane >> 4;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t aoff = a_lane_offset(lane);
-    const uint32_t tiles = n_tiles_for(d.H), gpe = (tiles + MOE_TILES_PER_ITEM - 1) / MOE_TILES_PER_ITEM;
+    const uint32_t tiles = n_tiles_for(d.H), gpe = (tiles + TPI - 1) / TPI;
     const ItemMap im(d, gpe, __builtin_amdgcn_readfirstlane(*ws.n_active), TB);
     const uint32_t np = d.T * d.K;
     for (uint32_t item = blockIdx.x; item < im.n_items; item += gridDim.x) {
@@ -524,11 +615,17 @@ __global__ void __launch_bounds__(256) moe_batch_down_kernel(MoeBatchDims d, con
         const uint4 ent = ws.active[a];
         const OrganView o = table[ent.x * 3u + 2u];
         const uint32_t S = o.steps, img_bytes = (uint32_t)x_lds_bytes<HK_Q4>(S);
-        const uint32_t T0 = tg * MOE_TILES_PER_ITEM + 2u * wave, T1 = T0 + 1u;
-        const bool v0 = T0 < o.n_tiles, v1 = T1 < o.n_tiles;
-        const uint32_t T1c = v1 ? T1 : T0;
-        const uint8_t* bd[2] = {o.data + ((size_t)T0 * S) * 1024u + 16u * lane, o.data + ((size_t)T1c * S) * 1024u + 16u * lane};
-        const uint16_t* bs[2] = {o.scales + (size_t)T0 * S * 64u + lane, o.scales + (size_t)T1c * S * 64u + lane};
+        const uint32_t Tb = tg * TPI + TPW * wave;
+        bool vw[TPW];
+        const uint8_t* bd[TPW];
+        const uint16_t* bs[TPW];
+#pragma unroll
+        for (int h = 0; h < TPW; ++h) {
+            vw[h] = Tb + h < o.n_tiles;
+            const size_t Tc = vw[h] ? Tb + h : Tb;
+            bd[h] = o.data + Tc * S * 1024u + 16u * lane;
+            bs[h] = o.scales + Tc * S * 64u + lane;
+        }
         const uint32_t m_end = mg_hi == 0xFFFFFFFFu ? ent.z : min(ent.z, mg_hi * (uint32_t)TB);
         for (uint32_t m0 = mg_lo * TB; m0 < m_end; m0 += TB) {
             const uint32_t nm = min((uint32_t)TB, ent.z - m0);
@@ -536,21 +633,21 @@ __global__ void __launch_bounds__(256) moe_batch_down_kernel(MoeBatchDims d, con
 #pragma unroll
             for (int j = 0; j < TB; ++j) pair[j] = ws.members[ent.y + m0 + min((uint32_t)j, nm - 1u)];
             __syncthreads();
-            stage_images(lds, ws.aimg, ws.aimg_stride, pair, nm, img_bytes);
+            stage_images<TB, 2>(lds, ws.aimg, ws.aimg_stride, pair, nm, img_bytes);
             __syncthreads();
-            if (!v0) continue;
-            float acc[TB][2] = {};
-            tiles_x_tokens<2, TB, D>(bd, bs, S, lds, img_bytes, nm, aoff, q, acc);
+            if (!vw[0]) continue;
+            float acc[TB][TPW] = {};
+            tiles_x_tokens<TPW, TB, D>(bd, bs, S, lds, img_bytes, nm, aoff, q, acc);
 #pragma unroll
             for (int j = 0; j < TB; ++j) {
                 if ((uint32_t)j >= nm) break;
                 const int E = ws.aimg_e[pair[j]];
                 const float w = pair[j] < np ? ws.w[pair[j]] : 1.0f;
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
+                for (int h = 0; h < TPW; ++h) {
                     const float y = ldexpf(tile_row_sum(acc[j][h]), -E);
-                    const uint32_t row = (h ? T1 : T0) * 16u + (uint32_t)(lane & 15);
-                    if (lane < 16 && (h ? v1 : v0) && row < d.H) ws.ybuf[(size_t)pair[j] * d.H + row] = y * w;
+                    const uint32_t row = (Tb + h) * 16u + (uint32_t)(lane & 15);
+                    if (lane < 16 && vw[h] && row < d.H) ws.ybuf[(size_t)pair[j] * d.H + row] = y * w;
                 }
             }
         }
@@ -578,31 +675,39 @@ hipError_t launch_moe_batch(const MoeBatchDims& d, const MoeLayerDev& L, const f
                             float* y, const MoeBatchWs& ws, int32_t* ids_out, float* w_out, hipStream_t s) {
     const uint32_t pairs = d.T * d.K + (d.SI ? d.T : 0u);
     const uint32_t max_active = min(d.E, d.T * d.K) + (d.SI ? 1u : 0u);
-    const uint32_t gpe_gu = (n_tiles_for(max(d.I, d.SI)) + MOE_TILES_PER_ITEM - 1) / MOE_TILES_PER_ITEM;
-    const uint32_t gpe_dn = (n_tiles_for(d.H) + MOE_TILES_PER_ITEM - 1) / MOE_TILES_PER_ITEM;
+    // from sweeps of config 5: gate/up 8-tile items, one tile per wave, 6 steps
+    // in flight; down 8-tile items, two tiles per wave, 4 steps in flight
+    constexpr int GU_TPI = 8, GU_TPW = 1, GU_D = 6, DN_TPI = 8, DN_TPW = 2, DN_D = 4;
+    const uint32_t gpe_gu = (n_tiles_for(max(d.I, d.SI)) + GU_TPI - 1) / GU_TPI;
+    const uint32_t gpe_dn = (n_tiles_for(d.H) + DN_TPI - 1) / DN_TPI;
     const uint32_t gu_items = (max_active + (d.SI ? d.T : 0u)) * gpe_gu, dn_items = (max_active + (d.SI ? d.T : 0u)) * gpe_dn;
     const uint32_t ximg = (uint32_t)moe_batch_img_bytes(d.H), aimg = (uint32_t)moe_batch_img_bytes(d.Imax);
     const uint32_t tb_gu = tokens_per_group(ximg, 2u), tb_dn = tokens_per_group(aimg, 4u);
     if (tb_gu == 0 || tb_dn == 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(moe_batch_xprep_kernel, dim3(d.T), dim3(256), (size_t)q4_stage_floats(d.H) * sizeof(float), s, d,
-                       x_bf16, ws);
+    hipLaunchKernelGGL(moe_batch_xprep_kernel, dim3(d.T, (d.H + XPART_COLS - 1) / XPART_COLS), dim3(256),
+                       (size_t)q4_stage_floats(d.H) * sizeof(float), s, d, x_bf16, ws);
     hipLaunchKernelGGL(moe_batch_router_kernel, dim3((d.E + RT_ROWS - 1) / RT_ROWS, d.S), dim3(256), 0, s, d, L.router_w,
                        ws);
-    hipLaunchKernelGGL(moe_batch_route_kernel, dim3(d.T), dim3(64), 0, s, d, bias, ws, ids_out, w_out);
+    hipLaunchKernelGGL(moe_batch_route_kernel, dim3(d.T), dim3(256), 0, s, d, bias, ws, ids_out, w_out);
     hipLaunchKernelGGL(moe_batch_group_kernel, dim3(1), dim3(1024), 0, s, d, ws);
-    const dim3 ggu(min(gu_items, 1024u)), gdn(min(dn_items, 2048u));
+    // one workgroup per item (the item count is an upper bound; the device
+    // count decides): the dispatcher then balances ~1 MB items across the CUs
+    // better than a persistent grid (measured: 862 vs 910 us per step)
+    const dim3 ggu(gu_items), gdn(dn_items);
+    // one tile per wave, 8 waves sharing the staged images
+    const dim3 bgu(64 * GU_TPI / GU_TPW), bdn(64 * DN_TPI / DN_TPW);
     if (tb_gu >= 2)
-        hipLaunchKernelGGL((moe_batch_gate_up_kernel<2, 4>), ggu, dim3(256), (size_t)2 * ximg, s, d, L.table, ws);
+        hipLaunchKernelGGL((moe_batch_gate_up_kernel<2, GU_D, GU_TPW, GU_TPI>), ggu, bgu, (size_t)2 * ximg, s, d, L.table, ws);
     else
-        hipLaunchKernelGGL((moe_batch_gate_up_kernel<1, 4>), ggu, dim3(256), (size_t)ximg, s, d, L.table, ws);
-    hipLaunchKernelGGL(moe_batch_act_image_kernel, dim3(pairs), dim3(256), (size_t)q4_stage_floats(d.Imax) * sizeof(float),
-                       s, d, ws);
+        hipLaunchKernelGGL((moe_batch_gate_up_kernel<1, GU_D, GU_TPW, GU_TPI>), ggu, bgu, (size_t)ximg, s, d, L.table, ws);
+    hipLaunchKernelGGL(moe_batch_act_image_kernel, dim3(pairs, (d.Imax + XPART_COLS - 1) / XPART_COLS), dim3(256),
+                       (size_t)q4_stage_floats(d.Imax) * sizeof(float), s, d, ws);
     if (tb_dn >= 4)
-        hipLaunchKernelGGL((moe_batch_down_kernel<4, 4>), gdn, dim3(256), (size_t)4 * aimg, s, d, L.table, ws);
+        hipLaunchKernelGGL((moe_batch_down_kernel<4, DN_D, DN_TPW, DN_TPI>), gdn, bdn, (size_t)4 * aimg, s, d, L.table, ws);
     else if (tb_dn >= 2)
-        hipLaunchKernelGGL((moe_batch_down_kernel<2, 4>), gdn, dim3(256), (size_t)2 * aimg, s, d, L.table, ws);
+        hipLaunchKernelGGL((moe_batch_down_kernel<2, DN_D, DN_TPW, DN_TPI>), gdn, bdn, (size_t)2 * aimg, s, d, L.table, ws);
     else
-        hipLaunchKernelGGL((moe_batch_down_kernel<1, 4>), gdn, dim3(256), (size_t)aimg, s, d, L.table, ws);
+        hipLaunchKernelGGL((moe_batch_down_kernel<1, DN_D, DN_TPW, DN_TPI>), gdn, bdn, (size_t)aimg, s, d, L.table, ws);
     hipLaunchKernelGGL(moe_batch_combine_kernel, dim3(d.T, (d.H + 255u) / 256u), dim3(256), 0, s, d, ws, y);
     return hipGetLastError();
 }

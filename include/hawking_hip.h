@@ -282,7 +282,7 @@ int hk_moe_decode_stack(hk_ctx* ctx, hk_moe_model* model, const float* h_in, flo
  * [n_tokens x top_k] (device, route order) may be NULL.  Each active expert's
  * weights are streamed once for all of its tokens (grouped expert GEMM).
  * Requires router == HK_ROUTER_NOAUX_TC, expert_kind == HK_Q4, no shared gate,
- * n_tokens <= 64, n_experts <= 512.  The workspace for n_tokens is allocated
+ * n_tokens <= 64, n_experts <= 512, x and y 16-byte aligned.  The workspace for n_tokens is allocated
  * on first use (not graph-capturable until then). */
 int hk_moe_forward_batch(hk_ctx* ctx, hk_moe_model* model, uint32_t layer, const uint16_t* x_bf16,
                          uint32_t n_tokens, float* y, int32_t* ids, float* weights, hk_stream stream);
