@@ -666,9 +666,21 @@ __global__ void __launch_bounds__(256) moe_batch_combine_kernel(MoeBatchDims d, 
     y[(size_t)t * d.H + row] = acc;
 }
 
-// Token images per member group that fit the 64 KiB LDS budget.
-static uint32_t tokens_per_group(uint32_t img_bytes, uint32_t cap) {
-    return min(cap, (uint32_t)(65536u / img_bytes));
+// LDS a grouped workgroup may fill with staged token images: the device's
+// per-block maximum, at most 128 KiB (gfx950: 160 KiB per CU; for config 5,
+// four 31 KB x images per gate/up group, one workgroup per CU, beat two
+// images and two workgroups: 775 vs 816 us per step, as fewer member groups
+// re-stream an expert's weights).
+static uint32_t image_lds_budget() {
+    int dev = 0, v = 65536;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+        v = 65536;
+    return min((uint32_t)v, 131072u);
+}
+
+// Token images per member group that fit the budget.
+static uint32_t tokens_per_group(uint32_t img_bytes, uint32_t cap, uint32_t budget) {
+    return min(cap, budget / img_bytes);
 }
 
 hipError_t launch_moe_batch(const MoeBatchDims& d, const MoeLayerDev& L, const float* bias, const uint16_t* x_bf16,
@@ -682,7 +694,8 @@ hipError_t launch_moe_batch(const MoeBatchDims& d, const MoeLayerDev& L, const f
     const uint32_t gpe_dn = (n_tiles_for(d.H) + DN_TPI - 1) / DN_TPI;
     const uint32_t gu_items = (max_active + (d.SI ? d.T : 0u)) * gpe_gu, dn_items = (max_active + (d.SI ? d.T : 0u)) * gpe_dn;
     const uint32_t ximg = (uint32_t)moe_batch_img_bytes(d.H), aimg = (uint32_t)moe_batch_img_bytes(d.Imax);
-    const uint32_t tb_gu = tokens_per_group(ximg, 2u), tb_dn = tokens_per_group(aimg, 4u);
+    const uint32_t budget = image_lds_budget();
+    const uint32_t tb_gu = tokens_per_group(ximg, 4u, budget), tb_dn = tokens_per_group(aimg, 4u, budget);
     if (tb_gu == 0 || tb_dn == 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL(moe_batch_xprep_kernel, dim3(d.T, (d.H + XPART_COLS - 1) / XPART_COLS), dim3(256),
                        (size_t)q4_stage_floats(d.H) * sizeof(float), s, d, x_bf16, ws);
@@ -696,7 +709,9 @@ hipError_t launch_moe_batch(const MoeBatchDims& d, const MoeLayerDev& L, const f
     const dim3 ggu(gu_items), gdn(dn_items);
     // one tile per wave, 8 waves sharing the staged images
     const dim3 bgu(64 * GU_TPI / GU_TPW), bdn(64 * DN_TPI / DN_TPW);
-    if (tb_gu >= 2)
+    if (tb_gu >= 4)
+        hipLaunchKernelGGL((moe_batch_gate_up_kernel<4, GU_D, GU_TPW, GU_TPI>), ggu, bgu, (size_t)4 * ximg, s, d, L.table, ws);
+    else if (tb_gu >= 2)
         hipLaunchKernelGGL((moe_batch_gate_up_kernel<2, GU_D, GU_TPW, GU_TPI>), ggu, bgu, (size_t)2 * ximg, s, d, L.table, ws);
     else
         hipLaunchKernelGGL((moe_batch_gate_up_kernel<1, GU_D, GU_TPW, GU_TPI>), ggu, bgu, (size_t)ximg, s, d, L.table, ws);
