@@ -410,6 +410,118 @@ int hko_q2_decode(const uint16_t* scales, const uint8_t* codes, size_t count, fl
 }
 
 /* ------------------------------------------------------------------------ */
+/* Uniform factor codec (HGRAVU01 q8 G64, HGRAVS01 factors)                  */
+/* ------------------------------------------------------------------------ */
+
+/* pack_unsigned / packed_byte_count (q80_mixed_decode.rs:83-92,149-183):
+ * codes of `bits` bits, LSB-first bitstream. */
+size_t hko_uniform_packed_bytes(size_t rows, size_t cols, int bits, size_t group) {
+    if (bits < 1 || bits > 8 || group == 0) return 0;
+    size_t elements = rows * cols, groups = (elements + group - 1) / group;
+    return (groups * group * (size_t)bits + 7) / 8;
+}
+
+static void put_unsigned(uint8_t* codes, size_t element, int bits, uint32_t value) {
+    size_t bit0 = element * (size_t)bits;
+    for (int b = 0; b < bits; ++b) {
+        size_t bi = bit0 + (size_t)b;
+        if ((value >> b) & 1u) codes[bi >> 3] |= (uint8_t)(1u << (bi & 7u));
+    }
+}
+
+/* extract_unsigned (q80_mixed_decode.rs:579-589). */
+static uint32_t get_unsigned(const uint8_t* codes, size_t element, int bits) {
+    size_t bit0 = element * (size_t)bits;
+    uint32_t value = 0;
+    for (int b = 0; b < bits; ++b) {
+        size_t bi = bit0 + (size_t)b;
+        value |= (uint32_t)((codes[bi >> 3] >> (bi & 7u)) & 1u) << b;
+    }
+    return value;
+}
+
+/* pack_uniform_factor (q80_mixed_decode.rs:529-577): groups over the flat
+ * elements, the last possibly partial (missing values pack as 0); bound =
+ * 2^(bits-1) - 1; scale = f16(max|w| / bound) (f32 divide); the quantizer
+ * divides by the f32 scale before rounding (1 when it is 0) and rounds half
+ * away from zero (Rust f32::round); code = q + bound. */
+int hko_uniform_pack(const float* w, size_t rows, size_t cols, int bits, size_t group, uint16_t* scales,
+                     uint8_t* codes) {
+    if (bits < 2 || bits > 8 || group == 0 || rows == 0 || cols == 0) return HKO_E_GEOMETRY;
+    size_t elements = rows * cols;
+    if (!all_finite(w, elements)) return HKO_E_NONFINITE;
+    size_t groups = (elements + group - 1) / group;
+    uint32_t bound = (1u << (bits - 1)) - 1u;
+    memset(codes, 0, hko_uniform_packed_bytes(rows, cols, bits, group));
+    for (size_t g = 0; g < groups; ++g) {
+        size_t start = g * group, end = start + group < elements ? start + group : elements;
+        float max_abs = 0.0f;
+        for (size_t e = start; e < end; ++e) max_abs = fmaxf(max_abs, fabsf(w[e]));
+        float scale = max_abs / (float)(bound ? bound : 1u);
+        scales[g] = hko_f32_to_f16(scale);
+        float denom = scale > 0.0f ? scale : 1.0f;
+        for (size_t i = 0; i < group; ++i) {
+            float value = start + i < elements ? w[start + i] : 0.0f;
+            float q = roundf(value / denom);
+            if (q < -(float)bound) q = -(float)bound;
+            if (q > (float)bound) q = (float)bound;
+            put_unsigned(codes, start + i, bits, (uint32_t)((int32_t)q + (int32_t)bound));
+        }
+    }
+    return HKO_OK;
+}
+
+/* uniform_factor_value (q80_mixed_decode.rs:591-598): (code - bound) * f32(scale). */
+static float uniform_value(const uint16_t* scales, const uint8_t* codes, size_t element, int bits, size_t group) {
+    int32_t bound = (int32_t)((1u << (bits - 1)) - 1u);
+    float scale = hko_f16_to_f32(scales[element / group]);
+    return (float)((int32_t)get_unsigned(codes, element, bits) - bound) * scale;
+}
+
+int hko_uniform_decode(const uint16_t* scales, const uint8_t* codes, size_t rows, size_t cols, int bits,
+                       size_t group, float* out) {
+    if (bits < 2 || bits > 8 || group == 0) return HKO_E_GEOMETRY;
+    for (size_t e = 0; e < rows * cols; ++e) out[e] = uniform_value(scales, codes, e, bits, group);
+    return HKO_OK;
+}
+
+/* uniform_factor_matvec_f32 (q80_mixed_decode.rs:600-612): per row, serial
+ * f32 sum += value * x over the columns; x must be finite. */
+int hko_uniform_matvec(const uint16_t* scales, const uint8_t* codes, size_t rows, size_t cols, int bits,
+                       size_t group, const float* x, float* y) {
+    if (bits < 2 || bits > 8 || group == 0) return HKO_E_GEOMETRY;
+    if (!all_finite(x, cols)) return HKO_E_NONFINITE;
+    for (size_t r = 0; r < rows; ++r) {
+        float sum = 0.0f;
+        for (size_t c = 0; c < cols; ++c) sum += uniform_value(scales, codes, r * cols + c, bits, group) * x[c];
+        y[r] = sum;
+    }
+    return HKO_OK;
+}
+
+int hko_uniform_matvec_f64(const uint16_t* scales, const uint8_t* codes, size_t rows, size_t cols, int bits,
+                           size_t group, const double* x, double* y) {
+    if (bits < 2 || bits > 8 || group == 0) return HKO_E_GEOMETRY;
+    for (size_t r = 0; r < rows; ++r) {
+        double sum = 0.0;
+        for (size_t c = 0; c < cols; ++c) sum += (double)uniform_value(scales, codes, r * cols + c, bits, group) * x[c];
+        y[r] = sum;
+    }
+    return HKO_OK;
+}
+
+/* hgravs01_two_stage_matvec_f32 (q80_mixed_decode.rs:614-629): mid = R x, y = L mid. */
+int hko_hgravs01_matvec(const uint16_t* ls, const uint8_t* lc, size_t rows, size_t rank, const uint16_t* rs,
+                        const uint8_t* rc, size_t cols, int bits, size_t group, const float* x, float* y) {
+    float* mid = (float*)malloc(rank * sizeof(float));
+    if (!mid) return HKO_E_INVALID_ARG;
+    int rc0 = hko_uniform_matvec(rs, rc, rank, cols, bits, group, x, mid);
+    if (rc0 == HKO_OK) rc0 = hko_uniform_matvec(ls, lc, rows, rank, bits, group, mid, y);
+    free(mid);
+    return rc0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* Mixed per-128-group binary | Q2                                           */
 /* ------------------------------------------------------------------------ */
 

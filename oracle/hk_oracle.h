@@ -88,6 +88,24 @@ int hko_bin_matvec_f64(const uint16_t* scales, const uint8_t* signs, size_t rows
 int hko_q2_pack(const float* w, size_t count, uint16_t* scales, uint8_t* codes);
 int hko_q2_decode(const uint16_t* scales, const uint8_t* codes, size_t count, float* out);
 
+/* ---- uniform factor codec: HGRAVU01 (q8, group 64) and the HGRAVS01 low-rank
+ * factors (3-bit, group 64); pack_uniform_factor / uniform_factor_value /
+ * uniform_factor_matvec_f32 / hgravs01_two_stage_matvec_f32
+ * (q80_mixed_decode.rs:529-629).  scales f16[groups] (flat groups, last one
+ * padded with zeros), codes = (groups*group) codes of `bits` bits, LSB-first. ---- */
+size_t hko_uniform_packed_bytes(size_t rows, size_t cols, int bits, size_t group);
+int hko_uniform_pack(const float* w, size_t rows, size_t cols, int bits, size_t group, uint16_t* scales,
+                     uint8_t* codes);
+int hko_uniform_decode(const uint16_t* scales, const uint8_t* codes, size_t rows, size_t cols, int bits,
+                       size_t group, float* out);
+int hko_uniform_matvec(const uint16_t* scales, const uint8_t* codes, size_t rows, size_t cols, int bits,
+                       size_t group, const float* x, float* y);
+int hko_uniform_matvec_f64(const uint16_t* scales, const uint8_t* codes, size_t rows, size_t cols, int bits,
+                           size_t group, const double* x, double* y);
+/* y = L (R x): L [rows x rank], R [rank x cols], both uniform factors of one bits/group. */
+int hko_hgravs01_matvec(const uint16_t* ls, const uint8_t* lc, size_t rows, size_t rank, const uint16_t* rs,
+                        const uint8_t* rc, size_t cols, int bits, size_t group, const float* x, float* y);
+
 /* ---- mixed <=1.5 BPW, per 128-group binary|Q2 (build-defined canonical stream):
  *   tags  u8[ceil(groups/8)]  LSB-first over flat group index, bit 1 = binary
  *   bin_scales f16[n_bin]     bin_signs u8[n_bin*16]      (binary groups in flat order)

@@ -61,6 +61,12 @@ def _declare(L: C.CDLL) -> None:
         "hko_bin_matvec_f64": (C.c_int, [_p, _p, _sz, _sz, C.c_int, _p, _p]),
         "hko_q2_pack": (C.c_int, [_p, _sz, _p, _p]),
         "hko_q2_decode": (C.c_int, [_p, _p, _sz, _p]),
+        "hko_uniform_packed_bytes": (_sz, [_sz, _sz, C.c_int, _sz]),
+        "hko_uniform_pack": (C.c_int, [_p, _sz, _sz, C.c_int, _sz, _p, _p]),
+        "hko_uniform_decode": (C.c_int, [_p, _p, _sz, _sz, C.c_int, _sz, _p]),
+        "hko_uniform_matvec": (C.c_int, [_p, _p, _sz, _sz, C.c_int, _sz, _p, _p]),
+        "hko_uniform_matvec_f64": (C.c_int, [_p, _p, _sz, _sz, C.c_int, _sz, _p, _p]),
+        "hko_hgravs01_matvec": (C.c_int, [_p, _p, _sz, _sz, _p, _p, _sz, C.c_int, _sz, _p, _p]),
         "hko_mixed_pack": (C.c_int, [_p, _sz, _sz, _p, _p]),
         "hko_mixed_free": (None, [_p]),
         "hko_mixed_decode": (C.c_int, [_p, _p]),
@@ -238,6 +244,52 @@ def q2_decode(scales, codes, count) -> np.ndarray:
     out = np.empty(count, np.float32)
     _check("hko_q2_decode", lib().hko_q2_decode(_ptr(scales), _ptr(codes), count, _ptr(out)))
     return out
+
+
+# ---- uniform factor codec (HGRAVU01 q8 G64, HGRAVS01 factors) -------------------
+
+def uniform_pack(w: np.ndarray, rows: int, cols: int, bits: int = 8, group: int = 64):
+    """pack_uniform_factor: (scales f16 bits [groups], packed codes)."""
+    w = np.ascontiguousarray(w, np.float32).reshape(-1)
+    assert w.size == rows * cols
+    groups = -(-rows * cols // group)
+    scales = np.zeros(groups, np.uint16)
+    codes = np.zeros(lib().hko_uniform_packed_bytes(rows, cols, bits, group), np.uint8)
+    _check("hko_uniform_pack", lib().hko_uniform_pack(_ptr(w), rows, cols, bits, group, _ptr(scales), _ptr(codes)))
+    return scales, codes
+
+
+def uniform_decode(scales, codes, rows, cols, bits=8, group=64) -> np.ndarray:
+    out = np.empty(rows * cols, np.float32)
+    _check("hko_uniform_decode",
+           lib().hko_uniform_decode(_ptr(scales), _ptr(codes), rows, cols, bits, group, _ptr(out)))
+    return out.reshape(rows, cols)
+
+
+def uniform_matvec(scales, codes, rows, cols, x, bits=8, group=64) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(rows, np.float32)
+    _check("hko_uniform_matvec",
+           lib().hko_uniform_matvec(_ptr(scales), _ptr(codes), rows, cols, bits, group, _ptr(x), _ptr(y)))
+    return y
+
+
+def uniform_matvec_f64(scales, codes, rows, cols, x, bits=8, group=64) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float64)
+    y = np.empty(rows, np.float64)
+    _check("hko_uniform_matvec_f64",
+           lib().hko_uniform_matvec_f64(_ptr(scales), _ptr(codes), rows, cols, bits, group, _ptr(x), _ptr(y)))
+    return y
+
+
+def hgravs01_matvec(left, right, rows, rank, cols, x, bits=3, group=64) -> np.ndarray:
+    """hgravs01_two_stage_matvec_f32: y = L (R x); left/right = (scales, codes)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(rows, np.float32)
+    _check("hko_hgravs01_matvec",
+           lib().hko_hgravs01_matvec(_ptr(left[0]), _ptr(left[1]), rows, rank, _ptr(right[0]), _ptr(right[1]),
+                                     cols, bits, group, _ptr(x), _ptr(y)))
+    return y
 
 
 class _Mixed(C.Structure):
