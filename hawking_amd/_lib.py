@@ -20,7 +20,7 @@ HK_E_UNSUPPORTED = 5
 HK_E_ROUTE = 6
 HK_E_NOMEM = 7
 
-HK_Q4, HK_BIN, HK_MIXED, HK_F32 = 0, 1, 2, 3
+HK_Q4, HK_BIN, HK_MIXED, HK_F32, HK_Q8 = 0, 1, 2, 3, 4
 HK_ROUTER_SOFTMAX, HK_ROUTER_NOAUX_TC = 0, 1
 
 STATUS_NAMES = {
@@ -96,6 +96,7 @@ PROTOTYPES = {
     "hk_pack_q4": (C.c_int, [_p, _p, _u32, _u32, _i32, _p, _p, _p]),
     "hk_pack_bin": (C.c_int, [_p, _p, _u32, _u32, _p, _p, _p]),
     "hk_pack_q2": (C.c_int, [_p, _p, _sz, _p, _p, _p]),
+    "hk_pack_q8": (C.c_int, [_p, _p, _u32, _u32, _p, _p, _p]),
     "hk_stream_key": (_u64, [_u64, _u64]),
     "hk_synth_normal": (C.c_int, [_p, _u64, _u64, _sz, C.c_float, _p, _p]),
     "hk_router_softmax_topk": (C.c_int, [_p, _p, _u32, _u32, _u32, C.c_float, C.c_int, _p, _p, _p]),

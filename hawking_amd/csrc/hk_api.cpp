@@ -96,6 +96,10 @@ static int validate_shape(hk_ctx* ctx, int kind, int group, uint32_t rows, uint3
     case HK_MIXED:
         if (cols % 128) return set_error(ctx, HK_E_GEOMETRY, "mixed organs require cols % 128 == 0");
         return HK_OK;
+    case HK_Q8:
+        if (group != 64) return set_error(ctx, HK_E_UNSUPPORTED, "uniform q8 organs use group_size 64 (HGRAVU01)");
+        if (cols % 64) return set_error(ctx, HK_E_GEOMETRY, "uniform q8 organs require cols % 64 == 0");
+        return HK_OK;
     case HK_F32:
         if (cols % 4) return set_error(ctx, HK_E_GEOMETRY, "dense organs require cols % 4 == 0");
         return HK_OK;
@@ -123,6 +127,10 @@ static Layout layout_for(int kind, int group, uint32_t rows, uint32_t cols, uint
     case HK_BIN:
         L.scales = n / 128 * 2;
         L.codes = n / 8;
+        break;
+    case HK_Q8:
+        L.scales = n / 64 * 2;
+        L.codes = n;
         break;
     case HK_MIXED: {
         const size_t groups = n / 128;
@@ -175,9 +183,9 @@ static int validate_src(hk_ctx* ctx, const hk_organ_src* s, Layout* out) {
     if (!rc) rc = validate_gemv_cols(ctx, s->kind, s->cols);
     if (rc) return rc;
     const size_t n = (size_t)s->rows * s->cols;
-    if (s->kind == HK_Q4 || s->kind == HK_BIN) {
+    if (s->kind == HK_Q4 || s->kind == HK_BIN || s->kind == HK_Q8) {
         if (!s->scales || !s->codes) return set_error(ctx, HK_E_INVALID_ARG, "organ scales/codes are NULL");
-        const size_t groups = n / (size_t)(s->kind == HK_Q4 ? s->group : 128);
+        const size_t groups = n / (size_t)(s->kind == HK_Q4 ? s->group : s->kind == HK_Q8 ? 64 : 128);
         for (size_t g = 0; g < groups; ++g)
             if (!f16_finite(s->scales[g]))
                 return set_error(ctx, HK_E_NONFINITE, "group " + std::to_string(g) + " scale is not a finite FP16");
@@ -214,7 +222,7 @@ static int copy_src(hk_ctx* ctx, const hk_organ_src* s, const Layout& L, uint8_t
                          "hipMemcpyAsync (organ upload)");
     };
     int rc = HK_OK;
-    if (s->kind == HK_Q4 || s->kind == HK_BIN) {
+    if (s->kind == HK_Q4 || s->kind == HK_BIN || s->kind == HK_Q8) {
         if ((rc = cp(v.scales, s->scales, L.scales))) return rc;
         if ((rc = cp(v.codes, s->codes, L.codes))) return rc;
     } else if (s->kind == HK_MIXED) {
@@ -582,6 +590,7 @@ extern "C" int hk_organ_synthetic(hk_ctx* ctx, int32_t kind, int32_t group, uint
     if (!ctx || !out) return HK_E_INVALID_ARG;
     *out = nullptr;
     if (kind == HK_BIN || kind == HK_MIXED) group = 128;
+    if (kind == HK_Q8) group = 64;
     int rc = validate_shape(ctx, kind, group, rows, cols);
     if (!rc) rc = validate_gemv_cols(ctx, kind, cols);
     if (rc) return rc;
@@ -693,6 +702,19 @@ extern "C" int hk_pack_bin(hk_ctx* ctx, const float* w, uint32_t rows, uint32_t 
     uint32_t* bad;
     if ((rc = pack_prologue(ctx, st, &bad))) return rc;
     return finish_pack(ctx, st, bad, launch_pack_bin(w, (size_t)rows * cols / 128, scales, signs, bad, st));
+}
+
+extern "C" int hk_pack_q8(hk_ctx* ctx, const float* w, uint32_t rows, uint32_t cols, uint16_t* scales,
+                          uint8_t* codes, hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    int rc = validate_shape(ctx, HK_Q8, 64, rows, cols);
+    if (rc) return rc;
+    if (!w || !scales || !codes || !aligned16(codes))
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_pack_q8: NULL or misaligned pointer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    uint32_t* bad;
+    if ((rc = pack_prologue(ctx, st, &bad))) return rc;
+    return finish_pack(ctx, st, bad, launch_pack_q8(w, (size_t)rows * cols / 64, scales, codes, bad, st));
 }
 
 extern "C" int hk_pack_q2(hk_ctx* ctx, const float* w, size_t count, uint16_t* scales, uint8_t* codes,

@@ -185,6 +185,7 @@ size_t gemv_lds_bytes(int kind, uint32_t cols) {
     const uint32_t S = n_steps_for(kind, cols);
     if (kind == HK_Q4) return gemv_hdr_offset<HK_Q4>(S);
     if (kind == HK_BIN) return gemv_hdr_offset<HK_BIN>(S);
+    if (kind == HK_Q8) return gemv_hdr_offset<HK_Q8>(S);
     if (S > GEMV_MAX_MIXED_STEPS) return SIZE_MAX;
     return gemv_hdr_offset<HK_MIXED>(S) + (size_t)GEMV_MAX_TILES_PER_WG * S * sizeof(uint4);
 }
@@ -219,7 +220,7 @@ static hipError_t launch_r(const OrganView* organs, uint32_t n, const OrganView&
         if constexpr (KIND == HK_BIN) {
             if (sh.steps >= 4) return launch_kind<KIND, 4, 3>(organs, n, sh, x, xs, y, ys, 16, s);
             return launch_kind<KIND, 2, 3>(organs, n, sh, x, xs, y, ys, 32, s);
-        } else if constexpr (KIND == HK_Q4) {
+        } else if constexpr (KIND == HK_Q4 || KIND == HK_Q8) {
             return launch_kind<KIND, 2, 3>(organs, n, sh, x, xs, y, ys, 16, s);
         } else {
             return launch_kind<KIND, 1, 3>(organs, n, sh, x, xs, y, ys, 16, s);
@@ -240,6 +241,7 @@ hipError_t launch_gemv_tiled(const OrganView* organs_dev, uint32_t n, const Orga
     case HK_BIN: return launch_r<HK_BIN>(organs_dev, n, sh, x, x_stride, y, y_stride, s);
     case HK_Q4: return launch_r<HK_Q4>(organs_dev, n, sh, x, x_stride, y, y_stride, s);
     case HK_MIXED: return launch_r<HK_MIXED>(organs_dev, n, sh, x, x_stride, y, y_stride, s);
+    case HK_Q8: return launch_r<HK_Q8>(organs_dev, n, sh, x, x_stride, y, y_stride, s);
     default: return hipErrorInvalidValue;
     }
 }

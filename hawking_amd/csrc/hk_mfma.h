@@ -60,6 +60,10 @@ template <>
 struct Kcfg<HK_MIXED> {
     static constexpr int P = 8, STEP_COLS = 512, DATA = 32, SXG = 64;
 };
+template <>
+struct Kcfg<HK_Q8> {
+    static constexpr int P = 1, STEP_COLS = 64, DATA = 16, SXG = 16;
+};
 
 constexpr int A_TILE_STRIDE = 272;  // 256 B of active-lane limbs + 16 B of zeros
 
@@ -95,6 +99,8 @@ __device__ __forceinline__ int32_t a_value(const float* xq, int t, int mu, int q
         return X(c0 + (uint32_t)mu) * (1 << (7 - mu)) + v7;
     } else if constexpr (KIND == HK_Q4) {
         return X((uint32_t)(t * 128 + q * 32 + 2 * i + mu));
+    } else if constexpr (KIND == HK_Q8) {
+        return X((uint32_t)(t * 64 + q * 16 + i));
     } else {
         const int h = mu >> 2, u = mu & 3, r = i >> 2, j = i & 3;
         const int a = r < 2 ? 2 * h + r : 2 * h + 2 + r;
@@ -304,6 +310,11 @@ struct Frag<HK_Q4, R> {
     uint16_t s[R];
 };
 template <int R>
+struct Frag<HK_Q8, R> {
+    uint4 v[R];
+    uint16_t s[R];
+};
+template <int R>
 struct Frag<HK_MIXED, R> {
     uint32_t V[R][8];
     uint16_t s0[R], s1[R];
@@ -340,6 +351,9 @@ __device__ __forceinline__ void fetch_one(const OrganView& o, uint32_t T, uint32
     if constexpr (KIND == HK_BIN || KIND == HK_Q4) {
         f.v[r] = ldg(reinterpret_cast<const uint4*>(o.data + ((size_t)T * o.steps + t) * 1024u + 16u * lane));
         f.s[r] = ldg(o.scales + ((size_t)T * o.steps + t) * 64u + lane);
+    } else if constexpr (KIND == HK_Q8) {
+        f.v[r] = ldg(reinterpret_cast<const uint4*>(o.data + ((size_t)T * o.steps + t) * 1024u + 16u * lane));
+        f.s[r] = ldg(o.scales + ((size_t)T * o.steps + t) * 16u + (lane & 15));
     } else {
         fetch_mixed<R>(o, ldg(o.hdr + (size_t)T * o.steps + t), lane, f, r);
     }
@@ -391,6 +405,19 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
         const float sx = SX[4 * t + q];
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] += f16_bits_to_f32(f.s[r]) * (combine_limbs(c[r]) - 8.0f * sx);
+    } else if constexpr (KIND == HK_Q8) {
+        // code - 127 = (code ^ 0x80 as a signed byte) + 1: the B bytes are the
+        // codes with the top bit flipped and the +1 is the slot's sum of X
+        const v4i a = A(t);
+        const uint32_t m = 0x80808080u;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const v4i b = {(int)(f.v[r].x ^ m), (int)(f.v[r].y ^ m), (int)(f.v[r].z ^ m), (int)(f.v[r].w ^ m)};
+            c[r] = mfma_i8(a, b, v4i{0, 0, 0, 0});
+        }
+        const float sx = SX[4 * t + q];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] += f16_bits_to_f32(f.s[r]) * (combine_limbs(c[r]) + sx);
     } else {
         uint32_t V[R][8];
 #pragma unroll

@@ -86,6 +86,33 @@ __device__ void q2_pack_group(const Src& src, uint16_t* scale_out, uint8_t* code
     *reinterpret_cast<uint4*>(codes_out) = make_uint4(words[0], words[1], words[2], words[3]);
 }
 
+// pack_uniform_factor at 8 bits (q80_mixed_decode.rs:529-577), one group of
+// 64: scale = f16(max|w| / 127); the quantizer divides by the f32 scale (1 if
+// it is 0) and rounds half away from zero (Rust f32::round); code = q + 127.
+template <typename Src>
+__device__ void q8_pack_group(const Src& src, uint16_t* scale_out, uint8_t* codes_out, uint32_t* bad) {
+    float max_abs = 0.0f;
+    for (int i = 0; i < 64; ++i) {
+        const float v = src(i);
+        if (!isfinite(v)) *bad = 1u;
+        max_abs = fmaxf(max_abs, fabsf(v));
+    }
+    const float scale = __fdiv_rn(max_abs, 127.0f);
+    const uint16_t sb = f32_to_f16_bits(scale);
+    if ((sb & 0x7C00u) == 0x7C00u) *bad = 1u;
+    *scale_out = sb;
+    const float denom = scale > 0.0f ? scale : 1.0f;
+    for (int i = 0; i < 64; i += 16) {
+        uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const float r = fminf(fmaxf(roundf(__fdiv_rn(src(i + k), denom)), -127.0f), 127.0f);
+            w[k >> 2] |= (uint32_t)((int)r + 127) << (8 * (k & 3));
+        }
+        reinterpret_cast<uint4*>(codes_out)[i >> 4] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
 struct BufSrc {
     const float* p;
     __device__ float operator()(int i) const { return p[i]; }
@@ -133,6 +160,16 @@ __global__ void pack_q2_kernel(const float* __restrict__ w, size_t groups,
     }
 }
 
+__global__ void pack_q8_kernel(const float* __restrict__ w, size_t groups, uint16_t* __restrict__ scales,
+                               uint8_t* __restrict__ codes, uint32_t* bad) {
+    for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < groups;
+         g += (size_t)gridDim.x * blockDim.x) {
+        uint32_t b = 0;
+        q8_pack_group(BufSrc{w + g * 64}, scales + g, codes + g * 64, &b);
+        if (b) atomicOr(bad, 1u);
+    }
+}
+
 __global__ void synth_normal_kernel(uint64_t key, uint64_t first, size_t count, float sigma,
                                     float* __restrict__ out) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
@@ -157,6 +194,12 @@ hipError_t launch_pack_bin(const float* w, size_t groups, uint16_t* scales, uint
                            uint32_t* bad, hipStream_t s) {
     hipLaunchKernelGGL(pack_bin_kernel, dim3(grid_for(groups, 256)), dim3(256), 0, s, w, groups,
                        scales, signs, bad);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack_q8(const float* w, size_t groups, uint16_t* scales, uint8_t* codes, uint32_t* bad,
+                          hipStream_t s) {
+    hipLaunchKernelGGL(pack_q8_kernel, dim3(grid_for(groups, 256)), dim3(256), 0, s, w, groups, scales, codes, bad);
     return hipGetLastError();
 }
 
@@ -200,6 +243,17 @@ __global__ void synth_pack_bin_kernel(const SynthJob* __restrict__ jobs, uint32_
          g += (size_t)gridDim.x * blockDim.x) {
         uint32_t b = 0;
         bin_pack_group(SynthSrc{j.key, g * 128, j.sigma}, j.scales + g, j.codes + g * 16, &b);
+        if (b) atomicOr(bad, 1u);
+    }
+}
+
+__global__ void synth_pack_q8_kernel(const SynthJob* __restrict__ jobs, uint32_t* bad) {
+    const SynthJob j = jobs[blockIdx.y];
+    const size_t groups = (size_t)j.rows * j.cols / 64;
+    for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < groups;
+         g += (size_t)gridDim.x * blockDim.x) {
+        uint32_t b = 0;
+        q8_pack_group(SynthSrc{j.key, g * 64, j.sigma}, j.scales + g, j.codes + g * 64, &b);
         if (b) atomicOr(bad, 1u);
     }
 }
@@ -315,6 +369,9 @@ hipError_t launch_synth_jobs(int kind, const SynthJob* jobs_dev, uint32_t njobs,
         break;
     case HK_BIN:
         hipLaunchKernelGGL(synth_pack_bin_kernel, dim3(bx ? bx : 1, njobs), dim3(256), 0, s, jobs_dev, bad);
+        break;
+    case HK_Q8:
+        hipLaunchKernelGGL(synth_pack_q8_kernel, dim3(bx ? bx : 1, njobs), dim3(256), 0, s, jobs_dev, bad);
         break;
     case HK_MIXED: {
         const size_t words = (max_groups + 31) / 32;

@@ -24,6 +24,11 @@ size_t tiled_bytes(int kind, int group, uint32_t rows, uint32_t cols, uint32_t n
         scales = nt * 64 * S * 2 + 16;
         packed = n / 2 + n / (size_t)group * 2;
         break;
+    case HK_Q8:
+        data = nt * S * 1024;
+        scales = nt * 16 * S * 2 + 16;
+        packed = n + n / 64 * 2;
+        break;
     case HK_MIXED: {
         const size_t items = nt * S * 64, pad = items - (size_t)n_bin - n_q2;
         data = ((size_t)n_bin + pad) * 16 + (size_t)n_q2 * 32;
@@ -54,6 +59,9 @@ OrganView tiled_place(int kind, int group, uint32_t rows, uint32_t cols, uint32_
     if (kind == HK_BIN || kind == HK_Q4) {
         data = nt * S * 1024;
         scales = nt * 64 * S * 2 + 16;
+    } else if (kind == HK_Q8) {
+        data = nt * S * 1024;
+        scales = nt * 16 * S * 2 + 16;
     } else if (kind == HK_MIXED) {
         const size_t items = nt * S * 64, pad = items - (size_t)n_bin - n_q2;
         data = ((size_t)n_bin + pad) * 16 + (size_t)n_q2 * 32;
@@ -90,6 +98,17 @@ __device__ void repack_fixed_body(const CanonView& src, const OrganView& dst) {
                 v = *reinterpret_cast<const uint4*>(src.codes + (size_t)r * (src.cols / 8u) + 16u * g);
                 s = src.scales[(size_t)r * (src.cols / 128u) + g];
             }
+        } else if (src.kind == HK_Q8) {
+            // padding (rows past the end) holds code 127 = 0 with scale 0
+            v = make_uint4(0x7F7F7F7Fu, 0x7F7F7F7Fu, 0x7F7F7F7Fu, 0x7F7F7F7Fu);
+            if (r < src.rows && t < src.cols / 64u) {
+                const size_t e = (size_t)r * src.cols + 64u * t + 16u * q;
+                v = *reinterpret_cast<const uint4*>(src.codes + e);
+                s = src.scales[e / 64u];
+            }
+            *reinterpret_cast<uint4*>(const_cast<uint8_t*>(dst.data) + (size_t)ts * 1024u + 16u * l) = v;
+            if (q == 0) const_cast<uint16_t*>(dst.scales)[(size_t)ts * 16u + n] = s;
+            continue;
         } else {
             const uint32_t c = 4u * t + q;
             if (r < src.rows && c < src.cols / 32u) {
@@ -222,7 +241,7 @@ __global__ void repack_mixed_items_batch_kernel(const RepackJob* __restrict__ jo
 
 hipError_t launch_repack(const CanonView& src, const OrganView& dst, void* scratch, hipStream_t s) {
     const size_t items = (size_t)dst.n_tiles * dst.steps * 64;
-    if (src.kind == HK_BIN || src.kind == HK_Q4) {
+    if (src.kind == HK_BIN || src.kind == HK_Q4 || src.kind == HK_Q8) {
         hipLaunchKernelGGL(repack_fixed_kernel, dim3(grid1(items)), dim3(256), 0, s, src, dst);
     } else if (src.kind == HK_MIXED) {
         uint32_t* counts = static_cast<uint32_t*>(scratch);
@@ -239,7 +258,7 @@ hipError_t launch_repack_batch(int kind, const RepackJob* jobs_dev, uint32_t n, 
     if (n == 0) return hipSuccess;
     if (n > 65535) return hipErrorInvalidValue;
     const unsigned gx = std::min(grid1(max_items), 1024u);
-    if (kind == HK_BIN || kind == HK_Q4) {
+    if (kind == HK_BIN || kind == HK_Q4 || kind == HK_Q8) {
         hipLaunchKernelGGL(repack_fixed_batch_kernel, dim3(gx, n), dim3(256), 0, s, jobs_dev);
     } else if (kind == HK_MIXED) {
         hipLaunchKernelGGL(repack_mixed_mask_batch_kernel, dim3(std::min(grid1(max_items / 64), 1024u), n), dim3(256),

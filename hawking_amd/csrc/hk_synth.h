@@ -71,6 +71,8 @@ hipError_t launch_pack_q4(const float* w, size_t groups, int G, uint16_t* scales
                           uint32_t* bad, hipStream_t s);
 hipError_t launch_pack_bin(const float* w, size_t groups, uint16_t* scales, uint8_t* signs,
                            uint32_t* bad, hipStream_t s);
+hipError_t launch_pack_q8(const float* w, size_t groups, uint16_t* scales, uint8_t* codes, uint32_t* bad,
+                          hipStream_t s);
 hipError_t launch_pack_q2(const float* w, size_t groups, uint16_t* scales, uint8_t* codes,
                           uint32_t* bad, hipStream_t s);
 hipError_t launch_synth_normal(uint64_t key, uint64_t first, size_t count, float sigma, float* out,

@@ -24,6 +24,10 @@
 //         kinds): dword a (0..3) byte j holds, in 2-bit fields u = 0..3, the
 //         codes of columns 32a + 8j + 2u; dword 4+a byte j holds columns
 //         32a + 8j + 2u + 1.
+//   Q8    step = 64 columns (one group); lane (n,q) holds the 16 code bytes
+//         of row n, columns 16q..16q+15 of the step (value (code-127)*scale).
+//         scales: [tile][step][row] f16 (32 bytes per step: the four lanes of
+//         a row read one scale, no duplication).
 #pragma once
 
 #include "hk_internal.h"
@@ -32,7 +36,9 @@ namespace hk {
 
 constexpr uint32_t TILE_ROWS = 16;
 
-__host__ __device__ inline uint32_t tile_step_cols(int kind) { return kind == HK_Q4 ? 128u : 512u; }
+__host__ __device__ inline uint32_t tile_step_cols(int kind) {
+    return kind == HK_Q4 ? 128u : kind == HK_Q8 ? 64u : 512u;
+}
 __host__ __device__ inline uint32_t n_tiles_for(uint32_t rows) { return (rows + TILE_ROWS - 1) / TILE_ROWS; }
 __host__ __device__ inline uint32_t n_steps_for(int kind, uint32_t cols) {
     const uint32_t sc = tile_step_cols(kind);
@@ -55,6 +61,12 @@ __device__ inline float tiled_weight(const OrganView& o, uint32_t r, uint32_t c)
         const int nib = (w & 1u) ? (b >> 4) : (b & 0xF);
         const float s = f16_bits_to_f32(o.scales[((size_t)T * o.steps + t) * 64u + l]);
         return (float)(nib - 8) * s;
+    }
+    if (o.kind == HK_Q8) {
+        const uint32_t t = c >> 6, q = (c >> 4) & 3u, l = n + 16u * q;
+        const uint8_t b = o.data[((size_t)T * o.steps + t) * 1024u + 16u * l + (c & 15u)];
+        const float s = f16_bits_to_f32(o.scales[((size_t)T * o.steps + t) * 16u + n]);
+        return (float)((int)b - 127) * s;
     }
     const uint32_t g = c >> 7, t = g >> 2, q = g & 3u, l = n + 16u * q, i = c & 127u;
     if (o.kind == HK_BIN) {

@@ -6,6 +6,8 @@ Reference names are kept where the reference has them:
   * BinaryGroupPacked + binary_group_matvec_f32
     (crates/hawking-core/src/model/qwen_complete_binary/q80_mixed_decode.rs:48-257)
   * MixedPackedTensor (q80_mixed_decode.rs:1073-1417)
+  * UniformFactorPacked + uniform_factor_matvec_f32 at 8 bits, group 64
+    (HGRAVU01, q80_mixed_decode.rs:529-612,1047-1070)
 Every matvec runs the gfx950 kernels through the C ABI; the inputs are the
 reference's canonical packed bytes, uploaded and repacked once.
 """
@@ -16,7 +18,7 @@ import ctypes as C
 import numpy as np
 
 from . import _lib
-from ._lib import HK_BIN, HK_F32, HK_MIXED, HK_Q4, OrganSrc
+from ._lib import HK_BIN, HK_F32, HK_MIXED, HK_Q4, HK_Q8, OrganSrc
 from .runtime import Context, DeviceArray
 
 
@@ -112,6 +114,26 @@ class BinaryGroupPacked(PackedOrgan):
 
 def binary_group_matvec_f32(packed: BinaryGroupPacked, x: np.ndarray) -> np.ndarray:
     """GPU counterpart of binary_group_matvec_f32 (q80_mixed_decode.rs:245-257)."""
+    return packed.matvec(x)
+
+
+class UniformFactorPacked(PackedOrgan):
+    """Uniform 8-bit, group 64 (HGRAVU01 body): scales f16[rows*cols/64] and
+    codes u8[rows*cols] (code = q + 127)."""
+
+    kind = HK_Q8
+
+    def __init__(self, ctx: Context, scales: np.ndarray, codes: np.ndarray, rows: int, cols: int):
+        scales = np.ascontiguousarray(scales, np.uint16)
+        codes = np.ascontiguousarray(codes, np.uint8)
+        if scales.size != rows * cols // 64 or codes.size != rows * cols:
+            raise ValueError("q8 scales/codes sizes disagree with the shape")
+        src = OrganSrc(kind=HK_Q8, group=64, rows=rows, cols=cols, scales=_ptr(scales), codes=_ptr(codes))
+        super().__init__(ctx, src, (scales, codes))
+
+
+def uniform_factor_matvec_f32(packed: UniformFactorPacked, x: np.ndarray) -> np.ndarray:
+    """GPU counterpart of uniform_factor_matvec_f32 (q80_mixed_decode.rs:600-612)."""
     return packed.matvec(x)
 
 
@@ -214,6 +236,13 @@ def pack_binary_group_device(ctx: Context, w: DeviceArray, rows: int, cols: int)
     signs = ctx.empty(rows * cols // 8, np.uint8)
     ctx.call("hk_pack_bin", w.ptr, rows, cols, scales.ptr, signs.ptr, ctx.stream)
     return scales, signs
+
+
+def pack_q8_device(ctx: Context, w: DeviceArray, rows: int, cols: int):
+    scales = ctx.empty(rows * cols // 64, np.uint16)
+    codes = ctx.empty(rows * cols, np.uint8)
+    ctx.call("hk_pack_q8", w.ptr, rows, cols, scales.ptr, codes.ptr, ctx.stream)
+    return scales, codes
 
 
 def pack_q2_device(ctx: Context, w: DeviceArray, count: int):

@@ -48,6 +48,7 @@ extern "C" {
 #define HK_BIN 1   /* binary sign plane, group 128, f16 mean|w| per group */
 #define HK_MIXED 2 /* per-128-group binary | Q2 (two f16 scales per 64) */
 #define HK_F32 3   /* dense row-major f32 (router, shared-expert gate) */
+#define HK_Q8 4    /* uniform 8-bit, group 64, f16 scale per group (HGRAVU01) */
 
 typedef struct hk_ctx hk_ctx;
 typedef struct hk_organ hk_organ;
@@ -99,6 +100,9 @@ int hk_check_device_status(hk_ctx* ctx, hk_stream stream, uint32_t* bits);
  *  HK_MIXED: tags u8[ceil(groups/8)], bin_scales f16[n_bin], bin_signs u8[16*n_bin],
  *            q2_scales f16[2*n_q2], q2_codes u8[32*n_q2] (build-defined stream)
  *  HK_F32:   dense f32[rows*cols]
+ *  HK_Q8:    scales f16[rows*cols/64] || codes u8[rows*cols], code = q + 127
+ *            (HGRAVU01 body, pack_uniform_factor at 8 bits,
+ *            model/qwen_complete_binary/q80_mixed_decode.rs:529-577,786-826)
  * Requires cols % group == 0 (row-aligned groups). */
 typedef struct hk_organ_src {
     int32_t kind;
@@ -164,6 +168,10 @@ int hk_pack_q4(hk_ctx* ctx, const float* w, uint32_t rows, uint32_t cols, int32_
 /* pack_binary_group (q80_mixed_decode.rs:185-230), group 128. */
 int hk_pack_bin(hk_ctx* ctx, const float* w, uint32_t rows, uint32_t cols, uint16_t* scales,
                 uint8_t* signs, hk_stream stream);
+/* pack_uniform_factor at 8 bits, group 64 (q80_mixed_decode.rs:529-577);
+ * cols % 64 == 0.  An f16 scale that overflows is reported as HK_E_NONFINITE. */
+int hk_pack_q8(hk_ctx* ctx, const float* w, uint32_t rows, uint32_t cols, uint16_t* scales, uint8_t* codes,
+               hk_stream stream);
 /* Q2 base stage of _additive_residual_codec
  * (lab/operators/ascension_dual_gravity_worker.py:898-911), group 64. */
 int hk_pack_q2(hk_ctx* ctx, const float* w, size_t count, uint16_t* scales, uint8_t* codes,

@@ -20,7 +20,7 @@ from tests import hk_testutil as U
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-5
-HK_Q4, HK_BIN, HK_MIXED = U.HK_Q4, U.HK_BIN, U.HK_MIXED
+HK_Q4, HK_BIN, HK_MIXED, HK_Q8 = U.HK_Q4, U.HK_BIN, U.HK_MIXED, 4
 
 
 def say(*a):
@@ -47,6 +47,9 @@ def _oracle_matvec(oracle, kind, group, rows, cols, key, coin_key, x):
     if kind == HK_Q4:
         s, c = oracle.q4_pack(w, group)
         return oracle.q4_matvec(s, c, rows, cols, group, x)
+    if kind == HK_Q8:
+        s, c = oracle.uniform_pack(w, rows, cols, 8, 64)
+        return oracle.uniform_matvec(s, c, rows, cols, x, 8, 64)
     m = oracle.mixed_pack(w, oracle.mixed_coins(coin_key, rows * cols // 128))
     return oracle.mixed_matvec(m, x)
 
@@ -65,6 +68,10 @@ CASES = [
     ("bin 5 rounds (re-read)", HK_BIN, 128, 40, 10240, 2),
     ("mixed 4 rounds", HK_MIXED, 128, 33, 7168, 2),
     ("q4 5 rounds (re-read)", HK_Q4, 128, 24, 9216, 2),
+    ("q8 streamed", HK_Q8, 64, 512, 2048, 512),
+    ("q8 mid ragged", HK_Q8, 64, 300, 1024, 240),
+    ("q8 small", HK_Q8, 64, 40, 704, 3),
+    ("q8 5 rounds (re-read)", HK_Q8, 64, 24, 9216, 2),
 ]
 
 

@@ -82,6 +82,19 @@ def test_device_q2_packer_bit_exact(ctx, oracle):
     assert np.array_equal(s.download(), rs) and np.array_equal(c.download(), rc)
 
 
+def test_device_q8_packer_bit_exact(ctx, oracle):
+    from hawking_amd import organs
+    rng = np.random.default_rng(8)
+    w = _edge_weights(rng, 64, 512)
+    d = 1.0 + 2.0 ** -11
+    w[3, :4] = [127 * d, 62.5 * d, 62.5, -62.5 * d]     # half-away rounding, f32 divisor
+    w[3, 4:64] = 0.0
+    say("pack_q8", w.shape)
+    s, c = organs.pack_q8_device(ctx, ctx.to_device(w), 64, 512)
+    rs, rc = oracle.uniform_pack(w, 64, 512, 8, 64)
+    assert np.array_equal(s.download(), rs) and np.array_equal(c.download(), rc)
+
+
 def test_device_packer_rejects_nonfinite(ctx):
     from hawking_amd import organs
     from hawking_amd._lib import HK_E_NONFINITE, HawkingError
@@ -154,6 +167,37 @@ def test_mixed_organ(ctx, oracle, shape):
     y = organ.matvec(x)
     assert oracle.relative_l2(y, oracle.mixed_matvec(m, x)) < TOL
     assert oracle.relative_l2(y, oracle.mixed_matvec_f64(m, x)) < TOL
+
+
+def _q8(ctx, oracle, w):
+    from hawking_amd.organs import UniformFactorPacked
+    s, c = oracle.uniform_pack(w, w.shape[0], w.shape[1], 8, 64)
+    return UniformFactorPacked(ctx, s, c, w.shape[0], w.shape[1]), (s, c)
+
+
+@pytest.mark.parametrize("shape", [(512, 2048), (2048, 512), (13, 384), (1, 7168)])
+def test_uniform_q8_organ(ctx, oracle, shape):
+    """HGRAVU01 (q8, group 64): decode bit-exact, matvec vs the serial f32
+    oracle and the FP64 authority."""
+    rows, cols = shape
+    w = oracle.normal(oracle.stream_key(U.SEED, 0xC8 + rows), rows * cols, 0.02).reshape(rows, cols)
+    x = oracle.normal(oracle.stream_key(U.SEED, 0xC8 + rows + 1), cols, 1.0)
+    say("uniform q8 organ", shape)
+    organ, (s, c) = _q8(ctx, oracle, w)
+    assert organ.packed_bytes == rows * cols + rows * cols // 64 * 2
+    assert np.array_equal(organ.decode(), oracle.uniform_decode(s, c, rows, cols, 8, 64))
+    y = organ.matvec(x)
+    assert oracle.relative_l2(y, oracle.uniform_matvec(s, c, rows, cols, x, 8, 64)) < TOL
+    assert oracle.relative_l2(y, oracle.uniform_matvec_f64(s, c, rows, cols, x, 8, 64)) < TOL
+
+
+def test_uniform_q8_rejects_bad_geometry(ctx, oracle):
+    from hawking_amd._lib import HK_E_GEOMETRY, HawkingError
+    from hawking_amd.organs import UniformFactorPacked
+    s, c = oracle.uniform_pack(np.ones((2, 96), np.float32), 2, 96, 8, 64)
+    with pytest.raises(HawkingError) as e:
+        UniformFactorPacked(ctx, s, c[:192], 2, 96)
+    assert e.value.code == HK_E_GEOMETRY
 
 
 @pytest.mark.parametrize("group,shape", [(64, (96, 1024)), (128, (7, 256)), (32, (1, 7168))])
