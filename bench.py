@@ -32,7 +32,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
 SEED = 0x48415752
-HK_Q4, HK_BIN, HK_MIXED, HK_F32, HK_Q8 = 0, 1, 2, 3, 4
+HK_Q4, HK_BIN, HK_MIXED, HK_F32, HK_Q8, HK_U3 = 0, 1, 2, 3, 4, 5
 WORKLOADS = {
     # name: (kind, group, rows, cols, n_organs)
     "binary_512x2048": (HK_BIN, 128, 512, 2048, 8192),
@@ -95,6 +95,35 @@ def streamed(ctx, name, steps, warmup, n_organs=None):
     ms = time_launches(ctx, lambda: oset.gemv(x, cols, y, rows), steps, warmup)
     return {"ms": ms, "bytes": nbytes, "gbps": nbytes / (ms * 1e-3) / 1e9, "organs": len(oset.organs),
             "packed_bytes_per_organ": oset.packed_bytes / len(oset.organs)}, (oset, x, y)
+
+
+def lowrank_streamed(ctx, steps, warmup, rows=2048, rank=160, cols=768, n=4096):
+    """HGRAVS01 r160 (3-bit factors) as the routed down_proj shape: n low-rank
+    organs, mid_i = R_i x_i for all i in one launch, then y_i = L_i mid_i in a
+    second.  Algorithmic bytes: the canonical packed factors plus x, mid
+    (written and read) and y."""
+    from hawking_amd import organs
+    lefts, rights = [], []
+    for i in range(n):
+        sid = (0xB5 << 48) | i
+        lefts.append(organs.SyntheticOrgan(ctx, HK_U3, rows, rank, organs.stream_key(SEED, sid), 0, group=64,
+                                           sigma=0.05))
+        rights.append(organs.SyntheticOrgan(ctx, HK_U3, rank, cols, organs.stream_key(SEED, sid ^ (1 << 47)), 0,
+                                            group=64))
+    ls, rs = organs.OrganSet(ctx, lefts), organs.OrganSet(ctx, rights)
+    x = ctx.empty((n, cols))
+    ctx.call("hk_synth_normal", organs.stream_key(SEED, 0xB50001), 0, n * cols, 1.0, x.ptr, ctx.stream)
+    mid, y = ctx.empty((n, rank)), ctx.empty((n, rows))
+
+    def step():
+        rs.gemv(x, cols, mid, rank)
+        ls.gemv(mid, rank, y, rows)
+
+    ms = time_launches(ctx, step, steps, warmup)
+    nbytes = ls.packed_bytes + rs.packed_bytes + n * (cols + 2 * rank + rows) * 4
+    return {"gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "us_per_step": round(ms * 1e3, 1), "organs": n, "shape": [rows, rank, cols],
+            "packed_bytes_per_organ": round((ls.packed_bytes + rs.packed_bytes) / n, 1)}
 
 
 def single_organ_us(ctx, steps=200):
@@ -296,6 +325,8 @@ def main():
                            "us_per_launch": round(r["ms"] * 1e3, 1), "organs": r["organs"],
                            "packed_bytes_per_organ": round(r["packed_bytes_per_organ"], 1)}
             log(name, extra[name])
+        extra["hgravs01_r160_2048x768"] = lowrank_streamed(ctx, args.steps, args.warmup)
+        log("hgravs01", extra["hgravs01_r160_2048x768"])
         extra["single_organ_binary_512x2048_us"] = round(single_organ_us(ctx), 2)
         log("single organ us", extra["single_organ_binary_512x2048_us"])
         if not args.no_moe:

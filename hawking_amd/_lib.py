@@ -20,7 +20,7 @@ HK_E_UNSUPPORTED = 5
 HK_E_ROUTE = 6
 HK_E_NOMEM = 7
 
-HK_Q4, HK_BIN, HK_MIXED, HK_F32, HK_Q8 = 0, 1, 2, 3, 4
+HK_Q4, HK_BIN, HK_MIXED, HK_F32, HK_Q8, HK_U3 = 0, 1, 2, 3, 4, 5
 HK_ROUTER_SOFTMAX, HK_ROUTER_NOAUX_TC = 0, 1
 
 STATUS_NAMES = {
@@ -87,6 +87,7 @@ PROTOTYPES = {
     "hk_organ_info": (C.c_int, [_p, C.POINTER(_i32), C.POINTER(_i32), C.POINTER(_u32),
                                 C.POINTER(_u32), C.POINTER(_sz)]),
     "hk_gemv": (C.c_int, [_p, _p, _p, _p, _p]),
+    "hk_gemv_lowrank": (C.c_int, [_p, _p, _p, _p, _p, _p, _p]),
     "hk_gemv_batch": (C.c_int, [_p, C.POINTER(_p), _u32, _p, _sz, _p, _sz, _p]),
     "hk_decode_rows": (C.c_int, [_p, _p, _u32, _u32, _p, _p]),
     "hk_organ_set_create": (C.c_int, [_p, C.POINTER(_p), _u32, C.POINTER(_p)]),
@@ -97,6 +98,7 @@ PROTOTYPES = {
     "hk_pack_bin": (C.c_int, [_p, _p, _u32, _u32, _p, _p, _p]),
     "hk_pack_q2": (C.c_int, [_p, _p, _sz, _p, _p, _p]),
     "hk_pack_q8": (C.c_int, [_p, _p, _u32, _u32, _p, _p, _p]),
+    "hk_pack_u3": (C.c_int, [_p, _p, _sz, _p, _p, _p]),
     "hk_stream_key": (_u64, [_u64, _u64]),
     "hk_synth_normal": (C.c_int, [_p, _u64, _u64, _sz, C.c_float, _p, _p]),
     "hk_router_softmax_topk": (C.c_int, [_p, _p, _u32, _u32, _u32, C.c_float, C.c_int, _p, _p, _p]),

@@ -22,6 +22,7 @@ using hk::CanonView;
 
 struct hk_organ {
     hk::OrganView view{};
+    int32_t kind = 0;          // the canonical kind it was uploaded as (view.kind is the engine's)
     void* view_dev = nullptr;  // device copy of `view` for single-organ launches
     void* mem = nullptr;
     size_t alloc_bytes = 0;
@@ -100,6 +101,10 @@ static int validate_shape(hk_ctx* ctx, int kind, int group, uint32_t rows, uint3
         if (group != 64) return set_error(ctx, HK_E_UNSUPPORTED, "uniform q8 organs use group_size 64 (HGRAVU01)");
         if (cols % 64) return set_error(ctx, HK_E_GEOMETRY, "uniform q8 organs require cols % 64 == 0");
         return HK_OK;
+    case HK_U3:
+        if (group != 64) return set_error(ctx, HK_E_UNSUPPORTED, "3-bit factors use group_size 64 (HGRAVS01)");
+        if (cols % 32) return set_error(ctx, HK_E_GEOMETRY, "3-bit factors require cols % 32 == 0");
+        return HK_OK;
     case HK_F32:
         if (cols % 4) return set_error(ctx, HK_E_GEOMETRY, "dense organs require cols % 4 == 0");
         return HK_OK;
@@ -112,7 +117,7 @@ static int validate_shape(hk_ctx* ctx, int kind, int group, uint32_t rows, uint3
 static int validate_gemv_cols(hk_ctx* ctx, int kind, uint32_t cols) {
     if (kind == HK_F32 || gemv_lds_bytes(kind, cols) <= GEMV_LDS_LIMIT) return HK_OK;
     return set_error(ctx, HK_E_GEOMETRY, "organ cols=" + std::to_string(cols) +
-                                             " exceeds the GEMV's LDS x image (at most ~12000 columns)");
+                                             " exceeds the GEMV's LDS x image (at most 12160 columns; 6144 for 3-bit factors)");
 }
 
 static Layout layout_for(int kind, int group, uint32_t rows, uint32_t cols, uint32_t n_bin,
@@ -131,6 +136,10 @@ static Layout layout_for(int kind, int group, uint32_t rows, uint32_t cols, uint
     case HK_Q8:
         L.scales = n / 64 * 2;
         L.codes = n;
+        break;
+    case HK_U3:
+        L.scales = (n + 63) / 64 * 2;
+        L.codes = (n + 63) / 64 * 24;
         break;
     case HK_MIXED: {
         const size_t groups = n / 128;
@@ -183,9 +192,10 @@ static int validate_src(hk_ctx* ctx, const hk_organ_src* s, Layout* out) {
     if (!rc) rc = validate_gemv_cols(ctx, s->kind, s->cols);
     if (rc) return rc;
     const size_t n = (size_t)s->rows * s->cols;
-    if (s->kind == HK_Q4 || s->kind == HK_BIN || s->kind == HK_Q8) {
+    if (s->kind == HK_Q4 || s->kind == HK_BIN || s->kind == HK_Q8 || s->kind == HK_U3) {
         if (!s->scales || !s->codes) return set_error(ctx, HK_E_INVALID_ARG, "organ scales/codes are NULL");
-        const size_t groups = n / (size_t)(s->kind == HK_Q4 ? s->group : s->kind == HK_Q8 ? 64 : 128);
+        const size_t G = s->kind == HK_Q4 ? s->group : (s->kind == HK_Q8 || s->kind == HK_U3) ? 64 : 128;
+        const size_t groups = (n + G - 1) / G;
         for (size_t g = 0; g < groups; ++g)
             if (!f16_finite(s->scales[g]))
                 return set_error(ctx, HK_E_NONFINITE, "group " + std::to_string(g) + " scale is not a finite FP16");
@@ -222,7 +232,7 @@ static int copy_src(hk_ctx* ctx, const hk_organ_src* s, const Layout& L, uint8_t
                          "hipMemcpyAsync (organ upload)");
     };
     int rc = HK_OK;
-    if (s->kind == HK_Q4 || s->kind == HK_BIN || s->kind == HK_Q8) {
+    if (s->kind == HK_Q4 || s->kind == HK_BIN || s->kind == HK_Q8 || s->kind == HK_U3) {
         if ((rc = cp(v.scales, s->scales, L.scales))) return rc;
         if ((rc = cp(v.codes, s->codes, L.codes))) return rc;
     } else if (s->kind == HK_MIXED) {
@@ -425,6 +435,7 @@ extern "C" int hk_event_elapsed_ms(hk_ctx* ctx, void* a, void* b, float* ms) {
 static int repack_into_organ(hk_ctx* ctx, const CanonView& canon, uint32_t n_bin, uint32_t n_q2, hipStream_t st,
                              hk_organ** out) {
     hk_organ* o = new hk_organ();
+    o->kind = canon.kind;
     o->alloc_bytes = tiled_bytes(canon.kind, canon.group, canon.rows, canon.cols, n_bin, n_q2, &o->packed_bytes);
     if (hipMalloc(&o->mem, o->alloc_bytes) != hipSuccess) {
         delete o;
@@ -481,7 +492,7 @@ extern "C" int hk_organ_free(hk_ctx* ctx, hk_organ* o) {
 extern "C" int hk_organ_info(const hk_organ* o, int32_t* kind, int32_t* group, uint32_t* rows, uint32_t* cols,
                              size_t* packed_bytes) {
     if (!o) return HK_E_INVALID_ARG;
-    if (kind) *kind = o->view.kind;
+    if (kind) *kind = o->kind;
     if (group) *group = o->view.group;
     if (rows) *rows = o->view.rows;
     if (cols) *cols = o->view.cols;
@@ -514,6 +525,20 @@ extern "C" int hk_gemv(hk_ctx* ctx, const hk_organ* o, const float* x, float* y,
     }
     return check_hip(ctx, launch_gemv_tiled(static_cast<const OrganView*>(o->view_dev), 1, o->view, x, 0, y, 0, st),
                      "gemv launch");
+}
+
+extern "C" int hk_gemv_lowrank(hk_ctx* ctx, const hk_organ* left, const hk_organ* right, const float* x, float* mid,
+                               float* y, hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (!left || !right) return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv_lowrank: NULL factor");
+    if (right->view.rows != left->view.cols)
+        return set_error(ctx, HK_E_GEOMETRY, "hk_gemv_lowrank: right rows (the rank) must equal left cols");
+    int rc = check_vectors(ctx, "hk_gemv_lowrank", x, 0, mid, 0, 1, right->view);
+    if (!rc) rc = check_vectors(ctx, "hk_gemv_lowrank", mid, 0, y, 0, 1, left->view);
+    if (rc) return rc;
+    // stream order carries mid from the first launch to the second
+    rc = hk_gemv(ctx, right, x, mid, stream);
+    return rc ? rc : hk_gemv(ctx, left, mid, y, stream);
 }
 
 struct hk_organ_set {
@@ -590,7 +615,7 @@ extern "C" int hk_organ_synthetic(hk_ctx* ctx, int32_t kind, int32_t group, uint
     if (!ctx || !out) return HK_E_INVALID_ARG;
     *out = nullptr;
     if (kind == HK_BIN || kind == HK_MIXED) group = 128;
-    if (kind == HK_Q8) group = 64;
+    if (kind == HK_Q8 || kind == HK_U3) group = 64;
     int rc = validate_shape(ctx, kind, group, rows, cols);
     if (!rc) rc = validate_gemv_cols(ctx, kind, cols);
     if (rc) return rc;
@@ -606,7 +631,8 @@ extern "C" int hk_organ_synthetic(hk_ctx* ctx, int32_t kind, int32_t group, uint
     j.group = group;
     j.rows = rows;
     j.cols = cols;
-    const size_t groups = (size_t)rows * cols / (size_t)(kind == HK_F32 ? 128 : group);
+    const size_t G = kind == HK_F32 ? 128 : (size_t)group;
+    const size_t groups = ((size_t)rows * cols + G - 1) / G;
     uint32_t nbin = 0;
     rc = check_hip(ctx, hipMemsetAsync(aux, 0, 8, st), "memset");
     if (!rc && kind == HK_MIXED) {
@@ -715,6 +741,19 @@ extern "C" int hk_pack_q8(hk_ctx* ctx, const float* w, uint32_t rows, uint32_t c
     uint32_t* bad;
     if ((rc = pack_prologue(ctx, st, &bad))) return rc;
     return finish_pack(ctx, st, bad, launch_pack_q8(w, (size_t)rows * cols / 64, scales, codes, bad, st));
+}
+
+extern "C" int hk_pack_u3(hk_ctx* ctx, const float* w, size_t count, uint16_t* scales, uint8_t* codes,
+                          hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (count == 0) return set_error(ctx, HK_E_GEOMETRY, "hk_pack_u3: count must be positive");
+    if (!w || !scales || !codes || !aligned16(codes))
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_pack_u3: NULL or misaligned pointer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    uint32_t* bad;
+    int rc;
+    if ((rc = pack_prologue(ctx, st, &bad))) return rc;
+    return finish_pack(ctx, st, bad, launch_pack_u3(w, count, scales, codes, bad, st));
 }
 
 extern "C" int hk_pack_q2(hk_ctx* ctx, const float* w, size_t count, uint16_t* scales, uint8_t* codes,

@@ -36,13 +36,20 @@ __device__ __forceinline__ void flush_group(float* acc, const uint32_t* T, int n
     }
 }
 
-constexpr uint32_t GEMV_MAX_TILES_PER_WG = 32;
 // Mixed step headers staged per workgroup: tiles x steps <= 32 x 24.
+constexpr uint32_t GEMV_MAX_MIXED_TILES_PER_WG = 32;
 constexpr int GEMV_HDR_PER_THREAD = 3;
-constexpr uint32_t GEMV_MAX_MIXED_STEPS = GEMV_HDR_PER_THREAD * 256 / GEMV_MAX_TILES_PER_WG;
+constexpr uint32_t GEMV_MAX_MIXED_STEPS = GEMV_HDR_PER_THREAD * 256 / GEMV_MAX_MIXED_TILES_PER_WG;
 
-// Dynamic LDS: x image, one quantization window (2048 columns), then (mixed)
-// the headers of the workgroup's tiles.
+// Tiles per workgroup of a launch: narrow 3-bit factors (<= 4 steps, e.g. the
+// rank-160 left factor) take 128 tiles so the x image is built once per 128
+// tiles; every other launch at most 32.
+__host__ __device__ inline uint32_t gemv_max_tiles(int kind, uint32_t steps) {
+    return kind == HK_U3 && steps <= 4 ? 128u : 32u;
+}
+
+// Dynamic LDS: x image, one quantization window (2048 columns), (mixed) the
+// headers of the workgroup's tiles, then the workgroup's row outputs.
 template <int KIND>
 __host__ __device__ constexpr size_t gemv_hdr_offset(uint32_t steps) {
     return x_lds_bytes<KIND>(steps) + (size_t)(steps * (uint32_t)Kcfg<KIND>::STEP_COLS < 2048u
@@ -71,7 +78,6 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const
                   uint32_t* status) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float red[4];
-    __shared__ float ysh[GEMV_MAX_TILES_PER_WG * 16];
     uint32_t oi, part;
     organ_part(blockIdx.x, parts, n_organs, &oi, &part);
     const OrganView o = organs[oi];
@@ -91,6 +97,8 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const
     const uint32_t nh = (t1 - t0) * o.steps;
     uint4 hreg[GEMV_HDR_PER_THREAD];
     uint4* hsh = reinterpret_cast<uint4*>(lds + gemv_hdr_offset<KIND>(o.steps));
+    float* ysh = reinterpret_cast<float*>(lds + gemv_hdr_offset<KIND>(o.steps) +
+                                          (KIND == HK_MIXED ? (size_t)tiles_per_wg * o.steps * sizeof(uint4) : 0));
     if constexpr (KIND == HK_MIXED) {
 #pragma unroll
         for (int k = 0; k < GEMV_HDR_PER_THREAD; ++k) {
@@ -183,11 +191,13 @@ __global__ void __launch_bounds__(256) gemv_f32_kernel(const OrganView* __restri
 
 size_t gemv_lds_bytes(int kind, uint32_t cols) {
     const uint32_t S = n_steps_for(kind, cols);
-    if (kind == HK_Q4) return gemv_hdr_offset<HK_Q4>(S);
-    if (kind == HK_BIN) return gemv_hdr_offset<HK_BIN>(S);
-    if (kind == HK_Q8) return gemv_hdr_offset<HK_Q8>(S);
+    const size_t ysh = (size_t)gemv_max_tiles(kind, S) * 16u * sizeof(float);
+    if (kind == HK_Q4) return gemv_hdr_offset<HK_Q4>(S) + ysh;
+    if (kind == HK_U3) return gemv_hdr_offset<HK_U3>(S) + ysh;
+    if (kind == HK_BIN) return gemv_hdr_offset<HK_BIN>(S) + ysh;
+    if (kind == HK_Q8) return gemv_hdr_offset<HK_Q8>(S) + ysh;
     if (S > GEMV_MAX_MIXED_STEPS) return SIZE_MAX;
-    return gemv_hdr_offset<HK_MIXED>(S) + (size_t)GEMV_MAX_TILES_PER_WG * S * sizeof(uint4);
+    return gemv_hdr_offset<HK_MIXED>(S) + (size_t)GEMV_MAX_MIXED_TILES_PER_WG * S * sizeof(uint4) + ysh;
 }
 
 template <int KIND, int R, int D>
@@ -198,7 +208,8 @@ static hipError_t launch_kind(const OrganView* organs, uint32_t n, const OrganVi
     // image + one quantization window (2048 columns); x chunks held in
     // registers: one per thread up to 2048 columns, else four
     const uint32_t kc = x_image_cols<KIND>(sh.steps);
-    const size_t lds = gemv_hdr_offset<KIND>(sh.steps) + (KIND == HK_MIXED ? (size_t)tpw * sh.steps * sizeof(uint4) : 0);
+    const size_t lds = gemv_hdr_offset<KIND>(sh.steps) + (KIND == HK_MIXED ? (size_t)tpw * sh.steps * sizeof(uint4) : 0) +
+                       (size_t)tpw * 16u * sizeof(float);
     if (kc <= 2048u)
         hipLaunchKernelGGL((gemv_tiled_kernel<KIND, R, D, 1>), grid, dim3(256), lds, s, organs, n, x, xs, y, ys, tpw,
                            parts, nullptr);
@@ -211,7 +222,8 @@ static hipError_t launch_kind(const OrganView* organs, uint32_t n, const OrganVi
 // Launch shape (R tiles per wave group, D steps in flight, tiles per
 // workgroup) by kind and size, from sweeps over the streamed workloads:
 // binary 4-tile groups over 16 tiles when the organ has >= 4 steps, else
-// 2-tile groups over 32; Q4 2 over 16; mixed (large fragments) 1 over 16.
+// 2-tile groups over 32; Q4 and Q8 2 over 16; 3-bit factors 2 over 16, or over
+// 128 when narrow; mixed (large fragments) 1 over 16.
 template <int KIND>
 static hipError_t launch_r(const OrganView* organs, uint32_t n, const OrganView& sh, const float* x, size_t xs,
                            float* y, size_t ys, hipStream_t s) {
@@ -220,6 +232,8 @@ static hipError_t launch_r(const OrganView* organs, uint32_t n, const OrganView&
         if constexpr (KIND == HK_BIN) {
             if (sh.steps >= 4) return launch_kind<KIND, 4, 3>(organs, n, sh, x, xs, y, ys, 16, s);
             return launch_kind<KIND, 2, 3>(organs, n, sh, x, xs, y, ys, 32, s);
+        } else if constexpr (KIND == HK_U3) {
+            return launch_kind<KIND, 2, 3>(organs, n, sh, x, xs, y, ys, gemv_max_tiles(KIND, sh.steps) == 128u ? 128 : 16, s);
         } else if constexpr (KIND == HK_Q4 || KIND == HK_Q8) {
             return launch_kind<KIND, 2, 3>(organs, n, sh, x, xs, y, ys, 16, s);
         } else {
@@ -242,6 +256,7 @@ hipError_t launch_gemv_tiled(const OrganView* organs_dev, uint32_t n, const Orga
     case HK_Q4: return launch_r<HK_Q4>(organs_dev, n, sh, x, x_stride, y, y_stride, s);
     case HK_MIXED: return launch_r<HK_MIXED>(organs_dev, n, sh, x, x_stride, y, y_stride, s);
     case HK_Q8: return launch_r<HK_Q8>(organs_dev, n, sh, x, x_stride, y, y_stride, s);
+    case HK_U3: return launch_r<HK_U3>(organs_dev, n, sh, x, x_stride, y, y_stride, s);
     default: return hipErrorInvalidValue;
     }
 }

@@ -53,7 +53,9 @@ struct OrganView {
     uint32_t rows;
     uint32_t cols;
     uint32_t n_tiles;           // ceil(rows / 16)
-    uint32_t steps;             // 1 KiB wave loads per tile
+    uint32_t steps;             // 1 KiB wave loads per tile (U3: 768 B)
+    uint32_t tail_q;            // U3: column slots stored in the last step (1..4)
+    uint32_t reserved;
     const uint8_t* data;        // signs / codes / mixed items
     const uint16_t* scales;
     const uint4* hdr;           // MIXED per-(tile, step) headers
@@ -75,6 +77,11 @@ typedef float hk_f32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ldg(const uint4* p) {
     const hk_u32x4 v = *(const __attribute__((address_space(1))) hk_u32x4*)(p);
     return make_uint4(v.x, v.y, v.z, v.w);
+}
+typedef unsigned int hk_u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint2 ldg(const uint2* p) {
+    const hk_u32x2 v = *(const __attribute__((address_space(1))) hk_u32x2*)(p);
+    return make_uint2(v.x, v.y);
 }
 __device__ __forceinline__ float4 ldg(const float4* p) {
     const hk_f32x4 v = *(const __attribute__((address_space(1))) hk_f32x4*)(p);
@@ -182,9 +189,11 @@ int ensure_scratch(hk_ctx* ctx, size_t bytes, void** out);
 
 // Kernel launchers (defined in the .hip files); all stream-ordered, no sync.
 // GEMV over n organs of one kind/shape (descriptor table in device memory).
-// Dynamic LDS of the GEMV kernel for a packed organ of `cols` columns.
+// Dynamic LDS of the GEMV kernel for a packed organ of `cols` columns (x
+// image, quantization window, mixed headers, row outputs), and its cap, which
+// keeps a workgroup within 64 KB.
 size_t gemv_lds_bytes(int kind, uint32_t cols);
-constexpr size_t GEMV_LDS_LIMIT = 60 * 1024;
+constexpr size_t GEMV_LDS_LIMIT = 62 * 1024;
 hipError_t launch_gemv_tiled(const OrganView* organs_dev, uint32_t n, const OrganView& shape,
                              const float* x, size_t x_stride, float* y, size_t y_stride,
                              hipStream_t s);

@@ -14,7 +14,9 @@
 //   * The B operand (64 x 16) comes straight from the packed bytes with one AND
 //     per 4 weights: a binary bit plane s is bytes & (0x01 << s) = bit * 2^s, a
 //     Q4 nibble plane is bytes & 0x0F, a Q2 field is bytes & (0x03 << 2u); the
-//     power of two is folded into the A limbs (X * 2^(7-s) etc.).  Binary plane
+//     power of two is folded into the A limbs (X * 2^(7-s) etc.).  A 3-bit code
+//     is split into its low 2-bit field and its high bit, each its own B bytes
+//     (the high bit's A carries the extra factor 4).  Binary plane
 //     7 is the raw signed byte (no AND): its A row is -X7 and every lower
 //     plane's A row carries +X7, which cancels the lower bits the raw byte
 //     brings in (sum_s<7 (X_s 2^(7-s) + X7) 2^s b_s - X7 byte = 128 sum X_s b_s).
@@ -64,6 +66,10 @@ template <>
 struct Kcfg<HK_Q8> {
     static constexpr int P = 1, STEP_COLS = 64, DATA = 16, SXG = 16;
 };
+template <>
+struct Kcfg<HK_U3> {
+    static constexpr int P = 4, STEP_COLS = 128, DATA = 12, SXG = 32;
+};
 
 constexpr int A_TILE_STRIDE = 272;  // 256 B of active-lane limbs + 16 B of zeros
 
@@ -101,6 +107,17 @@ __device__ __forceinline__ int32_t a_value(const float* xq, int t, int mu, int q
         return X((uint32_t)(t * 128 + q * 32 + 2 * i + mu));
     } else if constexpr (KIND == HK_Q8) {
         return X((uint32_t)(t * 64 + q * 16 + i));
+    } else if constexpr (KIND == HK_U3) {
+        // MFMA mu: dwords 0-1 are the low fields u = mu of low dwords 0-1
+        // (column 16d + 4j + mu, times 4^mu; mu = 3 is shifted down to 1),
+        // dwords 2-3 the high bits s = 2mu, 2mu+1 (column 8j + s, times 2^s,
+        // bit 7 as the signed byte -128); every product is scaled to 32 * code * X
+        const int d = i >> 2, j = i & 3;
+        const uint32_t c0 = (uint32_t)(t * 128 + q * 32);
+        if (d < 2) return X(c0 + (uint32_t)(16 * d + 4 * j + mu)) * (mu == 3 ? 32 : 1 << (5 - 2 * mu));
+        const int s = 2 * mu + d - 2;
+        const int32_t v = X(c0 + (uint32_t)(8 * j + s));
+        return s == 7 ? -v : v * (1 << (7 - s));
     } else {
         const int h = mu >> 2, u = mu & 3, r = i >> 2, j = i & 3;
         const int a = r < 2 ? 2 * h + r : 2 * h + 2 + r;
@@ -315,6 +332,12 @@ struct Frag<HK_Q8, R> {
     uint16_t s[R];
 };
 template <int R>
+struct Frag<HK_U3, R> {
+    uint2 lo[R];
+    uint32_t hi[R];
+    uint16_t s[R];
+};
+template <int R>
 struct Frag<HK_MIXED, R> {
     uint32_t V[R][8];
     uint16_t s0[R], s1[R];
@@ -354,6 +377,15 @@ __device__ __forceinline__ void fetch_one(const OrganView& o, uint32_t T, uint32
     } else if constexpr (KIND == HK_Q8) {
         f.v[r] = ldg(reinterpret_cast<const uint4*>(o.data + ((size_t)T * o.steps + t) * 1024u + 16u * lane));
         f.s[r] = ldg(o.scales + ((size_t)T * o.steps + t) * 16u + (lane & 15));
+    } else if constexpr (KIND == HK_U3) {
+        // the last step stores tail_q slots; lanes of absent slots re-read slot 0
+        const bool tail = t + 1 == o.steps;
+        const uint32_t nq = tail ? o.tail_q : 4u;
+        const uint32_t l = (uint32_t)(lane >> 4) < nq ? (uint32_t)lane : (uint32_t)(lane & 15);
+        const uint8_t* base = o.data + (size_t)T * u3_tile_data(o.steps, o.tail_q) + 768u * t;
+        f.lo[r] = ldg(reinterpret_cast<const uint2*>(base + 8u * l));
+        f.hi[r] = ldg(reinterpret_cast<const uint32_t*>(base + 128u * nq + 4u * l));
+        f.s[r] = ldg(o.scales + (size_t)T * u3_tile_scales(o.steps, o.tail_q) + 64u * t + l);
     } else {
         fetch_mixed<R>(o, ldg(o.hdr + (size_t)T * o.steps + t), lane, f, r);
     }
@@ -418,6 +450,24 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
         const float sx = SX[4 * t + q];
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] += f16_bits_to_f32(f.s[r]) * (combine_limbs(c[r]) + sx);
+    } else if constexpr (KIND == HK_U3) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) c[r] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int mu = 0; mu < 4; ++mu) {
+            const v4i a = A(t * 4 + mu);
+            const uint32_t m2 = 0x03030303u << (2 * mu), m1 = 0x01010101u << (2 * mu);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t l0 = mu < 3 ? (f.lo[r].x & m2) : ((f.lo[r].x >> 6) & 0x03030303u);
+                const uint32_t l1 = mu < 3 ? (f.lo[r].y & m2) : ((f.lo[r].y >> 6) & 0x03030303u);
+                const v4i b = {(int)l0, (int)l1, (int)(f.hi[r] & m1), (int)(f.hi[r] & (m1 << 1))};
+                c[r] = mfma_i8(a, b, c[r]);
+            }
+        }
+        const float sx = SX[4 * t + q];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] += f16_bits_to_f32(f.s[r]) * (combine_limbs(c[r]) * (1.0f / 32.0f) - 3.0f * sx);
     } else {
         uint32_t V[R][8];
 #pragma unroll

@@ -113,6 +113,38 @@ __device__ void q8_pack_group(const Src& src, uint16_t* scale_out, uint8_t* code
     }
 }
 
+// One flat 64-group of a 3-bit uniform factor (pack_uniform_factor at 3 bits,
+// q80_mixed_decode.rs:529-577): bound 3, values past n_valid pack as 0, and the
+// 64 codes q + 3 are written LSB-first as 24 bytes.
+template <class Src>
+__device__ void u3_pack_group(const Src& src, uint32_t n_valid, uint16_t* scale_out, uint8_t* codes_out,
+                              uint32_t* bad) {
+    float max_abs = 0.0f;
+    for (uint32_t i = 0; i < n_valid; ++i) {
+        const float v = src((int)i);
+        if (!isfinite(v)) *bad = 1u;
+        max_abs = fmaxf(max_abs, fabsf(v));
+    }
+    const float scale = __fdiv_rn(max_abs, 3.0f);
+    const uint16_t sb = f32_to_f16_bits(scale);
+    if ((sb & 0x7C00u) == 0x7C00u) *bad = 1u;
+    *scale_out = sb;
+    const float denom = scale > 0.0f ? scale : 1.0f;
+    uint64_t w[3] = {0, 0, 0};
+#pragma unroll
+    for (uint32_t i = 0; i < 64; ++i) {
+        const float v = i < n_valid ? src((int)i) : 0.0f;
+        const uint64_t code = (uint64_t)((int)fminf(fmaxf(roundf(__fdiv_rn(v, denom)), -3.0f), 3.0f) + 3);
+        const uint32_t p = 3u * i;
+        w[p >> 6] |= code << (p & 63u);
+        if ((p & 63u) > 61u) w[(p >> 6) + 1] |= code >> (64u - (p & 63u));
+    }
+    uint64_t* o = reinterpret_cast<uint64_t*>(codes_out);
+    o[0] = w[0];
+    o[1] = w[1];
+    o[2] = w[2];
+}
+
 struct BufSrc {
     const float* p;
     __device__ float operator()(int i) const { return p[i]; }
@@ -170,6 +202,18 @@ __global__ void pack_q8_kernel(const float* __restrict__ w, size_t groups, uint1
     }
 }
 
+__global__ void pack_u3_kernel(const float* __restrict__ w, size_t count, uint16_t* __restrict__ scales,
+                               uint8_t* __restrict__ codes, uint32_t* bad) {
+    const size_t groups = (count + 63) / 64;
+    for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < groups;
+         g += (size_t)gridDim.x * blockDim.x) {
+        uint32_t b = 0;
+        const uint32_t nv = (uint32_t)(count - g * 64 < 64 ? count - g * 64 : 64);
+        u3_pack_group(BufSrc{w + g * 64}, nv, scales + g, codes + g * 24, &b);
+        if (b) atomicOr(bad, 1u);
+    }
+}
+
 __global__ void synth_normal_kernel(uint64_t key, uint64_t first, size_t count, float sigma,
                                     float* __restrict__ out) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
@@ -200,6 +244,13 @@ hipError_t launch_pack_bin(const float* w, size_t groups, uint16_t* scales, uint
 hipError_t launch_pack_q8(const float* w, size_t groups, uint16_t* scales, uint8_t* codes, uint32_t* bad,
                           hipStream_t s) {
     hipLaunchKernelGGL(pack_q8_kernel, dim3(grid_for(groups, 256)), dim3(256), 0, s, w, groups, scales, codes, bad);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack_u3(const float* w, size_t count, uint16_t* scales, uint8_t* codes, uint32_t* bad,
+                          hipStream_t s) {
+    hipLaunchKernelGGL(pack_u3_kernel, dim3(grid_for((count + 63) / 64, 256)), dim3(256), 0, s, w, count, scales,
+                       codes, bad);
     return hipGetLastError();
 }
 
@@ -254,6 +305,18 @@ __global__ void synth_pack_q8_kernel(const SynthJob* __restrict__ jobs, uint32_t
          g += (size_t)gridDim.x * blockDim.x) {
         uint32_t b = 0;
         q8_pack_group(SynthSrc{j.key, g * 64, j.sigma}, j.scales + g, j.codes + g * 64, &b);
+        if (b) atomicOr(bad, 1u);
+    }
+}
+
+__global__ void synth_pack_u3_kernel(const SynthJob* __restrict__ jobs, uint32_t* bad) {
+    const SynthJob j = jobs[blockIdx.y];
+    const size_t n = (size_t)j.rows * j.cols, groups = (n + 63) / 64;
+    for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < groups;
+         g += (size_t)gridDim.x * blockDim.x) {
+        uint32_t b = 0;
+        const uint32_t nv = (uint32_t)(n - g * 64 < 64 ? n - g * 64 : 64);
+        u3_pack_group(SynthSrc{j.key, g * 64, j.sigma}, nv, j.scales + g, j.codes + g * 24, &b);
         if (b) atomicOr(bad, 1u);
     }
 }
@@ -369,6 +432,9 @@ hipError_t launch_synth_jobs(int kind, const SynthJob* jobs_dev, uint32_t njobs,
         break;
     case HK_BIN:
         hipLaunchKernelGGL(synth_pack_bin_kernel, dim3(bx ? bx : 1, njobs), dim3(256), 0, s, jobs_dev, bad);
+        break;
+    case HK_U3:
+        hipLaunchKernelGGL(synth_pack_u3_kernel, dim3(bx ? bx : 1, njobs), dim3(256), 0, s, jobs_dev, bad);
         break;
     case HK_Q8:
         hipLaunchKernelGGL(synth_pack_q8_kernel, dim3(bx ? bx : 1, njobs), dim3(256), 0, s, jobs_dev, bad);

@@ -29,6 +29,13 @@ size_t tiled_bytes(int kind, int group, uint32_t rows, uint32_t cols, uint32_t n
         scales = nt * 16 * S * 2 + 16;
         packed = n + n / 64 * 2;
         break;
+    case HK_U3: {
+        const size_t groups = (n + 63) / 64;
+        data = nt * u3_tile_data((uint32_t)S, u3_tail_q(cols));
+        scales = nt * u3_tile_scales((uint32_t)S, u3_tail_q(cols)) * 2 + 16;
+        packed = groups * 24 + groups * 2;
+        break;
+    }
     case HK_MIXED: {
         const size_t items = nt * S * 64, pad = items - (size_t)n_bin - n_q2;
         data = ((size_t)n_bin + pad) * 16 + (size_t)n_q2 * 32;
@@ -59,6 +66,10 @@ OrganView tiled_place(int kind, int group, uint32_t rows, uint32_t cols, uint32_
     if (kind == HK_BIN || kind == HK_Q4) {
         data = nt * S * 1024;
         scales = nt * 64 * S * 2 + 16;
+    } else if (kind == HK_U3) {
+        v.tail_q = u3_tail_q(cols);
+        data = nt * u3_tile_data((uint32_t)S, v.tail_q);
+        scales = nt * u3_tile_scales((uint32_t)S, v.tail_q) * 2 + 16;
     } else if (kind == HK_Q8) {
         data = nt * S * 1024;
         scales = nt * 16 * S * 2 + 16;
@@ -81,6 +92,14 @@ OrganView tiled_place(int kind, int group, uint32_t rows, uint32_t cols, uint32_
 }
 
 // ------------------------------------------------------------------ BIN / Q4
+
+// Code e of a 3-bit LSB-first stream (extract_unsigned, q80_mixed_decode.rs:579-589).
+__device__ inline uint32_t get_code3(const uint8_t* codes, size_t e) {
+    const size_t b = 3 * e;
+    uint32_t two = codes[b >> 3];
+    if ((b & 7u) > 5u) two |= (uint32_t)codes[(b >> 3) + 1] << 8;  // the code straddles a byte
+    return (two >> (b & 7u)) & 7u;
+}
 
 // One thread per (tile, step, lane) item: copy its 16 bytes and its scale.
 __device__ void repack_fixed_body(const CanonView& src, const OrganView& dst) {
@@ -119,6 +138,37 @@ __device__ void repack_fixed_body(const CanonView& src, const OrganView& dst) {
         }
         *reinterpret_cast<uint4*>(const_cast<uint8_t*>(dst.data) + (size_t)ts * 1024u + 16u * l) = v;
         const_cast<uint16_t*>(dst.scales)[(size_t)ts * 64u + l] = s;
+    }
+}
+
+// One thread per stored (tile, step, lane) item of a U3 organ: split the 32
+// codes of its chunk into the low 2-bit fields and the high bits, copy the
+// scale of the flat group holding the chunk.  Padding rows get scale 0.
+__device__ void repack_u3_body(const CanonView& src, const OrganView& dst) {
+    const uint32_t S = dst.steps, nql = dst.tail_q;
+    const size_t per_tile = (size_t)64 * (S - 1) + 16u * nql, total = dst.n_tiles * per_tile;
+    const size_t tile_data = u3_tile_data(S, nql), tile_sc = u3_tile_scales(S, nql);
+    for (size_t it = (size_t)blockIdx.x * blockDim.x + threadIdx.x; it < total;
+         it += (size_t)gridDim.x * blockDim.x) {
+        const uint32_t T = (uint32_t)(it / per_tile), rem = (uint32_t)(it % per_tile);
+        const uint32_t t = rem / 64u, l = rem % 64u, n = l & 15u, q = l >> 4;
+        const uint32_t nq = t + 1 == S ? nql : 4u, r = T * 16u + n;
+        uint32_t lo0 = 0, lo1 = 0, hi = 0;
+        uint16_t s = 0;
+        if (r < src.rows) {
+            const size_t e0 = (size_t)r * src.cols + 128u * t + 32u * q;
+            for (uint32_t k = 0; k < 32; ++k) {
+                const uint32_t code = get_code3(src.codes, e0 + k);
+                if (k < 16) lo0 |= (code & 3u) << (2u * k);
+                else lo1 |= (code & 3u) << (2u * (k - 16u));
+                hi |= (code >> 2) << k;
+            }
+            s = src.scales[e0 / 64u];
+        }
+        uint8_t* base = const_cast<uint8_t*>(dst.data) + (size_t)T * tile_data + 768u * t;
+        *reinterpret_cast<uint2*>(base + 8u * l) = make_uint2(lo0, lo1);
+        *reinterpret_cast<uint32_t*>(base + 128u * nq + 4u * l) = hi;
+        const_cast<uint16_t*>(dst.scales)[(size_t)T * tile_sc + 64u * t + l] = s;
     }
 }
 
@@ -217,6 +267,10 @@ static unsigned grid1(size_t n) {
 
 // Single organ (arguments by value) and batched (blockIdx.y = job) forms.
 __global__ void repack_fixed_kernel(CanonView src, OrganView dst) { repack_fixed_body(src, dst); }
+__global__ void repack_u3_kernel(CanonView src, OrganView dst) { repack_u3_body(src, dst); }
+__global__ void repack_u3_batch_kernel(const RepackJob* __restrict__ jobs) {
+    repack_u3_body(jobs[blockIdx.y].src, jobs[blockIdx.y].dst);
+}
 __global__ void repack_mixed_mask_kernel(CanonView src, OrganView dst, uint32_t* counts) {
     repack_mixed_mask_body(src, dst, counts);
 }
@@ -243,6 +297,8 @@ hipError_t launch_repack(const CanonView& src, const OrganView& dst, void* scrat
     const size_t items = (size_t)dst.n_tiles * dst.steps * 64;
     if (src.kind == HK_BIN || src.kind == HK_Q4 || src.kind == HK_Q8) {
         hipLaunchKernelGGL(repack_fixed_kernel, dim3(grid1(items)), dim3(256), 0, s, src, dst);
+    } else if (src.kind == HK_U3) {
+        hipLaunchKernelGGL(repack_u3_kernel, dim3(grid1(items)), dim3(256), 0, s, src, dst);
     } else if (src.kind == HK_MIXED) {
         uint32_t* counts = static_cast<uint32_t*>(scratch);
         hipLaunchKernelGGL(repack_mixed_mask_kernel, dim3(grid1(items / 64)), dim3(256), 0, s, src, dst, counts);
@@ -260,6 +316,8 @@ hipError_t launch_repack_batch(int kind, const RepackJob* jobs_dev, uint32_t n, 
     const unsigned gx = std::min(grid1(max_items), 1024u);
     if (kind == HK_BIN || kind == HK_Q4 || kind == HK_Q8) {
         hipLaunchKernelGGL(repack_fixed_batch_kernel, dim3(gx, n), dim3(256), 0, s, jobs_dev);
+    } else if (kind == HK_U3) {
+        hipLaunchKernelGGL(repack_u3_batch_kernel, dim3(gx, n), dim3(256), 0, s, jobs_dev);
     } else if (kind == HK_MIXED) {
         hipLaunchKernelGGL(repack_mixed_mask_batch_kernel, dim3(std::min(grid1(max_items / 64), 1024u), n), dim3(256),
                            0, s, jobs_dev);

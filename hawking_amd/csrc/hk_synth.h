@@ -73,6 +73,9 @@ hipError_t launch_pack_bin(const float* w, size_t groups, uint16_t* scales, uint
                            uint32_t* bad, hipStream_t s);
 hipError_t launch_pack_q8(const float* w, size_t groups, uint16_t* scales, uint8_t* codes, uint32_t* bad,
                           hipStream_t s);
+// 3-bit uniform factor over `count` flat values (groups of 64, the last zero-padded).
+hipError_t launch_pack_u3(const float* w, size_t count, uint16_t* scales, uint8_t* codes, uint32_t* bad,
+                          hipStream_t s);
 hipError_t launch_pack_q2(const float* w, size_t groups, uint16_t* scales, uint8_t* codes,
                           uint32_t* bad, hipStream_t s);
 hipError_t launch_synth_normal(uint64_t key, uint64_t first, size_t count, float sigma, float* out,

@@ -28,6 +28,16 @@
 //         of row n, columns 16q..16q+15 of the step (value (code-127)*scale).
 //         scales: [tile][step][row] f16 (32 bytes per step: the four lanes of
 //         a row read one scale, no duplication).
+//   U3    step = 128 columns, 768 bytes: lane (n,q) holds row n, 32-column
+//         chunk 4t+q as 8 bytes of the codes' low 2-bit fields (column k of
+//         the chunk at bits 2(k%16) of dword k/16) at 8*l, then, after all
+//         lanes, 4 bytes of their high bits (column k at bit k) at
+//         128*nq + 4*l, where nq = 4 column slots per step.  The last step
+//         stores only the tail_q slots that hold columns (nq = tail_q), so a
+//         narrow factor (cols = 160) carries no padded slots; lanes of absent
+//         slots read slot 0's bytes (the x image is zero there).  Value
+//         (lo + 4 hi - 3) * scale; scales: [tile][step][lane] f16 over the
+//         stored lanes (the scale of the flat 64-group holding the chunk).
 #pragma once
 
 #include "hk_internal.h"
@@ -36,8 +46,13 @@ namespace hk {
 
 constexpr uint32_t TILE_ROWS = 16;
 
+// U3 bytes of one tile's data and scales (steps S, tail slots nql).
+__host__ __device__ inline size_t u3_tile_data(uint32_t S, uint32_t nql) { return 768u * (size_t)(S - 1) + 192u * nql; }
+__host__ __device__ inline size_t u3_tile_scales(uint32_t S, uint32_t nql) { return 64u * (size_t)(S - 1) + 16u * nql; }
+__host__ __device__ inline uint32_t u3_tail_q(uint32_t cols) { return ((cols - 1u) % 128u) / 32u + 1u; }
+
 __host__ __device__ inline uint32_t tile_step_cols(int kind) {
-    return kind == HK_Q4 ? 128u : kind == HK_Q8 ? 64u : 512u;
+    return (kind == HK_Q4 || kind == HK_U3) ? 128u : kind == HK_Q8 ? 64u : 512u;
 }
 __host__ __device__ inline uint32_t n_tiles_for(uint32_t rows) { return (rows + TILE_ROWS - 1) / TILE_ROWS; }
 __host__ __device__ inline uint32_t n_steps_for(int kind, uint32_t cols) {
@@ -61,6 +76,16 @@ __device__ inline float tiled_weight(const OrganView& o, uint32_t r, uint32_t c)
         const int nib = (w & 1u) ? (b >> 4) : (b & 0xF);
         const float s = f16_bits_to_f32(o.scales[((size_t)T * o.steps + t) * 64u + l]);
         return (float)(nib - 8) * s;
+    }
+    if (o.kind == HK_U3) {
+        const uint32_t t = c >> 7, q = (c >> 5) & 3u, k = c & 31u, l = n + 16u * q;
+        const uint32_t nq = t + 1 == o.steps ? o.tail_q : 4u;
+        const uint8_t* base = o.data + (size_t)T * u3_tile_data(o.steps, o.tail_q) + 768u * t;
+        const uint32_t lo = *reinterpret_cast<const uint32_t*>(base + 8u * l + 4u * (k >> 4));
+        const uint32_t hi = *reinterpret_cast<const uint32_t*>(base + 128u * nq + 4u * l);
+        const uint32_t code = ((lo >> (2u * (k & 15u))) & 3u) + 4u * ((hi >> k) & 1u);
+        const float s = f16_bits_to_f32(o.scales[(size_t)T * u3_tile_scales(o.steps, o.tail_q) + 64u * t + l]);
+        return (float)((int)code - 3) * s;
     }
     if (o.kind == HK_Q8) {
         const uint32_t t = c >> 6, q = (c >> 4) & 3u, l = n + 16u * q;

@@ -8,6 +8,8 @@ Reference names are kept where the reference has them:
   * MixedPackedTensor (q80_mixed_decode.rs:1073-1417)
   * UniformFactorPacked + uniform_factor_matvec_f32 at 8 bits, group 64
     (HGRAVU01, q80_mixed_decode.rs:529-612,1047-1070)
+  * HGRAVS01 low-rank: two 3-bit uniform factors and
+    hgravs01_two_stage_matvec_f32 (q80_mixed_decode.rs:614-629,1019-1046)
 Every matvec runs the gfx950 kernels through the C ABI; the inputs are the
 reference's canonical packed bytes, uploaded and repacked once.
 """
@@ -18,7 +20,7 @@ import ctypes as C
 import numpy as np
 
 from . import _lib
-from ._lib import HK_BIN, HK_F32, HK_MIXED, HK_Q4, HK_Q8, OrganSrc
+from ._lib import HK_BIN, HK_F32, HK_MIXED, HK_Q4, HK_Q8, HK_U3, OrganSrc
 from .runtime import Context, DeviceArray
 
 
@@ -137,6 +139,54 @@ def uniform_factor_matvec_f32(packed: UniformFactorPacked, x: np.ndarray) -> np.
     return packed.matvec(x)
 
 
+class UniformFactor3(PackedOrgan):
+    """Uniform 3-bit factor, flat groups of 64 (an HGRAVS01 factor body):
+    scales f16[ceil(rows*cols/64)] and 24 code bytes per group (LSB-first,
+    code = q + 3).  Needs cols % 32 == 0."""
+
+    kind = HK_U3
+
+    def __init__(self, ctx: Context, scales: np.ndarray, codes: np.ndarray, rows: int, cols: int):
+        scales = np.ascontiguousarray(scales, np.uint16)
+        codes = np.ascontiguousarray(codes, np.uint8)
+        groups = (rows * cols + 63) // 64
+        if scales.size != groups or codes.size != groups * 24:
+            raise ValueError("3-bit factor scales/codes sizes disagree with the shape")
+        src = OrganSrc(kind=HK_U3, group=64, rows=rows, cols=cols, scales=_ptr(scales), codes=_ptr(codes))
+        super().__init__(ctx, src, (scales, codes))
+
+
+class HgravS01LowRank:
+    """W ~= L R with L rows x rank and R rank x cols (HGRAVS01): y = L (R x)
+    as two launches through a device mid vector of `rank` floats."""
+
+    def __init__(self, left: UniformFactor3, right: UniformFactor3):
+        if right.rows != left.cols:
+            raise ValueError("right rows (the rank) must equal left cols")
+        self.left, self.right = left, right
+        self.ctx = left.ctx
+        self.rows, self.rank, self.cols = left.rows, left.cols, right.cols
+        self.mid = self.ctx.empty(self.rank)
+
+    def matvec_device(self, x: DeviceArray, y: DeviceArray, stream=None) -> None:
+        self.ctx.call("hk_gemv_lowrank", self.left.h, self.right.h, x.ptr, self.mid.ptr, y.ptr,
+                      stream if stream is not None else self.ctx.stream)
+
+    def matvec(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        if x.shape != (self.cols,):
+            raise ValueError(f"matvec input {x.shape} != cols {self.cols}")
+        xd = self.ctx.to_device(x)
+        yd = self.ctx.empty(self.rows)
+        self.matvec_device(xd, yd)
+        return yd.download()
+
+
+def hgravs01_two_stage_matvec_f32(packed: HgravS01LowRank, x: np.ndarray) -> np.ndarray:
+    """GPU counterpart of hgravs01_two_stage_matvec_f32 (q80_mixed_decode.rs:614-629)."""
+    return packed.matvec(x)
+
+
 class MixedPackedTensor(PackedOrgan):
     """Per-128-group binary | Q2 organ from the canonical mixed stream."""
 
@@ -242,6 +292,14 @@ def pack_q8_device(ctx: Context, w: DeviceArray, rows: int, cols: int):
     scales = ctx.empty(rows * cols // 64, np.uint16)
     codes = ctx.empty(rows * cols, np.uint8)
     ctx.call("hk_pack_q8", w.ptr, rows, cols, scales.ptr, codes.ptr, ctx.stream)
+    return scales, codes
+
+
+def pack_u3_device(ctx: Context, w: DeviceArray, count: int):
+    groups = (count + 63) // 64
+    scales = ctx.empty(groups, np.uint16)
+    codes = ctx.empty(groups * 24, np.uint8)
+    ctx.call("hk_pack_u3", w.ptr, count, scales.ptr, codes.ptr, ctx.stream)
     return scales, codes
 
 

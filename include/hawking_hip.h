@@ -49,6 +49,8 @@ extern "C" {
 #define HK_MIXED 2 /* per-128-group binary | Q2 (two f16 scales per 64) */
 #define HK_F32 3   /* dense row-major f32 (router, shared-expert gate) */
 #define HK_Q8 4    /* uniform 8-bit, group 64, f16 scale per group (HGRAVU01) */
+#define HK_U3 5    /* uniform 3-bit, flat groups of 64 (HGRAVS01 low-rank factors);
+                      runs on the Q4 engine (nibble = code + 5) */
 
 typedef struct hk_ctx hk_ctx;
 typedef struct hk_organ hk_organ;
@@ -103,6 +105,10 @@ int hk_check_device_status(hk_ctx* ctx, hk_stream stream, uint32_t* bits);
  *  HK_Q8:    scales f16[rows*cols/64] || codes u8[rows*cols], code = q + 127
  *            (HGRAVU01 body, pack_uniform_factor at 8 bits,
  *            model/qwen_complete_binary/q80_mixed_decode.rs:529-577,786-826)
+ *  HK_U3:    scales f16[groups] || codes: groups*64 3-bit codes LSB-first,
+ *            groups = ceil(rows*cols/64) over the FLAT elements (a group may
+ *            span rows; the last is zero-padded), code = q + 3 (HGRAVS01
+ *            factor body, pack_uniform_factor at 3 bits); needs cols % 32 == 0.
  * Requires cols % group == 0 (row-aligned groups). */
 typedef struct hk_organ_src {
     int32_t kind;
@@ -152,6 +158,13 @@ int hk_organ_set_free(hk_ctx* ctx, hk_organ_set* set);
 int hk_gemv_set(hk_ctx* ctx, const hk_organ_set* set, const float* x, size_t x_stride, float* y,
                 size_t y_stride, hk_stream stream);
 
+/* HGRAVS01 low-rank organ: mid[rank] = right x, then y[rows] = left mid, two
+ * launches ordered on `stream` (mid is a caller buffer of rank floats, 16-byte
+ * aligned).  The factors are HK_U3 organs (left rows x rank, right rank x cols).
+ * Replaces hgravs01_two_stage_matvec_f32 (q80_mixed_decode.rs:614-629). */
+int hk_gemv_lowrank(hk_ctx* ctx, const hk_organ* left, const hk_organ* right, const float* x,
+                    float* mid, float* y, hk_stream stream);
+
 /* Bit-exact decode probe: out[nrows*cols] = decoded weights of rows
  * [row0, row0+nrows).  Replaces qwen_uniform_q4_decode_vector
  * (shaders/qwen_uniform_q4.metal:627) and gather_row
@@ -171,6 +184,11 @@ int hk_pack_bin(hk_ctx* ctx, const float* w, uint32_t rows, uint32_t cols, uint1
 /* pack_uniform_factor at 8 bits, group 64 (q80_mixed_decode.rs:529-577);
  * cols % 64 == 0.  An f16 scale that overflows is reported as HK_E_NONFINITE. */
 int hk_pack_q8(hk_ctx* ctx, const float* w, uint32_t rows, uint32_t cols, uint16_t* scales, uint8_t* codes,
+               hk_stream stream);
+/* pack_uniform_factor at 3 bits, group 64, over `count` flat values (the
+ * HGRAVS01 factor codec, q80_mixed_decode.rs:529-577): scales f16[ceil(count/64)],
+ * codes 24 bytes per group (16-byte aligned). */
+int hk_pack_u3(hk_ctx* ctx, const float* w, size_t count, uint16_t* scales, uint8_t* codes,
                hk_stream stream);
 /* Q2 base stage of _additive_residual_codec
  * (lab/operators/ascension_dual_gravity_worker.py:898-911), group 64. */

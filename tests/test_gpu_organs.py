@@ -200,6 +200,107 @@ def test_uniform_q8_rejects_bad_geometry(ctx, oracle):
     assert e.value.code == HK_E_GEOMETRY
 
 
+def _u3(ctx, oracle, w):
+    from hawking_amd.organs import UniformFactor3
+    s, c = oracle.uniform_pack(w, w.shape[0], w.shape[1], 3, 64)
+    return UniformFactor3(ctx, s, c, w.shape[0], w.shape[1]), (s, c)
+
+
+@pytest.mark.parametrize("count", [64 * 37, 1000])
+def test_device_u3_packer_bit_exact(ctx, oracle, count):
+    """3-bit factor packer (HGRAVS01 body): whole groups and a ragged last group."""
+    from hawking_amd import organs
+    rng = np.random.default_rng(count)
+    w = (rng.standard_normal(count) * 0.02).astype(np.float32)
+    d = 1.0 + 2.0 ** -11
+    w[:5] = [3 * d, 1.5 * d, -1.5 * d, 0.5 * d, 1.5]    # half-away ties under the f32 divisor
+    w[64:128] = 0.0                                     # an all-zero group
+    say("pack_u3", count)
+    s, c = organs.pack_u3_device(ctx, ctx.to_device(w), count)
+    rs, rc = oracle.uniform_pack(w, 1, count, 3, 64)
+    assert np.array_equal(s.download(), rs) and np.array_equal(c.download(), rc)
+
+
+@pytest.mark.parametrize("shape", [(2048, 160), (160, 2048), (13, 96), (16, 32), (1, 6144), (40, 224)])
+def test_uniform_u3_factor_organ(ctx, oracle, shape):
+    """HGRAVS01 factor (3-bit, flat 64-groups that may span rows): decode
+    bit-exact, matvec vs the serial f32 oracle and the FP64 authority."""
+    rows, cols = shape
+    w = oracle.normal(oracle.stream_key(U.SEED, 0xD3 + rows), rows * cols, 0.02).reshape(rows, cols)
+    x = oracle.normal(oracle.stream_key(U.SEED, 0xD3 + rows + 1), cols, 1.0)
+    say("uniform u3 factor", shape)
+    organ, (s, c) = _u3(ctx, oracle, w)
+    groups = (rows * cols + 63) // 64
+    assert organ.packed_bytes == groups * 26
+    assert np.array_equal(organ.decode(), oracle.uniform_decode(s, c, rows, cols, 3, 64))
+    y = organ.matvec(x)
+    assert oracle.relative_l2(y, oracle.uniform_matvec(s, c, rows, cols, x, 3, 64)) < TOL
+    assert oracle.relative_l2(y, oracle.uniform_matvec_f64(s, c, rows, cols, x, 3, 64)) < TOL
+
+
+@pytest.mark.parametrize("rows,rank,cols", [(2048, 160, 768), (768, 192, 2048), (16, 32, 32)])
+def test_hgravs01_low_rank_two_stage(ctx, oracle, rows, rank, cols):
+    """y = L (R x) through hk_gemv_lowrank vs hgravs01_two_stage_matvec_f32
+    and the FP64 product of the decoded factors; the (16, 32, 32) case is the
+    reference's two-stage test shape with the rank raised to the kernel's
+    32-column granularity (deterministic_matrix factors and input)."""
+    from hawking_amd.organs import HgravS01LowRank
+    say("hgravs01", rows, rank, cols)
+    if rows == 16:
+        Lw = oracle.deterministic_matrix(rows, rank, 3)
+        Rw = oracle.deterministic_matrix(rank, cols, 5)
+        x = oracle.deterministic_input(cols)
+    else:
+        Lw = oracle.normal(oracle.stream_key(U.SEED, 0xE1 + rank), rows * rank, 0.05).reshape(rows, rank)
+        Rw = oracle.normal(oracle.stream_key(U.SEED, 0xE2 + rank), rank * cols, 0.02).reshape(rank, cols)
+        x = oracle.normal(oracle.stream_key(U.SEED, 0xE3 + rank), cols, 1.0)
+    left, (ls, lc) = _u3(ctx, oracle, Lw)
+    right, (rs, rc) = _u3(ctx, oracle, Rw)
+    lr = HgravS01LowRank(left, right)
+    y = lr.matvec(x)
+    ref = oracle.hgravs01_matvec((ls, lc), (rs, rc), rows, rank, cols, x, 3, 64)
+    Ld = oracle.uniform_decode(ls, lc, rows, rank, 3, 64).astype(np.float64)
+    Rd = oracle.uniform_decode(rs, rc, rank, cols, 3, 64).astype(np.float64)
+    y64 = Ld @ (Rd @ x.astype(np.float64))
+    assert oracle.relative_l2(y, ref) < TOL
+    assert oracle.relative_l2(y, y64) < TOL
+
+
+@pytest.mark.parametrize("shape", [(13, 96), (2048, 160)])
+def test_synthetic_u3_factor_matches_oracle_pack(ctx, oracle, shape):
+    """The device generator + 3-bit packer equals the oracle packing the
+    oracle's draws (the bench's synthetic HGRAVS01 factors)."""
+    from hawking_amd._lib import HK_U3
+    from hawking_amd.organs import SyntheticOrgan
+    rows, cols = shape
+    key = oracle.stream_key(U.SEED, 0xD5 + rows)
+    say("synthetic u3", shape)
+    o = SyntheticOrgan(ctx, HK_U3, rows, cols, key, 0, group=64, sigma=0.05)
+    s, c = oracle.uniform_pack(oracle.normal(key, rows * cols, 0.05), rows, cols, 3, 64)
+    assert np.array_equal(o.decode(), oracle.uniform_decode(s, c, rows, cols, 3, 64))
+
+
+def test_u3_and_lowrank_reject_bad_geometry(ctx, oracle):
+    from hawking_amd._lib import HK_E_GEOMETRY, HawkingError
+    from hawking_amd.organs import HgravS01LowRank, UniformFactor3
+    s, c = oracle.uniform_pack(np.ones((16, 8), np.float32), 16, 8, 3, 64)
+    with pytest.raises(HawkingError) as e:        # rank 8: not a multiple of 32 columns
+        UniformFactor3(ctx, s, c, 16, 8)
+    assert e.value.code == HK_E_GEOMETRY
+    s, c = oracle.uniform_pack(np.ones((1, 6176), np.float32), 1, 6176, 3, 64)
+    with pytest.raises(HawkingError) as e:        # past the 3-bit x image's 6144 columns
+        UniformFactor3(ctx, s, c, 1, 6176)
+    assert e.value.code == HK_E_GEOMETRY
+    a, _ = _u3(ctx, oracle, np.ones((16, 64), np.float32))
+    b, _ = _u3(ctx, oracle, np.ones((32, 32), np.float32))
+    with pytest.raises(ValueError):
+        HgravS01LowRank(a, b)
+    mid, xd, yd = ctx.empty(64), ctx.empty(32), ctx.empty(16)
+    with pytest.raises(HawkingError) as e:
+        ctx.call("hk_gemv_lowrank", a.h, b.h, xd.ptr, mid.ptr, yd.ptr, ctx.stream)
+    assert e.value.code == HK_E_GEOMETRY
+
+
 @pytest.mark.parametrize("group,shape", [(64, (96, 1024)), (128, (7, 256)), (32, (1, 7168))])
 def test_q4_other_groups_and_ragged_rows(ctx, oracle, group, shape):
     rows, cols = shape
