@@ -32,7 +32,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
 SEED = 0x48415752
-HK_Q4, HK_BIN, HK_MIXED, HK_F32, HK_Q8, HK_U3 = 0, 1, 2, 3, 4, 5
+HK_Q4, HK_BIN, HK_MIXED, HK_F32, HK_Q8, HK_U3, HK_BIN_RICE = 0, 1, 2, 3, 4, 5, 6
 WORKLOADS = {
     # name: (kind, group, rows, cols, n_organs)
     "binary_512x2048": (HK_BIN, 128, 512, 2048, 8192),
@@ -40,6 +40,7 @@ WORKLOADS = {
     "q4g32_512x2048": (HK_Q4, 32, 512, 2048, 2048),
     "mixed_512x2048": (HK_MIXED, 128, 512, 2048, 6144),
     "q8g64_512x2048": (HK_Q8, 64, 512, 2048, 1024),
+    "binary_rice_512x2048": (HK_BIN_RICE, 128, 512, 2048, 4096),
 }
 
 
@@ -318,7 +319,7 @@ def main():
         rel = spot_check(ctx, oset, x, y)
         log("spot-check rel_l2", rel)
         del oset, x, y
-        for name in ("binary_2048x512", "q4g32_512x2048", "mixed_512x2048", "q8g64_512x2048"):
+        for name in ("binary_2048x512", "q4g32_512x2048", "mixed_512x2048", "q8g64_512x2048", "binary_rice_512x2048"):
             r, bufs = streamed(ctx, name, args.steps, args.warmup)
             del bufs
             extra[name] = {"gbps": round(r["gbps"], 1), "frac_hbm": round(r["gbps"] / HBM_PEAK_GBPS, 4),

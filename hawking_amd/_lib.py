@@ -20,7 +20,7 @@ HK_E_UNSUPPORTED = 5
 HK_E_ROUTE = 6
 HK_E_NOMEM = 7
 
-HK_Q4, HK_BIN, HK_MIXED, HK_F32, HK_Q8, HK_U3 = 0, 1, 2, 3, 4, 5
+HK_Q4, HK_BIN, HK_MIXED, HK_F32, HK_Q8, HK_U3, HK_BIN_RICE = 0, 1, 2, 3, 4, 5, 6
 HK_ROUTER_SOFTMAX, HK_ROUTER_NOAUX_TC = 0, 1
 
 STATUS_NAMES = {
@@ -41,6 +41,15 @@ class OrganSrc(C.Structure):
         ("kind", _i32), ("group", _i32), ("rows", _u32), ("cols", _u32),
         ("scales", _p), ("codes", _p), ("tags", _p), ("q2_scales", _p), ("q2_codes", _p),
         ("n_bin", _u32), ("n_q2", _u32), ("dense", _p),
+    ]
+
+
+class RiceQ1Src(C.Structure):
+    """hk_rice_q1: an HGRAVR02 body (host or device pointers)."""
+    _fields_ = [
+        ("rows", _u32), ("cols", _u32), ("bin_scales", _p), ("bin_signs", _p), ("first_index", _u32),
+        ("rice_k", _u32), ("rice", _p), ("rice_bytes", _sz), ("outlier_count", _sz),
+        ("residual_scale_f16", C.c_uint16), ("residual_signs", _p),
     ]
 
 
@@ -88,6 +97,9 @@ PROTOTYPES = {
                                 C.POINTER(_u32), C.POINTER(_sz)]),
     "hk_gemv": (C.c_int, [_p, _p, _p, _p, _p]),
     "hk_gemv_lowrank": (C.c_int, [_p, _p, _p, _p, _p, _p, _p]),
+    "hk_organ_upload_rice": (C.c_int, [_p, C.POINTER(RiceQ1Src), _p, C.POINTER(_p)]),
+    "hk_rice_apply": (C.c_int, [_p, _p, _p, _p, _p]),
+    "hk_pack_binary_rice": (C.c_int, [_p, _p, _u32, _u32, C.c_double, _p, _p, _p, _p, _sz, C.POINTER(RiceQ1Src), _p]),
     "hk_gemv_batch": (C.c_int, [_p, C.POINTER(_p), _u32, _p, _sz, _p, _sz, _p]),
     "hk_decode_rows": (C.c_int, [_p, _p, _u32, _u32, _p, _p]),
     "hk_organ_set_create": (C.c_int, [_p, C.POINTER(_p), _u32, C.POINTER(_p)]),

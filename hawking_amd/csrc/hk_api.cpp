@@ -23,6 +23,9 @@ using hk::CanonView;
 struct hk_organ {
     hk::OrganView view{};
     int32_t kind = 0;          // the canonical kind it was uploaded as (view.kind is the engine's)
+    hk::ResView res{};         // HGRAVR02 residual (res_dev non-null when present)
+    void* res_mem = nullptr;
+    const hk::ResView* res_dev = nullptr;
     void* view_dev = nullptr;  // device copy of `view` for single-organ launches
     void* mem = nullptr;
     size_t alloc_bytes = 0;
@@ -65,6 +68,12 @@ int ensure_scratch(hk_ctx* ctx, size_t bytes, void** out) {
 static inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 static inline bool f16_finite(uint16_t b) { return (b & 0x7C00u) != 0x7C00u; }
+// Exact value of a finite f16.
+static float f16_to_f32_host(uint16_t h) {
+    const uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    const float v = e == 0 ? std::ldexp((float)m, -24) : std::ldexp((float)(m | 0x400u), (int)e - 25);
+    return (h & 0x8000u) ? -v : v;
+}
 
 static int popcount8(uint8_t v) { return __builtin_popcount(v); }
 
@@ -108,6 +117,8 @@ static int validate_shape(hk_ctx* ctx, int kind, int group, uint32_t rows, uint3
     case HK_F32:
         if (cols % 4) return set_error(ctx, HK_E_GEOMETRY, "dense organs require cols % 4 == 0");
         return HK_OK;
+    case HK_BIN_RICE:
+        return set_error(ctx, HK_E_UNSUPPORTED, "HGRAVR02 organs are uploaded with hk_organ_upload_rice");
     default:
         return set_error(ctx, HK_E_UNSUPPORTED, "unknown organ kind " + std::to_string(kind));
     }
@@ -485,6 +496,7 @@ extern "C" int hk_organ_free(hk_ctx* ctx, hk_organ* o) {
     if (!o) return HK_OK;
     int rc = check_hip(ctx, hipFree(o->mem), "hipFree (organ)");
     if (o->view_dev) (void)hipFree(o->view_dev);
+    if (o->res_mem) (void)hipFree(o->res_mem);
     delete o;
     return rc;
 }
@@ -523,8 +535,20 @@ extern "C" int hk_gemv(hk_ctx* ctx, const hk_organ* o, const float* x, float* y,
         rc = check_hip(ctx, hipMemcpy(m->view_dev, &m->view, sizeof(OrganView), hipMemcpyHostToDevice), "descriptor upload");
         if (rc) return rc;
     }
-    return check_hip(ctx, launch_gemv_tiled(static_cast<const OrganView*>(o->view_dev), 1, o->view, x, 0, y, 0, st),
-                     "gemv launch");
+    rc = check_hip(ctx, launch_gemv_tiled(static_cast<const OrganView*>(o->view_dev), 1, o->view, x, 0, y, 0, st),
+                   "gemv launch");
+    if (!rc && o->res_dev) rc = check_hip(ctx, launch_rice_apply(o->res_dev, 1, o->view.rows, o->view.cols, x, 0, y, 0, st), "rice apply");
+    return rc;
+}
+
+extern "C" int hk_rice_apply(hk_ctx* ctx, const hk_organ* o, const float* x, float* y, hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (!o || !o->res_dev) return set_error(ctx, HK_E_INVALID_ARG, "hk_rice_apply: not an HGRAVR02 organ");
+    int rc = check_vectors(ctx, "hk_rice_apply", x, 0, y, 0, 1, o->view);
+    if (rc) return rc;
+    return check_hip(ctx, launch_rice_apply(o->res_dev, 1, o->view.rows, o->view.cols, x, 0, y, 0,
+                                            static_cast<hipStream_t>(stream)),
+                     "rice apply");
 }
 
 extern "C" int hk_gemv_lowrank(hk_ctx* ctx, const hk_organ* left, const hk_organ* right, const float* x, float* mid,
@@ -543,6 +567,7 @@ extern "C" int hk_gemv_lowrank(hk_ctx* ctx, const hk_organ* left, const hk_organ
 
 struct hk_organ_set {
     OrganView* dev = nullptr;
+    ResView* res_dev = nullptr;  // HGRAVR02 sets: the residual table
     uint32_t n = 0;
     OrganView first{};
 };
@@ -557,7 +582,7 @@ extern "C" int hk_organ_set_create(hk_ctx* ctx, const hk_organ* const* organs, u
         if (!organs[i]) return set_error(ctx, HK_E_INVALID_ARG, "organ set: NULL organ");
         views[i] = organs[i]->view;
         if (views[i].kind != views[0].kind || views[i].rows != views[0].rows || views[i].cols != views[0].cols ||
-            views[i].group != views[0].group)
+            views[i].group != views[0].group || organs[i]->kind != organs[0]->kind)
             return set_error(ctx, HK_E_GEOMETRY, "organ set: organs must share kind and shape");
     }
     hk_organ_set* set = new hk_organ_set();
@@ -572,6 +597,23 @@ extern "C" int hk_organ_set_create(hk_ctx* ctx, const hk_organ* const* organs, u
         delete set;
         return rc;
     }
+    if (organs[0]->res_dev) {
+        std::vector<ResView> res(n);
+        for (uint32_t i = 0; i < n; ++i) res[i] = organs[i]->res;
+        if (hipMalloc(&set->res_dev, n * sizeof(ResView)) != hipSuccess) {
+            (void)hipFree(set->dev);
+            delete set;
+            return set_error(ctx, HK_E_NOMEM, "organ set allocation failed");
+        }
+        rc = check_hip(ctx, hipMemcpy(set->res_dev, res.data(), n * sizeof(ResView), hipMemcpyHostToDevice),
+                       "organ set upload");
+        if (rc) {
+            (void)hipFree(set->dev);
+            (void)hipFree(set->res_dev);
+            delete set;
+            return rc;
+        }
+    }
     set->n = n;
     set->first = views[0];
     *out = set;
@@ -582,6 +624,7 @@ extern "C" int hk_organ_set_free(hk_ctx* ctx, hk_organ_set* set) {
     if (!ctx) return HK_E_INVALID_ARG;
     if (!set) return HK_OK;
     int rc = check_hip(ctx, hipFree(set->dev), "hipFree (organ set)");
+    if (set->res_dev) (void)hipFree(set->res_dev);
     delete set;
     return rc;
 }
@@ -592,10 +635,14 @@ extern "C" int hk_gemv_set(hk_ctx* ctx, const hk_organ_set* set, const float* x,
     if (!set) return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv_set: NULL set");
     int rc = check_vectors(ctx, "hk_gemv_set", x, x_stride, y, y_stride, set->n, set->first);
     if (rc) return rc;
-    return check_hip(ctx,
-                     launch_gemv_tiled(set->dev, set->n, set->first, x, x_stride, y, y_stride,
-                                       static_cast<hipStream_t>(stream)),
-                     "gemv_set launch");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    rc = check_hip(ctx, launch_gemv_tiled(set->dev, set->n, set->first, x, x_stride, y, y_stride, st),
+                   "gemv_set launch");
+    if (!rc && set->res_dev)
+        rc = check_hip(ctx, launch_rice_apply(set->res_dev, set->n, set->first.rows, set->first.cols, x, x_stride, y,
+                                              y_stride, st),
+                       "rice apply");
+    return rc;
 }
 
 extern "C" int hk_gemv_batch(hk_ctx* ctx, const hk_organ* const* organs, uint32_t n, const float* x,
@@ -610,10 +657,40 @@ extern "C" int hk_gemv_batch(hk_ctx* ctx, const hk_organ* const* organs, uint32_
     return rc ? rc : rc2;
 }
 
+static int upload_rice(hk_ctx* ctx, const hk_rice_q1* s, hipStream_t st, hk_organ** out);
+
+// Synthetic HGRAVR02 organ: weights from the generator, the device packer at
+// the shipped 2% outlier ratio, then the ordinary upload.
+static int synthetic_rice(hk_ctx* ctx, uint32_t rows, uint32_t cols, uint64_t key, float sigma, hipStream_t st,
+                          hk_organ** out) {
+    if (rows == 0 || cols == 0 || cols % 128 || (uint64_t)rows * cols > 0x7FFFFFFFull)
+        return set_error(ctx, HK_E_GEOMETRY, "synthetic HGRAVR02 organs need cols % 128 == 0 and rows * cols < 2^31");
+    const size_t n = (size_t)rows * cols, count = (size_t)std::ceil((double)n * 0.02);
+    const size_t a_w = align256(n * 4), a_s = align256(n / 128 * 2), a_g = align256(n / 8),
+                 a_r = align256((count + 7) / 8), cap = align256(n / 8 + 17 * count / 8 + 64);
+    uint8_t* m = nullptr;
+    if (hipMalloc(&m, a_w + a_s + a_g + a_r + cap) != hipSuccess)
+        return set_error(ctx, HK_E_NOMEM, "synthetic staging allocation failed");
+    float* w = reinterpret_cast<float*>(m);
+    hk_rice_q1 src{};
+    int rc = check_hip(ctx, launch_synth_normal(key, 0, n, sigma, w, st), "synth launch");
+    if (!rc)
+        rc = hk_pack_binary_rice(ctx, w, rows, cols, 0.02, reinterpret_cast<uint16_t*>(m + a_w), m + a_w + a_s,
+                                 m + a_w + a_s + a_g, m + a_w + a_s + a_g + a_r, cap, &src, st);
+    if (!rc) rc = upload_rice(ctx, &src, st, out);
+    (void)hipStreamSynchronize(st);
+    (void)hipFree(m);
+    return rc;
+}
+
 extern "C" int hk_organ_synthetic(hk_ctx* ctx, int32_t kind, int32_t group, uint32_t rows, uint32_t cols, uint64_t key,
                                   uint64_t coin_key, float sigma, hk_stream stream, hk_organ** out) {
     if (!ctx || !out) return HK_E_INVALID_ARG;
     *out = nullptr;
+    if (kind == HK_BIN_RICE) {
+        int rc = validate_gemv_cols(ctx, HK_BIN, cols);
+        return rc ? rc : synthetic_rice(ctx, rows, cols, key, sigma, static_cast<hipStream_t>(stream), out);
+    }
     if (kind == HK_BIN || kind == HK_MIXED) group = 128;
     if (kind == HK_Q8 || kind == HK_U3) group = 64;
     int rc = validate_shape(ctx, kind, group, rows, cols);
@@ -673,13 +750,145 @@ extern "C" int hk_organ_synthetic(hk_ctx* ctx, int32_t kind, int32_t group, uint
     return rc;
 }
 
+// Rice expand into the CSR the apply reads (unpack_rice + expand_rice_indices +
+// rice_q1_row_ptr, q80_mixed_decode.rs:348-381,462-507), on the host at bind
+// time as the reference's parse does.  recs is padded with zeros to a multiple
+// of 8 (the apply reads 16-byte pieces).  Returns "" or the error.
+static std::string rice_expand_csr(const uint8_t* rice, size_t len, uint32_t first, uint32_t k, size_t count,
+                                   uint32_t rows, uint32_t cols, const uint8_t* signs, std::vector<uint32_t>& row_ptr,
+                                   std::vector<uint16_t>& recs) {
+    const uint64_t limit = (uint64_t)rows * cols;
+    row_ptr.assign((size_t)rows + 1, 0u);
+    recs.assign((count + 7) & ~(size_t)7, 0u);
+    auto put = [&](size_t i, uint64_t f) {
+        recs[i] = (uint16_t)((f % cols) | ((uint32_t)((signs[i >> 3] >> (i & 7u)) & 1u) << 15));
+        row_ptr[f / cols + 1] += 1;
+    };
+    if (first >= limit) return "rice residual index out of range";
+    put(0, first);
+    uint64_t pos = 0, acc = first;
+    const uint64_t end = (uint64_t)len * 8u;
+    for (size_t i = 1; i < count; ++i) {
+        uint64_t q = 0;
+        for (;;) {
+            if (pos >= end) return "rice stream overran its payload";
+            const uint32_t b = (rice[pos >> 3] >> (pos & 7u)) & 1u;
+            ++pos;
+            if (!b) break;
+            if (++q > 0xFFFFFFFFull) return "rice quotient overflow";
+        }
+        uint32_t rem = 0;
+        for (uint32_t b = 0; b < k; ++b, ++pos) {
+            if (pos >= end) return "rice stream overran its payload";
+            rem |= (uint32_t)((rice[pos >> 3] >> (pos & 7u)) & 1u) << b;
+        }
+        acc += (uint64_t)((uint32_t)(q << k) | rem);
+        if (acc > 0xFFFFFFFFull) return "rice index exceeds u32";
+        if (acc >= limit) return "rice residual index out of range";
+        put(i, acc);
+    }
+    for (uint32_t r = 0; r < rows; ++r) row_ptr[r + 1] += row_ptr[r];
+    return "";
+}
+
+// Bind of an HGRAVR02 body: base repack on the device, Rice expand + CSR.
+static int upload_rice(hk_ctx* ctx, const hk_rice_q1* s, hipStream_t st, hk_organ** out) {
+    const size_t n = (size_t)s->rows * s->cols, count = s->outlier_count;
+    const size_t sign_bytes = (count + 7) / 8;
+    // the stream and signs on the host (the pointers may be device memory)
+    std::vector<uint8_t> rice(s->rice_bytes), signs(sign_bytes);
+    int rc = HK_OK;
+    if (s->rice_bytes)
+        rc = check_hip(ctx, hipMemcpy(rice.data(), s->rice, s->rice_bytes, hipMemcpyDefault), "rice stream read");
+    if (!rc) rc = check_hip(ctx, hipMemcpy(signs.data(), s->residual_signs, sign_bytes, hipMemcpyDefault), "sign read");
+    if (rc) return rc;
+    std::vector<uint32_t> row_ptr;
+    std::vector<uint16_t> recs;
+    const std::string err = rice_expand_csr(rice.data(), rice.size(), s->first_index, s->rice_k, count, s->rows, s->cols,
+                                            signs.data(), row_ptr, recs);
+    if (!err.empty()) return set_error(ctx, HK_E_GEOMETRY, err);
+
+    const Layout L = layout_for(HK_BIN, 128, s->rows, s->cols, 0, 0);
+    uint8_t* stage = nullptr;
+    if (hipMalloc(&stage, L.total() + 256) != hipSuccess) return set_error(ctx, HK_E_NOMEM, "staging allocation failed");
+    CanonView canon = place(HK_BIN, 128, s->rows, s->cols, L, stage);
+    uint32_t* status = reinterpret_cast<uint32_t*>(stage + L.total());
+    uint32_t hst = 0;
+    rc = check_hip(ctx, hipMemsetAsync(status, 0, 4, st), "hipMemsetAsync");
+    if (!rc)
+        rc = check_hip(ctx, hipMemcpyAsync(const_cast<uint16_t*>(canon.scales), s->bin_scales, L.scales, hipMemcpyDefault, st),
+                       "hipMemcpyAsync (HGRAVR02 upload)");
+    if (!rc)
+        rc = check_hip(ctx, hipMemcpyAsync(const_cast<uint8_t*>(canon.codes), s->bin_signs, L.codes, hipMemcpyDefault, st),
+                       "hipMemcpyAsync (HGRAVR02 upload)");
+    if (!rc) rc = check_hip(ctx, launch_f16_check(canon.scales, n / 128, status, st), "scale check");
+    if (!rc) rc = check_hip(ctx, hipMemcpyAsync(&hst, status, 4, hipMemcpyDeviceToHost, st), "status read");
+    if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "hipStreamSynchronize (HGRAVR02 upload)");
+    if (!rc && hst) rc = set_error(ctx, HK_E_NONFINITE, "HGRAVR02 binary scale is not a finite FP16");
+    hk_organ* o = nullptr;
+    if (!rc) rc = repack_into_organ(ctx, canon, 0, 0, st, &o);
+    if (!rc) {
+        const size_t a_rp = align256(row_ptr.size() * 4), a_rec = align256(recs.size() * 2);
+        if (hipMalloc(&o->res_mem, a_rp + a_rec + sizeof(ResView)) != hipSuccess) {
+            rc = set_error(ctx, HK_E_NOMEM, "residual allocation failed");
+        } else {
+            uint8_t* m = static_cast<uint8_t*>(o->res_mem);
+            o->res.row_ptr = reinterpret_cast<const uint32_t*>(m);
+            o->res.recs = reinterpret_cast<const uint16_t*>(m + a_rp);
+            o->res.rows = s->rows;
+            o->res.cols = s->cols;
+            o->res.scale = f16_to_f32_host(s->residual_scale_f16);
+            o->res.count = (uint32_t)count;
+            ResView* rd = reinterpret_cast<ResView*>(m + a_rp + a_rec);
+            rc = check_hip(ctx, hipMemcpy(m, row_ptr.data(), row_ptr.size() * 4, hipMemcpyHostToDevice), "row_ptr upload");
+            if (!rc) rc = check_hip(ctx, hipMemcpy(m + a_rp, recs.data(), recs.size() * 2, hipMemcpyHostToDevice), "record upload");
+            if (!rc) rc = check_hip(ctx, hipMemcpy(rd, &o->res, sizeof(ResView), hipMemcpyHostToDevice), "residual upload");
+            o->res_dev = rd;
+        }
+        o->kind = HK_BIN_RICE;
+        o->packed_bytes = n / 8 + n / 128 * 2 + 4 + s->rice_bytes + 2 + sign_bytes;
+        if (rc) {
+            (void)hk_organ_free(ctx, o);
+            o = nullptr;
+        }
+    }
+    (void)hipStreamSynchronize(st);
+    (void)hipFree(stage);
+    if (!rc) *out = o;
+    return rc;
+}
+
+extern "C" int hk_organ_upload_rice(hk_ctx* ctx, const hk_rice_q1* s, hk_stream stream, hk_organ** out) {
+    if (!ctx || !out) return HK_E_INVALID_ARG;
+    *out = nullptr;
+    if (!s) return set_error(ctx, HK_E_INVALID_ARG, "hk_organ_upload_rice: NULL source");
+    if (s->rows == 0 || s->cols == 0 || s->cols % 128)
+        return set_error(ctx, HK_E_GEOMETRY, "HGRAVR02 organs require rows > 0 and cols % 128 == 0");
+    if (s->cols >= 32768) return set_error(ctx, HK_E_GEOMETRY, "HGRAVR02 organs require cols < 32768");
+    if ((uint64_t)s->rows * s->cols > 0xFFFFFFFFull)
+        return set_error(ctx, HK_E_GEOMETRY, "HGRAVR02 flat indices are u32: rows * cols too large");
+    int rc = validate_gemv_cols(ctx, HK_BIN, s->cols);
+    if (rc) return rc;
+    if (s->outlier_count == 0) return set_error(ctx, HK_E_GEOMETRY, "rice residual requires at least one outlier");
+    if (s->outlier_count > (size_t)s->rows * s->cols)
+        return set_error(ctx, HK_E_GEOMETRY, "outlier_count exceeds rows * cols");
+    if (s->rice_k > 31) return set_error(ctx, HK_E_GEOMETRY, "rice_k must be below 32");
+    if (!s->bin_scales || !s->bin_signs || !s->residual_signs || (s->outlier_count > 1 && s->rice_bytes && !s->rice))
+        return set_error(ctx, HK_E_INVALID_ARG, "HGRAVR02 streams are NULL");
+    if ((s->residual_scale_f16 & 0x7C00u) == 0x7C00u)
+        return set_error(ctx, HK_E_NONFINITE, "HGRAVR02 residual scale is not a finite FP16");
+    return upload_rice(ctx, s, static_cast<hipStream_t>(stream), out);
+}
+
 extern "C" int hk_decode_rows(hk_ctx* ctx, const hk_organ* o, uint32_t row0, uint32_t nrows, float* out,
                               hk_stream stream) {
     if (!ctx) return HK_E_INVALID_ARG;
     if (!o || !out) return set_error(ctx, HK_E_INVALID_ARG, "hk_decode_rows: NULL argument");
     if ((uint64_t)row0 + nrows > o->view.rows) return set_error(ctx, HK_E_GEOMETRY, "hk_decode_rows: rows out of range");
-    return check_hip(ctx, launch_decode_rows(o->view, row0, nrows, out, static_cast<hipStream_t>(stream)),
-                     "decode launch");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int rc = check_hip(ctx, launch_decode_rows(o->view, row0, nrows, out, st), "decode launch");
+    if (!rc && o->res_dev) rc = check_hip(ctx, launch_rice_decode_add(o->res, row0, nrows, out, st), "rice decode");
+    return rc;
 }
 
 // ====================================================================== packers / generator
@@ -754,6 +963,43 @@ extern "C" int hk_pack_u3(hk_ctx* ctx, const float* w, size_t count, uint16_t* s
     int rc;
     if ((rc = pack_prologue(ctx, st, &bad))) return rc;
     return finish_pack(ctx, st, bad, launch_pack_u3(w, count, scales, codes, bad, st));
+}
+
+extern "C" int hk_pack_binary_rice(hk_ctx* ctx, const float* w, uint32_t rows, uint32_t cols, double ratio,
+                                   uint16_t* bin_scales, uint8_t* bin_signs, uint8_t* residual_signs, uint8_t* rice,
+                                   size_t rice_cap, hk_rice_q1* out, hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (!out) return set_error(ctx, HK_E_INVALID_ARG, "hk_pack_binary_rice: NULL out");
+    if (rows == 0 || cols == 0 || cols % 128)
+        return set_error(ctx, HK_E_GEOMETRY, "hk_pack_binary_rice: rows > 0 and cols % 128 == 0 required");
+    if ((uint64_t)rows * cols > 0x7FFFFFFFull)
+        return set_error(ctx, HK_E_GEOMETRY, "hk_pack_binary_rice: rows * cols must stay below 2^31");
+    if (!(ratio > 0.0 && ratio <= 0.1))
+        return set_error(ctx, HK_E_INVALID_ARG, "rice_q1 outlier ratio must be in (0, 0.1]");
+    if (!w || !bin_scales || !bin_signs || !residual_signs || !rice || !aligned16(rice) || !aligned16(w))
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_pack_binary_rice: NULL or misaligned pointer");
+    RicePackResult r{};
+    const hipError_t e = pack_binary_rice_device(w, rows, cols, ratio, bin_scales, bin_signs, residual_signs, rice,
+                                                 rice_cap, &r, static_cast<hipStream_t>(stream));
+    *out = hk_rice_q1{};
+    out->rows = rows;
+    out->cols = cols;
+    out->bin_scales = bin_scales;
+    out->bin_signs = bin_signs;
+    out->first_index = r.first;
+    out->rice_k = r.k;
+    out->rice = r.count > 1 ? rice : nullptr;
+    out->rice_bytes = r.rice_bytes;
+    out->outlier_count = r.count;
+    out->residual_scale_f16 = r.scale;
+    out->residual_signs = residual_signs;
+    if (e == hipErrorInvalidValue && r.rice_bytes)
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_pack_binary_rice: rice_cap below the " +
+                                                    std::to_string(((r.rice_bytes + 3) / 4) * 4) + " bytes needed");
+    int rc = check_hip(ctx, e, "pack_binary_rice");
+    if (rc) return rc;
+    if (r.bad) return set_error(ctx, HK_E_NONFINITE, "source tensor contains a non-finite value or scale");
+    return HK_OK;
 }
 
 extern "C" int hk_pack_q2(hk_ctx* ctx, const float* w, size_t count, uint16_t* scales, uint8_t* codes,

@@ -61,16 +61,6 @@ __host__ __device__ constexpr size_t gemv_hdr_offset(uint32_t steps) {
 // branch-free in memory operations (refetches are unconditional, past the end
 // they re-read the last item; y goes out through LDS after the loop) so the
 // compiler can wait for exactly the slot being consumed.
-// Workgroup -> (organ, part).  Workgroups are dispatched to the 8 XCDs round
-// robin by linear id, so ids 8 apart share an XCD and its L2: each run of
-// 8 * parts ids covers 8 organs with id % 8 selecting the organ, and all
-// parts of an organ (which read the same x) land on one XCD.
-__device__ __forceinline__ void organ_part(uint32_t L, uint32_t parts, uint32_t n, uint32_t* organ, uint32_t* part) {
-    const uint32_t c = L / (8u * parts), r = L % (8u * parts), g = min(8u, n - 8u * c);
-    *organ = 8u * c + r % g;
-    *part = r / g;
-}
-
 template <int KIND, int R, int D, int NC>
 __global__ void __launch_bounds__(256)
 gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const float* __restrict__ xall,

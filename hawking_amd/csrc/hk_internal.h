@@ -110,6 +110,16 @@ __device__ __forceinline__ void copy16_to_lds(uint4* dst, const uint4* src, uint
     }
 }
 
+// Workgroup -> (organ, part).  Workgroups are dispatched to the 8 XCDs round
+// robin by linear id, so ids 8 apart share an XCD and its L2: each run of
+// 8 * parts ids covers 8 organs with id % 8 selecting the organ, and all
+// parts of an organ (which read the same x) land on one XCD.
+__device__ __forceinline__ void organ_part(uint32_t L, uint32_t parts, uint32_t n, uint32_t* organ, uint32_t* part) {
+    const uint32_t c = L / (8u * parts), r = L % (8u * parts), g = min(8u, n - 8u * c);
+    *organ = 8u * c + r % g;
+    *part = r / g;
+}
+
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
     return static_cast<float>(__builtin_bit_cast(_Float16, b));
 }
@@ -210,6 +220,35 @@ struct RepackJob {
     uint32_t* counts;
 };
 hipError_t launch_repack_batch(int kind, const RepackJob* jobs_dev, uint32_t n, size_t max_items, hipStream_t s);
+// The residual of an HGRAVR02 organ on the device: CSR over its outliers
+// (row_ptr[rows + 1]; recs[count] = column | sign << 15, sign 1 = +scale).
+struct ResView {
+    const uint32_t* row_ptr;
+    const uint16_t* recs;
+    uint32_t rows, cols;
+    float scale;
+    uint32_t count;
+};
+// status |= 16 if any of the n f16 values is not finite.
+hipError_t launch_f16_check(const uint16_t* v, size_t n, uint32_t* status, hipStream_t s);
+// Adds the outliers of rows [row0, row0 + nrows) to a decoded base.
+hipError_t launch_rice_decode_add(const ResView& v, uint32_t row0, uint32_t nrows, float* out, hipStream_t s);
+// y_i += R_i x_i for n residuals of one shape (table in device memory).
+hipError_t launch_rice_apply(const ResView* res_dev, uint32_t n, uint32_t rows, uint32_t cols, const float* x,
+                             size_t x_stride, float* y, size_t y_stride, hipStream_t s);
+// Device packer (pack_binary_rice_q1): fills the canonical device buffers
+// and the host scalars; returns hipErrorInvalidValue if rice_cap is short
+// (*rice_bytes then holds the size needed).
+struct RicePackResult {
+    uint32_t first, k;
+    size_t count, rice_bytes;
+    uint16_t scale;
+    uint32_t bad;  // non-finite input
+};
+hipError_t pack_binary_rice_device(const float* w, uint32_t rows, uint32_t cols, double ratio, uint16_t* bin_scales,
+                                   uint8_t* bin_signs, uint8_t* res_signs, uint8_t* rice, size_t rice_cap,
+                                   RicePackResult* out, hipStream_t s);
+
 // Device bytes of the tiled layout (sections 256-B aligned); mixed needs n_bin/n_q2.
 size_t tiled_bytes(int kind, int group, uint32_t rows, uint32_t cols, uint32_t n_bin, uint32_t n_q2,
                    size_t* packed_bytes);

@@ -10,6 +10,8 @@ Reference names are kept where the reference has them:
     (HGRAVU01, q80_mixed_decode.rs:529-612,1047-1070)
   * HGRAVS01 low-rank: two 3-bit uniform factors and
     hgravs01_two_stage_matvec_f32 (q80_mixed_decode.rs:614-629,1019-1046)
+  * RiceQ1Packed + binary_rice_q1_matvec_f32 (HGRAVR02: binary base plus a
+    Rice-coded 1-bit residual, q80_mixed_decode.rs:60-69,383-527)
 Every matvec runs the gfx950 kernels through the C ABI; the inputs are the
 reference's canonical packed bytes, uploaded and repacked once.
 """
@@ -20,7 +22,7 @@ import ctypes as C
 import numpy as np
 
 from . import _lib
-from ._lib import HK_BIN, HK_F32, HK_MIXED, HK_Q4, HK_Q8, HK_U3, OrganSrc
+from ._lib import HK_BIN, HK_BIN_RICE, HK_F32, HK_MIXED, HK_Q4, HK_Q8, HK_U3, OrganSrc, RiceQ1Src
 from .runtime import Context, DeviceArray
 
 
@@ -185,6 +187,66 @@ class HgravS01LowRank:
 def hgravs01_two_stage_matvec_f32(packed: HgravS01LowRank, x: np.ndarray) -> np.ndarray:
     """GPU counterpart of hgravs01_two_stage_matvec_f32 (q80_mixed_decode.rs:614-629)."""
     return packed.matvec(x)
+
+
+class RiceQ1Packed(PackedOrgan):
+    """HGRAVR02 organ from its canonical body: binary group-128 base
+    (bin_scales, bin_signs), first_index + Rice(gaps) with rice_k, one sign
+    bit per outlier and the f16 residual scale.  matvec = base + residual."""
+
+    kind = HK_BIN_RICE
+
+    def __init__(self, ctx: Context, rows: int, cols: int, bin_scales: np.ndarray, bin_signs: np.ndarray,
+                 first_index: int, rice_k: int, rice: np.ndarray, outlier_count: int, residual_scale_f16: int,
+                 residual_signs: np.ndarray):
+        arrs = [np.ascontiguousarray(a, dt) for a, dt in
+                ((bin_scales, np.uint16), (bin_signs, np.uint8), (rice, np.uint8), (residual_signs, np.uint8))]
+        bs, bg, rc, sg = arrs
+        src = RiceQ1Src(rows=rows, cols=cols, bin_scales=_ptr(bs), bin_signs=_ptr(bg), first_index=first_index,
+                        rice_k=rice_k, rice=_ptr(rc) if rc.size else None, rice_bytes=rc.size,
+                        outlier_count=outlier_count, residual_scale_f16=residual_scale_f16,
+                        residual_signs=_ptr(sg))
+        self._upload_rice(ctx, src)
+
+    @classmethod
+    def from_device(cls, ctx: Context, src: RiceQ1Src) -> "RiceQ1Packed":
+        """An organ from a body already in device memory (hk_pack_binary_rice's output)."""
+        self = cls.__new__(cls)
+        self._upload_rice(ctx, src)
+        return self
+
+    def _upload_rice(self, ctx: Context, src: RiceQ1Src) -> None:
+        self.ctx = ctx
+        h = C.c_void_p()
+        ctx.call("hk_organ_upload_rice", C.byref(src), ctx.stream, C.byref(h))
+        self.h = h
+        self.rows, self.cols, self.group = int(src.rows), int(src.cols), 128
+        self.outlier_count = int(src.outlier_count)
+        sz = C.c_size_t()
+        ctx.check("hk_organ_info", ctx.L.hk_organ_info(h, None, None, None, None, C.byref(sz)))
+        self.packed_bytes = int(sz.value)
+
+    def apply_residual_device(self, x: DeviceArray, y: DeviceArray, stream=None) -> None:
+        """y += residual x (the outliers of each row in index order)."""
+        self.ctx.call("hk_rice_apply", self.h, x.ptr, y.ptr, stream if stream is not None else self.ctx.stream)
+
+
+def binary_rice_q1_matvec_f32(packed: RiceQ1Packed, x: np.ndarray) -> np.ndarray:
+    """GPU counterpart of binary_rice_q1_matvec_f32 (q80_mixed_decode.rs:509-527)."""
+    return packed.matvec(x)
+
+
+def pack_binary_rice_device(ctx: Context, w: DeviceArray, rows: int, cols: int, ratio: float = 0.02):
+    """pack_binary_rice_q1 on the device: returns (RiceQ1Src with device
+    pointers, the device buffers keeping them alive)."""
+    n = rows * cols
+    count = max(1, min(n, int(np.ceil(n * ratio))))
+    bufs = (ctx.empty(n // 128, np.uint16), ctx.empty(n // 8, np.uint8), ctx.empty((count + 7) // 8, np.uint8),
+            ctx.empty(((n + 17 * count) // 8 + 64) // 4 * 4, np.uint8))
+    out = RiceQ1Src()
+    ctx.call("hk_pack_binary_rice", w.ptr, rows, cols, ratio, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, bufs[3].ptr,
+             bufs[3].nbytes, C.byref(out), ctx.stream)
+    return out, bufs
 
 
 class MixedPackedTensor(PackedOrgan):

@@ -49,6 +49,8 @@ extern "C" {
 #define HK_MIXED 2 /* per-128-group binary | Q2 (two f16 scales per 64) */
 #define HK_F32 3   /* dense row-major f32 (router, shared-expert gate) */
 #define HK_Q8 4    /* uniform 8-bit, group 64, f16 scale per group (HGRAVU01) */
+#define HK_BIN_RICE 6 /* binary group-128 base + Rice-coded 1-bit residual (HGRAVR02);
+                         uploaded with hk_organ_upload_rice */
 #define HK_U3 5    /* uniform 3-bit, flat groups of 64 (HGRAVS01 low-rank factors);
                       runs on the Q4 engine (nibble = code + 5) */
 
@@ -132,6 +134,39 @@ typedef struct hk_organ_src {
  * of every scale.  Synchronous with respect to `stream`'s prior work. */
 int hk_organ_upload(hk_ctx* ctx, const hk_organ_src* src, hk_stream stream, hk_organ** out);
 int hk_organ_free(hk_ctx* ctx, hk_organ* organ);
+
+/* HGRAVR02 rice_q1_rms body (RiceQ1Packed, q80_mixed_decode.rs:60-69): the
+ * binary group-128 base, the outliers' flat indices as `first_index` then
+ * Rice-coded gaps (parameter rice_k, LSB-first), one sign bit per outlier
+ * (1 = +scale) and one f16 scale.  Pointers may be host or device memory. */
+typedef struct hk_rice_q1 {
+    uint32_t rows;
+    uint32_t cols;                /* multiple of 128, below 32768 */
+    const uint16_t* bin_scales;   /* rows*cols/128 */
+    const uint8_t* bin_signs;     /* rows*cols/8 */
+    uint32_t first_index;
+    uint32_t rice_k;
+    const uint8_t* rice;          /* rice_bytes (NULL when outlier_count == 1) */
+    size_t rice_bytes;
+    size_t outlier_count;         /* >= 1 */
+    uint16_t residual_scale_f16;
+    const uint8_t* residual_signs; /* (outlier_count + 7) / 8 */
+} hk_rice_q1;
+
+/* Upload of an HGRAVR02 organ: the base is repacked like a binary organ; the
+ * Rice stream is expanded once on the device into a CSR over rows
+ * (expand_rice_indices + rice_q1_row_ptr, q80_mixed_decode.rs:462-507, and
+ * the bind of parse_rice_q1_container, 868-946).  Errors: HK_E_GEOMETRY for
+ * a stream that overruns its bytes, a quotient or index above u32, or an index
+ * past rows*cols; HK_E_NONFINITE for a non-finite scale.  hk_gemv /
+ * hk_gemv_set on the organ compute base + residual
+ * (binary_rice_q1_matvec_f32, q80_mixed_decode.rs:509-527). */
+int hk_organ_upload_rice(hk_ctx* ctx, const hk_rice_q1* src, hk_stream stream, hk_organ** out);
+
+/* y += (residual of an HGRAVR02 organ) x, adding each row's outliers in index
+ * order: the residual half of binary_rice_q1_matvec_f32 and of
+ * q80_sparse_q1_apply_csr (shaders/q80_mixed_decode.metal:155-181). */
+int hk_rice_apply(hk_ctx* ctx, const hk_organ* organ, const float* x, float* y, hk_stream stream);
 int hk_organ_info(const hk_organ* organ, int32_t* kind, int32_t* group, uint32_t* rows,
                   uint32_t* cols, size_t* packed_bytes);
 
@@ -168,7 +203,8 @@ int hk_gemv_lowrank(hk_ctx* ctx, const hk_organ* left, const hk_organ* right, co
 /* Bit-exact decode probe: out[nrows*cols] = decoded weights of rows
  * [row0, row0+nrows).  Replaces qwen_uniform_q4_decode_vector
  * (shaders/qwen_uniform_q4.metal:627) and gather_row
- * (model/qwen80_uniform_q4_hybrid_decode.rs:900-911). */
+ * (model/qwen80_uniform_q4_hybrid_decode.rs:900-911).  An HGRAVR02 organ
+ * decodes to its base plus +-scale at each outlier. */
 int hk_decode_rows(hk_ctx* ctx, const hk_organ* organ, uint32_t row0, uint32_t nrows,
                    float* out, hk_stream stream);
 
@@ -190,6 +226,16 @@ int hk_pack_q8(hk_ctx* ctx, const float* w, uint32_t rows, uint32_t cols, uint16
  * codes 24 bytes per group (16-byte aligned). */
 int hk_pack_u3(hk_ctx* ctx, const float* w, size_t count, uint16_t* scales, uint8_t* codes,
                hk_stream stream);
+/* pack_binary_rice_q1 (q80_mixed_decode.rs:383-460) on the device: w
+ * (device, rows x cols, cols % 128 == 0) -> bin_scales [rows*cols/128],
+ * bin_signs [rows*cols/8], residual_signs [(count+7)/8] and the Rice stream in
+ * rice (16-byte aligned, rice_cap bytes; the writer needs the stream rounded
+ * up to whole 4-byte words).  *out receives the scalars and these pointers.
+ * outlier_ratio in (0, 0.1]; count = clamp(ceil(n * ratio), 1, n).  A short
+ * rice_cap fails with HK_E_INVALID_ARG and out->rice_bytes = the size needed. */
+int hk_pack_binary_rice(hk_ctx* ctx, const float* w, uint32_t rows, uint32_t cols, double outlier_ratio,
+                        uint16_t* bin_scales, uint8_t* bin_signs, uint8_t* residual_signs, uint8_t* rice,
+                        size_t rice_cap, hk_rice_q1* out, hk_stream stream);
 /* Q2 base stage of _additive_residual_codec
  * (lab/operators/ascension_dual_gravity_worker.py:898-911), group 64. */
 int hk_pack_q2(hk_ctx* ctx, const float* w, size_t count, uint16_t* scales, uint8_t* codes,

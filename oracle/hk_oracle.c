@@ -522,6 +522,224 @@ int hko_hgravs01_matvec(const uint16_t* ls, const uint8_t* lc, size_t rows, size
 }
 
 /* ------------------------------------------------------------------------ */
+/* HGRAVR02: binary base + Rice-coded 1-bit residual (rice_q1_rms)           */
+/* ------------------------------------------------------------------------ */
+
+/* best_rice_k (q80_mixed_decode.rs:314-333): the k in 0..15 minimising
+ * sum(v >> k) + n (1 + k), the first on ties; 0 for no values. */
+uint32_t hko_best_rice_k(const uint32_t* v, size_t n) {
+    if (n == 0) return 0;
+    uint32_t best_k = 0;
+    uint64_t best_bits = UINT64_MAX;
+    for (uint32_t k = 0; k < 16; ++k) {
+        uint64_t q = 0;
+        for (size_t i = 0; i < n; ++i) q += (uint64_t)(v[i] >> k);
+        uint64_t bits = q + (uint64_t)n * (1u + k);
+        if (bits < best_bits) {
+            best_bits = bits;
+            best_k = k;
+        }
+    }
+    return best_k;
+}
+
+/* Bytes of pack_rice's output: per value (v >> k) ones, a zero, k LSBs. */
+size_t hko_rice_bytes(const uint32_t* v, size_t n, uint32_t k) {
+    uint64_t bits = 0;
+    for (size_t i = 0; i < n; ++i) bits += (uint64_t)(v[i] >> k) + 1u + k;
+    return (size_t)((bits + 7) / 8);
+}
+
+static void put_bit(uint8_t* out, uint64_t* pos, uint32_t bit) {
+    if (bit) out[*pos >> 3] |= (uint8_t)(1u << (*pos & 7u));
+    ++*pos;
+}
+
+/* pack_rice / BitWriter (q80_mixed_decode.rs:260-346): LSB-first bits; the
+ * last byte is zero-padded.  out holds hko_rice_bytes(v, n, k) bytes. */
+void hko_rice_pack(const uint32_t* v, size_t n, uint32_t k, uint8_t* out) {
+    memset(out, 0, hko_rice_bytes(v, n, k));
+    uint64_t pos = 0;
+    for (size_t i = 0; i < n; ++i) {
+        for (uint32_t q = v[i] >> k; q; --q) put_bit(out, &pos, 1);
+        put_bit(out, &pos, 0);
+        for (uint32_t b = 0; b < k; ++b) put_bit(out, &pos, (v[i] >> b) & 1u);
+    }
+}
+
+/* unpack_rice (q80_mixed_decode.rs:348-381): reading past `len` bytes and a
+ * quotient above u32 are errors. */
+int hko_rice_unpack(const uint8_t* p, size_t len, size_t count, uint32_t k, uint32_t* out) {
+    uint64_t pos = 0, end = (uint64_t)len * 8u;
+    for (size_t i = 0; i < count; ++i) {
+        uint64_t q = 0;
+        for (;;) {
+            if (pos >= end) return HKO_E_GEOMETRY;
+            uint32_t bit = (p[pos >> 3] >> (pos & 7u)) & 1u;
+            ++pos;
+            if (!bit) break;
+            if (++q > UINT32_MAX) return HKO_E_GEOMETRY;
+        }
+        uint32_t rem = 0;
+        for (uint32_t b = 0; b < k; ++b) {
+            if (pos >= end) return HKO_E_GEOMETRY;
+            rem |= (uint32_t)((p[pos >> 3] >> (pos & 7u)) & 1u) << b;
+            ++pos;
+        }
+        out[i] = (uint32_t)(q << k) | rem;  /* the reference's u32 shift */
+    }
+    return HKO_OK;
+}
+
+/* expand_rice_indices (q80_mixed_decode.rs:486-507): first, then running
+ * sums of the diffs; an index above u32 is an error. */
+int hko_rice_expand(uint32_t first, const uint8_t* rice, size_t rice_len, uint32_t k, size_t count,
+                    uint32_t* indices) {
+    if (count == 0) return HKO_E_GEOMETRY;
+    indices[0] = first;
+    if (count == 1) return HKO_OK;
+    int rc = hko_rice_unpack(rice, rice_len, count - 1, k, indices + 1);
+    if (rc) return rc;
+    uint64_t acc = first;
+    for (size_t i = 1; i < count; ++i) {
+        acc += indices[i];
+        if (acc > UINT32_MAX) return HKO_E_GEOMETRY;
+        indices[i] = (uint32_t)acc;
+    }
+    return HKO_OK;
+}
+
+/* rice_q1_row_ptr (q80_mixed_decode.rs:462-484): CSR row pointers. */
+int hko_rice_row_ptr(const uint32_t* indices, size_t count, size_t rows, size_t cols, uint32_t* row_ptr) {
+    if (cols == 0) return HKO_E_GEOMETRY;
+    memset(row_ptr, 0, (rows + 1) * sizeof(uint32_t));
+    for (size_t i = 0; i < count; ++i) {
+        size_t row = indices[i] / cols;
+        if (row >= rows) return HKO_E_GEOMETRY;
+        row_ptr[row + 1] += 1;
+    }
+    for (size_t r = 0; r < rows; ++r) row_ptr[r + 1] += row_ptr[r];
+    return HKO_OK;
+}
+
+size_t hko_rice_q1_count(size_t n, double ratio) {
+    size_t count = (size_t)ceil((double)n * ratio);
+    if (count < 1) count = 1;
+    if (count > n) count = n;
+    return count;
+}
+
+static const float* g_sort_abs;
+static int by_abs_desc_then_index(const void* a, const void* b) {
+    uint32_t i = *(const uint32_t*)a, j = *(const uint32_t*)b;
+    float x = g_sort_abs[i], y = g_sort_abs[j];
+    if (x > y) return -1;
+    if (x < y) return 1;
+    return i < j ? -1 : (i > j ? 1 : 0);
+}
+static int u32_ascending(const void* a, const void* b) {
+    uint32_t i = *(const uint32_t*)a, j = *(const uint32_t*)b;
+    return i < j ? -1 : (i > j ? 1 : 0);
+}
+
+/* pack_binary_rice_q1 (q80_mixed_decode.rs:383-460): binary group-128 base;
+ * residual = w - binary weight; the count = clamp(ceil(n ratio), 1, n) largest
+ * |residual| (ties to the lower index), re-sorted by index; scale = f16 of
+ * the f32 rounding of sqrt(mean of squares in f64) (1.0 when not finite or
+ * <= 0); sign bit = residual >= 0; first index, then Rice(diffs) with
+ * best_rice_k (no stream for one outlier).  Caller buffers: bin_scales
+ * [n/128], bin_signs [n/8], indices [count], res_signs [(count+7)/8], rice
+ * [rice_cap]; rice_cap >= (n + 17 count) / 8 + 1 always suffices. */
+int hko_rice_q1_pack(const float* w, size_t rows, size_t cols, double ratio, uint16_t* bin_scales,
+                     uint8_t* bin_signs, uint32_t* indices, uint8_t* res_signs, uint16_t* res_scale,
+                     uint32_t* first, uint32_t* rice_k, uint8_t* rice, size_t rice_cap, size_t* rice_len) {
+    if (!(ratio > 0.0 && ratio <= 0.1)) return HKO_E_INVALID_ARG;
+    int rc = hko_bin_pack(w, rows, cols, 128, bin_scales, bin_signs);
+    if (rc) return rc;
+    size_t n = rows * cols, count = hko_rice_q1_count(n, ratio);
+    float* res = (float*)malloc(n * sizeof(float));
+    float* mag = (float*)malloc(n * sizeof(float));
+    uint32_t* order = (uint32_t*)malloc(n * sizeof(uint32_t));
+    uint32_t* diffs = (uint32_t*)malloc((count ? count : 1) * sizeof(uint32_t));
+    if (!res || !mag || !order || !diffs) {
+        free(res), free(mag), free(order), free(diffs);
+        return HKO_E_INVALID_ARG;
+    }
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t c = 0; c < cols; ++c) {
+            size_t f = r * cols + c;
+            res[f] = w[f] - bin_weight(bin_scales, bin_signs, cols, 128, r, c);
+            mag[f] = fabsf(res[f]);
+        }
+    for (size_t i = 0; i < n; ++i) order[i] = (uint32_t)i;
+    g_sort_abs = mag;
+    qsort(order, n, sizeof(uint32_t), by_abs_desc_then_index);
+    memcpy(indices, order, count * sizeof(uint32_t));
+    qsort(indices, count, sizeof(uint32_t), u32_ascending);
+    double sum_sq = 0.0;
+    memset(res_signs, 0, (count + 7) / 8);
+    for (size_t i = 0; i < count; ++i) {
+        float v = res[indices[i]];
+        sum_sq += (double)v * (double)v;
+        if (v >= 0.0f) res_signs[i >> 3] |= (uint8_t)(1u << (i & 7u));
+    }
+    float scale = (float)sqrt(sum_sq / (double)count);
+    if (!isfinite(scale) || scale <= 0.0f) scale = 1.0f;
+    *res_scale = hko_f32_to_f16(scale);
+    *first = indices[0];
+    *rice_k = 0;
+    *rice_len = 0;
+    rc = HKO_OK;
+    if (count > 1) {
+        for (size_t i = 1; i < count; ++i) diffs[i - 1] = indices[i] - indices[i - 1];
+        *rice_k = hko_best_rice_k(diffs, count - 1);
+        *rice_len = hko_rice_bytes(diffs, count - 1, *rice_k);
+        if (*rice_len > rice_cap) rc = HKO_E_GEOMETRY;
+        else hko_rice_pack(diffs, count - 1, *rice_k, rice);
+    }
+    free(res), free(mag), free(order), free(diffs);
+    return rc;
+}
+
+/* binary_rice_q1_matvec_f32 (q80_mixed_decode.rs:509-527): the serial binary
+ * matvec, then y[flat / cols] += (+-scale) * x[flat % cols] in index order. */
+int hko_rice_q1_matvec(const uint16_t* bin_scales, const uint8_t* bin_signs, size_t rows, size_t cols,
+                       const uint32_t* indices, const uint8_t* res_signs, size_t count, uint16_t res_scale,
+                       const float* x, float* y) {
+    int rc = hko_bin_matvec(bin_scales, bin_signs, rows, cols, 128, x, y);
+    if (rc) return rc;
+    return hko_rice_q1_apply(indices, res_signs, count, res_scale, rows, cols, x, y);
+}
+
+/* The residual half of binary_rice_q1_matvec_f32 on its own: y += R x. */
+int hko_rice_q1_apply(const uint32_t* indices, const uint8_t* res_signs, size_t count, uint16_t res_scale,
+                      size_t rows, size_t cols, const float* x, float* y) {
+    float scale = hko_f16_to_f32(res_scale);
+    for (size_t i = 0; i < count; ++i) {
+        size_t f = indices[i];
+        if (f / cols >= rows) return HKO_E_GEOMETRY;
+        float v = ((res_signs[i >> 3] >> (i & 7u)) & 1u) ? scale : -scale;
+        y[f / cols] += v * x[f % cols];
+    }
+    return HKO_OK;
+}
+
+int hko_rice_q1_matvec_f64(const uint16_t* bin_scales, const uint8_t* bin_signs, size_t rows, size_t cols,
+                           const uint32_t* indices, const uint8_t* res_signs, size_t count, uint16_t res_scale,
+                           const double* x, double* y) {
+    int rc = hko_bin_matvec_f64(bin_scales, bin_signs, rows, cols, 128, x, y);
+    if (rc) return rc;
+    double scale = (double)hko_f16_to_f32(res_scale);
+    for (size_t i = 0; i < count; ++i) {
+        size_t f = indices[i];
+        if (f / cols >= rows) return HKO_E_GEOMETRY;
+        double v = ((res_signs[i >> 3] >> (i & 7u)) & 1u) ? scale : -scale;
+        y[f / cols] += v * x[f % cols];
+    }
+    return HKO_OK;
+}
+
+/* ------------------------------------------------------------------------ */
 /* Mixed per-128-group binary | Q2                                           */
 /* ------------------------------------------------------------------------ */
 

@@ -106,6 +106,27 @@ int hko_uniform_matvec_f64(const uint16_t* scales, const uint8_t* codes, size_t 
 int hko_hgravs01_matvec(const uint16_t* ls, const uint8_t* lc, size_t rows, size_t rank, const uint16_t* rs,
                         const uint8_t* rc, size_t cols, int bits, size_t group, const float* x, float* y);
 
+/* HGRAVR02 rice_q1_rms (q80_mixed_decode.rs:260-527). */
+uint32_t hko_best_rice_k(const uint32_t* v, size_t n);
+size_t hko_rice_bytes(const uint32_t* v, size_t n, uint32_t k);
+void hko_rice_pack(const uint32_t* v, size_t n, uint32_t k, uint8_t* out);
+int hko_rice_unpack(const uint8_t* p, size_t len, size_t count, uint32_t k, uint32_t* out);
+int hko_rice_expand(uint32_t first, const uint8_t* rice, size_t rice_len, uint32_t k, size_t count,
+                    uint32_t* indices);
+int hko_rice_row_ptr(const uint32_t* indices, size_t count, size_t rows, size_t cols, uint32_t* row_ptr);
+size_t hko_rice_q1_count(size_t n, double ratio);
+int hko_rice_q1_pack(const float* w, size_t rows, size_t cols, double ratio, uint16_t* bin_scales,
+                     uint8_t* bin_signs, uint32_t* indices, uint8_t* res_signs, uint16_t* res_scale,
+                     uint32_t* first, uint32_t* rice_k, uint8_t* rice, size_t rice_cap, size_t* rice_len);
+int hko_rice_q1_apply(const uint32_t* indices, const uint8_t* res_signs, size_t count, uint16_t res_scale,
+                      size_t rows, size_t cols, const float* x, float* y);
+int hko_rice_q1_matvec(const uint16_t* bin_scales, const uint8_t* bin_signs, size_t rows, size_t cols,
+                       const uint32_t* indices, const uint8_t* res_signs, size_t count, uint16_t res_scale,
+                       const float* x, float* y);
+int hko_rice_q1_matvec_f64(const uint16_t* bin_scales, const uint8_t* bin_signs, size_t rows, size_t cols,
+                           const uint32_t* indices, const uint8_t* res_signs, size_t count, uint16_t res_scale,
+                           const double* x, double* y);
+
 /* ---- mixed <=1.5 BPW, per 128-group binary|Q2 (build-defined canonical stream):
  *   tags  u8[ceil(groups/8)]  LSB-first over flat group index, bit 1 = binary
  *   bin_scales f16[n_bin]     bin_signs u8[n_bin*16]      (binary groups in flat order)

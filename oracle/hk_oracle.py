@@ -67,6 +67,17 @@ def _declare(L: C.CDLL) -> None:
         "hko_uniform_matvec": (C.c_int, [_p, _p, _sz, _sz, C.c_int, _sz, _p, _p]),
         "hko_uniform_matvec_f64": (C.c_int, [_p, _p, _sz, _sz, C.c_int, _sz, _p, _p]),
         "hko_hgravs01_matvec": (C.c_int, [_p, _p, _sz, _sz, _p, _p, _sz, C.c_int, _sz, _p, _p]),
+        "hko_best_rice_k": (C.c_uint32, [_p, _sz]),
+        "hko_rice_bytes": (_sz, [_p, _sz, C.c_uint32]),
+        "hko_rice_pack": (None, [_p, _sz, C.c_uint32, _p]),
+        "hko_rice_unpack": (C.c_int, [_p, _sz, _sz, C.c_uint32, _p]),
+        "hko_rice_expand": (C.c_int, [C.c_uint32, _p, _sz, C.c_uint32, _sz, _p]),
+        "hko_rice_row_ptr": (C.c_int, [_p, _sz, _sz, _sz, _p]),
+        "hko_rice_q1_count": (_sz, [_sz, C.c_double]),
+        "hko_rice_q1_pack": (C.c_int, [_p, _sz, _sz, C.c_double, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p]),
+        "hko_rice_q1_apply": (C.c_int, [_p, _p, _sz, C.c_uint16, _sz, _sz, _p, _p]),
+        "hko_rice_q1_matvec": (C.c_int, [_p, _p, _sz, _sz, _p, _p, _sz, C.c_uint16, _p, _p]),
+        "hko_rice_q1_matvec_f64": (C.c_int, [_p, _p, _sz, _sz, _p, _p, _sz, C.c_uint16, _p, _p]),
         "hko_mixed_pack": (C.c_int, [_p, _sz, _sz, _p, _p]),
         "hko_mixed_free": (None, [_p]),
         "hko_mixed_decode": (C.c_int, [_p, _p]),
@@ -289,6 +300,108 @@ def hgravs01_matvec(left, right, rows, rank, cols, x, bits=3, group=64) -> np.nd
     _check("hko_hgravs01_matvec",
            lib().hko_hgravs01_matvec(_ptr(left[0]), _ptr(left[1]), rows, rank, _ptr(right[0]), _ptr(right[1]),
                                      cols, bits, group, _ptr(x), _ptr(y)))
+    return y
+
+
+# ---- HGRAVR02 binary + Rice-coded 1-bit residual (rice_q1_rms) ------------------
+
+def best_rice_k(values) -> int:
+    v = np.ascontiguousarray(values, np.uint32)
+    return int(lib().hko_best_rice_k(_ptr(v), v.size))
+
+
+def rice_pack(values, k: int) -> np.ndarray:
+    v = np.ascontiguousarray(values, np.uint32)
+    out = np.zeros(lib().hko_rice_bytes(_ptr(v), v.size, k), np.uint8)
+    lib().hko_rice_pack(_ptr(v), v.size, k, _ptr(out))
+    return out
+
+
+def rice_unpack(payload, count: int, k: int) -> np.ndarray:
+    p = np.ascontiguousarray(payload, np.uint8)
+    out = np.zeros(max(count, 1), np.uint32)
+    _check("hko_rice_unpack", lib().hko_rice_unpack(_ptr(p), p.size, count, k, _ptr(out)))
+    return out[:count]
+
+
+def rice_expand(first: int, rice, k: int, count: int) -> np.ndarray:
+    p = np.ascontiguousarray(rice, np.uint8)
+    out = np.zeros(max(count, 1), np.uint32)
+    _check("hko_rice_expand", lib().hko_rice_expand(first, _ptr(p) if p.size else None, p.size, k, count, _ptr(out)))
+    return out[:count]
+
+
+def rice_row_ptr(indices, rows: int, cols: int) -> np.ndarray:
+    i = np.ascontiguousarray(indices, np.uint32)
+    out = np.zeros(rows + 1, np.uint32)
+    _check("hko_rice_row_ptr", lib().hko_rice_row_ptr(_ptr(i), i.size, rows, cols, _ptr(out)))
+    return out
+
+
+@dataclass
+class RiceQ1:
+    """pack_binary_rice_q1's RiceQ1Packed: the binary body, the outliers'
+    flat indices, their sign bits, the f16 RMS scale, and the Rice stream."""
+    rows: int
+    cols: int
+    bin_scales: np.ndarray
+    bin_signs: np.ndarray
+    indices: np.ndarray
+    res_signs: np.ndarray
+    res_scale: int
+    first: int
+    rice_k: int
+    rice: np.ndarray
+
+    @property
+    def count(self) -> int:
+        return int(self.indices.size)
+
+
+def rice_q1_pack(w: np.ndarray, rows: int, cols: int, ratio: float = 0.02) -> RiceQ1:
+    w = np.ascontiguousarray(w, np.float32).reshape(-1)
+    assert w.size == rows * cols
+    n = rows * cols
+    count = int(lib().hko_rice_q1_count(n, ratio))
+    bs = np.zeros(max(n // 128, 1), np.uint16)
+    bg = np.zeros((n + 7) // 8, np.uint8)
+    idx = np.zeros(count, np.uint32)
+    sg = np.zeros((count + 7) // 8, np.uint8)
+    cap = (n + 17 * count) // 8 + 1
+    rice = np.zeros(cap, np.uint8)
+    sc, first, k, ln = C.c_uint16(), C.c_uint32(), C.c_uint32(), C.c_size_t()
+    _check("hko_rice_q1_pack",
+           lib().hko_rice_q1_pack(_ptr(w), rows, cols, ratio, _ptr(bs), _ptr(bg), _ptr(idx), _ptr(sg), C.byref(sc),
+                                  C.byref(first), C.byref(k), _ptr(rice), cap, C.byref(ln)))
+    return RiceQ1(rows, cols, bs, bg, idx, sg, int(sc.value), int(first.value), int(k.value),
+                  rice[:ln.value].copy())
+
+
+def rice_q1_apply(p: RiceQ1, x, y0) -> np.ndarray:
+    """y0 + the residual corrections in index order (the residual half of
+    binary_rice_q1_matvec_f32)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.array(y0, np.float32, copy=True)
+    _check("hko_rice_q1_apply", lib().hko_rice_q1_apply(_ptr(p.indices), _ptr(p.res_signs), p.count, p.res_scale,
+                                                        p.rows, p.cols, _ptr(x), _ptr(y)))
+    return y
+
+
+def rice_q1_matvec(p: RiceQ1, x) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(p.rows, np.float32)
+    _check("hko_rice_q1_matvec",
+           lib().hko_rice_q1_matvec(_ptr(p.bin_scales), _ptr(p.bin_signs), p.rows, p.cols, _ptr(p.indices),
+                                    _ptr(p.res_signs), p.count, p.res_scale, _ptr(x), _ptr(y)))
+    return y
+
+
+def rice_q1_matvec_f64(p: RiceQ1, x) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float64)
+    y = np.empty(p.rows, np.float64)
+    _check("hko_rice_q1_matvec_f64",
+           lib().hko_rice_q1_matvec_f64(_ptr(p.bin_scales), _ptr(p.bin_signs), p.rows, p.cols, _ptr(p.indices),
+                                        _ptr(p.res_signs), p.count, p.res_scale, _ptr(x), _ptr(y)))
     return y
 
 
