@@ -127,6 +127,29 @@ def lowrank_streamed(ctx, steps, warmup, rows=2048, rank=160, cols=768, n=4096):
             "packed_bytes_per_organ": round((ls.packed_bytes + rs.packed_bytes) / n, 1)}
 
 
+def terminal_head_bench(ctx, steps, warmup, vocab=151936, hidden=2048, n_valid=151669):
+    """The device terminal head on the Qwen80 shape: final RMSNorm(1+w), a
+    synthetic q8 G64 lm_head (vocab x hidden), greedy token on the device."""
+    from hawking_amd import organs
+    from hawking_amd.head import TerminalHead
+    lm = organs.SyntheticOrgan(ctx, HK_Q8, vocab, hidden, organs.stream_key(SEED, 0xEAD0), 0, group=64, sigma=0.02)
+    nw = np.zeros(hidden, np.float32)
+    head = TerminalHead(ctx, nw, lm, n_valid)
+    hs = ctx.empty((4, hidden))
+    ctx.call("hk_synth_normal", organs.stream_key(SEED, 0xEAD1), 0, 4 * hidden, 1.0, hs.ptr, ctx.stream)
+    state = {"i": 0}
+
+    def step():
+        head.greedy_device(hs.offset(hidden * (state["i"] % 4)))
+        state["i"] += 1
+
+    ms = time_launches(ctx, step, steps, warmup)
+    nbytes = lm.packed_bytes + hidden * 4 * 3 + vocab * 4
+    return {"us_per_token": round(ms * 1e3, 2), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "lm_head_bytes": lm.packed_bytes,
+            "shape": [vocab, hidden], "n_valid": n_valid}
+
+
 def single_organ_us(ctx, steps=200):
     from hawking_amd import organs
     o = organs.SyntheticOrgan(ctx, HK_BIN, 512, 2048, organs.stream_key(SEED, 0xBE0002))
@@ -328,6 +351,8 @@ def main():
             log(name, extra[name])
         extra["hgravs01_r160_2048x768"] = lowrank_streamed(ctx, args.steps, args.warmup)
         log("hgravs01", extra["hgravs01_r160_2048x768"])
+        extra["terminal_head_q8_151936x2048"] = terminal_head_bench(ctx, max(args.steps, 20), args.warmup)
+        log("terminal head", extra["terminal_head_q8_151936x2048"])
         extra["single_organ_binary_512x2048_us"] = round(single_organ_us(ctx), 2)
         log("single organ us", extra["single_organ_binary_512x2048_us"])
         if not args.no_moe:

@@ -26,7 +26,8 @@ struct hk_organ {
     hk::ResView res{};         // HGRAVR02 residual (res_dev non-null when present)
     void* res_mem = nullptr;
     const hk::ResView* res_dev = nullptr;
-    void* view_dev = nullptr;  // device copy of `view` for single-organ launches
+    void* view_dev = nullptr;  // device copy of `view` for single-organ launches, then the head's pick key
+    uint64_t* head_key = nullptr;
     void* mem = nullptr;
     size_t alloc_bytes = 0;
     size_t packed_bytes = 0;
@@ -453,12 +454,20 @@ static int repack_into_organ(hk_ctx* ctx, const CanonView& canon, uint32_t n_bin
         return set_error(ctx, HK_E_NOMEM, "organ allocation failed");
     }
     o->view = tiled_place(canon.kind, canon.group, canon.rows, canon.cols, n_bin, n_q2, static_cast<uint8_t*>(o->mem));
-    int rc = HK_OK;
-    if (canon.kind == HK_F32) {
+    // the single-organ descriptor and an 8-byte slot (the terminal head's pick)
+    if (hipMalloc(&o->view_dev, align256(sizeof(OrganView)) + 256) != hipSuccess) {
+        (void)hipFree(o->mem);
+        delete o;
+        return set_error(ctx, HK_E_NOMEM, "descriptor allocation failed");
+    }
+    o->head_key = reinterpret_cast<uint64_t*>(static_cast<uint8_t*>(o->view_dev) + align256(sizeof(OrganView)));
+    int rc = check_hip(ctx, hipMemcpyAsync(o->view_dev, &o->view, sizeof(OrganView), hipMemcpyHostToDevice, st),
+                       "descriptor upload");
+    if (!rc && canon.kind == HK_F32) {
         rc = check_hip(ctx, hipMemcpyAsync(const_cast<float*>(o->view.dense), canon.dense,
                                            (size_t)canon.rows * canon.cols * 4, hipMemcpyDeviceToDevice, st),
                        "dense copy");
-    } else {
+    } else if (!rc) {
         void* scratch = nullptr;
         rc = ensure_scratch(ctx, 8 * ((size_t)o->view.n_tiles * o->view.steps + 1), &scratch);
         if (!rc) rc = check_hip(ctx, launch_repack(canon, o->view, scratch, st), "repack launch");
@@ -466,6 +475,7 @@ static int repack_into_organ(hk_ctx* ctx, const CanonView& canon, uint32_t n_bin
     if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "hipStreamSynchronize (repack)");
     if (rc) {
         (void)hipFree(o->mem);
+        (void)hipFree(o->view_dev);
         delete o;
         return rc;
     }
@@ -526,15 +536,8 @@ extern "C" int hk_gemv(hk_ctx* ctx, const hk_organ* o, const float* x, float* y,
     if (!o) return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv: NULL organ");
     int rc = check_vectors(ctx, "hk_gemv", x, 0, y, 0, 1, o->view);
     if (rc) return rc;
-    // the single-organ descriptor lives in the organ's own scratch slot
+    // the single-organ descriptor was uploaded with the organ
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (!o->view_dev) {
-        hk_organ* m = const_cast<hk_organ*>(o);
-        if (hipMalloc(&m->view_dev, sizeof(OrganView)) != hipSuccess)
-            return set_error(ctx, HK_E_NOMEM, "descriptor allocation failed");
-        rc = check_hip(ctx, hipMemcpy(m->view_dev, &m->view, sizeof(OrganView), hipMemcpyHostToDevice), "descriptor upload");
-        if (rc) return rc;
-    }
     rc = check_hip(ctx, launch_gemv_tiled(static_cast<const OrganView*>(o->view_dev), 1, o->view, x, 0, y, 0, st),
                    "gemv launch");
     if (!rc && o->res_dev) rc = check_hip(ctx, launch_rice_apply(o->res_dev, 1, o->view.rows, o->view.cols, x, 0, y, 0, st), "rice apply");
@@ -1024,6 +1027,29 @@ extern "C" int hk_synth_normal(hk_ctx* ctx, uint64_t key, uint64_t first, size_t
     if (!count) return HK_OK;
     return check_hip(ctx, launch_synth_normal(key, first, count, sigma, out, static_cast<hipStream_t>(stream)),
                      "synth launch");
+}
+
+// ====================================================================== terminal head
+
+extern "C" int hk_terminal_greedy(hk_ctx* ctx, const float* hidden, const float* norm_w, float eps,
+                                  const hk_organ* lm_head, uint32_t n_valid, float* xn, float* logits, int32_t* token,
+                                  hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (!lm_head || !hidden || !norm_w || !xn || !logits || !token)
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_terminal_greedy: NULL argument");
+    if (n_valid == 0 || n_valid > lm_head->view.rows)
+        return set_error(ctx, HK_E_GEOMETRY, "hk_terminal_greedy: need 0 < n_valid <= lm_head rows");
+    if (!(eps >= 0.0f) || !std::isfinite(eps)) return set_error(ctx, HK_E_INVALID_ARG, "hk_terminal_greedy: bad eps");
+    if (!aligned16(hidden)) return set_error(ctx, HK_E_INVALID_ARG, "hk_terminal_greedy: hidden must be 16-byte aligned");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int rc = check_hip(ctx, launch_head_norm(hidden, norm_w, lm_head->view.cols, eps, xn, token, lm_head->head_key,
+                                             ctx->dev_status, st),
+                       "head norm");
+    if (!rc) rc = hk_gemv(ctx, lm_head, xn, logits, stream);
+    if (!rc)
+        rc = check_hip(ctx, launch_head_argmax(logits, n_valid, lm_head->head_key, token, ctx->dev_status, st),
+                       "head argmax");
+    return rc;
 }
 
 // ====================================================================== routers

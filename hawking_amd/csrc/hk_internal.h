@@ -249,6 +249,13 @@ hipError_t pack_binary_rice_device(const float* w, uint32_t rows, uint32_t cols,
                                    uint8_t* bin_signs, uint8_t* res_signs, uint8_t* rice, size_t rice_cap,
                                    RicePackResult* out, hipStream_t s);
 
+// Terminal head: the final RMSNorm(1+w) (one block) and the greedy pick.
+// key: an 8-byte device slot the pick reduces into (reset by the norm).
+hipError_t launch_head_norm(const float* h, const float* w, uint32_t n, float eps, float* xn, int32_t* token,
+                            uint64_t* key, uint32_t* status, hipStream_t s);
+hipError_t launch_head_argmax(const float* logits, uint32_t n_valid, uint64_t* key, int32_t* token, uint32_t* status,
+                              hipStream_t s);
+
 // Device bytes of the tiled layout (sections 256-B aligned); mixed needs n_bin/n_q2.
 size_t tiled_bytes(int kind, int group, uint32_t rows, uint32_t cols, uint32_t n_bin, uint32_t n_q2,
                    size_t* packed_bytes);

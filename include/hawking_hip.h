@@ -254,6 +254,24 @@ int hk_organ_synthetic(hk_ctx* ctx, int32_t kind, int32_t group, uint32_t rows, 
                        uint64_t key, uint64_t coin_key, float sigma, hk_stream stream,
                        hk_organ** out);
 
+/* ------------------------------------------------------------ terminal head */
+
+/* terminal_greedy on the device (model/qwen80_mixed_hybrid_decode.rs:3754-3790):
+ * xn = RMSNorm(1+w)(hidden) (source_qwen80_residual_rms_norm,
+ * model/qwen80_complete_runtime.rs:6778-6797), logits = lm_head xn (any organ
+ * kind; the reference's mixed pack stores it as HGRAVU01 q8 G64), and
+ * token = the lowest index of the largest non-NaN logit among the first
+ * n_valid (the rows past the tokenizer's vocabulary are never chosen).  All
+ * pointers are device memory: hidden and norm_w [lm_head cols], xn [cols] and
+ * logits [lm_head rows] are caller workspaces (16-byte aligned), token one
+ * int32.  A non-finite xn or a best logit that is not finite writes token -1
+ * and latches HK_E_NONFINITE in the device status (hk_check_device_status),
+ * where the reference returns an error.  Stream-ordered, no host round trip;
+ * the pick reduces into an 8-byte slot of the lm_head organ, so calls with one
+ * lm_head must not overlap (same stream, or synchronised streams). */
+int hk_terminal_greedy(hk_ctx* ctx, const float* hidden, const float* norm_w, float eps, const hk_organ* lm_head,
+                       uint32_t n_valid, float* xn, float* logits, int32_t* token, hk_stream stream);
+
 /* ------------------------------------------------------------------ routers */
 
 /* Per token: softmax over n_experts logits, top_k by strict '>' (lowest index

@@ -1030,6 +1030,40 @@ int hko_rmsnorm_1p(const float* x, const float* w, size_t n, float eps, float* o
     return HKO_OK;
 }
 
+/* The greedy pick of terminal_greedy (qwen80_mixed_hybrid_decode.rs:3775-3788):
+ * logits at n_valid.. are masked; best starts at (index 0, -inf) and moves on
+ * v > best (NaN never wins, ties keep the lower index); a best that is not
+ * finite (all masked, -inf or NaN, or a +inf winner) is an error. */
+int hko_argmax_greedy(const float* logits, size_t n_valid, int32_t* token) {
+    size_t best_i = 0;
+    float best_v = -INFINITY;
+    for (size_t i = 0; i < n_valid; ++i) {
+        float v = logits[i];
+        if (v > best_v || (v == best_v && i < best_i)) {
+            best_v = v;
+            best_i = i;
+        }
+    }
+    *token = (int32_t)best_i;
+    return isfinite(best_v) ? HKO_OK : HKO_E_NONFINITE;
+}
+
+/* terminal_greedy (qwen80_mixed_hybrid_decode.rs:3754-3790): residual
+ * RMSNorm(1+w) of the final hidden state, the lm_head matvec (an HGRAVU01
+ * uniform q8 G64 organ, uniform_factor_matvec_f32), then the greedy pick over
+ * the first n_valid logits.  logits (vocab floats) receives the matvec. */
+int hko_terminal_greedy(const float* hidden, const float* norm_w, size_t hidden_n, float eps, const uint16_t* scales,
+                        const uint8_t* codes, size_t vocab, size_t n_valid, float* logits, int32_t* token) {
+    if (n_valid == 0 || n_valid > vocab) return HKO_E_GEOMETRY;
+    float* xn = (float*)malloc(hidden_n * sizeof(float));
+    if (!xn) return HKO_E_INVALID_ARG;
+    int rc = hko_rmsnorm_1p(hidden, norm_w, hidden_n, eps, xn);
+    if (rc == HKO_OK) rc = hko_uniform_matvec(scales, codes, vocab, hidden_n, 8, 64, xn, logits);
+    free(xn);
+    if (rc) return rc;
+    return hko_argmax_greedy(logits, n_valid, token);
+}
+
 /* silu_mul, src/kernels/mod.rs:24-31. */
 void hko_silu_mul(const float* gate, const float* up, size_t n, float* out) {
     for (size_t i = 0; i < n; ++i) {

@@ -170,6 +170,9 @@ int hko_router_noaux_tc(const float* logits, const float* bias, size_t n_experts
 void hko_topk_desc(const float* values, size_t n, size_t k, int32_t* out);
 /* source_qwen80_residual_rms_norm (qwen80_complete_runtime.rs:6778-6797), eps given. */
 int hko_rmsnorm_1p(const float* x, const float* w, size_t n, float eps, float* out);
+int hko_argmax_greedy(const float* logits, size_t n_valid, int32_t* token);
+int hko_terminal_greedy(const float* hidden, const float* norm_w, size_t hidden_n, float eps, const uint16_t* scales,
+                        const uint8_t* codes, size_t vocab, size_t n_valid, float* logits, int32_t* token);
 /* silu_mul (src/kernels/mod.rs:24-31). */
 void hko_silu_mul(const float* gate, const float* up, size_t n, float* out);
 

@@ -90,6 +90,8 @@ def _declare(L: C.CDLL) -> None:
         "hko_topk_desc": (None, [_p, _sz, _sz, _p]),
         "hko_rmsnorm_1p": (C.c_int, [_p, _p, _sz, C.c_float, _p]),
         "hko_silu_mul": (None, [_p, _p, _sz, _p]),
+        "hko_argmax_greedy": (C.c_int, [_p, _sz, _p]),
+        "hko_terminal_greedy": (C.c_int, [_p, _p, _sz, C.c_float, _p, _p, _sz, _sz, _p, _p]),
         "hko_organ_matvec": (C.c_int, [_p, _p, _p]),
         "hko_mlp": (C.c_int, [_p, _p, _p, _p, _p, _p]),
         "hko_moe_layer_forward": (C.c_int, [_p, _p, _p, _p, _p, _p, _p]),
@@ -703,3 +705,26 @@ class NoauxMoe:
         _check("hko_noaux_moe_forward_f64",
                lib().hko_noaux_moe_forward_f64(C.byref(self.c), _ptr(x), _ptr(ids), _ptr(out)))
         return out
+
+
+# ---- terminal head (final RMSNorm(1+w) -> lm_head q8 -> greedy argmax) ------------
+
+def argmax_greedy(logits, n_valid: int | None = None) -> int:
+    """terminal_greedy's pick: the lowest index of the largest non-NaN logit
+    among the first n_valid; OracleError if that logit is not finite."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    n = lg.size if n_valid is None else n_valid
+    t = C.c_int32()
+    _check("hko_argmax_greedy", lib().hko_argmax_greedy(_ptr(lg), n, C.byref(t)))
+    return int(t.value)
+
+
+def terminal_greedy(hidden, norm_w, scales, codes, vocab: int, n_valid: int, eps: float = 1e-6):
+    """terminal_greedy with an HGRAVU01 lm_head: (token, logits)."""
+    h = np.ascontiguousarray(hidden, np.float32)
+    w = np.ascontiguousarray(norm_w, np.float32)
+    logits = np.empty(vocab, np.float32)
+    t = C.c_int32()
+    _check("hko_terminal_greedy", lib().hko_terminal_greedy(_ptr(h), _ptr(w), h.size, eps, _ptr(scales), _ptr(codes),
+                                                            vocab, n_valid, _ptr(logits), C.byref(t)))
+    return int(t.value), logits
