@@ -53,6 +53,16 @@ class RiceQ1Src(C.Structure):
     ]
 
 
+class CatalogRecord(C.Structure):
+    """hk_catalog_record: one 128-byte HQ80M15 tensor record, decoded."""
+    _fields_ = [
+        ("name", C.c_char_p), ("codec", _u32), ("organ", _u32), ("ndim", _u32), ("shape", _u32 * 4),
+        ("elements", _u64), ("segment_id", C.c_uint16), ("achieved_rank", C.c_uint16), ("offset", _u64),
+        ("nbytes", _u64), ("sha256", C.c_uint8 * 32), ("flags", _u32), ("n_fit_rows", _u32),
+        ("codec_bpw", C.c_float),
+    ]
+
+
 class MoeConfig(C.Structure):
     _fields_ = [
         ("n_layers", _u32), ("hidden", _u32), ("inter", _u32), ("shared_inter", _u32),
@@ -100,6 +110,15 @@ PROTOTYPES = {
     "hk_organ_upload_rice": (C.c_int, [_p, C.POINTER(RiceQ1Src), _p, C.POINTER(_p)]),
     "hk_rice_apply": (C.c_int, [_p, _p, _p, _p, _p]),
     "hk_terminal_greedy": (C.c_int, [_p, _p, _p, C.c_float, _p, _u32, _p, _p, _p, _p]),
+    "hk_organ_from_container": (C.c_int, [_p, _i32, _p, _sz, _p, C.POINTER(_p), C.POINTER(_p)]),
+    "hk_organ_from_hq30": (C.c_int, [_p, _p, _sz, _p, C.POINTER(_p)]),
+    "hk_catalog_open": (C.c_int, [_p, C.c_char_p, C.POINTER(_p)]),
+    "hk_catalog_close": (C.c_int, [_p]),
+    "hk_catalog_info": (C.c_int, [_p, C.POINTER(_u32), C.POINTER(_u32), C.POINTER(C.c_double), C.POINTER(_u64)]),
+    "hk_catalog_record_at": (C.c_int, [_p, _u32, C.POINTER(CatalogRecord)]),
+    "hk_catalog_find": (C.c_int, [_p, _p, C.c_char_p, C.POINTER(CatalogRecord)]),
+    "hk_catalog_payload": (C.c_int, [_p, _p, C.c_char_p, C.c_int, C.POINTER(_p), C.POINTER(_sz)]),
+    "hk_catalog_load": (C.c_int, [_p, _p, C.c_char_p, C.c_int, _p, C.POINTER(_p), C.POINTER(_p)]),
     "hk_pack_binary_rice": (C.c_int, [_p, _p, _u32, _u32, C.c_double, _p, _p, _p, _p, _sz, C.POINTER(RiceQ1Src), _p]),
     "hk_gemv_batch": (C.c_int, [_p, C.POINTER(_p), _u32, _p, _sz, _p, _sz, _p]),
     "hk_decode_rows": (C.c_int, [_p, _p, _u32, _u32, _p, _p]),

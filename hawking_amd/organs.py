@@ -46,6 +46,19 @@ class PackedOrgan:
         ctx.check("hk_organ_info", ctx.L.hk_organ_info(h, None, None, None, None, C.byref(sz)))
         self.packed_bytes = int(sz.value)
 
+    @classmethod
+    def _wrap(cls, ctx: Context, h: C.c_void_p) -> "PackedOrgan":
+        """An object of this class around an organ the library already built
+        (the loaders); shape and bytes come from hk_organ_info."""
+        self = cls.__new__(cls)
+        self.ctx, self.h = ctx, h
+        kind, group, rows, cols, sz = C.c_int32(), C.c_int32(), C.c_uint32(), C.c_uint32(), C.c_size_t()
+        ctx.check("hk_organ_info", ctx.L.hk_organ_info(h, C.byref(kind), C.byref(group), C.byref(rows),
+                                                         C.byref(cols), C.byref(sz)))
+        self.kind, self.group = int(kind.value), int(group.value)
+        self.rows, self.cols, self.packed_bytes = int(rows.value), int(cols.value), int(sz.value)
+        return self
+
     def free(self):
         if getattr(self, "h", None) and self.h.value and self.ctx.h:
             self.ctx.L.hk_organ_free(self.ctx.h, self.h)

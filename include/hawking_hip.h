@@ -254,6 +254,64 @@ int hk_organ_synthetic(hk_ctx* ctx, int32_t kind, int32_t group, uint32_t rows, 
                        uint64_t key, uint64_t coin_key, float sigma, hk_stream stream,
                        hk_organ** out);
 
+/* ------------------------------------------------------------ containers */
+
+/* Codec ids of the mixed catalog (qwen80_mixed_catalog.rs:30-33). */
+#define HK_CODEC_BINARY 0   /* HGRAVB01 binary_sign_scale, group 128 */
+#define HK_CODEC_RESIDUAL 1 /* HGRAVR02 binary + Rice-coded 1-bit residual */
+#define HK_CODEC_HGRAVS01 2 /* low-rank, two uniform factors (3-bit G64 on the device) */
+#define HK_CODEC_UNIFORM8 3 /* HGRAVU01 uniform q8 G64 */
+
+/* One HGRAV* container payload (host memory: 8-byte magic, u32 LE JSON header
+ * length, JSON header, body) parsed and validated as
+ * MixedPackedTensor::from_codec_payload does (q80_mixed_decode.rs:135-147,
+ * 823-1070,1336-1347) and bound: HGRAVB01 -> HK_BIN, HGRAVU01 -> HK_Q8,
+ * HGRAVR02 -> an HGRAVR02 organ, HGRAVS01 -> *out = the left factor and
+ * *right = the right one (HK_U3; use hk_gemv_lowrank).  right may be NULL
+ * except for HGRAVS01.  Errors: HK_E_INVALID_ARG (magic, JSON, schema,
+ * missing fields), HK_E_GEOMETRY (ledgers, shapes), HK_E_UNSUPPORTED (valid
+ * for the reference but not a device kind here: HGRAVS01 factors other than
+ * 3-bit G64, binary groups other than 128). */
+int hk_organ_from_container(hk_ctx* ctx, int32_t codec, const uint8_t* payload, size_t len, hk_stream stream,
+                            hk_organ** out, hk_organ** right);
+
+/* An HQ30UQ4 (uniform Q4, group 64/128) or HQ30G1B1 (binary) payload with its
+ * 32-byte header (parse_uniform_q4_header, qwen_complete_binary/uniform_q4.rs:57-150;
+ * parse_complete_binary_header, qwen_complete_binary/mod.rs:137-233) bound as
+ * an HK_Q4 / HK_BIN organ; shape [rows, cols] or [len] (= len x 1). */
+int hk_organ_from_hq30(hk_ctx* ctx, const uint8_t* payload, size_t len, hk_stream stream, hk_organ** out);
+
+/* The HQ80M15 mixed catalog (Qwen80MixedStreamingCatalog,
+ * qwen80_mixed_catalog.rs:176-555): the manifest JSON (schema, seal, bpw
+ * ledger, catalog path + SHA-256, checked), the catalog's segment table and
+ * 128-byte tensor records; payloads are windows of memory-mapped
+ * <manifest dir>/segments/<file>. */
+typedef struct hk_catalog hk_catalog;
+typedef struct hk_catalog_record {
+    const char* name;       /* valid while the catalog is open */
+    uint32_t codec, organ, ndim;
+    uint32_t shape[4];
+    uint64_t elements;
+    uint16_t segment_id, achieved_rank;
+    uint64_t offset, nbytes;
+    uint8_t sha256[32];
+    uint32_t flags, n_fit_rows;
+    float codec_bpw;
+} hk_catalog_record;
+int hk_catalog_open(hk_ctx* ctx, const char* manifest_path, hk_catalog** out);
+int hk_catalog_close(hk_catalog* catalog);
+int hk_catalog_info(const hk_catalog* catalog, uint32_t* n_tensors, uint32_t* n_segments,
+                    double* complete_physical_bpw, uint64_t* tensor_payload_bytes);
+int hk_catalog_record_at(const hk_catalog* catalog, uint32_t index, hk_catalog_record* out);
+int hk_catalog_find(hk_ctx* ctx, const hk_catalog* catalog, const char* name, hk_catalog_record* out);
+/* The tensor's payload window (valid while the catalog is open); with
+ * verify_sha256 its SHA-256 is checked against the record on first use. */
+int hk_catalog_payload(hk_ctx* ctx, hk_catalog* catalog, const char* name, int verify_sha256, const uint8_t** data,
+                       size_t* len);
+/* load_packed: the payload through hk_organ_from_container by its codec. */
+int hk_catalog_load(hk_ctx* ctx, hk_catalog* catalog, const char* name, int verify_sha256, hk_stream stream,
+                    hk_organ** out, hk_organ** right);
+
 /* ------------------------------------------------------------ terminal head */
 
 /* terminal_greedy on the device (model/qwen80_mixed_hybrid_decode.rs:3754-3790):
