@@ -150,6 +150,59 @@ def terminal_head_bench(ctx, steps, warmup, vocab=151936, hidden=2048, n_valid=1
             "shape": [vocab, hidden], "n_valid": n_valid}
 
 
+def moe15_bench(ctx, steps, warmup, n_layers=48, H=2048, I=512, SI=512, E=512, K=10, rank=160, n_inputs=16):
+    """The mixed-1p5-v1 token's MoE suffixes at batch 1 (config-4 shape,
+    Qwen3-Next-80B-A3B): per layer 512 experts with an HGRAVB01 gate, an
+    HGRAVR02 up (2% Rice residual) and an HGRAVS01 r160 3-bit down; q8
+    router, shared-expert gate and shared expert.  Tokens cycle over
+    n_inputs distinct hidden vectors (distinct routes).  Algorithmic bytes per
+    token: the canonical packed bytes of every organ the routes touch, the
+    norm weights and the hidden state in and out."""
+    from hawking_amd import organs
+    from hawking_amd.moe import Mixed15Layer, mixed15_decode_stack
+    t0 = time.time()
+    layers, expert_bytes, dense_bytes = [], [], []
+    for l in range(n_layers):
+        def syn(kind, rows, cols, e, p, group, sigma=0.02):
+            sid = (0xC15 << 40) | (l << 24) | (e << 8) | p
+            return organs.SyntheticOrgan(ctx, kind, rows, cols, organs.stream_key(SEED, sid), 0, group=group,
+                                         sigma=sigma)
+        experts = [(syn(HK_BIN, I, H, e, 0, 128), syn(HK_BIN_RICE, I, H, e, 1, 128),
+                    (syn(HK_U3, H, rank, e, 2, 64, 0.05), syn(HK_U3, rank, I, e, 3, 64))) for e in range(E)]
+        router = syn(HK_Q8, E, H, E, 16, 64)
+        sgate = syn(HK_Q8, 1, H, E, 17, 64)
+        shared = (syn(HK_Q8, SI, H, E, 18, 64), syn(HK_Q8, SI, H, E, 19, 64), syn(HK_Q8, H, SI, E, 20, 64))
+        nw = np.random.default_rng(l).normal(0.0, 0.02, H).astype(np.float32)
+        layers.append(Mixed15Layer(ctx, nw, router, experts, K, shared=shared, shared_gate=sgate))
+        expert_bytes.append([t[0].packed_bytes + t[1].packed_bytes + t[2][0].packed_bytes + t[2][1].packed_bytes
+                             for t in experts])
+        dense_bytes.append(router.packed_bytes + sgate.packed_bytes + sum(o.packed_bytes for o in shared) + H * 4)
+    ctx.synchronize()
+    gen_s = time.time() - t0
+    hs = ctx.empty((n_inputs, H))
+    ctx.call("hk_synth_normal", organs.stream_key(SEED, 0xBE0015), 0, n_inputs * H, 1.0, hs.ptr, ctx.stream)
+    out = ctx.empty(H)
+    ids = ctx.empty((n_inputs, n_layers, K), np.int32)
+    state = {"i": 0}
+
+    def step():
+        i = state["i"] % n_inputs
+        state["i"] += 1
+        mixed15_decode_stack(ctx, layers, hs.offset(i * H), out, ids.offset(i * n_layers * K))
+
+    ctx.device_status()
+    ms = time_launches(ctx, step, steps, warmup)
+    status = ctx.device_status()
+    routes = ids.download()
+    per_tok = [sum(dense_bytes[l] + 2 * H * 4 + sum(expert_bytes[l][int(e)] for e in routes[t, l])
+                   for l in range(n_layers)) for t in range(n_inputs)]
+    tok_bytes = float(np.mean(per_tok))
+    return {"us_per_token": round(ms * 1e3, 2), "bytes_per_token": round(tok_bytes),
+            "gbps": round(tok_bytes / (ms * 1e-3) / 1e9, 1), "tokens_per_s": round(1e3 / ms, 1),
+            "launches_per_layer": 12, "layers": n_layers, "device_status": status,
+            "distinct_routes": int(np.unique(routes.reshape(-1, K), axis=0).shape[0]), "gen_seconds": round(gen_s, 2)}
+
+
 def single_organ_us(ctx, steps=200):
     from hawking_amd import organs
     o = organs.SyntheticOrgan(ctx, HK_BIN, 512, 2048, organs.stream_key(SEED, 0xBE0002))
@@ -310,6 +363,7 @@ def main():
     ap.add_argument("--only-main", action="store_true", help="headline kernel only (for profiling)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
+    ap.add_argument("--moe15-only", action="store_true", help="only the mixed-1p5-v1 token (development)")
     ap.add_argument("--moe-layers", type=int, default=48)
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="run one device-to-device copy of this size first (PMC byte-counter calibration)")
@@ -331,6 +385,12 @@ def main():
         ctx.synchronize()
         log("calibration copy bytes", nb)
         del src, dst
+
+    if args.moe15_only:
+        r = moe15_bench(ctx, max(args.steps, 20), args.warmup, n_layers=args.moe_layers)
+        log("mixed-1p5 token", r)
+        print(json.dumps({"moe15_token_c4_mixed_1p5_v1": r}), flush=True)
+        return
 
     main_name = "binary_512x2048"
     log("headline", main_name)
@@ -367,6 +427,9 @@ def main():
             r = moe_bench(ctx, c4, max(args.steps, 20), args.warmup)
             extra["moe_token_c4_mixed"] = {k: (round(v, 2) if isinstance(v, float) else v) for k, v in r.items()}
             log("c4", extra["moe_token_c4_mixed"])
+            extra["moe15_token_c4_mixed_1p5_v1"] = moe15_bench(ctx, max(args.steps, 20), args.warmup,
+                                                               n_layers=args.moe_layers)
+            log("mixed-1p5 token", extra["moe15_token_c4_mixed_1p5_v1"])
             r = moe_batch_bench(ctx, max(args.steps, 10), args.warmup)
             extra["moe_batch_c5_dsv3"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
             log("c5", extra["moe_batch_c5_dsv3"])

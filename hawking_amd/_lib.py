@@ -79,6 +79,14 @@ class MoeLayerSrc(C.Structure):
     ]
 
 
+class Moe15LayerSrc(C.Structure):
+    _fields_ = [
+        ("hidden", _u32), ("inter", _u32), ("shared_inter", _u32), ("n_experts", _u32), ("top_k", _u32),
+        ("eps", C.c_float), ("norm_w", _p), ("router", _p), ("shared_gate", _p), ("shared_gate_proj", _p),
+        ("shared_up", _p), ("shared_down", _p), ("gate", _p), ("up", _p), ("down_left", _p), ("down_right", _p),
+    ]
+
+
 # name -> (restype, argtypes)
 PROTOTYPES = {
     "hk_ctx_create": (C.c_int, [C.c_int, C.POINTER(_p)]),
@@ -146,6 +154,10 @@ PROTOTYPES = {
     "hk_moe_decode_layer": (C.c_int, [_p, _p, _u32, _p, _p, _p, _p, _p]),
     "hk_moe_decode_stack": (C.c_int, [_p, _p, _p, _p, _p, _p, _p]),
     "hk_moe_forward_batch": (C.c_int, [_p, _p, _u32, _p, _u32, _p, _p, _p, _p]),
+    "hk_moe15_layer_create": (C.c_int, [_p, C.POINTER(Moe15LayerSrc), C.POINTER(_p)]),
+    "hk_moe15_layer_free": (C.c_int, [_p, _p]),
+    "hk_moe15_decode_layer": (C.c_int, [_p, _p, _p, _p, _p, _p, _p]),
+    "hk_moe15_decode_stack": (C.c_int, [_p, _p, _u32, _p, _p, _p, _p, _p]),
 }
 
 _lib: C.CDLL | None = None

@@ -20,19 +20,6 @@
 
 using hk::CanonView;
 
-struct hk_organ {
-    hk::OrganView view{};
-    int32_t kind = 0;          // the canonical kind it was uploaded as (view.kind is the engine's)
-    hk::ResView res{};         // HGRAVR02 residual (res_dev non-null when present)
-    void* res_mem = nullptr;
-    const hk::ResView* res_dev = nullptr;
-    void* view_dev = nullptr;  // device copy of `view` for single-organ launches, then the head's pick key
-    uint64_t* head_key = nullptr;
-    void* mem = nullptr;
-    size_t alloc_bytes = 0;
-    size_t packed_bytes = 0;
-};
-
 namespace hk {
 
 int set_error(hk_ctx* ctx, int code, const std::string& msg) {

@@ -263,3 +263,18 @@ OrganView tiled_place(int kind, int group, uint32_t rows, uint32_t cols, uint32_
                       uint8_t* base);
 
 }  // namespace hk
+
+// One packed matrix in library-owned device memory (the opaque hk_organ of
+// the C ABI).
+struct hk_organ {
+    hk::OrganView view{};
+    int32_t kind = 0;          // the canonical kind it was uploaded as (view.kind is the engine's)
+    hk::ResView res{};         // HGRAVR02 residual (res_dev non-null when present)
+    void* res_mem = nullptr;
+    const hk::ResView* res_dev = nullptr;
+    void* view_dev = nullptr;  // device copy of `view` for single-organ launches, then the head's pick key
+    uint64_t* head_key = nullptr;
+    void* mem = nullptr;
+    size_t alloc_bytes = 0;
+    size_t packed_bytes = 0;
+};

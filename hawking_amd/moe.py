@@ -222,3 +222,78 @@ class MoeModel:
         w = self.ctx.empty((T, s.top_k), np.float32)
         self.forward_batch_device(layer, xd, T, y, ids, w)
         return y.download(), ids.download(), w.download()
+
+
+class Mixed15Layer:
+    """One MoE layer of the mixed-1p5-v1 artifact over bound organs
+    (moe_suffix, model/qwen80_mixed_hybrid_decode.rs:3636-3752, with
+    routed_wave :2192-2386).
+
+    experts: per expert (gate BinaryGroupPacked, up RiceQ1Packed, down) with
+    down an HgravS01LowRank or its (left, right) factor organs; router /
+    shared_gate / shared (gate, up, down):
+    PackedOrgan (HGRAVU01 q8 in the artifact).  The layer keeps references
+    to the organs; they must outlive it."""
+
+    def __init__(self, ctx: Context, norm_w, router, experts, top_k: int, shared=None, shared_gate=None,
+                 eps: float = 1e-6):
+        from ._lib import Moe15LayerSrc
+        self.ctx = ctx
+        self.h = None
+        downs = [t[2] if isinstance(t[2], tuple) else (t[2].left, t[2].right) for t in experts]
+        g0 = experts[0][0]
+        self.hidden, self.inter, self.n_experts, self.top_k = downs[0][0].rows, g0.rows, len(experts), top_k
+        self.rank = downs[0][0].cols
+        self.shared_inter = shared[0].rows if shared is not None else 0
+        self._keep = (router, experts, shared, shared_gate)
+        self._norm = np.ascontiguousarray(norm_w, np.float32)
+        E = self.n_experts
+        tab = [(C.c_void_p * E)(*[t[0].h.value for t in experts]),
+               (C.c_void_p * E)(*[t[1].h.value for t in experts]),
+               (C.c_void_p * E)(*[d[0].h.value for d in downs]),
+               (C.c_void_p * E)(*[d[1].h.value for d in downs])]
+        self._tab = tab
+        sh = shared if shared is not None else (None, None, None)
+        src = Moe15LayerSrc(hidden=self.hidden, inter=self.inter, shared_inter=self.shared_inter, n_experts=E,
+                            top_k=top_k, eps=eps, norm_w=self._norm.ctypes.data, router=router.h,
+                            shared_gate=shared_gate.h if shared_gate is not None else None,
+                            shared_gate_proj=sh[0].h if sh[0] is not None else None,
+                            shared_up=sh[1].h if sh[1] is not None else None,
+                            shared_down=sh[2].h if sh[2] is not None else None,
+                            gate=C.cast(tab[0], C.c_void_p), up=C.cast(tab[1], C.c_void_p),
+                            down_left=C.cast(tab[2], C.c_void_p), down_right=C.cast(tab[3], C.c_void_p))
+        h = C.c_void_p()
+        ctx.call("hk_moe15_layer_create", C.byref(src), C.byref(h))
+        self.h = h
+
+    def free(self):
+        if self.h is not None:
+            self.ctx.call("hk_moe15_layer_free", self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def decode_device(self, h_in, h_out, ids=None, weights=None, stream=None) -> None:
+        self.ctx.call("hk_moe15_decode_layer", self.h, _pp(h_in), _pp(h_out), _pp(ids), _pp(weights),
+                      stream if stream is not None else self.ctx.stream)
+
+    def moe_suffix(self, h: np.ndarray):
+        """One layer on numpy input: returns (out, ids, weights)."""
+        hd = self.ctx.to_device(np.ascontiguousarray(h, np.float32))
+        out = self.ctx.empty(self.hidden)
+        ids = self.ctx.empty(self.top_k, np.int32)
+        w = self.ctx.empty(self.top_k, np.float32)
+        self.decode_device(hd, out, ids, w)
+        return out.download(), ids.download(), w.download()
+
+
+def mixed15_decode_stack(ctx: Context, layers: list[Mixed15Layer], h_in, h_out, ids=None, weights=None,
+                         stream=None) -> None:
+    """All layers for one token on device data (hk_moe15_decode_stack)."""
+    arr = (C.c_void_p * len(layers))(*[l.h.value for l in layers])
+    ctx.call("hk_moe15_decode_stack", arr, len(layers), _pp(h_in), _pp(h_out), _pp(ids), _pp(weights),
+             stream if stream is not None else ctx.stream)

@@ -435,6 +435,51 @@ int hk_moe_decode_stack(hk_ctx* ctx, hk_moe_model* model, const float* h_in, flo
 int hk_moe_forward_batch(hk_ctx* ctx, hk_moe_model* model, uint32_t layer, const uint16_t* x_bf16,
                          uint32_t n_tokens, float* y, int32_t* ids, float* weights, hk_stream stream);
 
+/* ------------------------------------------------- mixed-1p5 MoE layer */
+
+/* One MoE layer of the mixed-1p5-v1 artifact built from bound organs (the
+ * library keeps pointers to them: free the layer before its organs).
+ * Routed expert e: gate[e] HGRAVB01 (HK_BIN, inter x hidden), up[e] HGRAVR02
+ * (inter x hidden), down = down_left[e] (hidden x rank) . down_right[e]
+ * (rank x inter), the HGRAVS01 factors.  Router (n_experts x hidden),
+ * shared_gate (1 x hidden), shared_gate_proj / shared_up (shared_inter x
+ * hidden) and shared_down (hidden x shared_inter): any non-residual kind,
+ * HGRAVU01 q8 in the artifact.  shared_inter = 0: no shared expert (its
+ * organs may be NULL).  norm_w is a HOST pointer [hidden]. */
+typedef struct hk_moe15_layer hk_moe15_layer;
+typedef struct hk_moe15_layer_src {
+    uint32_t hidden, inter, shared_inter, n_experts, top_k;
+    float eps;
+    const float* norm_w;
+    const hk_organ* router;
+    const hk_organ* shared_gate;
+    const hk_organ* shared_gate_proj;
+    const hk_organ* shared_up;
+    const hk_organ* shared_down;
+    const hk_organ* const* gate;       /* [n_experts] */
+    const hk_organ* const* up;         /* [n_experts] */
+    const hk_organ* const* down_left;  /* [n_experts] */
+    const hk_organ* const* down_right; /* [n_experts] */
+} hk_moe15_layer_src;
+/* Limits: top_k <= 64, n_experts <= 512; rank, inter, hidden multiples of 4. */
+int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* src, hk_moe15_layer** out);
+int hk_moe15_layer_free(hk_ctx* ctx, hk_moe15_layer* layer);
+/* moe_suffix of the mixed decode (model/qwen80_mixed_hybrid_decode.rs:3636-3752
+ * with routed_wave :2192-2386) at batch 1 on device data:
+ * xn = RMSNorm(1+w)(h); route = softmax top-k renorm of router xn;
+ * act_r = silu(gate_r xn) * (up_r xn); y_r = L_r (R_r act_r);
+ * out = h + sum_r w_r y_r (route order) + sigmoid(shared_gate xn) * shared(xn).
+ * ids/weights (device, top_k each) may be NULL.  Stream-ordered, no sync;
+ * layer workspace is reused, so calls on one layer must not overlap. */
+int hk_moe15_decode_layer(hk_ctx* ctx, hk_moe15_layer* layer, const float* h, float* out, int32_t* ids,
+                          float* weights, hk_stream stream);
+/* n_layers layers for one token, h_{l+1} = layer_l(h_l) (forward_token's MoE
+ * suffixes, model/qwen80_mixed_hybrid_decode.rs:4682-4736, without the
+ * attention mixers); the intermediate states live in the layers' workspace.
+ * Layers share hidden and top_k; ids/weights may be NULL or [n_layers*top_k]. */
+int hk_moe15_decode_stack(hk_ctx* ctx, hk_moe15_layer* const* layers, uint32_t n_layers, const float* h, float* out,
+                          int32_t* ids, float* weights, hk_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1077,11 +1077,18 @@ void hko_silu_mul(const float* gate, const float* up, size_t n, float* out) {
 /* Organs, MLP, MoE layer                                                    */
 /* ------------------------------------------------------------------------ */
 
+/* MixedPackedTensor::cpu_matvec (q80_mixed_decode.rs:1362-1369) for the
+ * mixed-1p5 kinds, and the Q4/binary/mixed organs. */
 int hko_organ_matvec(const hko_organ* o, const float* x, float* y) {
     switch (o->kind) {
     case 0: return hko_q4_matvec(o->scales, o->codes, o->rows, o->cols, o->group, x, y);
     case 1: return hko_bin_matvec(o->scales, o->codes, o->rows, o->cols, o->group, x, y);
     case 2: return hko_mixed_matvec(o->mixed, x, y);
+    case 3: return hko_uniform_matvec(o->scales, o->codes, o->rows, o->cols, 8, 64, x, y);
+    case 4: return hko_hgravs01_matvec(o->scales, o->codes, o->rows, o->rank, o->r_scales, o->r_codes, o->cols, 3, 64,
+                                       x, y);
+    case 5: return hko_rice_q1_matvec(o->scales, o->codes, o->rows, o->cols, o->res_indices, o->res_signs,
+                                      o->res_count, o->res_scale, x, y);
     default: return HKO_E_UNSUPPORTED;
     }
 }
@@ -1091,6 +1098,17 @@ int hko_organ_matvec_f64(const hko_organ* o, const double* x, double* y) {
     case 0: return hko_q4_matvec_f64(o->scales, o->codes, o->rows, o->cols, o->group, x, y);
     case 1: return hko_bin_matvec_f64(o->scales, o->codes, o->rows, o->cols, o->group, x, y);
     case 2: return hko_mixed_matvec_f64(o->mixed, x, y);
+    case 3: return hko_uniform_matvec_f64(o->scales, o->codes, o->rows, o->cols, 8, 64, x, y);
+    case 4: {
+        double* mid = (double*)malloc(o->rank * sizeof(double));
+        if (!mid) return HKO_E_INVALID_ARG;
+        int rc = hko_uniform_matvec_f64(o->r_scales, o->r_codes, o->rank, o->cols, 3, 64, x, mid);
+        if (rc == HKO_OK) rc = hko_uniform_matvec_f64(o->scales, o->codes, o->rows, o->rank, 3, 64, mid, y);
+        free(mid);
+        return rc;
+    }
+    case 5: return hko_rice_q1_matvec_f64(o->scales, o->codes, o->rows, o->cols, o->res_indices, o->res_signs,
+                                          o->res_count, o->res_scale, x, y);
     default: return HKO_E_UNSUPPORTED;
     }
 }

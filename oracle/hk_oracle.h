@@ -179,12 +179,20 @@ void hko_silu_mul(const float* gate, const float* up, size_t n, float* out);
 /* ---- MoE layer (moe_suffix, qwen80_uniform_q4_hybrid_decode.rs:2615-2757) ----
  * One organ is either Q4 (kind 0) or mixed (kind 2). */
 typedef struct hko_organ {
-    int kind;          /* 0 = Q4, 1 = binary, 2 = mixed */
-    int group;         /* Q4 group size; 128 for binary */
+    int kind;          /* 0 = Q4, 1 = binary, 2 = mixed, 3 = uniform q8 G64 (HGRAVU01),
+                          4 = low-rank 3-bit G64 factors (HGRAVS01), 5 = binary + Rice residual (HGRAVR02) */
+    int group;         /* Q4 group size; 128 for binary; 64 for the uniform factors */
     size_t rows, cols;
-    const uint16_t* scales;   /* Q4 / binary */
-    const uint8_t* codes;     /* Q4 codes or binary signs */
+    const uint16_t* scales;   /* Q4 / binary / q8 / HGRAVS01 left factor / HGRAVR02 base */
+    const uint8_t* codes;     /* codes or binary signs, as for scales */
     const hko_mixed* mixed;   /* kind 2 */
+    size_t rank;              /* kind 4: left is rows x rank, right rank x cols */
+    const uint16_t* r_scales; /* kind 4: right factor */
+    const uint8_t* r_codes;
+    const uint32_t* res_indices; /* kind 5: outlier flat indices (expanded), signs, count, f16 scale */
+    const uint8_t* res_signs;
+    size_t res_count;
+    uint16_t res_scale;
 } hko_organ;
 int hko_organ_matvec(const hko_organ* o, const float* x, float* y);
 int hko_organ_matvec_f64(const hko_organ* o, const double* x, double* y);

@@ -565,17 +565,44 @@ class _Organ(C.Structure):
     _fields_ = [
         ("kind", C.c_int), ("group", C.c_int), ("rows", _sz), ("cols", _sz),
         ("scales", _p), ("codes", _p), ("mixed", _p),
+        ("rank", _sz), ("r_scales", _p), ("r_codes", _p),
+        ("res_indices", _p), ("res_signs", _p), ("res_count", _sz), ("res_scale", C.c_uint16),
     ]
 
 
 class Organ:
-    """One packed matrix for the oracle: kind 0 = Q4, 1 = binary, 2 = mixed."""
+    """One packed matrix for the oracle: kind 0 = Q4, 1 = binary, 2 = mixed,
+    3 = uniform q8 G64, 4 = low-rank 3-bit factors, 5 = binary + Rice residual."""
 
-    def __init__(self, kind, rows, cols, group=0, scales=None, codes=None, mixed=None):
+    def __init__(self, kind, rows, cols, group=0, scales=None, codes=None, mixed=None, rank=0, right=None,
+                 rice=None):
         self.kind, self.rows, self.cols, self.group = kind, rows, cols, group
-        self.scales, self.codes, self.mixed = scales, codes, mixed
+        self.scales, self.codes, self.mixed, self.rank, self.right, self.rice = scales, codes, mixed, rank, right, rice
         self.c = _Organ(kind, group, rows, cols, _ptr(scales), _ptr(codes),
-                        C.cast(C.byref(mixed._c), _p) if mixed is not None else None)
+                        C.cast(C.byref(mixed._c), _p) if mixed is not None else None, rank,
+                        _ptr(right[0]) if right is not None else None, _ptr(right[1]) if right is not None else None,
+                        _ptr(rice.indices) if rice is not None else None,
+                        _ptr(rice.res_signs) if rice is not None else None,
+                        rice.count if rice is not None else 0, rice.res_scale if rice is not None else 0)
+
+    @classmethod
+    def uniform8(cls, w):
+        s, c = uniform_pack(w, w.shape[0], w.shape[1], 8, 64)
+        return cls(3, w.shape[0], w.shape[1], 64, s, c)
+
+    @classmethod
+    def low_rank(cls, left_w, right_w):
+        """HGRAVS01 from its two factors (3-bit G64)."""
+        rows, rank = left_w.shape
+        cols = right_w.shape[1]
+        ls, lc = uniform_pack(left_w, rows, rank, 3, 64)
+        rs, rc = uniform_pack(right_w, rank, cols, 3, 64)
+        return cls(4, rows, cols, 64, ls, lc, rank=rank, right=(rs, rc))
+
+    @classmethod
+    def rice_q1(cls, w, ratio=0.02):
+        p = rice_q1_pack(w, w.shape[0], w.shape[1], ratio)
+        return cls(5, w.shape[0], w.shape[1], 128, p.bin_scales, p.bin_signs, rice=p)
 
     @classmethod
     def q4(cls, w, group):
