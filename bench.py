@@ -199,7 +199,7 @@ def moe15_bench(ctx, steps, warmup, n_layers=48, H=2048, I=512, SI=512, E=512, K
     tok_bytes = float(np.mean(per_tok))
     return {"us_per_token": round(ms * 1e3, 2), "bytes_per_token": round(tok_bytes),
             "gbps": round(tok_bytes / (ms * 1e-3) / 1e9, 1), "tokens_per_s": round(1e3 / ms, 1),
-            "launches_per_layer": 12, "layers": n_layers, "device_status": status,
+            "launches_per_layer": 4, "layers": n_layers, "device_status": status,
             "distinct_routes": int(np.unique(routes.reshape(-1, K), axis=0).shape[0]), "gen_seconds": round(gen_s, 2)}
 
 

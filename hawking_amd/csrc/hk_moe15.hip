@@ -4,129 +4,393 @@
 // up (binary base + Rice residual) and an HGRAVS01 down (y = L (R act));
 // router, shared-expert gate and shared expert as HGRAVU01 q8 organs.
 //
-// The layer is composed from the organ GEMVs on device-resident tables, no
-// host round trip:
-//   norm -> router, shared-gate logit and shared gate/up GEMVs -> one wave
-//   runs softmax / top-k / renormalise and copies the selected experts'
-//   descriptors into launch tables -> routed gate+up bases (one launch over
-//   2k organs) -> up residuals -> SwiGLU (routed and shared) -> down right
-//   factors -> down left factors -> shared down -> combine
-//   out = h + sum_r w_r y_r (slot order) + sigmoid(g) * shared.
+// Four stream-ordered launches per layer on the int8 matrix-core engine
+// (hk_mfma.h), no host round trip; the route never leaves the device:
+//   1. route:    every block recomputes xn = RMSNorm(1+w)(h) in LDS.  Router
+//                tiles (16 logits each), the shared-expert gate row, and the
+//                shared expert's gate/up tiles (SwiGLU in the epilogue) each
+//                build a q8 x image of xn of their own; the last blocks
+//                build the binary x image of xn for the routed gate/up
+//                (512 columns each) and publish xn.
+//   2. gate/up:  one workgroup per (16-row tile, slot): wave 0 ranks the
+//                logits (softmax / top-k / renormalise) to find the slot's
+//                expert while the others load the binary image; both binary
+//                bases share each image fetch; the epilogue adds the up's
+//                Rice residual in index order (rice_rows) and applies
+//                SwiGLU.  Tile 0 of each slot publishes the slot's two down
+//                factors.
+//   3. down R:   mid_r = R_r act_r (3-bit factor) per (slot, 16-row tile),
+//                and the shared expert's q8 down per 16-row tile.
+//   4. down L:   one workgroup per 16-row output tile, one wave per slot
+//                (y_r = L_r mid_r, an x image per wave); the block combines
+//                out = h + (sum_r w_r y_r in slot order + sigmoid(g) y_s).
+#include <algorithm>
 #include <cmath>
 #include <memory>
 #include <vector>
 
 #include "hk_internal.h"
+#include "hk_mfma.h"
+#include "hk_rice.h"
 #include "hk_router.h"
 #include "hk_router_dev.h"
 
 namespace hk {
 
-// xn = h * (1 / sqrt(mean(h^2) + eps)) * (1 + w) (source_qwen80_residual_rms_norm,
-// model/qwen80_complete_runtime.rs:6778-6797); one block.
-__global__ void __launch_bounds__(1024) moe15_norm_kernel(const float* __restrict__ h, const float* __restrict__ w,
-                                                          uint32_t n, float eps, float* __restrict__ xn,
-                                                          uint32_t* status) {
-    __shared__ float red[16];
-    const uint32_t tid = threadIdx.x;
-    float s = 0.0f;
-    for (uint32_t i = tid; i < n; i += 1024) s += h[i] * h[i];
-    s = wave_sum(s);
-    if ((tid & 63) == 0) red[tid >> 6] = s;
-    __syncthreads();
-    float total = 0.0f;
-    for (int k = 0; k < 16; ++k) total += red[k];
-    const float inv = 1.0f / sqrtf(total / (float)n + eps);
-    bool bad = false;
-    for (uint32_t i = tid; i < n; i += 1024) {
-        const float v = h[i] * inv * (1.0f + w[i]);
-        xn[i] = v;
-        bad |= !isfinite(v);
-    }
-    if (bad) atomicOr(status, HK_DEVERR_NONFINITE);
-}
+constexpr uint32_t M15_MAX_K = 16;  // one wave per slot in the down-L block
+constexpr int M15_D = 4;            // steps in flight per wave
 
-struct Moe15Tables {
-    const OrganView* gate;  // [E]
-    const OrganView* up;    // [E] (the binary bases)
-    const ResView* res;     // [E] (the up residuals)
-    const OrganView* dr;    // [E] right factors (rank x inter)
-    const OrganView* dl;    // [E] left factors (hidden x rank)
-    OrganView* sel_gu;      // [2K]: gate views, then up views
-    ResView* sel_res;       // [K]
-    OrganView* sel_dr;      // [K]
-    OrganView* sel_dl;      // [K]
+struct M15Dims {
+    uint32_t H, I, SI, E, K, rank;
+    float eps;
 };
 
-// One wave: softmax / top-k / renormalise (source_qwen80_topk_router) over
-// the E logits, the weights and ids, and the selected experts' descriptors.
-// An id outside [0, E) (only possible on invalid logits, which set the
-// status) is replaced by 0 so the launches stay in bounds.
-template <int NPL>
-__global__ void __launch_bounds__(64) moe15_select_kernel(const float* __restrict__ logits, uint32_t E, uint32_t K,
-                                                          Moe15Tables t, int32_t* __restrict__ ids_ws,
-                                                          float* __restrict__ w_ws, int32_t* ids_out, float* w_out,
-                                                          uint32_t* status) {
-    __shared__ TopkLds tk;
-    const uint32_t lane = threadIdx.x;
-    const ArgBest mine = softmax_topk_wave<NPL>(logits, E, K, 1, nullptr, nullptr, status, &tk);
-    if (lane < K) {
-        int32_t id = mine.i;
-        if (id < 0 || (uint32_t)id >= E) {
-            atomicOr(status, HK_DEVERR_ROUTE);
-            id = 0;
+// The layer's constants: single organs by value, per-expert tables in device memory.
+struct M15Dev {
+    const float* norm_w;
+    OrganView router, sgate, sg, su, sdown;  // sgate.n_tiles = 0: no shared expert
+    const OrganView* gate;                   // [E] binary gate
+    const OrganView* up;                     // [E] binary base of the HGRAVR02 up
+    const ResView* res;                      // [E] its residual
+    const OrganView* dr;                     // [E] down right factor (rank x I)
+    const OrganView* dl;                     // [E] down left factor (H x rank)
+};
+
+struct M15Ws {
+    float* logits;   // [E]
+    float* gate;     // [2]: shared-gate logit, sigmoid
+    float* xn;       // [H]
+    uint8_t* img;    // binary x image of xn
+    int32_t* img_e;  // [1]
+    float* act;      // [K * I]
+    float* act_s;    // [SI]
+    float* mid;      // [K * rank]
+    float* ys;       // [H] shared expert output (ungated)
+    int32_t* ids;    // [K]
+    float* w;        // [K]
+    OrganView* sel;  // [2K]: right, left factor of each slot
+    uint32_t* status;
+};
+
+__device__ __forceinline__ float dot4(const float4& a, const float4& b) {
+    return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+}
+
+// xn = h * (1 / sqrt(mean(h^2) + eps)) * (1 + w) (source_qwen80_residual_rms_norm,
+// model/qwen80_complete_runtime.rs:6778-6797) into xs (LDS) and, if out is
+// not null, to global memory.  Every thread of the block calls this.
+__device__ void block_rmsnorm(const float* __restrict__ h, const float* __restrict__ w, uint32_t H, float eps,
+                              float* xs, float* red, float* out) {
+    const uint32_t n4 = H / 4u;
+    const float4* h4 = reinterpret_cast<const float4*>(h);
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    float ss = 0.0f;
+    for (uint32_t j = threadIdx.x; j < n4; j += blockDim.x) {
+        const float4 v = ldg(h4 + j);
+        ss += dot4(v, v);
+    }
+    const float inv = 1.0f / sqrtf(block_sum(ss, red) / (float)H + eps);
+    for (uint32_t j = threadIdx.x; j < n4; j += blockDim.x) {
+        const float4 v = ldg(h4 + j), g = ldg(w4 + j);
+        const float4 x = make_float4(v.x * inv * (1.0f + g.x), v.y * inv * (1.0f + g.y), v.z * inv * (1.0f + g.z),
+                                     v.w * inv * (1.0f + g.w));
+        reinterpret_cast<float4*>(xs)[j] = x;
+        if (out) reinterpret_cast<float4*>(out)[j] = x;
+    }
+    __syncthreads();
+}
+
+// The first M15_D steps of [s0, s0 + n) of tile T of organs o[0..R-1].
+template <int KIND, int R>
+__device__ __forceinline__ void fetch_first(const OrganView (&o)[R], uint32_t T, uint32_t s0, uint32_t n, int lane,
+                                            Frag<KIND, R> (&f)[M15_D]) {
+#pragma unroll
+    for (int k = 0; k < M15_D; ++k)
+        if ((uint32_t)k < n)
+#pragma unroll
+            for (int r = 0; r < R; ++r) fetch_one<KIND, R>(o[r], T, s0 + (uint32_t)k, lane, f[k], r);
+}
+
+// Steps [s0, s0 + n) against the x image img (S steps), the first M15_D
+// already fetched into f; acc[r] in units of 2^-E.
+template <int KIND, int R>
+__device__ __forceinline__ void run_steps(const OrganView (&o)[R], uint32_t T, uint32_t s0, uint32_t n,
+                                          const uint8_t* img, uint32_t S, int lane, Frag<KIND, R> (&f)[M15_D],
+                                          float* acc) {
+    const ImageA A{img, a_lane_offset(lane)};
+    const float* SX = reinterpret_cast<const float*>(img + (size_t)S * Kcfg<KIND>::P * A_TILE_STRIDE);
+    const int q = lane >> 4;
+    for (uint32_t it = 0; it < n; it += M15_D) {
+#pragma unroll
+        for (int k = 0; k < M15_D; ++k) {
+            if (it + (uint32_t)k >= n) break;
+            compute_step<KIND, R>(f[k], s0 + it + (uint32_t)k, A, SX, q, acc);
+            const uint32_t nx = it + M15_D + (uint32_t)k;
+            if (nx < n)
+#pragma unroll
+                for (int r = 0; r < R; ++r) fetch_one<KIND, R>(o[r], T, s0 + nx, lane, f[k], r);
         }
-        ids_ws[lane] = id;
-        w_ws[lane] = mine.v;
-        if (ids_out) ids_out[lane] = id;
-        if (w_out) w_out[lane] = mine.v;
-        t.sel_gu[lane] = t.gate[id];
-        t.sel_gu[K + lane] = t.up[id];
-        t.sel_res[lane] = t.res[id];
-        t.sel_dr[lane] = t.dr[id];
-        t.sel_dl[lane] = t.dl[id];
     }
 }
 
-// act_r = silu(g_r) * u_r for the K routed slots (gu = [g_0..g_{K-1}, u_0..u_{K-1}],
-// I each) and act_s = silu(g_s) * u_s for the shared expert (sgu = [g_s, u_s], SI each).
-__global__ void moe15_swiglu_kernel(const float* __restrict__ gu, uint32_t K, uint32_t I,
-                                    const float* __restrict__ sgu, uint32_t SI, float* __restrict__ act,
-                                    float* __restrict__ act_s, uint32_t* status) {
-    const uint32_t n = K * I + SI;
+// The block's 4 waves each hold partial row sums of R organs for tile rows
+// lane % 16; returns, in thread t < 16, the totals of row t (sum over the
+// waves, times 2^-E) in v[0..R-1].  part: 4 * R * 16 floats of LDS.
+template <int R>
+__device__ __forceinline__ void block_rows(const float* acc, float* part, int E, float* v) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float s = tile_row_sum(acc[r]);
+        if (lane < 16) part[(wave * R + (uint32_t)r) * 16u + (uint32_t)lane] = s;
+    }
+    __syncthreads();
+    if (threadIdx.x < 16) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float t = 0.0f;
+            for (uint32_t w = 0; w < 4; ++w) t += part[(w * R + (uint32_t)r) * 16u + threadIdx.x];
+            v[r] = ldexpf(t, -E);
+        }
+    }
+}
+
+// This wave's share [s0, s0 + n) of S steps split over the block's 4 waves.
+__device__ __forceinline__ void wave_share(uint32_t S, uint32_t wave, uint32_t& s0, uint32_t& n) {
+    const uint32_t per = (S + 3u) / 4u;
+    s0 = min(wave * per, S);
+    n = min(s0 + per, S) - s0;
+}
+
+// q8 rows of tile T of o[0..R-1] (cols H) against xn, in a block of its own:
+// the weights' first steps are in flight while xn and its image are built.
+template <int R>
+__device__ __forceinline__ void q8_tile(const M15Dims& d, const M15Dev& L, const float* h, const OrganView (&o)[R],
+                                        uint32_t T, uint8_t* lds, float* red, float* part, uint32_t* status,
+                                        float* v) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t S = n_steps_for(HK_Q8, d.H);
+    uint32_t s0, n;
+    wave_share(S, wave, s0, n);
+    Frag<HK_Q8, R> f[M15_D];
+    fetch_first<HK_Q8, R>(o, T, s0, n, lane, f);
+    float* xs = reinterpret_cast<float*>(lds);  // stage: image columns of H (binary steps)
+    uint8_t* img = lds + (size_t)n_steps_for(HK_BIN, d.H) * 512u * 4u;
+    block_rmsnorm(h, L.norm_w, d.H, d.eps, xs, red, nullptr);
     bool bad = false;
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
-        float g, u;
-        if (i < K * I) {
-            g = gu[i];
-            u = gu[K * I + i];
-        } else {
-            g = sgu[i - K * I];
-            u = sgu[SI + (i - K * I)];
-        }
-        const float a = (g / (1.0f + expf(-g))) * u;
-        if (i < K * I) act[i] = a;
-        else act_s[i - K * I] = a;
-        bad |= !isfinite(a);
-    }
-    if (bad) atomicOr(status, HK_DEVERR_NONFINITE);
+    XChunks<1> xc;
+    load_x<1>(BlockTeam{}, xs, d.H, xc);
+    const int E = x_image<HK_Q8, 1>(BlockTeam{}, xc, xs, d.H, S, img, xs, 8u * blockDim.x, red, &bad);
+    if (bad && threadIdx.x == 0) atomicOr(status, HK_DEVERR_NONFINITE);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    run_steps<HK_Q8, R>(o, T, s0, n, img, S, lane, f, acc);
+    block_rows<R>(acc, part, E, v);
 }
 
-// out = h + ((sum_r yd_r * w_r, in slot order from 0) + ys * sigmoid(glogit)).
-__global__ void moe15_combine_kernel(const float* __restrict__ h, const float* __restrict__ yd, uint32_t K,
-                                     uint32_t H, const float* __restrict__ w, const float* __restrict__ ys,
-                                     const float* __restrict__ glogit, float* __restrict__ out, uint32_t* status) {
-    const float gate = ys ? 1.0f / (1.0f + expf(-glogit[0])) : 0.0f;
-    bool bad = ys && !(isfinite(gate) && gate >= 0.0f && gate <= 1.0f);
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < H; i += gridDim.x * blockDim.x) {
-        float c = 0.0f;
-        for (uint32_t r = 0; r < K; ++r) c += yd[(size_t)r * H + i] * w[r];
-        if (ys) c += ys[i] * gate;
-        const float o = h[i] + c;
-        out[i] = o;
-        bad |= !isfinite(o);
+__global__ void __launch_bounds__(256) m15_route_kernel(M15Dims d, M15Dev L, const float* __restrict__ h, M15Ws ws) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ float red[8];
+    __shared__ float part[4 * 2 * 16];
+    const uint32_t nR = L.router.n_tiles, nG = L.sgate.n_tiles, nS = nG ? L.sg.n_tiles : 0u;
+    const uint32_t b = blockIdx.x;
+    float v[2] = {0.0f, 0.0f};
+    if (b < nR) {
+        const OrganView o[1] = {L.router};
+        q8_tile<1>(d, L, h, o, b, lds, red, part, ws.status, v);
+        const uint32_t row = b * 16u + threadIdx.x;
+        if (threadIdx.x < 16 && row < d.E) ws.logits[row] = v[0];
+    } else if (b < nR + nG) {
+        const OrganView o[1] = {L.sgate};
+        q8_tile<1>(d, L, h, o, 0, lds, red, part, ws.status, v);
+        if (threadIdx.x == 0) {
+            // moe_suffix's shared-expert gate: sigmoid, finite and in [0, 1]
+            const float g = 1.0f / (1.0f + expf(-v[0]));
+            ws.gate[0] = v[0];
+            ws.gate[1] = g;
+            if (!(isfinite(g) && g >= 0.0f && g <= 1.0f)) atomicOr(ws.status, HK_DEVERR_NONFINITE);
+        }
+    } else if (b < nR + nG + nS) {
+        const uint32_t T = b - nR - nG;
+        const OrganView o[2] = {L.sg, L.su};
+        q8_tile<2>(d, L, h, o, T, lds, red, part, ws.status, v);
+        const uint32_t row = T * 16u + threadIdx.x;
+        if (threadIdx.x < 16 && row < d.SI) ws.act_s[row] = (v[0] / (1.0f + expf(-v[0]))) * v[1];
+    } else {
+        // the binary x image of xn, one 512-column step per block; the first publishes xn and E
+        const uint32_t tb = b - nR - nG - nS, S = n_steps_for(HK_BIN, d.H);
+        float* xs = reinterpret_cast<float*>(lds);
+        block_rmsnorm(h, L.norm_w, d.H, d.eps, xs, red, tb == 0 ? ws.xn : nullptr);
+        bool bad = false;
+        XChunks<1> xc;
+        load_x<1>(BlockTeam{}, xs, d.H, xc);
+        const int E = x_image<HK_BIN, 1>(BlockTeam{}, xc, xs, d.H, S, ws.img, xs + tb * 512u, 8u * blockDim.x, red,
+                                         &bad, tb, tb + 1u);
+        if (threadIdx.x == 0) {
+            if (tb == 0) ws.img_e[0] = E;
+            if (bad) atomicOr(ws.status, HK_DEVERR_NONFINITE);
+        }
     }
-    if (bad) atomicOr(status, HK_DEVERR_NONFINITE);
+}
+
+// Gate/up of one (16-row tile, slot).
+template <int NPL>
+__global__ void __launch_bounds__(256) m15_gate_up_kernel(M15Dims d, M15Dev L, M15Ws ws, int32_t* ids_out,
+                                                          float* w_out) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ int32_t sel_id;
+    __shared__ TopkLds tk;
+    __shared__ float part[4 * 2 * 16];
+    const uint32_t slot = blockIdx.y, T = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t S = n_steps_for(HK_BIN, d.H), ib = (uint32_t)x_lds_bytes<HK_BIN>(S);
+    const uint32_t ib16 = (ib + 15u) & ~15u;
+    if (wave == 0) {
+        const bool pub = T == 0 && slot == 0;
+        const ArgBest mine = softmax_topk_wave<NPL>(ws.logits, d.E, d.K, 1, pub ? ws.ids : nullptr,
+                                                    pub ? ws.w : nullptr, pub ? ws.status : nullptr, &tk);
+        if (pub && (uint32_t)lane < d.K) {
+            if (ids_out) ids_out[lane] = mine.i;
+            if (w_out) w_out[lane] = mine.v;
+        }
+        if ((uint32_t)lane == slot) sel_id = mine.i;
+    } else {
+        for (uint32_t o = (threadIdx.x - 64u) * 16u; o < ib; o += (blockDim.x - 64u) * 16u)
+            *reinterpret_cast<uint4*>(lds + o) = ldg(reinterpret_cast<const uint4*>(ws.img + o));
+    }
+    __syncthreads();
+    const int32_t id = sel_id;
+    // an invalid route selects no organ (all-zero down views: n_tiles = 0)
+    const bool ok = id >= 0 && (uint32_t)id < d.E;
+    if (T == 0 && threadIdx.x < 2u * (sizeof(OrganView) / 8u)) {
+        // word copies (a struct assignment here goes through scratch memory)
+        static_assert(sizeof(OrganView) % 8 == 0, "OrganView is copied in 8-byte words");
+        const uint32_t wpv = sizeof(OrganView) / 8u, which = threadIdx.x / wpv, word = threadIdx.x % wpv;
+        const OrganView* tab = which == 0 ? L.dr : L.dl;
+        const uint64_t* from = reinterpret_cast<const uint64_t*>(tab + (ok ? (uint32_t)id : 0u));
+        reinterpret_cast<uint64_t*>(ws.sel + slot * 2u + which)[word] = ok ? from[word] : 0ull;
+        if (!ok && threadIdx.x == 0) atomicOr(ws.status, HK_DEVERR_ROUTE);
+    }
+    if (!ok) return;
+    const OrganView o[2] = {L.gate[id], L.up[id]};
+    if (T >= o[0].n_tiles) return;
+    uint32_t s0, n;
+    wave_share(S, wave, s0, n);
+    Frag<HK_BIN, 2> f[M15_D];
+    fetch_first<HK_BIN, 2>(o, T, s0, n, lane, f);
+    const int E = ws.img_e[0];
+    float acc[2] = {0.0f, 0.0f};
+    run_steps<HK_BIN, 2>(o, T, s0, n, lds, S, lane, f, acc);
+    float v[2] = {0.0f, 0.0f};
+    block_rows<2>(acc, part, E, v);
+    // the up's residual after its base, each row's outliers in index order
+    const uint32_t r0 = T * 16u, r1 = min(r0 + 16u, d.I);
+    float racc[2] = {threadIdx.x < 16 ? v[1] : 0.0f, 0.0f};
+    float* xs = reinterpret_cast<float*>(lds + ib16);
+    rice_rows(L.res[id], ws.xn, r0, r1, racc, xs, xs + d.H);
+    const uint32_t row = r0 + threadIdx.x;
+    if (threadIdx.x < 16 && row < d.I) ws.act[(size_t)slot * d.I + row] = (v[0] / (1.0f + expf(-v[0]))) * racc[0];
+}
+
+// Down right factors (mid_r = R_r act_r) and the shared expert's down.
+__global__ void __launch_bounds__(256) m15_down_r_kernel(M15Dims d, M15Dev L, M15Ws ws) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ float red[8];
+    __shared__ float part[4 * 16];
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nTr = n_tiles_for(d.rank), nR = d.K * nTr;
+    bool bad = false;
+    float v[1] = {0.0f};
+    if (blockIdx.x < nR) {
+        const uint32_t slot = blockIdx.x / nTr, T = blockIdx.x % nTr;
+        const OrganView o[1] = {ws.sel[slot * 2u]};
+        if (T >= o[0].n_tiles) return;
+        const uint32_t S = o[0].steps;
+        uint32_t s0, n;
+        wave_share(S, wave, s0, n);
+        Frag<HK_U3, 1> f[M15_D];
+        fetch_first<HK_U3, 1>(o, T, s0, n, lane, f);
+        float* xs = reinterpret_cast<float*>(lds);
+        uint8_t* img = lds + (size_t)x_image_cols<HK_U3>(S) * 4u;
+        const float* x = ws.act + (size_t)slot * d.I;
+        XChunks<1> xc;
+        load_x<1>(BlockTeam{}, x, d.I, xc);
+        const int E = x_image<HK_U3, 1>(BlockTeam{}, xc, x, d.I, S, img, xs, 0, red, &bad);
+        float acc[1] = {0.0f};
+        run_steps<HK_U3, 1>(o, T, s0, n, img, S, lane, f, acc);
+        block_rows<1>(acc, part, E, v);
+        const uint32_t row = T * 16u + threadIdx.x;
+        if (threadIdx.x < 16 && row < d.rank) ws.mid[(size_t)slot * d.rank + row] = v[0];
+    } else {
+        const uint32_t T = blockIdx.x - nR;
+        const OrganView o[1] = {L.sdown};
+        const uint32_t S = o[0].steps;
+        uint32_t s0, n;
+        wave_share(S, wave, s0, n);
+        Frag<HK_Q8, 1> f[M15_D];
+        fetch_first<HK_Q8, 1>(o, T, s0, n, lane, f);
+        float* xs = reinterpret_cast<float*>(lds);
+        uint8_t* img = lds + (size_t)x_image_cols<HK_Q8>(S) * 4u;
+        XChunks<1> xc;
+        load_x<1>(BlockTeam{}, ws.act_s, d.SI, xc);
+        const int E = x_image<HK_Q8, 1>(BlockTeam{}, xc, ws.act_s, d.SI, S, img, xs, 0, red, &bad);
+        float acc[1] = {0.0f};
+        run_steps<HK_Q8, 1>(o, T, s0, n, img, S, lane, f, acc);
+        block_rows<1>(acc, part, E, v);
+        const uint32_t row = T * 16u + threadIdx.x;
+        if (threadIdx.x < 16 && row < d.H) ws.ys[row] = v[0];
+    }
+    if (bad && threadIdx.x == 0) atomicOr(ws.status, HK_DEVERR_NONFINITE);
+}
+
+// Down left factors and the combine; one wave per slot.
+__global__ void __launch_bounds__(1024) m15_down_l_kernel(M15Dims d, const float* __restrict__ h,
+                                                          float* __restrict__ out, M15Ws ws, uint32_t img_stride,
+                                                          uint32_t stage_floats) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const uint32_t T = blockIdx.x, slots = d.K;
+    const uint32_t slot = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const OrganView o[1] = {ws.sel[slot * 2u + 1u]};
+    const bool active = T < o[0].n_tiles;
+    const uint32_t S = active ? o[0].steps : 0u;
+    Frag<HK_U3, 1> f[M15_D];
+    fetch_first<HK_U3, 1>(o, T, 0u, S, lane, f);
+    uint8_t* img = lds + (size_t)slot * img_stride;
+    float* xs = reinterpret_cast<float*>(lds + (size_t)slots * img_stride) + (size_t)slot * stage_floats;
+    float* part = reinterpret_cast<float*>(lds + (size_t)slots * img_stride) + (size_t)slots * stage_floats;
+    int E = 0;
+    if (active) {
+        bool bad = false;
+        const WaveTeam team{(uint32_t)lane};
+        const float* x = ws.mid + (size_t)slot * d.rank;
+        XChunks<1> xc;
+        load_x<1>(team, x, d.rank, xc);
+        E = x_image<HK_U3, 1>(team, xc, x, d.rank, S, img, xs, 0, nullptr, &bad);
+        if (bad && lane == 0) atomicOr(ws.status, HK_DEVERR_NONFINITE);
+    }
+    float acc[1] = {0.0f};
+    run_steps<HK_U3, 1>(o, T, 0u, S, img, S, lane, f, acc);
+    const float y = tile_row_sum(acc[0]);
+    if (lane < 16) part[slot * 16u + (uint32_t)lane] = active ? ldexpf(y, -E) * ws.w[slot] : 0.0f;
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        // combined = sum_r out_r * w_r in route order, += gate * shared; out = h + combined
+        const uint32_t row = T * 16u + threadIdx.x;
+        float comb = 0.0f;
+        for (uint32_t r = 0; r < slots; ++r) comb += part[r * 16u + threadIdx.x];
+        if (row < d.H) {
+            if (d.SI) comb += ws.ys[row] * ws.gate[1];
+            const float v = h[row] + comb;
+            out[row] = v;
+            if (!isfinite(v)) atomicOr(ws.status, HK_DEVERR_NONFINITE);
+        }
+    }
 }
 
 }  // namespace hk
@@ -134,23 +398,17 @@ __global__ void moe15_combine_kernel(const float* __restrict__ h, const float* _
 using namespace hk;
 
 struct hk_moe15_layer {
-    uint32_t H = 0, I = 0, SI = 0, E = 0, K = 0, rank = 0;
-    float eps = 0.0f;
-    const hk_organ* router = nullptr;
-    const hk_organ* shared_gate = nullptr;
-    const hk_organ* s_down = nullptr;
-    OrganView gate_view{}, dr_view{}, dl_view{}, sgu_view{};
+    M15Dims d{};
+    M15Dev dev{};
+    M15Ws ws{};
     void* mem = nullptr;
-    float* norm_w = nullptr;
-    Moe15Tables t{};
-    OrganView* sgu_set = nullptr;  // [2] shared gate, shared up
-    float *xn = nullptr, *logits = nullptr, *glogit = nullptr, *gu = nullptr, *sgu = nullptr, *act = nullptr,
-          *act_s = nullptr, *mid = nullptr, *yd = nullptr, *ys = nullptr, *w = nullptr;
     float* hbuf = nullptr;  // this layer's output inside a stack
-    int32_t* ids = nullptr;
+    size_t lds_route = 0, lds_gu = 0, lds_dr = 0, lds_dl = 0;
+    uint32_t dl_img_stride = 0, dl_stage = 0, n_route_blocks = 0, n_dr_blocks = 0;
 };
 
 static inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+static inline size_t align16(size_t n) { return (n + 15) & ~(size_t)15; }
 
 static bool same_shape(const OrganView& a, const OrganView& b) {
     return a.kind == b.kind && a.rows == b.rows && a.cols == b.cols && a.group == b.group;
@@ -162,28 +420,33 @@ extern "C" int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* s, h
     if (!s || !s->norm_w || !s->router || !s->gate || !s->up || !s->down_left || !s->down_right)
         return set_error(ctx, HK_E_INVALID_ARG, "hk_moe15_layer_create: NULL argument");
     const uint32_t H = s->hidden, I = s->inter, SI = s->shared_inter, E = s->n_experts, K = s->top_k;
-    if (!H || !I || !E || !K || K > E || K > 64 || E > 512)
-        return set_error(ctx, HK_E_UNSUPPORTED, "mixed-1p5 layer: need 0 < top_k <= min(n_experts, 64), n_experts <= 512");
+    if (!H || !I || !E || !K || K > E || K > M15_MAX_K || E > 512)
+        return set_error(ctx, HK_E_UNSUPPORTED,
+                         "mixed-1p5 layer: need 0 < top_k <= min(n_experts, 16), n_experts <= 512");
     if (!(s->eps >= 0.0f) || !std::isfinite(s->eps)) return set_error(ctx, HK_E_INVALID_ARG, "mixed-1p5 layer: bad eps");
-    if (s->router->view.rows != E || s->router->view.cols != H)
-        return set_error(ctx, HK_E_GEOMETRY, "mixed-1p5 layer: router must be n_experts x hidden");
+    const OrganView& rv = s->router->view;
+    if (rv.rows != E || rv.cols != H || rv.kind != HK_Q8)
+        return set_error(ctx, HK_E_GEOMETRY, "mixed-1p5 layer: router must be a q8 organ of n_experts x hidden");
     if (SI && (!s->shared_gate || !s->shared_gate_proj || !s->shared_up || !s->shared_down))
         return set_error(ctx, HK_E_INVALID_ARG, "mixed-1p5 layer: shared expert organs are NULL");
-    if (SI && (s->shared_gate->view.rows != 1 || s->shared_gate->view.cols != H ||
-               s->shared_gate_proj->view.rows != SI || s->shared_gate_proj->view.cols != H ||
-               !same_shape(s->shared_gate_proj->view, s->shared_up->view) || s->shared_gate_proj->res_dev ||
-               s->shared_up->res_dev || s->shared_down->view.rows != H || s->shared_down->view.cols != SI))
-        return set_error(ctx, HK_E_GEOMETRY, "mixed-1p5 layer: shared expert shapes disagree with hidden/shared_inter");
+    if (SI && (s->shared_gate->view.kind != HK_Q8 || s->shared_gate->view.rows != 1 || s->shared_gate->view.cols != H ||
+               s->shared_gate_proj->view.kind != HK_Q8 || s->shared_gate_proj->view.rows != SI ||
+               s->shared_gate_proj->view.cols != H || !same_shape(s->shared_gate_proj->view, s->shared_up->view) ||
+               s->shared_gate_proj->res_dev || s->shared_up->res_dev || s->shared_down->view.kind != HK_Q8 ||
+               s->shared_down->view.rows != H || s->shared_down->view.cols != SI))
+        return set_error(ctx, HK_E_GEOMETRY,
+                         "mixed-1p5 layer: shared expert organs must be q8 of shapes 1 x hidden, shared_inter x "
+                         "hidden (twice) and hidden x shared_inter");
     const hk_organ *g0 = s->gate[0], *u0 = s->up[0], *l0 = s->down_left[0], *r0 = s->down_right[0];
     if (!g0 || !u0 || !l0 || !r0) return set_error(ctx, HK_E_INVALID_ARG, "mixed-1p5 layer: NULL expert organ");
     const uint32_t rank = r0->view.rows;
     if (g0->view.kind != HK_BIN || g0->view.rows != I || g0->view.cols != H || u0->kind != HK_BIN_RICE ||
-        !same_shape(g0->view, u0->view) || l0->view.rows != H || l0->view.cols != rank || r0->view.cols != I ||
-        rank % 4 || I % 4 || H % 4)
+        !same_shape(g0->view, u0->view) || l0->view.kind != HK_U3 || r0->view.kind != HK_U3 || l0->view.rows != H ||
+        l0->view.cols != rank || r0->view.cols != I || H % 64 || I % 4)
         return set_error(ctx, HK_E_GEOMETRY,
                          "mixed-1p5 layer: experts need a binary gate and an HGRAVR02 up of inter x hidden, and "
-                         "down factors hidden x rank, rank x inter");
-    std::vector<OrganView> gv(E), uv(E), lv(E), rv(E);
+                         "3-bit down factors hidden x rank, rank x inter (hidden a multiple of 64)");
+    std::vector<OrganView> gv(E), uv(E), lv(E), rvv(E);
     std::vector<ResView> res(E);
     for (uint32_t e = 0; e < E; ++e) {
         const hk_organ *g = s->gate[e], *u = s->up[e], *l = s->down_left[e], *r = s->down_right[e];
@@ -194,25 +457,26 @@ extern "C" int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* s, h
         gv[e] = g->view;
         uv[e] = u->view;
         lv[e] = l->view;
-        rv[e] = r->view;
+        rvv[e] = r->view;
         res[e] = u->res;
     }
     std::unique_ptr<hk_moe15_layer> L(new hk_moe15_layer());
-    L->H = H;
-    L->I = I;
-    L->SI = SI;
-    L->E = E;
-    L->K = K;
-    L->rank = rank;
-    L->eps = s->eps;
-    L->router = s->router;
-    L->shared_gate = SI ? s->shared_gate : nullptr;
-    L->s_down = SI ? s->shared_down : nullptr;
-    L->gate_view = g0->view;
-    L->dr_view = r0->view;
-    L->dl_view = l0->view;
-    if (SI) L->sgu_view = s->shared_gate_proj->view;
-    // one allocation: tables, launch tables, workspace (each section 256-B aligned)
+    L->d = M15Dims{H, I, SI, E, K, rank, s->eps};
+    // dynamic LDS of the four kernels (each within 64 KB)
+    const uint32_t Sb = n_steps_for(HK_BIN, H), Sq = n_steps_for(HK_Q8, H), Sr = n_steps_for(HK_U3, I),
+                   Sl = n_steps_for(HK_U3, rank), Ss = SI ? n_steps_for(HK_Q8, SI) : 0u;
+    L->lds_route = (size_t)Sb * 512u * 4u + x_lds_bytes<HK_Q8>(Sq);
+    L->lds_gu = align16(x_lds_bytes<HK_BIN>(Sb)) + (size_t)H * 4u + (size_t)RICE_BATCH * 4u;
+    L->lds_dr = std::max((size_t)x_image_cols<HK_U3>(Sr) * 4u + x_lds_bytes<HK_U3>(Sr),
+                         SI ? (size_t)x_image_cols<HK_Q8>(Ss) * 4u + x_lds_bytes<HK_Q8>(Ss) : (size_t)0);
+    L->dl_img_stride = (uint32_t)align16(x_lds_bytes<HK_U3>(Sl));
+    L->dl_stage = std::min(x_image_cols<HK_U3>(Sl), 8u * 64u);
+    L->lds_dl = (size_t)K * (L->dl_img_stride + L->dl_stage * 4u) + (size_t)K * 16u * 4u;
+    if (std::max({L->lds_route, L->lds_gu, L->lds_dr, L->lds_dl}) > 64u * 1024u)
+        return set_error(ctx, HK_E_UNSUPPORTED, "mixed-1p5 layer: shapes need more than 64 KB of LDS per workgroup");
+    L->n_route_blocks = rv.n_tiles + (SI ? 1u + s->shared_gate_proj->view.n_tiles : 0u) + Sb;
+    L->n_dr_blocks = K * n_tiles_for(rank) + (SI ? n_tiles_for(H) : 0u);
+    // one allocation: tables and workspace (each section 256-B aligned)
     size_t off = 0;
     auto take = [&](size_t bytes) {
         const size_t o = off;
@@ -221,52 +485,52 @@ extern "C" int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* s, h
     };
     const size_t o_norm = take(H * 4), o_gate = take(E * sizeof(OrganView)), o_up = take(E * sizeof(OrganView)),
                  o_res = take(E * sizeof(ResView)), o_dr = take(E * sizeof(OrganView)),
-                 o_dl = take(E * sizeof(OrganView)), o_sgu_tab = take(2 * K * sizeof(OrganView)),
-                 o_sres = take(K * sizeof(ResView)), o_sdr = take(K * sizeof(OrganView)),
-                 o_sdl = take(K * sizeof(OrganView)), o_sset = take(2 * sizeof(OrganView)), o_xn = take(H * 4),
-                 o_logits = take(E * 4), o_glogit = take(16), o_gu = take(2 * (size_t)K * I * 4),
-                 o_sgu = take(2 * (size_t)SI * 4 + 16), o_act = take((size_t)K * I * 4), o_acts = take(SI * 4 + 16),
-                 o_mid = take((size_t)K * rank * 4), o_yd = take((size_t)K * H * 4), o_ys = take(H * 4),
-                 o_w = take(K * 4), o_ids = take(K * 4), o_hbuf = take(H * 4);
+                 o_dl = take(E * sizeof(OrganView)), o_logits = take(E * 4), o_glogit = take(16), o_xn = take(H * 4),
+                 o_img = take(x_lds_bytes<HK_BIN>(Sb)), o_imge = take(4), o_act = take((size_t)K * I * 4),
+                 o_acts = take(SI * 4 + 16), o_mid = take((size_t)K * rank * 4), o_ys = take(H * 4),
+                 o_ids = take(K * 4), o_w = take(K * 4), o_sel = take(2 * K * sizeof(OrganView)),
+                 o_hbuf = take(H * 4);
     if (hipMalloc(&L->mem, off) != hipSuccess) return set_error(ctx, HK_E_NOMEM, "mixed-1p5 layer allocation failed");
     uint8_t* m = static_cast<uint8_t*>(L->mem);
-    L->norm_w = reinterpret_cast<float*>(m + o_norm);
-    L->t.gate = reinterpret_cast<const OrganView*>(m + o_gate);
-    L->t.up = reinterpret_cast<const OrganView*>(m + o_up);
-    L->t.res = reinterpret_cast<const ResView*>(m + o_res);
-    L->t.dr = reinterpret_cast<const OrganView*>(m + o_dr);
-    L->t.dl = reinterpret_cast<const OrganView*>(m + o_dl);
-    L->t.sel_gu = reinterpret_cast<OrganView*>(m + o_sgu_tab);
-    L->t.sel_res = reinterpret_cast<ResView*>(m + o_sres);
-    L->t.sel_dr = reinterpret_cast<OrganView*>(m + o_sdr);
-    L->t.sel_dl = reinterpret_cast<OrganView*>(m + o_sdl);
-    L->sgu_set = reinterpret_cast<OrganView*>(m + o_sset);
-    L->xn = reinterpret_cast<float*>(m + o_xn);
-    L->logits = reinterpret_cast<float*>(m + o_logits);
-    L->glogit = reinterpret_cast<float*>(m + o_glogit);
-    L->gu = reinterpret_cast<float*>(m + o_gu);
-    L->sgu = reinterpret_cast<float*>(m + o_sgu);
-    L->act = reinterpret_cast<float*>(m + o_act);
-    L->act_s = reinterpret_cast<float*>(m + o_acts);
-    L->mid = reinterpret_cast<float*>(m + o_mid);
-    L->yd = reinterpret_cast<float*>(m + o_yd);
-    L->ys = reinterpret_cast<float*>(m + o_ys);
-    L->w = reinterpret_cast<float*>(m + o_w);
-    L->ids = reinterpret_cast<int32_t*>(m + o_ids);
+    M15Dev& dv = L->dev;
+    dv.norm_w = reinterpret_cast<const float*>(m + o_norm);
+    dv.router = rv;
+    if (SI) {
+        dv.sgate = s->shared_gate->view;
+        dv.sg = s->shared_gate_proj->view;
+        dv.su = s->shared_up->view;
+        dv.sdown = s->shared_down->view;
+    }
+    dv.gate = reinterpret_cast<const OrganView*>(m + o_gate);
+    dv.up = reinterpret_cast<const OrganView*>(m + o_up);
+    dv.res = reinterpret_cast<const ResView*>(m + o_res);
+    dv.dr = reinterpret_cast<const OrganView*>(m + o_dr);
+    dv.dl = reinterpret_cast<const OrganView*>(m + o_dl);
+    M15Ws& w = L->ws;
+    w.logits = reinterpret_cast<float*>(m + o_logits);
+    w.gate = reinterpret_cast<float*>(m + o_glogit);
+    w.xn = reinterpret_cast<float*>(m + o_xn);
+    w.img = m + o_img;
+    w.img_e = reinterpret_cast<int32_t*>(m + o_imge);
+    w.act = reinterpret_cast<float*>(m + o_act);
+    w.act_s = reinterpret_cast<float*>(m + o_acts);
+    w.mid = reinterpret_cast<float*>(m + o_mid);
+    w.ys = reinterpret_cast<float*>(m + o_ys);
+    w.ids = reinterpret_cast<int32_t*>(m + o_ids);
+    w.w = reinterpret_cast<float*>(m + o_w);
+    w.sel = reinterpret_cast<OrganView*>(m + o_sel);
+    w.status = ctx->dev_status;
     L->hbuf = reinterpret_cast<float*>(m + o_hbuf);
     auto up_copy = [&](const void* dst, const void* src, size_t bytes) {
         return check_hip(ctx, hipMemcpy(const_cast<void*>(dst), src, bytes, hipMemcpyDefault), "mixed-1p5 layer upload");
     };
-    int rc = up_copy(L->norm_w, s->norm_w, H * 4);
-    if (!rc) rc = up_copy(L->t.gate, gv.data(), E * sizeof(OrganView));
-    if (!rc) rc = up_copy(L->t.up, uv.data(), E * sizeof(OrganView));
-    if (!rc) rc = up_copy(L->t.res, res.data(), E * sizeof(ResView));
-    if (!rc) rc = up_copy(L->t.dr, rv.data(), E * sizeof(OrganView));
-    if (!rc) rc = up_copy(L->t.dl, lv.data(), E * sizeof(OrganView));
-    if (!rc && SI) {
-        const OrganView sv[2] = {s->shared_gate_proj->view, s->shared_up->view};
-        rc = up_copy(L->sgu_set, sv, sizeof sv);
-    }
+    int rc = check_hip(ctx, hipMemset(L->mem, 0, off), "mixed-1p5 layer clear");
+    if (!rc) rc = up_copy(dv.norm_w, s->norm_w, H * 4);
+    if (!rc) rc = up_copy(dv.gate, gv.data(), E * sizeof(OrganView));
+    if (!rc) rc = up_copy(dv.up, uv.data(), E * sizeof(OrganView));
+    if (!rc) rc = up_copy(dv.res, res.data(), E * sizeof(ResView));
+    if (!rc) rc = up_copy(dv.dr, rvv.data(), E * sizeof(OrganView));
+    if (!rc) rc = up_copy(dv.dl, lv.data(), E * sizeof(OrganView));
     if (rc) {
         (void)hipFree(L->mem);
         return rc;
@@ -287,62 +551,22 @@ extern "C" int hk_moe15_decode_layer(hk_ctx* ctx, hk_moe15_layer* L, const float
                                      float* weights, hk_stream stream) {
     if (!ctx) return HK_E_INVALID_ARG;
     if (!L || !h || !out) return set_error(ctx, HK_E_INVALID_ARG, "hk_moe15_decode_layer: NULL argument");
+    if ((reinterpret_cast<uintptr_t>(h) & 15u) != 0)
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_moe15_decode_layer: h must be 16-byte aligned");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const uint32_t H = L->H, I = L->I, SI = L->SI, K = L->K;
-    uint32_t* st = ctx->dev_status;
-    int rc = check_hip(ctx, [&]() {
-        hipLaunchKernelGGL(moe15_norm_kernel, dim3(1), dim3(1024), 0, s, h, L->norm_w, H, L->eps, L->xn, st);
-        return hipGetLastError();
-    }(), "mixed-1p5 norm");
-    if (rc) return rc;
-    auto gemv = [&](const OrganView* views, uint32_t n, const OrganView& sh, const float* x, size_t xs, float* y,
-                    size_t ys, const char* what) {
-        return check_hip(ctx, launch_gemv_tiled(views, n, sh, x, xs, y, ys, s), what);
-    };
-    if ((rc = gemv(static_cast<const OrganView*>(L->router->view_dev), 1, L->router->view, L->xn, 0, L->logits, 0,
-                   "mixed-1p5 router")))
-        return rc;
-    if (SI) {
-        if ((rc = gemv(static_cast<const OrganView*>(L->shared_gate->view_dev), 1, L->shared_gate->view, L->xn, 0,
-                       L->glogit, 0, "mixed-1p5 shared gate")))
-            return rc;
-        if ((rc = gemv(L->sgu_set, 2, L->sgu_view, L->xn, 0, L->sgu, SI, "mixed-1p5 shared gate/up"))) return rc;
-    }
-    rc = check_hip(ctx, [&]() {
-        if (L->E <= 64)
-            hipLaunchKernelGGL((moe15_select_kernel<1>), dim3(1), dim3(64), 0, s, L->logits, L->E, K, L->t, L->ids, L->w,
-                               ids, weights, st);
-        else if (L->E <= 256)
-            hipLaunchKernelGGL((moe15_select_kernel<4>), dim3(1), dim3(64), 0, s, L->logits, L->E, K, L->t, L->ids, L->w,
-                               ids, weights, st);
-        else
-            hipLaunchKernelGGL((moe15_select_kernel<8>), dim3(1), dim3(64), 0, s, L->logits, L->E, K, L->t, L->ids, L->w,
-                               ids, weights, st);
-        return hipGetLastError();
-    }(), "mixed-1p5 select");
-    if (rc) return rc;
-    // routed gate and up bases in one launch (x broadcast), then the up residuals
-    if ((rc = gemv(L->t.sel_gu, 2 * K, L->gate_view, L->xn, 0, L->gu, I, "mixed-1p5 gate/up"))) return rc;
-    if ((rc = check_hip(ctx, launch_rice_apply(L->t.sel_res, K, I, H, L->xn, 0, L->gu + (size_t)K * I, I, s),
-                        "mixed-1p5 up residual")))
-        return rc;
-    rc = check_hip(ctx, [&]() {
-        const uint32_t n = K * I + SI;
-        hipLaunchKernelGGL(moe15_swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, s, L->gu, K, I, L->sgu, SI, L->act,
-                           L->act_s, st);
-        return hipGetLastError();
-    }(), "mixed-1p5 swiglu");
-    if (rc) return rc;
-    if ((rc = gemv(L->t.sel_dr, K, L->dr_view, L->act, I, L->mid, L->rank, "mixed-1p5 down right"))) return rc;
-    if ((rc = gemv(L->t.sel_dl, K, L->dl_view, L->mid, L->rank, L->yd, H, "mixed-1p5 down left"))) return rc;
-    if (SI && (rc = gemv(static_cast<const OrganView*>(L->s_down->view_dev), 1, L->s_down->view, L->act_s, 0, L->ys, 0,
-                         "mixed-1p5 shared down")))
-        return rc;
-    return check_hip(ctx, [&]() {
-        hipLaunchKernelGGL(moe15_combine_kernel, dim3((H + 255) / 256), dim3(256), 0, s, h, L->yd, K, H, L->w,
-                           SI ? L->ys : nullptr, L->glogit, out, st);
-        return hipGetLastError();
-    }(), "mixed-1p5 combine");
+    const M15Dims& d = L->d;
+    hipLaunchKernelGGL(m15_route_kernel, dim3(L->n_route_blocks), dim3(256), L->lds_route, s, d, L->dev, h, L->ws);
+    const dim3 gg(n_tiles_for(d.I), d.K);
+    if (d.E <= 64)
+        hipLaunchKernelGGL((m15_gate_up_kernel<1>), gg, dim3(256), L->lds_gu, s, d, L->dev, L->ws, ids, weights);
+    else if (d.E <= 256)
+        hipLaunchKernelGGL((m15_gate_up_kernel<4>), gg, dim3(256), L->lds_gu, s, d, L->dev, L->ws, ids, weights);
+    else
+        hipLaunchKernelGGL((m15_gate_up_kernel<8>), gg, dim3(256), L->lds_gu, s, d, L->dev, L->ws, ids, weights);
+    hipLaunchKernelGGL(m15_down_r_kernel, dim3(L->n_dr_blocks), dim3(256), L->lds_dr, s, d, L->dev, L->ws);
+    hipLaunchKernelGGL(m15_down_l_kernel, dim3(n_tiles_for(d.H)), dim3(64u * d.K), L->lds_dl, s, d, h, out, L->ws,
+                       L->dl_img_stride, L->dl_stage);
+    return check_hip(ctx, hipGetLastError(), "mixed-1p5 layer launch");
 }
 
 extern "C" int hk_moe15_decode_stack(hk_ctx* ctx, hk_moe15_layer* const* layers, uint32_t n_layers, const float* h,
@@ -350,9 +574,9 @@ extern "C" int hk_moe15_decode_stack(hk_ctx* ctx, hk_moe15_layer* const* layers,
     if (!ctx) return HK_E_INVALID_ARG;
     if (!layers || !n_layers || !h || !out) return set_error(ctx, HK_E_INVALID_ARG, "hk_moe15_decode_stack: NULL argument");
     for (uint32_t l = 0; l < n_layers; ++l)
-        if (!layers[l] || layers[l]->H != layers[0]->H || layers[l]->K != layers[0]->K)
+        if (!layers[l] || layers[l]->d.H != layers[0]->d.H || layers[l]->d.K != layers[0]->d.K)
             return set_error(ctx, HK_E_GEOMETRY, "hk_moe15_decode_stack: layers must share hidden and top_k");
-    const uint32_t K = layers[0]->K;
+    const uint32_t K = layers[0]->d.K;
     const float* cur = h;
     for (uint32_t l = 0; l < n_layers; ++l) {
         float* dst = l + 1 == n_layers ? out : layers[l]->hbuf;
