@@ -16,7 +16,8 @@
 //                logits (softmax / top-k / renormalise) to find the slot's
 //                expert while the others load the binary image; both binary
 //                bases share each image fetch; the epilogue adds the up's
-//                Rice residual in index order (rice_rows) and applies
+//                Rice residual in index order (rice_rows_from, its records
+//                fetched with the weights) and applies
 //                SwiGLU.  Tile 0 of each slot publishes the slot's two down
 //                factors.
 //   3. down R:   mid_r = R_r act_r (3-bit factor) per (slot, 16-row tile),
@@ -259,8 +260,11 @@ __global__ void __launch_bounds__(256) m15_gate_up_kernel(M15Dims d, M15Dev L, M
         }
         if ((uint32_t)lane == slot) sel_id = mine.i;
     } else {
+        // the binary image and xn (for the residual) into LDS
         for (uint32_t o = (threadIdx.x - 64u) * 16u; o < ib; o += (blockDim.x - 64u) * 16u)
             *reinterpret_cast<uint4*>(lds + o) = ldg(reinterpret_cast<const uint4*>(ws.img + o));
+        copy16_to_lds<4>(reinterpret_cast<uint4*>(lds + ib16), reinterpret_cast<const uint4*>(ws.xn), d.H / 4u,
+                         threadIdx.x - 64u, blockDim.x - 64u);
     }
     __syncthreads();
     const int32_t id = sel_id;
@@ -282,16 +286,20 @@ __global__ void __launch_bounds__(256) m15_gate_up_kernel(M15Dims d, M15Dev L, M
     wave_share(S, wave, s0, n);
     Frag<HK_BIN, 2> f[M15_D];
     fetch_first<HK_BIN, 2>(o, T, s0, n, lane, f);
+    // the residual's record ranges and first records, in flight with the weights
+    const ResView rv = L.res[id];
+    const uint32_t r0 = T * 16u, r1 = min(r0 + 16u, d.I);
+    RiceTile rt;
+    rice_prefetch(rv, r0, r1, rt);
     const int E = ws.img_e[0];
     float acc[2] = {0.0f, 0.0f};
     run_steps<HK_BIN, 2>(o, T, s0, n, lds, S, lane, f, acc);
     float v[2] = {0.0f, 0.0f};
     block_rows<2>(acc, part, E, v);
     // the up's residual after its base, each row's outliers in index order
-    const uint32_t r0 = T * 16u, r1 = min(r0 + 16u, d.I);
     float racc[2] = {threadIdx.x < 16 ? v[1] : 0.0f, 0.0f};
     float* xs = reinterpret_cast<float*>(lds + ib16);
-    rice_rows(L.res[id], ws.xn, r0, r1, racc, xs, xs + d.H);
+    rice_rows_from(rv, ws.xn, rt, racc, xs, xs + d.H, true);
     const uint32_t row = r0 + threadIdx.x;
     if (threadIdx.x < 16 && row < d.I) ws.act[(size_t)slot * d.I + row] = (v[0] / (1.0f + expf(-v[0]))) * racc[0];
 }

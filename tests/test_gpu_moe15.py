@@ -5,9 +5,11 @@ router, shared-expert gate and shared expert HGRAVU01 q8 (the oracle gets
 the router and shared gate as their decoded q8 weights, which is
 uniform_factor_matvec_f32's arithmetic).
 
-Router ids must match exactly under the margin rule; weights within 1e-6
-abs; layer outputs within 2e-5 rel-L2 of the oracle's f32 moe_suffix and of
-the FP64 authority on the GPU's ids."""
+Router ids must match exactly under the margin rule; weights within 1e-5
+relative (the q8 router runs on the fixed-point engine, so its logits agree
+with the serial f32 dot to about 1e-7 relative and a peaked softmax carries
+that into its largest weight); layer outputs within 2e-5 rel-L2 of the
+oracle's f32 moe_suffix and of the FP64 authority on the GPU's ids."""
 import sys
 
 import numpy as np
@@ -90,7 +92,7 @@ def _check(ctx, oracle, layer, ref, h, K):
     rout, rids, rw, _, logits = ref.forward(h)
     if U.router_margin_ok(logits, K):
         assert ids.tolist() == rids.tolist()
-        assert np.max(np.abs(w - rw)) <= 1e-6
+        assert np.all(np.abs(w - rw) <= 1e-5 * rw + 1e-7)
         assert oracle.relative_l2(out, rout) < TOL
     assert oracle.relative_l2(out, ref.forward_f64(h, ids)) < TOL
     return ids
@@ -100,6 +102,8 @@ def _check(ctx, oracle, layer, ref, h, K):
     (512, 256, 256, 32, 4, 64),     # one-lane router rows (E <= 64)
     (768, 128, 0, 128, 10, 32),     # no shared expert, E <= 256 form
     (512, 128, 128, 320, 8, 96),    # E > 256 form of the selection
+    (2048, 512, 512, 64, 10, 160),  # the artifact's Qwen3-Next shapes (r160 down), 64 experts
+    (1024, 256, 256, 48, 16, 64),   # the largest top_k (one wave per slot in the down-left block)
 ])
 def test_mixed15_layer_matches_oracle(ctx, oracle, H, I, SI, E, K, rank):
     say("mixed15 layer", H, I, SI, E, K, rank)
