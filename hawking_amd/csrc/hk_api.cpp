@@ -441,7 +441,7 @@ static int repack_into_organ(hk_ctx* ctx, const CanonView& canon, uint32_t n_bin
         return set_error(ctx, HK_E_NOMEM, "organ allocation failed");
     }
     o->view = tiled_place(canon.kind, canon.group, canon.rows, canon.cols, n_bin, n_q2, static_cast<uint8_t*>(o->mem));
-    // the single-organ descriptor and an 8-byte slot (the terminal head's pick)
+    // the single-organ descriptor and a zeroed 16-byte slot (the terminal head's pick key and flag)
     if (hipMalloc(&o->view_dev, align256(sizeof(OrganView)) + 256) != hipSuccess) {
         (void)hipFree(o->mem);
         delete o;
@@ -450,6 +450,7 @@ static int repack_into_organ(hk_ctx* ctx, const CanonView& canon, uint32_t n_bin
     o->head_key = reinterpret_cast<uint64_t*>(static_cast<uint8_t*>(o->view_dev) + align256(sizeof(OrganView)));
     int rc = check_hip(ctx, hipMemcpyAsync(o->view_dev, &o->view, sizeof(OrganView), hipMemcpyHostToDevice, st),
                        "descriptor upload");
+    if (!rc) rc = check_hip(ctx, hipMemsetAsync(o->head_key, 0, 16, st), "pick slot clear");
     if (!rc && canon.kind == HK_F32) {
         rc = check_hip(ctx, hipMemcpyAsync(const_cast<float*>(o->view.dense), canon.dense,
                                            (size_t)canon.rows * canon.cols * 4, hipMemcpyDeviceToDevice, st),
@@ -1029,6 +1030,12 @@ extern "C" int hk_terminal_greedy(hk_ctx* ctx, const float* hidden, const float*
     if (!(eps >= 0.0f) || !std::isfinite(eps)) return set_error(ctx, HK_E_INVALID_ARG, "hk_terminal_greedy: bad eps");
     if (!aligned16(hidden)) return set_error(ctx, HK_E_INVALID_ARG, "hk_terminal_greedy: hidden must be 16-byte aligned");
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (head_gemv_fusable(lm_head->view) && aligned16(norm_w) && aligned16(xn))
+        return check_hip(ctx,
+                         launch_head_fused(static_cast<const OrganView*>(lm_head->view_dev), lm_head->view, hidden,
+                                           norm_w, eps, xn, logits, n_valid, lm_head->head_key, token,
+                                           ctx->dev_status, st),
+                         "terminal head");
     int rc = check_hip(ctx, launch_head_norm(hidden, norm_w, lm_head->view.cols, eps, xn, token, lm_head->head_key,
                                              ctx->dev_status, st),
                        "head norm");

@@ -56,18 +56,85 @@ __host__ __device__ constexpr size_t gemv_hdr_offset(uint32_t steps) {
                                                    ? steps * (uint32_t)Kcfg<KIND>::STEP_COLS : 2048u) * sizeof(float);
 }
 
+// The terminal head's extras (HEAD launches): x = RMSNorm(1+w)(h) is formed
+// from the register chunks before the image is built (workgroup 0 also
+// stores it), and the epilogue reduces the greedy key of the logits below
+// n_valid into key[0] (one 64-bit atomic max per workgroup); a non-finite x
+// sets the low word of key[1].
+struct HeadArgs {
+    const float* norm_w;
+    float eps;
+    float* xn;
+    uint32_t n_valid;
+    uint64_t* key;
+};
+
+// The greedy order of a logit: larger value first, then lower index; NaN
+// never wins (key 0) and -0 ranks as +0.
+__device__ __forceinline__ uint64_t greedy_key(float v, uint32_t i) {
+    if (v != v) return 0ull;
+    const uint32_t b = __float_as_uint(v == 0.0f ? 0.0f : v);
+    const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)ord << 32) | (uint64_t)(~i);
+}
+
+// Block-wide sum (every thread gets it); red: one float per wave.
+__device__ __forceinline__ float block_sum_f(float v, float* red) {
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (uint32_t w = 0; w < (blockDim.x >> 6); ++w) t += red[w];
+    __syncthreads();
+    return t;
+}
+
+// xn = h * (1 / sqrt(mean(h^2) + eps)) * (1 + w) on this thread's register
+// chunks of h (source_qwen80_residual_rms_norm,
+// model/qwen80_complete_runtime.rs:6778-6797); every chunk of h must be in
+// registers (cols <= 8 * 256 * NC).
+template <int NC>
+__device__ __forceinline__ void head_norm_chunks(XChunks<NC>& xc, uint32_t cols, const HeadArgs& ha, float* red) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NC; ++j)
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const float4 v = xc.v[j][k];
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+    const float sum = block_sum_f(ss, red);
+    const float inv = 1.0f / sqrtf(sum / (float)cols + ha.eps);
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        const uint32_t c0 = 8u * (threadIdx.x + 256u * (uint32_t)j);
+        if (c0 < cols) {
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const float4 g = ldg(reinterpret_cast<const float4*>(ha.norm_w + c0) + k);
+                float4& v = xc.v[j][k];
+                v = make_float4(v.x * inv * (1.0f + g.x), v.y * inv * (1.0f + g.y), v.z * inv * (1.0f + g.z),
+                                v.w * inv * (1.0f + g.w));
+                if (blockIdx.x == 0) reinterpret_cast<float4*>(ha.xn + c0)[k] = v;
+            }
+        }
+    }
+}
+
 // D-deep software pipeline: D fetched steps are in flight while one is
 // consumed; slot d of the rotating buffer holds item it+d.  The loop body is
 // branch-free in memory operations (refetches are unconditional, past the end
 // they re-read the last item; y goes out through LDS after the loop) so the
 // compiler can wait for exactly the slot being consumed.
-template <int KIND, int R, int D, int NC>
+template <int KIND, int R, int D, int NC, bool HEAD>
 __global__ void __launch_bounds__(256)
 gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const float* __restrict__ xall,
                   size_t x_stride, float* __restrict__ yall, size_t y_stride, uint32_t tiles_per_wg, uint32_t parts,
-                  uint32_t* status) {
+                  uint32_t* status, HeadArgs ha) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float red[4];
+    __shared__ uint64_t kred[HEAD ? 4 : 1];
     uint32_t oi, part;
     organ_part(blockIdx.x, parts, n_organs, &oi, &part);
     const OrganView o = organs[oi];
@@ -116,10 +183,13 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const
             if (i < nh) hsh[i] = hreg[k];
         }
     }
+    if constexpr (HEAD) head_norm_chunks<NC>(xc, o.cols, ha, red);
     bool bad = false;
     float* xq = reinterpret_cast<float*>(lds + x_lds_bytes<KIND>(o.steps));
     const int E = x_image<KIND, NC>(BlockTeam{}, xc, x, o.cols, o.steps, lds, xq, 0u, red, &bad);
     if (bad && threadIdx.x == 0 && status) atomicOr(status, 1u);
+    if constexpr (HEAD)
+        if (bad && threadIdx.x == 0) atomicOr(reinterpret_cast<uint32_t*>(ha.key + 1), 1u);
     const ImageA A{lds, a_lane_offset(lane)};
     const float* SX = reinterpret_cast<const float*>(lds + (size_t)o.steps * Kcfg<KIND>::P * A_TILE_STRIDE);
 
@@ -154,9 +224,24 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const
     }
     __syncthreads();
     const uint32_t nrows = (t1 > t0 ? t1 - t0 : 0u) * 16u;
+    uint64_t best = 0;
     for (uint32_t i = threadIdx.x; i < nrows; i += blockDim.x) {
         const uint32_t row = t0 * 16u + i;
-        if (row < o.rows) y[row] = ldexpf(ysh[i], -E);
+        if (row < o.rows) {
+            const float v = ldexpf(ysh[i], -E);
+            y[row] = v;
+            if constexpr (HEAD)
+                if (row < ha.n_valid) best = max(best, greedy_key(v, row));
+        }
+    }
+    if constexpr (HEAD) {
+        for (int off = 32; off; off >>= 1) best = max(best, (uint64_t)__shfl_xor((unsigned long long)best, off, 64));
+        if ((threadIdx.x & 63) == 0) kred[threadIdx.x >> 6] = best;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            best = max(max(kred[0], kred[1]), max(kred[2], kred[3]));
+            if (best) atomicMax(reinterpret_cast<unsigned long long*>(ha.key), (unsigned long long)best);
+        }
     }
 }
 
@@ -190,9 +275,10 @@ size_t gemv_lds_bytes(int kind, uint32_t cols) {
     return gemv_hdr_offset<HK_MIXED>(S) + (size_t)GEMV_MAX_MIXED_TILES_PER_WG * S * sizeof(uint4) + ysh;
 }
 
-template <int KIND, int R, int D>
+template <int KIND, int R, int D, bool HEAD = false>
 static hipError_t launch_kind(const OrganView* organs, uint32_t n, const OrganView& sh, const float* x,
-                              size_t xs, float* y, size_t ys, uint32_t tpw, hipStream_t s) {
+                              size_t xs, float* y, size_t ys, uint32_t tpw, hipStream_t s, const HeadArgs& ha = {},
+                              uint32_t* status = nullptr) {
     const uint32_t parts = (sh.n_tiles + tpw - 1) / tpw;
     const dim3 grid(parts * n);
     // image + one quantization window (2048 columns); x chunks held in
@@ -201,11 +287,11 @@ static hipError_t launch_kind(const OrganView* organs, uint32_t n, const OrganVi
     const size_t lds = gemv_hdr_offset<KIND>(sh.steps) + (KIND == HK_MIXED ? (size_t)tpw * sh.steps * sizeof(uint4) : 0) +
                        (size_t)tpw * 16u * sizeof(float);
     if (kc <= 2048u)
-        hipLaunchKernelGGL((gemv_tiled_kernel<KIND, R, D, 1>), grid, dim3(256), lds, s, organs, n, x, xs, y, ys, tpw,
-                           parts, nullptr);
+        hipLaunchKernelGGL((gemv_tiled_kernel<KIND, R, D, 1, HEAD>), grid, dim3(256), lds, s, organs, n, x, xs, y, ys,
+                           tpw, parts, status, ha);
     else
-        hipLaunchKernelGGL((gemv_tiled_kernel<KIND, R, D, 4>), grid, dim3(256), lds, s, organs, n, x, xs, y, ys, tpw,
-                           parts, nullptr);
+        hipLaunchKernelGGL((gemv_tiled_kernel<KIND, R, D, 4, HEAD>), grid, dim3(256), lds, s, organs, n, x, xs, y, ys,
+                           tpw, parts, status, ha);
     return hipGetLastError();
 }
 
@@ -233,6 +319,43 @@ static hipError_t launch_r(const OrganView* organs, uint32_t n, const OrganView&
     if (tiles >= 4096) return launch_kind<KIND, 2, 2>(organs, n, sh, x, xs, y, ys, 8, s);
     const uint32_t tpw = (uint64_t)n * ((sh.n_tiles + 3) / 4) >= 256 ? 4 : 1;
     return launch_kind<KIND, 1, 2>(organs, n, sh, x, xs, y, ys, tpw, s);
+}
+
+// The terminal head on a q8 lm_head (cols <= 8192): one GEMV launch with the
+// norm prologue and the greedy-key epilogue, then the one-thread pick (which
+// also clears the key for the next call).  Launch shapes as for one q8 organ.
+__global__ void head_pick_fused_kernel(uint64_t* __restrict__ key, int32_t* __restrict__ token, uint32_t* status) {
+    if (threadIdx.x == 0) {
+        const uint64_t best = key[0];
+        const uint32_t flag = reinterpret_cast<const uint32_t*>(key + 1)[0];
+        const uint32_t ord = (uint32_t)(best >> 32);
+        const float v = __uint_as_float((ord & 0x80000000u) ? (ord & 0x7FFFFFFFu) : ~ord);
+        const bool ok = best != 0ull && isfinite(v) && flag == 0u;
+        token[0] = ok ? (int32_t)(~(uint32_t)best) : -1;
+        if (!ok) atomicOr(status, 1u);
+        key[0] = 0ull;
+        key[1] = 0ull;
+    }
+}
+
+bool head_gemv_fusable(const OrganView& sh) { return sh.kind == HK_Q8 && x_image_cols<HK_Q8>(sh.steps) <= 8192u; }
+
+hipError_t launch_head_fused(const OrganView* organ_dev, const OrganView& sh, const float* h, const float* norm_w,
+                             float eps, float* xn, float* logits, uint32_t n_valid, uint64_t* key, int32_t* token,
+                             uint32_t* status, hipStream_t s) {
+    if (!head_gemv_fusable(sh)) return hipErrorInvalidValue;
+    const HeadArgs ha{norm_w, eps, xn, n_valid, key};
+    hipError_t e;
+    if (sh.n_tiles >= 16384u)
+        e = launch_kind<HK_Q8, 2, 3, true>(organ_dev, 1, sh, h, 0, logits, 0, 16, s, ha, status);
+    else if (sh.n_tiles >= 4096u)
+        e = launch_kind<HK_Q8, 2, 2, true>(organ_dev, 1, sh, h, 0, logits, 0, 8, s, ha, status);
+    else
+        e = launch_kind<HK_Q8, 1, 2, true>(organ_dev, 1, sh, h, 0, logits, 0, (sh.n_tiles + 3) / 4 >= 256 ? 4 : 1, s,
+                                          ha, status);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(head_pick_fused_kernel, dim3(1), dim3(64), 0, s, key, token, status);
+    return hipGetLastError();
 }
 
 hipError_t launch_gemv_tiled(const OrganView* organs_dev, uint32_t n, const OrganView& sh, const float* x,

@@ -255,6 +255,13 @@ hipError_t launch_head_norm(const float* h, const float* w, uint32_t n, float ep
                             uint64_t* key, uint32_t* status, hipStream_t s);
 hipError_t launch_head_argmax(const float* logits, uint32_t n_valid, uint64_t* key, int32_t* token, uint32_t* status,
                               hipStream_t s);
+// The fused form for a q8 lm_head of at most 8192 columns: the GEMV forms the
+// norm itself and reduces the greedy key (key: 16 zeroed bytes, left zeroed),
+// then one pick; h, norm_w and xn 16-byte aligned.
+bool head_gemv_fusable(const OrganView& sh);
+hipError_t launch_head_fused(const OrganView* organ_dev, const OrganView& sh, const float* h, const float* norm_w,
+                             float eps, float* xn, float* logits, uint32_t n_valid, uint64_t* key, int32_t* token,
+                             uint32_t* status, hipStream_t s);
 
 // Device bytes of the tiled layout (sections 256-B aligned); mixed needs n_bin/n_q2.
 size_t tiled_bytes(int kind, int group, uint32_t rows, uint32_t cols, uint32_t n_bin, uint32_t n_q2,

@@ -176,9 +176,13 @@ __device__ __forceinline__ void load_x(const Team& team, const float* x, uint32_
     for (int j = 0; j < NC; ++j) load_chunk(x, 8u * (team.idx() + (uint32_t)j * team.size()), cols, xc.v[j]);
 }
 
+// max |v| of a chunk, +inf if any element is NaN (fmaxf drops NaN operands,
+// so a NaN must become a value the max keeps for the non-finite check).
 __device__ __forceinline__ float max_abs8(const float4* v) {
-    return fmaxf(fmaxf(fmaxf(fabsf(v[0].x), fabsf(v[0].y)), fmaxf(fabsf(v[0].z), fabsf(v[0].w))),
-                 fmaxf(fmaxf(fabsf(v[1].x), fabsf(v[1].y)), fmaxf(fabsf(v[1].z), fabsf(v[1].w))));
+    const float m = fmaxf(fmaxf(fmaxf(fabsf(v[0].x), fabsf(v[0].y)), fmaxf(fabsf(v[0].z), fabsf(v[0].w))),
+                          fmaxf(fmaxf(fabsf(v[1].x), fabsf(v[1].y)), fmaxf(fabsf(v[1].z), fabsf(v[1].w))));
+    const float s = v[0].x + v[0].y + v[0].z + v[0].w + v[1].x + v[1].y + v[1].z + v[1].w;
+    return s != s ? INFINITY : m;  // a NaN sum: a NaN, or +inf with -inf
 }
 
 __device__ __forceinline__ int32_t quantize8(const float4* v, int E, float* f) {

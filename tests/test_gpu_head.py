@@ -76,14 +76,17 @@ def test_terminal_head_tie_and_mask(ctx, oracle):
     assert lg[37] == lg[900] and lg[1010] > lg[37]
 
 
-def test_terminal_head_flags_nonfinite(ctx, oracle):
+@pytest.mark.parametrize("value", [np.inf, np.nan])
+def test_terminal_head_flags_nonfinite(ctx, oracle, value):
+    """A non-finite hidden state (inf, or a NaN, which a plain max would
+    drop) gives token -1 and HK_E_NONFINITE; the next good call recovers."""
     from hawking_amd._lib import HK_E_NONFINITE, HawkingError
     vocab, hidden_n = 256, 256
     h, nw, w = _inputs(oracle, vocab, hidden_n, "e")
     head, _ = _head(ctx, oracle, w, nw, vocab)
     bad = h.copy()
-    bad[7] = np.inf
-    say("terminal head non-finite")
+    bad[7] = value
+    say("terminal head non-finite", value)
     with pytest.raises(HawkingError) as e:
         head.greedy(bad)
     assert e.value.code == HK_E_NONFINITE
