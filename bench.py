@@ -100,9 +100,9 @@ def streamed(ctx, name, steps, warmup, n_organs=None):
 
 def lowrank_streamed(ctx, steps, warmup, rows=2048, rank=160, cols=768, n=4096):
     """HGRAVS01 r160 (3-bit factors) as the routed down_proj shape: n low-rank
-    organs, mid_i = R_i x_i for all i in one launch, then y_i = L_i mid_i in a
-    second.  Algorithmic bytes: the canonical packed factors plus x, mid
-    (written and read) and y."""
+    organs, y_i = L_i (R_i x_i) for all i in one launch (hk_gemv_lowrank_set:
+    one workgroup per pair, mid kept on chip).  Algorithmic bytes: the
+    canonical packed factors plus x and y."""
     from hawking_amd import organs
     lefts, rights = [], []
     for i in range(n):
@@ -114,14 +114,13 @@ def lowrank_streamed(ctx, steps, warmup, rows=2048, rank=160, cols=768, n=4096):
     ls, rs = organs.OrganSet(ctx, lefts), organs.OrganSet(ctx, rights)
     x = ctx.empty((n, cols))
     ctx.call("hk_synth_normal", organs.stream_key(SEED, 0xB50001), 0, n * cols, 1.0, x.ptr, ctx.stream)
-    mid, y = ctx.empty((n, rank)), ctx.empty((n, rows))
+    y = ctx.empty((n, rows))
 
     def step():
-        rs.gemv(x, cols, mid, rank)
-        ls.gemv(mid, rank, y, rows)
+        organs.gemv_lowrank_set(ctx, ls, rs, x, cols, y, rows)
 
     ms = time_launches(ctx, step, steps, warmup)
-    nbytes = ls.packed_bytes + rs.packed_bytes + n * (cols + 2 * rank + rows) * 4
+    nbytes = ls.packed_bytes + rs.packed_bytes + n * (cols + rows) * 4
     return {"gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
             "us_per_step": round(ms * 1e3, 1), "organs": n, "shape": [rows, rank, cols],
             "packed_bytes_per_organ": round((ls.packed_bytes + rs.packed_bytes) / n, 1)}

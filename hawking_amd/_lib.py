@@ -115,6 +115,7 @@ PROTOTYPES = {
                                 C.POINTER(_u32), C.POINTER(_sz)]),
     "hk_gemv": (C.c_int, [_p, _p, _p, _p, _p]),
     "hk_gemv_lowrank": (C.c_int, [_p, _p, _p, _p, _p, _p, _p]),
+    "hk_gemv_lowrank_set": (C.c_int, [_p, _p, _p, _p, _sz, _p, _sz, _p]),
     "hk_organ_upload_rice": (C.c_int, [_p, C.POINTER(RiceQ1Src), _p, C.POINTER(_p)]),
     "hk_rice_apply": (C.c_int, [_p, _p, _p, _p, _p]),
     "hk_terminal_greedy": (C.c_int, [_p, _p, _p, C.c_float, _p, _u32, _p, _p, _p, _p]),

@@ -551,6 +551,12 @@ extern "C" int hk_gemv_lowrank(hk_ctx* ctx, const hk_organ* left, const hk_organ
     int rc = check_vectors(ctx, "hk_gemv_lowrank", x, 0, mid, 0, 1, right->view);
     if (!rc) rc = check_vectors(ctx, "hk_gemv_lowrank", mid, 0, y, 0, 1, left->view);
     if (rc) return rc;
+    if (lowrank_fusable(left->view, right->view))
+        return check_hip(ctx,
+                         launch_lowrank(static_cast<const OrganView*>(left->view_dev),
+                                        static_cast<const OrganView*>(right->view_dev), 1, left->view, right->view, x, 0,
+                                        mid, 0, y, 0, nullptr, static_cast<hipStream_t>(stream)),
+                         "low-rank launch");
     // stream order carries mid from the first launch to the second
     rc = hk_gemv(ctx, right, x, mid, stream);
     return rc ? rc : hk_gemv(ctx, left, mid, y, stream);
@@ -633,6 +639,32 @@ extern "C" int hk_gemv_set(hk_ctx* ctx, const hk_organ_set* set, const float* x,
         rc = check_hip(ctx, launch_rice_apply(set->res_dev, set->n, set->first.rows, set->first.cols, x, x_stride, y,
                                               y_stride, st),
                        "rice apply");
+    return rc;
+}
+
+extern "C" int hk_gemv_lowrank_set(hk_ctx* ctx, const hk_organ_set* left, const hk_organ_set* right, const float* x,
+                                   size_t x_stride, float* y, size_t y_stride, hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (!left || !right) return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv_lowrank_set: NULL set");
+    if (left->n != right->n || right->first.rows != left->first.cols)
+        return set_error(ctx, HK_E_GEOMETRY,
+                         "hk_gemv_lowrank_set: the sets need as many organs and right rows (the rank) = left cols");
+    int rc = check_vectors(ctx, "hk_gemv_lowrank_set", x, x_stride, y, y_stride, left->n, right->first);
+    if (!rc && left->n > 1 && y_stride < left->first.rows)
+        rc = set_error(ctx, HK_E_GEOMETRY, "hk_gemv_lowrank_set: y stride smaller than the left factor's rows");
+    if (rc) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (lowrank_fusable(left->first, right->first))
+        return check_hip(ctx,
+                         launch_lowrank(left->dev, right->dev, left->n, left->first, right->first, x, x_stride, nullptr,
+                                        0, y, y_stride, nullptr, st),
+                         "low-rank set launch");
+    // other shapes: two launches through a mid buffer in the context's scratch
+    const size_t ms = (right->first.rows + 3u) & ~3u;
+    void* mid = nullptr;
+    rc = ensure_scratch(ctx, (size_t)left->n * ms * sizeof(float), &mid);
+    if (!rc) rc = hk_gemv_set(ctx, right, x, x_stride, static_cast<float*>(mid), ms, stream);
+    if (!rc) rc = hk_gemv_set(ctx, left, static_cast<const float*>(mid), ms, y, y_stride, stream);
     return rc;
 }
 

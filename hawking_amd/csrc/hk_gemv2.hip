@@ -245,6 +245,148 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const
     }
 }
 
+// One wave's walk over the row tiles [t0, t1) of organ o in groups of R tiles
+// (stride 4R over the block's four waves), every step of each, D steps in
+// flight -- the main loop of gemv_tiled_kernel for the non-mixed kinds.
+// start() issues the first D fetches (before the caller builds its x image);
+// run() consumes the walk against an x image, leaving the unscaled row totals
+// in ysh[(tile - t0) * 16 + row].
+template <int KIND, int R, int D>
+struct TileWalk {
+    WaveItems W;
+    uint32_t last;
+    Frag<KIND, R> f[D];
+    uint32_t T[D][R], ts[D];
+    int nv[D];
+
+    __device__ __forceinline__ void start(const OrganView& o, uint32_t t0, uint32_t t1, uint32_t wave, int lane) {
+        W = WaveItems{t0 + wave * R, 4u * R, t1, o.steps, 0};
+        W.n = W.g0 < t1 ? ((t1 - W.g0 + W.gstride - 1) / W.gstride) * o.steps : 0;
+        last = W.n ? W.n - 1u : 0u;
+        // a wave without items re-reads tile t0 (its results are never used)
+        const WaveItems P = W.n ? W : WaveItems{t0, 4u * R, t0 + 1u, o.steps, 1u};
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            P.at(min((uint32_t)d, last), T[d], R, &nv[d], &ts[d]);
+            fetch_step<KIND, R>(o, T[d], nv[d], ts[d], lane, f[d]);
+        }
+    }
+
+    __device__ __forceinline__ void run(const OrganView& o, uint32_t t0, const uint8_t* img, int lane, float* ysh) {
+        const ImageA A{img, a_lane_offset(lane)};
+        const float* SX = reinterpret_cast<const float*>(img + (size_t)o.steps * Kcfg<KIND>::P * A_TILE_STRIDE);
+        const int q = lane >> 4;
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+        uint32_t it = 0;
+        for (; it + D <= W.n; it += D) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                compute_step<KIND, R>(f[d], ts[d], A, SX, q, acc);
+                if (ts[d] + 1 == o.steps) flush_group<R>(acc, T[d], nv[d], t0, lane, ysh);
+                W.at(min(it + D + d, last), T[d], R, &nv[d], &ts[d]);
+                fetch_step<KIND, R>(o, T[d], nv[d], ts[d], lane, f[d]);
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (it + d >= W.n) break;
+            compute_step<KIND, R>(f[d], ts[d], A, SX, q, acc);
+            if (ts[d] + 1 == o.steps) flush_group<R>(acc, T[d], nv[d], t0, lane, ysh);
+        }
+    }
+};
+
+// LDS layout of the low-rank kernel: the right factor's x image and window,
+// mid (16 floats per right tile), the left factor's image and window, then
+// the left rows.
+struct LowrankLds {
+    size_t img_r, win_r, mid, img_l, win_l, ysh, total;
+};
+__host__ __device__ inline LowrankLds lowrank_lds(const OrganView& l, const OrganView& r) {
+    LowrankLds L{};
+    L.img_r = 0;
+    L.win_r = L.img_r + x_lds_bytes<HK_U3>(r.steps);
+    const uint32_t cr = x_image_cols<HK_U3>(r.steps), cl = x_image_cols<HK_U3>(l.steps);
+    L.mid = L.win_r + (size_t)(cr < 2048u ? cr : 2048u) * 4u;
+    L.img_l = L.mid + ((size_t)r.n_tiles * 16u * 4u + 15u) / 16u * 16u;
+    L.win_l = L.img_l + x_lds_bytes<HK_U3>(l.steps);
+    L.ysh = L.win_l + (size_t)(cl < 2048u ? cl : 2048u) * 4u;
+    L.total = L.ysh + (size_t)l.n_tiles * 16u * 4u;
+    return L;
+}
+
+// HGRAVS01 pairs y_i = L_i (R_i x_i), one workgroup per pair: the right
+// factor's rows (mid, kept in LDS) and then the left factor's, whose first
+// weight steps are already in flight while mid is computed.  The arithmetic
+// is that of two gemv_tiled_kernel launches (mid rounded to f32, then its own
+// x image), so the result is the same bits.  mid_all (may be null) also
+// receives mid.
+template <int NC>
+__global__ void __launch_bounds__(256)
+lowrank_kernel(const OrganView* __restrict__ lefts, const OrganView* __restrict__ rights, uint32_t n,
+               const float* __restrict__ xall, size_t x_stride, float* __restrict__ mid_all, size_t mid_stride,
+               float* __restrict__ yall, size_t y_stride, uint32_t* status) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ float red[4];
+    uint32_t oi, part;
+    organ_part(blockIdx.x, 1, n, &oi, &part);
+    const OrganView rv = rights[oi], lv = lefts[oi];
+    const float* __restrict__ x = xall + (size_t)oi * x_stride;
+    float* __restrict__ y = yall + (size_t)oi * y_stride;
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const LowrankLds M = lowrank_lds(lv, rv);
+    float* mid = reinterpret_cast<float*>(lds + M.mid);
+    float* ysh = reinterpret_cast<float*>(lds + M.ysh);
+
+    XChunks<NC> xc;
+    load_x<NC>(BlockTeam{}, x, rv.cols, xc);
+    TileWalk<HK_U3, 1, 3> wr;
+    wr.start(rv, 0, rv.n_tiles, wave, lane);
+    TileWalk<HK_U3, 2, 3> wl;
+    wl.start(lv, 0, lv.n_tiles, wave, lane);
+    bool bad = false, bad2 = false;
+    const int E1 = x_image<HK_U3, NC>(BlockTeam{}, xc, x, rv.cols, rv.steps, lds + M.img_r,
+                                      reinterpret_cast<float*>(lds + M.win_r), 0u, red, &bad);
+    wr.run(rv, 0, lds + M.img_r, lane, mid);
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < rv.rows; i += blockDim.x) {
+        const float m = ldexpf(mid[i], -E1);
+        mid[i] = m;
+        if (mid_all) mid_all[(size_t)oi * mid_stride + i] = m;
+    }
+    __syncthreads();
+    XChunks<1> xm;
+    load_x<1>(BlockTeam{}, mid, rv.rows, xm);
+    const int E2 = x_image<HK_U3, 1>(BlockTeam{}, xm, mid, rv.rows, lv.steps, lds + M.img_l,
+                                     reinterpret_cast<float*>(lds + M.win_l), 0u, red, &bad2);
+    wl.run(lv, 0, lds + M.img_l, lane, ysh);
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < lv.rows; i += blockDim.x) y[i] = ldexpf(ysh[i], -E2);
+    if ((bad || bad2) && threadIdx.x == 0 && status) atomicOr(status, 1u);
+}
+
+bool lowrank_fusable(const OrganView& l, const OrganView& r) {
+    return l.kind == HK_U3 && r.kind == HK_U3 && r.rows == l.cols && r.cols <= 8192u && r.rows <= 2048u &&
+           lowrank_lds(l, r).total <= GEMV_LDS_LIMIT;
+}
+
+hipError_t launch_lowrank(const OrganView* lefts, const OrganView* rights, uint32_t n, const OrganView& l,
+                          const OrganView& r, const float* x, size_t x_stride, float* mid, size_t mid_stride, float* y,
+                          size_t y_stride, uint32_t* status, hipStream_t s) {
+    if (!lowrank_fusable(l, r)) return hipErrorInvalidValue;
+    const size_t lds = lowrank_lds(l, r).total;
+    if (x_image_cols<HK_U3>(r.steps) <= 2048u)
+        hipLaunchKernelGGL(lowrank_kernel<1>, dim3(n), dim3(256), lds, s, lefts, rights, n, x, x_stride, mid,
+                           mid_stride, y, y_stride, status);
+    else
+        hipLaunchKernelGGL(lowrank_kernel<4>, dim3(n), dim3(256), lds, s, lefts, rights, n, x, x_stride, mid,
+                           mid_stride, y, y_stride, status);
+    return hipGetLastError();
+}
+
 // Dense f32 rows (router, shared-expert gate): one wave per row, float4 loads.
 __global__ void __launch_bounds__(256) gemv_f32_kernel(const OrganView* __restrict__ organs,
                                                        const float* __restrict__ xall, size_t x_stride,

@@ -255,6 +255,15 @@ hipError_t launch_head_norm(const float* h, const float* w, uint32_t n, float ep
                             uint64_t* key, uint32_t* status, hipStream_t s);
 hipError_t launch_head_argmax(const float* logits, uint32_t n_valid, uint64_t* key, int32_t* token, uint32_t* status,
                               hipStream_t s);
+// HGRAVS01 pairs y_i = L_i (R_i x_i) (3-bit factors, right rows = left cols)
+// in one launch, one workgroup per pair; mid (may be null) receives R_i x_i.
+// lowrank_fusable: the shapes this kernel takes (right cols <= 8192, rank <=
+// 2048, LDS within the cap); launch_lowrank returns hipErrorInvalidValue
+// otherwise.
+bool lowrank_fusable(const OrganView& l, const OrganView& r);
+hipError_t launch_lowrank(const OrganView* lefts, const OrganView* rights, uint32_t n, const OrganView& l,
+                          const OrganView& r, const float* x, size_t x_stride, float* mid, size_t mid_stride, float* y,
+                          size_t y_stride, uint32_t* status, hipStream_t s);
 // The fused form for a q8 lm_head of at most 8192 columns: the GEMV forms the
 // norm itself and reduces the greedy key (key: 16 zeroed bytes, left zeroed),
 // then one pick; h, norm_w and xn 16-byte aligned.

@@ -339,6 +339,14 @@ class OrganSet:
             pass
 
 
+def gemv_lowrank_set(ctx: Context, lefts: OrganSet, rights: OrganSet, x: DeviceArray, x_stride: int,
+                     y: DeviceArray, y_stride: int, stream=None) -> None:
+    """y_i = L_i (R_i x_i) over the HGRAVS01 pairs of two organ sets in one
+    launch (hk_gemv_lowrank_set)."""
+    ctx.call("hk_gemv_lowrank_set", lefts.h, rights.h, x.ptr, x_stride, y.ptr, y_stride,
+             stream if stream is not None else ctx.stream)
+
+
 def gemv_batch(ctx: Context, organs: list[PackedOrgan], x: DeviceArray, x_stride: int, y: DeviceArray,
                y_stride: int, stream=None) -> None:
     """y_i = W_i x_i for organs of one kind and shape, in one launch."""

@@ -193,12 +193,21 @@ int hk_organ_set_free(hk_ctx* ctx, hk_organ_set* set);
 int hk_gemv_set(hk_ctx* ctx, const hk_organ_set* set, const float* x, size_t x_stride, float* y,
                 size_t y_stride, hk_stream stream);
 
-/* HGRAVS01 low-rank organ: mid[rank] = right x, then y[rows] = left mid, two
- * launches ordered on `stream` (mid is a caller buffer of rank floats, 16-byte
- * aligned).  The factors are HK_U3 organs (left rows x rank, right rank x cols).
+/* HGRAVS01 low-rank organ: mid[rank] = right x, then y[rows] = left mid (mid
+ * is a caller buffer of rank floats, 16-byte aligned, and receives R x).  The
+ * factors are HK_U3 organs (left rows x rank, right rank x cols); one launch
+ * when cols <= 8192 and rank <= 2048, else two ordered on `stream`.
  * Replaces hgravs01_two_stage_matvec_f32 (q80_mixed_decode.rs:614-629). */
 int hk_gemv_lowrank(hk_ctx* ctx, const hk_organ* left, const hk_organ* right, const float* x,
                     float* mid, float* y, hk_stream stream);
+/* y_i = L_i (R_i x_i) for the n HGRAVS01 pairs of two organ sets (left set of
+ * HK_U3 rows x rank, right set of HK_U3 rank x cols, the same n), streamed in
+ * ONE launch (one workgroup per pair, mid kept on chip) for the shapes
+ * hk_gemv_lowrank fuses, else two set launches through library scratch.
+ * Strides as hk_gemv_batch.  The set form of hgravs01_two_stage_matvec_f32
+ * (q80_mixed_decode.rs:614-629) over a routed wave's down projections. */
+int hk_gemv_lowrank_set(hk_ctx* ctx, const hk_organ_set* left, const hk_organ_set* right, const float* x,
+                        size_t x_stride, float* y, size_t y_stride, hk_stream stream);
 
 /* Bit-exact decode probe: out[nrows*cols] = decoded weights of rows
  * [row0, row0+nrows).  Replaces qwen_uniform_q4_decode_vector

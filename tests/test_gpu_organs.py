@@ -238,6 +238,41 @@ def test_uniform_u3_factor_organ(ctx, oracle, shape):
     assert oracle.relative_l2(y, oracle.uniform_matvec_f64(s, c, rows, cols, x, 3, 64)) < TOL
 
 
+@pytest.mark.parametrize("rows,rank,cols,n", [(2048, 160, 768, 6), (512, 96, 2048, 5), (48, 32, 4096, 3)])
+def test_hgravs01_set_one_launch_matches_two_launches(ctx, oracle, rows, rank, cols, n):
+    """hk_gemv_lowrank_set (one workgroup per pair, mid on chip) gives the
+    same bits as the two set launches through a mid buffer, and stays within
+    tolerance of the oracle's two-stage matvec and the FP64 product."""
+    from hawking_amd.organs import OrganSet, gemv_lowrank_set
+    say("hgravs01 set", rows, rank, cols, n)
+    lefts, rights, packs, xs = [], [], [], []
+    for i in range(n):
+        key = lambda k: oracle.stream_key(U.SEED, (0xE5 << 20) + (rank << 8) + 16 * i + k)
+        Lw = oracle.normal(key(1), rows * rank, 0.05).reshape(rows, rank)
+        Rw = oracle.normal(key(2), rank * cols, 0.02).reshape(rank, cols)
+        lo, lp = _u3(ctx, oracle, Lw)
+        ro, rp = _u3(ctx, oracle, Rw)
+        lefts.append(lo)
+        rights.append(ro)
+        packs.append((lp, rp))
+        xs.append(oracle.normal(key(3), cols, 1.0))
+    ls, rs = OrganSet(ctx, lefts), OrganSet(ctx, rights)
+    xd = ctx.to_device(np.stack(xs))
+    y1, mid, y2 = ctx.empty((n, rows)), ctx.empty((n, rank)), ctx.empty((n, rows))
+    gemv_lowrank_set(ctx, ls, rs, xd, cols, y1, rows)
+    rs.gemv(xd, cols, mid, rank)
+    ls.gemv(mid, rank, y2, rows)
+    a, b = y1.download(), y2.download()
+    assert np.array_equal(a, b)
+    for i in range(n):
+        (ls_, lc), (rs_, rc) = packs[i]
+        ref = oracle.hgravs01_matvec((ls_, lc), (rs_, rc), rows, rank, cols, xs[i], 3, 64)
+        Ld = oracle.uniform_decode(ls_, lc, rows, rank, 3, 64).astype(np.float64)
+        Rd = oracle.uniform_decode(rs_, rc, rank, cols, 3, 64).astype(np.float64)
+        assert oracle.relative_l2(a[i], ref) < TOL
+        assert oracle.relative_l2(a[i], Ld.reshape(rows, rank) @ (Rd.reshape(rank, cols) @ xs[i].astype(np.float64))) < TOL
+
+
 @pytest.mark.parametrize("rows,rank,cols", [(2048, 160, 768), (768, 192, 2048), (16, 32, 32)])
 def test_hgravs01_low_rank_two_stage(ctx, oracle, rows, rank, cols):
     """y = L (R x) through hk_gemv_lowrank vs hgravs01_two_stage_matvec_f32
