@@ -101,32 +101,32 @@ __device__ void block_rmsnorm(const float* __restrict__ h, const float* __restri
     __syncthreads();
 }
 
-// The first M15_D steps of [s0, s0 + n) of tile T of organs o[0..R-1].
-template <int KIND, int R>
+// The first D steps of [s0, s0 + n) of tile T of organs o[0..R-1].
+template <int KIND, int R, int D = M15_D>
 __device__ __forceinline__ void fetch_first(const OrganView (&o)[R], uint32_t T, uint32_t s0, uint32_t n, int lane,
-                                            Frag<KIND, R> (&f)[M15_D]) {
+                                            Frag<KIND, R> (&f)[D]) {
 #pragma unroll
-    for (int k = 0; k < M15_D; ++k)
+    for (int k = 0; k < D; ++k)
         if ((uint32_t)k < n)
 #pragma unroll
             for (int r = 0; r < R; ++r) fetch_one<KIND, R>(o[r], T, s0 + (uint32_t)k, lane, f[k], r);
 }
 
-// Steps [s0, s0 + n) against the x image img (S steps), the first M15_D
+// Steps [s0, s0 + n) against the x image img (S steps), the first D
 // already fetched into f; acc[r] in units of 2^-E.
-template <int KIND, int R>
+template <int KIND, int R, int D = M15_D>
 __device__ __forceinline__ void run_steps(const OrganView (&o)[R], uint32_t T, uint32_t s0, uint32_t n,
-                                          const uint8_t* img, uint32_t S, int lane, Frag<KIND, R> (&f)[M15_D],
+                                          const uint8_t* img, uint32_t S, int lane, Frag<KIND, R> (&f)[D],
                                           float* acc) {
     const ImageA A{img, a_lane_offset(lane)};
     const float* SX = reinterpret_cast<const float*>(img + (size_t)S * Kcfg<KIND>::P * A_TILE_STRIDE);
     const int q = lane >> 4;
-    for (uint32_t it = 0; it < n; it += M15_D) {
+    for (uint32_t it = 0; it < n; it += D) {
 #pragma unroll
-        for (int k = 0; k < M15_D; ++k) {
+        for (int k = 0; k < D; ++k) {
             if (it + (uint32_t)k >= n) break;
             compute_step<KIND, R>(f[k], s0 + it + (uint32_t)k, A, SX, q, acc);
-            const uint32_t nx = it + M15_D + (uint32_t)k;
+            const uint32_t nx = it + D + (uint32_t)k;
             if (nx < n)
 #pragma unroll
                 for (int r = 0; r < R; ++r) fetch_one<KIND, R>(o[r], T, s0 + nx, lane, f[k], r);
@@ -165,8 +165,9 @@ __device__ __forceinline__ void wave_share(uint32_t S, uint32_t wave, uint32_t& 
 }
 
 // q8 rows of tile T of o[0..R-1] (cols H) against xn, in a block of its own:
-// the weights' first steps are in flight while xn and its image are built.
-template <int R>
+// the weights' first D steps per wave (a wave's whole share at H = 2048) are
+// in flight while xn and its image are built.
+template <int R, int D = 8 / R>
 __device__ __forceinline__ void q8_tile(const M15Dims& d, const M15Dev& L, const float* h, const OrganView (&o)[R],
                                         uint32_t T, uint8_t* lds, float* red, float* part, uint32_t* status,
                                         float* v) {
@@ -175,8 +176,8 @@ __device__ __forceinline__ void q8_tile(const M15Dims& d, const M15Dev& L, const
     const uint32_t S = n_steps_for(HK_Q8, d.H);
     uint32_t s0, n;
     wave_share(S, wave, s0, n);
-    Frag<HK_Q8, R> f[M15_D];
-    fetch_first<HK_Q8, R>(o, T, s0, n, lane, f);
+    Frag<HK_Q8, R> f[D];
+    fetch_first<HK_Q8, R, D>(o, T, s0, n, lane, f);
     float* xs = reinterpret_cast<float*>(lds);  // stage: image columns of H (binary steps)
     uint8_t* img = lds + (size_t)n_steps_for(HK_BIN, d.H) * 512u * 4u;
     block_rmsnorm(h, L.norm_w, d.H, d.eps, xs, red, nullptr);
@@ -188,7 +189,7 @@ __device__ __forceinline__ void q8_tile(const M15Dims& d, const M15Dev& L, const
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-    run_steps<HK_Q8, R>(o, T, s0, n, img, S, lane, f, acc);
+    run_steps<HK_Q8, R, D>(o, T, s0, n, img, S, lane, f, acc);
     block_rows<R>(acc, part, E, v);
 }
 
