@@ -8,9 +8,12 @@ Every timed loop is preceded by about 0.2 s of untimed launches of the same
 work (the GPU clocks ramp up over the first milliseconds of activity), then
 the W warmup steps, then exactly K timed steps between HIP events.
 
-Also reported (the same JSON line, "extra"): Q4 (config 1) and mixed streamed
-GB/s, the binary down shape (2048x512), single-organ latency, the config-3
-MoE layer and the config-4 48-layer mixed token in microseconds at batch 1.
+Also reported (the same JSON line, "extra"): Q4 (config 1), mixed, q8,
+HGRAVS01 low-rank and HGRAVR02 streamed GB/s, the binary down shape
+(2048x512), the terminal head, single-organ latency, the config-3 MoE layer,
+the config-4 48-layer mixed token and the mixed-1p5-v1 48-layer token (the
+reference's own codec triplet) in microseconds at batch 1, and the config-5
+batched block.
 
 The CPU baseline is the oracle's serial restatement of
 binary_group_matvec_f32 (crates/hawking-core/src/model/qwen_complete_binary/
@@ -369,7 +372,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
-              "(this build has no multi-GPU path; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "(this build has no multi-GPU path: organ GEMVs would shard by rows, MoE layers by experts)", file=sys.stderr)
         sys.exit(2)
 
     from hawking_amd.runtime import Context

@@ -78,7 +78,7 @@ def oracle_layer(oracle, seed, shape, layer, h):
 
 
 def router_margin_ok(logits: np.ndarray, k: int, rel: float = 1e-4) -> bool:
-    """Survey router margin rule: the f64 gap between the k-th and (k+1)-th
+    """Router margin rule: the f64 gap between the k-th and (k+1)-th
     score must be >= rel * max|score| for ids to be compared bit-exactly."""
     l64 = np.sort(logits.astype(np.float64))[::-1]
     if k >= l64.size:
