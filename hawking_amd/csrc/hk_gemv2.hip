@@ -440,8 +440,19 @@ static hipError_t launch_kind(const OrganView* organs, uint32_t n, const OrganVi
 // Launch shape (R tiles per wave group, D steps in flight, tiles per
 // workgroup) by kind and size, from sweeps over the streamed workloads:
 // binary 4-tile groups over 16 tiles when the organ has >= 4 steps, else
-// 2-tile groups over 32; Q4 and Q8 2 over 16; 3-bit factors 2 over 16, or over
-// 128 when narrow; mixed (large fragments) 1 over 16.
+// 2-tile groups 5 deep over 32; Q4 and Q8 2 over 16; 3-bit factors 2 over 16,
+// or over 128 when narrow; mixed (large fragments) 1 over 32.
+// (build-time overrides for launch-shape sweeps)
+#ifndef HK_BIN_NARROW_R
+#define HK_BIN_NARROW_R 2
+#define HK_BIN_NARROW_D 5
+#define HK_BIN_NARROW_TPW 32
+#endif
+#ifndef HK_MIX_R
+#define HK_MIX_R 1
+#define HK_MIX_D 3
+#define HK_MIX_TPW 32
+#endif
 template <int KIND>
 static hipError_t launch_r(const OrganView* organs, uint32_t n, const OrganView& sh, const float* x, size_t xs,
                            float* y, size_t ys, hipStream_t s) {
@@ -449,13 +460,13 @@ static hipError_t launch_r(const OrganView* organs, uint32_t n, const OrganView&
     if (tiles >= 16384) {
         if constexpr (KIND == HK_BIN) {
             if (sh.steps >= 4) return launch_kind<KIND, 4, 3>(organs, n, sh, x, xs, y, ys, 16, s);
-            return launch_kind<KIND, 2, 3>(organs, n, sh, x, xs, y, ys, 32, s);
+            return launch_kind<KIND, HK_BIN_NARROW_R, HK_BIN_NARROW_D>(organs, n, sh, x, xs, y, ys, HK_BIN_NARROW_TPW, s);
         } else if constexpr (KIND == HK_U3) {
             return launch_kind<KIND, 2, 3>(organs, n, sh, x, xs, y, ys, gemv_max_tiles(KIND, sh.steps) == 128u ? 128 : 16, s);
         } else if constexpr (KIND == HK_Q4 || KIND == HK_Q8) {
             return launch_kind<KIND, 2, 3>(organs, n, sh, x, xs, y, ys, 16, s);
         } else {
-            return launch_kind<KIND, 1, 3>(organs, n, sh, x, xs, y, ys, 16, s);
+            return launch_kind<KIND, HK_MIX_R, HK_MIX_D>(organs, n, sh, x, xs, y, ys, HK_MIX_TPW, s);
         }
     }
     if (tiles >= 4096) return launch_kind<KIND, 2, 2>(organs, n, sh, x, xs, y, ys, 8, s);

@@ -20,6 +20,8 @@
 //     7 is the raw signed byte (no AND): its A row is -X7 and every lower
 //     plane's A row carries +X7, which cancels the lower bits the raw byte
 //     brings in (sum_s<7 (X_s 2^(7-s) + X7) 2^s b_s - X7 byte = 128 sum X_s b_s).
+//     A mixed Q2 item's top field is read in place (bytes & 0xC0, with bit 7
+//     stored inverted: 64 (code - 2) as a signed byte), so no field needs a shift.
 //   * Per (row, group) the four int32 limbs are combined (pairs exactly in
 //     int32, then one f32 fma), the zero
 //     point is removed with the group's sum of X (binary: sum (2b-1) X =
@@ -49,35 +51,37 @@ __device__ __forceinline__ v4i mfma_i8(const v4i& a, const v4i& b, const v4i& c)
 template <int KIND>
 struct Kcfg;
 // P = A tiles per step, SXG = columns per x-sum (the zero-point granularity a
-// lane needs per step: one binary group, one Q4 group of 32, one Q2 half-group).
+// lane needs per step: one binary group, one Q4 group of 32, one Q2 half-group),
+// SXW = floats stored per x-sum (mixed: the binary and the Q2 correction).
 template <>
 struct Kcfg<HK_BIN> {
-    static constexpr int P = 8, STEP_COLS = 512, DATA = 16, SXG = 128;
+    static constexpr int P = 8, STEP_COLS = 512, DATA = 16, SXG = 128, SXW = 1;
 };
 template <>
 struct Kcfg<HK_Q4> {
-    static constexpr int P = 2, STEP_COLS = 128, DATA = 16, SXG = 32;
+    static constexpr int P = 2, STEP_COLS = 128, DATA = 16, SXG = 32, SXW = 1;
 };
 template <>
 struct Kcfg<HK_MIXED> {
-    static constexpr int P = 8, STEP_COLS = 512, DATA = 32, SXG = 64;
+    static constexpr int P = 8, STEP_COLS = 512, DATA = 32, SXG = 64, SXW = 2;
 };
 template <>
 struct Kcfg<HK_Q8> {
-    static constexpr int P = 1, STEP_COLS = 64, DATA = 16, SXG = 16;
+    static constexpr int P = 1, STEP_COLS = 64, DATA = 16, SXG = 16, SXW = 1;
 };
 template <>
 struct Kcfg<HK_U3> {
-    static constexpr int P = 4, STEP_COLS = 128, DATA = 12, SXG = 32;
+    static constexpr int P = 4, STEP_COLS = 128, DATA = 12, SXG = 32, SXW = 1;
 };
 
 constexpr int A_TILE_STRIDE = 272;  // 256 B of active-lane limbs + 16 B of zeros
 
 // Bytes of the x image of an organ with `steps` steps: the A tiles, then the
-// per-SXG-column sums of X (as f32).
+// per-SXG-column sums of X (as f32; SXW floats each).
 template <int KIND>
 __host__ __device__ constexpr size_t x_lds_bytes(uint32_t steps) {
-    return (size_t)steps * Kcfg<KIND>::P * A_TILE_STRIDE + (size_t)steps * (Kcfg<KIND>::STEP_COLS / Kcfg<KIND>::SXG) * 4;
+    return (size_t)steps * Kcfg<KIND>::P * A_TILE_STRIDE +
+           (size_t)steps * (Kcfg<KIND>::STEP_COLS / Kcfg<KIND>::SXG) * Kcfg<KIND>::SXW * 4;
 }
 // Columns of the image: cols rounded up to whole steps.
 template <int KIND>
@@ -122,7 +126,7 @@ __device__ __forceinline__ int32_t a_value(const float* xq, int t, int mu, int q
         const int h = mu >> 2, u = mu & 3, r = i >> 2, j = i & 3;
         const int a = r < 2 ? 2 * h + r : 2 * h + 2 + r;
         const int32_t v = X((uint32_t)(t * 512 + q * 128) + mixed_q2_col((uint32_t)a, (uint32_t)j, (uint32_t)u));
-        return v * (1 << (u < 3 ? 6 - 2 * u : 6));
+        return v * (1 << (6 - 2 * u));
     }
 }
 
@@ -258,7 +262,18 @@ __device__ int x_image(const Team& team, const XChunks<NC>& xc, const float* x, 
             // a sum's NL chunks belong to NL consecutive members, all active together
 #pragma unroll
             for (int k = 1; k < NL; k <<= 1) s += __shfl_xor(s, k, 64);
-            if ((me & (uint32_t)(NL - 1)) == 0) SX[ch / (uint32_t)NL] = (float)s;
+            if constexpr (KIND == HK_MIXED) {
+                // the Q2 top field (columns 6, 7 of every chunk) decodes as
+                // code - 2, so its items subtract 1.5 sum X - 2 sum_top X
+                // (3 sum X - 4 sum_top X < 2^31: exact in int32, halved exactly)
+                int32_t s3 = (int32_t)f[6] + (int32_t)f[7];
+#pragma unroll
+                for (int k = 1; k < NL; k <<= 1) s3 += __shfl_xor(s3, k, 64);
+                if ((me & (uint32_t)(NL - 1)) == 0)
+                    reinterpret_cast<float2*>(SX)[ch / (uint32_t)NL] = make_float2((float)s, (float)(3 * s - 4 * s3) * 0.5f);
+            } else {
+                if ((me & (uint32_t)(NL - 1)) == 0) SX[ch / (uint32_t)NL] = (float)s;
+            }
         }
         team.sync();
         // this round's steps; unit = (tau, slot q, dword d): 4 A bytes -> 4
@@ -355,6 +370,7 @@ __device__ __forceinline__ void fetch_mixed(const OrganView& o, const uint4& h, 
     const bool isq2 = ((lane < 32 ? (h.x >> lane) : (h.y >> (lane - 32))) & 1u) != 0;
     const uint8_t* p = o.data + h.z + 16u * ((uint32_t)lane + below);
     const uint4 va = ldg(reinterpret_cast<const uint4*>(p));
+    // binary lanes re-read their 16 bytes (an exec-masked load measured slower)
     const uint4 vb = ldg(reinterpret_cast<const uint4*>(p + (isq2 ? 16 : 0)));
     f.V[r][0] = va.x;
     f.V[r][1] = va.y;
@@ -473,6 +489,10 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] += f16_bits_to_f32(f.s[r]) * (combine_limbs(c[r]) * (1.0f / 32.0f) - 3.0f * sx);
     } else {
+        // field u of a byte is bits 2u..2u+1 (binary: bit 2u; the odd bits come
+        // from the copy shifted down by one).  A Q2 item's bit 7 is stored
+        // inverted, so its top field read as a signed byte is 64 (code - 2);
+        // the x image's second sum corrects for that.
         uint32_t V[R][8];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -483,6 +503,7 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
                 V[r][k + 4] = f.V[r][k + 4] >> sh;
             }
         }
+        const float4 sxq = reinterpret_cast<const float4*>(SX)[4 * t + q];  // {h0 bin, h0 q2, h1 bin, h1 q2}
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -492,32 +513,35 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
                 const v4i a = A(t * 8 + h * 4 + u);
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    const uint32_t bm = f.q2[r] ? 0x03030303u : 0x01010101u;
+                    const uint32_t bm = (f.q2[r] ? 0x03030303u : 0x01010101u) << (2 * u);
                     v4i b;
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
                         const int ai = k < 2 ? 2 * h + k : 2 * h + 2 + k;
-                        b[k] = (int)(u < 3 ? (V[r][ai] & (bm << (2 * u))) : ((V[r][ai] >> 6) & bm));
+                        b[k] = (int)(V[r][ai] & bm);
                     }
                     c[r] = mfma_i8(a, b, c[r]);
                 }
             }
-            const float sx = SX[8 * t + 2 * q + h];
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const float alpha = f.q2[r] ? (1.0f / 64.0f) : (2.0f / 64.0f);
-                const float beta = f.q2[r] ? 1.5f : 1.0f;
-                acc[r] += f16_bits_to_f32(h ? f.s1[r] : f.s0[r]) * (combine_limbs(c[r]) * alpha - beta * sx);
+                const float corr = f.q2[r] ? (h ? sxq.w : sxq.y) : (h ? sxq.z : sxq.x);
+                acc[r] += f16_bits_to_f32(h ? f.s1[r] : f.s0[r]) * (combine_limbs(c[r]) * alpha - corr);
             }
         }
     }
 }
 
 // Sum the four column-slot partials of a tile: every lane gets its row's total.
+// v_permlane16_swap(v, v) leaves rows {0,0,2,2} in one result and {1,1,3,3}
+// in the other (rows of 16 lanes), so their sum is v + v[lane ^ 16]; the
+// 32-lane swap does the same for lane ^ 32.  Same bits as two xor shuffles.
 __device__ __forceinline__ float tile_row_sum(float v) {
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    return v;
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 }  // namespace hk

@@ -250,7 +250,7 @@ __device__ void repack_mixed_items_body(const CanonView& src, const OrganView& d
                         const uint32_t code = (cs[e >> 2] >> (2u * (e & 3u))) & 3u;
                         word |= code << (8u * j + 2u * u);
                     }
-                w[a] = word;
+                w[a] = word ^ 0x80808080u;  // top field's high bit inverted (read as code - 2)
             }
             reinterpret_cast<uint4*>(item)[0] = make_uint4(w[0], w[1], w[2], w[3]);
             reinterpret_cast<uint4*>(item)[1] = make_uint4(w[4], w[5], w[6], w[7]);

@@ -23,7 +23,8 @@
 //         Q2 code order inside an item (so one shift pattern decodes both
 //         kinds): dword a (0..3) byte j holds, in 2-bit fields u = 0..3, the
 //         codes of columns 32a + 8j + 2u; dword 4+a byte j holds columns
-//         32a + 8j + 2u + 1.
+//         32a + 8j + 2u + 1.  Bit 7 of every Q2 byte is stored inverted, so
+//         the top field read as a signed byte (bytes & 0xC0) is 64 (code - 2).
 //   Q8    step = 64 columns (one group); lane (n,q) holds the 16 code bytes
 //         of row n, columns 16q..16q+15 of the step (value (code-127)*scale).
 //         scales: [tile][step][row] f16 (32 bytes per step: the four lanes of
@@ -110,7 +111,7 @@ __device__ inline float tiled_weight(const OrganView& o, uint32_t r, uint32_t c)
     }
     // invert mixed_q2_col: column i -> (a, j, u)
     const uint32_t a = ((i >> 5) & 3u) | ((i & 1u) << 2), j = (i >> 3) & 3u, u = (i >> 1) & 3u;
-    const uint32_t code = (item[4u * a + j] >> (2u * u)) & 3u;
+    const uint32_t code = ((item[4u * a + j] ^ 0x80u) >> (2u * u)) & 3u;  // bit 7 is stored inverted
     return ((float)code - 1.5f) * f16_bits_to_f32(sc[i >> 6]);
 }
 
