@@ -356,19 +356,25 @@ struct Frag<HK_U3, R> {
     uint32_t hi[R];
     uint16_t s[R];
 };
+// q2m: the step's Q2 lane mask, wave-uniform (scalar registers); a lane's
+// kind is its bit, read with inverse ballot (no vector register per step).
 template <int R>
 struct Frag<HK_MIXED, R> {
     uint32_t V[R][8];
     uint16_t s0[R], s1[R];
-    bool q2[R];
+    uint64_t q2m[R];
 };
 
 // Issue the loads of a mixed step with header h into slot r of f.
 template <int R>
 __device__ __forceinline__ void fetch_mixed(const OrganView& o, const uint4& h, int lane, Frag<HK_MIXED, R>& f, int r) {
-    const uint32_t below = __builtin_amdgcn_mbcnt_hi(h.y, __builtin_amdgcn_mbcnt_lo(h.x, 0u));
-    const bool isq2 = ((lane < 32 ? (h.x >> lane) : (h.y >> (lane - 32))) & 1u) != 0;
-    const uint8_t* p = o.data + h.z + 16u * ((uint32_t)lane + below);
+    // the header is wave-uniform: keep it in scalar registers
+    const uint32_t mlo = __builtin_amdgcn_readfirstlane(h.x), mhi = __builtin_amdgcn_readfirstlane(h.y);
+    const uint32_t doff = __builtin_amdgcn_readfirstlane(h.z), soff = __builtin_amdgcn_readfirstlane(h.w);
+    const uint64_t mask = ((uint64_t)mhi << 32) | mlo;
+    const uint32_t below = __builtin_amdgcn_mbcnt_hi(mhi, __builtin_amdgcn_mbcnt_lo(mlo, 0u));
+    const bool isq2 = __builtin_amdgcn_inverse_ballot_w64(mask);
+    const uint8_t* p = o.data + doff + 16u * ((uint32_t)lane + below);
     const uint4 va = ldg(reinterpret_cast<const uint4*>(p));
     // binary lanes re-read their 16 bytes (an exec-masked load measured slower)
     const uint4 vb = ldg(reinterpret_cast<const uint4*>(p + (isq2 ? 16 : 0)));
@@ -380,10 +386,10 @@ __device__ __forceinline__ void fetch_mixed(const OrganView& o, const uint4& h, 
     f.V[r][5] = vb.y;
     f.V[r][6] = vb.z;
     f.V[r][7] = vb.w;
-    const uint16_t* spp = o.scales + h.w + (uint32_t)lane + below;
+    const uint16_t* spp = o.scales + soff + (uint32_t)lane + below;
     f.s0[r] = ldg(spp);
     f.s1[r] = ldg(spp + (isq2 ? 1 : 0));
-    f.q2[r] = isq2;
+    f.q2m[r] = mask;
 }
 
 // Issue the loads of step t of tile T of organ o into slot r of f (a mixed
@@ -494,9 +500,11 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
         // inverted, so its top field read as a signed byte is 64 (code - 2);
         // the x image's second sum corrects for that.
         uint32_t V[R][8];
+        bool q2[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint32_t sh = f.q2[r] ? 0u : 1u;  // binary: odd columns are the signs >> 1
+            q2[r] = __builtin_amdgcn_inverse_ballot_w64(f.q2m[r]);
+            const uint32_t sh = q2[r] ? 0u : 1u;  // binary: odd columns are the signs >> 1
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 V[r][k] = f.V[r][k];
@@ -513,7 +521,7 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
                 const v4i a = A(t * 8 + h * 4 + u);
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    const uint32_t bm = (f.q2[r] ? 0x03030303u : 0x01010101u) << (2 * u);
+                    const uint32_t bm = (q2[r] ? 0x03030303u : 0x01010101u) << (2 * u);
                     v4i b;
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
@@ -525,8 +533,8 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
             }
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const float alpha = f.q2[r] ? (1.0f / 64.0f) : (2.0f / 64.0f);
-                const float corr = f.q2[r] ? (h ? sxq.w : sxq.y) : (h ? sxq.z : sxq.x);
+                const float alpha = q2[r] ? (1.0f / 64.0f) : (2.0f / 64.0f);
+                const float corr = q2[r] ? (h ? sxq.w : sxq.y) : (h ? sxq.z : sxq.x);
                 acc[r] += f16_bits_to_f32(h ? f.s1[r] : f.s0[r]) * (combine_limbs(c[r]) * alpha - corr);
             }
         }
