@@ -440,13 +440,24 @@ static hipError_t launch_kind(const OrganView* organs, uint32_t n, const OrganVi
 // Launch shape (R tiles per wave group, D steps in flight, tiles per
 // workgroup) by kind and size, from sweeps over the streamed workloads:
 // binary 4-tile groups over 16 tiles when the organ has >= 4 steps, else
-// 2-tile groups 5 deep over 32; Q4 and Q8 2 over 16; 3-bit factors 2 over 16,
+// 2-tile groups 5 deep over 32; Q4 and Q8 2 over 32; 3-bit factors 2 over 16,
 // or over 128 when narrow; mixed (large fragments) 1 over 32.
 // (build-time overrides for launch-shape sweeps)
 #ifndef HK_BIN_NARROW_R
 #define HK_BIN_NARROW_R 2
 #define HK_BIN_NARROW_D 5
 #define HK_BIN_NARROW_TPW 32
+#endif
+#ifndef HK_BIN_WIDE_TPW
+#define HK_BIN_WIDE_TPW 16
+#endif
+#ifndef HK_Q_TPW
+#define HK_Q_TPW 32
+#endif
+#ifndef HK_HEAD_R
+#define HK_HEAD_R 2
+#define HK_HEAD_D 3
+#define HK_HEAD_TPW 8
 #endif
 #ifndef HK_MIX_R
 #define HK_MIX_R 1
@@ -459,12 +470,12 @@ static hipError_t launch_r(const OrganView* organs, uint32_t n, const OrganView&
     const uint64_t tiles = (uint64_t)n * sh.n_tiles;
     if (tiles >= 16384) {
         if constexpr (KIND == HK_BIN) {
-            if (sh.steps >= 4) return launch_kind<KIND, 4, 3>(organs, n, sh, x, xs, y, ys, 16, s);
+            if (sh.steps >= 4) return launch_kind<KIND, 4, 3>(organs, n, sh, x, xs, y, ys, HK_BIN_WIDE_TPW, s);
             return launch_kind<KIND, HK_BIN_NARROW_R, HK_BIN_NARROW_D>(organs, n, sh, x, xs, y, ys, HK_BIN_NARROW_TPW, s);
         } else if constexpr (KIND == HK_U3) {
             return launch_kind<KIND, 2, 3>(organs, n, sh, x, xs, y, ys, gemv_max_tiles(KIND, sh.steps) == 128u ? 128 : 16, s);
         } else if constexpr (KIND == HK_Q4 || KIND == HK_Q8) {
-            return launch_kind<KIND, 2, 3>(organs, n, sh, x, xs, y, ys, 16, s);
+            return launch_kind<KIND, 2, 3>(organs, n, sh, x, xs, y, ys, HK_Q_TPW, s);
         } else {
             return launch_kind<KIND, HK_MIX_R, HK_MIX_D>(organs, n, sh, x, xs, y, ys, HK_MIX_TPW, s);
         }
@@ -476,7 +487,9 @@ static hipError_t launch_r(const OrganView* organs, uint32_t n, const OrganView&
 
 // The terminal head on a q8 lm_head (cols <= 8192): one GEMV launch with the
 // norm prologue and the greedy-key epilogue, then the one-thread pick (which
-// also clears the key for the next call).  Launch shapes as for one q8 organ.
+// also clears the key for the next call).  Launch shapes as for one q8 organ,
+// except 4,096-16,383 tiles (a 65k-262k vocabulary), where 3 steps in flight
+// over 8 tiles per workgroup measured fastest (151,936 x 2048: 59.6 vs 62.6 us).
 __global__ void head_pick_fused_kernel(uint64_t* __restrict__ key, int32_t* __restrict__ token, uint32_t* status) {
     if (threadIdx.x == 0) {
         const uint64_t best = key[0];
@@ -502,7 +515,7 @@ hipError_t launch_head_fused(const OrganView* organ_dev, const OrganView& sh, co
     if (sh.n_tiles >= 16384u)
         e = launch_kind<HK_Q8, 2, 3, true>(organ_dev, 1, sh, h, 0, logits, 0, 16, s, ha, status);
     else if (sh.n_tiles >= 4096u)
-        e = launch_kind<HK_Q8, 2, 2, true>(organ_dev, 1, sh, h, 0, logits, 0, 8, s, ha, status);
+        e = launch_kind<HK_Q8, HK_HEAD_R, HK_HEAD_D, true>(organ_dev, 1, sh, h, 0, logits, 0, HK_HEAD_TPW, s, ha, status);
     else
         e = launch_kind<HK_Q8, 1, 2, true>(organ_dev, 1, sh, h, 0, logits, 0, (sh.n_tiles + 3) / 4 >= 256 ? 4 : 1, s,
                                           ha, status);
