@@ -169,6 +169,26 @@ def test_mixed_organ(ctx, oracle, shape):
     assert oracle.relative_l2(y, oracle.mixed_matvec_f64(m, x)) < TOL
 
 
+@pytest.mark.parametrize("kinds", ["q2", "binary", "coin"])
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_mixed_organ_extreme_x(ctx, oracle, kinds, sign):
+    # every |x| near max|x| (fixed-point X within 0.1 % of 2^23), the Q2 top
+    # field's columns (6, 7 of every 8) of the opposite sign: the largest
+    # magnitudes the engine's exact int32 corrections 3 sum X - 4 sum_top X reach
+    rows, cols = 96, 1024
+    w = oracle.normal(oracle.stream_key(U.SEED, 0xC4E0), rows * cols, 0.02).reshape(rows, cols)
+    groups = rows * cols // 128
+    sel = {"q2": np.zeros(groups, np.uint8), "binary": np.ones(groups, np.uint8),
+           "coin": oracle.mixed_coins(oracle.stream_key(U.SEED, 0xC4E1), groups)}[kinds]
+    c = np.arange(cols)
+    x = (sign * np.where(c % 8 < 6, 0.999, -0.999) * (1.0 - 1e-4 * (c % 5))).astype(np.float32)
+    say("mixed organ extreme x", kinds, sign)
+    organ, m = _mixed(ctx, oracle, w, sel)
+    y = organ.matvec(x)
+    assert oracle.relative_l2(y, oracle.mixed_matvec(m, x)) < TOL
+    assert oracle.relative_l2(y, oracle.mixed_matvec_f64(m, x)) < TOL
+
+
 def _q8(ctx, oracle, w):
     from hawking_amd.organs import UniformFactorPacked
     s, c = oracle.uniform_pack(w, w.shape[0], w.shape[1], 8, 64)
