@@ -149,6 +149,27 @@ def test_rice_organ_set_matches_single(ctx, oracle):
         assert oracle.relative_l2(yy[i], oracle.rice_q1_matvec(ps[i], xs[i])) < TOL
 
 
+@pytest.mark.parametrize("n", [521, 3100])
+def test_rice_organ_set_large_matches_single(ctx, oracle, n):
+    # large HGRAVR02 sets (the streamed launch shapes): the same bits as one organ at a time
+    from hawking_amd._lib import HK_BIN_RICE
+    from hawking_amd.organs import OrganSet, SyntheticOrgan
+    rows, cols = 32, 256
+    say("rice set large", n, rows, cols)
+    orgs = [SyntheticOrgan(ctx, HK_BIN_RICE, rows, cols, oracle.stream_key(U.SEED, (0xA8 << 20) + i), 0, group=128,
+                           sigma=0.02) for i in range(n)]
+    s = OrganSet(ctx, orgs)
+    xs = np.stack([oracle.normal(oracle.stream_key(U.SEED, (0xA9 << 20) + i), cols, 1.0) for i in range(n)])
+    x = ctx.to_device(xs)
+    y = ctx.empty((n, rows))
+    s.gemv(x, cols, y, rows)
+    y1 = y.download()
+    s.gemv(x, cols, y, rows)  # a second call gives the same bits
+    assert np.array_equal(y.download(), y1)
+    for i in sorted({0, 1, n // 3, n // 2, n // 2 + 1, n - 2, n - 1}):
+        assert np.array_equal(y1[i], orgs[i].matvec(xs[i])), i
+
+
 def test_rice_upload_rejects_bad_streams(ctx, oracle):
     from hawking_amd._lib import HK_E_GEOMETRY, HK_E_NONFINITE, HawkingError
     from hawking_amd.organs import RiceQ1Packed
