@@ -115,10 +115,10 @@ PROTOTYPES = {
                                 C.POINTER(_u32), C.POINTER(_sz)]),
     "hk_gemv": (C.c_int, [_p, _p, _p, _p, _p]),
     "hk_gemv_lowrank": (C.c_int, [_p, _p, _p, _p, _p, _p, _p]),
-    "hk_gemv_lowrank_set": (C.c_int, [_p, _p, _p, _p, _sz, _p, _sz, _p]),
+    "hk_gemv_lowrank_set": (C.c_int, [_p, _p, _p, _p, _sz, _p, _sz, _p, _sz, _p]),
     "hk_organ_upload_rice": (C.c_int, [_p, C.POINTER(RiceQ1Src), _p, C.POINTER(_p)]),
     "hk_rice_apply": (C.c_int, [_p, _p, _p, _p, _p]),
-    "hk_terminal_greedy": (C.c_int, [_p, _p, _p, C.c_float, _p, _u32, _p, _p, _p, _p]),
+    "hk_terminal_greedy": (C.c_int, [_p, _p, _p, C.c_float, _p, _u32, _p, _p, _p, _p, _p]),
     "hk_organ_from_container": (C.c_int, [_p, _i32, _p, _sz, _p, C.POINTER(_p), C.POINTER(_p)]),
     "hk_organ_from_hq30": (C.c_int, [_p, _p, _sz, _p, C.POINTER(_p)]),
     "hk_catalog_open": (C.c_int, [_p, C.c_char_p, C.POINTER(_p)]),
@@ -129,6 +129,7 @@ PROTOTYPES = {
     "hk_catalog_payload": (C.c_int, [_p, _p, C.c_char_p, C.c_int, C.POINTER(_p), C.POINTER(_sz)]),
     "hk_catalog_load": (C.c_int, [_p, _p, C.c_char_p, C.c_int, _p, C.POINTER(_p), C.POINTER(_p)]),
     "hk_pack_binary_rice": (C.c_int, [_p, _p, _u32, _u32, C.c_double, _p, _p, _p, _p, _sz, C.POINTER(RiceQ1Src), _p]),
+    "hk_moe_block": (C.c_int, [_p, _p, _u32, _p, _p, _u32, C.c_int, _p, _p, _p]),
     "hk_gemv_batch": (C.c_int, [_p, C.POINTER(_p), _u32, _p, _sz, _p, _sz, _p]),
     "hk_decode_rows": (C.c_int, [_p, _p, _u32, _u32, _p, _p]),
     "hk_organ_set_create": (C.c_int, [_p, C.POINTER(_p), _u32, C.POINTER(_p)]),

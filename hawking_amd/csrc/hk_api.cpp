@@ -35,24 +35,6 @@ int check_hip(hk_ctx* ctx, hipError_t e, const char* what) {
     return set_error(ctx, HK_E_HIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 
-int ensure_scratch(hk_ctx* ctx, size_t bytes, void** out) {
-    if (ctx->scratch_bytes < bytes) {
-        if (ctx->scratch) {
-            hipError_t e = hipDeviceSynchronize();
-            if (e != hipSuccess) return check_hip(ctx, e, "hipDeviceSynchronize (scratch grow)");
-            (void)hipFree(ctx->scratch);
-            ctx->scratch = nullptr;
-            ctx->scratch_bytes = 0;
-        }
-        size_t want = std::max<size_t>(bytes, 1 << 20);
-        hipError_t e = hipMalloc(&ctx->scratch, want);
-        if (e != hipSuccess) return set_error(ctx, HK_E_NOMEM, "scratch allocation failed");
-        ctx->scratch_bytes = want;
-    }
-    *out = ctx->scratch;
-    return HK_OK;
-}
-
 static inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 static inline bool f16_finite(uint16_t b) { return (b & 0x7C00u) != 0x7C00u; }
@@ -284,12 +266,13 @@ extern "C" int hk_ctx_create(int device, hk_ctx** out) {
     hk_ctx* ctx = new hk_ctx();
     ctx->device = device;
     void* st = nullptr;
-    if (hipMalloc(&st, 256) != hipSuccess) {
+    if (hipMalloc(&st, 512) != hipSuccess) {
         delete ctx;
         return HK_E_NOMEM;
     }
-    (void)hipMemset(st, 0, 256);
+    (void)hipMemset(st, 0, 512);
     ctx->dev_status = static_cast<uint32_t*>(st);
+    ctx->pack_flag = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(st) + 256);
     *out = ctx;
     return HK_OK;
 }
@@ -298,7 +281,6 @@ extern "C" void hk_ctx_destroy(hk_ctx* ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     (void)hipDeviceSynchronize();
-    if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->dev_status) (void)hipFree(ctx->dev_status);
     delete ctx;
 }
@@ -441,26 +423,31 @@ static int repack_into_organ(hk_ctx* ctx, const CanonView& canon, uint32_t n_bin
         return set_error(ctx, HK_E_NOMEM, "organ allocation failed");
     }
     o->view = tiled_place(canon.kind, canon.group, canon.rows, canon.cols, n_bin, n_q2, static_cast<uint8_t*>(o->mem));
-    // the single-organ descriptor and a zeroed 16-byte slot (the terminal head's pick key and flag)
-    if (hipMalloc(&o->view_dev, align256(sizeof(OrganView)) + 256) != hipSuccess) {
+    // the single-organ descriptor; the repack's per-block counts live in a
+    // temporary freed after the synchronising upload
+    if (hipMalloc(&o->view_dev, align256(sizeof(OrganView))) != hipSuccess) {
         (void)hipFree(o->mem);
         delete o;
         return set_error(ctx, HK_E_NOMEM, "descriptor allocation failed");
     }
-    o->head_key = reinterpret_cast<uint64_t*>(static_cast<uint8_t*>(o->view_dev) + align256(sizeof(OrganView)));
     int rc = check_hip(ctx, hipMemcpyAsync(o->view_dev, &o->view, sizeof(OrganView), hipMemcpyHostToDevice, st),
                        "descriptor upload");
-    if (!rc) rc = check_hip(ctx, hipMemsetAsync(o->head_key, 0, 16, st), "pick slot clear");
+    void* counts = nullptr;
     if (!rc && canon.kind == HK_F32) {
         rc = check_hip(ctx, hipMemcpyAsync(const_cast<float*>(o->view.dense), canon.dense,
                                            (size_t)canon.rows * canon.cols * 4, hipMemcpyDeviceToDevice, st),
                        "dense copy");
     } else if (!rc) {
-        void* scratch = nullptr;
-        rc = ensure_scratch(ctx, 8 * ((size_t)o->view.n_tiles * o->view.steps + 1), &scratch);
-        if (!rc) rc = check_hip(ctx, launch_repack(canon, o->view, scratch, st), "repack launch");
+        if (hipMalloc(&counts, 8 * ((size_t)o->view.n_tiles * o->view.steps + 1)) != hipSuccess)
+            rc = set_error(ctx, HK_E_NOMEM, "repack count allocation failed");
+        else
+            rc = check_hip(ctx, launch_repack(canon, o->view, counts, st), "repack launch");
     }
     if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "hipStreamSynchronize (repack)");
+    if (counts) {
+        if (rc) (void)hipStreamSynchronize(st);
+        (void)hipFree(counts);
+    }
     if (rc) {
         (void)hipFree(o->mem);
         (void)hipFree(o->view_dev);
@@ -643,7 +630,8 @@ extern "C" int hk_gemv_set(hk_ctx* ctx, const hk_organ_set* set, const float* x,
 }
 
 extern "C" int hk_gemv_lowrank_set(hk_ctx* ctx, const hk_organ_set* left, const hk_organ_set* right, const float* x,
-                                   size_t x_stride, float* y, size_t y_stride, hk_stream stream) {
+                                   size_t x_stride, float* mid, size_t mid_stride, float* y, size_t y_stride,
+                                   hk_stream stream) {
     if (!ctx) return HK_E_INVALID_ARG;
     if (!left || !right) return set_error(ctx, HK_E_INVALID_ARG, "hk_gemv_lowrank_set: NULL set");
     if (left->n != right->n || right->first.rows != left->first.cols)
@@ -653,18 +641,25 @@ extern "C" int hk_gemv_lowrank_set(hk_ctx* ctx, const hk_organ_set* left, const 
     if (!rc && left->n > 1 && y_stride < left->first.rows)
         rc = set_error(ctx, HK_E_GEOMETRY, "hk_gemv_lowrank_set: y stride smaller than the left factor's rows");
     if (rc) return rc;
+    const bool fused = lowrank_fusable(left->first, right->first);
+    if (mid) {
+        if (!aligned16(mid) || (mid_stride % 4) || (left->n > 1 && mid_stride < right->first.rows))
+            return set_error(ctx, HK_E_INVALID_ARG,
+                             "hk_gemv_lowrank_set: mid must be 16-byte aligned with mid_stride % 4 == 0 and >= the rank");
+    } else if (!fused) {
+        return set_error(ctx, HK_E_INVALID_ARG,
+                         "hk_gemv_lowrank_set: this shape runs as two launches and needs a mid workspace "
+                         "(n x rank floats)");
+    }
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (lowrank_fusable(left->first, right->first))
+    if (fused)
         return check_hip(ctx,
-                         launch_lowrank(left->dev, right->dev, left->n, left->first, right->first, x, x_stride, nullptr,
-                                        0, y, y_stride, nullptr, st),
+                         launch_lowrank(left->dev, right->dev, left->n, left->first, right->first, x, x_stride, mid,
+                                        mid_stride, y, y_stride, nullptr, st),
                          "low-rank set launch");
-    // other shapes: two launches through a mid buffer in the context's scratch
-    const size_t ms = (right->first.rows + 3u) & ~3u;
-    void* mid = nullptr;
-    rc = ensure_scratch(ctx, (size_t)left->n * ms * sizeof(float), &mid);
-    if (!rc) rc = hk_gemv_set(ctx, right, x, x_stride, static_cast<float*>(mid), ms, stream);
-    if (!rc) rc = hk_gemv_set(ctx, left, static_cast<const float*>(mid), ms, y, y_stride, stream);
+    // other shapes: two launches ordered on the stream through the caller's mid
+    rc = hk_gemv_set(ctx, right, x, x_stride, mid, mid_stride, stream);
+    if (!rc) rc = hk_gemv_set(ctx, left, mid, mid_stride, y, y_stride, stream);
     return rc;
 }
 
@@ -928,11 +923,8 @@ static int finish_pack(hk_ctx* ctx, hipStream_t st, uint32_t* bad_dev, hipError_
 }
 
 static int pack_prologue(hk_ctx* ctx, hipStream_t st, uint32_t** bad) {
-    void* p = nullptr;
-    int rc = ensure_scratch(ctx, 256, &p);
-    if (rc) return rc;
-    *bad = static_cast<uint32_t*>(p);
-    return check_hip(ctx, hipMemsetAsync(p, 0, 4, st), "hipMemsetAsync (pack flag)");
+    *bad = ctx->pack_flag;
+    return check_hip(ctx, hipMemsetAsync(ctx->pack_flag, 0, 4, st), "hipMemsetAsync (pack flag)");
 }
 
 extern "C" int hk_pack_q4(hk_ctx* ctx, const float* w, uint32_t rows, uint32_t cols, int32_t group,
@@ -1051,31 +1043,37 @@ extern "C" int hk_synth_normal(hk_ctx* ctx, uint64_t key, uint64_t first, size_t
 
 // ====================================================================== terminal head
 
+// The head's launches: fused for a q8 lm_head the fused GEMV takes, else norm,
+// GEMV and pick.  `pick` holds 16 zero bytes and is left zeroed.
+static int head_greedy(hk_ctx* ctx, const float* hidden, const float* norm_w, float eps, const hk_organ* lm_head,
+                       uint32_t n_valid, float* xn, float* logits, uint64_t* pick, int32_t* token, hipStream_t st) {
+    if (head_gemv_fusable(lm_head->view) && aligned16(norm_w) && aligned16(xn))
+        return check_hip(ctx,
+                         launch_head_fused(static_cast<const OrganView*>(lm_head->view_dev), lm_head->view, hidden,
+                                           norm_w, eps, xn, logits, n_valid, pick, token, ctx->dev_status, st),
+                         "terminal head");
+    int rc = check_hip(ctx, launch_head_norm(hidden, norm_w, lm_head->view.cols, eps, xn, token, pick,
+                                             ctx->dev_status, st),
+                       "head norm");
+    if (!rc) rc = hk_gemv(ctx, lm_head, xn, logits, st);
+    if (!rc) rc = check_hip(ctx, launch_head_argmax(logits, n_valid, pick, token, ctx->dev_status, st), "head argmax");
+    return rc;
+}
+
 extern "C" int hk_terminal_greedy(hk_ctx* ctx, const float* hidden, const float* norm_w, float eps,
-                                  const hk_organ* lm_head, uint32_t n_valid, float* xn, float* logits, int32_t* token,
-                                  hk_stream stream) {
+                                  const hk_organ* lm_head, uint32_t n_valid, float* xn, float* logits, uint64_t* pick,
+                                  int32_t* token, hk_stream stream) {
     if (!ctx) return HK_E_INVALID_ARG;
-    if (!lm_head || !hidden || !norm_w || !xn || !logits || !token)
+    if (!lm_head || !hidden || !norm_w || !xn || !logits || !pick || !token)
         return set_error(ctx, HK_E_INVALID_ARG, "hk_terminal_greedy: NULL argument");
     if (n_valid == 0 || n_valid > lm_head->view.rows)
         return set_error(ctx, HK_E_GEOMETRY, "hk_terminal_greedy: need 0 < n_valid <= lm_head rows");
     if (!(eps >= 0.0f) || !std::isfinite(eps)) return set_error(ctx, HK_E_INVALID_ARG, "hk_terminal_greedy: bad eps");
     if (!aligned16(hidden)) return set_error(ctx, HK_E_INVALID_ARG, "hk_terminal_greedy: hidden must be 16-byte aligned");
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    if (head_gemv_fusable(lm_head->view) && aligned16(norm_w) && aligned16(xn))
-        return check_hip(ctx,
-                         launch_head_fused(static_cast<const OrganView*>(lm_head->view_dev), lm_head->view, hidden,
-                                           norm_w, eps, xn, logits, n_valid, lm_head->head_key, token,
-                                           ctx->dev_status, st),
-                         "terminal head");
-    int rc = check_hip(ctx, launch_head_norm(hidden, norm_w, lm_head->view.cols, eps, xn, token, lm_head->head_key,
-                                             ctx->dev_status, st),
-                       "head norm");
-    if (!rc) rc = hk_gemv(ctx, lm_head, xn, logits, stream);
-    if (!rc)
-        rc = check_hip(ctx, launch_head_argmax(logits, n_valid, lm_head->head_key, token, ctx->dev_status, st),
-                       "head argmax");
-    return rc;
+    if (reinterpret_cast<uintptr_t>(pick) & 7u)
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_terminal_greedy: pick must be 8-byte aligned");
+    return head_greedy(ctx, hidden, norm_w, eps, lm_head, n_valid, xn, logits, pick, token,
+                       static_cast<hipStream_t>(stream));
 }
 
 // ====================================================================== routers
@@ -1147,7 +1145,7 @@ struct hk_moe_model {
     void* tables = nullptr;  // device expert tables of all layers
     hk::MoeWs ws{};
     float* hbuf[2] = {nullptr, nullptr};
-    // batched (noaux_tc) workspace, grown on demand to bws_tokens tokens
+    // batched (noaux_tc) workspace for MOE_BATCH_MAX_TOKENS tokens (noaux_tc models)
     void* bws_mem = nullptr;
     uint32_t bws_tokens = 0;
     hk::MoeBatchWs bws{};
@@ -1172,6 +1170,63 @@ static void organ_shape(const hk_moe_config& c, uint32_t e, uint32_t p, uint32_t
 
 extern "C" uint64_t hk_moe_stream_id(uint32_t layer, uint32_t expert, uint32_t proj) {
     return ((uint64_t)(layer + 1) << 40) | ((uint64_t)expert << 8) | (uint64_t)proj;
+}
+
+// The batched (noaux_tc) block's workspace for its largest batch
+// (MOE_BATCH_MAX_TOKENS tokens), allocated with the model so that the
+// compute call allocates nothing.
+static int alloc_batch_ws(hk_ctx* ctx, hk_moe_model* m) {
+    const hk_moe_config& c = m->cfg;
+    const uint32_t T = hk::MOE_BATCH_MAX_TOKENS;
+    const uint32_t imax = std::max(c.inter, c.shared_inter), K = c.top_k, E = c.n_experts;
+    const uint32_t S = (c.hidden + hk::MOE_BATCH_ROUTER_COLS - 1) / hk::MOE_BATCH_ROUTER_COLS;
+    const size_t pairs = (size_t)T * K + (c.shared_inter ? T : 0);
+    const size_t xs = align256(moe_batch_img_bytes(c.hidden)), as = align256(moe_batch_img_bytes(imax));
+    const size_t sz[] = {
+        (size_t)T * c.hidden * 4,          // x32
+        (size_t)T * xs,                    // ximg
+        (size_t)T * 4,                     // ximg_e
+        (size_t)S * T * E * 4,             // part
+        (size_t)T * K * 4,                 // ids
+        (size_t)T * K * 4,                 // w
+        (size_t)T * K * 4,                 // order
+        ((size_t)E + 1) * 16,              // active
+        4,                                 // n_active
+        pairs * 4,                         // members
+        pairs * imax * 4,                  // act
+        pairs * as,                        // aimg
+        pairs * 4,                         // aimg_e
+        pairs * c.hidden * 4,              // ybuf
+    };
+    size_t total = 0;
+    for (size_t b : sz) total += align256(b);
+    if (hipMalloc(&m->bws_mem, total) != hipSuccess) return set_error(ctx, HK_E_NOMEM, "batched MoE workspace allocation failed");
+    uint8_t* p = static_cast<uint8_t*>(m->bws_mem);
+    void* ptr[sizeof(sz) / sizeof(sz[0])];
+    for (size_t i = 0; i < sizeof(sz) / sizeof(sz[0]); ++i) {
+        ptr[i] = p;
+        p += align256(sz[i]);
+    }
+    hk::MoeBatchWs& w = m->bws;
+    w.x32 = static_cast<float*>(ptr[0]);
+    w.ximg = static_cast<uint8_t*>(ptr[1]);
+    w.ximg_e = static_cast<int32_t*>(ptr[2]);
+    w.part = static_cast<float*>(ptr[3]);
+    w.ids = static_cast<int32_t*>(ptr[4]);
+    w.w = static_cast<float*>(ptr[5]);
+    w.order = static_cast<int32_t*>(ptr[6]);
+    w.active = static_cast<uint4*>(ptr[7]);
+    w.n_active = static_cast<uint32_t*>(ptr[8]);
+    w.members = static_cast<uint32_t*>(ptr[9]);
+    w.act = static_cast<float*>(ptr[10]);
+    w.aimg = static_cast<uint8_t*>(ptr[11]);
+    w.aimg_e = static_cast<int32_t*>(ptr[12]);
+    w.ybuf = static_cast<float*>(ptr[13]);
+    w.ximg_stride = (uint32_t)xs;
+    w.aimg_stride = (uint32_t)as;
+    w.status = ctx->dev_status;
+    m->bws_tokens = T;
+    return HK_OK;
 }
 
 extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe_model** out) {
@@ -1268,6 +1323,13 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
     w += align256((size_t)c.hidden * 4);
     m->hbuf[1] = reinterpret_cast<float*>(w);
     m->ws.status = ctx->dev_status;
+    if (c.router == HK_ROUTER_NOAUX_TC && (rc = alloc_batch_ws(ctx, m))) {
+        (void)hipFree(m->dense);
+        (void)hipFree(m->tables);
+        (void)hipFree(m->ws_mem);
+        delete m;
+        return rc;
+    }
     *out = m;
     return HK_OK;
 }
@@ -1587,67 +1649,30 @@ extern "C" int hk_moe_decode_stack(hk_ctx* ctx, hk_moe_model* m, const float* h_
     return HK_OK;
 }
 
-// Grows the batched workspace to hold `T` tokens (synchronising the device
-// before freeing a smaller one).
-static int ensure_batch_ws(hk_ctx* ctx, hk_moe_model* m, uint32_t T) {
-    if (m->bws_mem && m->bws_tokens >= T) return HK_OK;
+extern "C" int hk_moe_block(hk_ctx* ctx, hk_moe_model* m, uint32_t layer, const int32_t* route_ids,
+                            const float* route_weights, uint32_t n_routes, int include_shared, const float* x,
+                            float* out, hk_stream stream) {
+    if (!ctx || !m) return HK_E_INVALID_ARG;
     const hk_moe_config& c = m->cfg;
-    T = std::max(T, std::min(32u, hk::MOE_BATCH_MAX_TOKENS));
-    const uint32_t imax = std::max(c.inter, c.shared_inter), K = c.top_k, E = c.n_experts;
-    const uint32_t S = (c.hidden + hk::MOE_BATCH_ROUTER_COLS - 1) / hk::MOE_BATCH_ROUTER_COLS;
-    const size_t pairs = (size_t)T * K + (c.shared_inter ? T : 0);
-    const size_t xs = align256(moe_batch_img_bytes(c.hidden)), as = align256(moe_batch_img_bytes(imax));
-    const size_t sz[] = {
-        (size_t)T * c.hidden * 4,          // x32
-        (size_t)T * xs,                    // ximg
-        (size_t)T * 4,                     // ximg_e
-        (size_t)S * T * E * 4,             // part
-        (size_t)T * K * 4,                 // ids
-        (size_t)T * K * 4,                 // w
-        (size_t)T * K * 4,                 // order
-        ((size_t)E + 1) * 16,              // active
-        4,                                 // n_active
-        pairs * 4,                         // members
-        pairs * imax * 4,                  // act
-        pairs * as,                        // aimg
-        pairs * 4,                         // aimg_e
-        pairs * c.hidden * 4,              // ybuf
-    };
-    size_t total = 0;
-    for (size_t b : sz) total += align256(b);
-    if (m->bws_mem) {
-        (void)hipDeviceSynchronize();
-        (void)hipFree(m->bws_mem);
-        m->bws_mem = nullptr;
-        m->bws_tokens = 0;
-    }
-    if (hipMalloc(&m->bws_mem, total) != hipSuccess) return set_error(ctx, HK_E_NOMEM, "batched MoE workspace allocation failed");
-    uint8_t* p = static_cast<uint8_t*>(m->bws_mem);
-    void* ptr[sizeof(sz) / sizeof(sz[0])];
-    for (size_t i = 0; i < sizeof(sz) / sizeof(sz[0]); ++i) {
-        ptr[i] = p;
-        p += align256(sz[i]);
-    }
-    hk::MoeBatchWs& w = m->bws;
-    w.x32 = static_cast<float*>(ptr[0]);
-    w.ximg = static_cast<uint8_t*>(ptr[1]);
-    w.ximg_e = static_cast<int32_t*>(ptr[2]);
-    w.part = static_cast<float*>(ptr[3]);
-    w.ids = static_cast<int32_t*>(ptr[4]);
-    w.w = static_cast<float*>(ptr[5]);
-    w.order = static_cast<int32_t*>(ptr[6]);
-    w.active = static_cast<uint4*>(ptr[7]);
-    w.n_active = static_cast<uint32_t*>(ptr[8]);
-    w.members = static_cast<uint32_t*>(ptr[9]);
-    w.act = static_cast<float*>(ptr[10]);
-    w.aimg = static_cast<uint8_t*>(ptr[11]);
-    w.aimg_e = static_cast<int32_t*>(ptr[12]);
-    w.ybuf = static_cast<float*>(ptr[13]);
-    w.ximg_stride = (uint32_t)xs;
-    w.aimg_stride = (uint32_t)as;
-    w.status = ctx->dev_status;
-    m->bws_tokens = T;
-    return HK_OK;
+    if (!route_ids || !route_weights || !x || !out) return set_error(ctx, HK_E_INVALID_ARG, "moe block: NULL pointer");
+    if (!aligned16(x) || !aligned16(out)) return set_error(ctx, HK_E_INVALID_ARG, "moe block: x/out must be 16-byte aligned");
+    if (n_routes == 0 || n_routes > c.top_k)
+        return set_error(ctx, HK_E_INVALID_ARG, "moe block: need 1 <= n_routes <= the model's top_k");
+    MoeLayerDev L;
+    int rc = moe_layer_dev(ctx, m, layer, &L);
+    if (rc) return rc;
+    const bool shared = include_shared && c.shared_inter;
+    const uint32_t slots = n_routes + (shared ? 1u : 0u), imax = std::max(c.inter, c.shared_inter);
+    if (moe_block_gate_up_lds_bytes(c.expert_kind, c.hidden) > MOE_LDS_LIMIT ||
+        moe_down_lds_bytes(c.expert_kind, imax, slots) > MOE_LDS_LIMIT)
+        return set_error(ctx, HK_E_UNSUPPORTED, "moe block: x images of hidden / intermediate exceed 64 KiB of LDS");
+    hk::MoeDims d = m->dims;
+    d.K = n_routes;
+    d.has_shared = shared ? 1 : 0;
+    return check_hip(ctx,
+                     launch_moe_block(c.expert_kind, d, L, route_ids, route_weights, x, out, m->ws,
+                                      static_cast<hipStream_t>(stream)),
+                     "moe block launch");
 }
 
 extern "C" int hk_moe_forward_batch(hk_ctx* ctx, hk_moe_model* m, uint32_t layer, const uint16_t* x_bf16,
@@ -1663,7 +1688,6 @@ extern "C" int hk_moe_forward_batch(hk_ctx* ctx, hk_moe_model* m, uint32_t layer
     MoeLayerDev L;
     int rc = moe_layer_dev(ctx, m, layer, &L);
     if (rc) return rc;
-    if ((rc = ensure_batch_ws(ctx, m, n_tokens))) return rc;
     hk::MoeBatchDims d{};
     d.T = n_tokens;
     d.H = c.hidden;

@@ -78,10 +78,12 @@ __global__ void __launch_bounds__(256) head_argmax_kernel(const float* __restric
 // The lowest index of the largest non-NaN logit among the first n_valid (the
 // reference's scan keeps the first maximum), or -1 and the status bit when
 // that logit is not finite or there is none; a token the norm marked -1
-// stays -1.
-__global__ void head_pick_kernel(const uint64_t* __restrict__ key, int32_t* __restrict__ token, uint32_t* status) {
+// stays -1.  The key is left zeroed for the next call.
+__global__ void head_pick_kernel(uint64_t* __restrict__ key, int32_t* __restrict__ token, uint32_t* status) {
     if (threadIdx.x == 0) {
         const uint64_t best = key[0];
+        key[0] = 0ull;
+        key[1] = 0ull;
         const uint32_t ord = (uint32_t)(best >> 32);
         const float v = __uint_as_float((ord & 0x80000000u) ? (ord & 0x7FFFFFFFu) : ~ord);
         const bool ok = best != 0ull && isfinite(v) && token[0] != -1;

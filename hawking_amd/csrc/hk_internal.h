@@ -183,19 +183,17 @@ struct hk_ctx {
     int device = 0;
     int last_status = HK_OK;
     std::string last_error;
-    // Library-owned device scratch reused across calls (grown on demand).
-    void* scratch = nullptr;
-    size_t scratch_bytes = 0;
     // Device word that kernels OR error bits into (read by hk_check_device_status).
     uint32_t* dev_status = nullptr;
+    // The packers' non-finite flag (its own 256-byte allocation; the packers
+    // synchronise their stream before they return, so calls never overlap).
+    uint32_t* pack_flag = nullptr;
 };
 
 namespace hk {
 
 int set_error(hk_ctx* ctx, int code, const std::string& msg);
 int check_hip(hk_ctx* ctx, hipError_t e, const char* what);
-// Grows ctx->scratch to at least `bytes` (device memory, 256-B aligned).
-int ensure_scratch(hk_ctx* ctx, size_t bytes, void** out);
 
 // Kernel launchers (defined in the .hip files); all stream-ordered, no sync.
 // GEMV over n organs of one kind/shape (descriptor table in device memory).
@@ -250,7 +248,8 @@ hipError_t pack_binary_rice_device(const float* w, uint32_t rows, uint32_t cols,
                                    RicePackResult* out, hipStream_t s);
 
 // Terminal head: the final RMSNorm(1+w) (one block) and the greedy pick.
-// key: an 8-byte device slot the pick reduces into (reset by the norm).
+// key: the caller's 16-byte device slot the pick reduces into (reset by the
+// norm, left zeroed by the pick).
 hipError_t launch_head_norm(const float* h, const float* w, uint32_t n, float eps, float* xn, int32_t* token,
                             uint64_t* key, uint32_t* status, hipStream_t s);
 hipError_t launch_head_argmax(const float* logits, uint32_t n_valid, uint64_t* key, int32_t* token, uint32_t* status,
@@ -288,8 +287,7 @@ struct hk_organ {
     hk::ResView res{};         // HGRAVR02 residual (res_dev non-null when present)
     void* res_mem = nullptr;
     const hk::ResView* res_dev = nullptr;
-    void* view_dev = nullptr;  // device copy of `view` for single-organ launches, then the head's pick key
-    uint64_t* head_key = nullptr;
+    void* view_dev = nullptr;  // device copy of `view` for single-organ launches
     void* mem = nullptr;
     size_t alloc_bytes = 0;
     size_t packed_bytes = 0;

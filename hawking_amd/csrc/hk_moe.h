@@ -43,6 +43,12 @@ size_t moe_img_bytes(int kind, uint32_t H);
 size_t moe_down_lds_bytes(int kind, uint32_t Imax, uint32_t slots);
 size_t moe_gate_up_lds_bytes(int kind, uint32_t H);
 
+// The expert block for caller routes (d.K = n_routes, d.has_shared = the
+// shared slot included): out += sum_r w_r mlp_r(x) (+ g mlp_shared(x)).
+size_t moe_block_gate_up_lds_bytes(int kind, uint32_t H);
+hipError_t launch_moe_block(int kind, const MoeDims& d, const MoeLayerDev& L, const int32_t* route_ids,
+                            const float* route_weights, const float* x, float* out, const MoeWs& ws, hipStream_t s);
+
 // ids_out / w_out (device, top_k each) may be null.
 hipError_t launch_moe_layer(int kind, const MoeDims& d, const MoeLayerDev& L, const float* h_in,
                             float* h_out, const MoeWs& ws, int32_t* ids_out, float* w_out, hipStream_t s);

@@ -223,9 +223,11 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev
     }
 }
 
+// h_in and h_out may be the same vector (each row is read, then written, by
+// one thread); route weights come from `wts` (slot order).
 template <int KIND, int D>
-__global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, const float* __restrict__ h_in,
-                                                        float* __restrict__ h_out, MoeWs ws, uint32_t img_stride) {
+__global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, const float* h_in, float* h_out, MoeWs ws,
+                                                        const float* __restrict__ wts, uint32_t img_stride) {
     extern __shared__ __align__(16) uint8_t lds[];
     const uint32_t T = blockIdx.x, slots = blockDim.x >> 6;
     const uint32_t slot = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -237,7 +239,7 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, const float* 
 #pragma unroll
     for (int k = 0; k < D; ++k)
         if ((uint32_t)k < S) fetch_one<KIND, 1>(o, T, (uint32_t)k, lane, f[k], 0);
-    const float wgt = !active ? 0.0f : (slot < d.K ? ws.weights[slot] : ws.gate[1]);
+    const float wgt = !active ? 0.0f : (slot < d.K ? wts[slot] : ws.gate[1]);
     // this slot's activations: staged in LDS with one batch of loads, then
     // turned into an x image of the slot's own
     uint8_t* img = lds + (size_t)slot * img_stride;
@@ -283,6 +285,126 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, const float* 
     }
 }
 
+// Gate/up of one (16-row tile, slot) of the expert block for caller routes
+// (BackendMoe::moe_block): slot r < d.K takes route_ids[r], slot d.K the
+// shared expert.  The slot's first weight steps are issued as soon as its id
+// is read; the workgroup then builds the x image of x itself (no route
+// kernel) and, for the shared slot, tile 0 forms the shared gate
+// sigmoid(wg . x) (1 without a gate).  Tile 0 publishes the slot's down organ.
+template <int KIND, int D>
+__global__ void __launch_bounds__(256) moe_block_gate_up_kernel(MoeDims d, MoeLayerDev L, MoeWs ws,
+                                                                const int32_t* __restrict__ route_ids,
+                                                                const float* __restrict__ x) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ float red[4];
+    const uint32_t slot = blockIdx.y, T = blockIdx.x;
+    const int lane = threadIdx.x & 63, q = lane >> 4;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool routed = slot < d.K;
+    const int32_t id = routed ? __builtin_amdgcn_readfirstlane(route_ids[slot]) : (int32_t)d.E;
+    // an invalid route selects no organ (all-zero down view: n_tiles = 0)
+    const bool ok = !routed || (id >= 0 && (uint32_t)id < d.E);
+    if (T == 0 && threadIdx.x < sizeof(OrganView) / 8) {
+        const uint64_t* from = reinterpret_cast<const uint64_t*>(L.table + (ok ? (uint32_t)id * 3u + 2u : 0u));
+        reinterpret_cast<uint64_t*>(ws.sel + slot * 3u + 2u)[threadIdx.x] = ok ? from[threadIdx.x] : 0ull;
+        if (!ok && threadIdx.x == 0) atomicOr(ws.status, HK_DEVERR_ROUTE);
+    }
+    if (!ok) return;
+    const OrganView g = L.table[(uint32_t)id * 3u + 0u];
+    if (T >= g.n_tiles) return;
+    const OrganView u = L.table[(uint32_t)id * 3u + 1u];
+    const uint32_t S = n_steps_for(KIND, d.H), ib = (uint32_t)x_lds_bytes<KIND>(S);
+    const uint32_t per = (S + 3u) / 4u;
+    const uint32_t s0 = min(wave * per, S), n = min(s0 + per, S) - s0;
+    Frag<KIND, 2> f[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+        if ((uint32_t)k < n) {
+            fetch_one<KIND, 2>(g, T, s0 + k, lane, f[k], 0);
+            fetch_one<KIND, 2>(u, T, s0 + k, lane, f[k], 1);
+        }
+    }
+    if (!routed && T == 0) {
+        // the shared-expert gate: sigmoid(wg . x), a block dot over 8-column chunks
+        float acc = 0.0f;
+        if (L.gate_w) {
+            for (uint32_t c = 8u * threadIdx.x; c < d.H; c += 8u * blockDim.x) {
+                float4 xv[2], wv[2];
+                load_chunk(x, c, d.H, xv);
+                load_chunk(L.gate_w, c, d.H, wv);
+                acc += dot4(xv[0], wv[0]) + dot4(xv[1], wv[1]);
+            }
+        }
+        const float lg = block_sum(acc, red);
+        if (threadIdx.x == 0) ws.gate[1] = L.gate_w ? 1.0f / (1.0f + expf(-lg)) : 1.0f;
+    }
+    bool bad = false;
+    XChunks<1> xc;
+    load_x<1>(BlockTeam{}, x, d.H, xc);
+    float* xq = reinterpret_cast<float*>(lds + ib + 4u * 32u * sizeof(float));
+    const int E = x_image<KIND, 1>(BlockTeam{}, xc, x, d.H, S, lds, xq, 0u, red, &bad);
+    if (bad && threadIdx.x == 0 && T == 0 && slot == 0) atomicOr(ws.status, HK_DEVERR_NONFINITE);
+    const ImageA A{lds, a_lane_offset(lane)};
+    const float* SX = reinterpret_cast<const float*>(lds + (size_t)S * Kcfg<KIND>::P * A_TILE_STRIDE);
+    float acc[2] = {0.0f, 0.0f};
+    for (uint32_t it = 0; it < n; it += D) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            if (it + k >= n) break;
+            compute_step<KIND, 2>(f[k], s0 + it + k, A, SX, q, acc);
+            const uint32_t nx = it + D + k;
+            if (nx < n) {
+                fetch_one<KIND, 2>(g, T, s0 + nx, lane, f[k], 0);
+                fetch_one<KIND, 2>(u, T, s0 + nx, lane, f[k], 1);
+            }
+        }
+    }
+    float* part = reinterpret_cast<float*>(lds + ib);  // [wave][gate 16 | up 16]
+    const float gs = tile_row_sum(acc[0]), us = tile_row_sum(acc[1]);
+    if (lane < 16) {
+        part[wave * 32u + lane] = gs;
+        part[wave * 32u + 16u + lane] = us;
+    }
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        float gv = 0.f, uv = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            gv += part[w * 32 + threadIdx.x];
+            uv += part[w * 32 + 16 + threadIdx.x];
+        }
+        gv = ldexpf(gv, -E);
+        uv = ldexpf(uv, -E);
+        const uint32_t row = T * 16u + threadIdx.x;
+        if (row < g.rows) ws.act[(size_t)slot * d.Imax + row] = (gv / (1.0f + expf(-gv))) * uv;
+    }
+}
+
+size_t moe_block_gate_up_lds_bytes(int kind, uint32_t H) {
+    return moe_gate_up_lds_bytes(kind, H) + (size_t)std::min<uint32_t>(stage_floats(kind, H), 2048u) * sizeof(float);
+}
+
+template <int KIND>
+static hipError_t launch_block(const MoeDims& d, const MoeLayerDev& L, const int32_t* route_ids,
+                               const float* route_weights, const float* x, float* out, const MoeWs& ws,
+                               hipStream_t s) {
+    const uint32_t slots = d.K + (d.has_shared ? 1u : 0u);
+    const uint32_t gu_tiles = n_tiles_for(d.has_shared ? max(d.I, d.SI) : d.I);
+    const uint32_t img_stride = (uint32_t)moe_img_bytes(KIND, d.Imax);
+    hipLaunchKernelGGL((moe_block_gate_up_kernel<KIND, 4>), dim3(gu_tiles, slots), dim3(256),
+                       moe_block_gate_up_lds_bytes(KIND, d.H), s, d, L, ws, route_ids, x);
+    hipLaunchKernelGGL((moe_down_kernel<KIND, 4>), dim3(n_tiles_for(d.H)), dim3(64u * slots),
+                       moe_down_lds_bytes(KIND, d.Imax, slots), s, d, out, out, ws, route_weights, img_stride);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_block(int kind, const MoeDims& d, const MoeLayerDev& L, const int32_t* route_ids,
+                            const float* route_weights, const float* x, float* out, const MoeWs& ws, hipStream_t s) {
+    if (kind == HK_Q4) return launch_block<HK_Q4>(d, L, route_ids, route_weights, x, out, ws, s);
+    if (kind == HK_MIXED) return launch_block<HK_MIXED>(d, L, route_ids, route_weights, x, out, ws, s);
+    return hipErrorInvalidValue;
+}
+
 template <int KIND>
 static hipError_t launch_layer(const MoeDims& d, const MoeLayerDev& L, const float* h_in, float* h_out,
                                const MoeWs& ws, int32_t* ids_out, float* w_out, hipStream_t s) {
@@ -304,7 +426,7 @@ static hipError_t launch_layer(const MoeDims& d, const MoeLayerDev& L, const flo
     else
         hipLaunchKernelGGL((moe_gate_up_kernel<KIND, 4, 64>), gg, dim3(256), gl, s, d, L, ws, ids_out, w_out);
     hipLaunchKernelGGL((moe_down_kernel<KIND, 4>), dim3(n_tiles_for(d.H)), dim3(64u * slots),
-                       moe_down_lds_bytes(KIND, d.Imax, slots), s, d, h_in, h_out, ws, img_stride);
+                       moe_down_lds_bytes(KIND, d.Imax, slots), s, d, h_in, h_out, ws, ws.weights, img_stride);
     return hipGetLastError();
 }
 

@@ -258,6 +258,12 @@ __device__ ArgBest softmax_topk_wave(const float* __restrict__ logits, uint32_t 
     const uint32_t C = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
     ArgBest mine{0.0f, -1};
     if (C <= 64u) {
+        // slots no candidate fills (fewer than k candidates: a NaN logit never
+        // passes p >= tf) stay id -1, weight 0; the status bit is already set
+        if ((uint32_t)lane < k) {
+            t->sel_i[lane] = -1;
+            t->sel_v[lane] = 0.0f;
+        }
         uint32_t o = incl - cnt;
 #pragma unroll
         for (int j = 0; j < NPL; ++j)

@@ -17,7 +17,9 @@ QWEN80_RMS_EPS = 1.0e-6
 
 class TerminalHead:
     """model.norm.weight + lm_head.weight bound on the device, with the
-    workspaces (normalised hidden state, logits, token) the call writes."""
+    workspaces (normalised hidden state, logits, pick key, token) the call
+    writes.  Heads that share an lm_head but not these workspaces may run on
+    different streams at once."""
 
     def __init__(self, ctx: Context, norm_w: np.ndarray, lm_head: PackedOrgan,
                  n_valid: int | None = None, eps: float = QWEN80_RMS_EPS):
@@ -30,6 +32,8 @@ class TerminalHead:
         self.xn = ctx.empty(lm_head.cols)
         self.logits = ctx.empty(lm_head.rows)
         self.token = ctx.empty(1, np.int32)
+        # the pick's 16-byte key slot: zero before the first call, left zeroed by each call
+        self.pick = ctx.to_device(np.zeros(2, np.uint64))
 
     def greedy_device(self, hidden, token=None, stream=None) -> None:
         """Enqueue the head; the token lands in `token` (or self.token)."""
@@ -37,7 +41,8 @@ class TerminalHead:
         hp = hidden.ptr if isinstance(hidden, DeviceArray) else hidden
         tp = out.ptr if isinstance(out, DeviceArray) else out
         self.ctx.call("hk_terminal_greedy", hp, self.norm_w.ptr, self.eps, self.lm_head.h, self.n_valid,
-                      self.xn.ptr, self.logits.ptr, tp, stream if stream is not None else self.ctx.stream)
+                      self.xn.ptr, self.logits.ptr, self.pick.ptr, tp,
+                      stream if stream is not None else self.ctx.stream)
 
     def greedy(self, hidden: np.ndarray) -> int:
         """Host convenience: upload, run, synchronise; HawkingError

@@ -184,6 +184,25 @@ class MoeModel:
                       _pp(ids), _pp(weights),
                       stream if stream is not None else self.ctx.stream)
 
+    def moe_block_device(self, layer: int, route_ids: DeviceArray, route_weights: DeviceArray, n_routes: int,
+                         x: DeviceArray, out: DeviceArray, include_shared: bool = True, stream=None) -> None:
+        """BackendMoe::moe_block: out += sum_r w_r mlp_r(x) (+ g mlp_shared(x)),
+        routes supplied by the caller on the device (hk_moe_block)."""
+        self.ctx.call("hk_moe_block", self.h, layer, _pp(route_ids), _pp(route_weights), n_routes,
+                      int(include_shared), _pp(x), _pp(out), stream if stream is not None else self.ctx.stream)
+
+    def moe_block(self, layer: int, route_ids, route_weights, x: np.ndarray, out: np.ndarray | None = None,
+                  include_shared: bool = True) -> np.ndarray:
+        """Host convenience of moe_block_device: returns out + combined (out
+        defaults to zeros)."""
+        ids = self.ctx.to_device(np.ascontiguousarray(route_ids, np.int32))
+        w = self.ctx.to_device(np.ascontiguousarray(route_weights, np.float32))
+        xd = self.ctx.to_device(np.ascontiguousarray(x, np.float32))
+        o = np.zeros(self.shape.hidden, np.float32) if out is None else np.ascontiguousarray(out, np.float32)
+        od = self.ctx.to_device(o)
+        self.moe_block_device(layer, ids, w, int(ids.shape[0]), xd, od, include_shared)
+        return od.download()
+
     def moe_suffix(self, layer: int, h: np.ndarray):
         """One layer on numpy input: returns (out, ids, weights)."""
         hd = self.ctx.to_device(np.ascontiguousarray(h, np.float32))

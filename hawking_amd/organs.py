@@ -340,16 +340,21 @@ class OrganSet:
 
 
 def gemv_lowrank_set(ctx: Context, lefts: OrganSet, rights: OrganSet, x: DeviceArray, x_stride: int,
-                     y: DeviceArray, y_stride: int, stream=None) -> None:
-    """y_i = L_i (R_i x_i) over the HGRAVS01 pairs of two organ sets in one
-    launch (hk_gemv_lowrank_set)."""
-    ctx.call("hk_gemv_lowrank_set", lefts.h, rights.h, x.ptr, x_stride, y.ptr, y_stride,
-             stream if stream is not None else ctx.stream)
+                     y: DeviceArray, y_stride: int, stream=None, mid: DeviceArray | None = None,
+                     mid_stride: int = 0) -> None:
+    """y_i = L_i (R_i x_i) over the HGRAVS01 pairs of two organ sets
+    (hk_gemv_lowrank_set): one launch for the shapes the fused kernel takes,
+    else two through `mid` (n x rank floats, required then); mid, when given,
+    receives R_i x_i."""
+    ctx.call("hk_gemv_lowrank_set", lefts.h, rights.h, x.ptr, x_stride, mid.ptr if mid is not None else None,
+             mid_stride, y.ptr, y_stride, stream if stream is not None else ctx.stream)
 
 
 def gemv_batch(ctx: Context, organs: list[PackedOrgan], x: DeviceArray, x_stride: int, y: DeviceArray,
                y_stride: int, stream=None) -> None:
-    """y_i = W_i x_i for organs of one kind and shape, in one launch."""
+    """y_i = W_i x_i for organs of one kind and shape, in one launch
+    (hk_gemv_batch: a synchronous helper that builds and frees a transient
+    organ set; stream-ordered callers keep an OrganSet)."""
     arr = (C.c_void_p * len(organs))(*[o.h.value for o in organs])
     ctx.call("hk_gemv_batch", arr, len(organs), x.ptr, x_stride, y.ptr, y_stride,
              stream if stream is not None else ctx.stream)

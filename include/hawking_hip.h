@@ -12,11 +12,13 @@
  *     substitute (mirrors the fail-closed fallback counters,
  *     model/qwen80_mixed_hybrid_decode.rs:4694-4699,4728-4733).
  *   - Compute entry points take DEVICE pointers, enqueue on the given HIP
- *     stream (hk_stream = hipStream_t; NULL = the null stream) and never
- *     synchronise, like CommandRecorder ops that record and do not commit
- *     (backend/mod.rs:36-41, 227-263).  Geometry is validated on the host
- *     before any launch (the reference kernels silently no-op on bad
- *     geometry, so its hosts validate first).
+ *     stream (hk_stream = hipStream_t; NULL = the null stream), allocate
+ *     nothing and never synchronise, like CommandRecorder ops that record
+ *     and do not commit (backend/mod.rs:36-41, 227-263).  Geometry is
+ *     validated on the host before any launch (the reference kernels
+ *     silently no-op on bad geometry, so its hosts validate first).
+ *   - Uploads, packers, model/set creation and the helpers marked
+ *     "synchronous" allocate and synchronise their stream before they return.
  *   - An hk_ctx is bound to one device and is not thread-safe: one per
  *     host thread.
  */
@@ -154,7 +156,7 @@ typedef struct hk_rice_q1 {
 } hk_rice_q1;
 
 /* Upload of an HGRAVR02 organ: the base is repacked like a binary organ; the
- * Rice stream is expanded once on the device into a CSR over rows
+ * Rice stream is expanded once, on the host at bind time, into a CSR over rows
  * (expand_rice_indices + rice_q1_row_ptr, q80_mixed_decode.rs:462-507, and
  * the bind of parse_rice_q1_container, 868-946).  Errors: HK_E_GEOMETRY for
  * a stream that overruns its bytes, a quotient or index above u32, or an index
@@ -177,9 +179,12 @@ int hk_organ_info(const hk_organ* organ, int32_t* kind, int32_t* group, uint32_t
  * of Qwen80Q4PackedTensor::matvec / binary_group_matvec_f32. */
 int hk_gemv(hk_ctx* ctx, const hk_organ* organ, const float* x, float* y, hk_stream stream);
 
-/* n organs of one kind and shape in ONE launch: y_i = W_i x_i with
- * x_i = x + i*x_stride, y_i = y + i*y_stride (element strides).  The batched
- * form of matvec_batch (gravity_glm.rs:515-548) / the routed wave. */
+/* SYNCHRONOUS helper: n organs of one kind and shape in ONE launch,
+ * y_i = W_i x_i with x_i = x + i*x_stride, y_i = y + i*y_stride (element
+ * strides).  The batched form of matvec_batch (gravity_glm.rs:515-548).  It
+ * builds a transient organ set (device allocation and a blocking copy),
+ * launches, synchronises `stream` and frees the set: stream-ordered callers
+ * create the set once (hk_organ_set_create) and call hk_gemv_set. */
 int hk_gemv_batch(hk_ctx* ctx, const hk_organ* const* organs, uint32_t n, const float* x,
                   size_t x_stride, float* y, size_t y_stride, hk_stream stream);
 
@@ -203,11 +208,15 @@ int hk_gemv_lowrank(hk_ctx* ctx, const hk_organ* left, const hk_organ* right, co
 /* y_i = L_i (R_i x_i) for the n HGRAVS01 pairs of two organ sets (left set of
  * HK_U3 rows x rank, right set of HK_U3 rank x cols, the same n), streamed in
  * ONE launch (one workgroup per pair, mid kept on chip) for the shapes
- * hk_gemv_lowrank fuses, else two set launches through library scratch.
+ * hk_gemv_lowrank fuses, else two set launches ordered on `stream` through
+ * mid.  mid (device, mid_i = mid + i*mid_stride, 16-byte aligned) may be
+ * NULL when the pair is fused; when given it receives R_i x_i; the two-launch
+ * shapes (right cols > 8192 or rank > 2048) require it (HK_E_INVALID_ARG).
  * Strides as hk_gemv_batch.  The set form of hgravs01_two_stage_matvec_f32
  * (q80_mixed_decode.rs:614-629) over a routed wave's down projections. */
 int hk_gemv_lowrank_set(hk_ctx* ctx, const hk_organ_set* left, const hk_organ_set* right, const float* x,
-                        size_t x_stride, float* y, size_t y_stride, hk_stream stream);
+                        size_t x_stride, float* mid, size_t mid_stride, float* y, size_t y_stride,
+                        hk_stream stream);
 
 /* Bit-exact decode probe: out[nrows*cols] = decoded weights of rows
  * [row0, row0+nrows).  Replaces qwen_uniform_q4_decode_vector
@@ -330,14 +339,17 @@ int hk_catalog_load(hk_ctx* ctx, hk_catalog* catalog, const char* name, int veri
  * token = the lowest index of the largest non-NaN logit among the first
  * n_valid (the rows past the tokenizer's vocabulary are never chosen).  All
  * pointers are device memory: hidden and norm_w [lm_head cols], xn [cols] and
- * logits [lm_head rows] are caller workspaces (16-byte aligned), token one
- * int32.  A non-finite xn or a best logit that is not finite writes token -1
- * and latches HK_E_NONFINITE in the device status (hk_check_device_status),
- * where the reference returns an error.  Stream-ordered, no host round trip;
- * the pick reduces into an 8-byte slot of the lm_head organ, so calls with one
- * lm_head must not overlap (same stream, or synchronised streams). */
+ * logits [lm_head rows] are caller workspaces (16-byte aligned), pick a
+ * 16-byte caller workspace (8-byte aligned) the greedy key reduces into,
+ * which must hold zeros before its first use and which every call leaves
+ * zeroed, token one int32.  A non-finite xn or a best logit that is not
+ * finite writes token -1 and latches HK_E_NONFINITE in the device status
+ * (hk_check_device_status), where the reference returns an error.
+ * Stream-ordered, no host round trip; the lm_head organ is only read, so
+ * calls with separate workspaces may share it across streams. */
 int hk_terminal_greedy(hk_ctx* ctx, const float* hidden, const float* norm_w, float eps, const hk_organ* lm_head,
-                       uint32_t n_valid, float* xn, float* logits, int32_t* token, hk_stream stream);
+                       uint32_t n_valid, float* xn, float* logits, uint64_t* pick, int32_t* token,
+                       hk_stream stream);
 
 /* ------------------------------------------------------------------ routers */
 
@@ -397,7 +409,11 @@ typedef struct hk_moe_layer_src {
 
 /* Expert table + per-layer dense weights in device memory: each expert's
  * gate|up|down laid out contiguously (Qwen80DeviceExpertTriplet,
- * model/qwen80_device_expert_table.rs:116-156). */
+ * model/qwen80_device_expert_table.rs:116-156).
+ * Limits (HK_E_UNSUPPORTED beyond): top_k + (1 if shared_inter) <= 16 (one
+ * wave per slot in the down kernel), n_experts <= 4096 (<= 512 for
+ * HK_ROUTER_NOAUX_TC), hidden % 128 == 0 and hidden <= 8192, and the x
+ * images of hidden / intermediate within 64 KiB of LDS. */
 int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe_model** out);
 int hk_moe_model_free(hk_ctx* ctx, hk_moe_model* model);
 int hk_moe_model_set_layer(hk_ctx* ctx, hk_moe_model* model, uint32_t layer,
@@ -431,6 +447,31 @@ int hk_moe_decode_layer(hk_ctx* ctx, hk_moe_model* model, uint32_t layer, const 
 int hk_moe_decode_stack(hk_ctx* ctx, hk_moe_model* model, const float* h_in, float* h_out,
                         int32_t* ids, float* weights, hk_stream stream);
 
+/* BackendMoe::moe_block (backend/mod.rs:509-521) on one layer of a model:
+ * the routed (and optional shared) expert block for CALLER-supplied routes,
+ * accumulated into out:
+ *   combined = sum_r w_r mlp_{id_r}(x)   (route order, r < n_routes)
+ *              + g * mlp_shared(x)        (include_shared and a shared expert;
+ *                                          g = sigmoid(shared_gate . x), or 1
+ *                                          for a model without the gate)
+ *   out = out + combined
+ * with mlp(x) = down(silu(gate x) * up x).  x is the block input (no
+ * RMSNorm, no router here); route_ids (int32) and route_weights (f32) are
+ * device arrays of n_routes entries, 1 <= n_routes <= the model's top_k.
+ * With include_shared = 0 and out zeroed this is
+ * run_qwen80_routed_expert_table's combined
+ * (model/qwen80_device_expert_table.rs:1204-1247, weighted_sum
+ * shaders/qwen80_device_expert_table.metal:430-446); moe_suffix is RMSNorm,
+ * the router (hk_router_softmax_topk) and this block with out = h.  An id
+ * outside [0, n_experts) contributes nothing and latches HK_E_ROUTE's device
+ * bit (hk_check_device_status).  x and out are device vectors of hidden
+ * floats, 16-byte aligned, and may be the same vector.  Two launches, no
+ * host round trip; calls on one model share its workspace and must not
+ * overlap. */
+int hk_moe_block(hk_ctx* ctx, hk_moe_model* model, uint32_t layer, const int32_t* route_ids,
+                 const float* route_weights, uint32_t n_routes, int include_shared, const float* x, float* out,
+                 hk_stream stream);
+
 /* The noaux_tc MoE block for a batch of tokens (routed_moe, gravity_glm.rs:550-600,
  * with batched_mlp :515-548): per token t, logits = Wr x_t; route = noaux_tc;
  * y_t = sum over the routed experts in ascending id of w_e mlp_e(x_t), then
@@ -439,8 +480,9 @@ int hk_moe_decode_stack(hk_ctx* ctx, hk_moe_model* model, const float* h_in, flo
  * [n_tokens x top_k] (device, route order) may be NULL.  Each active expert's
  * weights are streamed once for all of its tokens (grouped expert GEMM).
  * Requires router == HK_ROUTER_NOAUX_TC, expert_kind == HK_Q4, no shared gate,
- * n_tokens <= 64, n_experts <= 512, x and y 16-byte aligned.  The workspace for n_tokens is allocated
- * on first use (not graph-capturable until then). */
+ * n_tokens <= 64, n_experts <= 512, x and y 16-byte aligned.  The workspace
+ * (for 64 tokens) is allocated with the model; calls on one model must not
+ * overlap. */
 int hk_moe_forward_batch(hk_ctx* ctx, hk_moe_model* model, uint32_t layer, const uint16_t* x_bf16,
                          uint32_t n_tokens, float* y, int32_t* ids, float* weights, hk_stream stream);
 

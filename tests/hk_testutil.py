@@ -77,6 +77,34 @@ def oracle_layer(oracle, seed, shape, layer, h):
     return L, out, ids2, w, logits2
 
 
+def oracle_layer_cached(oracle, seed, shape, layer, h, cache, pool=None):
+    """oracle_layer with the generated expert organs kept in `cache`
+    ((layer, expert) -> (gate, up, down)) and generated on `pool` (a
+    thread pool: the oracle's C calls release the GIL).  Returns
+    (layer_obj, out, ids, weights, logits, xn)."""
+    norm, router, gate = cache.get(("dense", layer)) or dense(oracle, seed, shape, layer)
+    cache[("dense", layer)] = (norm, router, gate)
+    xn = oracle.rmsnorm_1p(h, norm, shape.eps)
+    logits = oracle.gemv_f32(router, xn)
+    ids, _ = oracle.router_softmax_topk(logits, shape.top_k)
+    want = [int(e) for e in ids] + ([shape.n_experts] if shape.shared_inter else [])
+    todo = [(e, p) for e in want if (layer, e) not in cache for p in range(3)]
+    make = lambda ep: oracle_organ(oracle, seed, shape, layer, ep[0], ep[1])
+    made = list(pool.map(make, todo)) if pool is not None else [make(t) for t in todo]
+    for i in range(0, len(todo), 3):
+        cache[(layer, todo[i][0])] = tuple(made[i:i + 3])
+    experts = [None] * shape.n_experts
+    for e in ids.tolist():
+        experts[e] = cache[(layer, e)]
+    shared = cache[(layer, shape.n_experts)] if shape.shared_inter else None
+    L = oracle.MoeLayer(shape.hidden, shape.inter, shape.n_experts, shape.top_k, norm, router, experts,
+                        shared=shared, shared_gate_w=gate if (shape.shared_gate and shape.shared_inter) else None,
+                        eps=shape.eps)
+    out, ids2, w, xn2, logits2 = L.forward(h)
+    assert np.array_equal(ids, ids2)
+    return L, out, ids2, w, logits2, xn2
+
+
 def router_margin_ok(logits: np.ndarray, k: int, rel: float = 1e-4) -> bool:
     """Router margin rule: the f64 gap between the k-th and (k+1)-th
     score must be >= rel * max|score| for ids to be compared bit-exactly."""

@@ -22,7 +22,7 @@ def declared_functions():
 
 def test_header_declares_the_boundary():
     names = declared_functions()
-    for must in ("hk_ctx_create", "hk_gemv", "hk_gemv_batch", "hk_decode_rows", "hk_router_softmax_topk",
+    for must in ("hk_ctx_create", "hk_gemv", "hk_gemv_batch", "hk_decode_rows", "hk_router_softmax_topk", "hk_moe_block",
                  "hk_router_noaux_tc", "hk_moe_decode_layer", "hk_moe_decode_stack", "hk_last_error"):
         assert must in names
 

@@ -1,0 +1,104 @@
+"""Config 4 at full depth: the 48-layer Qwen3-Next-shaped MoE stack in the
+mixed <=1.5 BPW per-group format (hidden 2048, 512 experts x inter 512,
+top-10 softmax + renorm, gated shared expert, RMSNorm(1+w) eps 1e-6), one
+token at batch 1 (forward_token's MoE suffixes,
+crates/hawking-core/src/model/qwen80_mixed_hybrid_decode.rs:4682-4736, with
+moe_suffix :3636-3752).
+
+Checks, against the oracle (which regenerates only the routed and shared
+experts of each layer):
+  * layer by layer on the device's own hidden state: route ids exact,
+    router weights within 1e-6, the layer output within 2e-5 rel-L2 of the
+    oracle's f32 moe_suffix and of its FP64 authority;
+  * hk_moe_decode_stack's ids, weights and final state equal the 48
+    chained single-layer calls bit for bit;
+  * the final state within 2e-5 rel-L2 of the oracle's own 48-layer f32
+    chain and of the FP64 chain (same routes).
+Router margin rule: the oracle's f64-sorted logits must keep the 10th/11th
+gap >= 1e-4 max|logit| at every layer; otherwise the input's seed advances
+(0xC4, 0xC5, ...) and the walk restarts.
+"""
+import concurrent.futures as cf
+import sys
+
+import numpy as np
+import pytest
+
+from tests import hk_testutil as U
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-5
+N_LAYERS = 48
+
+
+def say(*a):
+    print("[gpu-case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from hawking_amd.runtime import Context
+    return Context(0)
+
+
+def test_config4_48_layer_stack_layer_by_layer(ctx, oracle):
+    from hawking_amd.moe import MoeModel, MoeShape
+    shape = MoeShape(n_layers=N_LAYERS, hidden=2048, inter=512, shared_inter=512, n_experts=512, top_k=10,
+                     expert_kind=U.HK_MIXED, expert_group=128)
+    say("config4: 48 mixed layers, device fill")
+    m = MoeModel(ctx, shape)
+    m.fill_synthetic(U.SEED)
+    ctx.device_status()
+    cache = {}
+    with cf.ThreadPoolExecutor(max_workers=8) as pool:
+        for attempt in range(4):
+            h0 = oracle.normal(oracle.stream_key(U.SEED, 0xC4 + attempt), 2048, 1.0)
+            out, sids, sw = m.forward_token(h0)
+            h = h0
+            near_tie = None
+            for layer in range(N_LAYERS):
+                g_out, g_ids, g_w = m.moe_suffix(layer, h)
+                L, r_out, r_ids, r_w, logits, xn = U.oracle_layer_cached(oracle, U.SEED, shape, layer, h, cache, pool)
+                if not U.router_margin_ok(logits, shape.top_k):
+                    near_tie = layer
+                    break
+                assert g_ids.tolist() == r_ids.tolist(), f"layer {layer}"
+                assert np.max(np.abs(g_w - r_w)) <= 1e-6, f"layer {layer}"
+                assert oracle.relative_l2(g_out, r_out) < TOL, f"layer {layer}"
+                assert oracle.relative_l2(g_out, L.forward_f64(h, g_ids)) < TOL, f"layer {layer}"
+                assert g_ids.tolist() == sids[layer].tolist() and np.array_equal(g_w, sw[layer]), f"layer {layer}"
+                if layer % 8 == 7:
+                    say(f"layer {layer} ok (attempt {attempt})")
+                h = g_out
+            if near_tie is None:
+                break
+            say(f"near tie at layer {near_tie}: advancing the input seed")
+        else:
+            pytest.fail("four input seeds all met a router near tie")
+        assert np.array_equal(out, h), "stack != chained single-layer calls"
+
+        # the oracle's own chains from h0: FP64 on the stack's routes (in a
+        # worker thread), and f32 with its own routes, which must agree
+        def chain64():
+            r64 = h0.astype(np.float64)
+            for layer in range(N_LAYERS):
+                norm, router, gate = cache[("dense", layer)]
+                experts = [None] * shape.n_experts
+                for e in sids[layer].tolist():
+                    experts[e] = cache[(layer, e)]
+                L = oracle.MoeLayer(shape.hidden, shape.inter, shape.n_experts, shape.top_k, norm, router, experts,
+                                    shared=cache[(layer, shape.n_experts)], shared_gate_w=gate, eps=shape.eps)
+                r64 = L.forward_f64(r64, sids[layer])
+            return r64
+
+        fut64 = pool.submit(chain64)
+        r = h0
+        for layer in range(N_LAYERS):
+            _, r, r_ids, _, _, _ = U.oracle_layer_cached(oracle, U.SEED, shape, layer, r, cache, pool)
+            assert r_ids.tolist() == sids[layer].tolist(), f"oracle chain route differs at layer {layer}"
+        r64 = fut64.result()
+    say("final state vs f32 chain / FP64 chain")
+    assert oracle.relative_l2(out, r) < TOL
+    assert oracle.relative_l2(out, r64) < TOL
+    assert ctx.device_status() == 0

@@ -102,3 +102,49 @@ def test_organ_wider_than_lds_image_is_rejected(ctx):
     with pytest.raises(HawkingError) as e:
         organs.SyntheticOrgan(ctx, HK_BIN, 16, 16384, 1, 2)
     assert e.value.code == HK_E_GEOMETRY
+
+
+def _oracle_decode(oracle, kind, group, rows, cols, key, coin_key):
+    """The oracle's pack of the same draws, decoded, and its canonical byte count."""
+    w = oracle.normal(key, rows * cols, U.SIGMA_W).reshape(rows, cols)
+    if kind == HK_BIN:
+        s, g = oracle.bin_pack(w)
+        return oracle.bin_decode(s, g, rows, cols), s.nbytes + g.nbytes
+    if kind == HK_Q4:
+        s, c = oracle.q4_pack(w, group)
+        return oracle.q4_decode(s, c, rows, cols, group), s.nbytes + c.nbytes
+    if kind == HK_Q8:
+        s, c = oracle.uniform_pack(w, rows, cols, 8, 64)
+        return oracle.uniform_decode(s, c, rows, cols, 8, 64), s.nbytes + c.nbytes
+    m = oracle.mixed_pack(w, oracle.mixed_coins(coin_key, rows * cols // 128))
+    return oracle.mixed_decode(m), m.nbytes()
+
+
+SYNTH = [
+    ("q4 g32", HK_Q4, 32, 512, 2048),
+    ("q4 g64", HK_Q4, 64, 48, 1024),
+    ("q4 g128", HK_Q4, 128, 40, 640),
+    ("bin 512x2048", HK_BIN, 128, 512, 2048),
+    ("bin 2048x512", HK_BIN, 128, 2048, 512),
+    ("mixed 512x2048", HK_MIXED, 128, 512, 2048),
+    ("mixed 2048x512", HK_MIXED, 128, 2048, 512),
+    ("mixed ragged", HK_MIXED, 128, 33, 1152),
+    ("q8 512x2048", HK_Q8, 64, 512, 2048),
+]
+
+
+@pytest.mark.parametrize("label,kind,group,rows,cols", SYNTH, ids=[c[0] for c in SYNTH])
+def test_synthetic_organ_decodes_bit_exact(ctx, oracle, label, kind, group, rows, cols):
+    """hk_organ_synthetic (device draws, device packer, load-time repack: the
+    path that builds the benchmark's organs and the config-4 model) decodes
+    bit for bit to the oracle's pack of the same draws (hk_decode_rows), and
+    reports the oracle's canonical byte count."""
+    from hawking_amd import organs
+    say("synthetic decode", label)
+    tag = 0x400 + SYNTH.index((label, kind, group, rows, cols))
+    k, ck = _keys(oracle, tag, 0)
+    o = organs.SyntheticOrgan(ctx, kind, rows, cols, k, ck, group=group)
+    want, nbytes = _oracle_decode(oracle, kind, group, rows, cols, k, ck)
+    got = o.decode()
+    assert np.array_equal(got.view(np.uint32), np.asarray(want, np.float32).reshape(rows, cols).view(np.uint32))
+    assert o.packed_bytes == nbytes

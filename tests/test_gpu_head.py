@@ -92,3 +92,37 @@ def test_terminal_head_flags_nonfinite(ctx, oracle, value):
     assert e.value.code == HK_E_NONFINITE
     assert int(head.token.download()[0]) == -1
     assert head.greedy(h) == oracle.argmax_greedy(head.logits.download())   # recovers on good input
+
+
+def test_two_heads_share_one_lm_head_on_two_streams(ctx, oracle):
+    """The lm_head organ is read-only: two heads over one lm_head with their
+    own workspaces run on two streams at once and each gets its own token."""
+    from hawking_amd.head import TerminalHead
+    from hawking_amd.organs import UniformFactorPacked
+    vocab, hidden_n = 8192, 1024
+    h1, nw, w = _inputs(oracle, vocab, hidden_n, "s")
+    h2 = oracle.normal(oracle.stream_key(U.SEED, 0xF2F2), hidden_n, 1.0)
+    s, c = oracle.uniform_pack(w, vocab, hidden_n, 8, 64)
+    lm = UniformFactorPacked(ctx, s, c, vocab, hidden_n)
+    a, b = TerminalHead(ctx, nw, lm), TerminalHead(ctx, nw, lm)
+    sa, sb = ctx.new_stream(), ctx.new_stream()
+    say("two heads, two streams")
+    refs = [oracle.terminal_greedy(hh, nw, s, c, vocab, vocab) for hh in (h1, h2)]
+    d1, d2 = ctx.to_device(h1), ctx.to_device(h2)
+    ctx.synchronize()
+    for _ in range(20):
+        a.greedy_device(d1, stream=sa)
+        b.greedy_device(d2, stream=sb)
+    ctx.call("hk_stream_synchronize", sa)
+    ctx.call("hk_stream_synchronize", sb)
+    ta, tb = int(a.token.download()[0]), int(b.token.download()[0])
+    assert ta == oracle.argmax_greedy(a.logits.download(), vocab)
+    assert tb == oracle.argmax_greedy(b.logits.download(), vocab)
+    for tok, head, (rtok, rlog) in ((ta, a, refs[0]), (tb, b, refs[1])):
+        assert oracle.relative_l2(head.logits.download(), rlog) < TOL
+        top2 = np.sort(rlog)[-2:]
+        if top2[1] - top2[0] > 1e-4 * np.abs(rlog).max():
+            assert tok == rtok
+    assert a.pick.download().tolist() == [0, 0] and b.pick.download().tolist() == [0, 0]
+    ctx.call("hk_stream_destroy", sa)
+    ctx.call("hk_stream_destroy", sb)

@@ -183,6 +183,36 @@ def test_decode_router_exact_ties_and_flat_logits(ctx, oracle):
             assert pos == sorted(pos)
 
 
+def test_decode_router_nan_logit_leaves_no_unset_slot(ctx, oracle):
+    """One NaN router logit (a NaN in one router row): the status bit is set,
+    and every published route slot is a valid distinct id or -1 with weight
+    0 -- never an unset slot (a NaN probability is never a candidate, so
+    fewer than k candidates can remain)."""
+    from hawking_amd.moe import MoeModel, MoeShape
+    E, K = 64, 8
+    shape = MoeShape(n_layers=1, hidden=256, inter=128, shared_inter=128, n_experts=E, top_k=K,
+                     expert_kind=U.HK_Q4, expert_group=32)
+    seed = 78
+    experts = [tuple(U.oracle_organ(oracle, seed, shape, 0, e, p) for p in range(3)) for e in range(E)]
+    shared = tuple(U.oracle_organ(oracle, seed, shape, 0, E, p) for p in range(3))
+    norm, router, gate = U.dense(oracle, seed, shape, 0)
+    h = oracle.normal(oracle.stream_key(U.SEED, 0x7A7), 256, 1.0)
+    m = MoeModel(ctx, shape)
+    for label, rows in (("one NaN row", [9]), ("all NaN", list(range(E)))):
+        say("decode router", label)
+        R = router.copy()
+        R[rows, 3] = np.nan
+        m.set_layer(0, norm, R, [tuple(U.organ_dict(o) for o in t) for t in experts],
+                    shared=[U.organ_dict(o) for o in shared], shared_gate_w=gate)
+        ctx.device_status()
+        out, ids, w = m.moe_suffix(0, h)
+        assert ctx.device_status() & 1
+        valid = [int(i) for i in ids if i >= 0]
+        assert all(i < E for i in valid) and len(set(valid)) == len(valid)
+        assert all((i >= 0) or (wt == 0.0) for i, wt in zip(ids.tolist(), w.tolist()))
+        assert set(ids.tolist()) <= set(range(E)) | {-1}
+
+
 @pytest.mark.parametrize("kind", [U.HK_Q4, U.HK_MIXED])
 def test_synthetic_layer_matches_oracle_regeneration(ctx, oracle, kind):
     """Device-generated weights == oracle-regenerated weights, end to end."""

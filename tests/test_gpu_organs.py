@@ -284,6 +284,9 @@ def test_hgravs01_set_one_launch_matches_two_launches(ctx, oracle, rows, rank, c
     ls.gemv(mid, rank, y2, rows)
     a, b = y1.download(), y2.download()
     assert np.array_equal(a, b)
+    y3, mid3 = ctx.empty((n, rows)), ctx.empty((n, rank))
+    gemv_lowrank_set(ctx, ls, rs, xd, cols, y3, rows, mid=mid3, mid_stride=rank)
+    assert np.array_equal(y3.download(), a) and np.array_equal(mid3.download(), mid.download())
     for i in range(n):
         (ls_, lc), (rs_, rc) = packs[i]
         ref = oracle.hgravs01_matvec((ls_, lc), (rs_, rc), rows, rank, cols, xs[i], 3, 64)
@@ -291,6 +294,37 @@ def test_hgravs01_set_one_launch_matches_two_launches(ctx, oracle, rows, rank, c
         Rd = oracle.uniform_decode(rs_, rc, rank, cols, 3, 64).astype(np.float64)
         assert oracle.relative_l2(a[i], ref) < TOL
         assert oracle.relative_l2(a[i], Ld.reshape(rows, rank) @ (Rd.reshape(rank, cols) @ xs[i].astype(np.float64))) < TOL
+
+
+def test_hgravs01_set_two_launch_shape_uses_caller_mid(ctx, oracle):
+    """A rank above 2048 runs as two set launches through the caller's mid
+    workspace (no library scratch); without one the call is refused."""
+    from hawking_amd._lib import HK_E_INVALID_ARG, HawkingError
+    from hawking_amd.organs import OrganSet, gemv_lowrank_set
+    rows, rank, cols, n = 64, 2080, 256, 2
+    say("hgravs01 set, two-launch shape", rows, rank, cols)
+    lefts, rights, packs, xs = [], [], [], []
+    for i in range(n):
+        key = lambda k: oracle.stream_key(U.SEED, (0xE6 << 20) + 16 * i + k)
+        lo, lp = _u3(ctx, oracle, oracle.normal(key(1), rows * rank, 0.05).reshape(rows, rank))
+        ro, rp = _u3(ctx, oracle, oracle.normal(key(2), rank * cols, 0.02).reshape(rank, cols))
+        lefts.append(lo)
+        rights.append(ro)
+        packs.append((lp, rp))
+        xs.append(oracle.normal(key(3), cols, 1.0))
+    ls, rs = OrganSet(ctx, lefts), OrganSet(ctx, rights)
+    xd = ctx.to_device(np.stack(xs))
+    y = ctx.empty((n, rows))
+    with pytest.raises(HawkingError) as e:
+        gemv_lowrank_set(ctx, ls, rs, xd, cols, y, rows)
+    assert e.value.code == HK_E_INVALID_ARG
+    mid = ctx.empty((n, rank))
+    gemv_lowrank_set(ctx, ls, rs, xd, cols, y, rows, mid=mid, mid_stride=rank)
+    a = y.download()
+    for i in range(n):
+        (ls_, lc), (rs_, rc) = packs[i]
+        ref = oracle.hgravs01_matvec((ls_, lc), (rs_, rc), rows, rank, cols, xs[i], 3, 64)
+        assert oracle.relative_l2(a[i], ref) < TOL
 
 
 @pytest.mark.parametrize("rows,rank,cols", [(2048, 160, 768), (768, 192, 2048), (16, 32, 32)])
