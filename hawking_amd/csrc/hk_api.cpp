@@ -637,9 +637,10 @@ extern "C" int hk_gemv_lowrank_set(hk_ctx* ctx, const hk_organ_set* left, const 
     if (left->n != right->n || right->first.rows != left->first.cols)
         return set_error(ctx, HK_E_GEOMETRY,
                          "hk_gemv_lowrank_set: the sets need as many organs and right rows (the rank) = left cols");
-    int rc = check_vectors(ctx, "hk_gemv_lowrank_set", x, x_stride, y, y_stride, left->n, right->first);
-    if (!rc && left->n > 1 && y_stride < left->first.rows)
-        rc = set_error(ctx, HK_E_GEOMETRY, "hk_gemv_lowrank_set: y stride smaller than the left factor's rows");
+    // x is the right factor's input, y the left factor's output
+    OrganView io = right->first;
+    io.rows = left->first.rows;
+    int rc = check_vectors(ctx, "hk_gemv_lowrank_set", x, x_stride, y, y_stride, left->n, io);
     if (rc) return rc;
     const bool fused = lowrank_fusable(left->first, right->first);
     if (mid) {

@@ -320,7 +320,7 @@ __device__ ArgBest softmax_topk_wave(const float* __restrict__ logits, uint32_t 
     if (renorm) {
         float sel = -0.0f;
         for (uint32_t r = 0; r < k; ++r) sel += __shfl(mine.v, (int)r, 64);
-        mine.v = mine.v / sel;
+        mine.v = mine.i >= 0 ? mine.v / sel : 0.0f;
     }
     if ((uint32_t)lane < k) {
         if (ids_out) ids_out[lane] = mine.i;
