@@ -119,6 +119,7 @@ PROTOTYPES = {
     "hk_organ_upload_rice": (C.c_int, [_p, C.POINTER(RiceQ1Src), _p, C.POINTER(_p)]),
     "hk_rice_apply": (C.c_int, [_p, _p, _p, _p, _p]),
     "hk_terminal_greedy": (C.c_int, [_p, _p, _p, C.c_float, _p, _u32, _p, _p, _p, _p, _p]),
+    "hk_terminal_greedy_noalloc": (C.c_int, [_p, _p, _p, C.c_float, _p, _u32, _p, _p]),
     "hk_organ_from_container": (C.c_int, [_p, _i32, _p, _sz, _p, C.POINTER(_p), C.POINTER(_p)]),
     "hk_organ_from_hq30": (C.c_int, [_p, _p, _sz, _p, C.POINTER(_p)]),
     "hk_catalog_open": (C.c_int, [_p, C.c_char_p, C.POINTER(_p)]),

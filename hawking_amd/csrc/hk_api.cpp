@@ -9,6 +9,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -247,6 +248,37 @@ static int copy_src(hk_ctx* ctx, const hk_organ_src* s, const Layout& L, uint8_t
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// ---- the no-allocation entry point's workspace
+// hk_terminal_greedy_noalloc keeps the head's logits, xn and pick slot in
+// this file-scope device array: every device the library runs on holds one
+// copy until the process ends.  Host code never passes the array's name to
+// a kernel (on the host it is only a stand-in symbol); it uses the device
+// address hipGetSymbolAddress returns, looked up once per device by
+// hk_ctx_create with that device current.
+constexpr size_t NOALLOC_LOGITS = (size_t)HK_NOALLOC_HEAD_MAX_ROWS * 4;
+constexpr size_t NOALLOC_XN = (size_t)HK_NOALLOC_HEAD_MAX_COLS * 4;
+constexpr size_t NOALLOC_BYTES = NOALLOC_LOGITS + NOALLOC_XN + 256;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_BYTES];
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static uint8_t* g_scratch_dev[NOALLOC_MAX_DEVICES] = {};
+static std::mutex g_scratch_mu;
+
+// Device address of this device's copy of `scratch` (looked up on the
+// first call for the device; the caller has made the device current).
+static int noalloc_scratch(hk_ctx* ctx, uint8_t** out) {
+    if (ctx->device < 0 || ctx->device >= NOALLOC_MAX_DEVICES)
+        return set_error(ctx, HK_E_UNSUPPORTED, "no-allocation workspace: device index above 63");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[ctx->device]) {
+        void* ptr = nullptr;
+        hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return check_hip(ctx, e, "hipGetSymbolAddress (no-allocation workspace)");
+        g_scratch_dev[ctx->device] = static_cast<uint8_t*>(ptr);
+    }
+    *out = g_scratch_dev[ctx->device];
+    return HK_OK;
+}
+
 }  // namespace hk
 
 using namespace hk;
@@ -273,6 +305,12 @@ extern "C" int hk_ctx_create(int device, hk_ctx** out) {
     (void)hipMemset(st, 0, 512);
     ctx->dev_status = static_cast<uint32_t*>(st);
     ctx->pack_flag = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(st) + 256);
+    // this device's copy of the no-allocation workspace, with the device current
+    if (noalloc_scratch(ctx, &ctx->noalloc) != HK_OK) {
+        (void)hipFree(st);
+        delete ctx;
+        return HK_E_HIP;
+    }
     *out = ctx;
     return HK_OK;
 }
@@ -1073,6 +1111,33 @@ extern "C" int hk_terminal_greedy(hk_ctx* ctx, const float* hidden, const float*
     if (!aligned16(hidden)) return set_error(ctx, HK_E_INVALID_ARG, "hk_terminal_greedy: hidden must be 16-byte aligned");
     if (reinterpret_cast<uintptr_t>(pick) & 7u)
         return set_error(ctx, HK_E_INVALID_ARG, "hk_terminal_greedy: pick must be 8-byte aligned");
+    return head_greedy(ctx, hidden, norm_w, eps, lm_head, n_valid, xn, logits, pick, token,
+                       static_cast<hipStream_t>(stream));
+}
+
+extern "C" int hk_terminal_greedy_noalloc(hk_ctx* ctx, const float* hidden, const float* norm_w, float eps,
+                                          const hk_organ* lm_head, uint32_t n_valid, int32_t* token,
+                                          hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (!lm_head || !hidden || !norm_w || !token)
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_terminal_greedy_noalloc: NULL argument");
+    if (lm_head->view.rows > HK_NOALLOC_HEAD_MAX_ROWS || lm_head->view.cols > HK_NOALLOC_HEAD_MAX_COLS)
+        return set_error(ctx, HK_E_UNSUPPORTED,
+                         "hk_terminal_greedy_noalloc: lm_head above the workspace's " +
+                             std::to_string(HK_NOALLOC_HEAD_MAX_ROWS) + " rows x " +
+                             std::to_string(HK_NOALLOC_HEAD_MAX_COLS) + " cols");
+    if (n_valid == 0 || n_valid > lm_head->view.rows)
+        return set_error(ctx, HK_E_GEOMETRY, "hk_terminal_greedy_noalloc: need 0 < n_valid <= lm_head rows");
+    if (!(eps >= 0.0f) || !std::isfinite(eps))
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_terminal_greedy_noalloc: bad eps");
+    if (!aligned16(hidden))
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_terminal_greedy_noalloc: hidden must be 16-byte aligned");
+    // [logits | xn | pick]: the pick slot is zero (static storage, and every
+    // call leaves it zeroed)
+    uint8_t* ws = ctx->noalloc;
+    float* logits = reinterpret_cast<float*>(ws);
+    float* xn = reinterpret_cast<float*>(ws + NOALLOC_LOGITS);
+    uint64_t* pick = reinterpret_cast<uint64_t*>(ws + NOALLOC_LOGITS + NOALLOC_XN);
     return head_greedy(ctx, hidden, norm_w, eps, lm_head, n_valid, xn, logits, pick, token,
                        static_cast<hipStream_t>(stream));
 }

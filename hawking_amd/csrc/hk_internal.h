@@ -188,6 +188,8 @@ struct hk_ctx {
     // The packers' non-finite flag (its own 256-byte allocation; the packers
     // synchronise their stream before they return, so calls never overlap).
     uint32_t* pack_flag = nullptr;
+    // This device's copy of the no-allocation workspace (a static device array).
+    uint8_t* noalloc = nullptr;
 };
 
 namespace hk {

@@ -351,6 +351,20 @@ int hk_terminal_greedy(hk_ctx* ctx, const float* hidden, const float* norm_w, fl
                        uint32_t n_valid, float* xn, float* logits, uint64_t* pick, int32_t* token,
                        hk_stream stream);
 
+/* NO reference counterpart: hk_terminal_greedy for callers that cannot
+ * allocate (code under HIP graph capture, serving loops that forbid
+ * hipMalloc): the same result with the xn, logits and pick workspaces in a
+ * library-owned static device array of 1 MiB + 32 KiB + 256 B per device,
+ * held until the process ends.  Limits: lm_head rows <= HK_NOALLOC_HEAD_MAX_ROWS,
+ * cols <= HK_NOALLOC_HEAD_MAX_COLS (HK_E_UNSUPPORTED beyond).  Allocates
+ * nothing.  Every call on a device shares that device's array, which keeps
+ * the last call's xn and logits: calls that overlap on one device race (use
+ * one stream, or synchronised streams). */
+#define HK_NOALLOC_HEAD_MAX_ROWS 262144
+#define HK_NOALLOC_HEAD_MAX_COLS 8192
+int hk_terminal_greedy_noalloc(hk_ctx* ctx, const float* hidden, const float* norm_w, float eps,
+                               const hk_organ* lm_head, uint32_t n_valid, int32_t* token, hk_stream stream);
+
 /* ------------------------------------------------------------------ routers */
 
 /* Per token: softmax over n_experts logits, top_k by strict '>' (lowest index
