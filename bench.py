@@ -18,13 +18,20 @@ batched block.
 The CPU baseline is the oracle's serial restatement of
 binary_group_matvec_f32 (crates/hawking-core/src/model/qwen_complete_binary/
 q80_mixed_decode.rs:245-257) on a bounded sample of the same organs, one
-thread, timed on this host.
+thread, timed on this host; "extra.cpu_baselines" times the oracle on the
+other configs the same way (c1 Q4 organ, c3 layer, c4 token from a sample of
+layers, c5 block from a sample of tokens) and the c2 organ on every host
+thread.  `--only NAME` runs one workload and prints its result (for
+profiler runs).
 """
 from __future__ import annotations
 
 import argparse
+import concurrent.futures as cf
 import json
 import os
+import platform
+import subprocess
 import sys
 import time
 
@@ -255,6 +262,40 @@ def moe_bench(ctx, shape, steps, warmup, n_inputs=16):
             "model_device_bytes": dev_bytes, "gen_seconds": round(gen_s, 2), "layers": L}
 
 
+def moe_layer_cold_bench(ctx, steps, warmup, n_layers=16, n_inputs=16):
+    """Config 3's layer with the MALL defeated: a 16-layer model of c3 layers
+    (distinct weights), step i runs layer i % 16 on input i % 16, so the
+    bytes a step touches (about 24 MB) were last read 16 steps (about
+    380 MB of other layers' data) earlier."""
+    from hawking_amd.moe import MoeModel, MoeShape
+    from hawking_amd.organs import stream_key
+    shape = MoeShape(n_layers=n_layers, hidden=2048, inter=512, shared_inter=512, n_experts=512, top_k=10,
+                     expert_kind=HK_Q4, expert_group=32)
+    m = MoeModel(ctx, shape)
+    m.fill_synthetic(SEED)
+    H, K = shape.hidden, shape.top_k
+    hs = ctx.empty((n_inputs, H))
+    ctx.call("hk_synth_normal", stream_key(SEED, 0xBE0005), 0, n_inputs * H, 1.0, hs.ptr, ctx.stream)
+    out = ctx.empty(H)
+    ids = ctx.empty((n_layers * n_inputs, K), np.int32)
+    state = {"i": 0}
+
+    def step():
+        i = state["i"]
+        state["i"] += 1
+        m.decode_layer_device(i % n_layers, hs.offset((i % n_inputs) * H), out,
+                              ids.offset(((i % n_layers) * n_inputs + (i // n_layers) % n_inputs) * K), None)
+
+    ms = time_launches(ctx, step, max(steps, 64), warmup)
+    routes = ids.download()
+    _, dense_per_layer = m.model_bytes()
+    per = [dense_per_layer + 2 * H * 4 + sum(m.expert_bytes(l, int(e)) for e in routes[l * n_inputs + j])
+           + m.expert_bytes(l, shape.n_experts) for l in range(n_layers) for j in range(n_inputs)]
+    nbytes = float(np.mean(per))
+    return {"us_per_layer": round(ms * 1e3, 2), "bytes_per_layer": round(nbytes), "gbps": round(nbytes / ms / 1e6, 1),
+            "cache": "MALL-cold (16 distinct layers cycled)"}
+
+
 def measured_traffic(workload: str):
     """HBM bytes per launch of the headline kernel from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary (each counter scaled by what it reads for a
@@ -337,7 +378,119 @@ def cpu_baseline(budget_s: float = 12.0, n_distinct: int = 64):
     return {"value": round(done * per_organ / t_total / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"{done} matvecs cycling over {n_distinct} distinct binary 512x2048 organs of the headline "
                       f"workload (9.4 MB, cache-resident on the CPU): the oracle's serial f32 restatement of "
-                      f"binary_group_matvec_f32 (gcc -O2 -ffp-contract=off), 1 thread, {t_total:.1f} s"}
+                      f"binary_group_matvec_f32, 1 thread, {t_total:.1f} s",
+            **host_info()}
+
+
+def host_info() -> dict:
+    """The host CPU (model, threads this process may use) and the oracle's compiler and flags."""
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        cc = subprocess.run(["gcc", "--version"], capture_output=True, text=True).stdout.splitlines()[0]
+    except (OSError, IndexError):
+        cc = "gcc (version unknown)"
+    return {"cpu_model": model, "host_threads": len(os.sched_getaffinity(0)), "compiler": cc,
+            "flags": "-O2 -std=c11 -ffp-contract=off -fno-fast-math"}
+
+
+def cpu_baselines(budget_s: float = 3.0) -> dict:
+    """The oracle on the other configs, each on a bounded sample (about
+    budget_s of timed work after building the sample), one thread unless
+    stated.  Weights are the same draws the device generates."""
+    from oracle import hk_oracle as oracle
+    from tests import hk_testutil as U
+    from hawking_amd.moe import MoeShape
+    out = {}
+
+    def timed(fn, budget=budget_s):
+        n, t = 0, 0.0
+        while t < budget:
+            t0 = time.perf_counter()
+            fn()
+            t += time.perf_counter() - t0
+            n += 1
+        return t / n
+
+    # c1: one Q4 G32 organ 512x2048 (the workload's first organ)
+    sid = organ_stream_id("q4g32_512x2048", 0)
+    w = oracle.normal(oracle.stream_key(SEED, sid), 512 * 2048, 0.02).reshape(512, 2048)
+    s, c = oracle.q4_pack(w, 32)
+    x = oracle.normal(oracle.stream_key(SEED, 0xBE0001), 2048, 1.0)
+    sec = timed(lambda: oracle.q4_matvec(s, c, 512, 2048, 32, x))
+    out["c1_q4g32_512x2048"] = {"us_per_organ": round(sec * 1e6, 1), "gbps": round(600_064 / sec / 1e9, 4),
+                                "cores": 1, "sample": "Qwen80Q4PackedTensor::matvec restated, one organ, repeated"}
+    # c2 on every host thread: whole organs per thread (each keeps the serial row order)
+    nt = len(os.sched_getaffinity(0))
+    orgs = []
+    for i in range(4 * nt):
+        sid = organ_stream_id("binary_512x2048", i)
+        w = oracle.normal(oracle.stream_key(SEED, sid), 512 * 2048, 0.02).reshape(512, 2048)
+        orgs.append(oracle.bin_pack(w) + (oracle.normal(oracle.stream_key(SEED, 0xBE0001), 2048, 1.0, first=i * 2048),))
+    with cf.ThreadPoolExecutor(max_workers=nt) as pool:
+        def wave():
+            list(pool.map(lambda o: oracle.bin_matvec(o[0], o[1], 512, 2048, o[2]), orgs))
+        sec = timed(wave)
+    out["c2_binary_512x2048_all_threads"] = {"gbps": round(len(orgs) * 157_696 / sec / 1e9, 4), "cores": nt,
+                                             "sample": f"{len(orgs)} distinct organs per wave over {nt} threads"}
+    # c3 and c4: moe_suffix of sampled layers (the oracle regenerates the routed and shared experts)
+    cache = {}
+    with cf.ThreadPoolExecutor(max_workers=nt) as pool:
+        for label, kind, group, layers in (("c3_qwen3next_layer_q4", HK_Q4, 32, 1),
+                                           ("c4_48_layer_token_mixed", HK_MIXED, 128, 3)):
+            shape = MoeShape(n_layers=48, hidden=2048, inter=512, shared_inter=512, n_experts=512, top_k=10,
+                             expert_kind=kind, expert_group=group)
+            h = oracle.normal(oracle.stream_key(SEED, 0xBE0004), 2048, 1.0)
+            per_layer = []
+            for layer in range(layers):
+                cache.clear()
+                L, h2, *_ = U.oracle_layer_cached(oracle, SEED, shape, layer, h, cache, pool)
+                per_layer.append(timed(lambda: L.forward(h), budget_s / layers))
+                h = h2
+            mean = float(np.mean(per_layer))
+            if layers == 1:
+                out[label] = {"us_per_layer": round(mean * 1e6, 1), "cores": 1,
+                              "sample": "moe_suffix restated (f32 router, top-10, 10 routed + shared Q4 experts)"}
+            else:
+                out[label] = {"ms_per_token": round(mean * 48 * 1e3, 2), "cores": 1,
+                              "sample": f"48 x the mean moe_suffix time of layers 0..{layers - 1} (mixed experts)"}
+        # c5: routed_moe per token on sampled tokens; a batch of 32 = 32 tokens
+        shape = MoeShape.deepseek_v3()
+        xs = oracle.normal(oracle.stream_key(SEED, 0xC5C5), 2 * 7168, 1.0).reshape(2, 7168)
+        per_tok = []
+        for t in range(2):
+            xb = U.bf16_to_f32(U.to_bf16_bits(xs[t]))
+            M, *_ = _oracle_noaux_pooled(oracle, U, shape, xb, pool)
+            per_tok.append(timed(lambda: M.forward(xb), budget_s / 2))
+        out["c5_dsv3_block_32_tokens"] = {"ms_per_step": round(float(np.mean(per_tok)) * 32 * 1e3, 1), "cores": 1,
+                                          "sample": "32 x the mean routed_moe time of 2 tokens (8 routed + shared "
+                                                    "Q4 experts each, f32 router, noaux_tc)"}
+    return out
+
+
+def _oracle_noaux_pooled(oracle, U, shape, x, pool):
+    """U.oracle_noaux with the experts generated on a thread pool."""
+    _, router, _ = U.dense(oracle, SEED, shape, 0)
+    bias = U.router_bias(oracle, SEED, shape, 0)
+    logits = oracle.gemv_f32(router, x)
+    ids, _ = oracle.router_noaux_tc(logits, bias, shape.n_group, shape.topk_group, shape.top_k,
+                                    shape.norm_topk_prob, shape.routed_scaling_factor)
+    want = [int(e) for e in ids] + [shape.n_experts]
+    made = list(pool.map(lambda ep: U.oracle_organ(oracle, SEED, shape, 0, ep[0], ep[1]),
+                         [(e, p) for e in want for p in range(3)]))
+    experts = [None] * shape.n_experts
+    for i, e in enumerate(want[:-1]):
+        experts[e] = tuple(made[3 * i:3 * i + 3])
+    M = oracle.NoauxMoe(shape.hidden, shape.n_experts, shape.top_k, shape.n_group, shape.topk_group,
+                        shape.norm_topk_prob, shape.routed_scaling_factor, router, bias, experts, tuple(made[-3:]))
+    return M, ids
 
 
 def spot_check(ctx, oset, x, y, n_check=4):
@@ -366,6 +519,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--moe15-only", action="store_true", help="only the mixed-1p5-v1 token (development)")
+    ap.add_argument("--only", default="", help="run one named workload and print its result (profiling)")
     ap.add_argument("--moe-layers", type=int, default=48)
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="run one device-to-device copy of this size first (PMC byte-counter calibration)")
@@ -394,6 +548,54 @@ def main():
         print(json.dumps({"moe15_token_c4_mixed_1p5_v1": r}), flush=True)
         return
 
+    from hawking_amd.moe import MoeShape
+    c3 = MoeShape(n_layers=1, hidden=2048, inter=512, shared_inter=512, n_experts=512, top_k=10,
+                  expert_kind=HK_Q4, expert_group=32)
+    c4 = MoeShape(n_layers=args.moe_layers, hidden=2048, inter=512, shared_inter=512, n_experts=512,
+                  top_k=10, expert_kind=HK_MIXED, expert_group=128)
+    tok_steps = max(args.steps, 20)
+
+    def streamed_extra(name):
+        r, bufs = streamed(ctx, name, args.steps, args.warmup)
+        del bufs
+        return {"gbps": round(r["gbps"], 1), "frac_hbm": round(r["gbps"] / HBM_PEAK_GBPS, 4),
+                "us_per_launch": round(r["ms"] * 1e3, 1), "organs": r["organs"],
+                "packed_bytes_per_organ": round(r["packed_bytes_per_organ"], 1)}
+
+    def rounded(r, nd=2):
+        return {k: (round(v, nd) if isinstance(v, float) else v) for k, v in r.items()}
+
+    workloads = {name: (lambda n=name: streamed_extra(n)) for name in
+                 ("binary_2048x512", "q4g32_512x2048", "mixed_512x2048", "q8g64_512x2048", "binary_rice_512x2048")}
+    workloads.update({
+        "hgravs01_r160_2048x768": lambda: lowrank_streamed(ctx, args.steps, args.warmup),
+        "terminal_head_q8_151936x2048": lambda: terminal_head_bench(ctx, tok_steps, args.warmup),
+        "single_organ_binary_512x2048_us": lambda: round(single_organ_us(ctx), 2),
+    })
+    moe_workloads = {
+        "moe_layer_c3_q4": lambda: dict(rounded(moe_bench(ctx, c3, tok_steps, args.warmup)),
+                                        cache="MALL-warm (one layer, 16 inputs: about 24 MB per token, "
+                                              "all within the 256 MB Infinity Cache)"),
+        "moe_layer_c3_q4_cold": lambda: moe_layer_cold_bench(ctx, tok_steps, args.warmup),
+        "moe_token_c4_mixed": lambda: rounded(moe_bench(ctx, c4, tok_steps, args.warmup)),
+        "moe15_token_c4_mixed_1p5_v1": lambda: moe15_bench(ctx, tok_steps, args.warmup, n_layers=args.moe_layers),
+        "moe_batch_c5_dsv3": lambda: rounded(moe_batch_bench(ctx, max(args.steps, 10), args.warmup), 4),
+    }
+    if args.only:
+        table = dict(workloads, **moe_workloads)
+        if args.only not in table and args.only not in WORKLOADS:
+            print(f"--only: unknown workload {args.only}; one of {sorted(set(table) | set(WORKLOADS))}", file=sys.stderr)
+            sys.exit(2)
+        if args.only in table:
+            r = table[args.only]()
+        else:
+            r, bufs = streamed(ctx, args.only, args.steps, args.warmup)
+            del bufs
+            r = rounded(r, 4)
+        log(args.only, r)
+        print(json.dumps({args.only: r}), flush=True)
+        return
+
     main_name = "binary_512x2048"
     log("headline", main_name)
     head, (oset, x, y) = streamed(ctx, main_name, args.steps, args.warmup)
@@ -404,40 +606,14 @@ def main():
         rel = spot_check(ctx, oset, x, y)
         log("spot-check rel_l2", rel)
         del oset, x, y
-        for name in ("binary_2048x512", "q4g32_512x2048", "mixed_512x2048", "q8g64_512x2048", "binary_rice_512x2048"):
-            r, bufs = streamed(ctx, name, args.steps, args.warmup)
-            del bufs
-            extra[name] = {"gbps": round(r["gbps"], 1), "frac_hbm": round(r["gbps"] / HBM_PEAK_GBPS, 4),
-                           "us_per_launch": round(r["ms"] * 1e3, 1), "organs": r["organs"],
-                           "packed_bytes_per_organ": round(r["packed_bytes_per_organ"], 1)}
+        for name, fn in list(workloads.items()) + ([] if args.no_moe else list(moe_workloads.items())):
+            extra[name] = fn()
             log(name, extra[name])
-        extra["hgravs01_r160_2048x768"] = lowrank_streamed(ctx, args.steps, args.warmup)
-        log("hgravs01", extra["hgravs01_r160_2048x768"])
-        extra["terminal_head_q8_151936x2048"] = terminal_head_bench(ctx, max(args.steps, 20), args.warmup)
-        log("terminal head", extra["terminal_head_q8_151936x2048"])
-        extra["single_organ_binary_512x2048_us"] = round(single_organ_us(ctx), 2)
-        log("single organ us", extra["single_organ_binary_512x2048_us"])
-        if not args.no_moe:
-            from hawking_amd.moe import MoeShape
-            c3 = MoeShape(n_layers=1, hidden=2048, inter=512, shared_inter=512, n_experts=512, top_k=10,
-                          expert_kind=HK_Q4, expert_group=32)
-            r = moe_bench(ctx, c3, max(args.steps, 20), args.warmup)
-            extra["moe_layer_c3_q4"] = {k: (round(v, 2) if isinstance(v, float) else v) for k, v in r.items()}
-            log("c3", extra["moe_layer_c3_q4"])
-            c4 = MoeShape(n_layers=args.moe_layers, hidden=2048, inter=512, shared_inter=512, n_experts=512,
-                          top_k=10, expert_kind=HK_MIXED, expert_group=128)
-            r = moe_bench(ctx, c4, max(args.steps, 20), args.warmup)
-            extra["moe_token_c4_mixed"] = {k: (round(v, 2) if isinstance(v, float) else v) for k, v in r.items()}
-            log("c4", extra["moe_token_c4_mixed"])
-            extra["moe15_token_c4_mixed_1p5_v1"] = moe15_bench(ctx, max(args.steps, 20), args.warmup,
-                                                               n_layers=args.moe_layers)
-            log("mixed-1p5 token", extra["moe15_token_c4_mixed_1p5_v1"])
-            r = moe_batch_bench(ctx, max(args.steps, 10), args.warmup)
-            extra["moe_batch_c5_dsv3"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
-            log("c5", extra["moe_batch_c5_dsv3"])
     cpu = None if (args.no_cpu or args.only_main) else cpu_baseline()
     if cpu:
         log("cpu", cpu)
+        extra["cpu_baselines"] = cpu_baselines()
+        log("cpu baselines", extra["cpu_baselines"])
 
     line = {
         "metric": "packed-matvec GB/s (% HBM peak); MoE decode µs/token at batch 1",

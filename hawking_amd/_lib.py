@@ -131,6 +131,8 @@ PROTOTYPES = {
     "hk_catalog_load": (C.c_int, [_p, _p, C.c_char_p, C.c_int, _p, C.POINTER(_p), C.POINTER(_p)]),
     "hk_pack_binary_rice": (C.c_int, [_p, _p, _u32, _u32, C.c_double, _p, _p, _p, _p, _sz, C.POINTER(RiceQ1Src), _p]),
     "hk_moe_block": (C.c_int, [_p, _p, _u32, _p, _p, _u32, C.c_int, _p, _p, _p]),
+    "hk_pack_mixed": (C.c_int, [_p, _p, _u32, _u32, _p, _p, _p, _p, _u32, _p, _p, _u32, C.POINTER(_u32), _p]),
+    "hk_organ_from_q4_0": (C.c_int, [_p, _p, _sz, _u32, _u32, _p, C.POINTER(_p)]),
     "hk_gemv_batch": (C.c_int, [_p, C.POINTER(_p), _u32, _p, _sz, _p, _sz, _p]),
     "hk_decode_rows": (C.c_int, [_p, _p, _u32, _u32, _p, _p]),
     "hk_organ_set_create": (C.c_int, [_p, C.POINTER(_p), _u32, C.POINTER(_p)]),

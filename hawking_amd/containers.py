@@ -6,6 +6,7 @@ loader (hk_container.cpp), mirroring the reference's loaders:
   * organ_from_hq30(payload) -- HQ30UQ4 / HQ30G1B1 32-byte-header payloads
     (qwen_complete_binary/uniform_q4.rs:57-150, qwen_complete_binary/mod.rs:137-233)
   * MixedCatalog -- Qwen80MixedStreamingCatalog (model/qwen80_mixed_catalog.rs:176-555)
+  * organ_from_q4_0(blocks, rows, cols) -- GGUF Q4_0 AoS blocks (dequant_q4_0, quant.rs:473-498)
 """
 from __future__ import annotations
 
@@ -49,6 +50,16 @@ def organ_from_hq30(ctx: Context, payload: bytes) -> PackedOrgan:
     buf = np.frombuffer(payload, np.uint8)
     out = C.c_void_p()
     ctx.call("hk_organ_from_hq30", buf.ctypes.data, buf.size, ctx.stream, C.byref(out))
+    return _wrap(ctx, out)
+
+
+def organ_from_q4_0(ctx: Context, blocks, rows: int, cols: int) -> PackedOrgan:
+    """GGUF Q4_0 blocks (18 bytes per 32 elements: f16 d, then 16 bytes of
+    nibbles, element j low / j + 16 high) bound as a Q4 group-32 organ."""
+    buf = np.ascontiguousarray(np.frombuffer(bytes(blocks), np.uint8) if not isinstance(blocks, np.ndarray)
+                               else blocks.reshape(-1).view(np.uint8))
+    out = C.c_void_p()
+    ctx.call("hk_organ_from_q4_0", buf.ctypes.data, buf.size, rows, cols, ctx.stream, C.byref(out))
     return _wrap(ctx, out)
 
 

@@ -1069,6 +1069,62 @@ extern "C" int hk_pack_q2(hk_ctx* ctx, const float* w, size_t count, uint16_t* s
     return finish_pack(ctx, st, bad, launch_pack_q2(w, count / 64, scales, codes, bad, st));
 }
 
+extern "C" int hk_pack_mixed(hk_ctx* ctx, const float* w, uint32_t rows, uint32_t cols, const uint8_t* is_binary,
+                             uint8_t* tags, uint16_t* bin_scales, uint8_t* bin_signs, uint32_t bin_cap,
+                             uint16_t* q2_scales, uint8_t* q2_codes, uint32_t q2_cap, uint32_t* n_bin_out,
+                             hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    int rc = validate_shape(ctx, HK_MIXED, 128, rows, cols);
+    if (rc) return rc;
+    if (!w || !is_binary || !tags || !n_bin_out || !aligned16(w))
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_pack_mixed: NULL or misaligned pointer");
+    if ((bin_cap && (!bin_scales || !bin_signs || !aligned16(bin_signs))) ||
+        (q2_cap && (!q2_scales || !q2_codes || !aligned16(q2_codes))) ||
+        (reinterpret_cast<uintptr_t>(bin_scales) & 1u) || (reinterpret_cast<uintptr_t>(q2_scales) & 1u))
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_pack_mixed: NULL or misaligned output section");
+    const size_t groups = (size_t)rows * cols / 128;
+    if (groups > 0xFFFFFFFFull) return set_error(ctx, HK_E_GEOMETRY, "hk_pack_mixed: more than 2^32 groups");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    // pass 1: tags and the binary count (into the packer flag's neighbour word)
+    uint32_t* bad;
+    if ((rc = pack_prologue(ctx, st, &bad))) return rc;
+    uint32_t* count = ctx->pack_flag + 1;
+    uint32_t nb = 0;
+    rc = check_hip(ctx, hipMemsetAsync(count, 0, 4, st), "hipMemsetAsync (mixed count)");
+    if (!rc) rc = check_hip(ctx, launch_mixed_tags_from_sel(is_binary, groups, tags, count, st), "mixed tags");
+    if (!rc) rc = check_hip(ctx, hipMemcpyAsync(&nb, count, 4, hipMemcpyDeviceToHost, st), "mixed count read");
+    if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "hipStreamSynchronize (mixed count)");
+    if (rc) return rc;
+    *n_bin_out = nb;
+    const uint32_t nq = (uint32_t)(groups - nb);
+    if (nb > bin_cap || nq > q2_cap)
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_pack_mixed: the selector has " + std::to_string(nb) +
+                                                    " binary and " + std::to_string(nq) +
+                                                    " Q2 groups, above bin_cap / q2_cap");
+    // passes 2-3: per-row prefix tables (temporary), then one thread per group
+    void* tmp = nullptr;
+    if (hipMalloc(&tmp, align256(sizeof(SynthJob)) + 2 * align256(((size_t)rows + 1) * 4)) != hipSuccess)
+        return set_error(ctx, HK_E_NOMEM, "hk_pack_mixed: row table allocation failed");
+    uint8_t* tp = static_cast<uint8_t*>(tmp);
+    SynthJob j{};
+    j.group = 128;
+    j.rows = rows;
+    j.cols = cols;
+    j.scales = bin_scales;
+    j.codes = bin_signs;
+    j.tags = tags;
+    j.q2_scales = q2_scales;
+    j.q2_codes = q2_codes;
+    j.row_bin = reinterpret_cast<uint32_t*>(tp + align256(sizeof(SynthJob)));
+    j.row_q2 = reinterpret_cast<uint32_t*>(tp + align256(sizeof(SynthJob)) + align256(((size_t)rows + 1) * 4));
+    j.w = w;
+    rc = check_hip(ctx, hipMemcpyAsync(tmp, &j, sizeof(j), hipMemcpyHostToDevice, st), "mixed job upload");
+    if (!rc) rc = finish_pack(ctx, st, bad, launch_mixed_pack_buffer(static_cast<SynthJob*>(tmp), groups, bad, st));
+    (void)hipStreamSynchronize(st);
+    (void)hipFree(tmp);
+    return rc;
+}
+
 extern "C" uint64_t hk_stream_key(uint64_t seed, uint64_t stream_id) { return hk::stream_key(seed, stream_id); }
 
 extern "C" int hk_synth_normal(hk_ctx* ctx, uint64_t key, uint64_t first, size_t count, float sigma, float* out,

@@ -531,7 +531,47 @@ extern "C" int hk_organ_from_hq30(hk_ctx* ctx, const uint8_t* payload, size_t le
     return bind(ctx, b, stream, out, nullptr);
 }
 
-// ====================================================================== catalog
+// GGUF Q4_0 blocks (dequant_q4_0, quant.rs:473-498): per 32 elements
+// {f16 d; u8 qs[16]}, element j < 16 in the low nibble of qs[j], element
+// j >= 16 in the high nibble of qs[j - 16].  The canonical Q4 group-32 body
+// keeps d as the group's scale and the nibbles unchanged, paired (2i, 2i+1)
+// per byte, so the bound organ decodes to the same (nibble - 8) * d.
+extern "C" int hk_organ_from_q4_0(hk_ctx* ctx, const uint8_t* blocks, size_t len, uint32_t rows, uint32_t cols,
+                                  hk_stream stream, hk_organ** out) {
+    if (!ctx || !out) return HK_E_INVALID_ARG;
+    *out = nullptr;
+    if (!blocks) return set_error(ctx, HK_E_INVALID_ARG, "hk_organ_from_q4_0: NULL blocks");
+    if (rows == 0 || cols == 0 || cols % 32)
+        return set_error(ctx, HK_E_GEOMETRY, "q4_0 tensors need rows > 0 and cols % 32 == 0");
+    const size_t nb = (size_t)rows * cols / 32;
+    if (len != nb * 18)
+        return set_error(ctx, HK_E_GEOMETRY, "q4_0 data is " + std::to_string(len) + " bytes, expected " +
+                                                 std::to_string(nb * 18));
+    std::vector<uint16_t> scales(nb);
+    std::vector<uint8_t> codes(nb * 16);
+    for (size_t b = 0; b < nb; ++b) {
+        const uint8_t* blk = blocks + b * 18;
+        scales[b] = rd16(blk);
+        uint8_t* c = codes.data() + b * 16;
+        for (int i = 0; i < 16; ++i) {
+            // canonical byte i holds elements 2i (low) and 2i + 1 (high)
+            const int e0 = 2 * i, e1 = 2 * i + 1;
+            const uint8_t n0 = e0 < 16 ? (blk[2 + e0] & 0x0F) : (blk[2 + e0 - 16] >> 4);
+            const uint8_t n1 = e1 < 16 ? (blk[2 + e1] & 0x0F) : (blk[2 + e1 - 16] >> 4);
+            c[i] = (uint8_t)(n0 | (n1 << 4));
+        }
+    }
+    hk_organ_src src{};
+    src.kind = HK_Q4;
+    src.group = 32;
+    src.rows = rows;
+    src.cols = cols;
+    src.scales = scales.data();
+    src.codes = codes.data();
+    return hk_organ_upload(ctx, &src, stream, out);
+}
+
+// ====================================================================== catalog// ====================================================================== catalog
 
 struct hk_catalog {
     std::string root;

@@ -376,9 +376,11 @@ __global__ void __launch_bounds__(1024) mixed_row_scan_kernel(const SynthJob* __
     }
 }
 
-// Mixed, pass 3: thread per (row, group) generates and packs its group.
+// Mixed, pass 3: thread per (row, group) generates (or reads, for a job
+// with dense weights: hk_pack_mixed) and packs its group.
 __global__ void synth_mixed_pack_kernel(const SynthJob* __restrict__ jobs, uint32_t* bad) {
     const SynthJob j = jobs[blockIdx.y];
+    const bool buf = j.w != nullptr;
     const uint32_t gpr = j.cols / 128;
     const size_t groups = (size_t)j.rows * gpr;
     for (size_t fg = (size_t)blockIdx.x * blockDim.x + threadIdx.x; fg < groups;
@@ -389,17 +391,57 @@ __global__ void synth_mixed_pack_kernel(const SynthJob* __restrict__ jobs, uint3
         uint32_t b = 0;
         if ((j.tags[fg >> 3] >> (fg & 7u)) & 1u) {
             const uint32_t idx = j.row_bin[r] + nb;
-            bin_pack_group(SynthSrc{j.key, fg * 128, j.sigma}, j.scales + idx,
-                           j.codes + (size_t)idx * 16, &b);
+            if (buf)
+                bin_pack_group(BufSrc{j.w + fg * 128}, j.scales + idx, j.codes + (size_t)idx * 16, &b);
+            else
+                bin_pack_group(SynthSrc{j.key, fg * 128, j.sigma}, j.scales + idx, j.codes + (size_t)idx * 16, &b);
         } else {
             const uint32_t idx = j.row_q2[r] + (g - nb);
-            q2_pack_group(SynthSrc{j.key, fg * 128, j.sigma}, j.q2_scales + 2 * idx,
-                          j.q2_codes + (size_t)idx * 32, &b);
-            q2_pack_group(SynthSrc{j.key, fg * 128 + 64, j.sigma}, j.q2_scales + 2 * idx + 1,
-                          j.q2_codes + (size_t)idx * 32 + 16, &b);
+            for (int half = 0; half < 2; ++half) {
+                uint16_t* so = j.q2_scales + 2 * idx + half;
+                uint8_t* co = j.q2_codes + (size_t)idx * 32 + 16 * half;
+                if (buf)
+                    q2_pack_group(BufSrc{j.w + fg * 128 + 64 * half}, so, co, &b);
+                else
+                    q2_pack_group(SynthSrc{j.key, fg * 128 + 64 * (uint64_t)half, j.sigma}, so, co, &b);
+            }
         }
         if (b) atomicOr(bad, 1u);
     }
+}
+
+// hk_pack_mixed, pass 1: tag bytes from a per-group selector (8 groups per
+// thread) and the binary-group count.
+__global__ void mixed_tags_from_sel_kernel(const uint8_t* __restrict__ sel, size_t groups, uint8_t* __restrict__ tags,
+                                           uint32_t* count) {
+    uint32_t local = 0;
+    for (size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x; b < (groups + 7) / 8;
+         b += (size_t)gridDim.x * blockDim.x) {
+        uint32_t t = 0;
+        for (uint32_t k = 0; k < 8; ++k) {
+            const size_t g = b * 8 + k;
+            if (g < groups && sel[g]) t |= 1u << k;
+        }
+        tags[b] = (uint8_t)t;
+        local += (uint32_t)__builtin_popcount(t);
+    }
+    for (int off = 32; off >= 1; off >>= 1) local += __shfl_xor(local, off, 64);
+    if ((threadIdx.x & 63) == 0 && local) atomicAdd(count, local);
+}
+
+hipError_t launch_mixed_tags_from_sel(const uint8_t* sel, size_t groups, uint8_t* tags, uint32_t* count,
+                                      hipStream_t s) {
+    hipLaunchKernelGGL(mixed_tags_from_sel_kernel, dim3(grid_for((groups + 7) / 8, 256)), dim3(256), 0, s, sel,
+                       groups, tags, count);
+    return hipGetLastError();
+}
+
+// hk_pack_mixed, passes 2-3 on one job (tags, row tables, w).
+hipError_t launch_mixed_pack_buffer(const SynthJob* job_dev, size_t groups, uint32_t* bad, hipStream_t s) {
+    hipLaunchKernelGGL(mixed_row_scan_kernel, dim3(1), dim3(1024), 0, s, job_dev);
+    hipLaunchKernelGGL(synth_mixed_pack_kernel, dim3(grid_for(groups, 256) < 4096 ? grid_for(groups, 256) : 4096, 1),
+                       dim3(256), 0, s, job_dev, bad);
+    return hipGetLastError();
 }
 
 // Mixed: count binary groups per organ (for exact allocation).

@@ -61,10 +61,16 @@ struct SynthJob {
     uint32_t* row_bin;   // mixed [rows+1]
     uint32_t* row_q2;    // mixed [rows+1]
     float* dense;        // f32
+    const float* w;      // mixed: weights to pack instead of generated ones (hk_pack_mixed), or null
 };
 
 hipError_t launch_synth_jobs(int kind, const SynthJob* jobs_dev, uint32_t njobs, size_t max_groups,
                              uint32_t* bad, hipStream_t s);
+// hk_pack_mixed: tag bytes and the binary count from a per-group selector,
+// then the row tables and the packer over the job's dense weights.
+hipError_t launch_mixed_tags_from_sel(const uint8_t* sel, size_t groups, uint8_t* tags, uint32_t* count,
+                                      hipStream_t s);
+hipError_t launch_mixed_pack_buffer(const SynthJob* job_dev, size_t groups, uint32_t* bad, hipStream_t s);
 hipError_t launch_synth_mixed_count(const SynthJob* jobs_dev, uint32_t njobs, size_t max_groups,
                                     uint32_t* counts, hipStream_t s);
 hipError_t launch_pack_q4(const float* w, size_t groups, int G, uint16_t* scales, uint8_t* codes,

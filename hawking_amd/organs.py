@@ -398,6 +398,25 @@ def pack_q2_device(ctx: Context, w: DeviceArray, count: int):
     return scales, codes
 
 
+def pack_mixed_device(ctx: Context, w: DeviceArray, rows: int, cols: int, is_binary: DeviceArray):
+    """The per-group mixed packer on device buffers (hk_pack_mixed): returns
+    the canonical stream (tags, bin_scales, bin_signs, q2_scales, q2_codes)
+    as device arrays sized for the selector."""
+    groups = rows * cols // 128
+    sel = is_binary.download() if isinstance(is_binary, DeviceArray) else np.asarray(is_binary)
+    nb = int(np.count_nonzero(sel))
+    nq = groups - nb
+    tags = ctx.empty((groups + 7) // 8, np.uint8)
+    bs, bg = ctx.empty(max(nb, 1), np.uint16), ctx.empty(max(nb, 1) * 16, np.uint8)
+    qs, qc = ctx.empty(max(nq, 1) * 2, np.uint16), ctx.empty(max(nq, 1) * 32, np.uint8)
+    n_bin = C.c_uint32()
+    sd = is_binary if isinstance(is_binary, DeviceArray) else ctx.to_device(np.ascontiguousarray(sel, np.uint8))
+    ctx.call("hk_pack_mixed", w.ptr, rows, cols, sd.ptr, tags.ptr, bs.ptr, bg.ptr, nb, qs.ptr, qc.ptr, nq,
+             C.byref(n_bin), ctx.stream)
+    assert n_bin.value == nb
+    return tags, bs, bg, qs, qc
+
+
 def stream_key(seed: int, stream_id: int) -> int:
     return int(_lib.lib().hk_stream_key(seed, stream_id))
 

@@ -258,6 +258,22 @@ int hk_pack_binary_rice(hk_ctx* ctx, const float* w, uint32_t rows, uint32_t col
  * (lab/operators/ascension_dual_gravity_worker.py:898-911), group 64. */
 int hk_pack_q2(hk_ctx* ctx, const float* w, size_t count, uint16_t* scales, uint8_t* codes,
                hk_stream stream);
+/* The per-group mixed packer (HK_MIXED, build-defined stream; no reference
+ * counterpart packs per group -- the reference mixes codecs per tensor,
+ * q80_mixed_decode.rs:1073-1417): w (device, rows x cols f32, cols % 128 ==
+ * 0) in flat groups of 128; group g is packed by pack_binary_group
+ * (q80_mixed_decode.rs:185-230) when is_binary[g] != 0 (device u8 per
+ * group), else by the Q2 base stage on each half of 64
+ * (ascension_dual_gravity_worker.py:898-911), into the canonical stream of
+ * hk_organ_src: tags [(groups + 7) / 8] (1 = binary, LSB-first), bin_scales
+ * [n_bin] and bin_signs [16 n_bin] (16-byte aligned), q2_scales [2 n_q2] and
+ * q2_codes [32 n_q2] (16-byte aligned), sections in group order.  *n_bin_out
+ * receives n_bin; a selector with more binary (Q2) groups than bin_cap
+ * (q2_cap) fails with HK_E_INVALID_ARG before anything past the tags is
+ * written.  Bit-exact with the oracle's mixed pack; synchronous. */
+int hk_pack_mixed(hk_ctx* ctx, const float* w, uint32_t rows, uint32_t cols, const uint8_t* is_binary,
+                  uint8_t* tags, uint16_t* bin_scales, uint8_t* bin_signs, uint32_t bin_cap, uint16_t* q2_scales,
+                  uint8_t* q2_codes, uint32_t q2_cap, uint32_t* n_bin_out, hk_stream stream);
 /* Synthetic N(0, sigma): counter-based SplitMix64 words -> Irwin-Hall(12),
  * integer-exact so host and device draws agree bit for bit.  No reference
  * counterpart (the reference's synthetic inputs are deterministic_matrix /
@@ -298,6 +314,17 @@ int hk_organ_from_container(hk_ctx* ctx, int32_t codec, const uint8_t* payload, 
  * parse_complete_binary_header, qwen_complete_binary/mod.rs:137-233) bound as
  * an HK_Q4 / HK_BIN organ; shape [rows, cols] or [len] (= len x 1). */
 int hk_organ_from_hq30(hk_ctx* ctx, const uint8_t* payload, size_t len, hk_stream stream, hk_organ** out);
+
+/* GGUF Q4_0 (dequant_q4_0, quant.rs:473-498): rows*cols/32 AoS blocks of 18
+ * bytes {f16 d (LE); u8 qs[16]} (HOST memory, row-major, blocks along each
+ * row; cols % 32 == 0), element j of a block in the low nibble of qs[j] for
+ * j < 16 and in the high nibble of qs[j - 16] for j >= 16, value
+ * (nibble - 8) * d.  Bound as an HK_Q4 group-32 organ (the same d and
+ * nibbles, reordered into the canonical even/odd pairs), so it decodes bit
+ * for bit to dequant_q4_0.  Errors: HK_E_GEOMETRY (shape, cols % 32, len !=
+ * rows*cols/32*18), HK_E_NONFINITE (a d that is not a finite f16). */
+int hk_organ_from_q4_0(hk_ctx* ctx, const uint8_t* blocks, size_t len, uint32_t rows, uint32_t cols,
+                       hk_stream stream, hk_organ** out);
 
 /* The HQ80M15 mixed catalog (Qwen80MixedStreamingCatalog,
  * qwen80_mixed_catalog.rs:176-555): the manifest JSON (schema, seal, bpw

@@ -812,7 +812,9 @@ int hko_mixed_decode(const hko_mixed* m, float* out) {
     return HKO_OK;
 }
 
-/* Same serial order as binary_group_matvec_f32: per row, column order, sum += w*x. */
+/* Same serial order as binary_group_matvec_f32: per row, column order, sum += w*x.
+ * Each weight is mixed_weight's value; the group's f16 scales are converted
+ * once per group (the conversion is exact, so the values are the same). */
 int hko_mixed_matvec(const hko_mixed* m, const float* x, float* y) {
     if (!all_finite(x, m->cols)) return HKO_E_NONFINITE;
     size_t gpr = m->cols / 128, ib = 0, iq = 0;
@@ -821,8 +823,24 @@ int hko_mixed_matvec(const hko_mixed* m, const float* x, float* y) {
         for (size_t gg = 0; gg < gpr; ++gg) {
             size_t g = r * gpr + gg;
             int binary = (m->tags[g >> 3] >> (g & 7u)) & 1u;
-            for (size_t i = 0; i < 128; ++i) sum += mixed_weight(m, binary, ib, iq, i) * x[gg * 128 + i];
-            if (binary) ib++; else iq++;
+            const float* xg = x + gg * 128;
+            if (binary) {
+                const float s = hko_f16_to_f32(m->bin_scales[ib]);
+                for (size_t i = 0; i < 128; ++i) {
+                    size_t bit = ib * 128 + i;
+                    float w = ((m->bin_signs[bit >> 3] >> (bit & 7u)) & 1u) ? s : -s;
+                    sum += w * xg[i];
+                }
+                ib++;
+            } else {
+                const float s0 = hko_f16_to_f32(m->q2_scales[2 * iq]), s1 = hko_f16_to_f32(m->q2_scales[2 * iq + 1]);
+                for (size_t i = 0; i < 128; ++i) {
+                    size_t e = iq * 128 + i;
+                    uint32_t code = (m->q2_codes[e >> 2] >> (2u * (e & 3u))) & 3u;
+                    sum += q2_level(code, i < 64 ? s0 : s1) * xg[i];
+                }
+                iq++;
+            }
         }
         if (!isfinite(sum)) return HKO_E_NONFINITE;
         y[r] = sum;

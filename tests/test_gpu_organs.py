@@ -456,3 +456,90 @@ def test_upload_validation_errors(ctx, oracle):
     with pytest.raises(HawkingError) as e:
         BinaryGroupPacked(ctx, np.zeros(3, np.uint16), np.zeros(4 * 96 // 8, np.uint8), 4, 96)
     assert e.value.code == HK_E_GEOMETRY
+
+
+def test_device_mixed_packer_bit_exact(ctx, oracle):
+    """hk_pack_mixed (per-group selector over f32 weights) is bit-exact with
+    the oracle's mixed pack, edge groups included, and its output uploads as
+    an organ that decodes bit-exactly."""
+    from hawking_amd import organs
+    rng = np.random.default_rng(12)
+    rows, cols = 64, 1024
+    w = _edge_weights(rng, rows, cols)
+    w[5, :64] = np.linspace(-1.5, 1.5, 64, dtype=np.float32)     # Q2 ties
+    v0 = np.float32(2.0**-14 * (1 + 2.0**-11))                    # binary double rounding
+    w[6, :128] = v0
+    groups = rows * cols // 128
+    for label, sel in (("coins", oracle.mixed_coins(oracle.stream_key(U.SEED, 0x31A), groups)),
+                       ("all binary", np.ones(groups, np.uint8)), ("all q2", np.zeros(groups, np.uint8))):
+        say("pack_mixed", label)
+        tags, bs, bg, qs, qc = organs.pack_mixed_device(ctx, ctx.to_device(w), rows, cols, sel)
+        m = oracle.mixed_pack(w, sel)
+        nb, nq = m.n_bin, m.n_q2
+        assert np.array_equal(tags.download(), m.tags)
+        assert np.array_equal(bs.download()[:nb], m.bin_scales) and np.array_equal(bg.download()[:16 * nb], m.bin_signs)
+        assert np.array_equal(qs.download()[:2 * nq], m.q2_scales) and np.array_equal(qc.download()[:32 * nq], m.q2_codes)
+        o = organs.MixedPackedTensor(ctx, rows, cols, tags.download(), bs.download()[:nb], bg.download()[:16 * nb],
+                                     qs.download()[:2 * nq], qc.download()[:32 * nq])
+        assert np.array_equal(o.decode().view(np.uint32), oracle.mixed_decode(m).view(np.uint32))
+
+
+def test_device_mixed_packer_capacity_and_rejects(ctx):
+    from hawking_amd._lib import HK_E_INVALID_ARG, HK_E_NONFINITE, HawkingError
+    rows, cols = 8, 256
+    w = np.zeros((rows, cols), np.float32)
+    sel = np.ones(rows * cols // 128, np.uint8)
+    d = ctx.to_device(w)
+    tags = ctx.empty(2, np.uint8)
+    small = ctx.empty(64, np.uint8)
+    n = C_uint32()
+    with pytest.raises(HawkingError) as e:   # 16 binary groups, room for 4
+        ctx.call("hk_pack_mixed", d.ptr, rows, cols, ctx.to_device(sel).ptr, tags.ptr, small.ptr, small.ptr, 4,
+                 small.ptr, small.ptr, 0, n, ctx.stream)
+    assert e.value.code == HK_E_INVALID_ARG
+    w[3, 7] = np.inf
+    from hawking_amd import organs
+    with pytest.raises(HawkingError) as e:
+        organs.pack_mixed_device(ctx, ctx.to_device(w), rows, cols, sel)
+    assert e.value.code == HK_E_NONFINITE
+
+
+def C_uint32():
+    import ctypes
+    return ctypes.byref(ctypes.c_uint32())
+
+
+def test_gguf_q4_0_blocks_decode_bit_exact(ctx, oracle):
+    """hk_organ_from_q4_0: GGUF Q4_0 AoS blocks (dequant_q4_0, quant.rs:473-498)
+    bound as a Q4 group-32 organ decode bit for bit to the oracle's
+    dequant_q4_0, and its matvec is within tolerance of the FP64 product."""
+    from hawking_amd.containers import organ_from_q4_0
+    rng = np.random.default_rng(40)
+    rows, cols = 96, 2048
+    nb = rows * cols // 32
+    blocks = np.zeros((nb, 18), np.uint8)
+    d = (rng.standard_normal(nb) * 0.003).astype(np.float16)
+    d[0], d[1], d[2] = 0.0, np.float16(6.1e-5), np.float16(-0.25)   # zero, subnormal, negative scale
+    blocks[:, :2] = d.view(np.uint8).reshape(nb, 2)
+    blocks[:, 2:] = rng.integers(0, 256, (nb, 16), dtype=np.uint8)
+    blocks[3, 2:] = 0x0F      # low nibbles 15, high nibbles 0
+    say("gguf q4_0", rows, cols)
+    o = organ_from_q4_0(ctx, blocks, rows, cols)
+    want = oracle.q4_0_dequant(blocks, rows * cols).reshape(rows, cols)
+    assert np.array_equal(o.decode().view(np.uint32), want.view(np.uint32))
+    x = rng.standard_normal(cols).astype(np.float32)
+    y = o.matvec(x)
+    assert oracle.relative_l2(y, want.astype(np.float64) @ x.astype(np.float64)) < TOL
+
+
+def test_gguf_q4_0_rejects_bad_blocks(ctx):
+    from hawking_amd._lib import HK_E_GEOMETRY, HK_E_NONFINITE, HawkingError
+    from hawking_amd.containers import organ_from_q4_0
+    blocks = np.zeros((8, 18), np.uint8)
+    with pytest.raises(HawkingError) as e:
+        organ_from_q4_0(ctx, blocks[:7], 4, 64)
+    assert e.value.code == HK_E_GEOMETRY
+    blocks[5, :2] = np.array([np.float16(np.inf)]).view(np.uint8)
+    with pytest.raises(HawkingError) as e:
+        organ_from_q4_0(ctx, blocks, 4, 64)
+    assert e.value.code == HK_E_NONFINITE
