@@ -80,10 +80,13 @@ def build_stream(ctx, name: str, n_organs: int | None = None):
     return oset, x, y, alg_bytes
 
 
-def time_launches(ctx, fn, steps: int, warmup: int, ramp_s: float = 0.2) -> float:
+RAMP_S = 0.2  # seconds of untimed launches before each timed loop (--ramp)
+
+
+def time_launches(ctx, fn, steps: int, warmup: int, ramp_s: float | None = None) -> float:
     """Average ms per call of fn() over `steps` calls, HIP events on ctx.stream,
     after ramp_s seconds of untimed calls and `warmup` more."""
-    t_end = time.perf_counter() + ramp_s
+    t_end = time.perf_counter() + (RAMP_S if ramp_s is None else ramp_s)
     while time.perf_counter() < t_end:
         for _ in range(8):
             fn()
@@ -521,9 +524,13 @@ def main():
     ap.add_argument("--moe15-only", action="store_true", help="only the mixed-1p5-v1 token (development)")
     ap.add_argument("--only", default="", help="run one named workload and print its result (profiling)")
     ap.add_argument("--moe-layers", type=int, default=48)
+    ap.add_argument("--ramp", type=float, default=0.2,
+                    help="seconds of untimed launches before each timed loop (0 under counter collection)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="run one device-to-device copy of this size first (PMC byte-counter calibration)")
     args = ap.parse_args()
+    global RAMP_S
+    RAMP_S = args.ramp
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
               "(this build has no multi-GPU path: organ GEMVs would shard by rows, MoE layers by experts)", file=sys.stderr)
