@@ -98,8 +98,11 @@ static int validate_shape(hk_ctx* ctx, int kind, int group, uint32_t rows, uint3
 // The GEMV keeps one organ's x image (and a quantization window) in LDS.
 static int validate_gemv_cols(hk_ctx* ctx, int kind, uint32_t cols) {
     if (kind == HK_F32 || gemv_lds_bytes(kind, cols) <= GEMV_LDS_LIMIT) return HK_OK;
+    uint32_t most = 0;  // the widest organ of this kind whose x image fits
+    for (uint32_t c = 32; c <= 65536 && gemv_lds_bytes(kind, c) <= GEMV_LDS_LIMIT; c += 32) most = c;
     return set_error(ctx, HK_E_GEOMETRY, "organ cols=" + std::to_string(cols) +
-                                             " exceeds the GEMV's LDS x image (at most 12160 columns; 6144 for 3-bit factors)");
+                                             " exceeds the GEMV's LDS x image (at most " + std::to_string(most) +
+                                             " columns for this kind)");
 }
 
 static Layout layout_for(int kind, int group, uint32_t rows, uint32_t cols, uint32_t n_bin,

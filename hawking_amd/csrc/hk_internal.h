@@ -200,10 +200,10 @@ int check_hip(hk_ctx* ctx, hipError_t e, const char* what);
 // Kernel launchers (defined in the .hip files); all stream-ordered, no sync.
 // GEMV over n organs of one kind/shape (descriptor table in device memory).
 // Dynamic LDS of the GEMV kernel for a packed organ of `cols` columns (x
-// image, quantization window, mixed headers, row outputs), and its cap, which
-// keeps a workgroup within 64 KB.
+// image, quantization window, mixed headers, row outputs), and its cap of
+// 64 KB (two workgroups per CU of 160 KB at the widest organs).
 size_t gemv_lds_bytes(int kind, uint32_t cols);
-constexpr size_t GEMV_LDS_LIMIT = 62 * 1024;
+constexpr size_t GEMV_LDS_LIMIT = 64 * 1024;
 hipError_t launch_gemv_tiled(const OrganView* organs_dev, uint32_t n, const OrganView& shape,
                              const float* x, size_t x_stride, float* y, size_t y_stride,
                              hipStream_t s);

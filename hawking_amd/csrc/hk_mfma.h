@@ -5,12 +5,18 @@
 // at HBM speed for binary weights (8 weights per byte).  So the decode is
 // moved into v_mfma_i32_16x16x64_i8:
 //
-//   * x is converted once per workgroup to a fixed-point integer
-//     X = rint(x * 2^E) (|X| <= 2^23), and X * 2^k is split into four signed
-//     base-256 "limbs".  The MFMA A operand (16 x 64) holds, in row
-//     m = 4*slot + limb, the limbs of the columns that lane-group `slot` of the
-//     B operand covers (zero elsewhere), so one MFMA yields exact int32 partial
-//     sums for 4 column groups x 4 limbs of 16 weight rows.
+//   * x is converted once per workgroup to fixed-point integers, one exponent
+//     per zero-point unit (the SXG columns a lane's product covers):
+//     X = rint(x * 2^E_u) with E_u = 23 - exponent(max |x| over the unit)
+//     (|X| <= 2^23), and X * 2^k is split into four signed base-256 "limbs".
+//     A unit's sums are scaled back by f_u = 2^(E - E_u) (E the exponent of
+//     the whole vector's max, f_u <= 1, exact), so every element keeps 24
+//     bits relative to its own unit's max, as an f32 product would, even
+//     when one element of x is orders of magnitude above the rest.  The MFMA
+//     A operand (16 x 64) holds, in row m = 4*slot + limb, the limbs of the
+//     columns that lane-group `slot` of the B operand covers (zero elsewhere),
+//     so one MFMA yields exact int32 partial sums for 4 column groups x 4
+//     limbs of 16 weight rows.
 //   * The B operand (64 x 16) comes straight from the packed bytes with one AND
 //     per 4 weights: a binary bit plane s is bytes & (0x01 << s) = bit * 2^s, a
 //     Q4 nibble plane is bytes & 0x0F, a Q2 field is bytes & (0x03 << 2u); the
@@ -23,18 +29,19 @@
 //     A mixed Q2 item's top field is read in place (bytes & 0xC0, with bit 7
 //     stored inverted: 64 (code - 2) as a signed byte), so no field needs a shift.
 //   * Per (row, group) the four int32 limbs are combined (pairs exactly in
-//     int32, then one f32 fma), the zero
-//     point is removed with the group's sum of X (binary: sum (2b-1) X =
-//     2 sum bX - sum X; Q4: sum (n-8) X; Q2: sum (c-1.5) X) and the f16 group
-//     scale is applied; y = 2^-E * sum over groups.
+//     int32, then one f32 fma), scaled by the unit's alpha * f_u and the zero
+//     point removed with its beta * f_u * (sum of X) (binary: sum (2b-1) X =
+//     2 sum bX - sum X; Q4: sum (n-8) X; Q2: sum (c-1.5) X) -- the x image
+//     stores both per unit, so this is one fma as with a single exponent --
+//     and the f16 group scale is applied; y = 2^-E * sum over groups.
 //   * A tiles live in LDS in compact form: per tile 16 lanes x 16 B of limbs
 //     plus a 16-byte zero block (stride 272 B); a lane whose row slot differs
 //     from its column slot reads the zero block through a per-lane constant
 //     offset, so the operand fetch is one ds_read_b128 with no VALU work.  One
 //     A fetch feeds R row tiles.
 // Weights arrive in the tiled layout of hk_tile.h.  Numerics: the only
-// roundings are X (2^-24 of max|x|), the f32 limb combine and the f32
-// accumulation over groups; rel-L2 vs the serial f32 reference is ~1e-7.
+// roundings are X (2^-24 of its unit's max |x|), the f32 limb combine and the
+// f32 accumulation over groups; rel-L2 vs the serial f32 reference is ~1e-7.
 #pragma once
 
 #include "hk_internal.h"
@@ -50,34 +57,42 @@ __device__ __forceinline__ v4i mfma_i8(const v4i& a, const v4i& b, const v4i& c)
 
 template <int KIND>
 struct Kcfg;
-// P = A tiles per step, SXG = columns per x-sum (the zero-point granularity a
-// lane needs per step: one binary group, one Q4 group of 32, one Q2 half-group),
-// SXW = floats stored per x-sum (mixed: the binary and the Q2 correction).
+// P = A tiles per step, SXG = columns per unit (the zero-point granularity a
+// lane needs per step: one binary group, one Q4 group of 32, one Q2 half-group;
+// each unit has its own exponent), SXW = floats stored per unit: {ALPHA f_u,
+// BETA f_u sum X} (mixed: the binary and the Q2 correction, then the binary
+// and the Q2 alpha, all times f_u).  A lane's partial for a unit is
+// combine(c) * SX[0] - SX[1] (in units of 2^-E).
 template <>
 struct Kcfg<HK_BIN> {
-    static constexpr int P = 8, STEP_COLS = 512, DATA = 16, SXG = 128, SXW = 1;
+    static constexpr int P = 8, STEP_COLS = 512, DATA = 16, SXG = 128, SXW = 2;
+    static constexpr float ALPHA = 1.0f / 64.0f, BETA = 1.0f;  // 2 sum bX - sum X
 };
 template <>
 struct Kcfg<HK_Q4> {
-    static constexpr int P = 2, STEP_COLS = 128, DATA = 16, SXG = 32, SXW = 1;
+    static constexpr int P = 2, STEP_COLS = 128, DATA = 16, SXG = 32, SXW = 2;
+    static constexpr float ALPHA = 1.0f, BETA = 8.0f;  // sum (n - 8) X
 };
 template <>
 struct Kcfg<HK_MIXED> {
-    static constexpr int P = 8, STEP_COLS = 512, DATA = 32, SXG = 64, SXW = 2;
+    static constexpr int P = 8, STEP_COLS = 512, DATA = 32, SXG = 64, SXW = 4;
+    static constexpr float ALPHA = 2.0f / 64.0f, BETA = 1.0f;  // binary items (Q2 items: alpha / 2)
 };
 template <>
 struct Kcfg<HK_Q8> {
-    static constexpr int P = 1, STEP_COLS = 64, DATA = 16, SXG = 16, SXW = 1;
+    static constexpr int P = 1, STEP_COLS = 64, DATA = 16, SXG = 16, SXW = 2;
+    static constexpr float ALPHA = 1.0f, BETA = -1.0f;  // code ^ 0x80 = code - 128: + sum X
 };
 template <>
 struct Kcfg<HK_U3> {
-    static constexpr int P = 4, STEP_COLS = 128, DATA = 12, SXG = 32, SXW = 1;
+    static constexpr int P = 4, STEP_COLS = 128, DATA = 12, SXG = 32, SXW = 2;
+    static constexpr float ALPHA = 1.0f / 32.0f, BETA = 3.0f;  // 32 code X, code = q + 3
 };
 
 constexpr int A_TILE_STRIDE = 272;  // 256 B of active-lane limbs + 16 B of zeros
 
 // Bytes of the x image of an organ with `steps` steps: the A tiles, then the
-// per-SXG-column sums of X (as f32; SXW floats each).
+// per-unit (SXG columns) scale factors and sums of X (SXW floats each).
 template <int KIND>
 __host__ __device__ constexpr size_t x_lds_bytes(uint32_t steps) {
     return (size_t)steps * Kcfg<KIND>::P * A_TILE_STRIDE +
@@ -201,9 +216,11 @@ __device__ __forceinline__ int32_t quantize8(const float4* v, int E, float* f) {
 }
 
 // The x image: fixed-point x (E = 23 - exponent of max|x|; 0 for x = 0 or
-// non-finite x, which sets the flag), X = rint(x 2^E), and from it the A tiles
-// and the per-SXG-column sums of X, written to img (x_lds_bytes<KIND>(steps)
-// bytes, any address space).  Returns E.
+// non-finite x, which sets the flag), per unit of SXG columns E_u = 23 -
+// exponent of the unit's max (at most E + 100; E for an all-zero unit),
+// X = rint(x 2^E_u), and from it the A tiles and each unit's {ALPHA f_u,
+// BETA f_u sum X} with f_u = 2^(E - E_u), written to img
+// (x_lds_bytes<KIND>(steps) bytes, any address space).  Returns E.
 //
 // The image columns (cols rounded up to whole steps, zero past cols) go in
 // rounds of 8 * team size columns: each member quantizes its chunk of the
@@ -254,12 +271,19 @@ __device__ int x_image(const Team& team, const XChunks<NC>& xc, const float* x, 
         const uint32_t ch = cb + me + j * ts;
         if (ch < ce) {
             if (bad) v[0] = v[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            // a unit's NL chunks belong to NL consecutive members, all active together
+            float mu = max_abs8(v);
+#pragma unroll
+            for (int k = 1; k < NL; k <<= 1) mu = fmaxf(mu, __shfl_xor(mu, k, 64));
+            int eu = 0;
+            if (mu > 0.0f) (void)frexpf(mu, &eu);
+            const int Eu = mu > 0.0f ? min(23 - eu, E + 100) : E;
+            const float fu = ldexpf(1.0f, E - Eu);
             float f[8];
-            int32_t s = quantize8(v, E, f);
+            int32_t s = quantize8(v, Eu, f);
             float4* o = reinterpret_cast<float4*>(w + 8u * me);
             o[0] = make_float4(f[0], f[1], f[2], f[3]);
             o[1] = make_float4(f[4], f[5], f[6], f[7]);
-            // a sum's NL chunks belong to NL consecutive members, all active together
 #pragma unroll
             for (int k = 1; k < NL; k <<= 1) s += __shfl_xor(s, k, 64);
             if constexpr (KIND == HK_MIXED) {
@@ -270,9 +294,13 @@ __device__ int x_image(const Team& team, const XChunks<NC>& xc, const float* x, 
 #pragma unroll
                 for (int k = 1; k < NL; k <<= 1) s3 += __shfl_xor(s3, k, 64);
                 if ((me & (uint32_t)(NL - 1)) == 0)
-                    reinterpret_cast<float2*>(SX)[ch / (uint32_t)NL] = make_float2((float)s, (float)(3 * s - 4 * s3) * 0.5f);
+                    reinterpret_cast<float4*>(SX)[ch / (uint32_t)NL] =
+                        make_float4((float)s * fu, (float)(3 * s - 4 * s3) * 0.5f * fu, Kcfg<KIND>::ALPHA * fu,
+                                    0.5f * Kcfg<KIND>::ALPHA * fu);
             } else {
-                if ((me & (uint32_t)(NL - 1)) == 0) SX[ch / (uint32_t)NL] = (float)s;
+                if ((me & (uint32_t)(NL - 1)) == 0)
+                    reinterpret_cast<float2*>(SX)[ch / (uint32_t)NL] =
+                        make_float2(Kcfg<KIND>::ALPHA * fu, Kcfg<KIND>::BETA * (float)s * fu);
             }
         }
         team.sync();
@@ -446,9 +474,9 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
                 c[r] = mfma_i8(a, b, c[r]);
             }
         }
-        const float sx = SX[4 * t + q];
+        const float2 u = reinterpret_cast<const float2*>(SX)[4 * t + q];
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] += f16_bits_to_f32(f.s[r]) * (combine_limbs(c[r]) * (1.0f / 64.0f) - sx);
+        for (int r = 0; r < R; ++r) acc[r] += f16_bits_to_f32(f.s[r]) * (combine_limbs(c[r]) * u.x - u.y);
     } else if constexpr (KIND == HK_Q4) {
         const uint32_t m = 0x0F0F0F0Fu;
         const v4i alo = A(t * 2), ahi = A(t * 2 + 1);
@@ -460,9 +488,9 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
             c[r] = mfma_i8(alo, lo, v4i{0, 0, 0, 0});
             c[r] = mfma_i8(ahi, hi, c[r]);
         }
-        const float sx = SX[4 * t + q];
+        const float2 u = reinterpret_cast<const float2*>(SX)[4 * t + q];
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] += f16_bits_to_f32(f.s[r]) * (combine_limbs(c[r]) - 8.0f * sx);
+        for (int r = 0; r < R; ++r) acc[r] += f16_bits_to_f32(f.s[r]) * (combine_limbs(c[r]) * u.x - u.y);
     } else if constexpr (KIND == HK_Q8) {
         // code - 127 = (code ^ 0x80 as a signed byte) + 1: the B bytes are the
         // codes with the top bit flipped and the +1 is the slot's sum of X
@@ -473,9 +501,9 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
             const v4i b = {(int)(f.v[r].x ^ m), (int)(f.v[r].y ^ m), (int)(f.v[r].z ^ m), (int)(f.v[r].w ^ m)};
             c[r] = mfma_i8(a, b, v4i{0, 0, 0, 0});
         }
-        const float sx = SX[4 * t + q];
+        const float2 u = reinterpret_cast<const float2*>(SX)[4 * t + q];
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] += f16_bits_to_f32(f.s[r]) * (combine_limbs(c[r]) + sx);
+        for (int r = 0; r < R; ++r) acc[r] += f16_bits_to_f32(f.s[r]) * (combine_limbs(c[r]) * u.x - u.y);
     } else if constexpr (KIND == HK_U3) {
 #pragma unroll
         for (int r = 0; r < R; ++r) c[r] = v4i{0, 0, 0, 0};
@@ -491,9 +519,9 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
                 c[r] = mfma_i8(a, b, c[r]);
             }
         }
-        const float sx = SX[4 * t + q];
+        const float2 u = reinterpret_cast<const float2*>(SX)[4 * t + q];
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] += f16_bits_to_f32(f.s[r]) * (combine_limbs(c[r]) * (1.0f / 32.0f) - 3.0f * sx);
+        for (int r = 0; r < R; ++r) acc[r] += f16_bits_to_f32(f.s[r]) * (combine_limbs(c[r]) * u.x - u.y);
     } else {
         // field u of a byte is bits 2u..2u+1 (binary: bit 2u; the odd bits come
         // from the copy shifted down by one).  A Q2 item's bit 7 is stored
@@ -511,7 +539,9 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
                 V[r][k + 4] = f.V[r][k + 4] >> sh;
             }
         }
-        const float4 sxq = reinterpret_cast<const float4*>(SX)[4 * t + q];  // {h0 bin, h0 q2, h1 bin, h1 q2}
+        // per half: {binary correction, Q2 correction, binary alpha, Q2 alpha}
+        const float4 uh[2] = {reinterpret_cast<const float4*>(SX)[2 * (4 * t + q)],
+                              reinterpret_cast<const float4*>(SX)[2 * (4 * t + q) + 1]};
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -533,8 +563,8 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
             }
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const float alpha = q2[r] ? (1.0f / 64.0f) : (2.0f / 64.0f);
-                const float corr = q2[r] ? (h ? sxq.w : sxq.y) : (h ? sxq.z : sxq.x);
+                const float alpha = q2[r] ? uh[h].w : uh[h].z;
+                const float corr = q2[r] ? uh[h].y : uh[h].x;
                 acc[r] += f16_bits_to_f32(h ? f.s1[r] : f.s0[r]) * (combine_limbs(c[r]) * alpha - corr);
             }
         }

@@ -406,14 +406,14 @@ __device__ __forceinline__ void tiles_x_tokens(const uint8_t* const* base_d, con
     const float* SX0 = reinterpret_cast<const float*>(img + (size_t)S * 2u * A_TILE_STRIDE);
     auto consume = [&](const Frag<HK_Q4, R>& fr, uint32_t t) {
         v4i alo[TB], ahi[TB];
-        float sx[TB];
+        float2 sx[TB];  // the unit's {f_u, 8 f_u sum X}
 #pragma unroll
         for (int j = 0; j < TB; ++j) {
             if ((uint32_t)j < nm) {
                 const uint8_t* ij = img + (size_t)j * img_bytes;
                 alo[j] = lds_a(ij, 2u * t, aoff);
                 ahi[j] = lds_a(ij, 2u * t + 1u, aoff);
-                sx[j] = reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(SX0) + (size_t)j * img_bytes)[4u * t + (uint32_t)q];
+                sx[j] = reinterpret_cast<const float2*>(reinterpret_cast<const uint8_t*>(SX0) + (size_t)j * img_bytes)[4u * t + (uint32_t)q];
             }
         }
         const uint32_t m = 0x0F0F0F0Fu;
@@ -428,7 +428,7 @@ __device__ __forceinline__ void tiles_x_tokens(const uint8_t* const* base_d, con
                 if ((uint32_t)j < nm) {
                     v4i c = mfma_i8(alo[j], lo, v4i{0, 0, 0, 0});
                     c = mfma_i8(ahi[j], hi, c);
-                    acc[j][r] += sc * (combine_limbs(c) - 8.0f * sx[j]);
+                    acc[j][r] += sc * (combine_limbs(c) * sx[j].x - sx[j].y);
                 }
             }
         }
