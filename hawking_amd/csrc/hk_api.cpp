@@ -1249,6 +1249,7 @@ constexpr uint32_t MOE_MAX_SLOTS = 16;
 struct MoeLayerHost {
     void* slab = nullptr;
     size_t slab_bytes = 0;
+    size_t stride = 0;             // bytes between consecutive routed experts in the slab
     std::vector<OrganView> table;  // (E+1)*3
     std::vector<size_t> packed;    // per organ, algorithmic bytes
     OrganView* table_dev = nullptr;
@@ -1396,9 +1397,8 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
     const size_t dpl = dense_per_layer(c);
     const size_t tab = align256((size_t)(c.n_experts + 1) * 3 * sizeof(OrganView));
     const size_t img = align256(moe_img_bytes(c.expert_kind, c.hidden));
-    const size_t sel = align256((size_t)slots * 3 * sizeof(OrganView));
     const size_t ws = align256(((size_t)c.n_experts + 4) * 4) + 4 * 256 + align256((size_t)slots * imax * 4) + img + 256 +
-                      sel + 2 * align256((size_t)c.hidden * 4);
+                      2 * align256((size_t)c.hidden * 4);
     if (hipMalloc(&m->dense, dpl * c.n_layers) != hipSuccess || hipMalloc(&m->tables, tab * c.n_layers) != hipSuccess ||
         hipMalloc(&m->ws_mem, ws) != hipSuccess) {
         if (m->dense) (void)hipFree(m->dense);
@@ -1442,8 +1442,6 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
     m->ws.img = w;
     w += img;
     w += 256;
-    m->ws.sel = reinterpret_cast<OrganView*>(w);
-    w += sel;
     m->hbuf[0] = reinterpret_cast<float*>(w);
     w += align256((size_t)c.hidden * 4);
     m->hbuf[1] = reinterpret_cast<float*>(w);
@@ -1474,25 +1472,43 @@ extern "C" int hk_moe_model_free(hk_ctx* ctx, hk_moe_model* m) {
 }
 
 // Repacks one layer's staged canonical organs (canon[i], mixed binary-group
-// counts nbin[i]) into a fresh slab of tiled organs and uploads the layer's
-// device table.  Synchronises `st`.
+// counts nbin[i]; organ i = expert i / 3, projection i % 3, expert
+// n_experts = the shared one) into a fresh slab of tiled organs and uploads
+// the layer's device table.  Routed experts sit at a uniform stride: each
+// projection is placed with the layer's largest layout of it (mixed: the
+// most Q2 groups), so routed expert e's views are expert 0's advanced by
+// e * stride.  Synchronises `st`.
 static int repack_layer(hk_ctx* ctx, MoeLayerHost& L, const std::vector<CanonView>& canon,
-                        const std::vector<uint32_t>& nbin, hipStream_t st) {
+                        const std::vector<uint32_t>& nbin, uint32_t n_experts, hipStream_t st) {
     const size_t n_org = canon.size();
     const int kind = canon[0].kind;
-    std::vector<size_t> bytes(n_org);
     std::vector<uint32_t> nq2(n_org, 0);
-    size_t total = 0, words = 0, max_items = 0;
+    size_t words = 0, max_items = 0;
+    uint32_t max_q2[3] = {0, 0, 0};
     for (size_t i = 0; i < n_org; ++i) {
         const CanonView& v = canon[i];
         const uint32_t nb = kind == HK_MIXED ? nbin[i] : 0;
         if (kind == HK_MIXED) nq2[i] = (uint32_t)((size_t)v.rows * v.cols / 128) - nb;
-        bytes[i] = tiled_bytes(kind, v.group, v.rows, v.cols, nb, nq2[i], &L.packed[i]);
-        total += bytes[i];
+        (void)tiled_bytes(kind, v.group, v.rows, v.cols, nb, nq2[i], &L.packed[i]);
+        if (i / 3 < n_experts) max_q2[i % 3] = std::max(max_q2[i % 3], nq2[i]);
         const size_t blocks = (size_t)n_tiles_for(v.rows) * n_steps_for(kind, v.cols);
         words += blocks;
         max_items = std::max(max_items, blocks * 64);
     }
+    // the envelope layout of each routed projection, and the shared expert's own
+    size_t off[3], stride = 0;
+    uint32_t env_bin[3];
+    for (int p = 0; p < 3; ++p) {
+        const CanonView& v = canon[(size_t)p];
+        const uint32_t groups = kind == HK_MIXED ? (uint32_t)((size_t)v.rows * v.cols / 128) : 0;
+        env_bin[p] = groups - max_q2[p];
+        off[p] = stride;
+        stride += tiled_bytes(kind, v.group, v.rows, v.cols, env_bin[p], max_q2[p], nullptr);
+    }
+    size_t total = stride * n_experts;
+    for (size_t i = (size_t)n_experts * 3; i < n_org; ++i)
+        total += tiled_bytes(kind, canon[i].group, canon[i].rows, canon[i].cols, kind == HK_MIXED ? nbin[i] : 0, nq2[i],
+                             nullptr);
     if (L.slab) {
         (void)hipStreamSynchronize(st);
         (void)hipFree(L.slab);
@@ -1502,18 +1518,26 @@ static int repack_layer(hk_ctx* ctx, MoeLayerHost& L, const std::vector<CanonVie
     L.ready = false;
     if (hipMalloc(&L.slab, total) != hipSuccess) return set_error(ctx, HK_E_NOMEM, "expert slab allocation failed");
     L.slab_bytes = total;
+    L.stride = stride;
     void* aux = nullptr;
     const size_t jobs_bytes = align256(n_org * sizeof(RepackJob));
     if (hipMalloc(&aux, jobs_bytes + words * 4 + 256) != hipSuccess) return set_error(ctx, HK_E_NOMEM, "repack job allocation failed");
     std::vector<RepackJob> jobs(n_org);
-    uint8_t* p = static_cast<uint8_t*>(L.slab);
+    uint8_t* slab = static_cast<uint8_t*>(L.slab);
+    uint8_t* p_shared = slab + stride * n_experts;
     uint32_t* counts = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(aux) + jobs_bytes);
     for (size_t i = 0; i < n_org; ++i) {
         const CanonView& v = canon[i];
-        L.table[i] = tiled_place(kind, v.group, v.rows, v.cols, kind == HK_MIXED ? nbin[i] : 0, nq2[i], p);
+        const size_t e = i / 3, p = i % 3;
+        if (e < n_experts) {
+            L.table[i] = tiled_place(kind, v.group, v.rows, v.cols, kind == HK_MIXED ? env_bin[p] : 0,
+                                     kind == HK_MIXED ? max_q2[p] : 0, slab + e * stride + off[p]);
+        } else {
+            L.table[i] = tiled_place(kind, v.group, v.rows, v.cols, kind == HK_MIXED ? nbin[i] : 0, nq2[i], p_shared);
+            p_shared += tiled_bytes(kind, v.group, v.rows, v.cols, kind == HK_MIXED ? nbin[i] : 0, nq2[i], nullptr);
+        }
         jobs[i] = RepackJob{v, L.table[i], counts};
         counts += (size_t)L.table[i].n_tiles * L.table[i].steps;
-        p += bytes[i];
     }
     int rc = check_hip(ctx, hipMemcpyAsync(aux, jobs.data(), n_org * sizeof(RepackJob), hipMemcpyHostToDevice, st),
                        "repack job upload");
@@ -1567,7 +1591,7 @@ extern "C" int hk_moe_model_set_layer(hk_ctx* ctx, hk_moe_model* m, uint32_t lay
         nbin[i] = srcs[i]->n_bin;
         p += lay[i].total();
     }
-    if (!rc) rc = repack_layer(ctx, L, canon, nbin, st);
+    if (!rc) rc = repack_layer(ctx, L, canon, nbin, c.n_experts, st);
     (void)hipStreamSynchronize(st);
     (void)hipFree(stage);
     if (rc) return rc;
@@ -1690,7 +1714,7 @@ extern "C" int hk_moe_model_fill_synthetic(hk_ctx* ctx, hk_moe_model* m, uint64_
         rc = check_hip(ctx, hipMemcpyAsync(jobs_dev, jobs.data(), n_org * sizeof(SynthJob), hipMemcpyHostToDevice, st), "job upload");
         if (!rc) rc = check_hip(ctx, launch_synth_jobs(c.expert_kind, static_cast<SynthJob*>(jobs_dev), n_org, max_groups, bad, st),
                                 "expert synth");
-        if (!rc) rc = repack_layer(ctx, L, canon, nbin, st);
+        if (!rc) rc = repack_layer(ctx, L, canon, nbin, c.n_experts, st);
         if (!rc) L.ready = true;
     }
     uint32_t badv = 0;
@@ -1728,7 +1752,8 @@ static int moe_layer_dev(hk_ctx* ctx, hk_moe_model* m, uint32_t layer, MoeLayerD
     if (layer >= m->cfg.n_layers) return set_error(ctx, HK_E_INVALID_ARG, "layer index out of range");
     MoeLayerHost& L = m->layers[layer];
     if (!L.ready) return set_error(ctx, HK_E_INVALID_ARG, "layer " + std::to_string(layer) + " has no weights");
-    *out = MoeLayerDev{L.norm_w, L.router_w, (m->cfg.shared_gate && m->cfg.shared_inter) ? L.gate_w : nullptr, L.table_dev};
+    *out = MoeLayerDev{L.norm_w, L.router_w, (m->cfg.shared_gate && m->cfg.shared_inter) ? L.gate_w : nullptr,
+                       L.table_dev, L.stride};
     return HK_OK;
 }
 

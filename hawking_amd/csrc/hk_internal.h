@@ -110,6 +110,29 @@ __device__ __forceinline__ void copy16_to_lds(uint4* dst, const uint4* src, uint
     }
 }
 
+// Two such copies at once (src0 -> dst0 with n0 pieces, then src1 -> dst1
+// with n1) sharing one batch of loads: one latency where two calls of
+// copy16_to_lds would take two.
+template <int PT>
+__device__ __forceinline__ void copy16x2_to_lds(uint4* dst0, const uint4* src0, uint32_t n0, uint4* dst1,
+                                                const uint4* src1, uint32_t n1, uint32_t tid, uint32_t nthreads) {
+    const uint32_t n = n0 + n1;
+    for (uint32_t b = 0; b < n; b += PT * nthreads) {
+        uint4 v[PT];
+#pragma unroll
+        for (int i = 0; i < PT; ++i) {
+            const uint32_t k = b + tid + (uint32_t)i * nthreads;
+            if (k < n) v[i] = ldg(k < n0 ? src0 + k : src1 + (k - n0));
+        }
+#pragma unroll
+        for (int i = 0; i < PT; ++i) {
+            const uint32_t k = b + tid + (uint32_t)i * nthreads;
+            if (k < n0) dst0[k] = v[i];
+            else if (k < n) dst1[k - n0] = v[i];
+        }
+    }
+}
+
 // Workgroup -> (organ, part).  Workgroups are dispatched to the 8 XCDs round
 // robin by linear id, so ids 8 apart share an XCD and its L2: each run of
 // 8 * parts ids covers 8 organs with id % 8 selecting the organ, and all

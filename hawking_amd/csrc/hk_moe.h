@@ -17,13 +17,29 @@ struct MoeDims {
 };
 
 // One layer's device weights; table holds (E+1)*3 tiled organ views:
-// [expert*3 + {0: gate, 1: up, 2: down}], expert E = shared expert.
+// [expert*3 + {0: gate, 1: up, 2: down}], expert E = shared expert.  The
+// routed experts sit at a uniform stride in the layer's slab (each
+// projection placed with the layer's largest layout of it), so routed expert
+// e's views are expert 0's with every section pointer advanced by
+// e * stride: a kernel loads table[p] (or the shared expert's entry) when it
+// starts, in parallel with its other loads, and forms the routed views from
+// the route id with no dependent table load.
 struct MoeLayerDev {
     const float* norm_w;
     const float* router_w;
     const float* gate_w;   // shared-expert gate, may be null
     const OrganView* table;
+    uint64_t stride;
 };
+
+// View v (expert 0's, projection p) advanced to routed expert e.
+__device__ __forceinline__ OrganView advance_view(OrganView v, uint32_t e, uint64_t stride) {
+    const size_t off = (size_t)e * stride;
+    v.data += off;
+    v.scales = reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(v.scales) + off);
+    v.hdr = reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(v.hdr) + off);
+    return v;
+}
 
 // Per-model device workspace.
 struct MoeWs {
@@ -34,7 +50,6 @@ struct MoeWs {
     float* act;        // [(K+1) * Imax]
     uint8_t* img;      // x image of RMSNorm(h) for the gate/up organs
     int32_t* img_e;    // [1]: its exponent E
-    OrganView* sel;    // [(K+1)*3]: the organs of the selected experts, slot order
     uint32_t* status;  // device error bits
 };
 

@@ -132,8 +132,8 @@ __global__ void __launch_bounds__(256) moe_route_kernel(MoeDims d, MoeLayerDev L
 // ranks the router logits itself (softmax, top-k, renormalise:
 // source_qwen80_topk_router; one wave, about 2 us) while its other waves copy
 // the layer's x image into LDS, and takes its slot's expert; this saves a
-// launch.  Tile 0 of each slot publishes the slot's down organ (and slot 0
-// the route and the shared-gate value) for the down kernel.
+// launch.  Slot 0's tile 0 publishes the route and the shared-gate value
+// for the down kernel.
 template <int KIND, int D, int NPL>
 __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev L, MoeWs ws, int32_t* ids_out,
                                                           float* w_out) {
@@ -145,6 +145,9 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const bool lead = T == 0, routed = slot < d.K;
     const uint32_t S = n_steps_for(KIND, d.H), ib = (uint32_t)x_lds_bytes<KIND>(S);
+    // the slot's base views (expert 0's, or the shared expert's), loaded with the logits
+    const uint32_t base = routed ? 0u : d.E * 3u;
+    const OrganView g0 = L.table[base], u0 = L.table[base + 1u];
     if (routed && wave == 0) {
         const bool pub = lead && slot == 0;
         const ArgBest mine = softmax_topk_wave<NPL>(ws.logits, d.E, d.K, 1, pub ? ws.ids : nullptr,
@@ -156,26 +159,24 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev
         if (pub && lane == 0) ws.gate[1] = L.gate_w ? 1.0f / (1.0f + expf(-ws.gate[0])) : 1.0f;
         if ((uint32_t)lane == slot) sel_id = mine.i;
     } else {
-        // the x image built by the route kernel, into LDS
+        // the x image built by the route kernel, into LDS (every load in
+        // flight before the first store: one memory latency)
         const uint32_t t0 = routed ? 64u : 0u;
-        for (uint32_t o = (threadIdx.x - t0) * 16u; o < ib; o += (blockDim.x - t0) * 16u)
-            *reinterpret_cast<uint4*>(lds + o) = *reinterpret_cast<const uint4*>(ws.img + o);
+        copy16_to_lds<4>(reinterpret_cast<uint4*>(lds), reinterpret_cast<const uint4*>(ws.img), ib / 16u,
+                         threadIdx.x - t0, blockDim.x - t0);
     }
     __syncthreads();
     const int32_t id = routed ? sel_id : (int32_t)d.E;
-    // an invalid route selects no organ (all-zero down view: n_tiles = 0)
+    // an invalid route selects no organ (the down kernel skips it too)
     const bool ok = !routed || (id >= 0 && (uint32_t)id < d.E);
-    if (lead && threadIdx.x < sizeof(OrganView) / 8) {
-        // word copy (a struct assignment here goes through scratch memory)
-        static_assert(sizeof(OrganView) % 8 == 0, "OrganView is copied in 8-byte words");
-        const uint64_t* from = reinterpret_cast<const uint64_t*>(L.table + (ok ? (uint32_t)id * 3u + 2u : 0u));
-        reinterpret_cast<uint64_t*>(ws.sel + slot * 3u + 2u)[threadIdx.x] = ok ? from[threadIdx.x] : 0ull;
-        if (!ok && threadIdx.x == 0) atomicOr(ws.status, HK_DEVERR_ROUTE);
+    if (!ok) {
+        if (lead && threadIdx.x == 0) atomicOr(ws.status, HK_DEVERR_ROUTE);
+        return;
     }
-    if (!ok) return;
-    const OrganView g = L.table[(uint32_t)id * 3u + 0u];
+    // the slot's organs from the id: no table load between the route and the weights
+    const OrganView g = routed ? advance_view(g0, (uint32_t)id, L.stride) : g0;
     if (T >= g.n_tiles) return;
-    const OrganView u = L.table[(uint32_t)id * 3u + 1u];
+    const OrganView u = routed ? advance_view(u0, (uint32_t)id, L.stride) : u0;
     const uint32_t per = (S + 3u) / 4u;
     const uint32_t s0 = min(wave * per, S), n = min(s0 + per, S) - s0;
     Frag<KIND, 2> f[D];
@@ -224,31 +225,37 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev
 }
 
 // h_in and h_out may be the same vector (each row is read, then written, by
-// one thread); route weights come from `wts` (slot order).
+// one thread); the route (ids, weights) in slot order; slot d.K = the shared
+// expert.  A slot with an invalid id contributes nothing.
 template <int KIND, int D>
-__global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, const float* h_in, float* h_out, MoeWs ws,
+__global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, MoeLayerDev L, const float* h_in, float* h_out,
+                                                        MoeWs ws, const int32_t* __restrict__ ids,
                                                         const float* __restrict__ wts, uint32_t img_stride) {
     extern __shared__ __align__(16) uint8_t lds[];
     const uint32_t T = blockIdx.x, slots = blockDim.x >> 6;
     const uint32_t slot = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, q = lane >> 4;
-    const OrganView o = ws.sel[slot * 3u + 2u];
-    const bool active = T < o.n_tiles;
+    const bool routed = slot < d.K;
+    const OrganView o0 = L.table[routed ? 2u : d.E * 3u + 2u];  // loaded with the route
+    const int32_t id = routed ? __builtin_amdgcn_readfirstlane(ids[slot]) : (int32_t)d.E;
+    const bool ok = !routed || (id >= 0 && (uint32_t)id < d.E);
+    const OrganView o = routed ? advance_view(o0, ok ? (uint32_t)id : 0u, L.stride) : o0;
+    const bool active = ok && T < o.n_tiles;
     const uint32_t S = active ? o.steps : 0u;
     Frag<KIND, 1> f[D];
 #pragma unroll
     for (int k = 0; k < D; ++k)
         if ((uint32_t)k < S) fetch_one<KIND, 1>(o, T, (uint32_t)k, lane, f[k], 0);
     const float wgt = !active ? 0.0f : (slot < d.K ? wts[slot] : ws.gate[1]);
-    // this slot's activations: staged in LDS with one batch of loads, then
-    // turned into an x image of the slot's own
+    // this slot's activations: staged in LDS with one batch of loads (sized
+    // from the dims, so they do not wait for the route), then turned into an
+    // x image of the slot's own
     uint8_t* img = lds + (size_t)slot * img_stride;
     const uint32_t kst = x_image_cols<KIND>(n_steps_for(KIND, d.Imax));
     float* xs = reinterpret_cast<float*>(lds + (size_t)slots * (img_stride + 64u)) + (size_t)slot * kst;
-    if (active) {
-        const float4* a4 = reinterpret_cast<const float4*>(ws.act + (size_t)slot * d.Imax);
-        for (uint32_t j = (uint32_t)lane; j < o.cols / 4u; j += 64u) reinterpret_cast<float4*>(xs)[j] = a4[j];
-    }
+    const uint32_t acols = routed ? d.I : d.SI;
+    copy16_to_lds<4>(reinterpret_cast<uint4*>(xs), reinterpret_cast<const uint4*>(ws.act + (size_t)slot * d.Imax),
+                     acols / 4u, (uint32_t)lane, 64u);
     __syncthreads();
     int E = 0;
     if (active) {
@@ -290,7 +297,7 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, const float* 
 // shared expert.  The slot's first weight steps are issued as soon as its id
 // is read; the workgroup then builds the x image of x itself (no route
 // kernel) and, for the shared slot, tile 0 forms the shared gate
-// sigmoid(wg . x) (1 without a gate).  Tile 0 publishes the slot's down organ.
+// sigmoid(wg . x) (1 without a gate).
 template <int KIND, int D>
 __global__ void __launch_bounds__(256) moe_block_gate_up_kernel(MoeDims d, MoeLayerDev L, MoeWs ws,
                                                                 const int32_t* __restrict__ route_ids,
@@ -301,18 +308,18 @@ __global__ void __launch_bounds__(256) moe_block_gate_up_kernel(MoeDims d, MoeLa
     const int lane = threadIdx.x & 63, q = lane >> 4;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const bool routed = slot < d.K;
+    const uint32_t base = routed ? 0u : d.E * 3u;
+    const OrganView g0 = L.table[base], u0 = L.table[base + 1u];
     const int32_t id = routed ? __builtin_amdgcn_readfirstlane(route_ids[slot]) : (int32_t)d.E;
-    // an invalid route selects no organ (all-zero down view: n_tiles = 0)
+    // an invalid route selects no organ (the down kernel skips it too)
     const bool ok = !routed || (id >= 0 && (uint32_t)id < d.E);
-    if (T == 0 && threadIdx.x < sizeof(OrganView) / 8) {
-        const uint64_t* from = reinterpret_cast<const uint64_t*>(L.table + (ok ? (uint32_t)id * 3u + 2u : 0u));
-        reinterpret_cast<uint64_t*>(ws.sel + slot * 3u + 2u)[threadIdx.x] = ok ? from[threadIdx.x] : 0ull;
-        if (!ok && threadIdx.x == 0) atomicOr(ws.status, HK_DEVERR_ROUTE);
+    if (!ok) {
+        if (T == 0 && threadIdx.x == 0) atomicOr(ws.status, HK_DEVERR_ROUTE);
+        return;
     }
-    if (!ok) return;
-    const OrganView g = L.table[(uint32_t)id * 3u + 0u];
+    const OrganView g = routed ? advance_view(g0, (uint32_t)id, L.stride) : g0;
     if (T >= g.n_tiles) return;
-    const OrganView u = L.table[(uint32_t)id * 3u + 1u];
+    const OrganView u = routed ? advance_view(u0, (uint32_t)id, L.stride) : u0;
     const uint32_t S = n_steps_for(KIND, d.H), ib = (uint32_t)x_lds_bytes<KIND>(S);
     const uint32_t per = (S + 3u) / 4u;
     const uint32_t s0 = min(wave * per, S), n = min(s0 + per, S) - s0;
@@ -394,7 +401,8 @@ static hipError_t launch_block(const MoeDims& d, const MoeLayerDev& L, const int
     hipLaunchKernelGGL((moe_block_gate_up_kernel<KIND, 4>), dim3(gu_tiles, slots), dim3(256),
                        moe_block_gate_up_lds_bytes(KIND, d.H), s, d, L, ws, route_ids, x);
     hipLaunchKernelGGL((moe_down_kernel<KIND, 4>), dim3(n_tiles_for(d.H)), dim3(64u * slots),
-                       moe_down_lds_bytes(KIND, d.Imax, slots), s, d, out, out, ws, route_weights, img_stride);
+                       moe_down_lds_bytes(KIND, d.Imax, slots), s, d, L, out, out, ws, route_ids, route_weights,
+                       img_stride);
     return hipGetLastError();
 }
 
@@ -426,7 +434,8 @@ static hipError_t launch_layer(const MoeDims& d, const MoeLayerDev& L, const flo
     else
         hipLaunchKernelGGL((moe_gate_up_kernel<KIND, 4, 64>), gg, dim3(256), gl, s, d, L, ws, ids_out, w_out);
     hipLaunchKernelGGL((moe_down_kernel<KIND, 4>), dim3(n_tiles_for(d.H)), dim3(64u * slots),
-                       moe_down_lds_bytes(KIND, d.Imax, slots), s, d, h_in, h_out, ws, ws.weights, img_stride);
+                       moe_down_lds_bytes(KIND, d.Imax, slots), s, d, L, h_in, h_out, ws, ws.ids, ws.weights,
+                       img_stride);
     return hipGetLastError();
 }
 

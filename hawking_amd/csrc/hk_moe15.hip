@@ -262,10 +262,9 @@ __global__ void __launch_bounds__(256) m15_gate_up_kernel(M15Dims d, M15Dev L, M
         if ((uint32_t)lane == slot) sel_id = mine.i;
     } else {
         // the binary image and xn (for the residual) into LDS
-        for (uint32_t o = (threadIdx.x - 64u) * 16u; o < ib; o += (blockDim.x - 64u) * 16u)
-            *reinterpret_cast<uint4*>(lds + o) = ldg(reinterpret_cast<const uint4*>(ws.img + o));
-        copy16_to_lds<4>(reinterpret_cast<uint4*>(lds + ib16), reinterpret_cast<const uint4*>(ws.xn), d.H / 4u,
-                         threadIdx.x - 64u, blockDim.x - 64u);
+        copy16x2_to_lds<6>(reinterpret_cast<uint4*>(lds), reinterpret_cast<const uint4*>(ws.img), ib / 16u,
+                           reinterpret_cast<uint4*>(lds + ib16), reinterpret_cast<const uint4*>(ws.xn), d.H / 4u,
+                           threadIdx.x - 64u, blockDim.x - 64u);
     }
     __syncthreads();
     const int32_t id = sel_id;
