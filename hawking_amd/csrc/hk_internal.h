@@ -91,17 +91,16 @@ __device__ __forceinline__ float4 ldg(const float4* p) {
 // Copies n16 16-byte pieces from global memory to dst (LDS) with `nthreads`
 // threads (this one is `tid`); each thread issues PT loads before its first
 // store, so the copy costs about one memory latency per PT * nthreads pieces
-// (a load-then-store loop would wait for every load in turn).
+// (a load-then-store loop would wait for every load in turn).  The loads are
+// unconditional (an index past the end re-reads the last piece), so no branch
+// holds them back.
 template <int PT>
 __device__ __forceinline__ void copy16_to_lds(uint4* dst, const uint4* src, uint32_t n16, uint32_t tid,
                                               uint32_t nthreads) {
     for (uint32_t b = 0; b < n16; b += PT * nthreads) {
         uint4 v[PT];
 #pragma unroll
-        for (int i = 0; i < PT; ++i) {
-            const uint32_t k = b + tid + (uint32_t)i * nthreads;
-            if (k < n16) v[i] = ldg(src + k);
-        }
+        for (int i = 0; i < PT; ++i) v[i] = ldg(src + min(b + tid + (uint32_t)i * nthreads, n16 - 1u));
 #pragma unroll
         for (int i = 0; i < PT; ++i) {
             const uint32_t k = b + tid + (uint32_t)i * nthreads;

@@ -215,6 +215,52 @@ __device__ __forceinline__ int32_t quantize8(const float4* v, int E, float* f) {
     return s;
 }
 
+// Reductions over aligned groups of G lanes (G a power of two <= 64) as an
+// xor butterfly, every lane of a group getting its group's result: distances
+// 1 and 2 are DPP quad permutations, 4 and 8 two DPP row shifts each (row_shl
+// on the lower bank of every pair, row_shr on the upper, selected by the
+// bank mask), 16 and 32 the permlane16 / permlane32 swaps.  No LDS round
+// trip, unlike a shuffle; exact for integer sums and for max.  The lanes of a
+// group must be active together.
+template <int K>
+__device__ __forceinline__ uint32_t xor_partner(uint32_t v) {
+    const int x = (int)v;
+    if constexpr (K == 1) return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);  // quad_perm 1,0,3,2
+    if constexpr (K == 2) return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);  // quad_perm 2,3,0,1
+    if constexpr (K == 4)  // row_shr:4 into banks 1, 3; row_shl:4 into banks 0, 2
+        return (uint32_t)__builtin_amdgcn_update_dpp(__builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xA, false), x,
+                                                     0x104, 0xF, 0x5, false);
+    if constexpr (K == 8)  // row_shr:8 into banks 2, 3; row_shl:8 into banks 0, 1
+        return (uint32_t)__builtin_amdgcn_update_dpp(__builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xC, false), x,
+                                                     0x108, 0xF, 0x3, false);
+}
+template <int G, class Op>
+__device__ __forceinline__ uint32_t group_reduce(uint32_t v, Op op) {
+    if constexpr (G > 1) v = op(v, xor_partner<1>(v));
+    if constexpr (G > 2) v = op(v, xor_partner<2>(v));
+    if constexpr (G > 4) v = op(v, xor_partner<4>(v));
+    if constexpr (G > 8) v = op(v, xor_partner<8>(v));
+    if constexpr (G > 16) {
+        const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        v = op(a[0], a[1]);
+    }
+    if constexpr (G > 32) {
+        const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        v = op(b[0], b[1]);
+    }
+    return v;
+}
+template <int G>
+__device__ __forceinline__ int32_t group_sum(int32_t v) {
+    return (int32_t)group_reduce<G>((uint32_t)v, [](uint32_t a, uint32_t b) { return a + b; });
+}
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+    return __uint_as_float(group_reduce<G>(__float_as_uint(v), [](uint32_t a, uint32_t b) {
+        return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+    }));
+}
+
 // The x image: fixed-point x (E = 23 - exponent of max|x|; 0 for x = 0 or
 // non-finite x, which sets the flag), per unit of SXG columns E_u = 23 -
 // exponent of the unit's max (at most E + 100; E for an all-zero unit),
@@ -272,9 +318,7 @@ __device__ int x_image(const Team& team, const XChunks<NC>& xc, const float* x, 
         if (ch < ce) {
             if (bad) v[0] = v[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             // a unit's NL chunks belong to NL consecutive members, all active together
-            float mu = max_abs8(v);
-#pragma unroll
-            for (int k = 1; k < NL; k <<= 1) mu = fmaxf(mu, __shfl_xor(mu, k, 64));
+            const float mu = group_max<NL>(max_abs8(v));
             int eu = 0;
             if (mu > 0.0f) (void)frexpf(mu, &eu);
             const int Eu = mu > 0.0f ? min(23 - eu, E + 100) : E;
@@ -284,15 +328,12 @@ __device__ int x_image(const Team& team, const XChunks<NC>& xc, const float* x, 
             float4* o = reinterpret_cast<float4*>(w + 8u * me);
             o[0] = make_float4(f[0], f[1], f[2], f[3]);
             o[1] = make_float4(f[4], f[5], f[6], f[7]);
-#pragma unroll
-            for (int k = 1; k < NL; k <<= 1) s += __shfl_xor(s, k, 64);
+            s = group_sum<NL>(s);
             if constexpr (KIND == HK_MIXED) {
                 // the Q2 top field (columns 6, 7 of every chunk) decodes as
                 // code - 2, so its items subtract 1.5 sum X - 2 sum_top X
                 // (3 sum X - 4 sum_top X < 2^31: exact in int32, halved exactly)
-                int32_t s3 = (int32_t)f[6] + (int32_t)f[7];
-#pragma unroll
-                for (int k = 1; k < NL; k <<= 1) s3 += __shfl_xor(s3, k, 64);
+                const int32_t s3 = group_sum<NL>((int32_t)f[6] + (int32_t)f[7]);
                 if ((me & (uint32_t)(NL - 1)) == 0)
                     reinterpret_cast<float4*>(SX)[ch / (uint32_t)NL] =
                         make_float4((float)s * fu, (float)(3 * s - 4 * s3) * 0.5f * fu, Kcfg<KIND>::ALPHA * fu,
@@ -339,6 +380,93 @@ __device__ int x_image(const Team& team, const XChunks<NC>& xc, const float* x, 
         round(j, v);
     }
     return E;
+}
+
+// Where column c's A bytes go in an x image (a_value inverted): tile tau and
+// the byte offset of limb 0 inside it (limb L at + 16 L), and the power of
+// two the column's X is scaled by.
+template <int KIND>
+__device__ __forceinline__ void a_pos(uint32_t c, uint32_t& tau, uint32_t& off, int& sh) {
+    static_assert(KIND == HK_MIXED || KIND == HK_Q4, "scatter image builds cover the MoE expert kinds");
+    if constexpr (KIND == HK_MIXED) {
+        // column i of the 128-column group q -> (a, j, u): tile mu = 4h + u,
+        // byte 4r + j of rows 4q + limb
+        const uint32_t i = c & 127u, h = i >> 6;
+        const uint32_t av = ((i >> 5) & 3u) | ((i & 1u) << 2), j = (i >> 3) & 3u, u = (i >> 1) & 3u;
+        const uint32_t r = (av & 3u) - 2u * h + ((i & 1u) ? 2u : 0u);
+        tau = (c >> 9) * (uint32_t)Kcfg<KIND>::P + 4u * h + u;
+        off = 64u * ((c >> 7) & 3u) + 4u * r + j;
+        sh = 6 - 2 * (int)u;
+    } else {
+        const uint32_t cs = c & 127u;
+        tau = (c >> 7) * (uint32_t)Kcfg<KIND>::P + (cs & 1u);
+        off = 64u * (cs >> 5) + ((cs & 31u) >> 1);
+        sh = 0;
+    }
+}
+
+// The x image of x (cols columns in LDS, cols a multiple of 8; the image
+// columns past cols are zero) with E = 0, built by one wave straight into img
+// (LDS): lane l takes chunks l, l + 64, ... of 8 columns; each unit (SXG
+// columns = NL consecutive lanes) has E_u = 23 - exponent of its max (at most
+// 100, so f_u = 2^-E_u is a normal float; 0 for an all-zero unit), and every
+// column's limbs of X = rint(x 2^E_u) are stored as bytes at their tile
+// positions (a_pos).  These are the bytes x_image makes, and its unit entries
+// divided by its 2^E (every scale a power of two times the same roundings),
+// so a dot product on this image is x_image's times 2^-E exactly: no
+// whole-vector maximum, no gather pass.  A non-finite value zeroes its unit
+// and sets *nonfinite.  Only this wave's LDS is touched (no barrier).
+template <int KIND>
+__device__ void image_wave(uint32_t lane, const float* x, uint32_t cols, uint32_t steps, uint8_t* img,
+                           bool* nonfinite) {
+    constexpr int P = Kcfg<KIND>::P, SC = Kcfg<KIND>::STEP_COLS, NL = Kcfg<KIND>::SXG / 8;
+    float* SX = reinterpret_cast<float*>(img + (size_t)steps * P * A_TILE_STRIDE);
+    for (uint32_t i = lane; i < steps * (uint32_t)P; i += 64u)
+        *reinterpret_cast<uint4*>(img + (size_t)i * A_TILE_STRIDE + 256u) = make_uint4(0u, 0u, 0u, 0u);
+    bool any_bad = false;
+    // a unit's NL chunks are NL consecutive lanes, active together (the chunk count is a multiple of NL)
+    for (uint32_t ch = lane; ch < steps * (uint32_t)SC / 8u; ch += 64u) {
+        float4 v[2];
+        load_chunk(x, 8u * ch, cols, v);
+        float m = group_max<NL>(max_abs8(v));
+        const bool bad = !isfinite(m);
+        any_bad |= bad;
+        if (bad) {
+            v[0] = v[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            m = 0.0f;
+        }
+        int eu = 0;
+        if (m > 0.0f) (void)frexpf(m, &eu);
+        const int Eu = m > 0.0f ? min(23 - eu, 100) : 0;
+        const float fu = ldexpf(1.0f, -Eu);
+        float f[8];
+        const int32_t s = group_sum<NL>(quantize8(v, Eu, f));
+        if constexpr (KIND == HK_MIXED) {
+            const int32_t s3 = group_sum<NL>((int32_t)f[6] + (int32_t)f[7]);
+            if ((ch & (uint32_t)(NL - 1)) == 0)
+                reinterpret_cast<float4*>(SX)[ch / (uint32_t)NL] =
+                    make_float4((float)s * fu, (float)(3 * s - 4 * s3) * 0.5f * fu, Kcfg<KIND>::ALPHA * fu,
+                                0.5f * Kcfg<KIND>::ALPHA * fu);
+        } else {
+            if ((ch & (uint32_t)(NL - 1)) == 0)
+                reinterpret_cast<float2*>(SX)[ch / (uint32_t)NL] =
+                    make_float2(Kcfg<KIND>::ALPHA * fu, Kcfg<KIND>::BETA * (float)s * fu);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            uint32_t tau, off;
+            int sh;
+            a_pos<KIND>(8u * ch + (uint32_t)e, tau, off, sh);
+            // signed base-256 limbs of the scaled value
+            const uint32_t z = ((uint32_t)((int32_t)f[e] * (1 << sh)) + 0x80808080u) ^ 0x80808080u;
+            uint8_t* p = img + (size_t)tau * A_TILE_STRIDE + off;
+            p[0] = (uint8_t)z;
+            p[16] = (uint8_t)(z >> 8);
+            p[32] = (uint8_t)(z >> 16);
+            p[48] = (uint8_t)(z >> 24);
+        }
+    }
+    *nonfinite = any_bad;
 }
 
 // Per-lane byte offset of this lane's A operand inside a tile.

@@ -226,7 +226,10 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev
 
 // h_in and h_out may be the same vector (each row is read, then written, by
 // one thread); the route (ids, weights) in slot order; slot d.K = the shared
-// expert.  A slot with an invalid id contributes nothing.
+// expert.  A slot with an invalid id contributes nothing.  Each wave owns one
+// slot: it stages the slot's activations in LDS (loads issued before the
+// route is read), issues its weight steps, and builds the slot's x image with
+// E = 0 while they are in flight (image_wave: no barrier, no gather pass).
 template <int KIND, int D>
 __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, MoeLayerDev L, const float* h_in, float* h_out,
                                                         MoeWs ws, const int32_t* __restrict__ ids,
@@ -236,8 +239,19 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, MoeLayerDev L
     const uint32_t slot = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, q = lane >> 4;
     const bool routed = slot < d.K;
-    const OrganView o0 = L.table[routed ? 2u : d.E * 3u + 2u];  // loaded with the route
-    const int32_t id = routed ? __builtin_amdgcn_readfirstlane(ids[slot]) : (int32_t)d.E;
+    // the route and the slot's base view (scalar loads), the residual this
+    // thread adds at the end and the slot's activations (sized from the dims,
+    // so they wait for no route) all in flight together
+    const OrganView o0 = L.table[routed ? 2u : d.E * 3u + 2u];
+    const int32_t idr = __builtin_amdgcn_readfirstlane(ids[min(slot, d.K - 1u)]);  // no branch before the load
+    const int32_t id = routed ? idr : (int32_t)d.E;
+    const uint32_t row = T * 16u + threadIdx.x;
+    const float hres = h_in[min(row, d.H - 1u)];  // every lane loads (no branch); threads 0-15 use it
+    uint8_t* img = lds + (size_t)slot * img_stride;
+    const uint32_t kst = x_image_cols<KIND>(n_steps_for(KIND, d.Imax)), acols = routed ? d.I : d.SI;
+    float* xs = reinterpret_cast<float*>(lds + (size_t)slots * (img_stride + 64u)) + (size_t)slot * kst;
+    copy16_to_lds<4>(reinterpret_cast<uint4*>(xs), reinterpret_cast<const uint4*>(ws.act + (size_t)slot * d.Imax),
+                     acols / 4u, (uint32_t)lane, 64u);
     const bool ok = !routed || (id >= 0 && (uint32_t)id < d.E);
     const OrganView o = routed ? advance_view(o0, ok ? (uint32_t)id : 0u, L.stride) : o0;
     const bool active = ok && T < o.n_tiles;
@@ -247,26 +261,11 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, MoeLayerDev L
     for (int k = 0; k < D; ++k)
         if ((uint32_t)k < S) fetch_one<KIND, 1>(o, T, (uint32_t)k, lane, f[k], 0);
     const float wgt = !active ? 0.0f : (slot < d.K ? wts[slot] : ws.gate[1]);
-    // this slot's activations: staged in LDS with one batch of loads (sized
-    // from the dims, so they do not wait for the route), then turned into an
-    // x image of the slot's own
-    uint8_t* img = lds + (size_t)slot * img_stride;
-    const uint32_t kst = x_image_cols<KIND>(n_steps_for(KIND, d.Imax));
-    float* xs = reinterpret_cast<float*>(lds + (size_t)slots * (img_stride + 64u)) + (size_t)slot * kst;
-    const uint32_t acols = routed ? d.I : d.SI;
-    copy16_to_lds<4>(reinterpret_cast<uint4*>(xs), reinterpret_cast<const uint4*>(ws.act + (size_t)slot * d.Imax),
-                     acols / 4u, (uint32_t)lane, 64u);
-    __syncthreads();
-    int E = 0;
     if (active) {
         bool bad = false;
-        const WaveTeam team{(uint32_t)lane};
-        XChunks<1> xc;
-        load_x<1>(team, xs, o.cols, xc);
-        E = x_image<KIND, 1>(team, xc, xs, o.cols, S, img, xs, 8u * 64u, nullptr, &bad);
-        if (bad && lane == 0) atomicOr(ws.status, HK_DEVERR_NONFINITE);
+        image_wave<KIND>((uint32_t)lane, xs, o.cols, S, img, &bad);
+        if (__ballot(bad) != 0 && lane == 0) atomicOr(ws.status, HK_DEVERR_NONFINITE);
     }
-    __syncthreads();
     const ImageA A{img, a_lane_offset(lane)};
     const float* SX = reinterpret_cast<const float*>(img + (size_t)S * Kcfg<KIND>::P * A_TILE_STRIDE);
     float acc[1] = {0.0f};
@@ -281,14 +280,13 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, MoeLayerDev L
     }
     float* part = reinterpret_cast<float*>(lds + (size_t)slots * img_stride);  // [slots][16]
     const float y = tile_row_sum(acc[0]);
-    if (lane < 16) part[slot * 16u + lane] = active ? ldexpf(y, -E) * wgt : 0.0f;
+    if (lane < 16) part[slot * 16u + lane] = active ? y * wgt : 0.0f;
     __syncthreads();
     if (threadIdx.x < 16) {
         // combined += out_r * w_r in route order, then += gate * shared; out = h + combined
         float comb = 0.0f;
         for (uint32_t r = 0; r < slots; ++r) comb += part[r * 16u + threadIdx.x];
-        const uint32_t row = T * 16u + threadIdx.x;
-        if (row < d.H) h_out[row] = h_in[row] + comb;
+        if (row < d.H) h_out[row] = hres + comb;
     }
 }
 
