@@ -1387,6 +1387,7 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
     if (!(c.eps > 0.0f) || !std::isfinite(c.eps)) return set_error(ctx, HK_E_INVALID_ARG, "moe config: eps must be positive");
     const uint32_t imax = std::max(c.inter, c.shared_inter);
     if (c.router == HK_ROUTER_SOFTMAX && (moe_gate_up_lds_bytes(c.expert_kind, c.hidden) > MOE_LDS_LIMIT ||
+                                          moe_route_lds_bytes(c.expert_kind, c.hidden) > MOE_LDS_LIMIT ||
                                           moe_down_lds_bytes(c.expert_kind, imax, slots) > MOE_LDS_LIMIT))
         return set_error(ctx, HK_E_UNSUPPORTED, "moe config: x images of hidden / intermediate exceed 64 KiB of LDS");
     hk_moe_model* m = new hk_moe_model();
@@ -1397,7 +1398,7 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
     const size_t dpl = dense_per_layer(c);
     const size_t tab = align256((size_t)(c.n_experts + 1) * 3 * sizeof(OrganView));
     const size_t img = align256(moe_img_bytes(c.expert_kind, c.hidden));
-    const size_t ws = align256(((size_t)c.n_experts + 4) * 4) + 4 * 256 + align256((size_t)slots * imax * 4) + img + 256 +
+    const size_t ws = align256(((size_t)c.n_experts + 4) * 4) + 3 * 256 + align256((size_t)slots * imax * 4) + img + 256 +
                       2 * align256((size_t)c.hidden * 4);
     if (hipMalloc(&m->dense, dpl * c.n_layers) != hipSuccess || hipMalloc(&m->tables, tab * c.n_layers) != hipSuccess ||
         hipMalloc(&m->ws_mem, ws) != hipSuccess) {
@@ -1434,8 +1435,6 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
     m->ws.weights = reinterpret_cast<float*>(w);
     w += 256;
     m->ws.gate = reinterpret_cast<float*>(w);
-    w += 256;
-    m->ws.img_e = reinterpret_cast<int32_t*>(w);
     w += 256;
     m->ws.act = reinterpret_cast<float*>(w);
     w += align256((size_t)slots * imax * 4);

@@ -405,9 +405,12 @@ __device__ __forceinline__ void a_pos(uint32_t c, uint32_t& tau, uint32_t& off, 
     }
 }
 
-// The x image of x (cols columns in LDS, cols a multiple of 8; the image
-// columns past cols are zero) with E = 0, built by one wave straight into img
-// (LDS): lane l takes chunks l, l + 64, ... of 8 columns; each unit (SXG
+// The x image of x (cols columns, cols a multiple of 8; the image columns
+// past cols are zero) with E = 0, or the part of it in chunks [cb, ce) of 8
+// columns (whole steps), built by one wave straight into `tiles` (the A tiles
+// from the range's first step on) and `sx` (the unit entries from the
+// range's first unit on), in LDS or global memory: lane l takes chunks cb + l,
+// cb + l + 64, ...; each unit (SXG
 // columns = NL consecutive lanes) has E_u = 23 - exponent of its max (at most
 // 100, so f_u = 2^-E_u is a normal float; 0 for an all-zero unit), and every
 // column's limbs of X = rint(x 2^E_u) are stored as bytes at their tile
@@ -415,17 +418,18 @@ __device__ __forceinline__ void a_pos(uint32_t c, uint32_t& tau, uint32_t& off, 
 // divided by its 2^E (every scale a power of two times the same roundings),
 // so a dot product on this image is x_image's times 2^-E exactly: no
 // whole-vector maximum, no gather pass.  A non-finite value zeroes its unit
-// and sets *nonfinite.  Only this wave's LDS is touched (no barrier).
+// and sets *nonfinite.  Touches only the image range it builds (no barrier).
 template <int KIND>
-__device__ void image_wave(uint32_t lane, const float* x, uint32_t cols, uint32_t steps, uint8_t* img,
-                           bool* nonfinite) {
+__device__ void image_wave(uint32_t lane, const float* x, uint32_t cols, uint8_t* tiles, float* sx, uint32_t cb,
+                           uint32_t ce, bool* nonfinite) {
     constexpr int P = Kcfg<KIND>::P, SC = Kcfg<KIND>::STEP_COLS, NL = Kcfg<KIND>::SXG / 8;
-    float* SX = reinterpret_cast<float*>(img + (size_t)steps * P * A_TILE_STRIDE);
-    for (uint32_t i = lane; i < steps * (uint32_t)P; i += 64u)
-        *reinterpret_cast<uint4*>(img + (size_t)i * A_TILE_STRIDE + 256u) = make_uint4(0u, 0u, 0u, 0u);
+    const uint32_t tau0 = cb * 8u / SC * P;
+    // the tile zero blocks of the steps in range
+    for (uint32_t i = lane; i < (ce - cb) * 8u / SC * P; i += 64u)
+        *reinterpret_cast<uint4*>(tiles + (size_t)i * A_TILE_STRIDE + 256u) = make_uint4(0u, 0u, 0u, 0u);
     bool any_bad = false;
-    // a unit's NL chunks are NL consecutive lanes, active together (the chunk count is a multiple of NL)
-    for (uint32_t ch = lane; ch < steps * (uint32_t)SC / 8u; ch += 64u) {
+    // a unit's NL chunks are NL consecutive lanes, active together (ranges are whole steps)
+    for (uint32_t ch = cb + lane; ch < ce; ch += 64u) {
         float4 v[2];
         load_chunk(x, 8u * ch, cols, v);
         float m = group_max<NL>(max_abs8(v));
@@ -444,12 +448,12 @@ __device__ void image_wave(uint32_t lane, const float* x, uint32_t cols, uint32_
         if constexpr (KIND == HK_MIXED) {
             const int32_t s3 = group_sum<NL>((int32_t)f[6] + (int32_t)f[7]);
             if ((ch & (uint32_t)(NL - 1)) == 0)
-                reinterpret_cast<float4*>(SX)[ch / (uint32_t)NL] =
+                reinterpret_cast<float4*>(sx)[(ch - cb) / (uint32_t)NL] =
                     make_float4((float)s * fu, (float)(3 * s - 4 * s3) * 0.5f * fu, Kcfg<KIND>::ALPHA * fu,
                                 0.5f * Kcfg<KIND>::ALPHA * fu);
         } else {
             if ((ch & (uint32_t)(NL - 1)) == 0)
-                reinterpret_cast<float2*>(SX)[ch / (uint32_t)NL] =
+                reinterpret_cast<float2*>(sx)[(ch - cb) / (uint32_t)NL] =
                     make_float2(Kcfg<KIND>::ALPHA * fu, Kcfg<KIND>::BETA * (float)s * fu);
         }
 #pragma unroll
@@ -459,7 +463,7 @@ __device__ void image_wave(uint32_t lane, const float* x, uint32_t cols, uint32_
             a_pos<KIND>(8u * ch + (uint32_t)e, tau, off, sh);
             // signed base-256 limbs of the scaled value
             const uint32_t z = ((uint32_t)((int32_t)f[e] * (1 << sh)) + 0x80808080u) ^ 0x80808080u;
-            uint8_t* p = img + (size_t)tau * A_TILE_STRIDE + off;
+            uint8_t* p = tiles + (size_t)(tau - tau0) * A_TILE_STRIDE + off;
             p[0] = (uint8_t)z;
             p[16] = (uint8_t)(z >> 8);
             p[32] = (uint8_t)(z >> 16);

@@ -48,14 +48,14 @@ struct MoeWs {
     float* weights;    // [K]
     float* gate;       // [2]: shared-gate logit, shared-gate value
     float* act;        // [(K+1) * Imax]
-    uint8_t* img;      // x image of RMSNorm(h) for the gate/up organs
-    int32_t* img_e;    // [1]: its exponent E
+    uint8_t* img;      // x image (E = 0) of RMSNorm(h) for the gate/up organs
     uint32_t* status;  // device error bits
 };
 
 // Bytes of the gate/up x image and of the down kernel's LDS.
 size_t moe_img_bytes(int kind, uint32_t H);
 size_t moe_down_lds_bytes(int kind, uint32_t Imax, uint32_t slots);
+size_t moe_route_lds_bytes(int kind, uint32_t H);
 size_t moe_gate_up_lds_bytes(int kind, uint32_t H);
 
 // The expert block for caller routes (d.K = n_routes, d.has_shared = the

@@ -8,8 +8,8 @@
 //   1. route:   every block recomputes xn = RMSNorm(1+w)(h) in LDS; blocks
 //               0..ceil(E/4)-1 compute the router logits (one row per wave),
 //               the next block also the shared-gate logit, and the blocks
-//               from there build the x image of xn (fixed-point limb tiles,
-//               once per layer), 512 columns each.
+//               from there build the x image of xn (fixed-point limb tiles
+//               with E = 0, once per layer), 512 columns per wave.
 //   2. gate/up: one workgroup per (16-row tile, slot); each runs softmax /
 //               top-k / renormalise over the logits itself to find its
 //               slot's expert (slot K = the shared expert), then its 4 waves
@@ -36,6 +36,9 @@ size_t moe_gate_up_lds_bytes(int kind, uint32_t H) { return moe_img_bytes(kind, 
 
 // Floats of x staging for an image of `cols` columns (cols rounded up to whole steps).
 static uint32_t stage_floats(int kind, uint32_t cols) { return n_steps_for(kind, cols) * tile_step_cols(kind); }
+
+// The route kernel's LDS: xn (whole steps).
+size_t moe_route_lds_bytes(int kind, uint32_t H) { return (size_t)stage_floats(kind, H) * sizeof(float); }
 
 size_t moe_down_lds_bytes(int kind, uint32_t Imax, uint32_t slots) {
     return (size_t)slots * (moe_img_bytes(kind, Imax) + 16 * sizeof(float) + (size_t)stage_floats(kind, Imax) * sizeof(float));
@@ -66,25 +69,26 @@ __global__ void __launch_bounds__(256) moe_route_kernel(MoeDims d, MoeLayerDev L
     } else if (blockIdx.x == nrb && wave == 0) {
         wrow = L.gate_w;
     }
-    const float4* w4 = reinterpret_cast<const float4*>(wrow);
-    float4 wv[ROW_PRE];
-#pragma unroll
-    for (int k = 0; k < ROW_PRE; ++k) {
-        const uint32_t j = (uint32_t)lane + 64u * k;
-        wv[k] = (wrow && j < n4) ? w4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    // every load is unconditional (indices clamped to the vector, values past
+    // it dropped afterwards): a load under a per-lane condition makes the
+    // compiler wait for it before the next one issues.  h and the norm
+    // weight come first, so the RMSNorm waits for them only.
     const float4* h4 = reinterpret_cast<const float4*>(h);
     const float4* g4 = reinterpret_cast<const float4*>(L.norm_w);
     float4 hv[H_PRE], gv[H_PRE];
-    float ss = 0.f;
 #pragma unroll
     for (int k = 0; k < H_PRE; ++k) {
-        const uint32_t j = threadIdx.x + 256u * k;
-        hv[k] = j < n4 ? h4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
-        gv[k] = j < n4 ? g4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const uint32_t j = min(threadIdx.x + 256u * k, n4 - 1u);
+        hv[k] = ldg(h4 + j);
+        gv[k] = ldg(g4 + j);
     }
+    const float4* w4 = reinterpret_cast<const float4*>(wrow ? wrow : L.router_w);
+    float4 wv[ROW_PRE];
 #pragma unroll
-    for (int k = 0; k < H_PRE; ++k) ss += dot4(hv[k], hv[k]);
+    for (int k = 0; k < ROW_PRE; ++k) wv[k] = ldg(w4 + min((uint32_t)lane + 64u * k, n4 - 1u));
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < H_PRE; ++k) ss += threadIdx.x + 256u * k < n4 ? dot4(hv[k], hv[k]) : 0.0f;
     // xn = RMSNorm(1+w)(h) = h * (mean(h^2) + eps)^-1/2 * (1 + w)
     const float inv = 1.0f / sqrtf(block_sum(ss, red) / (float)d.H + d.eps);
     float4* x4 = reinterpret_cast<float4*>(xn);
@@ -113,17 +117,20 @@ __global__ void __launch_bounds__(256) moe_route_kernel(MoeDims d, MoeLayerDev L
         }
     }
     if (blockIdx.x >= nrb) {
-        // the x image of xn for every gate/up organ of this layer, 512 columns
-        // per block (xn quantized in place)
-        bool bad = false;
-        const uint32_t S = n_steps_for(KIND, d.H), spb = 512u / tile_step_cols(KIND), tb = (blockIdx.x - nrb) * spb;
-        XChunks<1> xc;
-        load_x<1>(BlockTeam{}, xn, d.H, xc);
-        const int E = x_image<KIND, 1>(BlockTeam{}, xc, xn, d.H, S, ws.img, xn + tb * tile_step_cols(KIND),
-                                       8u * blockDim.x, red, &bad, tb, tb + spb);
-        if (threadIdx.x == 0) {
-            if (blockIdx.x == nrb) ws.img_e[0] = E;
-            if (bad) atomicOr(ws.status, HK_DEVERR_NONFINITE);
+        // the x image of xn (E = 0) for every gate/up organ of this layer:
+        // 512 columns per wave, limb bytes stored straight to their tiles
+        // (measured faster than staging the part in LDS for 16-byte stores)
+        const uint32_t S = n_steps_for(KIND, d.H), nch = S * tile_step_cols(KIND) / 8u;
+        const uint32_t cb = ((blockIdx.x - nrb) * 4u + wave) * 64u;
+        if (cb < nch) {
+            constexpr uint32_t TB = 512u / Kcfg<KIND>::STEP_COLS * Kcfg<KIND>::P * A_TILE_STRIDE;  // tile bytes per wave
+            constexpr uint32_t SB = 512u / Kcfg<KIND>::SXG * Kcfg<KIND>::SXW * 4u;                // unit bytes per wave
+            bool bad = false;
+            image_wave<KIND>((uint32_t)lane, xn, d.H, ws.img + (size_t)(cb / 64u) * TB,
+                             reinterpret_cast<float*>(ws.img + (size_t)S * Kcfg<KIND>::P * A_TILE_STRIDE +
+                                                      (size_t)(cb / 64u) * SB),
+                             cb, min(cb + 64u, nch), &bad);
+            if (__ballot(bad) != 0 && lane == 0) atomicOr(ws.status, HK_DEVERR_NONFINITE);
         }
     }
 }
@@ -187,7 +194,7 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev
             fetch_one<KIND, 2>(u, T, s0 + k, lane, f[k], 1);
         }
     }
-    const int E = ws.img_e[0];
+    const int E = 0;  // the route kernel's image is built with E = 0
     const ImageA A{lds, a_lane_offset(lane)};
     const float* SX = reinterpret_cast<const float*>(lds + (size_t)S * Kcfg<KIND>::P * A_TILE_STRIDE);
     float acc[2] = {0.0f, 0.0f};
@@ -263,7 +270,9 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, MoeLayerDev L
     const float wgt = !active ? 0.0f : (slot < d.K ? wts[slot] : ws.gate[1]);
     if (active) {
         bool bad = false;
-        image_wave<KIND>((uint32_t)lane, xs, o.cols, S, img, &bad);
+        image_wave<KIND>((uint32_t)lane, xs, o.cols, img,
+                         reinterpret_cast<float*>(img + (size_t)S * Kcfg<KIND>::P * A_TILE_STRIDE), 0u,
+                         S * tile_step_cols(KIND) / 8u, &bad);
         if (__ballot(bad) != 0 && lane == 0) atomicOr(ws.status, HK_DEVERR_NONFINITE);
     }
     const ImageA A{img, a_lane_offset(lane)};
@@ -418,9 +427,9 @@ static hipError_t launch_layer(const MoeDims& d, const MoeLayerDev& L, const flo
     const uint32_t slots = d.K + (d.has_shared ? 1u : 0u);
     const uint32_t gu_tiles = n_tiles_for(d.has_shared ? max(d.I, d.SI) : d.I);
     const uint32_t img_stride = (uint32_t)moe_img_bytes(KIND, d.Imax);
-    const uint32_t nib = (d.H + 511u) / 512u;  // image blocks, 512 columns each
-    hipLaunchKernelGGL(moe_route_kernel<KIND>, dim3(nrb + nib), dim3(256), (size_t)stage_floats(KIND, d.H) * sizeof(float),
-                       s, d, L, h_in, ws);
+    const uint32_t nib = (n_steps_for(KIND, d.H) * tile_step_cols(KIND) + 2047u) / 2048u;  // image blocks, 2048 columns each
+    hipLaunchKernelGGL(moe_route_kernel<KIND>, dim3(nrb + nib), dim3(256), moe_route_lds_bytes(KIND, d.H), s, d, L,
+                       h_in, ws);
     const dim3 gg(gu_tiles, slots);
     const size_t gl = moe_gate_up_lds_bytes(KIND, d.H);
     if (d.E <= 512)
