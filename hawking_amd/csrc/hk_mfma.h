@@ -180,13 +180,14 @@ struct XChunks {
     float4 v[NC][2];
 };
 
+// The load is unconditional (a chunk past cols re-reads the last one and is
+// zeroed after): a load under a per-lane condition would wait for the one
+// before it.
 __device__ __forceinline__ void load_chunk(const float* x, uint32_t c0, uint32_t cols, float4* v) {
-    if (c0 < cols) {
-        v[0] = *reinterpret_cast<const float4*>(x + c0);
-        v[1] = *reinterpret_cast<const float4*>(x + c0 + 4);
-    } else {
-        v[0] = v[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
+    const uint32_t c = min(c0, cols - 8u);
+    v[0] = *reinterpret_cast<const float4*>(x + c);
+    v[1] = *reinterpret_cast<const float4*>(x + c + 4);
+    if (c0 >= cols) v[0] = v[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
 template <int NC, class Team>

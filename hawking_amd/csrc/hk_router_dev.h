@@ -218,16 +218,20 @@ struct TopkLds {
 // rounds of a wave-wide key max.  Returns, in lane r < k, the r-th selection
 // (id, weight); ids_out / w_out (if not null) get all k.
 template <int NPL>
-__device__ ArgBest softmax_topk_wave(const float* __restrict__ logits, uint32_t n, uint32_t k, int renorm,
+__device__ __forceinline__ ArgBest softmax_topk_wave(const float* __restrict__ logits, uint32_t n, uint32_t k, int renorm,
                                      int32_t* ids_out, float* w_out, uint32_t* status, TopkLds* t) {
     const int lane = threadIdx.x & 63;
     float p[NPL];
     float m = -INFINITY;
     uint32_t bad = 0;
+    // unconditional loads (index clamped, value dropped past n): a load under
+    // a per-lane condition would wait for the one before it
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) p[j] = logits[min((uint32_t)lane + 64u * j, n - 1u)];
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
         const uint32_t i = (uint32_t)lane + 64u * j;
-        p[j] = i < n ? logits[i] : -INFINITY;
+        p[j] = i < n ? p[j] : -INFINITY;
         if (i < n && !isfinite(p[j])) bad = 1;
         m = fmaxf(m, p[j]);
     }
