@@ -158,6 +158,7 @@ PROTOTYPES = {
     "hk_moe_expert_bytes": (C.c_int, [_p, _u32, _u32, C.POINTER(_sz)]),
     "hk_moe_decode_layer": (C.c_int, [_p, _p, _u32, _p, _p, _p, _p, _p]),
     "hk_moe_decode_stack": (C.c_int, [_p, _p, _p, _p, _p, _p, _p]),
+    "hk_moe_decode_stack_persistent": (C.c_int, [_p, _p, _p]),
     "hk_moe_forward_batch": (C.c_int, [_p, _p, _u32, _p, _u32, _p, _p, _p, _p]),
     "hk_moe15_layer_create": (C.c_int, [_p, C.POINTER(Moe15LayerSrc), C.POINTER(_p)]),
     "hk_moe15_layer_free": (C.c_int, [_p, _p]),

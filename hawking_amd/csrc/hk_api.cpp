@@ -9,6 +9,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -1275,6 +1276,15 @@ struct hk_moe_model {
     void* bws_mem = nullptr;
     uint32_t bws_tokens = 0;
     hk::MoeBatchWs bws{};
+    // persistent decode (softmax models): per-layer descriptors on the device,
+    // the flag-tagged hand-off words (every layer its own) and the next
+    // launch's tag
+    hk::MoeLayerDev* ldev = nullptr;
+    void* stack_mem = nullptr;
+    size_t stack_bytes = 0;
+    hk::StackArgs st{};  // the buffer pointers and strides (per-call fields unset)
+    uint32_t tag = 1;
+    int cu_count = 0;
 };
 
 // Per layer: norm weight [H], router [E x H], shared-expert gate [H], router bias [E].
@@ -1352,6 +1362,68 @@ static int alloc_batch_ws(hk_ctx* ctx, hk_moe_model* m) {
     w.aimg_stride = (uint32_t)as;
     w.status = ctx->dev_status;
     m->bws_tokens = T;
+    return HK_OK;
+}
+
+// Layer l's descriptor for the persistent decode (after the layer is set).
+static int upload_ldev(hk_ctx* ctx, hk_moe_model* m, uint32_t l) {
+    if (!m->ldev) return HK_OK;
+    const MoeLayerHost& L = m->layers[l];
+    const hk::MoeLayerDev d{L.norm_w, L.router_w, (m->cfg.shared_gate && m->cfg.shared_inter) ? L.gate_w : nullptr,
+                            L.table_dev, L.stride};
+    return check_hip(ctx, hipMemcpy(m->ldev + l, &d, sizeof d, hipMemcpyHostToDevice), "layer descriptor upload");
+}
+
+// The persistent decode's buffers (zeroed: tag 0 is never waited for).  The
+// The persistent decode's hand-off words: per layer, h [H], the logits
+// [E + 1] and the activations [slots x Imax], then RDY_REP replicas of each
+// ready array (down tiles of H, route blocks, gate/up tiles x slots).  Every
+// array starts on a 256-byte boundary; replicas are an odd number of
+// 256-byte units apart so that they fall in different memory channels.
+// About (8 (H + E + slots Imax) + 24 (tiles + blocks) RDY_REP) bytes a layer.
+static int alloc_stack(hk_ctx* ctx, hk_moe_model* m) {
+    const hk_moe_config& c = m->cfg;
+    const uint32_t slots = c.top_k + (c.shared_inter ? 1u : 0u), imax = std::max(c.inter, c.shared_inter);
+    const uint32_t gu_tiles = n_tiles_for(c.shared_inter ? imax : c.inter);
+    auto words = [](size_t n) { return (uint32_t)((n + 31) / 32 * 32); };       // 256-byte units
+    auto rstride = [&](size_t n) { return words(n) | 32u; };                   // odd number of units
+    hk::StackArgs& a = m->st;
+    a.hs = words(c.hidden);
+    a.ls = words((size_t)c.n_experts + 1);
+    a.as = words((size_t)slots * imax);
+    a.hrs = rstride(n_tiles_for(c.hidden));
+    a.lrs = rstride((size_t)c.n_experts / 4 + 2);
+    a.ars = rstride((size_t)slots * gu_tiles);
+    const size_t per_layer = (size_t)a.hs + a.ls + a.as + (size_t)hk::RDY_REP * (a.hrs + a.lrs + a.ars);
+    m->stack_bytes = (per_layer * c.n_layers + 32) * 8;
+    int cu = 0;
+    if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, ctx->device) != hipSuccess)
+        return set_error(ctx, HK_E_HIP, "hipDeviceGetAttribute (CU count)");
+    m->cu_count = cu;
+    if (hipMalloc(&m->ldev, (size_t)c.n_layers * sizeof(hk::MoeLayerDev)) != hipSuccess ||
+        hipMalloc(&m->stack_mem, m->stack_bytes) != hipSuccess) {
+        if (m->ldev) (void)hipFree(m->ldev);
+        m->ldev = nullptr;
+        m->stack_mem = nullptr;
+        return set_error(ctx, HK_E_NOMEM, "persistent decode buffers: allocation failed");
+    }
+    if (hipMemset(m->stack_mem, 0, m->stack_bytes) != hipSuccess ||
+        hipMemset(m->ldev, 0, (size_t)c.n_layers * sizeof(hk::MoeLayerDev)) != hipSuccess) {
+        (void)hipFree(m->ldev);
+        (void)hipFree(m->stack_mem);
+        m->ldev = nullptr;
+        m->stack_mem = nullptr;
+        return set_error(ctx, HK_E_HIP, "persistent decode buffers: clear failed");
+    }
+    uint64_t* p = static_cast<uint64_t*>(m->stack_mem);
+    const size_t L = c.n_layers;
+    a.h = p;
+    a.logits = a.h + L * a.hs;
+    a.act = a.logits + L * a.ls;
+    a.h_rdy = a.act + L * a.as;
+    a.l_rdy = a.h_rdy + L * hk::RDY_REP * a.hrs;
+    a.a_rdy = a.l_rdy + L * hk::RDY_REP * a.lrs;
+    a.abort = reinterpret_cast<uint32_t*>(a.a_rdy + L * hk::RDY_REP * a.ars);
     return HK_OK;
 }
 
@@ -1445,6 +1517,13 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
     w += align256((size_t)c.hidden * 4);
     m->hbuf[1] = reinterpret_cast<float*>(w);
     m->ws.status = ctx->dev_status;
+    if (c.router == HK_ROUTER_SOFTMAX && (rc = alloc_stack(ctx, m))) {
+        (void)hipFree(m->dense);
+        (void)hipFree(m->tables);
+        (void)hipFree(m->ws_mem);
+        delete m;
+        return rc;
+    }
     if (c.router == HK_ROUTER_NOAUX_TC && (rc = alloc_batch_ws(ctx, m))) {
         (void)hipFree(m->dense);
         (void)hipFree(m->tables);
@@ -1466,6 +1545,8 @@ extern "C" int hk_moe_model_free(hk_ctx* ctx, hk_moe_model* m) {
     (void)hipFree(m->tables);
     (void)hipFree(m->ws_mem);
     if (m->bws_mem) (void)hipFree(m->bws_mem);
+    if (m->ldev) (void)hipFree(m->ldev);
+    if (m->stack_mem) (void)hipFree(m->stack_mem);
     delete m;
     return HK_OK;
 }
@@ -1606,6 +1687,8 @@ extern "C" int hk_moe_model_set_layer(hk_ctx* ctx, hk_moe_model* m, uint32_t lay
     if (!rc) rc = check_hip(ctx, hipStreamSynchronize(st), "hipStreamSynchronize (layer upload)");
     if (rc) return rc;
     L.ready = true;
+    rc = upload_ldev(ctx, m, layer);
+    if (rc) return rc;
     return HK_OK;
 }
 
@@ -1715,6 +1798,7 @@ extern "C" int hk_moe_model_fill_synthetic(hk_ctx* ctx, hk_moe_model* m, uint64_
                                 "expert synth");
         if (!rc) rc = repack_layer(ctx, L, canon, nbin, c.n_experts, st);
         if (!rc) L.ready = true;
+        if (!rc) rc = upload_ldev(ctx, m, l);
     }
     uint32_t badv = 0;
     if (!rc) rc = check_hip(ctx, hipMemcpyAsync(&badv, bad, 4, hipMemcpyDeviceToHost, st), "flag read");
@@ -1771,6 +1855,43 @@ extern "C" int hk_moe_decode_layer(hk_ctx* ctx, hk_moe_model* m, uint32_t layer,
                      "moe layer launch");
 }
 
+// The persistent launch is opt-in (HK_MOE_PERSISTENT=1): at config-4 shapes
+// its hand-offs still cost more than the per-layer launch boundaries.
+static bool stack_enabled(const hk_moe_model* m) {
+    const char* pe = std::getenv("HK_MOE_PERSISTENT");
+    return m->ldev && pe && pe[0] == '1';
+}
+
+static hk::StackArgs stack_args(hk_ctx* ctx, hk_moe_model* m, const float* h_in, float* h_out, int32_t* ids,
+                                float* weights) {
+    hk::StackArgs a = m->st;
+    a.d = m->dims;
+    a.layers = m->ldev;
+    a.n_layers = m->cfg.n_layers;
+    a.tag = m->tag;
+    a.h_in = h_in;
+    a.h_out = h_out;
+    a.ids = ids;
+    a.weights = weights;
+    a.status = ctx->dev_status;
+    a.gu_tiles = n_tiles_for(m->dims.has_shared ? std::max(m->dims.I, m->dims.SI) : m->dims.I);
+    a.ng = a.gu_tiles * (m->dims.K + (m->dims.has_shared ? 1u : 0u));
+    return a;
+}
+
+extern "C" int hk_moe_decode_stack_persistent(hk_ctx* ctx, hk_moe_model* m, int* persistent) {
+    if (!ctx || !m || !persistent) return HK_E_INVALID_ARG;
+    *persistent = 0;
+    if (m->cfg.router != HK_ROUTER_SOFTMAX || !stack_enabled(m)) return HK_OK;
+    bool fits = false;
+    const hk::StackArgs a = stack_args(ctx, m, nullptr, nullptr, nullptr, nullptr);
+    int rc = check_hip(ctx, launch_moe_stack(m->cfg.expert_kind, a, m->cu_count, nullptr, &fits, false),
+                       "persistent decode check");
+    if (rc) return rc;
+    *persistent = fits ? 1 : 0;
+    return HK_OK;
+}
+
 extern "C" int hk_moe_decode_stack(hk_ctx* ctx, hk_moe_model* m, const float* h_in, float* h_out, int32_t* ids,
                                    float* weights, hk_stream stream) {
     if (!ctx || !m) return HK_E_INVALID_ARG;
@@ -1782,6 +1903,23 @@ extern "C" int hk_moe_decode_stack(hk_ctx* ctx, hk_moe_model* m, const float* h_
     const uint32_t n = m->cfg.n_layers, K = m->cfg.top_k;
     for (uint32_t l = 0; l < n; ++l)
         if (!m->layers[l].ready) return set_error(ctx, HK_E_INVALID_ARG, "layer " + std::to_string(l) + " has no weights");
+    // the whole token in one persistent launch when enabled and its grid can
+    // be resident
+    if (stack_enabled(m)) {
+        if (m->tag > 0xF0000000u) {  // tags never wrap: clear the words and restart
+            int rc = check_hip(ctx, hipMemsetAsync(m->stack_mem, 0, m->stack_bytes, st), "hand-off clear");
+            if (rc) return rc;
+            m->tag = 1;
+        }
+        hk::StackArgs a = stack_args(ctx, m, h_in, h_out, ids, weights);
+        bool fits = false;
+        int rc = check_hip(ctx, launch_moe_stack(m->cfg.expert_kind, a, m->cu_count, st, &fits), "persistent decode launch");
+        if (rc) return rc;
+        if (fits) {
+            m->tag += 1;
+            return HK_OK;
+        }
+    }
     const float* cur = h_in;
     for (uint32_t l = 0; l < n; ++l) {
         MoeLayerDev L;

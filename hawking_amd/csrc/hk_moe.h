@@ -64,6 +64,44 @@ size_t moe_block_gate_up_lds_bytes(int kind, uint32_t H);
 hipError_t launch_moe_block(int kind, const MoeDims& d, const MoeLayerDev& L, const int32_t* route_ids,
                             const float* route_weights, const float* x, float* out, const MoeWs& ws, hipStream_t s);
 
+// Every layer of a token in one persistent cooperative launch (hk_moe_stack.hip).
+// Hand-off buffers are flag-tagged 64-bit words {value, tag}, one set per
+// layer, all carrying the launch's tag.  Blocks: (E + 3) / 4 + 1 route,
+// ng = gu_tiles * slots gate/up, n_tiles(H) down.
+constexpr uint32_t RDY_REP = 8;  // replicas of each ready word (readers spread over them)
+
+struct StackArgs {
+    MoeDims d;
+    const MoeLayerDev* layers;  // [n_layers], device
+    uint32_t n_layers;
+    uint32_t tag;       // this launch's tag (every hand-off word of the launch carries it)
+    const float* h_in;
+    float* h_out;
+    int32_t* ids;       // [n_layers * K] or null
+    float* weights;     // [n_layers * K] or null
+    uint32_t* status;
+    // hand-off words {value bits, tag}, every layer its own (layer l at l * stride)
+    uint64_t* h;        // [H]: the layer's input h
+    uint64_t* logits;   // [E + 1]: router logits, then the shared-gate logit
+    uint64_t* act;      // [slots * Imax]
+    uint32_t hs, ls, as;
+    // ready words (value unused), RDY_REP replicas per layer (replica r of
+    // layer l at (l RDY_REP + r) * stride): one per producer, stored after
+    // its outputs; a reader polls these first and then reads the outputs
+    // once (the outputs' own tags decide)
+    uint64_t* h_rdy;    // [n_tiles(H)]: down tile T wrote its rows of the layer's h
+    uint64_t* l_rdy;    // [E/4 + 1]: route block b wrote its logits
+    uint64_t* a_rdy;    // [slots * gu_tiles]: gate/up tile T of a slot wrote its activations
+    uint32_t hrs, lrs, ars;
+    uint32_t* abort;    // the tag of a launch whose wait ran out
+    uint32_t ng, gu_tiles;
+};
+size_t moe_stack_lds_bytes(int kind, const MoeDims& d);
+// *fits = false (nothing launched) when the grid cannot be resident at once
+// or the shape is outside the kernel's limits; the caller then uses the
+// per-layer launches.  launch = false only answers *fits.
+hipError_t launch_moe_stack(int kind, const StackArgs& a, int cu_count, hipStream_t s, bool* fits, bool launch = true);
+
 // ids_out / w_out (device, top_k each) may be null.
 hipError_t launch_moe_layer(int kind, const MoeDims& d, const MoeLayerDev& L, const float* h_in,
                             float* h_out, const MoeWs& ws, int32_t* ids_out, float* w_out, hipStream_t s);

@@ -10,6 +10,7 @@ namespace hk {
 // invalid data (read back by hk_check_device_status).
 constexpr uint32_t HK_DEVERR_NONFINITE = 1u;
 constexpr uint32_t HK_DEVERR_ROUTE = 2u;
+constexpr uint32_t HK_DEVERR_STALL = 4u;  // a persistent decode launch gave up waiting for a hand-off
 
 hipError_t launch_softmax_topk(const float* logits, uint32_t n_tokens, uint32_t n, uint32_t k,
                                float tie_eps, int renorm, int32_t* ids, float* weights,

@@ -219,8 +219,8 @@ struct TopkLds {
 // (id, weight); ids_out / w_out (if not null) get all k.
 template <int NPL>
 __device__ __forceinline__ ArgBest softmax_topk_wave(const float* __restrict__ logits, uint32_t n, uint32_t k, int renorm,
-                                     int32_t* ids_out, float* w_out, uint32_t* status, TopkLds* t) {
-    const int lane = threadIdx.x & 63;
+                                     int32_t* ids_out, float* w_out, uint32_t* status, TopkLds* t,
+                                     int lane = (int)(threadIdx.x & 63)) {
     float p[NPL];
     float m = -INFINITY;
     uint32_t bad = 0;

@@ -184,6 +184,12 @@ class MoeModel:
                       _pp(ids), _pp(weights),
                       stream if stream is not None else self.ctx.stream)
 
+    def stack_is_persistent(self) -> bool:
+        """Whether decode_stack runs as one persistent launch here (hk_moe_decode_stack_persistent)."""
+        v = C.c_int(0)
+        self.ctx.call("hk_moe_decode_stack_persistent", self.h, C.byref(v))
+        return bool(v.value)
+
     def moe_block_device(self, layer: int, route_ids: DeviceArray, route_weights: DeviceArray, n_routes: int,
                          x: DeviceArray, out: DeviceArray, include_shared: bool = True, stream=None) -> None:
         """BackendMoe::moe_block: out += sum_r w_r mlp_r(x) (+ g mlp_shared(x)),

@@ -92,7 +92,7 @@ int hk_event_record(hk_ctx* ctx, void* event, hk_stream stream);
 int hk_event_elapsed_ms(hk_ctx* ctx, void* start, void* stop, float* ms);
 /* Synchronises `stream`, returns and clears the device error bits that
  * kernels set when they meet invalid data (1 = non-finite input, 2 = invalid
- * route).  The GPU-side counterpart of the reference's per-op Result
+ * route, 4 = a persistent decode launch gave up waiting for a hand-off).  The GPU-side counterpart of the reference's per-op Result
  * checks, which cannot be returned from stream-ordered launches. */
 int hk_check_device_status(hk_ctx* ctx, hk_stream stream, uint32_t* bits);
 
@@ -484,9 +484,19 @@ int hk_moe_decode_layer(hk_ctx* ctx, hk_moe_model* model, uint32_t layer, const 
                         float* h_out, int32_t* ids, float* weights, hk_stream stream);
 /* All layers for one token: h_{l+1} = moe_layer_l(h_l) (forward_token's MoE
  * suffixes, model/qwen80_mixed_hybrid_decode.rs:4682-4736, without the
- * attention mixers).  ids/weights may be NULL or [n_layers*top_k]. */
+ * attention mixers).  ids/weights may be NULL or [n_layers*top_k].  Runs as
+ * three launches per layer, or, with environment HK_MOE_PERSISTENT=1, as one
+ * persistent cooperative launch (the reference's one command buffer per
+ * token) when the model's grid fits the device at once (hidden <= 2048,
+ * n_experts <= 512, intermediate <= 2048, top_k + shared <= 12); both give
+ * the same bits.  A hand-off the persistent launch waited for too long sets
+ * device status bit 4 (the output is then undefined). */
 int hk_moe_decode_stack(hk_ctx* ctx, hk_moe_model* model, const float* h_in, float* h_out,
                         int32_t* ids, float* weights, hk_stream stream);
+/* *persistent = 1 when hk_moe_decode_stack on this model runs as one
+ * persistent launch (enabled and admitted), 0 when it uses per-layer launches.  Diagnostic with no
+ * counterpart in the reference (its token is one command buffer). */
+int hk_moe_decode_stack_persistent(hk_ctx* ctx, hk_moe_model* model, int* persistent);
 
 /* BackendMoe::moe_block (backend/mod.rs:509-521) on one layer of a model:
  * the routed (and optional shared) expert block for CALLER-supplied routes,

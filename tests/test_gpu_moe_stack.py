@@ -1,0 +1,93 @@
+"""The persistent decode (hk_moe_decode_stack as one cooperative launch with
+flag-tagged hand-offs, HK_MOE_PERSISTENT=1) against the per-layer launches: the same bits, layer
+ids and weights, over repeated calls (the tags advance), and the same status
+bits for a non-finite hidden state.  The per-layer path itself is checked
+against the oracle in test_gpu_moe.py / test_gpu_c4_stack.py."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from tests import hk_testutil as U
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[gpu-case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from hawking_amd.runtime import Context
+    return Context(0)
+
+
+SHAPES = [
+    # (label, n_layers, hidden, inter, shared_inter, experts, top_k, kind, group, shared_gate)
+    ("config4-geometry", 4, 2048, 512, 512, 512, 10, U.HK_MIXED, 128, True),
+    ("config3-geometry", 3, 2048, 512, 512, 512, 10, U.HK_Q4, 32, True),
+    ("small-mixed-no-shared", 3, 512, 384, 0, 32, 5, U.HK_MIXED, 128, False),
+    ("small-q4-wide-ungated-shared", 3, 512, 128, 256, 64, 6, U.HK_Q4, 64, False),
+]
+
+
+def run_mode(m, hd, persistent):
+    """One token with the persistent launch (HK_MOE_PERSISTENT=1) or the
+    per-layer launches (the default)."""
+    os.environ["HK_MOE_PERSISTENT"] = "1" if persistent else "0"
+    try:
+        return m.forward_token(hd)
+    finally:
+        del os.environ["HK_MOE_PERSISTENT"]
+
+
+def admitted(m):
+    os.environ["HK_MOE_PERSISTENT"] = "1"
+    try:
+        return m.stack_is_persistent()
+    finally:
+        del os.environ["HK_MOE_PERSISTENT"]
+
+
+@pytest.mark.parametrize("label,n,H,I,SI,E,K,kind,group,gate", SHAPES)
+def test_persistent_stack_bit_exact_vs_per_layer(ctx, label, n, H, I, SI, E, K, kind, group, gate):
+    from hawking_amd.moe import MoeModel, MoeShape
+    say("persistent stack", label)
+    shape = MoeShape(n_layers=n, hidden=H, inter=I, shared_inter=SI, n_experts=E, top_k=K, expert_kind=kind,
+                     expert_group=group, shared_gate=gate)
+    m = MoeModel(ctx, shape)
+    m.fill_synthetic(U.SEED + n)
+    assert admitted(m), "the persistent launch must be admitted for this shape"
+    ctx.device_status()  # clear
+    rng = np.random.default_rng(7)
+    for call in range(3):  # the tags advance from call to call
+        h = rng.standard_normal(H).astype(np.float32) * (1.0 + call)
+        out, ids, w = run_mode(m, h, True)
+        rout, rids, rw = run_mode(m, h, False)
+        assert np.array_equal(ids, rids), (label, call)
+        assert np.array_equal(w.view(np.uint32), rw.view(np.uint32)), (label, call)
+        assert np.array_equal(out.view(np.uint32), rout.view(np.uint32)), (label, call)
+    assert ctx.device_status() == 0
+
+
+def test_persistent_stack_flags_nonfinite_then_recovers(ctx):
+    from hawking_amd.moe import MoeModel, MoeShape
+    say("persistent stack non-finite")
+    shape = MoeShape(n_layers=2, hidden=512, inter=128, shared_inter=128, n_experts=16, top_k=4,
+                     expert_kind=U.HK_Q4, expert_group=32)
+    m = MoeModel(ctx, shape)
+    m.fill_synthetic(U.SEED)
+    assert admitted(m)
+    ctx.device_status()
+    h = np.ones(512, np.float32)
+    h[3] = np.nan
+    run_mode(m, h, True)
+    assert ctx.device_status() & 1
+    h = np.random.default_rng(3).standard_normal(512).astype(np.float32)
+    out, ids, w = run_mode(m, h, True)
+    rout, rids, rw = run_mode(m, h, False)
+    assert ctx.device_status() == 0
+    assert np.array_equal(out.view(np.uint32), rout.view(np.uint32))
