@@ -406,6 +406,61 @@ __device__ __forceinline__ void a_pos(uint32_t c, uint32_t& tau, uint32_t& off, 
     }
 }
 
+// One chunk (8 columns, values v, zero past the organ's columns) of an x
+// image with E = 0 (image_wave's unit rule), written at its tile positions
+// relative to tile tau0 and to the unit entries of chunk cb on.  Every lane
+// of the chunk's unit (SXG / 8 consecutive lanes) calls it together.
+// Returns whether the unit held a non-finite value (then zeroed).
+template <int KIND>
+__device__ __forceinline__ bool image_chunk(uint32_t ch, float4 (&v)[2], uint8_t* tiles, float* sx, uint32_t cb,
+                                            uint32_t tau0) {
+    constexpr int NL = Kcfg<KIND>::SXG / 8;
+    float m = group_max<NL>(max_abs8(v));
+    const bool bad = !isfinite(m);
+    if (bad) {
+        v[0] = v[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        m = 0.0f;
+    }
+    int eu = 0;
+    if (m > 0.0f) (void)frexpf(m, &eu);
+    const int Eu = m > 0.0f ? min(23 - eu, 100) : 0;
+    const float fu = ldexpf(1.0f, -Eu);
+    float f[8];
+    const int32_t s = group_sum<NL>(quantize8(v, Eu, f));
+    if constexpr (KIND == HK_MIXED) {
+        const int32_t s3 = group_sum<NL>((int32_t)f[6] + (int32_t)f[7]);
+        if ((ch & (uint32_t)(NL - 1)) == 0)
+            reinterpret_cast<float4*>(sx)[(ch - cb) / (uint32_t)NL] =
+                make_float4((float)s * fu, (float)(3 * s - 4 * s3) * 0.5f * fu, Kcfg<KIND>::ALPHA * fu,
+                            0.5f * Kcfg<KIND>::ALPHA * fu);
+    } else {
+        if ((ch & (uint32_t)(NL - 1)) == 0)
+            reinterpret_cast<float2*>(sx)[(ch - cb) / (uint32_t)NL] =
+                make_float2(Kcfg<KIND>::ALPHA * fu, Kcfg<KIND>::BETA * (float)s * fu);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        uint32_t tau, off;
+        int sh;
+        a_pos<KIND>(8u * ch + (uint32_t)e, tau, off, sh);
+        // signed base-256 limbs of the scaled value
+        const uint32_t z = ((uint32_t)((int32_t)f[e] * (1 << sh)) + 0x80808080u) ^ 0x80808080u;
+        uint8_t* p = tiles + (size_t)(tau - tau0) * A_TILE_STRIDE + off;
+        p[0] = (uint8_t)z;
+        p[16] = (uint8_t)(z >> 8);
+        p[32] = (uint8_t)(z >> 16);
+        p[48] = (uint8_t)(z >> 24);
+    }
+    return bad;
+}
+
+// The zero blocks (bytes 256..271) of the A tiles of `steps` steps.
+template <int KIND>
+__device__ __forceinline__ void image_zero_blocks(uint32_t lane, uint8_t* tiles, uint32_t steps) {
+    for (uint32_t i = lane; i < steps * (uint32_t)Kcfg<KIND>::P; i += 64u)
+        *reinterpret_cast<uint4*>(tiles + (size_t)i * A_TILE_STRIDE + 256u) = make_uint4(0u, 0u, 0u, 0u);
+}
+
 // The x image of x (cols columns, cols a multiple of 8; the image columns
 // past cols are zero) with E = 0, or the part of it in chunks [cb, ce) of 8
 // columns (whole steps), built by one wave straight into `tiles` (the A tiles
@@ -423,53 +478,15 @@ __device__ __forceinline__ void a_pos(uint32_t c, uint32_t& tau, uint32_t& off, 
 template <int KIND>
 __device__ void image_wave(uint32_t lane, const float* x, uint32_t cols, uint8_t* tiles, float* sx, uint32_t cb,
                            uint32_t ce, bool* nonfinite) {
-    constexpr int P = Kcfg<KIND>::P, SC = Kcfg<KIND>::STEP_COLS, NL = Kcfg<KIND>::SXG / 8;
+    constexpr int P = Kcfg<KIND>::P, SC = Kcfg<KIND>::STEP_COLS;
     const uint32_t tau0 = cb * 8u / SC * P;
-    // the tile zero blocks of the steps in range
-    for (uint32_t i = lane; i < (ce - cb) * 8u / SC * P; i += 64u)
-        *reinterpret_cast<uint4*>(tiles + (size_t)i * A_TILE_STRIDE + 256u) = make_uint4(0u, 0u, 0u, 0u);
+    image_zero_blocks<KIND>(lane, tiles, (ce - cb) * 8u / SC);
     bool any_bad = false;
     // a unit's NL chunks are NL consecutive lanes, active together (ranges are whole steps)
     for (uint32_t ch = cb + lane; ch < ce; ch += 64u) {
         float4 v[2];
         load_chunk(x, 8u * ch, cols, v);
-        float m = group_max<NL>(max_abs8(v));
-        const bool bad = !isfinite(m);
-        any_bad |= bad;
-        if (bad) {
-            v[0] = v[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            m = 0.0f;
-        }
-        int eu = 0;
-        if (m > 0.0f) (void)frexpf(m, &eu);
-        const int Eu = m > 0.0f ? min(23 - eu, 100) : 0;
-        const float fu = ldexpf(1.0f, -Eu);
-        float f[8];
-        const int32_t s = group_sum<NL>(quantize8(v, Eu, f));
-        if constexpr (KIND == HK_MIXED) {
-            const int32_t s3 = group_sum<NL>((int32_t)f[6] + (int32_t)f[7]);
-            if ((ch & (uint32_t)(NL - 1)) == 0)
-                reinterpret_cast<float4*>(sx)[(ch - cb) / (uint32_t)NL] =
-                    make_float4((float)s * fu, (float)(3 * s - 4 * s3) * 0.5f * fu, Kcfg<KIND>::ALPHA * fu,
-                                0.5f * Kcfg<KIND>::ALPHA * fu);
-        } else {
-            if ((ch & (uint32_t)(NL - 1)) == 0)
-                reinterpret_cast<float2*>(sx)[(ch - cb) / (uint32_t)NL] =
-                    make_float2(Kcfg<KIND>::ALPHA * fu, Kcfg<KIND>::BETA * (float)s * fu);
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            uint32_t tau, off;
-            int sh;
-            a_pos<KIND>(8u * ch + (uint32_t)e, tau, off, sh);
-            // signed base-256 limbs of the scaled value
-            const uint32_t z = ((uint32_t)((int32_t)f[e] * (1 << sh)) + 0x80808080u) ^ 0x80808080u;
-            uint8_t* p = tiles + (size_t)(tau - tau0) * A_TILE_STRIDE + off;
-            p[0] = (uint8_t)z;
-            p[16] = (uint8_t)(z >> 8);
-            p[32] = (uint8_t)(z >> 16);
-            p[48] = (uint8_t)(z >> 24);
-        }
+        any_bad |= image_chunk<KIND>(ch, v, tiles, sx, cb, tau0);
     }
     *nonfinite = any_bad;
 }

@@ -23,13 +23,12 @@
 // Cost is in the polls and the fan-out, not the hand-off itself (a word
 // crosses between XCDs in ~0.5 us).  ~500 waves polling the same lines, or
 // all reading h with loads that bypass the caches, queue on a few memory
-// channels and starve the producers.  So each producer, once its output
-// stores have completed, stores one ready word into RDY_REP replicas (the
-// readers spread over them); a reader polls only the ready words of its
-// producers with one wave, then reads the outputs with ordinary loads, so
-// the L2 of each XCD serves the fan-out (a line read before it was complete
-// would show an older tag: the read then falls back to polling the words
-// past the caches).  Roles by block:
+// channels and starve the producers.  So each producer, right behind its
+// output stores, stores one ready word into RDY_REP replicas (the readers
+// spread over them); a reader polls only the ready words of its producers
+// with one wave, then reads the outputs with ordinary loads, so the L2 of
+// each XCD serves the fan-out (a word read before it arrived shows an older
+// tag: the read then falls back to polling the words past the caches).  Roles by block:
 //   route   (E/4 + 1 blocks): prefetch the layer's router rows, wait for h,
 //           RMSNorm(1+w), one logit per wave (the last block: the shared-gate
 //           logit) -- moe_route_kernel's arithmetic.
@@ -62,7 +61,7 @@ constexpr int gu_depth() { return KIND == HK_MIXED ? 2 : 4; }
 // down steps in flight per slot (a wave holds every one of its slots' steps
 // across the activation waits; a mixed step is 12 registers, a Q4 step 5)
 template <int KIND>
-constexpr int dn_depth() { return KIND == HK_MIXED ? 1 : 4; }
+constexpr int dn_depth() { return KIND == HK_MIXED ? 1 : 3; }
 constexpr int DN_SPW = 3;  // slots per down wave: top_k + shared <= 12
 
 // Stores and polls at system scope: they write through and read past the L2
@@ -78,14 +77,13 @@ __device__ __forceinline__ uint64_t ll_get(const uint64_t* p) {
 __device__ __forceinline__ uint64_t ll_get_cached(const uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
-// The wave's outstanding memory operations have completed (its system-scope
-// stores are visible) before anything after this.
-__device__ __forceinline__ void stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Ready word i of a ready array, into every replica (lanes 0..RDY_REP-1 of
-// the calling wave store; the wave's output stores complete first).
+// the calling wave store), right behind the wave's output stores.  Not
+// waiting for those stores to complete first saves their acknowledgement
+// (~0.5 us) on every hand-off; a reader that sees the ready word before an
+// output word reads an older tag there and polls that word.
 __device__ __forceinline__ void put_ready(uint64_t* rdy, uint32_t rstride, uint32_t i, uint32_t lane, uint32_t tag) {
-    stores_done();
     if (lane < RDY_REP) ll_put(rdy + (size_t)lane * rstride + i, 0.0f, tag);
 }
 
@@ -118,6 +116,40 @@ __device__ uint32_t ll_wait(const uint64_t* p, const uint32_t (&idx)[N], uint32_
             return WAIT_ABORT;
         }
         __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// A chunk of 8 consecutive tagged words at bp, read like ll_read in two
+// parts so that several chunks can be in flight: chunk_issue (ordinary
+// loads), then chunk_finish (tag check; the bounded poll past the caches if
+// any word is not there yet).
+__device__ __forceinline__ void chunk_issue(const uint64_t* bp, uint64_t (&w)[8]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w[e] = ll_get_cached(bp + e);
+}
+__device__ uint32_t chunk_finish(const uint64_t* bp, uint64_t (&w)[8], uint32_t tag, float4 (&out)[2],
+                                 const StackArgs& a) {
+    for (uint32_t spin = 0;; ++spin) {
+        bool ok = true;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ok = ok && (uint32_t)(w[e] >> 32) == tag;
+        if (__all(ok)) {
+            out[0] = make_float4(__uint_as_float((uint32_t)w[0]), __uint_as_float((uint32_t)w[1]),
+                                 __uint_as_float((uint32_t)w[2]), __uint_as_float((uint32_t)w[3]));
+            out[1] = make_float4(__uint_as_float((uint32_t)w[4]), __uint_as_float((uint32_t)w[5]),
+                                 __uint_as_float((uint32_t)w[6]), __uint_as_float((uint32_t)w[7]));
+            return WAIT_OK;
+        }
+        const uint32_t ab = __hip_atomic_load(a.abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        if ((int32_t)(ab - a.tag) >= 0) return WAIT_ABORT;
+        if (spin >= SPIN_LIMIT) {
+            __hip_atomic_store(a.abort, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (__lane_id() == 0) atomicOr(a.status, HK_DEVERR_STALL);
+            return WAIT_ABORT;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) w[e] = ll_get(bp + e);
     }
 }
 
@@ -282,9 +314,8 @@ __device__ void route_role(const StackArgs& a, uint32_t b, uint8_t* lds) {
             for (uint32_t j = lane + 64u * ROW_PRE; j < n4; j += 64u) acc += dot4s(w4[j], x4[j]);
             acc = wave_sum(acc);
             if (lane == 0 && st == WAIT_OK) ll_put(a.logits + (size_t)l * a.ls + out, acc, a.tag);
-            stores_done();
         }
-        __syncthreads();  // the logit stores are done; xn is rewritten next layer
+        __syncthreads();  // xn is rewritten next layer
         if (wave == 0 && st == WAIT_OK) put_ready(a.l_rdy + (size_t)l * RDY_REP * a.lrs, a.lrs, b, lane, a.tag);
     }
 }
@@ -403,18 +434,18 @@ __device__ void down_role(const StackArgs& a, uint32_t T, uint8_t* lds) {
     const MoeDims& d = a.d;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t slots = d.K + (d.has_shared ? 1u : 0u);
-    const uint32_t img_stride = (uint32_t)x_lds_bytes<KIND>(n_steps_for(KIND, d.Imax));
-    const uint32_t kst = x_image_cols<KIND>(n_steps_for(KIND, d.Imax));
-    uint8_t* img = lds + (size_t)wave * img_stride;                                   // per wave
-    float* xs = reinterpret_cast<float*>(lds + 4u * img_stride) + (size_t)wave * kst;  // per wave
-    float* part = reinterpret_cast<float*>(lds + 4u * img_stride) + 4u * kst;         // [slots][16]
-    float* lg = part + 16u * slots;                                                    // [E + 1]
+    const uint32_t smax = n_steps_for(KIND, d.Imax);
+    const uint32_t img_stride = (uint32_t)x_lds_bytes<KIND>(smax);
+    uint8_t* img = lds + (size_t)wave * DN_SPW * img_stride;                   // [DN_SPW] per wave
+    float* part = reinterpret_cast<float*>(lds + 4u * DN_SPW * img_stride);   // [slots][16]
+    float* lg = part + 16u * slots;                                            // [E + 1]
     __shared__ TopkLds tk;
     __shared__ int32_t sel_i[HK_TOPK_MAX];
     __shared__ float sel_w[HK_TOPK_MAX];
     __shared__ float gate_v;
     __shared__ uint32_t state;
     const uint32_t row = T * 16u + threadIdx.x;
+    for (int j = 0; j < DN_SPW; ++j) image_zero_blocks<KIND>(threadIdx.x & 63u, img + (size_t)j * img_stride, smax);
     // the rows of h this block owns live in registers across the layers
     float hreg = threadIdx.x < 16u && row < d.H ? a.h_in[row] : 0.0f;
     if (threadIdx.x < 16u) {
@@ -462,36 +493,72 @@ __device__ void down_role(const StackArgs& a, uint32_t T, uint8_t* lds) {
             for (int k = 0; k < DN_D; ++k)
                 if ((uint32_t)k < S[j]) fetch_one<KIND, 1>(o[j], T, (uint32_t)k, lane, f[j][k], 0);
         }
+        // the wave's slots together: one poll of their producers' ready words,
+        // then their activations in rounds of 512 columns (8 per lane per
+        // slot), each slot's chunk imaged straight from registers
+        uint32_t acols[DN_SPW];
+        int jf = -1;  // the first active slot (stands in for inactive ones' indices)
+#pragma unroll
+        for (int j = DN_SPW - 1; j >= 0; --j) {
+            const uint32_t s = wave + 4u * (uint32_t)j;
+            acols[j] = act[j] ? (s < d.K ? d.I : d.SI) : 0u;
+            if (act[j]) jf = j;
+        }
+        bool bad = false;
+        if (jf >= 0) {
+            uint32_t ridx[2 * DN_SPW];
+            float rv[2 * DN_SPW];
+            const uint32_t r0 = (blockIdx.x % RDY_REP) * a.ars;
+#pragma unroll
+            for (int j = 0; j < DN_SPW; ++j) {
+                const int sj = act[j] ? j : jf;
+                const uint32_t s = wave + 4u * (uint32_t)sj, ntl = (acols[sj] + 15u) / 16u;
+#pragma unroll
+                for (int k = 0; k < 2; ++k) ridx[2 * j + k] = r0 + s * a.gu_tiles + min(lane + 64u * (uint32_t)k, ntl - 1u);
+            }
+            const uint32_t str = ll_wait<2 * DN_SPW>(a.a_rdy + (size_t)l * RDY_REP * a.ars, ridx, a.tag, rv, a);
+            if (str != WAIT_OK && lane == 0) atomicMax(&state, str);
+            uint32_t maxc = 0;
+#pragma unroll
+            for (int j = 0; j < DN_SPW; ++j) maxc = max(maxc, acols[j]);
+            for (uint32_t c0 = 0; c0 < maxc; c0 += 512u) {
+                // slot j + 1's chunk is in flight while slot j's is imaged
+                const uint64_t* bp[DN_SPW];
+#pragma unroll
+                for (int j = 0; j < DN_SPW; ++j) {
+                    // whole chunks (acols is a multiple of 8)
+                    const int sj = act[j] ? j : jf;
+                    bp[j] = a.act + (size_t)l * a.as + (wave + 4u * (uint32_t)sj) * d.Imax +
+                            min(c0 + 8u * lane, acols[sj] - 8u);
+                }
+                uint64_t w[2][8];
+                chunk_issue(bp[0], w[0]);
+#pragma unroll
+                for (int j = 0; j < DN_SPW; ++j) {
+                    if (j + 1 < DN_SPW) chunk_issue(bp[j + 1], w[(j + 1) & 1]);
+                    float4 cv[2];
+                    const uint32_t sta = chunk_finish(bp[j], w[j & 1], a.tag, cv, a);
+                    if (sta != WAIT_OK && lane == 0) atomicMax(&state, sta);
+                    const uint32_t ch = c0 / 8u + lane;
+                    if (!act[j] || ch >= S[j] * tile_step_cols(KIND) / 8u) continue;
+                    if (c0 + 8u * lane >= acols[j]) cv[0] = cv[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    uint8_t* im = img + (size_t)j * img_stride;
+                    bad |= image_chunk<KIND>(ch, cv, im,
+                                             reinterpret_cast<float*>(im + (size_t)S[j] * Kcfg<KIND>::P * A_TILE_STRIDE),
+                                             0u, 0u);
+                }
+            }
+        }
+        if (__ballot(bad) != 0 && lane == 0) atomicOr(a.status, HK_DEVERR_NONFINITE);
 #pragma unroll
         for (int j = 0; j < DN_SPW; ++j) {
             const uint32_t s = wave + 4u * (uint32_t)j;
             if (s >= slots) break;
             float y = 0.0f;
             if (act[j]) {
-                // the slot's activations (8 columns per lane per round) from their tagged words
-                const uint32_t acols = s < d.K ? d.I : d.SI;
-                {
-                    const uint32_t str = wait_ready<2>(a.a_rdy + (size_t)l * RDY_REP * a.ars + (size_t)s * a.gu_tiles,
-                                                       a.ars, (acols + 15u) / 16u, lane, a.tag, a);
-                    if (str != WAIT_OK) atomicMax(&state, str);
-                }
-                for (uint32_t c0 = 8u * lane; c0 < acols; c0 += 512u) {
-                    uint32_t idx[8];
-                    float v[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) idx[e] = s * d.Imax + min(c0 + (uint32_t)e, acols - 1u);
-                    const uint32_t sta = ll_read<8>(a.act + (size_t)l * a.as, idx, a.tag, v, a);
-                    if (sta != WAIT_OK) atomicMax(&state, sta);
-                    reinterpret_cast<float4*>(xs + c0)[0] = make_float4(v[0], v[1], v[2], v[3]);
-                    reinterpret_cast<float4*>(xs + c0)[1] = make_float4(v[4], v[5], v[6], v[7]);
-                }
-                bool bad = false;
-                image_wave<KIND>(lane, xs, o[j].cols, img,
-                                 reinterpret_cast<float*>(img + (size_t)S[j] * Kcfg<KIND>::P * A_TILE_STRIDE), 0u,
-                                 S[j] * tile_step_cols(KIND) / 8u, &bad);
-                if (__ballot(bad) != 0 && lane == 0) atomicOr(a.status, HK_DEVERR_NONFINITE);
-                const ImageA A{img, a_lane_offset((int)lane)};
-                const float* SX = reinterpret_cast<const float*>(img + (size_t)S[j] * Kcfg<KIND>::P * A_TILE_STRIDE);
+                const uint8_t* im = img + (size_t)j * img_stride;
+                const ImageA A{im, a_lane_offset((int)lane)};
+                const float* SX = reinterpret_cast<const float*>(im + (size_t)S[j] * Kcfg<KIND>::P * A_TILE_STRIDE);
                 float acc[1] = {0.0f};
                 for (uint32_t it = 0; it < S[j]; it += DN_D) {
 #pragma unroll
@@ -543,8 +610,7 @@ size_t stack_lds(const MoeDims& d) {
     const size_t gu = x_lds_bytes<KIND>(S) + 128 * 4 + (size_t)hcols * 4 + ((size_t)d.E + 1) * 4;
     const uint32_t slots = d.K + (d.has_shared ? 1u : 0u);
     const size_t img_stride = x_lds_bytes<KIND>(n_steps_for(KIND, d.Imax));
-    const size_t kst = x_image_cols<KIND>(n_steps_for(KIND, d.Imax));
-    const size_t dn = 4 * img_stride + 4 * kst * 4 + (size_t)slots * 16 * 4 + ((size_t)d.E + 1) * 4;
+    const size_t dn = 4 * DN_SPW * img_stride + (size_t)slots * 16 * 4 + ((size_t)d.E + 1) * 4;
     const size_t rt = (size_t)hcols * 4;
     return std::max(gu, std::max(dn, rt));
 }

@@ -323,7 +323,8 @@ __device__ __forceinline__ ArgBest softmax_topk_wave(const float* __restrict__ l
     }
     if (renorm) {
         float sel = -0.0f;
-        for (uint32_t r = 0; r < k; ++r) sel += __shfl(mine.v, (int)r, 64);
+        for (uint32_t r = 0; r < k; ++r)
+            sel += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine.v), (int)r));
         mine.v = mine.i >= 0 ? mine.v / sel : 0.0f;
     }
     if ((uint32_t)lane < k) {
