@@ -60,9 +60,9 @@ struct Kcfg;
 // P = A tiles per step, SXG = columns per unit (the zero-point granularity a
 // lane needs per step: one binary group, one Q4 group of 32, one Q2 half-group;
 // each unit has its own exponent), SXW = floats stored per unit: {ALPHA f_u,
-// BETA f_u sum X} (mixed: the binary and the Q2 correction, then the binary
-// and the Q2 alpha, all times f_u).  A lane's partial for a unit is
-// combine(c) * SX[0] - SX[1] (in units of 2^-E).
+// BETA f_u sum X} (mixed: {alpha, correction} of binary items, then of Q2
+// items, all times f_u; a lane reads the pair of its item's kind).  A lane's
+// partial for a unit is combine(c) * pair[0] - pair[1] (in units of 2^-E).
 template <>
 struct Kcfg<HK_BIN> {
     static constexpr int P = 8, STEP_COLS = 512, DATA = 16, SXG = 128, SXW = 2;
@@ -337,8 +337,8 @@ __device__ int x_image(const Team& team, const XChunks<NC>& xc, const float* x, 
                 const int32_t s3 = group_sum<NL>((int32_t)f[6] + (int32_t)f[7]);
                 if ((me & (uint32_t)(NL - 1)) == 0)
                     reinterpret_cast<float4*>(SX)[ch / (uint32_t)NL] =
-                        make_float4((float)s * fu, (float)(3 * s - 4 * s3) * 0.5f * fu, Kcfg<KIND>::ALPHA * fu,
-                                    0.5f * Kcfg<KIND>::ALPHA * fu);
+                        make_float4(Kcfg<KIND>::ALPHA * fu, (float)s * fu, 0.5f * Kcfg<KIND>::ALPHA * fu,
+                                    (float)(3 * s - 4 * s3) * 0.5f * fu);
             } else {
                 if ((me & (uint32_t)(NL - 1)) == 0)
                     reinterpret_cast<float2*>(SX)[ch / (uint32_t)NL] =
@@ -431,8 +431,8 @@ __device__ __forceinline__ bool image_chunk(uint32_t ch, float4 (&v)[2], uint8_t
         const int32_t s3 = group_sum<NL>((int32_t)f[6] + (int32_t)f[7]);
         if ((ch & (uint32_t)(NL - 1)) == 0)
             reinterpret_cast<float4*>(sx)[(ch - cb) / (uint32_t)NL] =
-                make_float4((float)s * fu, (float)(3 * s - 4 * s3) * 0.5f * fu, Kcfg<KIND>::ALPHA * fu,
-                            0.5f * Kcfg<KIND>::ALPHA * fu);
+                make_float4(Kcfg<KIND>::ALPHA * fu, (float)s * fu, 0.5f * Kcfg<KIND>::ALPHA * fu,
+                            (float)(3 * s - 4 * s3) * 0.5f * fu);
     } else {
         if ((ch & (uint32_t)(NL - 1)) == 0)
             reinterpret_cast<float2*>(sx)[(ch - cb) / (uint32_t)NL] =
@@ -552,10 +552,13 @@ __device__ __forceinline__ void fetch_mixed(const OrganView& o, const uint4& h, 
     const uint64_t mask = ((uint64_t)mhi << 32) | mlo;
     const uint32_t below = __builtin_amdgcn_mbcnt_hi(mhi, __builtin_amdgcn_mbcnt_lo(mlo, 0u));
     const bool isq2 = __builtin_amdgcn_inverse_ballot_w64(mask);
-    const uint8_t* p = o.data + doff + 16u * ((uint32_t)lane + below);
-    const uint4 va = ldg(reinterpret_cast<const uint4*>(p));
+    // uniform bases (scalar registers) plus 32-bit lane offsets: the loads
+    // take the scalar-base form, no 64-bit address arithmetic per lane
+    const uint8_t* db = o.data + doff;
+    const uint32_t dl = 16u * ((uint32_t)lane + below);
+    const uint4 va = ldg(reinterpret_cast<const uint4*>(db + dl));
     // binary lanes re-read their 16 bytes (an exec-masked load measured slower)
-    const uint4 vb = ldg(reinterpret_cast<const uint4*>(p + (isq2 ? 16 : 0)));
+    const uint4 vb = ldg(reinterpret_cast<const uint4*>(db + (dl + (isq2 ? 16u : 0u))));
     f.V[r][0] = va.x;
     f.V[r][1] = va.y;
     f.V[r][2] = va.z;
@@ -564,9 +567,10 @@ __device__ __forceinline__ void fetch_mixed(const OrganView& o, const uint4& h, 
     f.V[r][5] = vb.y;
     f.V[r][6] = vb.z;
     f.V[r][7] = vb.w;
-    const uint16_t* spp = o.scales + soff + (uint32_t)lane + below;
-    f.s0[r] = ldg(spp);
-    f.s1[r] = ldg(spp + (isq2 ? 1 : 0));
+    const uint8_t* sb = reinterpret_cast<const uint8_t*>(o.scales + soff);
+    const uint32_t sl = 2u * ((uint32_t)lane + below);
+    f.s0[r] = ldg(reinterpret_cast<const uint16_t*>(sb + sl));
+    f.s1[r] = ldg(reinterpret_cast<const uint16_t*>(sb + (sl + (isq2 ? 2u : 0u))));
     f.q2m[r] = mask;
 }
 
@@ -689,9 +693,15 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
                 V[r][k + 4] = f.V[r][k + 4] >> sh;
             }
         }
-        // per half: {binary correction, Q2 correction, binary alpha, Q2 alpha}
-        const float4 uh[2] = {reinterpret_cast<const float4*>(SX)[2 * (4 * t + q)],
-                              reinterpret_cast<const float4*>(SX)[2 * (4 * t + q) + 1]};
+        // per half: {binary alpha, binary correction, Q2 alpha, Q2 correction};
+        // each lane reads the pair of its kind
+        float2 uh[2][R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float2* u2 = reinterpret_cast<const float2*>(SX) + 4 * (4 * t + q) + (q2[r] ? 1 : 0);
+            uh[0][r] = u2[0];
+            uh[1][r] = u2[2];
+        }
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -712,11 +722,8 @@ __device__ __forceinline__ void compute_step(const Frag<KIND, R>& f, uint32_t t,
                 }
             }
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const float alpha = q2[r] ? uh[h].w : uh[h].z;
-                const float corr = q2[r] ? uh[h].y : uh[h].x;
-                acc[r] += f16_bits_to_f32(h ? f.s1[r] : f.s0[r]) * (combine_limbs(c[r]) * alpha - corr);
-            }
+            for (int r = 0; r < R; ++r)
+                acc[r] += f16_bits_to_f32(h ? f.s1[r] : f.s0[r]) * (combine_limbs(c[r]) * uh[h][r].x - uh[h][r].y);
         }
     }
 }
