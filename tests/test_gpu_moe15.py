@@ -86,13 +86,30 @@ def build_layer(ctx, oracle, H, I, SI, E, K, rank, tag=0x15, ratio=0.02):
     return layer, ref
 
 
+def router_weights_f64(ref, h, ids, eps=1e-6):
+    """The routed weights in FP64 (RMSNorm(1+w), the decoded q8 router, softmax,
+    renormalised over the selection): the numeric authority for the weights."""
+    h64 = np.asarray(h, np.float64)
+    xn = h64 / np.sqrt(np.dot(h64, h64) / h64.size + eps) * (1.0 + ref.norm_w.astype(np.float64))
+    lg = ref.router_w.astype(np.float64) @ xn
+    p = np.exp(lg - lg.max())
+    sel = p[np.asarray(ids)] / p.sum()
+    return sel / sel.sum()
+
+
 def _check(ctx, oracle, layer, ref, h, K):
     out, ids, w = layer.moe_suffix(h)
     assert ctx.device_status() == 0
     rout, rids, rw, _, logits = ref.forward(h)
     if U.router_margin_ok(logits, K):
         assert ids.tolist() == rids.tolist()
-        assert np.all(np.abs(w - rw) <= 1e-5 * rw + 1e-7)
+        # the weights within 1e-6 of the FP64 authority; the serial f32 oracle
+        # (whose own router dot differs from FP64 by up to ~1e-6) within 2e-6
+        w64 = router_weights_f64(ref, h, ids)
+        print("[gpu-case] router weight max abs dev: vs FP64", float(np.max(np.abs(w - w64))),
+              "oracle vs FP64", float(np.max(np.abs(rw - w64))), "vs oracle", float(np.max(np.abs(w - rw))), flush=True)
+        assert np.all(np.abs(w - w64) <= 1e-6)
+        assert np.all(np.abs(w - rw) <= 2e-6)
         assert oracle.relative_l2(out, rout) < TOL
     assert oracle.relative_l2(out, ref.forward_f64(h, ids)) < TOL
     return ids
