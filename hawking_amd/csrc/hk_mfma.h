@@ -388,7 +388,7 @@ __device__ int x_image(const Team& team, const XChunks<NC>& xc, const float* x, 
 // two the column's X is scaled by.
 template <int KIND>
 __device__ __forceinline__ void a_pos(uint32_t c, uint32_t& tau, uint32_t& off, int& sh) {
-    static_assert(KIND == HK_MIXED || KIND == HK_Q4, "scatter image builds cover the MoE expert kinds");
+    static_assert(KIND == HK_MIXED || KIND == HK_Q4 || KIND == HK_Q8, "per-column scatter kinds");
     if constexpr (KIND == HK_MIXED) {
         // column i of the 128-column group q -> (a, j, u): tile mu = 4h + u,
         // byte 4r + j of rows 4q + limb
@@ -398,10 +398,15 @@ __device__ __forceinline__ void a_pos(uint32_t c, uint32_t& tau, uint32_t& off, 
         tau = (c >> 9) * (uint32_t)Kcfg<KIND>::P + 4u * h + u;
         off = 64u * ((c >> 7) & 3u) + 4u * r + j;
         sh = 6 - 2 * (int)u;
-    } else {
+    } else if constexpr (KIND == HK_Q4) {
         const uint32_t cs = c & 127u;
         tau = (c >> 7) * (uint32_t)Kcfg<KIND>::P + (cs & 1u);
         off = 64u * (cs >> 5) + ((cs & 31u) >> 1);
+        sh = 0;
+    } else {
+        // q8: step = one tile of 64 columns, lane group (c / 16) % 4, byte c % 16
+        tau = c >> 6;
+        off = 64u * ((c >> 4) & 3u) + (c & 15u);
         sh = 0;
     }
 }
@@ -438,18 +443,36 @@ __device__ __forceinline__ bool image_chunk(uint32_t ch, float4 (&v)[2], uint8_t
             reinterpret_cast<float2*>(sx)[(ch - cb) / (uint32_t)NL] =
                 make_float2(Kcfg<KIND>::ALPHA * fu, Kcfg<KIND>::BETA * (float)s * fu);
     }
+    if constexpr (KIND == HK_BIN) {
+        // the chunk is byte ch % 16 of lane group (ch / 16) % 4 in all 8 bit
+        // planes of step ch / 64: plane mu < 7 holds X_mu 2^(7-mu) + X_7,
+        // plane 7 holds -X_7 (a_value's binary rule)
+        const uint32_t off = 64u * ((ch >> 4) & 3u) + (ch & 15u), tb = (ch >> 6) * 8u - tau0;
+        const int32_t x7 = (int32_t)f[7];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        uint32_t tau, off;
-        int sh;
-        a_pos<KIND>(8u * ch + (uint32_t)e, tau, off, sh);
-        // signed base-256 limbs of the scaled value
-        const uint32_t z = ((uint32_t)((int32_t)f[e] * (1 << sh)) + 0x80808080u) ^ 0x80808080u;
-        uint8_t* p = tiles + (size_t)(tau - tau0) * A_TILE_STRIDE + off;
-        p[0] = (uint8_t)z;
-        p[16] = (uint8_t)(z >> 8);
-        p[32] = (uint8_t)(z >> 16);
-        p[48] = (uint8_t)(z >> 24);
+        for (int mu = 0; mu < 8; ++mu) {
+            const int32_t a = mu < 7 ? (int32_t)f[mu] * (1 << (7 - mu)) + x7 : -x7;
+            const uint32_t z = ((uint32_t)a + 0x80808080u) ^ 0x80808080u;
+            uint8_t* p = tiles + (size_t)(tb + (uint32_t)mu) * A_TILE_STRIDE + off;
+            p[0] = (uint8_t)z;
+            p[16] = (uint8_t)(z >> 8);
+            p[32] = (uint8_t)(z >> 16);
+            p[48] = (uint8_t)(z >> 24);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            uint32_t tau, off;
+            int sh;
+            a_pos<KIND>(8u * ch + (uint32_t)e, tau, off, sh);
+            // signed base-256 limbs of the scaled value
+            const uint32_t z = ((uint32_t)((int32_t)f[e] * (1 << sh)) + 0x80808080u) ^ 0x80808080u;
+            uint8_t* p = tiles + (size_t)(tau - tau0) * A_TILE_STRIDE + off;
+            p[0] = (uint8_t)z;
+            p[16] = (uint8_t)(z >> 8);
+            p[32] = (uint8_t)(z >> 16);
+            p[48] = (uint8_t)(z >> 24);
+        }
     }
     return bad;
 }

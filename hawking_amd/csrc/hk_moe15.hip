@@ -78,27 +78,42 @@ __device__ __forceinline__ float dot4(const float4& a, const float4& b) {
 }
 
 // xn = h * (1 / sqrt(mean(h^2) + eps)) * (1 + w) (source_qwen80_residual_rms_norm,
-// model/qwen80_complete_runtime.rs:6778-6797) into xs (LDS) and, if out is
-// not null, to global memory.  Every thread of the block calls this.
-__device__ void block_rmsnorm(const float* __restrict__ h, const float* __restrict__ w, uint32_t H, float eps,
-                              float* xs, float* red, float* out) {
-    const uint32_t n4 = H / 4u;
+// model/qwen80_complete_runtime.rs:6778-6797) held in registers: thread t has chunks t + 256 k
+// (8 columns each, k < M15_NC; hidden <= 8 * 256 * M15_NC).  h and w are
+// loaded once, unconditionally (index clamped, value dropped past H), so
+// every load is in flight before the block's one reduction.  Every thread
+// of the 256-thread block calls this.
+constexpr int M15_NC = 4;
+struct XnRegs {
+    float4 v[M15_NC][2];
+};
+__device__ __forceinline__ void block_xn(const float* __restrict__ h, const float* __restrict__ w, uint32_t H,
+                                         float eps, float* red, XnRegs& x) {
+    const uint32_t nch = H / 8u;
     const float4* h4 = reinterpret_cast<const float4*>(h);
     const float4* w4 = reinterpret_cast<const float4*>(w);
+    float4 wv[M15_NC][2];
+#pragma unroll
+    for (int k = 0; k < M15_NC; ++k) {
+        const uint32_t ch = min(threadIdx.x + 256u * (uint32_t)k, nch - 1u);
+        x.v[k][0] = ldg(h4 + 2u * ch);
+        x.v[k][1] = ldg(h4 + 2u * ch + 1u);
+        wv[k][0] = ldg(w4 + 2u * ch);
+        wv[k][1] = ldg(w4 + 2u * ch + 1u);
+    }
     float ss = 0.0f;
-    for (uint32_t j = threadIdx.x; j < n4; j += blockDim.x) {
-        const float4 v = ldg(h4 + j);
-        ss += dot4(v, v);
-    }
+#pragma unroll
+    for (int k = 0; k < M15_NC; ++k)
+        if (threadIdx.x + 256u * (uint32_t)k < nch) ss += dot4(x.v[k][0], x.v[k][0]) + dot4(x.v[k][1], x.v[k][1]);
     const float inv = 1.0f / sqrtf(block_sum(ss, red) / (float)H + eps);
-    for (uint32_t j = threadIdx.x; j < n4; j += blockDim.x) {
-        const float4 v = ldg(h4 + j), g = ldg(w4 + j);
-        const float4 x = make_float4(v.x * inv * (1.0f + g.x), v.y * inv * (1.0f + g.y), v.z * inv * (1.0f + g.z),
-                                     v.w * inv * (1.0f + g.w));
-        reinterpret_cast<float4*>(xs)[j] = x;
-        if (out) reinterpret_cast<float4*>(out)[j] = x;
-    }
-    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < M15_NC; ++k)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const float4 v = x.v[k][j], g = wv[k][j];
+            x.v[k][j] = make_float4(v.x * inv * (1.0f + g.x), v.y * inv * (1.0f + g.y), v.z * inv * (1.0f + g.z),
+                                    v.w * inv * (1.0f + g.w));
+        }
 }
 
 // The first D steps of [s0, s0 + n) of tile T of organs o[0..R-1].
@@ -166,31 +181,38 @@ __device__ __forceinline__ void wave_share(uint32_t S, uint32_t wave, uint32_t& 
 
 // q8 rows of tile T of o[0..R-1] (cols H) against xn, in a block of its own:
 // the weights' first D steps per wave (a wave's whole share at H = 2048) are
-// in flight while xn and its image are built.
+// in flight while xn is formed in registers and each thread scatters its
+// chunks of the q8 x image (E = 0: one exponent per 16-column unit, no
+// block-wide maximum) into LDS.
 template <int R, int D = 8 / R>
 __device__ __forceinline__ void q8_tile(const M15Dims& d, const M15Dev& L, const float* h, const OrganView (&o)[R],
                                         uint32_t T, uint8_t* lds, float* red, float* part, uint32_t* status,
                                         float* v) {
     const int lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t S = n_steps_for(HK_Q8, d.H);
+    const uint32_t S = n_steps_for(HK_Q8, d.H), nch = d.H / 8u;
     uint32_t s0, n;
     wave_share(S, wave, s0, n);
     Frag<HK_Q8, R> f[D];
     fetch_first<HK_Q8, R, D>(o, T, s0, n, lane, f);
-    float* xs = reinterpret_cast<float*>(lds);  // stage: image columns of H (binary steps)
-    uint8_t* img = lds + (size_t)n_steps_for(HK_BIN, d.H) * 512u * 4u;
-    block_rmsnorm(h, L.norm_w, d.H, d.eps, xs, red, nullptr);
+    uint8_t* img = lds;
+    float* sx = reinterpret_cast<float*>(img + (size_t)S * Kcfg<HK_Q8>::P * A_TILE_STRIDE);
+    if (threadIdx.x < 64u) image_zero_blocks<HK_Q8>(threadIdx.x, img, S);
+    XnRegs x;
+    block_xn(h, L.norm_w, d.H, d.eps, red, x);
     bool bad = false;
-    XChunks<1> xc;
-    load_x<1>(BlockTeam{}, xs, d.H, xc);
-    const int E = x_image<HK_Q8, 1>(BlockTeam{}, xc, xs, d.H, S, img, xs, 8u * blockDim.x, red, &bad);
-    if (bad && threadIdx.x == 0) atomicOr(status, HK_DEVERR_NONFINITE);
+#pragma unroll
+    for (int k = 0; k < M15_NC; ++k) {
+        const uint32_t ch = threadIdx.x + 256u * (uint32_t)k;
+        if (ch < nch) bad |= image_chunk<HK_Q8>(ch, x.v[k], img, sx, 0u, 0u);
+    }
+    if (bad) atomicOr(status, HK_DEVERR_NONFINITE);
+    __syncthreads();
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
     run_steps<HK_Q8, R, D>(o, T, s0, n, img, S, lane, f, acc);
-    block_rows<R>(acc, part, E, v);
+    block_rows<R>(acc, part, 0, v);
 }
 
 __global__ void __launch_bounds__(256) m15_route_kernel(M15Dims d, M15Dev L, const float* __restrict__ h, M15Ws ws) {
@@ -222,18 +244,34 @@ __global__ void __launch_bounds__(256) m15_route_kernel(M15Dims d, M15Dev L, con
         const uint32_t row = T * 16u + threadIdx.x;
         if (threadIdx.x < 16 && row < d.SI) ws.act_s[row] = (v[0] / (1.0f + expf(-v[0]))) * v[1];
     } else {
-        // the binary x image of xn, one 512-column step per block; the first publishes xn and E
-        const uint32_t tb = b - nR - nG - nS, S = n_steps_for(HK_BIN, d.H);
-        float* xs = reinterpret_cast<float*>(lds);
-        block_rmsnorm(h, L.norm_w, d.H, d.eps, xs, red, tb == 0 ? ws.xn : nullptr);
-        bool bad = false;
-        XChunks<1> xc;
-        load_x<1>(BlockTeam{}, xs, d.H, xc);
-        const int E = x_image<HK_BIN, 1>(BlockTeam{}, xc, xs, d.H, S, ws.img, xs + tb * 512u, 8u * blockDim.x, red,
-                                         &bad, tb, tb + 1u);
-        if (threadIdx.x == 0) {
-            if (tb == 0) ws.img_e[0] = E;
-            if (bad) atomicOr(ws.status, HK_DEVERR_NONFINITE);
+        // the binary x image of xn (E = 0), one 512-column step per block,
+        // scattered by the wave whose threads hold that step's 64 chunks;
+        // the first block publishes xn
+        const uint32_t tb = b - nR - nG - nS, S = n_steps_for(HK_BIN, d.H), nch = d.H / 8u;
+        XnRegs x;
+        block_xn(h, L.norm_w, d.H, d.eps, red, x);
+        if (tb == 0) {
+#pragma unroll
+            for (int k = 0; k < M15_NC; ++k) {
+                const uint32_t ch = threadIdx.x + 256u * (uint32_t)k;
+                if (ch < nch) {
+                    reinterpret_cast<float4*>(ws.xn)[2u * ch] = x.v[k][0];
+                    reinterpret_cast<float4*>(ws.xn)[2u * ch + 1u] = x.v[k][1];
+                }
+            }
+            if (threadIdx.x == 0) ws.img_e[0] = 0;
+        }
+        uint8_t* tiles = ws.img + (size_t)tb * Kcfg<HK_BIN>::P * A_TILE_STRIDE;
+        float* sx = reinterpret_cast<float*>(ws.img + (size_t)S * Kcfg<HK_BIN>::P * A_TILE_STRIDE) +
+                    (size_t)tb * (512u / Kcfg<HK_BIN>::SXG) * Kcfg<HK_BIN>::SXW;
+        if ((threadIdx.x >> 6) == (tb & 3u)) {
+            const uint32_t lane = threadIdx.x & 63u;
+            image_zero_blocks<HK_BIN>(lane, tiles, 1u);
+            bool bad = false;
+#pragma unroll
+            for (int k = 0; k < M15_NC; ++k)
+                if ((uint32_t)k == (tb >> 2)) bad = image_chunk<HK_BIN>(64u * tb + lane, x.v[k], tiles, sx, 64u * tb, 8u * tb);
+            if (__ballot(bad) != 0 && lane == 0) atomicOr(ws.status, HK_DEVERR_NONFINITE);
         }
     }
 }
@@ -450,10 +488,10 @@ extern "C" int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* s, h
     const uint32_t rank = r0->view.rows;
     if (g0->view.kind != HK_BIN || g0->view.rows != I || g0->view.cols != H || u0->kind != HK_BIN_RICE ||
         !same_shape(g0->view, u0->view) || l0->view.kind != HK_U3 || r0->view.kind != HK_U3 || l0->view.rows != H ||
-        l0->view.cols != rank || r0->view.cols != I || H % 64 || I % 4)
+        l0->view.cols != rank || r0->view.cols != I || H % 64 || H > 8192 || I % 4)
         return set_error(ctx, HK_E_GEOMETRY,
                          "mixed-1p5 layer: experts need a binary gate and an HGRAVR02 up of inter x hidden, and "
-                         "3-bit down factors hidden x rank, rank x inter (hidden a multiple of 64)");
+                         "3-bit down factors hidden x rank, rank x inter (hidden a multiple of 64, at most 8192)");
     std::vector<OrganView> gv(E), uv(E), lv(E), rvv(E);
     std::vector<ResView> res(E);
     for (uint32_t e = 0; e < E; ++e) {
@@ -473,7 +511,7 @@ extern "C" int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* s, h
     // dynamic LDS of the four kernels (each within 64 KB)
     const uint32_t Sb = n_steps_for(HK_BIN, H), Sq = n_steps_for(HK_Q8, H), Sr = n_steps_for(HK_U3, I),
                    Sl = n_steps_for(HK_U3, rank), Ss = SI ? n_steps_for(HK_Q8, SI) : 0u;
-    L->lds_route = (size_t)Sb * 512u * 4u + x_lds_bytes<HK_Q8>(Sq);
+    L->lds_route = x_lds_bytes<HK_Q8>(Sq);
     L->lds_gu = align16(x_lds_bytes<HK_BIN>(Sb)) + (size_t)H * 4u + (size_t)RICE_BATCH * 4u;
     L->lds_dr = std::max((size_t)x_image_cols<HK_U3>(Sr) * 4u + x_lds_bytes<HK_U3>(Sr),
                          SI ? (size_t)x_image_cols<HK_Q8>(Ss) * 4u + x_lds_bytes<HK_Q8>(Ss) : (size_t)0);

@@ -563,7 +563,9 @@ typedef struct hk_moe15_layer_src {
     const hk_organ* const* down_left;  /* [n_experts] */
     const hk_organ* const* down_right; /* [n_experts] */
 } hk_moe15_layer_src;
-/* Limits: top_k <= 64, n_experts <= 512; rank, inter, hidden multiples of 4. */
+/* Limits: top_k <= 16 (and <= n_experts), n_experts <= 512, hidden a
+ * multiple of 64 and at most 8192, inter a multiple of 4, each kernel's LDS
+ * within 64 KiB (HK_E_UNSUPPORTED / HK_E_GEOMETRY otherwise). */
 int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* src, hk_moe15_layer** out);
 int hk_moe15_layer_free(hk_ctx* ctx, hk_moe15_layer* layer);
 /* moe_suffix of the mixed decode (model/qwen80_mixed_hybrid_decode.rs:3636-3752
