@@ -443,7 +443,35 @@ __device__ __forceinline__ bool image_chunk(uint32_t ch, float4 (&v)[2], uint8_t
             reinterpret_cast<float2*>(sx)[(ch - cb) / (uint32_t)NL] =
                 make_float2(Kcfg<KIND>::ALPHA * fu, Kcfg<KIND>::BETA * (float)s * fu);
     }
-    if constexpr (KIND == HK_BIN) {
+    if constexpr (KIND == HK_U3) {
+        // a 3-bit step is 128 columns in 4 lane groups of 32; column o of a
+        // group sits twice: as a low 2-bit field (tile o % 4, byte
+        // 4 (o / 16) + (o / 4) % 4, times 4^(2 - o % 4), field 3 times 32)
+        // and as a high bit s = o % 8 (tile s / 2, byte 4 (2 + s % 2) + o / 8,
+        // times 2^(7 - s), bit 7 as -X): a_value's 3-bit rule inverted
+        const uint32_t m = ch & 3u, base = 64u * ((ch >> 2) & 3u), tb = (ch >> 4) * 4u - tau0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int32_t x = (int32_t)f[e];
+            const uint32_t mu = (uint32_t)e & 3u;
+            const int32_t lo = x * (mu == 3u ? 32 : 1 << (5 - 2 * (int)mu));
+            const int32_t hi = e == 7 ? -x : x * (1 << (7 - e));
+            const uint32_t ilo = 4u * (m >> 1) + ((2u * m + ((uint32_t)e >> 2)) & 3u);
+            const uint32_t ihi = 4u * (2u + ((uint32_t)e & 1u)) + m;
+            const uint32_t zl = ((uint32_t)lo + 0x80808080u) ^ 0x80808080u;
+            const uint32_t zh = ((uint32_t)hi + 0x80808080u) ^ 0x80808080u;
+            uint8_t* pl = tiles + (size_t)(tb + mu) * A_TILE_STRIDE + base + ilo;
+            uint8_t* ph = tiles + (size_t)(tb + ((uint32_t)e >> 1)) * A_TILE_STRIDE + base + ihi;
+            pl[0] = (uint8_t)zl;
+            pl[16] = (uint8_t)(zl >> 8);
+            pl[32] = (uint8_t)(zl >> 16);
+            pl[48] = (uint8_t)(zl >> 24);
+            ph[0] = (uint8_t)zh;
+            ph[16] = (uint8_t)(zh >> 8);
+            ph[32] = (uint8_t)(zh >> 16);
+            ph[48] = (uint8_t)(zh >> 24);
+        }
+    } else if constexpr (KIND == HK_BIN) {
         // the chunk is byte ch % 16 of lane group (ch / 16) % 4 in all 8 bit
         // planes of step ch / 64: plane mu < 7 holds X_mu 2^(7-mu) + X_7,
         // plane 7 holds -X_7 (a_value's binary rule)

@@ -342,10 +342,28 @@ __global__ void __launch_bounds__(256) m15_gate_up_kernel(M15Dims d, M15Dev L, M
     if (threadIdx.x < 16 && row < d.I) ws.act[(size_t)slot * d.I + row] = (v[0] / (1.0f + expf(-v[0]))) * racc[0];
 }
 
+// The x image (E = 0) of x (cols columns, S steps) in LDS, scattered by the
+// block's threads one 8-column chunk each (chunks past cols are zero); the
+// block synchronises before returning.  Returns this thread's non-finite flag.
+template <int KIND>
+__device__ __forceinline__ bool scatter_image(const float* __restrict__ x, uint32_t cols, uint32_t S, uint8_t* img) {
+    if (threadIdx.x < 64u) image_zero_blocks<KIND>(threadIdx.x, img, S);
+    float* sx = reinterpret_cast<float*>(img + (size_t)S * Kcfg<KIND>::P * A_TILE_STRIDE);
+    const uint32_t nch = S * (uint32_t)Kcfg<KIND>::STEP_COLS / 8u;
+    bool bad = false;
+    // a unit's chunks are consecutive threads, active together (nch is whole units)
+    for (uint32_t ch = threadIdx.x; ch < nch; ch += blockDim.x) {
+        float4 v[2];
+        load_chunk(x, 8u * ch, cols, v);
+        bad |= image_chunk<KIND>(ch, v, img, sx, 0u, 0u);
+    }
+    __syncthreads();
+    return bad;
+}
+
 // Down right factors (mid_r = R_r act_r) and the shared expert's down.
 __global__ void __launch_bounds__(256) m15_down_r_kernel(M15Dims d, M15Dev L, M15Ws ws) {
     extern __shared__ __align__(16) uint8_t lds[];
-    __shared__ float red[8];
     __shared__ float part[4 * 16];
     const int lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -361,15 +379,10 @@ __global__ void __launch_bounds__(256) m15_down_r_kernel(M15Dims d, M15Dev L, M1
         wave_share(S, wave, s0, n);
         Frag<HK_U3, 1> f[M15_D];
         fetch_first<HK_U3, 1>(o, T, s0, n, lane, f);
-        float* xs = reinterpret_cast<float*>(lds);
-        uint8_t* img = lds + (size_t)x_image_cols<HK_U3>(S) * 4u;
-        const float* x = ws.act + (size_t)slot * d.I;
-        XChunks<1> xc;
-        load_x<1>(BlockTeam{}, x, d.I, xc);
-        const int E = x_image<HK_U3, 1>(BlockTeam{}, xc, x, d.I, S, img, xs, 0, red, &bad);
+        bad = scatter_image<HK_U3>(ws.act + (size_t)slot * d.I, d.I, S, lds);
         float acc[1] = {0.0f};
-        run_steps<HK_U3, 1>(o, T, s0, n, img, S, lane, f, acc);
-        block_rows<1>(acc, part, E, v);
+        run_steps<HK_U3, 1>(o, T, s0, n, lds, S, lane, f, acc);
+        block_rows<1>(acc, part, 0, v);
         const uint32_t row = T * 16u + threadIdx.x;
         if (threadIdx.x < 16 && row < d.rank) ws.mid[(size_t)slot * d.rank + row] = v[0];
     } else {
@@ -380,14 +393,10 @@ __global__ void __launch_bounds__(256) m15_down_r_kernel(M15Dims d, M15Dev L, M1
         wave_share(S, wave, s0, n);
         Frag<HK_Q8, 1> f[M15_D];
         fetch_first<HK_Q8, 1>(o, T, s0, n, lane, f);
-        float* xs = reinterpret_cast<float*>(lds);
-        uint8_t* img = lds + (size_t)x_image_cols<HK_Q8>(S) * 4u;
-        XChunks<1> xc;
-        load_x<1>(BlockTeam{}, ws.act_s, d.SI, xc);
-        const int E = x_image<HK_Q8, 1>(BlockTeam{}, xc, ws.act_s, d.SI, S, img, xs, 0, red, &bad);
+        bad = scatter_image<HK_Q8>(ws.act_s, d.SI, S, lds);
         float acc[1] = {0.0f};
-        run_steps<HK_Q8, 1>(o, T, s0, n, img, S, lane, f, acc);
-        block_rows<1>(acc, part, E, v);
+        run_steps<HK_Q8, 1>(o, T, s0, n, lds, S, lane, f, acc);
+        block_rows<1>(acc, part, 0, v);
         const uint32_t row = T * 16u + threadIdx.x;
         if (threadIdx.x < 16 && row < d.H) ws.ys[row] = v[0];
     }
@@ -396,8 +405,7 @@ __global__ void __launch_bounds__(256) m15_down_r_kernel(M15Dims d, M15Dev L, M1
 
 // Down left factors and the combine; one wave per slot.
 __global__ void __launch_bounds__(1024) m15_down_l_kernel(M15Dims d, const float* __restrict__ h,
-                                                          float* __restrict__ out, M15Ws ws, uint32_t img_stride,
-                                                          uint32_t stage_floats) {
+                                                          float* __restrict__ out, M15Ws ws, uint32_t img_stride) {
     extern __shared__ __align__(16) uint8_t lds[];
     const uint32_t T = blockIdx.x, slots = d.K;
     const uint32_t slot = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -408,22 +416,24 @@ __global__ void __launch_bounds__(1024) m15_down_l_kernel(M15Dims d, const float
     Frag<HK_U3, 1> f[M15_D];
     fetch_first<HK_U3, 1>(o, T, 0u, S, lane, f);
     uint8_t* img = lds + (size_t)slot * img_stride;
-    float* xs = reinterpret_cast<float*>(lds + (size_t)slots * img_stride) + (size_t)slot * stage_floats;
-    float* part = reinterpret_cast<float*>(lds + (size_t)slots * img_stride) + (size_t)slots * stage_floats;
-    int E = 0;
+    float* part = reinterpret_cast<float*>(lds + (size_t)slots * img_stride);
     if (active) {
-        bool bad = false;
-        const WaveTeam team{(uint32_t)lane};
+        // the wave's x image of mid_r (E = 0), one 8-column chunk per lane and round
         const float* x = ws.mid + (size_t)slot * d.rank;
-        XChunks<1> xc;
-        load_x<1>(team, x, d.rank, xc);
-        E = x_image<HK_U3, 1>(team, xc, x, d.rank, S, img, xs, 0, nullptr, &bad);
-        if (bad && lane == 0) atomicOr(ws.status, HK_DEVERR_NONFINITE);
+        image_zero_blocks<HK_U3>((uint32_t)lane, img, S);
+        float* sx = reinterpret_cast<float*>(img + (size_t)S * Kcfg<HK_U3>::P * A_TILE_STRIDE);
+        bool bad = false;
+        for (uint32_t ch = (uint32_t)lane; ch < S * 16u; ch += 64u) {
+            float4 v[2];
+            load_chunk(x, 8u * ch, d.rank, v);
+            bad |= image_chunk<HK_U3>(ch, v, img, sx, 0u, 0u);
+        }
+        if (__ballot(bad) != 0 && lane == 0) atomicOr(ws.status, HK_DEVERR_NONFINITE);
     }
     float acc[1] = {0.0f};
     run_steps<HK_U3, 1>(o, T, 0u, S, img, S, lane, f, acc);
     const float y = tile_row_sum(acc[0]);
-    if (lane < 16) part[slot * 16u + (uint32_t)lane] = active ? ldexpf(y, -E) * ws.w[slot] : 0.0f;
+    if (lane < 16) part[slot * 16u + (uint32_t)lane] = active ? y * ws.w[slot] : 0.0f;
     __syncthreads();
     if (threadIdx.x < 16) {
         // combined = sum_r out_r * w_r in route order, += gate * shared; out = h + combined
@@ -450,7 +460,7 @@ struct hk_moe15_layer {
     void* mem = nullptr;
     float* hbuf = nullptr;  // this layer's output inside a stack
     size_t lds_route = 0, lds_gu = 0, lds_dr = 0, lds_dl = 0;
-    uint32_t dl_img_stride = 0, dl_stage = 0, n_route_blocks = 0, n_dr_blocks = 0;
+    uint32_t dl_img_stride = 0, n_route_blocks = 0, n_dr_blocks = 0;
 };
 
 static inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -513,11 +523,9 @@ extern "C" int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* s, h
                    Sl = n_steps_for(HK_U3, rank), Ss = SI ? n_steps_for(HK_Q8, SI) : 0u;
     L->lds_route = x_lds_bytes<HK_Q8>(Sq);
     L->lds_gu = align16(x_lds_bytes<HK_BIN>(Sb)) + (size_t)H * 4u + (size_t)RICE_BATCH * 4u;
-    L->lds_dr = std::max((size_t)x_image_cols<HK_U3>(Sr) * 4u + x_lds_bytes<HK_U3>(Sr),
-                         SI ? (size_t)x_image_cols<HK_Q8>(Ss) * 4u + x_lds_bytes<HK_Q8>(Ss) : (size_t)0);
+    L->lds_dr = std::max(x_lds_bytes<HK_U3>(Sr), SI ? x_lds_bytes<HK_Q8>(Ss) : (size_t)0);
     L->dl_img_stride = (uint32_t)align16(x_lds_bytes<HK_U3>(Sl));
-    L->dl_stage = std::min(x_image_cols<HK_U3>(Sl), 8u * 64u);
-    L->lds_dl = (size_t)K * (L->dl_img_stride + L->dl_stage * 4u) + (size_t)K * 16u * 4u;
+    L->lds_dl = (size_t)K * L->dl_img_stride + (size_t)K * 16u * 4u;
     if (std::max({L->lds_route, L->lds_gu, L->lds_dr, L->lds_dl}) > 64u * 1024u)
         return set_error(ctx, HK_E_UNSUPPORTED, "mixed-1p5 layer: shapes need more than 64 KB of LDS per workgroup");
     L->n_route_blocks = rv.n_tiles + (SI ? 1u + s->shared_gate_proj->view.n_tiles : 0u) + Sb;
@@ -611,7 +619,7 @@ extern "C" int hk_moe15_decode_layer(hk_ctx* ctx, hk_moe15_layer* L, const float
         hipLaunchKernelGGL((m15_gate_up_kernel<8>), gg, dim3(256), L->lds_gu, s, d, L->dev, L->ws, ids, weights);
     hipLaunchKernelGGL(m15_down_r_kernel, dim3(L->n_dr_blocks), dim3(256), L->lds_dr, s, d, L->dev, L->ws);
     hipLaunchKernelGGL(m15_down_l_kernel, dim3(n_tiles_for(d.H)), dim3(64u * d.K), L->lds_dl, s, d, h, out, L->ws,
-                       L->dl_img_stride, L->dl_stage);
+                       L->dl_img_stride);
     return check_hip(ctx, hipGetLastError(), "mixed-1p5 layer launch");
 }
 
