@@ -132,6 +132,30 @@ __device__ __forceinline__ void copy16x2_to_lds(uint4* dst0, const uint4* src0, 
     }
 }
 
+// Three such copies at once, every load unconditional (an index past the
+// end re-reads the last piece of src2): one latency for all three.
+template <int PT>
+__device__ __forceinline__ void copy16x3_to_lds(uint4* dst0, const uint4* src0, uint32_t n0, uint4* dst1,
+                                                const uint4* src1, uint32_t n1, uint4* dst2, const uint4* src2,
+                                                uint32_t n2, uint32_t tid, uint32_t nthreads) {
+    const uint32_t n01 = n0 + n1, n = n01 + n2;
+    for (uint32_t b = 0; b < n; b += PT * nthreads) {
+        uint4 v[PT];
+#pragma unroll
+        for (int i = 0; i < PT; ++i) {
+            const uint32_t k = b + tid + (uint32_t)i * nthreads;
+            v[i] = ldg(k < n0 ? src0 + k : k < n01 ? src1 + (k - n0) : src2 + min(k - n01, n2 - 1u));
+        }
+#pragma unroll
+        for (int i = 0; i < PT; ++i) {
+            const uint32_t k = b + tid + (uint32_t)i * nthreads;
+            if (k < n0) dst0[k] = v[i];
+            else if (k < n01) dst1[k - n0] = v[i];
+            else if (k < n) dst2[k - n01] = v[i];
+        }
+    }
+}
+
 // Workgroup -> (organ, part).  Workgroups are dispatched to the 8 XCDs round
 // robin by linear id, so ids 8 apart share an XCD and its L2: each run of
 // 8 * parts ids covers 8 organs with id % 8 selecting the organ, and all

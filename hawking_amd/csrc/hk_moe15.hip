@@ -46,6 +46,22 @@ struct M15Dims {
     float eps;
 };
 
+// What differs between one routed expert's gate/up and another's (32 bytes):
+// every other field of their views is the same (one shape per layer), and
+// within an organ the scales and the residual records sit at offsets from
+// the data and the row pointers that are the same for every expert
+// (checked at create), so the gate/up kernel copies the whole table into
+// LDS while its top-k runs and forms the slot's views with no dependent
+// global load.
+struct M15Expert {
+    const uint8_t* gate;    // gate data
+    const uint8_t* up;      // up data
+    const uint32_t* rptr;   // up residual row pointers
+    float rscale;           // up residual scale
+    uint32_t pad;
+};
+static_assert(sizeof(M15Expert) == 32, "an expert record is two 16-byte pieces");
+
 // The layer's constants: single organs by value, per-expert tables in device memory.
 struct M15Dev {
     const float* norm_w;
@@ -55,6 +71,8 @@ struct M15Dev {
     const ResView* res;                      // [E] its residual
     const OrganView* dr;                     // [E] down right factor (rank x I)
     const OrganView* dl;                     // [E] down left factor (H x rank)
+    const M15Expert* ex;                     // [E] compact gate/up records
+    uint32_t g_soff, u_soff, rec_off;        // scales - data (gate, up), recs - row_ptr (bytes)
 };
 
 struct M15Ws {
@@ -289,6 +307,10 @@ __global__ void __launch_bounds__(256) m15_gate_up_kernel(M15Dims d, M15Dev L, M
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t S = n_steps_for(HK_BIN, d.H), ib = (uint32_t)x_lds_bytes<HK_BIN>(S);
     const uint32_t ib16 = (ib + 15u) & ~15u;
+    // expert 0's views: every field but the pointers is every expert's
+    const OrganView g0 = L.gate[0], u0 = L.up[0];
+    const ResView r0v = L.res[0];
+    M15Expert* ext = reinterpret_cast<M15Expert*>(lds + ib16 + (size_t)d.H * 4u + (size_t)RICE_BATCH * 4u);
     if (wave == 0) {
         const bool pub = T == 0 && slot == 0;
         const ArgBest mine = softmax_topk_wave<NPL>(ws.logits, d.E, d.K, 1, pub ? ws.ids : nullptr,
@@ -299,10 +321,11 @@ __global__ void __launch_bounds__(256) m15_gate_up_kernel(M15Dims d, M15Dev L, M
         }
         if ((uint32_t)lane == slot) sel_id = mine.i;
     } else {
-        // the binary image and xn (for the residual) into LDS
-        copy16x2_to_lds<6>(reinterpret_cast<uint4*>(lds), reinterpret_cast<const uint4*>(ws.img), ib / 16u,
-                           reinterpret_cast<uint4*>(lds + ib16), reinterpret_cast<const uint4*>(ws.xn), d.H / 4u,
-                           threadIdx.x - 64u, blockDim.x - 64u);
+        // the binary image, xn (for the residual) and the expert records into LDS
+        copy16x3_to_lds<12>(reinterpret_cast<uint4*>(lds), reinterpret_cast<const uint4*>(ws.img), ib / 16u,
+                            reinterpret_cast<uint4*>(lds + ib16), reinterpret_cast<const uint4*>(ws.xn), d.H / 4u,
+                            reinterpret_cast<uint4*>(ext), reinterpret_cast<const uint4*>(L.ex), 2u * d.E,
+                            threadIdx.x - 64u, blockDim.x - 64u);
     }
     __syncthreads();
     const int32_t id = sel_id;
@@ -318,14 +341,22 @@ __global__ void __launch_bounds__(256) m15_gate_up_kernel(M15Dims d, M15Dev L, M
         if (!ok && threadIdx.x == 0) atomicOr(ws.status, HK_DEVERR_ROUTE);
     }
     if (!ok) return;
-    const OrganView o[2] = {L.gate[id], L.up[id]};
-    if (T >= o[0].n_tiles) return;
+    if (T >= g0.n_tiles) return;
+    const M15Expert ex = ext[id];
+    OrganView o[2] = {g0, u0};
+    o[0].data = ex.gate;
+    o[0].scales = reinterpret_cast<const uint16_t*>(ex.gate + L.g_soff);
+    o[1].data = ex.up;
+    o[1].scales = reinterpret_cast<const uint16_t*>(ex.up + L.u_soff);
     uint32_t s0, n;
     wave_share(S, wave, s0, n);
     Frag<HK_BIN, 2> f[M15_D];
     fetch_first<HK_BIN, 2>(o, T, s0, n, lane, f);
     // the residual's record ranges and first records, in flight with the weights
-    const ResView rv = L.res[id];
+    ResView rv = r0v;
+    rv.row_ptr = ex.rptr;
+    rv.recs = reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(ex.rptr) + L.rec_off);
+    rv.scale = ex.rscale;
     const uint32_t r0 = T * 16u, r1 = min(r0 + 16u, d.I);
     RiceTile rt;
     rice_prefetch(rv, r0, r1, rt);
@@ -516,13 +547,30 @@ extern "C" int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* s, h
         rvv[e] = r->view;
         res[e] = u->res;
     }
+    // the compact gate/up records: scales and residual records must sit at
+    // the same offsets from the data and the row pointers in every expert
+    auto byte_off = [](const void* a, const void* b) {
+        return (int64_t)(reinterpret_cast<uintptr_t>(a) - reinterpret_cast<uintptr_t>(b));
+    };
+    const int64_t g_soff = byte_off(gv[0].scales, gv[0].data), u_soff = byte_off(uv[0].scales, uv[0].data),
+                  rec_off = byte_off(res[0].recs, res[0].row_ptr);
+    std::vector<M15Expert> exv(E);
+    for (uint32_t e = 0; e < E; ++e) {
+        if (byte_off(gv[e].scales, gv[e].data) != g_soff || byte_off(uv[e].scales, uv[e].data) != u_soff ||
+            byte_off(res[e].recs, res[e].row_ptr) != rec_off)
+            return set_error(ctx, HK_E_UNSUPPORTED,
+                             "mixed-1p5 layer: expert organs must come from the library's uploads (same layout)");
+        exv[e] = M15Expert{gv[e].data, uv[e].data, res[e].row_ptr, res[e].scale, 0u};
+    }
+    if (g_soff < 0 || u_soff < 0 || rec_off < 0 || g_soff > 0xFFFFFFFF || u_soff > 0xFFFFFFFF || rec_off > 0xFFFFFFFF)
+        return set_error(ctx, HK_E_UNSUPPORTED, "mixed-1p5 layer: unexpected organ layout");
     std::unique_ptr<hk_moe15_layer> L(new hk_moe15_layer());
     L->d = M15Dims{H, I, SI, E, K, rank, s->eps};
     // dynamic LDS of the four kernels (each within 64 KB)
     const uint32_t Sb = n_steps_for(HK_BIN, H), Sq = n_steps_for(HK_Q8, H), Sr = n_steps_for(HK_U3, I),
                    Sl = n_steps_for(HK_U3, rank), Ss = SI ? n_steps_for(HK_Q8, SI) : 0u;
     L->lds_route = x_lds_bytes<HK_Q8>(Sq);
-    L->lds_gu = align16(x_lds_bytes<HK_BIN>(Sb)) + (size_t)H * 4u + (size_t)RICE_BATCH * 4u;
+    L->lds_gu = align16(x_lds_bytes<HK_BIN>(Sb)) + (size_t)H * 4u + (size_t)RICE_BATCH * 4u + (size_t)E * sizeof(M15Expert);
     L->lds_dr = std::max(x_lds_bytes<HK_U3>(Sr), SI ? x_lds_bytes<HK_Q8>(Ss) : (size_t)0);
     L->dl_img_stride = (uint32_t)align16(x_lds_bytes<HK_U3>(Sl));
     L->lds_dl = (size_t)K * L->dl_img_stride + (size_t)K * 16u * 4u;
@@ -539,7 +587,7 @@ extern "C" int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* s, h
     };
     const size_t o_norm = take(H * 4), o_gate = take(E * sizeof(OrganView)), o_up = take(E * sizeof(OrganView)),
                  o_res = take(E * sizeof(ResView)), o_dr = take(E * sizeof(OrganView)),
-                 o_dl = take(E * sizeof(OrganView)), o_logits = take(E * 4), o_glogit = take(16), o_xn = take(H * 4),
+                 o_dl = take(E * sizeof(OrganView)), o_ex = take(E * sizeof(M15Expert)), o_logits = take(E * 4), o_glogit = take(16), o_xn = take(H * 4),
                  o_img = take(x_lds_bytes<HK_BIN>(Sb)), o_imge = take(4), o_act = take((size_t)K * I * 4),
                  o_acts = take(SI * 4 + 16), o_mid = take((size_t)K * rank * 4), o_ys = take(H * 4),
                  o_ids = take(K * 4), o_w = take(K * 4), o_sel = take(2 * K * sizeof(OrganView)),
@@ -560,6 +608,10 @@ extern "C" int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* s, h
     dv.res = reinterpret_cast<const ResView*>(m + o_res);
     dv.dr = reinterpret_cast<const OrganView*>(m + o_dr);
     dv.dl = reinterpret_cast<const OrganView*>(m + o_dl);
+    dv.ex = reinterpret_cast<const M15Expert*>(m + o_ex);
+    dv.g_soff = (uint32_t)g_soff;
+    dv.u_soff = (uint32_t)u_soff;
+    dv.rec_off = (uint32_t)rec_off;
     M15Ws& w = L->ws;
     w.logits = reinterpret_cast<float*>(m + o_logits);
     w.gate = reinterpret_cast<float*>(m + o_glogit);
@@ -585,6 +637,7 @@ extern "C" int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* s, h
     if (!rc) rc = up_copy(dv.res, res.data(), E * sizeof(ResView));
     if (!rc) rc = up_copy(dv.dr, rvv.data(), E * sizeof(OrganView));
     if (!rc) rc = up_copy(dv.dl, lv.data(), E * sizeof(OrganView));
+    if (!rc) rc = up_copy(dv.ex, exv.data(), E * sizeof(M15Expert));
     if (rc) {
         (void)hipFree(L->mem);
         return rc;
