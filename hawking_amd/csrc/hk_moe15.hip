@@ -350,16 +350,18 @@ __global__ void __launch_bounds__(256) m15_gate_up_kernel(M15Dims d, M15Dev L, M
     o[1].scales = reinterpret_cast<const uint16_t*>(ex.up + L.u_soff);
     uint32_t s0, n;
     wave_share(S, wave, s0, n);
-    Frag<HK_BIN, 2> f[M15_D];
-    fetch_first<HK_BIN, 2>(o, T, s0, n, lane, f);
-    // the residual's record ranges and first records, in flight with the weights
+    // the residual's row pointers first, then the weights, then the first
+    // records (which wait for the row pointers only)
     ResView rv = r0v;
     rv.row_ptr = ex.rptr;
     rv.recs = reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(ex.rptr) + L.rec_off);
     rv.scale = ex.rscale;
     const uint32_t r0 = T * 16u, r1 = min(r0 + 16u, d.I);
     RiceTile rt;
-    rice_prefetch(rv, r0, r1, rt);
+    rice_ranges(rv, r0, r1, rt);
+    Frag<HK_BIN, 2> f[M15_D];
+    fetch_first<HK_BIN, 2>(o, T, s0, n, lane, f);
+    rice_first_records(rv, rt);
     const int E = ws.img_e[0];
     float acc[2] = {0.0f, 0.0f};
     run_steps<HK_BIN, 2>(o, T, s0, n, lds, S, lane, f, acc);
@@ -442,6 +444,11 @@ __global__ void __launch_bounds__(1024) m15_down_l_kernel(M15Dims d, const float
     const uint32_t slot = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const OrganView o[1] = {ws.sel[slot * 2u + 1u]};
+    // the combine's inputs (the slot's weight, and in the first 16 threads
+    // the tile's residual rows, the shared expert's output and its gate)
+    // are loaded now, unconditionally, in flight with everything else
+    const uint32_t crow = min(T * 16u + (threadIdx.x & 15u), d.H - 1u);
+    const float wslot = ws.w[slot], hres = h[crow], ysh = d.SI ? ws.ys[crow] : 0.0f, gsh = ws.gate[1];
     const bool active = T < o[0].n_tiles;
     const uint32_t S = active ? o[0].steps : 0u;
     Frag<HK_U3, 1> f[M15_D];
@@ -464,7 +471,7 @@ __global__ void __launch_bounds__(1024) m15_down_l_kernel(M15Dims d, const float
     float acc[1] = {0.0f};
     run_steps<HK_U3, 1>(o, T, 0u, S, img, S, lane, f, acc);
     const float y = tile_row_sum(acc[0]);
-    if (lane < 16) part[slot * 16u + (uint32_t)lane] = active ? y * ws.w[slot] : 0.0f;
+    if (lane < 16) part[slot * 16u + (uint32_t)lane] = active ? y * wslot : 0.0f;
     __syncthreads();
     if (threadIdx.x < 16) {
         // combined = sum_r out_r * w_r in route order, += gate * shared; out = h + combined
@@ -472,8 +479,8 @@ __global__ void __launch_bounds__(1024) m15_down_l_kernel(M15Dims d, const float
         float comb = 0.0f;
         for (uint32_t r = 0; r < slots; ++r) comb += part[r * 16u + threadIdx.x];
         if (row < d.H) {
-            if (d.SI) comb += ws.ys[row] * ws.gate[1];
-            const float v = h[row] + comb;
+            if (d.SI) comb += ysh * gsh;
+            const float v = hres + comb;
             out[row] = v;
             if (!isfinite(v)) atomicOr(ws.status, HK_DEVERR_NONFINITE);
         }

@@ -24,6 +24,23 @@ __device__ __forceinline__ void rice_load_batch(const ResView& v, uint32_t base,
     }
 }
 
+// rice_prefetch in two parts, so that loads issued between them (weights)
+// do not hold back the first records: rice_ranges loads the row pointers,
+// rice_first_records (which waits for them) the first batch of records.
+__device__ __forceinline__ void rice_ranges(const ResView& v, uint32_t r0, uint32_t r1, RiceTile& t) {
+    t.e0 = ldg(v.row_ptr + r0);
+    t.e1 = ldg(v.row_ptr + r1);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t row = min(r0 + threadIdx.x + 256u * (uint32_t)h, r1);
+        t.my0[h] = ldg(v.row_ptr + row);
+        t.my1[h] = ldg(v.row_ptr + min(row + 1u, r1));
+    }
+}
+__device__ __forceinline__ void rice_first_records(const ResView& v, RiceTile& t) {
+    rice_load_batch(v, t.e0 & ~7u, t.e1, t.rv);
+}
+
 __device__ __forceinline__ void rice_prefetch(const ResView& v, uint32_t r0, uint32_t r1, RiceTile& t) {
     t.e0 = ldg(v.row_ptr + r0);
     t.e1 = ldg(v.row_ptr + r1);
