@@ -52,8 +52,7 @@ __host__ __device__ inline uint32_t gemv_max_tiles(int kind, uint32_t steps) {
 // headers of the workgroup's tiles, then the workgroup's row outputs.
 template <int KIND>
 __host__ __device__ constexpr size_t gemv_hdr_offset(uint32_t steps) {
-    return x_lds_bytes<KIND>(steps) + (size_t)(steps * (uint32_t)Kcfg<KIND>::STEP_COLS < 2048u
-                                                   ? steps * (uint32_t)Kcfg<KIND>::STEP_COLS : 2048u) * sizeof(float);
+    return x_lds_bytes<KIND>(steps);
 }
 
 // The terminal head's extras (HEAD launches): x = RMSNorm(1+w)(h) is formed
@@ -184,12 +183,30 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const
         }
     }
     if constexpr (HEAD) head_norm_chunks<NC>(xc, o.cols, ha, red);
+    // the x image with E = 0: every thread scatters its own chunks (no
+    // block-wide maximum, no gather pass); a unit's chunks are consecutive
+    // threads, active together
     bool bad = false;
-    float* xq = reinterpret_cast<float*>(lds + x_lds_bytes<KIND>(o.steps));
-    const int E = x_image<KIND, NC>(BlockTeam{}, xc, x, o.cols, o.steps, lds, xq, 0u, red, &bad);
-    if (bad && threadIdx.x == 0 && status) atomicOr(status, 1u);
+    {
+        const uint32_t nch = o.steps * (uint32_t)Kcfg<KIND>::STEP_COLS / 8u;
+        float* sxw = reinterpret_cast<float*>(lds + (size_t)o.steps * Kcfg<KIND>::P * A_TILE_STRIDE);
+        if (threadIdx.x < 64u) image_zero_blocks<KIND>(threadIdx.x, lds, o.steps);
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const uint32_t ch = threadIdx.x + 256u * (uint32_t)j;
+            if (ch < nch) bad |= image_chunk<KIND>(ch, xc.v[j], lds, sxw, 0u, 0u);
+        }
+        for (uint32_t ch = threadIdx.x + 256u * NC; ch < nch; ch += 256u) {
+            float4 v[2];
+            load_chunk(x, 8u * ch, o.cols, v);
+            bad |= image_chunk<KIND>(ch, v, lds, sxw, 0u, 0u);
+        }
+        __syncthreads();
+    }
+    const int E = 0;
+    if (bad && status) atomicOr(status, 1u);
     if constexpr (HEAD)
-        if (bad && threadIdx.x == 0) atomicOr(reinterpret_cast<uint32_t*>(ha.key + 1), 1u);
+        if (bad) atomicOr(reinterpret_cast<uint32_t*>(ha.key + 1), 1u);
     const ImageA A{lds, a_lane_offset(lane)};
     const float* SX = reinterpret_cast<const float*>(lds + (size_t)o.steps * Kcfg<KIND>::P * A_TILE_STRIDE);
 

@@ -12,7 +12,8 @@
 // (+-scale) * x[col] in LDS, and each row's thread adds its products in index
 // order -- the reference's serial apply order, so given the same base the
 // correction is bit-exact.
-#include <hipcub/hipcub.hpp>
+#include <rocprim/device/device_radix_sort.hpp>
+#include <rocprim/device/device_scan.hpp>
 
 #include "hk_internal.h"
 #include "hk_rice.h"
@@ -238,21 +239,21 @@ hipError_t pack_binary_rice_device(const float* w, uint32_t rows, uint32_t cols,
     out->count = count;
     hipError_t e = hipSuccess;
     // layout of one temporary allocation
-    size_t cub_sort = 0, cub_sort2 = 0, cub_scan = 0;
-    if ((e = hipcub::DeviceRadixSort::SortPairs(nullptr, cub_sort, (const uint32_t*)nullptr, (uint32_t*)nullptr,
-                                                (const uint32_t*)nullptr, (uint32_t*)nullptr, (int)n, 0, 32, s)))
+    size_t sort_tmp = 0, sort_tmp2 = 0, scan_tmp = 0;
+    if ((e = rocprim::radix_sort_pairs(nullptr, sort_tmp, (const uint32_t*)nullptr, (uint32_t*)nullptr,
+                                       (const uint32_t*)nullptr, (uint32_t*)nullptr, n, 0u, 32u, s)))
         return e;
-    if ((e = hipcub::DeviceRadixSort::SortKeys(nullptr, cub_sort2, (const uint32_t*)nullptr, (uint32_t*)nullptr,
-                                               (int)count, 0, 32, s)))
+    if ((e = rocprim::radix_sort_keys(nullptr, sort_tmp2, (const uint32_t*)nullptr, (uint32_t*)nullptr, count, 0u, 32u,
+                                      s)))
         return e;
     const size_t nd = count - 1;
-    if (nd && (e = hipcub::DeviceScan::ExclusiveSum(nullptr, cub_scan, (const uint64_t*)nullptr, (uint64_t*)nullptr,
-                                                    (int)nd, s)))
+    if (nd && (e = rocprim::exclusive_scan(nullptr, scan_tmp, (const uint64_t*)nullptr, (uint64_t*)nullptr, (uint64_t)0,
+                                           nd, rocprim::plus<uint64_t>(), s)))
         return e;
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
-    const size_t cub_bytes = std::max(cub_sort, std::max(cub_sort2, cub_scan));
+    const size_t tmp_bytes = std::max(sort_tmp, std::max(sort_tmp2, scan_tmp));
     const size_t total =
-        al(n * 4) * 5 + al(count * 4) * 2 + al(nd * 8) * 2 + al(sizeof(RiceStats)) + al(cub_bytes) + 256;
+        al(n * 4) * 5 + al(count * 4) * 2 + al(nd * 8) * 2 + al(sizeof(RiceStats)) + al(tmp_bytes) + 256;
     uint8_t* mem = nullptr;
     if ((e = hipMalloc(&mem, total))) return e;
     uint8_t* p = mem;
@@ -271,7 +272,7 @@ hipError_t pack_binary_rice_device(const float* w, uint32_t rows, uint32_t cols,
     uint64_t* len = (uint64_t*)take(nd * 8);
     uint64_t* off = (uint64_t*)take(nd * 8);
     RiceStats* st = (RiceStats*)take(sizeof(RiceStats));
-    void* cub_tmp = take(cub_bytes);
+    void* tmp = take(tmp_bytes);
     uint32_t* bad = (uint32_t*)take(4);
     RiceStats hs{};
     uint32_t hbad = 0;
@@ -281,10 +282,10 @@ hipError_t pack_binary_rice_device(const float* w, uint32_t rows, uint32_t cols,
         hipLaunchKernelGGL(rice_residual_kernel, dim3(grid_n(n)), dim3(256), 0, s, w, n, bin_scales, bin_signs, r, key,
                            val);
         if ((e = hipGetLastError())) break;
-        size_t tb = cub_bytes;
-        if ((e = hipcub::DeviceRadixSort::SortPairs(cub_tmp, tb, key, key2, val, val2, (int)n, 0, 32, s))) break;
-        tb = cub_bytes;
-        if ((e = hipcub::DeviceRadixSort::SortKeys(cub_tmp, tb, val2, idx, (int)count, 0, 32, s))) break;
+        size_t tb = tmp_bytes;
+        if ((e = rocprim::radix_sort_pairs(tmp, tb, key, key2, val, val2, n, 0u, 32u, s))) break;
+        tb = tmp_bytes;
+        if ((e = rocprim::radix_sort_keys(tmp, tb, val2, idx, count, 0u, 32u, s))) break;
         hipLaunchKernelGGL(rice_stats_kernel, dim3(1), dim3(256), 0, s, r, idx, count, sel, res_signs, st);
         if ((e = hipGetLastError())) break;
         if ((e = hipMemcpyAsync(&hs, st, sizeof(hs), hipMemcpyDeviceToHost, s))) break;
@@ -303,8 +304,8 @@ hipError_t pack_binary_rice_device(const float* w, uint32_t rows, uint32_t cols,
         }
         hipLaunchKernelGGL(rice_len_kernel, dim3(grid_n(nd)), dim3(256), 0, s, idx, nd, st, len);
         if ((e = hipGetLastError())) break;
-        tb = cub_bytes;
-        if ((e = hipcub::DeviceScan::ExclusiveSum(cub_tmp, tb, len, off, (int)nd, s))) break;
+        tb = tmp_bytes;
+        if ((e = rocprim::exclusive_scan(tmp, tb, len, off, (uint64_t)0, nd, rocprim::plus<uint64_t>(), s))) break;
         if ((e = hipMemsetAsync(rice, 0, ((hs.bits + 31) / 32) * 4, s))) break;
         hipLaunchKernelGGL(rice_write_kernel, dim3(grid_n(nd)), dim3(256), 0, s, idx, nd, st, off,
                            reinterpret_cast<uint32_t*>(rice));

@@ -376,9 +376,9 @@ def test_u3_and_lowrank_reject_bad_geometry(ctx, oracle):
     with pytest.raises(HawkingError) as e:        # rank 8: not a multiple of 32 columns
         UniformFactor3(ctx, s, c, 16, 8)
     assert e.value.code == HK_E_GEOMETRY
-    s, c = oracle.uniform_pack(np.ones((1, 6304), np.float32), 1, 6304, 3, 64)
-    with pytest.raises(HawkingError) as e:        # past the 3-bit x image's 6272 columns (64 KB of LDS)
-        UniformFactor3(ctx, s, c, 1, 6304)
+    s, c = oracle.uniform_pack(np.ones((1, 7200), np.float32), 1, 7200, 3, 64)
+    with pytest.raises(HawkingError) as e:        # past the 3-bit x image's 7168 columns (64 KB of LDS)
+        UniformFactor3(ctx, s, c, 1, 7200)
     assert e.value.code == HK_E_GEOMETRY
     a, _ = _u3(ctx, oracle, np.ones((16, 64), np.float32))
     b, _ = _u3(ctx, oracle, np.ones((32, 32), np.float32))
