@@ -315,9 +315,8 @@ struct TileWalk {
     }
 };
 
-// LDS layout of the low-rank kernel: the right factor's x image and window,
-// mid (16 floats per right tile), the left factor's image and window, then
-// the left rows.
+// LDS layout of the low-rank kernel: the right factor's x image, mid (16
+// floats per right tile), the left factor's image, then the left rows.
 struct LowrankLds {
     size_t img_r, win_r, mid, img_l, win_l, ysh, total;
 };
@@ -325,11 +324,10 @@ __host__ __device__ inline LowrankLds lowrank_lds(const OrganView& l, const Orga
     LowrankLds L{};
     L.img_r = 0;
     L.win_r = L.img_r + x_lds_bytes<HK_U3>(r.steps);
-    const uint32_t cr = x_image_cols<HK_U3>(r.steps), cl = x_image_cols<HK_U3>(l.steps);
-    L.mid = L.win_r + (size_t)(cr < 2048u ? cr : 2048u) * 4u;
+    L.mid = L.win_r;
     L.img_l = L.mid + ((size_t)r.n_tiles * 16u * 4u + 15u) / 16u * 16u;
     L.win_l = L.img_l + x_lds_bytes<HK_U3>(l.steps);
-    L.ysh = L.win_l + (size_t)(cl < 2048u ? cl : 2048u) * 4u;
+    L.ysh = L.win_l;
     L.total = L.ysh + (size_t)l.n_tiles * 16u * 4u;
     return L;
 }
@@ -346,7 +344,6 @@ lowrank_kernel(const OrganView* __restrict__ lefts, const OrganView* __restrict_
                const float* __restrict__ xall, size_t x_stride, float* __restrict__ mid_all, size_t mid_stride,
                float* __restrict__ yall, size_t y_stride, uint32_t* status) {
     extern __shared__ __align__(16) uint8_t lds[];
-    __shared__ float red[4];
     uint32_t oi, part;
     organ_part(blockIdx.x, 1, n, &oi, &part);
     const OrganView rv = rights[oi], lv = lefts[oi];
@@ -364,25 +361,46 @@ lowrank_kernel(const OrganView* __restrict__ lefts, const OrganView* __restrict_
     wr.start(rv, 0, rv.n_tiles, wave, lane);
     TileWalk<HK_U3, 2, 3> wl;
     wl.start(lv, 0, lv.n_tiles, wave, lane);
-    bool bad = false, bad2 = false;
-    const int E1 = x_image<HK_U3, NC>(BlockTeam{}, xc, x, rv.cols, rv.steps, lds + M.img_r,
-                                      reinterpret_cast<float*>(lds + M.win_r), 0u, red, &bad);
+    // both x images with E = 0, scattered from each thread's chunks (the
+    // two launches' images to the bit: the GEMV builds them the same way)
+    bool bad = false;
+    {
+        uint8_t* img = lds + M.img_r;
+        float* sx = reinterpret_cast<float*>(img + (size_t)rv.steps * Kcfg<HK_U3>::P * A_TILE_STRIDE);
+        const uint32_t nch = rv.steps * (uint32_t)Kcfg<HK_U3>::STEP_COLS / 8u;
+        if (threadIdx.x < 64u) image_zero_blocks<HK_U3>(threadIdx.x, img, rv.steps);
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const uint32_t ch = threadIdx.x + 256u * (uint32_t)j;
+            if (ch < nch) bad |= image_chunk<HK_U3>(ch, xc.v[j], img, sx, 0u, 0u);
+        }
+        for (uint32_t ch = threadIdx.x + 256u * NC; ch < nch; ch += 256u) {
+            float4 v[2];
+            load_chunk(x, 8u * ch, rv.cols, v);
+            bad |= image_chunk<HK_U3>(ch, v, img, sx, 0u, 0u);
+        }
+        __syncthreads();
+    }
     wr.run(rv, 0, lds + M.img_r, lane, mid);
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < rv.rows; i += blockDim.x) {
-        const float m = ldexpf(mid[i], -E1);
-        mid[i] = m;
-        if (mid_all) mid_all[(size_t)oi * mid_stride + i] = m;
+    if (mid_all)
+        for (uint32_t i = threadIdx.x; i < rv.rows; i += blockDim.x) mid_all[(size_t)oi * mid_stride + i] = mid[i];
+    {
+        uint8_t* img = lds + M.img_l;
+        float* sx = reinterpret_cast<float*>(img + (size_t)lv.steps * Kcfg<HK_U3>::P * A_TILE_STRIDE);
+        const uint32_t nch = lv.steps * (uint32_t)Kcfg<HK_U3>::STEP_COLS / 8u;
+        if (threadIdx.x < 64u) image_zero_blocks<HK_U3>(threadIdx.x, img, lv.steps);
+        for (uint32_t ch = threadIdx.x; ch < nch; ch += 256u) {
+            float4 v[2];
+            load_chunk(mid, 8u * ch, rv.rows, v);
+            bad |= image_chunk<HK_U3>(ch, v, img, sx, 0u, 0u);
+        }
+        __syncthreads();
     }
-    __syncthreads();
-    XChunks<1> xm;
-    load_x<1>(BlockTeam{}, mid, rv.rows, xm);
-    const int E2 = x_image<HK_U3, 1>(BlockTeam{}, xm, mid, rv.rows, lv.steps, lds + M.img_l,
-                                     reinterpret_cast<float*>(lds + M.win_l), 0u, red, &bad2);
     wl.run(lv, 0, lds + M.img_l, lane, ysh);
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < lv.rows; i += blockDim.x) y[i] = ldexpf(ysh[i], -E2);
-    if ((bad || bad2) && threadIdx.x == 0 && status) atomicOr(status, 1u);
+    for (uint32_t i = threadIdx.x; i < lv.rows; i += blockDim.x) y[i] = ysh[i];
+    if (bad && status) atomicOr(status, 1u);
 }
 
 bool lowrank_fusable(const OrganView& l, const OrganView& r) {
