@@ -1470,8 +1470,9 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
     const size_t dpl = dense_per_layer(c);
     const size_t tab = align256((size_t)(c.n_experts + 1) * 3 * sizeof(OrganView));
     const size_t img = align256(moe_img_bytes(c.expert_kind, c.hidden));
+    const size_t dnh = align256((size_t)slots * hk::moe_dn_hdr_stride(c.hidden, imax) * 16);
     const size_t ws = align256(((size_t)c.n_experts + 4) * 4) + 3 * 256 + align256((size_t)slots * imax * 4) + img + 256 +
-                      2 * align256((size_t)c.hidden * 4);
+                      2 * align256((size_t)c.hidden * 4) + dnh;
     if (hipMalloc(&m->dense, dpl * c.n_layers) != hipSuccess || hipMalloc(&m->tables, tab * c.n_layers) != hipSuccess ||
         hipMalloc(&m->ws_mem, ws) != hipSuccess) {
         if (m->dense) (void)hipFree(m->dense);
@@ -1516,6 +1517,8 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
     m->hbuf[0] = reinterpret_cast<float*>(w);
     w += align256((size_t)c.hidden * 4);
     m->hbuf[1] = reinterpret_cast<float*>(w);
+    w += align256((size_t)c.hidden * 4);
+    m->ws.dn_hdr = reinterpret_cast<uint4*>(w);
     m->ws.status = ctx->dev_status;
     if (c.router == HK_ROUTER_SOFTMAX && (rc = alloc_stack(ctx, m))) {
         (void)hipFree(m->dense);

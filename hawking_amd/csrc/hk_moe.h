@@ -2,6 +2,7 @@
 #pragma once
 
 #include "hk_internal.h"
+#include "hk_tile.h"
 
 namespace hk {
 
@@ -49,8 +50,15 @@ struct MoeWs {
     float* gate;       // [2]: shared-gate logit, shared-gate value
     float* act;        // [(K+1) * Imax]
     uint8_t* img;      // x image (E = 0) of RMSNorm(h) for the gate/up organs
+    uint4* dn_hdr;     // [slots][moe_dn_hdr_stride]: the step headers of each slot's down organ (mixed), copied
+                       // by the gate/up kernel so the down kernel needs no route before them
     uint32_t* status;  // device error bits
 };
+
+// Headers per slot of the down organs (hidden rows, Imax columns).
+__host__ __device__ inline uint32_t moe_dn_hdr_stride(uint32_t H, uint32_t Imax) {
+    return n_tiles_for(H) * n_steps_for(HK_MIXED, Imax);
+}
 
 // Bytes of the gate/up x image and of the down kernel's LDS.
 size_t moe_img_bytes(int kind, uint32_t H);

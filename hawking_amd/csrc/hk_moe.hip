@@ -155,6 +155,8 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev
     // the slot's base views (expert 0's, or the shared expert's), loaded with the logits
     const uint32_t base = routed ? 0u : d.E * 3u;
     const OrganView g0 = L.table[base], u0 = L.table[base + 1u];
+    OrganView dn0{};
+    if constexpr (KIND == HK_MIXED) dn0 = L.table[base + 2u];
     if (routed && wave == 0) {
         const bool pub = lead && slot == 0;
         const ArgBest mine = softmax_topk_wave<NPL>(ws.logits, d.E, d.K, 1, pub ? ws.ids : nullptr,
@@ -182,7 +184,24 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev
     }
     // the slot's organs from the id: no table load between the route and the weights
     const OrganView g = routed ? advance_view(g0, (uint32_t)id, L.stride) : g0;
-    if (T >= g.n_tiles) return;
+    // mixed: this workgroup's share of the slot's down-organ step headers,
+    // loaded now and stored at the end (for the down kernel, which then
+    // needs no route before its weights)
+    uint4 dh = make_uint4(0u, 0u, 0u, 0u);
+    uint32_t dhi = 0xFFFFFFFFu;
+    if constexpr (KIND == HK_MIXED) {
+        const OrganView dn = routed ? advance_view(dn0, (uint32_t)id, L.stride) : dn0;
+        const uint32_t nh = dn.n_tiles * dn.steps, share = (nh + gridDim.x - 1u) / gridDim.x;
+        const uint32_t i = T * share + threadIdx.x;
+        if (threadIdx.x < share && i < nh) {
+            dh = ldg(dn.hdr + i);
+            dhi = slot * moe_dn_hdr_stride(d.H, d.Imax) + i;
+        }
+    }
+    if (T >= g.n_tiles) {
+        if (dhi != 0xFFFFFFFFu) ws.dn_hdr[dhi] = dh;
+        return;
+    }
     const OrganView u = routed ? advance_view(u0, (uint32_t)id, L.stride) : u0;
     const uint32_t per = (S + 3u) / 4u;
     const uint32_t s0 = min(wave * per, S), n = min(s0 + per, S) - s0;
@@ -229,6 +248,7 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev
         const uint32_t row = T * 16u + threadIdx.x;
         if (row < g.rows) ws.act[(size_t)slot * d.Imax + row] = (gv / (1.0f + expf(-gv))) * uv;
     }
+    if (dhi != 0xFFFFFFFFu) ws.dn_hdr[dhi] = dh;
 }
 
 // h_in and h_out may be the same vector (each row is read, then written, by
@@ -237,7 +257,7 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev
 // slot: it stages the slot's activations in LDS (loads issued before the
 // route is read), issues its weight steps, and builds the slot's x image with
 // E = 0 while they are in flight (image_wave: no barrier, no gather pass).
-template <int KIND, int D>
+template <int KIND, int D, bool HDR_WS>
 __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, MoeLayerDev L, const float* h_in, float* h_out,
                                                         MoeWs ws, const int32_t* __restrict__ ids,
                                                         const float* __restrict__ wts, uint32_t img_stride) {
@@ -251,6 +271,15 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, MoeLayerDev L
     // so they wait for no route) all in flight together
     const OrganView o0 = L.table[routed ? 2u : d.E * 3u + 2u];
     const int32_t idr = __builtin_amdgcn_readfirstlane(ids[min(slot, d.K - 1u)]);  // no branch before the load
+    // HDR_WS (mixed, per-layer launches): the slot's step headers as the
+    // gate/up kernel copied them, loaded with the route instead of after it
+    uint4 hws[D];
+    if constexpr (HDR_WS) {
+        const uint32_t ns = n_steps_for(HK_MIXED, d.Imax);
+#pragma unroll
+        for (int k = 0; k < D; ++k)
+            hws[k] = ldg(ws.dn_hdr + (size_t)slot * moe_dn_hdr_stride(d.H, d.Imax) + T * ns + min((uint32_t)k, ns - 1u));
+    }
     const int32_t id = routed ? idr : (int32_t)d.E;
     const uint32_t row = T * 16u + threadIdx.x;
     const float hres = h_in[min(row, d.H - 1u)];  // every lane loads (no branch); threads 0-15 use it
@@ -266,7 +295,10 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, MoeLayerDev L
     Frag<KIND, 1> f[D];
 #pragma unroll
     for (int k = 0; k < D; ++k)
-        if ((uint32_t)k < S) fetch_one<KIND, 1>(o, T, (uint32_t)k, lane, f[k], 0);
+        if ((uint32_t)k < S) {
+            if constexpr (HDR_WS) fetch_mixed<1>(o, hws[k], lane, f[k], 0);
+            else fetch_one<KIND, 1>(o, T, (uint32_t)k, lane, f[k], 0);
+        }
     const float wgt = !active ? 0.0f : (slot < d.K ? wts[slot] : ws.gate[1]);
     if (active) {
         bool bad = false;
@@ -407,7 +439,7 @@ static hipError_t launch_block(const MoeDims& d, const MoeLayerDev& L, const int
     const uint32_t img_stride = (uint32_t)moe_img_bytes(KIND, d.Imax);
     hipLaunchKernelGGL((moe_block_gate_up_kernel<KIND, 4>), dim3(gu_tiles, slots), dim3(256),
                        moe_block_gate_up_lds_bytes(KIND, d.H), s, d, L, ws, route_ids, x);
-    hipLaunchKernelGGL((moe_down_kernel<KIND, 4>), dim3(n_tiles_for(d.H)), dim3(64u * slots),
+    hipLaunchKernelGGL((moe_down_kernel<KIND, 4, false>), dim3(n_tiles_for(d.H)), dim3(64u * slots),
                        moe_down_lds_bytes(KIND, d.Imax, slots), s, d, L, out, out, ws, route_ids, route_weights,
                        img_stride);
     return hipGetLastError();
@@ -440,9 +472,16 @@ static hipError_t launch_layer(const MoeDims& d, const MoeLayerDev& L, const flo
         hipLaunchKernelGGL((moe_gate_up_kernel<KIND, 4, 32>), gg, dim3(256), gl, s, d, L, ws, ids_out, w_out);
     else
         hipLaunchKernelGGL((moe_gate_up_kernel<KIND, 4, 64>), gg, dim3(256), gl, s, d, L, ws, ids_out, w_out);
-    hipLaunchKernelGGL((moe_down_kernel<KIND, 4>), dim3(n_tiles_for(d.H)), dim3(64u * slots),
-                       moe_down_lds_bytes(KIND, d.Imax, slots), s, d, L, h_in, h_out, ws, ws.ids, ws.weights,
-                       img_stride);
+    // mixed: the down weights follow the headers the gate/up kernel copied
+    // (when every step of the down organs is in the first fetch)
+    if (KIND == HK_MIXED && n_steps_for(HK_MIXED, d.Imax) <= 4u)
+        hipLaunchKernelGGL((moe_down_kernel<KIND, 4, KIND == HK_MIXED>), dim3(n_tiles_for(d.H)), dim3(64u * slots),
+                           moe_down_lds_bytes(KIND, d.Imax, slots), s, d, L, h_in, h_out, ws, ws.ids, ws.weights,
+                           img_stride);
+    else
+        hipLaunchKernelGGL((moe_down_kernel<KIND, 4, false>), dim3(n_tiles_for(d.H)), dim3(64u * slots),
+                           moe_down_lds_bytes(KIND, d.Imax, slots), s, d, L, h_in, h_out, ws, ws.ids, ws.weights,
+                           img_stride);
     return hipGetLastError();
 }
 
