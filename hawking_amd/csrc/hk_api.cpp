@@ -557,7 +557,9 @@ extern "C" int hk_gemv(hk_ctx* ctx, const hk_organ* o, const float* x, float* y,
     hipStream_t st = static_cast<hipStream_t>(stream);
     rc = check_hip(ctx, launch_gemv_tiled(static_cast<const OrganView*>(o->view_dev), 1, o->view, x, 0, y, 0, st),
                    "gemv launch");
-    if (!rc && o->res_dev) rc = check_hip(ctx, launch_rice_apply(o->res_dev, 1, o->view.rows, o->view.cols, x, 0, y, 0, st), "rice apply");
+    if (!rc && o->res_dev)
+        rc = check_hip(ctx, launch_rice_apply(o->res_dev, 1, o->view.rows, o->view.cols, o->res_pieces, x, 0, y, 0, st),
+                       "rice apply");
     return rc;
 }
 
@@ -566,7 +568,7 @@ extern "C" int hk_rice_apply(hk_ctx* ctx, const hk_organ* o, const float* x, flo
     if (!o || !o->res_dev) return set_error(ctx, HK_E_INVALID_ARG, "hk_rice_apply: not an HGRAVR02 organ");
     int rc = check_vectors(ctx, "hk_rice_apply", x, 0, y, 0, 1, o->view);
     if (rc) return rc;
-    return check_hip(ctx, launch_rice_apply(o->res_dev, 1, o->view.rows, o->view.cols, x, 0, y, 0,
+    return check_hip(ctx, launch_rice_apply(o->res_dev, 1, o->view.rows, o->view.cols, o->res_pieces, x, 0, y, 0,
                                             static_cast<hipStream_t>(stream)),
                      "rice apply");
 }
@@ -594,6 +596,7 @@ extern "C" int hk_gemv_lowrank(hk_ctx* ctx, const hk_organ* left, const hk_organ
 struct hk_organ_set {
     OrganView* dev = nullptr;
     ResView* res_dev = nullptr;  // HGRAVR02 sets: the residual table
+    uint32_t res_pieces = 0;     // the most record pieces of any organ's apply part
     uint32_t n = 0;
     OrganView first{};
 };
@@ -625,7 +628,10 @@ extern "C" int hk_organ_set_create(hk_ctx* ctx, const hk_organ* const* organs, u
     }
     if (organs[0]->res_dev) {
         std::vector<ResView> res(n);
-        for (uint32_t i = 0; i < n; ++i) res[i] = organs[i]->res;
+        for (uint32_t i = 0; i < n; ++i) {
+            res[i] = organs[i]->res;
+            set->res_pieces = std::max(set->res_pieces, organs[i]->res_pieces);
+        }
         if (hipMalloc(&set->res_dev, n * sizeof(ResView)) != hipSuccess) {
             (void)hipFree(set->dev);
             delete set;
@@ -665,7 +671,8 @@ extern "C" int hk_gemv_set(hk_ctx* ctx, const hk_organ_set* set, const float* x,
     rc = check_hip(ctx, launch_gemv_tiled(set->dev, set->n, set->first, x, x_stride, y, y_stride, st),
                    "gemv_set launch");
     if (!rc && set->res_dev)
-        rc = check_hip(ctx, launch_rice_apply(set->res_dev, set->n, set->first.rows, set->first.cols, x, x_stride, y,
+        rc = check_hip(ctx, launch_rice_apply(set->res_dev, set->n, set->first.rows, set->first.cols, set->res_pieces, x,
+                                              x_stride, y,
                                               y_stride, st),
                        "rice apply");
     return rc;
@@ -813,8 +820,11 @@ extern "C" int hk_organ_synthetic(hk_ctx* ctx, int32_t kind, int32_t group, uint
 
 // Rice expand into the CSR the apply reads (unpack_rice + expand_rice_indices +
 // rice_q1_row_ptr, q80_mixed_decode.rs:348-381,462-507), on the host at bind
-// time as the reference's parse does.  recs is padded with zeros to a multiple
-// of 8 (the apply reads 16-byte pieces).  Returns "" or the error.
+// time as the reference's parse does; records are column << 1 | sign.  Each
+// row's records are then padded to a multiple of 4 with cols << 1 (the apply
+// reads a row four records at a time and the padding adds -0, which changes
+// no sum), and recs to a multiple of 8 (16-byte pieces).  Returns "" or the
+// error.
 static std::string rice_expand_csr(const uint8_t* rice, size_t len, uint32_t first, uint32_t k, size_t count,
                                    uint32_t rows, uint32_t cols, const uint8_t* signs, std::vector<uint32_t>& row_ptr,
                                    std::vector<uint16_t>& recs) {
@@ -822,7 +832,7 @@ static std::string rice_expand_csr(const uint8_t* rice, size_t len, uint32_t fir
     row_ptr.assign((size_t)rows + 1, 0u);
     recs.assign((count + 7) & ~(size_t)7, 0u);
     auto put = [&](size_t i, uint64_t f) {
-        recs[i] = (uint16_t)((f % cols) | ((uint32_t)((signs[i >> 3] >> (i & 7u)) & 1u) << 15));
+        recs[i] = (uint16_t)(((f % cols) << 1) | ((uint32_t)(signs[i >> 3] >> (i & 7u)) & 1u));
         row_ptr[f / cols + 1] += 1;
     };
     if (first >= limit) return "rice residual index out of range";
@@ -849,6 +859,13 @@ static std::string rice_expand_csr(const uint8_t* rice, size_t len, uint32_t fir
         put(i, acc);
     }
     for (uint32_t r = 0; r < rows; ++r) row_ptr[r + 1] += row_ptr[r];
+    std::vector<uint32_t> pp((size_t)rows + 1, 0u);
+    for (uint32_t r = 0; r < rows; ++r) pp[r + 1] = pp[r] + ((row_ptr[r + 1] - row_ptr[r] + 3u) & ~3u);
+    std::vector<uint16_t> pr(((size_t)pp[rows] + 7) & ~(size_t)7, (uint16_t)(cols << 1));
+    for (uint32_t r = 0; r < rows; ++r)
+        std::copy(recs.begin() + row_ptr[r], recs.begin() + row_ptr[r + 1], pr.begin() + pp[r]);
+    row_ptr.swap(pp);
+    recs.swap(pr);
     return "";
 }
 
@@ -899,7 +916,8 @@ static int upload_rice(hk_ctx* ctx, const hk_rice_q1* s, hipStream_t st, hk_orga
             o->res.rows = s->rows;
             o->res.cols = s->cols;
             o->res.scale = f16_to_f32_host(s->residual_scale_f16);
-            o->res.count = (uint32_t)count;
+            o->res.count = row_ptr[s->rows];
+            o->res_pieces = rice_part_pieces(row_ptr.data(), s->rows, RICE_APPLY_ROWS);
             ResView* rd = reinterpret_cast<ResView*>(m + a_rp + a_rec);
             rc = check_hip(ctx, hipMemcpy(m, row_ptr.data(), row_ptr.size() * 4, hipMemcpyHostToDevice), "row_ptr upload");
             if (!rc) rc = check_hip(ctx, hipMemcpy(m + a_rp, recs.data(), recs.size() * 2, hipMemcpyHostToDevice), "record upload");

@@ -266,8 +266,11 @@ struct RepackJob {
     uint32_t* counts;
 };
 hipError_t launch_repack_batch(int kind, const RepackJob* jobs_dev, uint32_t n, size_t max_items, hipStream_t s);
-// The residual of an HGRAVR02 organ on the device: CSR over its outliers
-// (row_ptr[rows + 1]; recs[count] = column | sign << 15, sign 1 = +scale).
+// The residual of an HGRAVR02 organ on the device: CSR over its outliers,
+// row_ptr[rows + 1] and recs[count] = column << 1 | sign (sign 1 = +scale),
+// each row's records in index order and padded to a multiple of 4 with the
+// record cols << 1 (a column past the end: adds nothing); count (the padded
+// total) is a multiple of 4 and recs is readable to the next multiple of 8.
 struct ResView {
     const uint32_t* row_ptr;
     const uint16_t* recs;
@@ -280,8 +283,16 @@ hipError_t launch_f16_check(const uint16_t* v, size_t n, uint32_t* status, hipSt
 // Adds the outliers of rows [row0, row0 + nrows) to a decoded base.
 hipError_t launch_rice_decode_add(const ResView& v, uint32_t row0, uint32_t nrows, float* out, hipStream_t s);
 // y_i += R_i x_i for n residuals of one shape (table in device memory).
-hipError_t launch_rice_apply(const ResView* res_dev, uint32_t n, uint32_t rows, uint32_t cols, const float* x,
-                             size_t x_stride, float* y, size_t y_stride, hipStream_t s);
+// pieces: the most 16-byte record pieces any RICE_APPLY_ROWS-row part of the
+// n residuals spans (rice_part_pieces).
+constexpr uint32_t RICE_APPLY_ROWS = 512;
+// Bytes of the apply's signed product table in LDS: T[2 c + sign] =
+// (sign ? scale : -scale) * x[c] for c < cols, T[2 cols] = -0 (the padding
+// records' entry), 16-byte aligned.
+__host__ __device__ inline size_t rice_table_bytes(uint32_t cols) { return ((size_t)cols * 8u + 8u + 15u) & ~(size_t)15; }
+uint32_t rice_part_pieces(const uint32_t* row_ptr, uint32_t rows, uint32_t part_rows);
+hipError_t launch_rice_apply(const ResView* res_dev, uint32_t n, uint32_t rows, uint32_t cols, uint32_t pieces,
+                             const float* x, size_t x_stride, float* y, size_t y_stride, hipStream_t s);
 // Device packer (pack_binary_rice_q1): fills the canonical device buffers
 // and the host scalars; returns hipErrorInvalidValue if rice_cap is short
 // (*rice_bytes then holds the size needed).
@@ -335,6 +346,7 @@ struct hk_organ {
     hk::ResView res{};         // HGRAVR02 residual (res_dev non-null when present)
     void* res_mem = nullptr;
     const hk::ResView* res_dev = nullptr;
+    uint32_t res_pieces = 0;   // rice_part_pieces of the residual (RICE_APPLY_ROWS-row parts)
     void* view_dev = nullptr;  // device copy of `view` for single-organ launches
     void* mem = nullptr;
     size_t alloc_bytes = 0;

@@ -81,10 +81,12 @@ __device__ __forceinline__ void rice_rows_from(const ResView& v, const float* __
             float p[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                const uint32_t rec = (w[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
-                const bool in = e + (uint32_t)k >= t.e0 && e + (uint32_t)k < t.e1;
-                const float xv = xs[in ? (rec & 0x7FFFu) : 0u];
-                p[k] = in ? ((rec >> 15) ? v.scale : -v.scale) * xv : 0.0f;
+                // a row's padding records (column cols) add -0, which leaves
+                // every sum as it is
+                const uint32_t rec = (w[k >> 1] >> (16 * (k & 1))) & 0xFFFFu, col = rec >> 1;
+                const bool in = e + (uint32_t)k >= t.e0 && e + (uint32_t)k < t.e1 && col < v.cols;
+                const float xv = xs[in ? col : 0u];
+                p[k] = in ? ((rec & 1u) ? v.scale : -v.scale) * xv : -0.0f;
             }
             float4* o = reinterpret_cast<float4*>(vals + 8u * (tid + 256u * j));
             o[0] = make_float4(p[0], p[1], p[2], p[3]);

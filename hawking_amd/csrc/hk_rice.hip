@@ -6,12 +6,11 @@
 //
 // The Rice stream is decoded once at bind time (on the host, in hk_api.cpp)
 // into a CSR over rows (row_ptr plus one u16 record per outlier:
-// column | sign << 15).  Per token the base
-// runs on the tiled binary GEMV and rice_apply adds the outliers: each
-// workgroup owns 256 rows, stages batches of records with their products
-// (+-scale) * x[col] in LDS, and each row's thread adds its products in index
-// order -- the reference's serial apply order, so given the same base the
-// correction is bit-exact.
+// column << 1 | sign, each row padded to a multiple of four records).  Per
+// token the base runs on the tiled binary GEMV and rice_apply adds the
+// outliers, each row's thread adding its products in index order -- the
+// reference's serial apply order, so given the same base the correction is
+// bit-exact.
 #include <rocprim/device/device_radix_sort.hpp>
 #include <rocprim/device/device_scan.hpp>
 
@@ -40,6 +39,7 @@ hipError_t launch_f16_check(const uint16_t* v, size_t n, uint32_t* status, hipSt
 // ------------------------------------------------------------------ per token
 
 constexpr uint32_t RICE_ROWS_PER_WG = 256;  // at most 512 (two rows per thread)
+constexpr size_t RICE_APPLY_LDS_MAX = 64u * 1024u;
 
 // y[row] += sum over the row's outliers, in index order, of (+-scale) * x[col]
 // (the apply on its own, for a base computed elsewhere).
@@ -70,9 +70,102 @@ __global__ void __launch_bounds__(256) rice_apply_kernel(const ResView* __restri
     }
 }
 
-hipError_t launch_rice_apply(const ResView* res_dev, uint32_t n, uint32_t rows, uint32_t cols, const float* x,
-                             size_t x_stride, float* y, size_t y_stride, hipStream_t s) {
+// The apply with one thread per row: a workgroup of RICE_APPLY_ROWS threads
+// owns that many rows of one residual, loads every record piece its rows
+// span in one round (part 0 starts at record 0, so its loads wait for
+// nothing but the residual's view), stages them in LDS next to the signed
+// product table T[2 c + sign] = (sign ? scale : -scale) * x[c] (T[2 cols] =
+// -0, the padding records' entry: x + -0 is x for every x), and each thread
+// adds its row's products in index order, four records per LDS read (rows
+// are padded to multiples of four).  Same sums as rice_apply_kernel, to the
+// bit: (-scale) * x is -(scale * x) exactly.  NP pieces per thread cover
+// `pieces` (<= NP * RICE_APPLY_ROWS).
+template <int NP>
+__global__ void __launch_bounds__(RICE_APPLY_ROWS)
+rice_apply_rows_kernel(const ResView* __restrict__ views, uint32_t n, const float* __restrict__ xall, size_t x_stride,
+                       float* __restrict__ yall, size_t y_stride, uint32_t parts, uint32_t pieces) {
+    extern __shared__ __align__(16) uint8_t rl[];
+    uint32_t oi, part;
+    organ_part(blockIdx.x, parts, n, &oi, &part);
+    const ResView v = views[oi];
+    const uint32_t tid = threadIdx.x, r0 = part * RICE_APPLY_ROWS;
+    if (r0 >= v.rows || v.count == 0u) return;  // uniform over the workgroup
+    const uint32_t r1 = min(r0 + RICE_APPLY_ROWS, v.rows);
+    const float* __restrict__ x = xall + (size_t)oi * x_stride;
+    float* __restrict__ y = yall + (size_t)oi * y_stride;
+    uint32_t p0 = 0;
+    if (part) p0 = ldg(v.row_ptr + r0) / 8u;
+    // unconditional loads, clamped to the residual's last piece: a load under
+    // a per-lane condition would wait for the ones before it
+    const uint4* recs = reinterpret_cast<const uint4*>(v.recs);
+    const uint32_t plast = (v.count + 7u) / 8u - 1u;
+    uint4 rv[NP];
+#pragma unroll
+    for (int j = 0; j < NP; ++j) rv[j] = ldg(recs + min(p0 + tid + RICE_APPLY_ROWS * (uint32_t)j, plast));
+    const bool mine = tid < r1 - r0;
+    const uint32_t row = mine ? r0 + tid : r0;
+    const uint32_t my0 = ldg(v.row_ptr + row), my1 = mine ? ldg(v.row_ptr + row + 1u) : my0;
+    float acc = ldg(y + row);
+    float2* T = reinterpret_cast<float2*>(rl);
+#pragma unroll 4
+    for (uint32_t c = tid; c < v.cols; c += RICE_APPLY_ROWS) {
+        const float p = v.scale * ldg(x + c);
+        T[c] = make_float2(-p, p);
+    }
+    if (tid == 0) T[v.cols] = make_float2(-0.0f, -0.0f);
+    uint4* R = reinterpret_cast<uint4*>(rl + rice_table_bytes(v.cols));
+#pragma unroll
+    for (int j = 0; j < NP; ++j)
+        if (tid + RICE_APPLY_ROWS * (uint32_t)j < pieces) R[tid + RICE_APPLY_ROWS * j] = rv[j];
+    __syncthreads();
+    const float* Tf = reinterpret_cast<const float*>(rl);
+    const uint2* R2 = reinterpret_cast<const uint2*>(R);
+#pragma unroll 2
+    for (uint32_t e = my0; e < my1; e += 4u) {
+        const uint2 w = R2[(e - 8u * p0) / 4u];
+        acc += Tf[w.x & 0xFFFFu];
+        acc += Tf[w.x >> 16];
+        acc += Tf[w.y & 0xFFFFu];
+        acc += Tf[w.y >> 16];
+    }
+    if (mine) y[row] = acc;
+}
+
+uint32_t rice_part_pieces(const uint32_t* row_ptr, uint32_t rows, uint32_t part_rows) {
+    uint32_t most = 0;
+    for (uint32_t r0 = 0; r0 < rows; r0 += part_rows) {
+        const uint32_t r1 = std::min(r0 + part_rows, rows);
+        most = std::max(most, (row_ptr[r1] + 7u) / 8u - row_ptr[r0] / 8u);
+    }
+    return most;
+}
+
+hipError_t launch_rice_apply(const ResView* res_dev, uint32_t n, uint32_t rows, uint32_t cols, uint32_t pieces,
+                             const float* x, size_t x_stride, float* y, size_t y_stride, hipStream_t s) {
     if (n == 0 || rows == 0) return hipSuccess;
+    const uint32_t np = (pieces + RICE_APPLY_ROWS - 1u) / RICE_APPLY_ROWS;
+    const size_t lds_rows = rice_table_bytes(cols) + (size_t)pieces * 16u;
+    if (np >= 1u && np <= 8u && lds_rows <= RICE_APPLY_LDS_MAX) {
+        const uint32_t parts = (rows + RICE_APPLY_ROWS - 1u) / RICE_APPLY_ROWS;
+        const dim3 g(parts * n), b(RICE_APPLY_ROWS);
+#define HK_RICE_ROWS(NP)                                                                                            \
+    case NP:                                                                                                        \
+        hipLaunchKernelGGL(rice_apply_rows_kernel<NP>, g, b, lds_rows, s, res_dev, n, x, x_stride, y, y_stride, parts, \
+                           pieces);                                                                                 \
+        break;
+        switch (np) {
+            HK_RICE_ROWS(1)
+            HK_RICE_ROWS(2)
+            HK_RICE_ROWS(3)
+            HK_RICE_ROWS(4)
+            HK_RICE_ROWS(5)
+            HK_RICE_ROWS(6)
+            HK_RICE_ROWS(7)
+            HK_RICE_ROWS(8)
+        }
+#undef HK_RICE_ROWS
+        return hipGetLastError();
+    }
     const uint32_t parts = (rows + RICE_ROWS_PER_WG - 1) / RICE_ROWS_PER_WG;
     const size_t lds = ((size_t)cols + RICE_BATCH) * sizeof(float);
     hipLaunchKernelGGL(rice_apply_kernel, dim3(parts * n), dim3(256), lds, s, res_dev, n, x, x_stride, y, y_stride,
@@ -92,8 +185,8 @@ __global__ void rice_decode_add_kernel(ResView v, uint32_t row0, uint32_t nrows,
             if (v.row_ptr[mid] <= e) lo = mid;
             else hi = mid;
         }
-        const uint16_t rec = v.recs[e];
-        atomicAdd(out + (size_t)(lo - row0) * v.cols + (rec & 0x7FFFu), (rec >> 15) ? v.scale : -v.scale);
+        const uint32_t rec = v.recs[e], col = rec >> 1;
+        if (col < v.cols) atomicAdd(out + (size_t)(lo - row0) * v.cols + col, (rec & 1u) ? v.scale : -v.scale);
     }
 }
 
