@@ -597,6 +597,7 @@ struct hk_organ_set {
     OrganView* dev = nullptr;
     ResView* res_dev = nullptr;  // HGRAVR02 sets: the residual table
     uint32_t res_pieces = 0;     // the most record pieces of any organ's apply part
+    uint32_t res_pieces_256 = 0;  // the same for 256-row parts
     uint32_t n = 0;
     OrganView first{};
 };
@@ -631,6 +632,7 @@ extern "C" int hk_organ_set_create(hk_ctx* ctx, const hk_organ* const* organs, u
         for (uint32_t i = 0; i < n; ++i) {
             res[i] = organs[i]->res;
             set->res_pieces = std::max(set->res_pieces, organs[i]->res_pieces);
+            set->res_pieces_256 = std::max(set->res_pieces_256, organs[i]->res_pieces_256);
         }
         if (hipMalloc(&set->res_dev, n * sizeof(ResView)) != hipSuccess) {
             (void)hipFree(set->dev);
@@ -668,12 +670,20 @@ extern "C" int hk_gemv_set(hk_ctx* ctx, const hk_organ_set* set, const float* x,
     int rc = check_vectors(ctx, "hk_gemv_set", x, x_stride, y, y_stride, set->n, set->first);
     if (rc) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    rc = check_hip(ctx, launch_gemv_tiled(set->dev, set->n, set->first, x, x_stride, y, y_stride, st),
-                   "gemv_set launch");
-    if (!rc && set->res_dev)
+    // HGRAVR02: the residual in the GEMV's epilogue where the launch shape
+    // has that form, else the apply after the GEMV
+    bool fused = false;
+    if (set->res_dev)
+        rc = check_hip(ctx,
+                       launch_gemv_rice(set->dev, set->res_dev, set->n, set->first, set->res_pieces_256,
+                                        set->res_pieces, x, x_stride, y, y_stride, st, &fused),
+                       "gemv_set launch");
+    if (!rc && !fused)
+        rc = check_hip(ctx, launch_gemv_tiled(set->dev, set->n, set->first, x, x_stride, y, y_stride, st),
+                       "gemv_set launch");
+    if (!rc && !fused && set->res_dev)
         rc = check_hip(ctx, launch_rice_apply(set->res_dev, set->n, set->first.rows, set->first.cols, set->res_pieces, x,
-                                              x_stride, y,
-                                              y_stride, st),
+                                              x_stride, y, y_stride, st),
                        "rice apply");
     return rc;
 }
@@ -918,6 +928,7 @@ static int upload_rice(hk_ctx* ctx, const hk_rice_q1* s, hipStream_t st, hk_orga
             o->res.scale = f16_to_f32_host(s->residual_scale_f16);
             o->res.count = row_ptr[s->rows];
             o->res_pieces = rice_part_pieces(row_ptr.data(), s->rows, RICE_APPLY_ROWS);
+            o->res_pieces_256 = rice_part_pieces(row_ptr.data(), s->rows, 256u);
             ResView* rd = reinterpret_cast<ResView*>(m + a_rp + a_rec);
             rc = check_hip(ctx, hipMemcpy(m, row_ptr.data(), row_ptr.size() * 4, hipMemcpyHostToDevice), "row_ptr upload");
             if (!rc) rc = check_hip(ctx, hipMemcpy(m + a_rp, recs.data(), recs.size() * 2, hipMemcpyHostToDevice), "record upload");

@@ -121,16 +121,42 @@ __device__ __forceinline__ void head_norm_chunks(XChunks<NC>& xc, uint32_t cols,
     }
 }
 
+// The HGRAVR02 residual added in the binary GEMV's epilogue (RES): views
+// per organ, and the most 16-byte record pieces any workgroup's rows span.
+struct ResArgs {
+    const ResView* views;
+    uint32_t pieces;
+};
+constexpr int GEMV_RES_NP = 12;  // record pieces per thread (pieces <= 12 * 256)
+
+// Where the workgroup's row totals sit in LDS: after the x image (and the
+// mixed headers), and with RES after the epilogue's residual table and
+// records, which reuse the image's bytes.
+template <int KIND, bool RES>
+__host__ __device__ inline size_t gemv_ysh_offset(uint32_t steps, uint32_t tpw, uint32_t cols, uint32_t pieces) {
+    size_t off = gemv_hdr_offset<KIND>(steps) + (KIND == HK_MIXED ? (size_t)tpw * steps * sizeof(uint4) : 0);
+    if (RES) off = std::max(off, (rice_table_bytes(cols) + (size_t)pieces * 16u + 15u) & ~(size_t)15);
+    return off;
+}
+
 // D-deep software pipeline: D fetched steps are in flight while one is
 // consumed; slot d of the rotating buffer holds item it+d.  The loop body is
 // branch-free in memory operations (refetches are unconditional, past the end
 // they re-read the last item; y goes out through LDS after the loop) so the
 // compiler can wait for exactly the slot being consumed.
-template <int KIND, int R, int D, int NC, bool HEAD>
+//
+// RES (binary, at most 512 rows per workgroup): y = base + the HGRAVR02
+// residual, to the bit what rice_apply does after the plain GEMV.  The row
+// pointers load with the first weights; after the main loop the image's
+// LDS takes the signed product table (from the x chunks still in
+// registers) and the workgroup's record pieces (loaded in one round), and
+// each row's thread adds its products to the row total in index order.
+template <int KIND, int R, int D, int NC, bool HEAD, bool RES = false>
 __global__ void __launch_bounds__(256)
 gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const float* __restrict__ xall,
                   size_t x_stride, float* __restrict__ yall, size_t y_stride, uint32_t tiles_per_wg, uint32_t parts,
-                  uint32_t* status, HeadArgs ha) {
+                  uint32_t* status, HeadArgs ha, ResArgs ra) {
+    static_assert(!RES || (KIND == HK_BIN && NC == 1 && !HEAD), "the fused residual is for binary organs");
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float red[4];
     __shared__ uint64_t kred[HEAD ? 4 : 1];
@@ -153,8 +179,7 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const
     const uint32_t nh = (t1 - t0) * o.steps;
     uint4 hreg[GEMV_HDR_PER_THREAD];
     uint4* hsh = reinterpret_cast<uint4*>(lds + gemv_hdr_offset<KIND>(o.steps));
-    float* ysh = reinterpret_cast<float*>(lds + gemv_hdr_offset<KIND>(o.steps) +
-                                          (KIND == HK_MIXED ? (size_t)tiles_per_wg * o.steps * sizeof(uint4) : 0));
+    float* ysh = reinterpret_cast<float*>(lds + gemv_ysh_offset<KIND, RES>(o.steps, tiles_per_wg, o.cols, ra.pieces));
     if constexpr (KIND == HK_MIXED) {
 #pragma unroll
         for (int k = 0; k < GEMV_HDR_PER_THREAD; ++k) {
@@ -182,6 +207,21 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const
             if (i < nh) hsh[i] = hreg[k];
         }
     }
+    // RES: the residual's view and the row pointers of this workgroup's rows
+    // (two rows a thread), issued after the first weights
+    ResView rv{};
+    uint32_t rp0 = 0, my0[2] = {0u, 0u}, my1[2] = {0u, 0u};
+    if constexpr (RES) {
+        rv = ra.views[oi];
+        const uint32_t r0 = t0 * 16u, r1 = min(t1 * 16u, o.rows);
+        rp0 = ldg(rv.row_ptr + r0) / 8u;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t row = min(r0 + threadIdx.x + 256u * (uint32_t)h, r1);
+            my0[h] = ldg(rv.row_ptr + row);
+            my1[h] = ldg(rv.row_ptr + min(row + 1u, r1));
+        }
+    }
     if constexpr (HEAD) head_norm_chunks<NC>(xc, o.cols, ha, red);
     // the x image with E = 0: every thread scatters its own chunks (no
     // block-wide maximum, no gather pass); a unit's chunks are consecutive
@@ -207,6 +247,7 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const
     if (bad && status) atomicOr(status, 1u);
     if constexpr (HEAD)
         if (bad) atomicOr(reinterpret_cast<uint32_t*>(ha.key + 1), 1u);
+
     const ImageA A{lds, a_lane_offset(lane)};
     const float* SX = reinterpret_cast<const float*>(lds + (size_t)o.steps * Kcfg<KIND>::P * A_TILE_STRIDE);
 
@@ -241,6 +282,54 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const
     }
     __syncthreads();
     const uint32_t nrows = (t1 > t0 ? t1 - t0 : 0u) * 16u;
+    if constexpr (RES) {
+        // the image is dead: its bytes take the residual's table and records
+        const uint32_t np = (ra.pieces + 255u) / 256u;
+        const uint4* recs = reinterpret_cast<const uint4*>(rv.recs);
+        const uint32_t plast = (rv.count + 7u) / 8u - 1u;
+        uint4 rr[GEMV_RES_NP];
+#pragma unroll
+        for (int j = 0; j < GEMV_RES_NP; ++j)
+            if ((uint32_t)j < np) rr[j] = ldg(recs + min(rp0 + threadIdx.x + 256u * (uint32_t)j, plast));
+        float2* Tt = reinterpret_cast<float2*>(lds);
+        {
+            const uint32_t c0 = 8u * threadIdx.x;
+            if (c0 < o.cols) {
+                const float xv[8] = {xc.v[0][0].x, xc.v[0][0].y, xc.v[0][0].z, xc.v[0][0].w,
+                                     xc.v[0][1].x, xc.v[0][1].y, xc.v[0][1].z, xc.v[0][1].w};
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const float p = rv.scale * xv[k];
+                    Tt[c0 + (uint32_t)k] = make_float2(-p, p);
+                }
+            }
+        }
+        if (threadIdx.x == 0) Tt[o.cols] = make_float2(-0.0f, -0.0f);
+        uint4* Rr = reinterpret_cast<uint4*>(lds + rice_table_bytes(o.cols));
+#pragma unroll
+        for (int j = 0; j < GEMV_RES_NP; ++j)
+            if ((uint32_t)j < np && threadIdx.x + 256u * (uint32_t)j < ra.pieces) Rr[threadIdx.x + 256u * j] = rr[j];
+        __syncthreads();
+        const float* Tf = reinterpret_cast<const float*>(lds);
+        const uint2* R2 = reinterpret_cast<const uint2*>(Rr);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t i = threadIdx.x + 256u * (uint32_t)h, row = t0 * 16u + i;
+            if (i < nrows && row < o.rows) {
+                float acc = ldexpf(ysh[i], -E);
+#pragma unroll 2
+                for (uint32_t e = my0[h]; e < my1[h]; e += 4u) {
+                    const uint2 w = R2[(e - 8u * rp0) / 4u];
+                    acc += Tf[w.x & 0xFFFFu];
+                    acc += Tf[w.x >> 16];
+                    acc += Tf[w.y & 0xFFFFu];
+                    acc += Tf[w.y >> 16];
+                }
+                y[row] = acc;
+            }
+        }
+        return;
+    }
     uint64_t best = 0;
     for (uint32_t i = threadIdx.x; i < nrows; i += blockDim.x) {
         const uint32_t row = t0 * 16u + i;
@@ -452,23 +541,22 @@ size_t gemv_lds_bytes(int kind, uint32_t cols) {
     return gemv_hdr_offset<HK_MIXED>(S) + (size_t)GEMV_MAX_MIXED_TILES_PER_WG * S * sizeof(uint4) + ysh;
 }
 
-template <int KIND, int R, int D, bool HEAD = false>
+template <int KIND, int R, int D, bool HEAD = false, bool RES = false>
 static hipError_t launch_kind(const OrganView* organs, uint32_t n, const OrganView& sh, const float* x,
                               size_t xs, float* y, size_t ys, uint32_t tpw, hipStream_t s, const HeadArgs& ha = {},
-                              uint32_t* status = nullptr) {
+                              uint32_t* status = nullptr, const ResArgs& ra = {}) {
     const uint32_t parts = (sh.n_tiles + tpw - 1) / tpw;
     const dim3 grid(parts * n);
     // image + one quantization window (2048 columns); x chunks held in
     // registers: one per thread up to 2048 columns, else four
     const uint32_t kc = x_image_cols<KIND>(sh.steps);
-    const size_t lds = gemv_hdr_offset<KIND>(sh.steps) + (KIND == HK_MIXED ? (size_t)tpw * sh.steps * sizeof(uint4) : 0) +
-                       (size_t)tpw * 16u * sizeof(float);
+    const size_t lds = gemv_ysh_offset<KIND, RES>(sh.steps, tpw, sh.cols, ra.pieces) + (size_t)tpw * 16u * sizeof(float);
     if (kc <= 2048u)
-        hipLaunchKernelGGL((gemv_tiled_kernel<KIND, R, D, 1, HEAD>), grid, dim3(256), lds, s, organs, n, x, xs, y, ys,
-                           tpw, parts, status, ha);
-    else
+        hipLaunchKernelGGL((gemv_tiled_kernel<KIND, R, D, 1, HEAD, RES>), grid, dim3(256), lds, s, organs, n, x, xs, y,
+                           ys, tpw, parts, status, ha, ra);
+    else if constexpr (!RES)
         hipLaunchKernelGGL((gemv_tiled_kernel<KIND, R, D, 4, HEAD>), grid, dim3(256), lds, s, organs, n, x, xs, y, ys,
-                           tpw, parts, status, ha);
+                           tpw, parts, status, ha, ra);
     return hipGetLastError();
 }
 
@@ -557,6 +645,28 @@ hipError_t launch_head_fused(const OrganView* organ_dev, const OrganView& sh, co
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(head_pick_fused_kernel, dim3(1), dim3(64), 0, s, key, token, status);
     return hipGetLastError();
+}
+
+hipError_t launch_gemv_rice(const OrganView* organs_dev, const ResView* res_dev, uint32_t n, const OrganView& sh,
+                            uint32_t pieces256, uint32_t pieces512, const float* x, size_t x_stride, float* y,
+                            size_t y_stride, hipStream_t s, bool* fused) {
+    *fused = false;
+    // the streamed binary shapes (launch_r), with x in one register chunk
+    if (sh.kind != HK_BIN || (uint64_t)n * sh.n_tiles < 16384 || x_image_cols<HK_BIN>(sh.steps) > 2048u)
+        return hipSuccess;
+    const bool wide = sh.steps >= 4;
+    const uint32_t tpw = wide ? HK_BIN_WIDE_TPW : HK_BIN_NARROW_TPW, pieces = wide ? pieces256 : pieces512;
+    static_assert(HK_BIN_WIDE_TPW * 16 == 256 && HK_BIN_NARROW_TPW * 16 == 512, "RES rows per workgroup");
+    // the fused kernel runs 4 workgroups per CU (its registers): LDS up to a
+    // quarter of the CU's 160 KiB costs no occupancy
+    if (pieces == 0 || pieces > 256u * GEMV_RES_NP ||
+        gemv_ysh_offset<HK_BIN, true>(sh.steps, tpw, sh.cols, pieces) + (size_t)tpw * 64u > 40u * 1024u)
+        return hipSuccess;
+    const ResArgs ra{res_dev, pieces};
+    *fused = true;
+    if (wide) return launch_kind<HK_BIN, 4, 3, false, true>(organs_dev, n, sh, x, x_stride, y, y_stride, tpw, s, {}, nullptr, ra);
+    return launch_kind<HK_BIN, HK_BIN_NARROW_R, HK_BIN_NARROW_D, false, true>(organs_dev, n, sh, x, x_stride, y,
+                                                                              y_stride, tpw, s, {}, nullptr, ra);
 }
 
 hipError_t launch_gemv_tiled(const OrganView* organs_dev, uint32_t n, const OrganView& sh, const float* x,

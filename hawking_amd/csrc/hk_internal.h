@@ -250,6 +250,14 @@ int check_hip(hk_ctx* ctx, hipError_t e, const char* what);
 // 64 KB (two workgroups per CU of 160 KB at the widest organs).
 size_t gemv_lds_bytes(int kind, uint32_t cols);
 constexpr size_t GEMV_LDS_LIMIT = 64 * 1024;
+struct ResView;
+// The binary GEMV of HGRAVR02 organs with the residual added in its
+// epilogue (the bits of launch_gemv_tiled then launch_rice_apply); pieces256
+// / pieces512: rice_part_pieces of the organs for 256- and 512-row parts.
+// *fused = false (nothing launched) when the launch shape has no fused form.
+hipError_t launch_gemv_rice(const OrganView* organs_dev, const ResView* res_dev, uint32_t n, const OrganView& sh,
+                            uint32_t pieces256, uint32_t pieces512, const float* x, size_t x_stride, float* y,
+                            size_t y_stride, hipStream_t s, bool* fused);
 hipError_t launch_gemv_tiled(const OrganView* organs_dev, uint32_t n, const OrganView& shape,
                              const float* x, size_t x_stride, float* y, size_t y_stride,
                              hipStream_t s);
@@ -347,6 +355,7 @@ struct hk_organ {
     void* res_mem = nullptr;
     const hk::ResView* res_dev = nullptr;
     uint32_t res_pieces = 0;   // rice_part_pieces of the residual (RICE_APPLY_ROWS-row parts)
+    uint32_t res_pieces_256 = 0;  // the same for 256-row parts
     void* view_dev = nullptr;  // device copy of `view` for single-organ launches
     void* mem = nullptr;
     size_t alloc_bytes = 0;

@@ -170,6 +170,28 @@ def test_rice_organ_set_large_matches_single(ctx, oracle, n):
         assert np.array_equal(y1[i], orgs[i].matvec(xs[i])), i
 
 
+@pytest.mark.parametrize("rows,cols,n", [(512, 2048, 520), (2048, 512, 130)])
+def test_rice_organ_set_fused_matches_single(ctx, oracle, rows, cols, n):
+    # sets of >= 16,384 row tiles take the GEMV with the residual in its
+    # epilogue (256 rows a workgroup for 2048 columns, 512 for 512): the same
+    # bits as the GEMV followed by the apply, one organ at a time
+    from hawking_amd._lib import HK_BIN_RICE
+    from hawking_amd.organs import OrganSet, SyntheticOrgan
+    say("rice set fused", n, rows, cols)
+    orgs = [SyntheticOrgan(ctx, HK_BIN_RICE, rows, cols, oracle.stream_key(U.SEED, (0xAA << 20) + i), 0, group=128,
+                           sigma=0.02) for i in range(n)]
+    s = OrganSet(ctx, orgs)
+    xs = np.stack([oracle.normal(oracle.stream_key(U.SEED, (0xAB << 20) + i), cols, 1.0) for i in range(n)])
+    x = ctx.to_device(xs)
+    y = ctx.empty((n, rows))
+    s.gemv(x, cols, y, rows)
+    y1 = y.download()
+    s.gemv(x, cols, y, rows)
+    assert np.array_equal(y.download(), y1)
+    for i in range(n):
+        assert np.array_equal(y1[i], orgs[i].matvec(xs[i])), i
+
+
 def test_rice_upload_rejects_bad_streams(ctx, oracle):
     from hawking_amd._lib import HK_E_GEOMETRY, HK_E_NONFINITE, HawkingError
     from hawking_amd.organs import RiceQ1Packed
