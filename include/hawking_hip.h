@@ -157,6 +157,7 @@ typedef struct hk_rice_q1 {
 
 /* Upload of an HGRAVR02 organ: the base is repacked like a binary organ; the
  * Rice stream is expanded once, on the host at bind time, into a CSR over rows
+ * (2 bytes per outlier, rows padded to multiples of four records)
  * (expand_rice_indices + rice_q1_row_ptr, q80_mixed_decode.rs:462-507, and
  * the bind of parse_rice_q1_container, 868-946).  Errors: HK_E_GEOMETRY for
  * a stream that overruns its bytes, a quotient or index above u32, or an index
