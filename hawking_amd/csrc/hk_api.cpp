@@ -1498,7 +1498,7 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
     m->layers.resize(c.n_layers);
     const size_t dpl = dense_per_layer(c);
     const size_t tab = align256((size_t)(c.n_experts + 1) * 3 * sizeof(OrganView));
-    const size_t img = align256(moe_img_bytes(c.expert_kind, c.hidden));
+    const size_t img = align256((size_t)c.hidden * 4);
     const size_t dnh = align256((size_t)slots * hk::moe_dn_hdr_stride(c.hidden, imax) * 16);
     const size_t ws = align256(((size_t)c.n_experts + 4) * 4) + 3 * 256 + align256((size_t)slots * imax * 4) + img + 256 +
                       2 * align256((size_t)c.hidden * 4) + dnh;
@@ -1540,7 +1540,7 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
     w += 256;
     m->ws.act = reinterpret_cast<float*>(w);
     w += align256((size_t)slots * imax * 4);
-    m->ws.img = w;
+    m->ws.xn = reinterpret_cast<float*>(w);
     w += img;
     w += 256;
     m->hbuf[0] = reinterpret_cast<float*>(w);

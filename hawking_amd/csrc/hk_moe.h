@@ -49,7 +49,7 @@ struct MoeWs {
     float* weights;    // [K]
     float* gate;       // [2]: shared-gate logit, shared-gate value
     float* act;        // [(K+1) * Imax]
-    uint8_t* img;      // x image (E = 0) of RMSNorm(h) for the gate/up organs
+    float* xn;         // [H] RMSNorm(1+w)(h): the gate/up kernel builds its x image (E = 0) from it
     uint4* dn_hdr;     // [slots][moe_dn_hdr_stride]: the step headers of each slot's down organ (mixed), copied
                        // by the gate/up kernel so the down kernel needs no route before them
     uint32_t* status;  // device error bits

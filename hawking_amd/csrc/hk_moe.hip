@@ -7,12 +7,13 @@
 //  crates/hawking-core/src/model/qwen80_device_expert_table.rs:1204-1247):
 //   1. route:   every block recomputes xn = RMSNorm(1+w)(h) in LDS; blocks
 //               0..ceil(E/4)-1 compute the router logits (one row per wave),
-//               the next block also the shared-gate logit, and the blocks
-//               from there build the x image of xn (fixed-point limb tiles
-//               with E = 0, once per layer), 512 columns per wave.
+//               the next block also the shared-gate logit and stores xn.
 //   2. gate/up: one workgroup per (16-row tile, slot); each runs softmax /
 //               top-k / renormalise over the logits itself to find its
-//               slot's expert (slot K = the shared expert), then its 4 waves
+//               slot's expert (slot K = the shared expert) while its other
+//               waves build the x image of xn in LDS (fixed-point limb tiles
+//               with E = 0; a separate image block in the route kernel was
+//               that kernel's last to finish), then its 4 waves
 //               split the columns, both organs share each x-image fetch, and
 //               the epilogue applies SwiGLU: act = silu(gate.xn) * (up.xn).
 //   3. down:    one workgroup per 16-row output tile, one wave per slot; each
@@ -116,31 +117,20 @@ __global__ void __launch_bounds__(256) moe_route_kernel(MoeDims d, MoeLayerDev L
                 ws.gate[0] = acc;
         }
     }
-    if (blockIdx.x >= nrb) {
-        // the x image of xn (E = 0) for every gate/up organ of this layer:
-        // 512 columns per wave, limb bytes stored straight to their tiles
-        // (measured faster than staging the part in LDS for 16-byte stores)
-        const uint32_t S = n_steps_for(KIND, d.H), nch = S * tile_step_cols(KIND) / 8u;
-        const uint32_t cb = ((blockIdx.x - nrb) * 4u + wave) * 64u;
-        if (cb < nch) {
-            constexpr uint32_t TB = 512u / Kcfg<KIND>::STEP_COLS * Kcfg<KIND>::P * A_TILE_STRIDE;  // tile bytes per wave
-            constexpr uint32_t SB = 512u / Kcfg<KIND>::SXG * Kcfg<KIND>::SXW * 4u;                // unit bytes per wave
-            bool bad = false;
-            image_wave<KIND>((uint32_t)lane, xn, d.H, ws.img + (size_t)(cb / 64u) * TB,
-                             reinterpret_cast<float*>(ws.img + (size_t)S * Kcfg<KIND>::P * A_TILE_STRIDE +
-                                                      (size_t)(cb / 64u) * SB),
-                             cb, min(cb + 64u, nch), &bad);
-            if (__ballot(bad) != 0 && lane == 0) atomicOr(ws.status, HK_DEVERR_NONFINITE);
-        }
+    if (blockIdx.x == nrb) {
+        // xn for the gate/up kernel, which builds its x image from it
+        for (uint32_t j = threadIdx.x; j < n4; j += 256u) reinterpret_cast<float4*>(ws.xn)[j] = x4[j];
     }
 }
 
 // Gate/up of one (16-row tile, slot).  Every workgroup of a routed slot first
 // ranks the router logits itself (softmax, top-k, renormalise:
-// source_qwen80_topk_router; one wave, about 2 us) while its other waves copy
-// the layer's x image into LDS, and takes its slot's expert; this saves a
-// launch.  Slot 0's tile 0 publishes the route and the shared-gate value
+// source_qwen80_topk_router; one wave, about 2 us) while its other waves
+// build the layer's x image of xn (E = 0) in LDS, and takes its slot's
+// expert; this saves a launch.  Slot 0's tile 0 publishes the route and the shared-gate value
 // for the down kernel.
+constexpr int GU_IMG_PT = 2;  // x chunks per thread loaded before the scatter (2,048 columns)
+
 template <int KIND, int D, int NPL>
 __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev L, MoeWs ws, int32_t* ids_out,
                                                           float* w_out) {
@@ -157,7 +147,11 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev
     const OrganView g0 = L.table[base], u0 = L.table[base + 1u];
     OrganView dn0{};
     if constexpr (KIND == HK_MIXED) dn0 = L.table[base + 2u];
-    if (routed && wave == 0) {
+    // the ranking wave: slots 8 apart share CUs when the grid exceeds the
+    // CU count (workgroups i and i + 256 of a 32-tile grid), so theirs rank
+    // on different SIMDs
+    const uint32_t tw = (slot >> 3) & 3u;
+    if (routed && wave == tw) {
         const bool pub = lead && slot == 0;
         const ArgBest mine = softmax_topk_wave<NPL>(ws.logits, d.E, d.K, 1, pub ? ws.ids : nullptr,
                                                     pub ? ws.weights : nullptr, pub ? ws.status : nullptr, &tk);
@@ -168,11 +162,29 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev
         if (pub && lane == 0) ws.gate[1] = L.gate_w ? 1.0f / (1.0f + expf(-ws.gate[0])) : 1.0f;
         if ((uint32_t)lane == slot) sel_id = mine.i;
     } else {
-        // the x image built by the route kernel, into LDS (every load in
-        // flight before the first store: one memory latency)
-        const uint32_t t0 = routed ? 64u : 0u;
-        copy16_to_lds<4>(reinterpret_cast<uint4*>(lds), reinterpret_cast<const uint4*>(ws.img), ib / 16u,
-                         threadIdx.x - t0, blockDim.x - t0);
+        // the x image of xn with E = 0, scattered into LDS by the other waves
+        // (the image the GEMV engine builds: the same bits); every chunk's
+        // load in flight before the first scatter
+        const uint32_t nt = routed ? blockDim.x - 64u : blockDim.x;
+        const uint32_t tid = routed && threadIdx.x >= 64u * tw ? threadIdx.x - 64u : threadIdx.x;
+        const uint32_t nch = S * tile_step_cols(KIND) / 8u;
+        float* sxw = reinterpret_cast<float*>(lds + (size_t)S * Kcfg<KIND>::P * A_TILE_STRIDE);
+        if (tid < 64u) image_zero_blocks<KIND>(tid, lds, S);
+        float4 v[GU_IMG_PT][2];
+#pragma unroll
+        for (int j = 0; j < GU_IMG_PT; ++j) load_chunk(ws.xn, 8u * (tid + nt * (uint32_t)j), d.H, v[j]);
+        bool bad = false;
+#pragma unroll
+        for (int j = 0; j < GU_IMG_PT; ++j) {
+            const uint32_t ch = tid + nt * (uint32_t)j;
+            if (ch < nch) bad |= image_chunk<KIND>(ch, v[j], lds, sxw, 0u, 0u);
+        }
+        for (uint32_t ch = tid + nt * GU_IMG_PT; ch < nch; ch += nt) {
+            float4 w[2];
+            load_chunk(ws.xn, 8u * ch, d.H, w);
+            bad |= image_chunk<KIND>(ch, w, lds, sxw, 0u, 0u);
+        }
+        if (bad && lead && slot == 0) atomicOr(ws.status, HK_DEVERR_NONFINITE);  // every workgroup's image is the same
     }
     __syncthreads();
     const int32_t id = routed ? sel_id : (int32_t)d.E;
@@ -459,8 +471,7 @@ static hipError_t launch_layer(const MoeDims& d, const MoeLayerDev& L, const flo
     const uint32_t slots = d.K + (d.has_shared ? 1u : 0u);
     const uint32_t gu_tiles = n_tiles_for(d.has_shared ? max(d.I, d.SI) : d.I);
     const uint32_t img_stride = (uint32_t)moe_img_bytes(KIND, d.Imax);
-    const uint32_t nib = (n_steps_for(KIND, d.H) * tile_step_cols(KIND) + 2047u) / 2048u;  // image blocks, 2048 columns each
-    hipLaunchKernelGGL(moe_route_kernel<KIND>, dim3(nrb + nib), dim3(256), moe_route_lds_bytes(KIND, d.H), s, d, L,
+    hipLaunchKernelGGL(moe_route_kernel<KIND>, dim3(nrb + 1u), dim3(256), moe_route_lds_bytes(KIND, d.H), s, d, L,
                        h_in, ws);
     const dim3 gg(gu_tiles, slots);
     const size_t gl = moe_gate_up_lds_bytes(KIND, d.H);
