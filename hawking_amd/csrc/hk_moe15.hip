@@ -198,10 +198,11 @@ __device__ __forceinline__ void wave_share(uint32_t S, uint32_t wave, uint32_t& 
 }
 
 // q8 rows of tile T of o[0..R-1] (cols H) against xn, in a block of its own:
-// the weights' first D steps per wave (a wave's whole share at H = 2048) are
-// in flight while xn is formed in registers and each thread scatters its
-// chunks of the q8 x image (E = 0: one exponent per 16-column unit, no
-// block-wide maximum) into LDS.
+// the weights' first D steps per wave (a wave's whole share at H = 2048, for
+// one organ or two: the shared expert's gate/up blocks take D = 8 too, 163
+// VGPRs, which one block per CU affords) are in flight while xn is formed in
+// registers and each thread scatters its chunks of the q8 x image (E = 0:
+// one exponent per 16-column unit, no block-wide maximum) into LDS.
 template <int R, int D = 8 / R>
 __device__ __forceinline__ void q8_tile(const M15Dims& d, const M15Dev& L, const float* h, const OrganView (&o)[R],
                                         uint32_t T, uint8_t* lds, float* red, float* part, uint32_t* status,
@@ -258,7 +259,7 @@ __global__ void __launch_bounds__(256) m15_route_kernel(M15Dims d, M15Dev L, con
     } else if (b < nR + nG + nS) {
         const uint32_t T = b - nR - nG;
         const OrganView o[2] = {L.sg, L.su};
-        q8_tile<2>(d, L, h, o, T, lds, red, part, ws.status, v);
+        q8_tile<2, 8>(d, L, h, o, T, lds, red, part, ws.status, v);
         const uint32_t row = T * 16u + threadIdx.x;
         if (threadIdx.x < 16 && row < d.SI) ws.act_s[row] = (v[0] / (1.0f + expf(-v[0]))) * v[1];
     } else {
