@@ -160,6 +160,25 @@ __device__ __forceinline__ void copy16x3_to_lds(uint4* dst0, const uint4* src0, 
 // robin by linear id, so ids 8 apart share an XCD and its L2: each run of
 // 8 * parts ids covers 8 organs with id % 8 selecting the organ, and all
 // parts of an organ (which read the same x) land on one XCD.
+// Make a kernel-argument value available here: the argument segment is
+// fresh memory at every launch (a full memory round trip), and the compiler
+// otherwise loads each field where a branch first needs it, one round trip
+// per branch level; a kernel that branches on its arguments names the fields
+// its branches read at its top, so all are loaded in one round.  Emits no
+// instruction.
+template <class V>
+__device__ __forceinline__ void arg_here(V v) {
+    asm volatile("" ::"s"(v));
+}
+__device__ __forceinline__ void view_here(const OrganView& o) {
+    arg_here(o.data);
+    arg_here(o.scales);
+    arg_here(o.steps);
+    arg_here(o.n_tiles);
+    arg_here(o.rows);
+    arg_here(o.cols);
+}
+
 __device__ __forceinline__ void organ_part(uint32_t L, uint32_t parts, uint32_t n, uint32_t* organ, uint32_t* part) {
     const uint32_t c = L / (8u * parts), r = L % (8u * parts), g = min(8u, n - 8u * c);
     *organ = 8u * c + r % g;

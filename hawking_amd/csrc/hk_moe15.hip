@@ -238,6 +238,24 @@ __global__ void __launch_bounds__(256) m15_route_kernel(M15Dims d, M15Dev L, con
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float red[8];
     __shared__ float part[4 * 2 * 16];
+    // every descriptor field a role reads, in one round trip before the role branch
+    arg_here(d.H);
+    arg_here(d.E);
+    arg_here(d.SI);
+    arg_here(d.eps);
+    arg_here(ws.logits);
+    arg_here(ws.gate);
+    arg_here(ws.act_s);
+    arg_here(ws.xn);
+    arg_here(ws.img);
+    arg_here(ws.img_e);
+    arg_here(ws.status);
+    view_here(L.router);
+    view_here(L.sgate);
+    view_here(L.sg);
+    view_here(L.su);
+    arg_here(L.norm_w);
+    arg_here(h);
     const uint32_t nR = L.router.n_tiles, nG = L.sgate.n_tiles, nS = nG ? L.sg.n_tiles : 0u;
     const uint32_t b = blockIdx.x;
     float v[2] = {0.0f, 0.0f};
