@@ -580,7 +580,7 @@ static hipError_t launch_kind(const OrganView* organs, uint32_t n, const OrganVi
 #ifndef HK_HEAD_R
 #define HK_HEAD_R 2
 #define HK_HEAD_D 3
-#define HK_HEAD_TPW 8
+#define HK_HEAD_TPW 5
 #endif
 #ifndef HK_MIX_R
 #define HK_MIX_R 1
@@ -611,8 +611,10 @@ static hipError_t launch_r(const OrganView* organs, uint32_t n, const OrganView&
 // The terminal head on a q8 lm_head (cols <= 8192): one GEMV launch with the
 // norm prologue and the greedy-key epilogue, then the one-thread pick (which
 // also clears the key for the next call).  Launch shapes as for one q8 organ,
-// except 4,096-16,383 tiles (a 65k-262k vocabulary), where 3 steps in flight
-// over 8 tiles per workgroup measured fastest (151,936 x 2048: 59.6 vs 62.6 us).
+// except 4,096-16,383 tiles (a 65k-262k vocabulary), where 2-tile groups, 3
+// steps in flight, over 5 tiles per workgroup measured fastest (151,936 x
+// 2048: 1,900 workgroups, under the 2,048 resident at once; 56.5 us against
+// 57.6 for 6 tiles, 59.3 for 8, 64.0 for 4).
 __global__ void head_pick_fused_kernel(uint64_t* __restrict__ key, int32_t* __restrict__ token, uint32_t* status) {
     if (threadIdx.x == 0) {
         const uint64_t best = key[0];
