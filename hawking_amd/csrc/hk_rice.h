@@ -97,16 +97,17 @@ __device__ __forceinline__ void rice_rows_from(const ResView& v, const float* __
         __syncthreads();
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
+            // rows start at multiples of four records and batches at
+            // multiples of eight, so a row's products are whole 16-byte
+            // pieces: four per LDS read, added in order
             const uint32_t lo = max(t.my0[h], base), hi = min(t.my1[h], base + RICE_BATCH);
-            uint32_t e = lo;
-            for (; e + 8 <= hi; e += 8) {  // eight reads in flight, adds in order
-                float q[8];
-#pragma unroll
-                for (int k = 0; k < 8; ++k) q[k] = vals[e - base + (uint32_t)k];
-#pragma unroll
-                for (int k = 0; k < 8; ++k) acc[h] += q[k];
+            const float4* v4 = reinterpret_cast<const float4*>(vals + (lo - base));
+            const uint32_t n4 = hi > lo ? (hi - lo) / 4u : 0u;
+#pragma unroll 4
+            for (uint32_t j = 0; j < n4; ++j) {
+                const float4 q = v4[j];
+                acc[h] = (((acc[h] + q.x) + q.y) + q.z) + q.w;
             }
-            for (; e < hi; ++e) acc[h] += vals[e - base];
         }
     }
 }
