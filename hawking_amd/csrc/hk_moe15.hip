@@ -14,12 +14,12 @@
 //                (512 columns each) and publish xn.
 //   2. gate/up:  one workgroup per (16-row tile, slot): wave 0 ranks the
 //                logits (softmax / top-k / renormalise) to find the slot's
-//                expert while the others load the binary image; both binary
-//                bases share each image fetch; the epilogue adds the up's
-//                Rice residual in index order (rice_rows_from, its records
-//                fetched with the weights) and applies
-//                SwiGLU.  Tile 0 of each slot publishes the slot's two down
-//                factors.
+//                expert while the others load the binary image and the
+//                tile's row of record starts per expert; both binary bases
+//                share each image fetch; the epilogue adds the up's Rice
+//                residual in index order (rice_rows_from, its records
+//                fetched with the weights) and applies SwiGLU.  Tile 0 of
+//                each slot publishes the slot's two down factors.
 //   3. down R:   mid_r = R_r act_r (3-bit factor) per (slot, 16-row tile),
 //                and the shared expert's q8 down per 16-row tile.
 //   4. down L:   one workgroup per 16-row output tile, one wave per slot
@@ -72,6 +72,11 @@ struct M15Dev {
     const OrganView* dr;                     // [E] down right factor (rank x I)
     const OrganView* dl;                     // [E] down left factor (H x rank)
     const M15Expert* ex;                     // [E] compact gate/up records
+    // [n_tiles(I) + 1][tstride]: entry (T, e) is expert e's up residual
+    // row_ptr[min(16 T, I)], so rows T and T + 1 give every expert's record
+    // range of tile T (tstride = E rounded up to a multiple of 4)
+    const uint32_t* tstart;
+    uint32_t tstride;
     uint32_t g_soff, u_soff, rec_off;        // scales - data (gate, up), recs - row_ptr (bytes)
 };
 
@@ -330,6 +335,7 @@ __global__ void __launch_bounds__(256) m15_gate_up_kernel(M15Dims d, M15Dev L, M
     const OrganView g0 = L.gate[0], u0 = L.up[0];
     const ResView r0v = L.res[0];
     M15Expert* ext = reinterpret_cast<M15Expert*>(lds + ib16 + (size_t)d.H * 4u + (size_t)RICE_BATCH * 4u);
+    uint32_t* tsl = reinterpret_cast<uint32_t*>(ext + d.E);  // rows T and T + 1 of the tile-start table
     if (wave == 0) {
         const bool pub = T == 0 && slot == 0;
         const ArgBest mine = softmax_topk_wave<NPL>(ws.logits, d.E, d.K, 1, pub ? ws.ids : nullptr,
@@ -340,11 +346,21 @@ __global__ void __launch_bounds__(256) m15_gate_up_kernel(M15Dims d, M15Dev L, M
         }
         if ((uint32_t)lane == slot) sel_id = mine.i;
     } else {
-        // the binary image, xn (for the residual) and the expert records into LDS
+        // the binary image, xn (for the residual), the expert records and the
+        // tile's two rows of record starts into LDS (at most two 16-byte
+        // pieces per thread: tstride <= 512 <= 4 (blockDim.x - 64), as
+        // n_experts <= 512 is checked at create)
+        const uint32_t tt = threadIdx.x - 64u, nt = blockDim.x - 64u, nts = L.tstride / 2u;
+        const uint4* tsrc = reinterpret_cast<const uint4*>(L.tstart + (size_t)T * L.tstride);
+        uint4 tv[2];
+#pragma unroll
+        for (uint32_t i = 0; i < 2u; ++i) tv[i] = ldg(tsrc + min(tt + nt * i, nts - 1u));
         copy16x3_to_lds<12>(reinterpret_cast<uint4*>(lds), reinterpret_cast<const uint4*>(ws.img), ib / 16u,
                             reinterpret_cast<uint4*>(lds + ib16), reinterpret_cast<const uint4*>(ws.xn), d.H / 4u,
-                            reinterpret_cast<uint4*>(ext), reinterpret_cast<const uint4*>(L.ex), 2u * d.E,
-                            threadIdx.x - 64u, blockDim.x - 64u);
+                            reinterpret_cast<uint4*>(ext), reinterpret_cast<const uint4*>(L.ex), 2u * d.E, tt, nt);
+#pragma unroll
+        for (uint32_t i = 0; i < 2u; ++i)
+            if (tt + nt * i < nts) reinterpret_cast<uint4*>(tsl)[tt + nt * i] = tv[i];
     }
     __syncthreads();
     const int32_t id = sel_id;
@@ -369,15 +385,15 @@ __global__ void __launch_bounds__(256) m15_gate_up_kernel(M15Dims d, M15Dev L, M
     o[1].scales = reinterpret_cast<const uint16_t*>(ex.up + L.u_soff);
     uint32_t s0, n;
     wave_share(S, wave, s0, n);
-    // the residual's row pointers first, then the weights, then the first
-    // records (which wait for the row pointers only)
+    // the rows' residual pointers, the weights, then the first records: the
+    // tile's record range comes from LDS, so no global load precedes them
     ResView rv = r0v;
     rv.row_ptr = ex.rptr;
     rv.recs = reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(ex.rptr) + L.rec_off);
     rv.scale = ex.rscale;
     const uint32_t r0 = T * 16u, r1 = min(r0 + 16u, d.I);
     RiceTile rt;
-    rice_ranges(rv, r0, r1, rt);
+    rice_ranges_known(rv, r0, r1, tsl[id], tsl[L.tstride + (uint32_t)id], rt);
     Frag<HK_BIN, 2> f[M15_D];
     fetch_first<HK_BIN, 2>(o, T, s0, n, lane, f);
     rice_first_records(rv, rt);
@@ -506,6 +522,16 @@ __global__ void __launch_bounds__(1024) m15_down_l_kernel(M15Dims d, const float
     }
 }
 
+// The tile-start table: ts[T * stride + e] = expert e's up residual
+// row_ptr[min(16 T, I)] for T = 0..nt (zero for the padding entries e >= E).
+__global__ void m15_tile_starts_kernel(const M15Expert* __restrict__ ex, uint32_t E, uint32_t I, uint32_t nt,
+                                       uint32_t stride, uint32_t* __restrict__ ts) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= (nt + 1u) * stride) return;
+    const uint32_t T = i / stride, e = i % stride;
+    ts[i] = e < E ? ex[e].rptr[min(16u * T, I)] : 0u;
+}
+
 }  // namespace hk
 
 using namespace hk;
@@ -596,7 +622,9 @@ extern "C" int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* s, h
     const uint32_t Sb = n_steps_for(HK_BIN, H), Sq = n_steps_for(HK_Q8, H), Sr = n_steps_for(HK_U3, I),
                    Sl = n_steps_for(HK_U3, rank), Ss = SI ? n_steps_for(HK_Q8, SI) : 0u;
     L->lds_route = x_lds_bytes<HK_Q8>(Sq);
-    L->lds_gu = align16(x_lds_bytes<HK_BIN>(Sb)) + (size_t)H * 4u + (size_t)RICE_BATCH * 4u + (size_t)E * sizeof(M15Expert);
+    const uint32_t nti = n_tiles_for(I), tstride = (E + 3u) & ~3u;
+    L->lds_gu = align16(x_lds_bytes<HK_BIN>(Sb)) + (size_t)H * 4u + (size_t)RICE_BATCH * 4u +
+                (size_t)E * sizeof(M15Expert) + (size_t)2u * tstride * 4u;
     L->lds_dr = std::max(x_lds_bytes<HK_U3>(Sr), SI ? x_lds_bytes<HK_Q8>(Ss) : (size_t)0);
     L->dl_img_stride = (uint32_t)align16(x_lds_bytes<HK_U3>(Sl));
     L->lds_dl = (size_t)K * L->dl_img_stride + (size_t)K * 16u * 4u;
@@ -613,7 +641,8 @@ extern "C" int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* s, h
     };
     const size_t o_norm = take(H * 4), o_gate = take(E * sizeof(OrganView)), o_up = take(E * sizeof(OrganView)),
                  o_res = take(E * sizeof(ResView)), o_dr = take(E * sizeof(OrganView)),
-                 o_dl = take(E * sizeof(OrganView)), o_ex = take(E * sizeof(M15Expert)), o_logits = take(E * 4), o_glogit = take(16), o_xn = take(H * 4),
+                 o_dl = take(E * sizeof(OrganView)), o_ex = take(E * sizeof(M15Expert)),
+                 o_ts = take((size_t)(nti + 1u) * tstride * 4u), o_logits = take(E * 4), o_glogit = take(16), o_xn = take(H * 4),
                  o_img = take(x_lds_bytes<HK_BIN>(Sb)), o_imge = take(4), o_act = take((size_t)K * I * 4),
                  o_acts = take(SI * 4 + 16), o_mid = take((size_t)K * rank * 4), o_ys = take(H * 4),
                  o_ids = take(K * 4), o_w = take(K * 4), o_sel = take(2 * K * sizeof(OrganView)),
@@ -635,6 +664,8 @@ extern "C" int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* s, h
     dv.dr = reinterpret_cast<const OrganView*>(m + o_dr);
     dv.dl = reinterpret_cast<const OrganView*>(m + o_dl);
     dv.ex = reinterpret_cast<const M15Expert*>(m + o_ex);
+    dv.tstart = reinterpret_cast<const uint32_t*>(m + o_ts);
+    dv.tstride = tstride;
     dv.g_soff = (uint32_t)g_soff;
     dv.u_soff = (uint32_t)u_soff;
     dv.rec_off = (uint32_t)rec_off;
@@ -664,6 +695,13 @@ extern "C" int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* s, h
     if (!rc) rc = up_copy(dv.dr, rvv.data(), E * sizeof(OrganView));
     if (!rc) rc = up_copy(dv.dl, lv.data(), E * sizeof(OrganView));
     if (!rc) rc = up_copy(dv.ex, exv.data(), E * sizeof(M15Expert));
+    if (!rc) {
+        const uint32_t n = (nti + 1u) * tstride;
+        hipLaunchKernelGGL(m15_tile_starts_kernel, dim3((n + 255u) / 256u), dim3(256), 0, 0, dv.ex, E, I, nti, tstride,
+                           const_cast<uint32_t*>(dv.tstart));
+        rc = check_hip(ctx, hipGetLastError(), "mixed-1p5 tile starts");
+        if (!rc) rc = check_hip(ctx, hipDeviceSynchronize(), "mixed-1p5 tile starts");
+    }
     if (rc) {
         (void)hipFree(L->mem);
         return rc;

@@ -37,6 +37,20 @@ __device__ __forceinline__ void rice_ranges(const ResView& v, uint32_t r0, uint3
         t.my1[h] = ldg(v.row_ptr + min(row + 1u, r1));
     }
 }
+// rice_ranges for a caller that already holds the range (e0 = row_ptr[r0],
+// e1 = row_ptr[r1], say from a table in LDS): only the rows' own pointers
+// are loaded, and the first records need not wait for any global load.
+__device__ __forceinline__ void rice_ranges_known(const ResView& v, uint32_t r0, uint32_t r1, uint32_t e0,
+                                                  uint32_t e1, RiceTile& t) {
+    t.e0 = e0;
+    t.e1 = e1;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t row = min(r0 + threadIdx.x + 256u * (uint32_t)h, r1);
+        t.my0[h] = ldg(v.row_ptr + row);
+        t.my1[h] = ldg(v.row_ptr + min(row + 1u, r1));
+    }
+}
 __device__ __forceinline__ void rice_first_records(const ResView& v, RiceTile& t) {
     rice_load_batch(v, t.e0 & ~7u, t.e1, t.rv);
 }
