@@ -398,14 +398,24 @@ __global__ void __launch_bounds__(256) m15_gate_up_kernel(M15Dims d, M15Dev L, M
     fetch_first<HK_BIN, 2>(o, T, s0, n, lane, f);
     rice_first_records(rv, rt);
     const int E = ws.img_e[0];
+    // the residual's first batch of products as soon as its records land
+    // (xn has been in LDS since the barrier above, and the records were
+    // issued right after this wave's weights, so the steps below find their
+    // data there); block_rows' barrier then publishes them to the row sums
+    float* xs = reinterpret_cast<float*>(lds + ib16);
+    float* vals = xs + d.H;
+    const uint32_t b0 = rt.e0 & ~7u;
+    rice_products(rv, rt, b0, xs, vals);
     float acc[2] = {0.0f, 0.0f};
     run_steps<HK_BIN, 2>(o, T, s0, n, lds, S, lane, f, acc);
     float v[2] = {0.0f, 0.0f};
     block_rows<2>(acc, part, E, v);
     // the up's residual after its base, each row's outliers in index order
+    // (the first batch here, any further batch of a long tile after it)
     float racc[2] = {threadIdx.x < 16 ? v[1] : 0.0f, 0.0f};
-    float* xs = reinterpret_cast<float*>(lds + ib16);
-    rice_rows_from(rv, ws.xn, rt, racc, xs, xs + d.H, true);
+    rice_load_batch(rv, b0 + RICE_BATCH, rt.e1, rt.rv);
+    rice_row_sums(rt, b0, vals, racc);
+    rice_batches_from(rv, rt, b0 + RICE_BATCH, racc, xs, vals);
     const uint32_t row = r0 + threadIdx.x;
     if (threadIdx.x < 16 && row < d.I) ws.act[(size_t)slot * d.I + row] = (v[0] / (1.0f + expf(-v[0]))) * racc[0];
 }
