@@ -8,8 +8,8 @@
 // (hk_mfma.h), no host round trip; the route never leaves the device:
 //   1. route:    every block recomputes xn = RMSNorm(1+w)(h) in LDS.  Router
 //                tiles (16 logits each), the shared-expert gate row, and the
-//                shared expert's gate/up tiles (SwiGLU in the epilogue) each
-//                build a q8 x image of xn of their own; the last blocks
+//                shared expert's gate and up tiles (one organ per block)
+//                each build a q8 x image of xn of their own; the last blocks
 //                build the binary x image of xn for the routed gate/up
 //                (512 columns each) and publish xn.
 //   2. gate/up:  one workgroup per (16-row tile, slot): wave 0 ranks the
@@ -21,7 +21,8 @@
 //                fetched with the weights) and applies SwiGLU.  Tile 0 of
 //                each slot publishes the slot's two down factors.
 //   3. down R:   mid_r = R_r act_r (3-bit factor) per (slot, 16-row tile),
-//                and the shared expert's q8 down per 16-row tile.
+//                and the shared expert's q8 down per 16-row tile (its x
+//                image formed from silu(gate) * up).
 //   4. down L:   one workgroup per 16-row output tile, one wave per slot
 //                (y_r = L_r mid_r, an x image per wave); the block combines
 //                out = h + (sum_r w_r y_r in slot order + sigmoid(g) y_s).
@@ -87,7 +88,7 @@ struct M15Ws {
     uint8_t* img;    // binary x image of xn
     int32_t* img_e;  // [1]
     float* act;      // [K * I]
-    float* act_s;    // [SI]
+    float* act_s;    // [2 SI]: the shared expert's gate, then up projection (SwiGLU formed by their reader)
     float* mid;      // [K * rank]
     float* ys;       // [H] shared expert output (ungated)
     int32_t* ids;    // [K]
@@ -279,17 +280,19 @@ __global__ void __launch_bounds__(256) m15_route_kernel(M15Dims d, M15Dev L, con
             ws.gate[1] = g;
             if (!(isfinite(g) && g >= 0.0f && g <= 1.0f)) atomicOr(ws.status, HK_DEVERR_NONFINITE);
         }
-    } else if (b < nR + nG + nS) {
-        const uint32_t T = b - nR - nG;
-        const OrganView o[2] = {L.sg, L.su};
-        q8_tile<2, 8>(d, L, h, o, T, lds, red, part, ws.status, v);
+    } else if (b < nR + nG + 2u * nS) {
+        // a 16-row tile of the shared expert's gate (the first nS blocks) or
+        // up projection (the next nS), each block one organ's share
+        const uint32_t k = b - nR - nG, which = k >= nS ? 1u : 0u, T = k - which * nS;
+        const OrganView o[1] = {which ? L.su : L.sg};
+        q8_tile<1>(d, L, h, o, T, lds, red, part, ws.status, v);
         const uint32_t row = T * 16u + threadIdx.x;
-        if (threadIdx.x < 16 && row < d.SI) ws.act_s[row] = (v[0] / (1.0f + expf(-v[0]))) * v[1];
+        if (threadIdx.x < 16 && row < d.SI) ws.act_s[which * d.SI + row] = v[0];
     } else {
         // the binary x image of xn (E = 0), one 512-column step per block,
         // scattered by the wave whose threads hold that step's 64 chunks;
         // the first block publishes xn
-        const uint32_t tb = b - nR - nG - nS, S = n_steps_for(HK_BIN, d.H), nch = d.H / 8u;
+        const uint32_t tb = b - nR - nG - 2u * nS, S = n_steps_for(HK_BIN, d.H), nch = d.H / 8u;
         XnRegs x;
         block_xn(h, L.norm_w, d.H, d.eps, red, x);
         if (tb == 0) {
@@ -439,6 +442,29 @@ __device__ __forceinline__ bool scatter_image(const float* __restrict__ x, uint3
     return bad;
 }
 
+// scatter_image of silu(g) * u (the shared expert's SwiGLU, formed from its
+// two projections with the routed epilogue's expression).
+template <int KIND>
+__device__ __forceinline__ bool scatter_image_swiglu(const float* __restrict__ g, const float* __restrict__ u,
+                                                     uint32_t cols, uint32_t S, uint8_t* img) {
+    if (threadIdx.x < 64u) image_zero_blocks<KIND>(threadIdx.x, img, S);
+    float* sx = reinterpret_cast<float*>(img + (size_t)S * Kcfg<KIND>::P * A_TILE_STRIDE);
+    const uint32_t nch = S * (uint32_t)Kcfg<KIND>::STEP_COLS / 8u;
+    bool bad = false;
+    for (uint32_t ch = threadIdx.x; ch < nch; ch += blockDim.x) {
+        float4 a[2], v[2];
+        load_chunk(g, 8u * ch, cols, a);
+        load_chunk(u, 8u * ch, cols, v);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            v[j] = make_float4((a[j].x / (1.0f + expf(-a[j].x))) * v[j].x, (a[j].y / (1.0f + expf(-a[j].y))) * v[j].y,
+                               (a[j].z / (1.0f + expf(-a[j].z))) * v[j].z, (a[j].w / (1.0f + expf(-a[j].w))) * v[j].w);
+        bad |= image_chunk<KIND>(ch, v, img, sx, 0u, 0u);
+    }
+    __syncthreads();
+    return bad;
+}
+
 // Down right factors (mid_r = R_r act_r) and the shared expert's down.
 __global__ void __launch_bounds__(256) m15_down_r_kernel(M15Dims d, M15Dev L, M15Ws ws) {
     extern __shared__ __align__(16) uint8_t lds[];
@@ -471,7 +497,7 @@ __global__ void __launch_bounds__(256) m15_down_r_kernel(M15Dims d, M15Dev L, M1
         wave_share(S, wave, s0, n);
         Frag<HK_Q8, 1> f[M15_D];
         fetch_first<HK_Q8, 1>(o, T, s0, n, lane, f);
-        bad = scatter_image<HK_Q8>(ws.act_s, d.SI, S, lds);
+        bad = scatter_image_swiglu<HK_Q8>(ws.act_s, ws.act_s + d.SI, d.SI, S, lds);
         float acc[1] = {0.0f};
         run_steps<HK_Q8, 1>(o, T, s0, n, lds, S, lane, f, acc);
         block_rows<1>(acc, part, 0, v);
@@ -640,7 +666,7 @@ extern "C" int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* s, h
     L->lds_dl = (size_t)K * L->dl_img_stride + (size_t)K * 16u * 4u;
     if (std::max({L->lds_route, L->lds_gu, L->lds_dr, L->lds_dl}) > 64u * 1024u)
         return set_error(ctx, HK_E_UNSUPPORTED, "mixed-1p5 layer: shapes need more than 64 KB of LDS per workgroup");
-    L->n_route_blocks = rv.n_tiles + (SI ? 1u + s->shared_gate_proj->view.n_tiles : 0u) + Sb;
+    L->n_route_blocks = rv.n_tiles + (SI ? 1u + 2u * s->shared_gate_proj->view.n_tiles : 0u) + Sb;
     L->n_dr_blocks = K * n_tiles_for(rank) + (SI ? n_tiles_for(H) : 0u);
     // one allocation: tables and workspace (each section 256-B aligned)
     size_t off = 0;
@@ -654,7 +680,7 @@ extern "C" int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* s, h
                  o_dl = take(E * sizeof(OrganView)), o_ex = take(E * sizeof(M15Expert)),
                  o_ts = take((size_t)(nti + 1u) * tstride * 4u), o_logits = take(E * 4), o_glogit = take(16), o_xn = take(H * 4),
                  o_img = take(x_lds_bytes<HK_BIN>(Sb)), o_imge = take(4), o_act = take((size_t)K * I * 4),
-                 o_acts = take(SI * 4 + 16), o_mid = take((size_t)K * rank * 4), o_ys = take(H * 4),
+                 o_acts = take(2 * SI * 4 + 16), o_mid = take((size_t)K * rank * 4), o_ys = take(H * 4),
                  o_ids = take(K * 4), o_w = take(K * 4), o_sel = take(2 * K * sizeof(OrganView)),
                  o_hbuf = take(H * 4);
     if (hipMalloc(&L->mem, off) != hipSuccess) return set_error(ctx, HK_E_NOMEM, "mixed-1p5 layer allocation failed");
