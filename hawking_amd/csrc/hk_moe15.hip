@@ -204,10 +204,10 @@ __device__ __forceinline__ void wave_share(uint32_t S, uint32_t wave, uint32_t& 
 }
 
 // q8 rows of tile T of o[0..R-1] (cols H) against xn, in a block of its own:
-// the weights' first D steps per wave (a wave's whole share at H = 2048, for
-// one organ or two: the shared expert's gate/up blocks take D = 8 too, 163
-// VGPRs, which one block per CU affords) are in flight while xn is formed in
-// registers and each thread scatters its chunks of the q8 x image (E = 0:
+// the weights' first D steps per wave (a wave's whole share at H = 2048;
+// every route block runs one organ: router, shared gate, or one of the
+// shared expert's gate and up projections) are in flight while xn is formed
+// in registers and each thread scatters its chunks of the q8 x image (E = 0:
 // one exponent per 16-column unit, no block-wide maximum) into LDS.
 template <int R, int D = 8 / R>
 __device__ __forceinline__ void q8_tile(const M15Dims& d, const M15Dev& L, const float* h, const OrganView (&o)[R],
