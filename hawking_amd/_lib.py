@@ -22,6 +22,7 @@ HK_E_NOMEM = 7
 
 HK_Q4, HK_BIN, HK_MIXED, HK_F32, HK_Q8, HK_U3, HK_BIN_RICE = 0, 1, 2, 3, 4, 5, 6
 HK_ROUTER_SOFTMAX, HK_ROUTER_NOAUX_TC = 0, 1
+HK_STACK_PER_LAYER, HK_STACK_PERSISTENT = 0, 1
 
 STATUS_NAMES = {
     HK_OK: "HK_OK", HK_E_INVALID_ARG: "HK_E_INVALID_ARG", HK_E_GEOMETRY: "HK_E_GEOMETRY",
@@ -68,7 +69,8 @@ class MoeConfig(C.Structure):
         ("n_layers", _u32), ("hidden", _u32), ("inter", _u32), ("shared_inter", _u32),
         ("n_experts", _u32), ("top_k", _u32), ("expert_kind", _i32), ("expert_group", _i32),
         ("shared_gate", _i32), ("eps", C.c_float), ("router", _i32), ("n_group", _u32), ("topk_group", _u32),
-        ("norm_topk_prob", _i32), ("routed_scaling_factor", C.c_float),
+        ("norm_topk_prob", _i32), ("routed_scaling_factor", C.c_float), ("route_tie_eps", C.c_float),
+        ("stack_launch", _i32),
     ]
 
 
@@ -82,7 +84,7 @@ class MoeLayerSrc(C.Structure):
 class Moe15LayerSrc(C.Structure):
     _fields_ = [
         ("hidden", _u32), ("inter", _u32), ("shared_inter", _u32), ("n_experts", _u32), ("top_k", _u32),
-        ("eps", C.c_float), ("norm_w", _p), ("router", _p), ("shared_gate", _p), ("shared_gate_proj", _p),
+        ("eps", C.c_float), ("route_tie_eps", C.c_float), ("norm_w", _p), ("router", _p), ("shared_gate", _p), ("shared_gate_proj", _p),
         ("shared_up", _p), ("shared_down", _p), ("gate", _p), ("up", _p), ("down_left", _p), ("down_right", _p),
     ]
 
@@ -109,6 +111,7 @@ PROTOTYPES = {
     "hk_event_record": (C.c_int, [_p, _p, _p]),
     "hk_event_elapsed_ms": (C.c_int, [_p, _p, _p, C.POINTER(C.c_float)]),
     "hk_check_device_status": (C.c_int, [_p, _p, C.POINTER(_u32)]),
+    "hk_stream_control": (C.c_int, [_p, _p, _sz, _p, _u32, _p]),
     "hk_organ_upload": (C.c_int, [_p, C.POINTER(OrganSrc), _p, C.POINTER(_p)]),
     "hk_organ_free": (C.c_int, [_p, _p]),
     "hk_organ_info": (C.c_int, [_p, C.POINTER(_i32), C.POINTER(_i32), C.POINTER(_u32),
@@ -159,6 +162,7 @@ PROTOTYPES = {
     "hk_moe_decode_layer": (C.c_int, [_p, _p, _u32, _p, _p, _p, _p, _p]),
     "hk_moe_decode_stack": (C.c_int, [_p, _p, _p, _p, _p, _p, _p]),
     "hk_moe_decode_stack_persistent": (C.c_int, [_p, _p, _p]),
+    "hk_moe_model_set_stack_launch": (C.c_int, [_p, _p, _i32]),
     "hk_moe_forward_batch": (C.c_int, [_p, _p, _u32, _p, _u32, _p, _p, _p, _p]),
     "hk_moe15_layer_create": (C.c_int, [_p, C.POINTER(Moe15LayerSrc), C.POINTER(_p)]),
     "hk_moe15_layer_free": (C.c_int, [_p, _p]),

@@ -32,8 +32,8 @@ CFLAGS = [
     f"-I{os.path.join(ROOT, 'include')}",
 ]
 SOURCES = ["hk_api.cpp", "hk_gemv2.hip", "hk_repack.hip", "hk_pack.hip", "hk_router.hip", "hk_moe.hip",
-           "hk_moe_batch.hip", "hk_rice.hip", "hk_head.hip", "hk_container.cpp", "hk_moe15.hip",
-           "hk_moe_stack.hip"]
+           "hk_moe_batch.hip", "hk_rice.hip", "hk_head.hip", "hk_container.cpp", "hk_parse.cpp", "hk_moe15.hip",
+           "hk_moe_stack.hip", "hk_control.hip"]
 
 
 def _compile(src: str) -> str:

@@ -257,8 +257,9 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // this file-scope device array: every device the library runs on holds one
 // copy until the process ends.  Host code never passes the array's name to
 // a kernel (on the host it is only a stand-in symbol); it uses the device
-// address hipGetSymbolAddress returns, looked up once per device by
-// hk_ctx_create with that device current.
+// address hipGetSymbolAddress returns, looked up once per device on the
+// entry point's first call there, with that device current (a context that
+// never calls the entry point never looks it up, so it cannot fail on it).
 constexpr size_t NOALLOC_LOGITS = (size_t)HK_NOALLOC_HEAD_MAX_ROWS * 4;
 constexpr size_t NOALLOC_XN = (size_t)HK_NOALLOC_HEAD_MAX_COLS * 4;
 constexpr size_t NOALLOC_BYTES = NOALLOC_LOGITS + NOALLOC_XN + 256;
@@ -267,15 +268,22 @@ constexpr int NOALLOC_MAX_DEVICES = 64;
 static uint8_t* g_scratch_dev[NOALLOC_MAX_DEVICES] = {};
 static std::mutex g_scratch_mu;
 
-// Device address of this device's copy of `scratch` (looked up on the
-// first call for the device; the caller has made the device current).
+// Device address of this device's copy of `scratch`, looked up on the first
+// call for the device with that device made current (the caller's current
+// device is restored).
 static int noalloc_scratch(hk_ctx* ctx, uint8_t** out) {
     if (ctx->device < 0 || ctx->device >= NOALLOC_MAX_DEVICES)
         return set_error(ctx, HK_E_UNSUPPORTED, "no-allocation workspace: device index above 63");
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_dev[ctx->device]) {
+        int prev = -1;
+        hipError_t e = hipGetDevice(&prev);
+        if (e != hipSuccess) return check_hip(ctx, e, "hipGetDevice (no-allocation workspace)");
+        if (prev != ctx->device && (e = hipSetDevice(ctx->device)) != hipSuccess)
+            return check_hip(ctx, e, "hipSetDevice (no-allocation workspace)");
         void* ptr = nullptr;
-        hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (prev != ctx->device) (void)hipSetDevice(prev);
         if (e != hipSuccess) return check_hip(ctx, e, "hipGetSymbolAddress (no-allocation workspace)");
         g_scratch_dev[ctx->device] = static_cast<uint8_t*>(ptr);
     }
@@ -309,12 +317,6 @@ extern "C" int hk_ctx_create(int device, hk_ctx** out) {
     (void)hipMemset(st, 0, 512);
     ctx->dev_status = static_cast<uint32_t*>(st);
     ctx->pack_flag = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(st) + 256);
-    // this device's copy of the no-allocation workspace, with the device current
-    if (noalloc_scratch(ctx, &ctx->noalloc) != HK_OK) {
-        (void)hipFree(st);
-        delete ctx;
-        return HK_E_HIP;
-    }
     *out = ctx;
     return HK_OK;
 }
@@ -325,6 +327,17 @@ extern "C" void hk_ctx_destroy(hk_ctx* ctx) {
     (void)hipDeviceSynchronize();
     if (ctx->dev_status) (void)hipFree(ctx->dev_status);
     delete ctx;
+}
+
+extern "C" int hk_stream_control(hk_ctx* ctx, const void* data, size_t nbytes, float* out, uint32_t workgroups,
+                                 hk_stream stream) {
+    if (!ctx) return HK_E_INVALID_ARG;
+    if (!data || !out || nbytes < 16 || nbytes % 16 || (reinterpret_cast<uintptr_t>(data) & 15u))
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_stream_control: need a 16-byte aligned buffer of a multiple of 16 bytes");
+    if (workgroups == 0 || workgroups > (1u << 20))
+        return set_error(ctx, HK_E_INVALID_ARG, "hk_stream_control: workgroups must be in [1, 2^20]");
+    return check_hip(ctx, launch_stream_control(data, nbytes, out, workgroups, static_cast<hipStream_t>(stream)),
+                     "stream control launch");
 }
 
 extern "C" int hk_last_error(const hk_ctx* ctx, char* buf, size_t len) {
@@ -1223,6 +1236,10 @@ extern "C" int hk_terminal_greedy_noalloc(hk_ctx* ctx, const float* hidden, cons
         return set_error(ctx, HK_E_INVALID_ARG, "hk_terminal_greedy_noalloc: hidden must be 16-byte aligned");
     // [logits | xn | pick]: the pick slot is zero (static storage, and every
     // call leaves it zeroed)
+    if (!ctx->noalloc) {
+        const int st = noalloc_scratch(ctx, &ctx->noalloc);
+        if (st != HK_OK) return st;
+    }
     uint8_t* ws = ctx->noalloc;
     float* logits = reinterpret_cast<float*>(ws);
     float* xn = reinterpret_cast<float*>(ws + NOALLOC_LOGITS);
@@ -1486,6 +1503,10 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
     if (!rc && c.shared_inter) rc = validate_shape(ctx, c.expert_kind, grp, c.hidden, c.shared_inter);
     if (rc) return rc;
     if (!(c.eps > 0.0f) || !std::isfinite(c.eps)) return set_error(ctx, HK_E_INVALID_ARG, "moe config: eps must be positive");
+    if (!(c.route_tie_eps >= 0.0f) || !std::isfinite(c.route_tie_eps))
+        return set_error(ctx, HK_E_INVALID_ARG, "moe config: route_tie_eps must be finite and >= 0");
+    if (c.stack_launch != HK_STACK_PER_LAYER && c.stack_launch != HK_STACK_PERSISTENT)
+        return set_error(ctx, HK_E_INVALID_ARG, "moe config: stack_launch must be HK_STACK_PER_LAYER or HK_STACK_PERSISTENT");
     const uint32_t imax = std::max(c.inter, c.shared_inter);
     if (c.router == HK_ROUTER_SOFTMAX && (moe_gate_up_lds_bytes(c.expert_kind, c.hidden) > MOE_LDS_LIMIT ||
                                           moe_route_lds_bytes(c.expert_kind, c.hidden) > MOE_LDS_LIMIT ||
@@ -1494,7 +1515,8 @@ extern "C" int hk_moe_model_create(hk_ctx* ctx, const hk_moe_config* cfg, hk_moe
     hk_moe_model* m = new hk_moe_model();
     m->cfg = c;
     m->cfg.expert_group = grp;
-    m->dims = hk::MoeDims{c.hidden, c.inter, c.shared_inter, imax, c.n_experts, c.top_k, c.shared_inter ? 1 : 0, c.eps};
+    m->dims = hk::MoeDims{c.hidden,    c.inter, c.shared_inter, imax, c.n_experts, c.top_k, c.shared_inter ? 1 : 0,
+                          c.eps,       c.route_tie_eps};
     m->layers.resize(c.n_layers);
     const size_t dpl = dense_per_layer(c);
     const size_t tab = align256((size_t)(c.n_experts + 1) * 3 * sizeof(OrganView));
@@ -1887,11 +1909,16 @@ extern "C" int hk_moe_decode_layer(hk_ctx* ctx, hk_moe_model* m, uint32_t layer,
                      "moe layer launch");
 }
 
-// The persistent launch is opt-in (HK_MOE_PERSISTENT=1): at config-4 shapes
-// its hand-offs still cost more than the per-layer launch boundaries.
-static bool stack_enabled(const hk_moe_model* m) {
-    const char* pe = std::getenv("HK_MOE_PERSISTENT");
-    return m->ldev && pe && pe[0] == '1';
+// The persistent launch is selected per model (hk_moe_config.stack_launch);
+// the default is the per-layer launches, which are faster at config-4 shapes.
+static bool stack_enabled(const hk_moe_model* m) { return m->ldev && m->cfg.stack_launch == HK_STACK_PERSISTENT; }
+
+extern "C" int hk_moe_model_set_stack_launch(hk_ctx* ctx, hk_moe_model* m, int32_t stack_launch) {
+    if (!ctx || !m) return HK_E_INVALID_ARG;
+    if (stack_launch != HK_STACK_PER_LAYER && stack_launch != HK_STACK_PERSISTENT)
+        return set_error(ctx, HK_E_INVALID_ARG, "stack_launch must be HK_STACK_PER_LAYER or HK_STACK_PERSISTENT");
+    m->cfg.stack_launch = stack_launch;
+    return HK_OK;
 }
 
 static hk::StackArgs stack_args(hk_ctx* ctx, hk_moe_model* m, const float* h_in, float* h_out, int32_t* ids,
@@ -1939,7 +1966,8 @@ extern "C" int hk_moe_decode_stack(hk_ctx* ctx, hk_moe_model* m, const float* h_
     // be resident
     if (stack_enabled(m)) {
         if (m->tag > 0xF0000000u) {  // tags never wrap: clear the words and restart
-            int rc = check_hip(ctx, hipMemsetAsync(m->stack_mem, 0, m->stack_bytes, st), "hand-off clear");
+            int rc = check_hip(ctx, launch_zero_words(static_cast<uint64_t*>(m->stack_mem), m->stack_bytes / 8, st),
+                               "hand-off clear");
             if (rc) return rc;
             m->tag = 1;
         }

@@ -253,7 +253,8 @@ struct hk_ctx {
     // The packers' non-finite flag (its own 256-byte allocation; the packers
     // synchronise their stream before they return, so calls never overlap).
     uint32_t* pack_flag = nullptr;
-    // This device's copy of the no-allocation workspace (a static device array).
+    // This device's copy of the no-allocation workspace (a static device
+    // array), looked up on the first hk_terminal_greedy_noalloc call.
     uint8_t* noalloc = nullptr;
 };
 
@@ -277,6 +278,8 @@ struct ResView;
 hipError_t launch_gemv_rice(const OrganView* organs_dev, const ResView* res_dev, uint32_t n, const OrganView& sh,
                             uint32_t pieces256, uint32_t pieces512, const float* x, size_t x_stride, float* y,
                             size_t y_stride, hipStream_t s, bool* fused);
+// The read-only bandwidth control (hk_control.hip).
+hipError_t launch_stream_control(const void* data, size_t nbytes, float* out, uint32_t workgroups, hipStream_t s);
 hipError_t launch_gemv_tiled(const OrganView* organs_dev, uint32_t n, const OrganView& shape,
                              const float* x, size_t x_stride, float* y, size_t y_stride,
                              hipStream_t s);

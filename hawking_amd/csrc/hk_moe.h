@@ -15,6 +15,7 @@ struct MoeDims {
     uint32_t K;      // top-k
     int32_t has_shared;
     float eps;
+    float tie_eps;   // router tie window (route_tie_epsilon); 0 = strict '>'
 };
 
 // One layer's device weights; table holds (E+1)*3 tiled organ views:
@@ -105,6 +106,8 @@ struct StackArgs {
     uint32_t ng, gu_tiles;
 };
 size_t moe_stack_lds_bytes(int kind, const MoeDims& d);
+// Zeroes n 64-bit words on stream s with a kernel (graph-capture safe).
+hipError_t launch_zero_words(uint64_t* p, size_t n, hipStream_t s);
 // *fits = false (nothing launched) when the grid cannot be resident at once
 // or the shape is outside the kernel's limits; the caller then uses the
 // per-layer launches.  launch = false only answers *fits.

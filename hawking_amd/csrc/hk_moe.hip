@@ -154,7 +154,8 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeDims d, MoeLayerDev
     if (routed && wave == tw) {
         const bool pub = lead && slot == 0;
         const ArgBest mine = softmax_topk_wave<NPL>(ws.logits, d.E, d.K, 1, pub ? ws.ids : nullptr,
-                                                    pub ? ws.weights : nullptr, pub ? ws.status : nullptr, &tk);
+                                                    pub ? ws.weights : nullptr, pub ? ws.status : nullptr, &tk,
+                                                    lane, d.tie_eps);
         if (pub && (uint32_t)lane < d.K) {
             if (ids_out) ids_out[lane] = mine.i;
             if (w_out) w_out[lane] = mine.v;
@@ -284,10 +285,12 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDims d, MoeLayerDev L
     const OrganView o0 = L.table[routed ? 2u : d.E * 3u + 2u];
     const int32_t idr = __builtin_amdgcn_readfirstlane(ids[min(slot, d.K - 1u)]);  // no branch before the load
     // HDR_WS (mixed, per-layer launches): the slot's step headers as the
-    // gate/up kernel copied them, loaded with the route instead of after it
+    // gate/up kernel copied them (tile T's at T * steps of the slot's own
+    // down organ: the routed and shared intermediates may differ in steps),
+    // loaded with the route instead of after it
     uint4 hws[D];
     if constexpr (HDR_WS) {
-        const uint32_t ns = n_steps_for(HK_MIXED, d.Imax);
+        const uint32_t ns = n_steps_for(HK_MIXED, routed ? d.I : d.SI);
 #pragma unroll
         for (int k = 0; k < D; ++k)
             hws[k] = ldg(ws.dn_hdr + (size_t)slot * moe_dn_hdr_stride(d.H, d.Imax) + T * ns + min((uint32_t)k, ns - 1u));

@@ -45,6 +45,7 @@ constexpr int M15_D = 4;            // steps in flight per wave
 struct M15Dims {
     uint32_t H, I, SI, E, K, rank;
     float eps;
+    float tie_eps;  // router tie window (route_tie_epsilon); 0 = strict '>'
 };
 
 // What differs between one routed expert's gate/up and another's (32 bytes):
@@ -342,7 +343,8 @@ __global__ void __launch_bounds__(256) m15_gate_up_kernel(M15Dims d, M15Dev L, M
     if (wave == 0) {
         const bool pub = T == 0 && slot == 0;
         const ArgBest mine = softmax_topk_wave<NPL>(ws.logits, d.E, d.K, 1, pub ? ws.ids : nullptr,
-                                                    pub ? ws.w : nullptr, pub ? ws.status : nullptr, &tk);
+                                                    pub ? ws.w : nullptr, pub ? ws.status : nullptr, &tk,
+                                                    lane, d.tie_eps);
         if (pub && (uint32_t)lane < d.K) {
             if (ids_out) ids_out[lane] = mine.i;
             if (w_out) w_out[lane] = mine.v;
@@ -598,6 +600,8 @@ extern "C" int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* s, h
     if (!H || !I || !E || !K || K > E || K > M15_MAX_K || E > 512)
         return set_error(ctx, HK_E_UNSUPPORTED,
                          "mixed-1p5 layer: need 0 < top_k <= min(n_experts, 16), n_experts <= 512");
+    if (!(s->route_tie_eps >= 0.0f) || !std::isfinite(s->route_tie_eps))
+        return set_error(ctx, HK_E_INVALID_ARG, "mixed-1p5 layer: route_tie_eps must be finite and >= 0");
     if (!(s->eps >= 0.0f) || !std::isfinite(s->eps)) return set_error(ctx, HK_E_INVALID_ARG, "mixed-1p5 layer: bad eps");
     const OrganView& rv = s->router->view;
     if (rv.rows != E || rv.cols != H || rv.kind != HK_Q8)
@@ -653,7 +657,7 @@ extern "C" int hk_moe15_layer_create(hk_ctx* ctx, const hk_moe15_layer_src* s, h
     if (g_soff < 0 || u_soff < 0 || rec_off < 0 || g_soff > 0xFFFFFFFF || u_soff > 0xFFFFFFFF || rec_off > 0xFFFFFFFF)
         return set_error(ctx, HK_E_UNSUPPORTED, "mixed-1p5 layer: unexpected organ layout");
     std::unique_ptr<hk_moe15_layer> L(new hk_moe15_layer());
-    L->d = M15Dims{H, I, SI, E, K, rank, s->eps};
+    L->d = M15Dims{H, I, SI, E, K, rank, s->eps, s->route_tie_eps};
     // dynamic LDS of the four kernels (each within 64 KB)
     const uint32_t Sb = n_steps_for(HK_BIN, H), Sq = n_steps_for(HK_Q8, H), Sr = n_steps_for(HK_U3, I),
                    Sl = n_steps_for(HK_U3, rank), Ss = SI ? n_steps_for(HK_Q8, SI) : 0u;

@@ -367,7 +367,8 @@ __device__ void gate_up_role(const StackArgs& a, uint32_t gi, uint8_t* lds) {
         if (routed && wave == 0) {
             const uint32_t stl = wait_logits<NPL>(a, l, tid, lg, false);
             if (stl != WAIT_OK && lane == 0) atomicMax(&state, stl);
-            const ArgBest mine = softmax_topk_wave<NPL>(lg, d.E, d.K, 1, nullptr, nullptr, nullptr, &tk, (int)lane);
+            const ArgBest mine = softmax_topk_wave<NPL>(lg, d.E, d.K, 1, nullptr, nullptr, nullptr, &tk, (int)lane,
+                                                        d.tie_eps);
             if (lane == slot) sel_id = mine.i;
         }
         __syncthreads();
@@ -461,7 +462,8 @@ __device__ void down_role(const StackArgs& a, uint32_t T, uint8_t* lds) {
             const uint32_t stl = wait_logits<NPL>(a, l, tid, lg, L.gate_w != nullptr);
             if (stl != WAIT_OK && lane == 0) atomicMax(&state, stl);
             const ArgBest mine = softmax_topk_wave<NPL>(lg, d.E, d.K, 1, nullptr, nullptr,
-                                                        T == 0 && stl == WAIT_OK ? a.status : nullptr, &tk, (int)lane);
+                                                        T == 0 && stl == WAIT_OK ? a.status : nullptr, &tk, (int)lane,
+                                                        d.tie_eps);
             if (lane < d.K) {
                 sel_i[lane] = mine.i;
                 sel_w[lane] = mine.v;
@@ -636,6 +638,18 @@ hipError_t launch_stack_k(const StackArgs& a, int cu_count, hipStream_t s, bool*
 }
 
 }  // namespace
+
+// Zero n 64-bit words with a kernel (not a memset node: a caller may capture
+// the decode in a graph, and memset nodes have replayed wrongly here).
+__global__ void zero_words_kernel(uint64_t* __restrict__ p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0ull;
+}
+
+hipError_t launch_zero_words(uint64_t* p, size_t n, hipStream_t s) {
+    const size_t blocks = std::min<size_t>((n + 255) / 256, 2048);
+    if (blocks) hipLaunchKernelGGL(zero_words_kernel, dim3((uint32_t)blocks), dim3(256), 0, s, p, n);
+    return hipGetLastError();
+}
 
 size_t moe_stack_lds_bytes(int kind, const MoeDims& d) {
     return kind == HK_Q4 ? stack_lds<HK_Q4>(d) : stack_lds<HK_MIXED>(d);

@@ -195,6 +195,64 @@ __device__ __forceinline__ uint32_t wave_incl_sum_u32(uint32_t v) {
     return v;
 }
 
+// Wave-wide minimum of unsigned words on the DPP network; every lane gets it.
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    v = min(v, (uint32_t)dpp_i32<DPP_ROW_SHR1, 0xF>(-1, (int)v));
+    v = min(v, (uint32_t)dpp_i32<DPP_ROW_SHR2, 0xF>(-1, (int)v));
+    v = min(v, (uint32_t)dpp_i32<DPP_ROW_SHR4, 0xF>(-1, (int)v));
+    v = min(v, (uint32_t)dpp_i32<DPP_ROW_SHR8, 0xF>(-1, (int)v));
+    v = min(v, (uint32_t)dpp_i32<DPP_ROW_BCAST15, 0xA>(-1, (int)v));
+    v = min(v, (uint32_t)dpp_i32<DPP_ROW_BCAST31, 0xC>(-1, (int)v));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// The tie-window selection of source_qwen80_topk_router
+// (model/qwen80_complete_runtime.rs:5988-6000 with route_tie_epsilon,
+// moe.rs:8-14) for one wave: lane l holds q[l + 64 j] (the normalised
+// probabilities, -inf past n).  The reference scans left to right and a later
+// q replaces the best only when it is above it and not within eps of it (a
+// later index never has the lower index, so its "tied and lower index" branch
+// cannot fire); the result is the last of a chain of replacements, which the
+// wave follows one link per reduction: the next link is the lowest index past
+// the current best that would replace it.  Returns, in lane r < k, the r-th
+// selection (id -1, weight 0 if nothing is selectable).  q is consumed.
+template <int NPL>
+__device__ __forceinline__ ArgBest tie_eps_select_wave(float (&q)[NPL], uint32_t n, uint32_t k, float eps, int lane) {
+    ArgBest mine{0.0f, -1};
+    for (uint32_t r = 0; r < k; ++r) {
+        float bv = -INFINITY;
+        uint32_t bi = 0;
+        bool any = false;
+        for (;;) {
+            uint32_t cand = 0xFFFFFFFFu;
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) {
+                const uint32_t i = (uint32_t)lane + 64u * (uint32_t)j;
+                const float v = q[j];
+                const bool tied = isfinite(bv) && isfinite(v) && fabsf(v - bv) <= eps;
+                if (i < n && (!any || i > bi) && v > bv && !tied) cand = min(cand, i);
+            }
+            cand = wave_min_u32(cand);
+            if (cand == 0xFFFFFFFFu) break;
+            float v = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) v = (cand >> 6) == (uint32_t)j ? q[j] : v;
+            bv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), (int)(cand & 63u)));
+            bi = cand;
+            any = true;
+        }
+        if ((uint32_t)lane == r) {
+            mine.i = any ? (int)bi : -1;
+            mine.v = any ? bv : 0.0f;
+        }
+        if (any && (bi & 63u) == (uint32_t)lane) {
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) q[j] = (bi >> 6) == (uint32_t)j ? -INFINITY : q[j];
+        }
+    }
+    return mine;
+}
+
 // LDS a wave's top-k selection works in (HK_TOPK_MAX candidates and slots).
 struct TopkLds {
     uint64_t cand[64];
@@ -217,10 +275,13 @@ struct TopkLds {
 // With more than 64 candidates (flat distributions) it falls back to k
 // rounds of a wave-wide key max.  Returns, in lane r < k, the r-th selection
 // (id, weight); ids_out / w_out (if not null) get all k.
+//
+// tie_eps > 0 selects with the reference's tie window instead
+// (tie_eps_select_wave); renormalisation and outputs are the same.
 template <int NPL>
 __device__ __forceinline__ ArgBest softmax_topk_wave(const float* __restrict__ logits, uint32_t n, uint32_t k, int renorm,
                                      int32_t* ids_out, float* w_out, uint32_t* status, TopkLds* t,
-                                     int lane = (int)(threadIdx.x & 63)) {
+                                     int lane = (int)(threadIdx.x & 63), float tie_eps = 0.0f) {
     float p[NPL];
     float m = -INFINITY;
     uint32_t bad = 0;
@@ -247,76 +308,83 @@ __device__ __forceinline__ ArgBest softmax_topk_wave(const float* __restrict__ l
     }
     const float sum = wave_sum(local);
     const float inv = 1.0f / sum;
-    const uint32_t kk = min(k, 64u);
-    uint32_t tau = 0;
-#pragma unroll
-    for (int b = 30; b >= 15; --b) {
-        const uint32_t c = tau | (1u << b);
-        if ((uint32_t)__popcll(__ballot(bv >= c)) >= kk) tau = c;
-    }
-    const float tf = __builtin_bit_cast(float, tau) * (1.0f - 0x1p-20f);
-    uint32_t cnt = 0;
-#pragma unroll
-    for (int j = 0; j < NPL; ++j) cnt += ((uint32_t)lane + 64u * j < n && p[j] >= tf) ? 1u : 0u;
-    const uint32_t incl = wave_incl_sum_u32(cnt);
-    const uint32_t C = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
     ArgBest mine{0.0f, -1};
-    if (C <= 64u) {
-        // slots no candidate fills (fewer than k candidates: a NaN logit never
-        // passes p >= tf) stay id -1, weight 0; the status bit is already set
-        if ((uint32_t)lane < k) {
-            t->sel_i[lane] = -1;
-            t->sel_v[lane] = 0.0f;
-        }
-        uint32_t o = incl - cnt;
+    if (tie_eps > 0.0f) {
 #pragma unroll
         for (int j = 0; j < NPL; ++j)
-            if ((uint32_t)lane + 64u * j < n && p[j] >= tf)
-                t->cand[o++] = ((uint64_t)__builtin_bit_cast(uint32_t, p[j]) << 32) | (uint64_t)((uint32_t)lane + 64u * j);
-        __builtin_amdgcn_wave_barrier();
-        uint64_t me = 0;
-        if ((uint32_t)lane < C) {
-            const uint64_t c = t->cand[lane];
-            const float pv = __builtin_bit_cast(float, (uint32_t)(c >> 32));
-            const float q = renorm ? pv / sum : pv * inv;
-            me = ((uint64_t)(__builtin_bit_cast(uint32_t, q) + 1u) << 32) | (uint64_t)(~(uint32_t)c);
-        }
-        __builtin_amdgcn_wave_barrier();
-        if ((uint32_t)lane < C) t->cand[lane] = me;
-        __builtin_amdgcn_wave_barrier();
-        uint32_t rank = 0;
-        for (uint32_t u = 0; u < C; ++u) rank += t->cand[u] > me ? 1u : 0u;
-        if ((uint32_t)lane < C && rank < k) {
-            t->sel_i[rank] = (int32_t)~(uint32_t)me;
-            t->sel_v[rank] = __builtin_bit_cast(float, (uint32_t)(me >> 32) - 1u);
-        }
-        __builtin_amdgcn_wave_barrier();
-        if ((uint32_t)lane < k) {
-            mine.i = t->sel_i[lane];
-            mine.v = t->sel_v[lane];
-        }
+            p[j] = (uint32_t)lane + 64u * j < n ? (renorm ? p[j] / sum : p[j] * inv) : -INFINITY;
+        mine = tie_eps_select_wave<NPL>(p, n, k, tie_eps, lane);
     } else {
-        uint64_t key[NPL];
-        uint64_t best = 0;
+        const uint32_t kk = min(k, 64u);
+        uint32_t tau = 0;
 #pragma unroll
-        for (int j = 0; j < NPL; ++j) {
-            const uint32_t i = (uint32_t)lane + 64u * j;
-            key[j] = i < n ? prob_key(renorm ? p[j] / sum : p[j] * inv, i) : 0ull;
-            best = umax64(best, key[j]);
+        for (int b = 30; b >= 15; --b) {
+            const uint32_t c = tau | (1u << b);
+            if ((uint32_t)__popcll(__ballot(bv >= c)) >= kk) tau = c;
         }
-        for (uint32_t r = 0; r < k; ++r) {
-            const uint64_t w = wave_max_key(best);
-            const uint32_t wi = ~(uint32_t)w;
-            if ((uint32_t)lane == r) {
-                mine.i = w ? (int)wi : -1;
-                mine.v = __builtin_bit_cast(float, (uint32_t)(w >> 32) - 1u);
-            }
-            if (w && (wi & 63u) == (uint32_t)lane) {
-                best = 0;
+        const float tf = __builtin_bit_cast(float, tau) * (1.0f - 0x1p-20f);
+        uint32_t cnt = 0;
 #pragma unroll
-                for (int j = 0; j < NPL; ++j) {
-                    key[j] = key[j] == w ? 0ull : key[j];
-                    best = umax64(best, key[j]);
+        for (int j = 0; j < NPL; ++j) cnt += ((uint32_t)lane + 64u * j < n && p[j] >= tf) ? 1u : 0u;
+        const uint32_t incl = wave_incl_sum_u32(cnt);
+        const uint32_t C = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+        if (C <= 64u) {
+            // slots no candidate fills (fewer than k candidates: a NaN logit never
+            // passes p >= tf) stay id -1, weight 0; the status bit is already set
+            if ((uint32_t)lane < k) {
+                t->sel_i[lane] = -1;
+                t->sel_v[lane] = 0.0f;
+            }
+            uint32_t o = incl - cnt;
+#pragma unroll
+            for (int j = 0; j < NPL; ++j)
+                if ((uint32_t)lane + 64u * j < n && p[j] >= tf)
+                    t->cand[o++] = ((uint64_t)__builtin_bit_cast(uint32_t, p[j]) << 32) | (uint64_t)((uint32_t)lane + 64u * j);
+            __builtin_amdgcn_wave_barrier();
+            uint64_t me = 0;
+            if ((uint32_t)lane < C) {
+                const uint64_t c = t->cand[lane];
+                const float pv = __builtin_bit_cast(float, (uint32_t)(c >> 32));
+                const float q = renorm ? pv / sum : pv * inv;
+                me = ((uint64_t)(__builtin_bit_cast(uint32_t, q) + 1u) << 32) | (uint64_t)(~(uint32_t)c);
+            }
+            __builtin_amdgcn_wave_barrier();
+            if ((uint32_t)lane < C) t->cand[lane] = me;
+            __builtin_amdgcn_wave_barrier();
+            uint32_t rank = 0;
+            for (uint32_t u = 0; u < C; ++u) rank += t->cand[u] > me ? 1u : 0u;
+            if ((uint32_t)lane < C && rank < k) {
+                t->sel_i[rank] = (int32_t)~(uint32_t)me;
+                t->sel_v[rank] = __builtin_bit_cast(float, (uint32_t)(me >> 32) - 1u);
+            }
+            __builtin_amdgcn_wave_barrier();
+            if ((uint32_t)lane < k) {
+                mine.i = t->sel_i[lane];
+                mine.v = t->sel_v[lane];
+            }
+        } else {
+            uint64_t key[NPL];
+            uint64_t best = 0;
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) {
+                const uint32_t i = (uint32_t)lane + 64u * j;
+                key[j] = i < n ? prob_key(renorm ? p[j] / sum : p[j] * inv, i) : 0ull;
+                best = umax64(best, key[j]);
+            }
+            for (uint32_t r = 0; r < k; ++r) {
+                const uint64_t w = wave_max_key(best);
+                const uint32_t wi = ~(uint32_t)w;
+                if ((uint32_t)lane == r) {
+                    mine.i = w ? (int)wi : -1;
+                    mine.v = __builtin_bit_cast(float, (uint32_t)(w >> 32) - 1u);
+                }
+                if (w && (wi & 63u) == (uint32_t)lane) {
+                    best = 0;
+#pragma unroll
+                    for (int j = 0; j < NPL; ++j) {
+                        key[j] = key[j] == w ? 0ull : key[j];
+                        best = umax64(best, key[j]);
+                    }
                 }
             }
         }

@@ -84,6 +84,8 @@ class MoeShape:
     topk_group: int = 1
     norm_topk_prob: bool = True
     routed_scaling_factor: float = 1.0
+    route_tie_eps: float = 0.0  # softmax router tie window (route_tie_epsilon, moe.rs:8-14); 0 = strict
+    stack_launch: int = 0       # HK_STACK_PER_LAYER (0) or HK_STACK_PERSISTENT (1)
 
     @classmethod
     def deepseek_v3(cls, n_layers=1, n_group=1, topk_group=1, **kw):
@@ -105,7 +107,7 @@ class MoeModel:
         cfg = MoeConfig(shape.n_layers, shape.hidden, shape.inter, shape.shared_inter, shape.n_experts,
                         shape.top_k, shape.expert_kind, shape.expert_group, int(shape.shared_gate), shape.eps,
                         shape.router, shape.n_group, shape.topk_group, int(shape.norm_topk_prob),
-                        shape.routed_scaling_factor)
+                        shape.routed_scaling_factor, shape.route_tie_eps, shape.stack_launch)
         h = C.c_void_p()
         ctx.call("hk_moe_model_create", C.byref(cfg), C.byref(h))
         self.h = h
@@ -184,6 +186,11 @@ class MoeModel:
                       _pp(ids), _pp(weights),
                       stream if stream is not None else self.ctx.stream)
 
+    def set_stack_launch(self, mode: int) -> None:
+        """HK_STACK_PER_LAYER (0) or HK_STACK_PERSISTENT (1) for decode_stack (hk_moe_model_set_stack_launch)."""
+        self.ctx.call("hk_moe_model_set_stack_launch", self.h, int(mode))
+        self.shape.stack_launch = int(mode)
+
     def stack_is_persistent(self) -> bool:
         """Whether decode_stack runs as one persistent launch here (hk_moe_decode_stack_persistent)."""
         v = C.c_int(0)
@@ -261,7 +268,7 @@ class Mixed15Layer:
     to the organs; they must outlive it."""
 
     def __init__(self, ctx: Context, norm_w, router, experts, top_k: int, shared=None, shared_gate=None,
-                 eps: float = 1e-6):
+                 eps: float = 1e-6, route_tie_eps: float = 0.0):
         from ._lib import Moe15LayerSrc
         self.ctx = ctx
         self.h = None
@@ -280,7 +287,8 @@ class Mixed15Layer:
         self._tab = tab
         sh = shared if shared is not None else (None, None, None)
         src = Moe15LayerSrc(hidden=self.hidden, inter=self.inter, shared_inter=self.shared_inter, n_experts=E,
-                            top_k=top_k, eps=eps, norm_w=self._norm.ctypes.data, router=router.h,
+                            top_k=top_k, eps=eps, route_tie_eps=route_tie_eps, norm_w=self._norm.ctypes.data,
+                            router=router.h,
                             shared_gate=shared_gate.h if shared_gate is not None else None,
                             shared_gate_proj=sh[0].h if sh[0] is not None else None,
                             shared_up=sh[1].h if sh[1] is not None else None,
@@ -322,3 +330,96 @@ def mixed15_decode_stack(ctx: Context, layers: list[Mixed15Layer], h_in, h_out, 
     arr = (C.c_void_p * len(layers))(*[l.h.value for l in layers])
     ctx.call("hk_moe15_decode_stack", arr, len(layers), _pp(h_in), _pp(h_out), _pp(ids), _pp(weights),
              stream if stream is not None else ctx.stream)
+
+
+# ---------------------------------------------------------------- synthetic mixed-1p5-v1 model
+# The reference's measured artifact is a Qwen3-Next-80B-A3B pack whose experts
+# mix three codecs per tensor (q80_mixed_decode.rs:7-21,
+# qwen80_mixed_catalog.rs:30-33): gate HGRAVB01, up HGRAVR02 (2 % Rice
+# residual), down HGRAVS01 (rank-160 3-bit factors); router, shared-expert
+# gate and shared expert HGRAVU01 q8.  The synthetic stand-in draws every
+# tensor from the counter-based generator on the device (no checkpoint is
+# available), so the oracle can regenerate any one of them.
+MIXED15_GATE, MIXED15_UP, MIXED15_DOWN_LEFT, MIXED15_DOWN_RIGHT = 0, 1, 2, 3
+MIXED15_ROUTER, MIXED15_SHARED_GATE, MIXED15_SHARED_GATE_PROJ, MIXED15_SHARED_UP, MIXED15_SHARED_DOWN = 16, 17, 18, 19, 20
+MIXED15_NORM = 21
+
+
+@dataclass
+class Mixed15Dims:
+    hidden: int = 2048
+    inter: int = 512
+    shared_inter: int = 512
+    n_experts: int = 512
+    top_k: int = 10
+    rank: int = 160
+    eps: float = 1e-6
+
+
+def mixed15_stream_id(layer: int, expert: int, proj: int) -> int:
+    """Generator stream of one tensor of the synthetic mixed-1p5 model; expert
+    n_experts holds the router, the shared gate and the shared expert."""
+    return (0xC15 << 40) | (layer << 24) | (expert << 8) | proj
+
+
+def mixed15_tensor(d: Mixed15Dims, expert: int, proj: int):
+    """(kind, rows, cols, group, sigma) of one synthetic tensor."""
+    from ._lib import HK_BIN, HK_BIN_RICE, HK_Q8, HK_U3
+    H, I, SI, E, r = d.hidden, d.inter, d.shared_inter, d.n_experts, d.rank
+    table = {
+        MIXED15_GATE: (HK_BIN, I, H, 128, 0.02),
+        MIXED15_UP: (HK_BIN_RICE, I, H, 128, 0.02),
+        MIXED15_DOWN_LEFT: (HK_U3, H, r, 64, 0.05),
+        MIXED15_DOWN_RIGHT: (HK_U3, r, I, 64, 0.02),
+        MIXED15_ROUTER: (HK_Q8, E, H, 64, 0.02),
+        MIXED15_SHARED_GATE: (HK_Q8, 1, H, 64, 0.02),
+        MIXED15_SHARED_GATE_PROJ: (HK_Q8, SI, H, 64, 0.02),
+        MIXED15_SHARED_UP: (HK_Q8, SI, H, 64, 0.02),
+        MIXED15_SHARED_DOWN: (HK_Q8, H, SI, 64, 0.02),
+    }
+    return table[proj]
+
+
+def synthetic_mixed15_layers(ctx: Context, seed: int, n_layers: int, d: Mixed15Dims = Mixed15Dims(),
+                             route_tie_eps: float = 0.0):
+    """n_layers synthetic mixed-1p5 layers generated and packed on the device.
+    Returns (layers, expert_bytes[l][e] = packed bytes of expert e's four
+    organs, dense_bytes[l] = router + shared gate + shared expert + norm)."""
+    from .organs import SyntheticOrgan, stream_key
+    layers, expert_bytes, dense_bytes = [], [], []
+    E = d.n_experts
+    nbuf = ctx.empty(d.hidden)
+    for l in range(n_layers):
+        def syn(e, p):
+            kind, rows, cols, group, sigma = mixed15_tensor(d, e, p)
+            return SyntheticOrgan(ctx, kind, rows, cols, stream_key(seed, mixed15_stream_id(l, e, p)), 0,
+                                  group=group, sigma=sigma)
+        experts = [(syn(e, MIXED15_GATE), syn(e, MIXED15_UP), (syn(e, MIXED15_DOWN_LEFT), syn(e, MIXED15_DOWN_RIGHT)))
+                   for e in range(E)]
+        router = syn(E, MIXED15_ROUTER)
+        sgate = shared = None
+        if d.shared_inter:
+            sgate = syn(E, MIXED15_SHARED_GATE)
+            shared = (syn(E, MIXED15_SHARED_GATE_PROJ), syn(E, MIXED15_SHARED_UP), syn(E, MIXED15_SHARED_DOWN))
+        ctx.call("hk_synth_normal", stream_key(seed, mixed15_stream_id(l, E, MIXED15_NORM)), 0, d.hidden, 0.02,
+                 nbuf.ptr, ctx.stream)
+        nw = nbuf.download()
+        layers.append(Mixed15Layer(ctx, nw, router, experts, d.top_k, shared=shared, shared_gate=sgate, eps=d.eps,
+                                   route_tie_eps=route_tie_eps))
+        expert_bytes.append([t[0].packed_bytes + t[1].packed_bytes + t[2][0].packed_bytes + t[2][1].packed_bytes
+                             for t in experts])
+        dense_bytes.append(router.packed_bytes + d.hidden * 4 +
+                           ((sgate.packed_bytes + sum(o.packed_bytes for o in shared)) if shared else 0))
+    return layers, expert_bytes, dense_bytes
+
+
+def mixed15_forward_token(ctx: Context, layers: list[Mixed15Layer], h: np.ndarray):
+    """All layers for one token on numpy input through hk_moe15_decode_stack:
+    returns (out, ids[n_layers, k], weights[n_layers, k])."""
+    H, K, n = layers[0].hidden, layers[0].top_k, len(layers)
+    hd = ctx.to_device(np.ascontiguousarray(h, np.float32))
+    out = ctx.empty(H)
+    ids = ctx.empty(n * K, np.int32)
+    w = ctx.empty(n * K, np.float32)
+    mixed15_decode_stack(ctx, layers, hd, out, ids, w)
+    return out.download(), ids.download().reshape(n, K), w.download().reshape(n, K)

@@ -96,6 +96,16 @@ int hk_event_elapsed_ms(hk_ctx* ctx, void* start, void* stop, float* ms);
  * checks, which cannot be returned from stream-ordered launches. */
 int hk_check_device_status(hk_ctx* ctx, hk_stream stream, uint32_t* bits);
 
+/* Achievable-bandwidth control, run beside the packed GEMVs to measure what
+ * HBM delivers with the same timing (the reference's q80_geo_stream_control,
+ * shaders/q80_matvec_geometry_gen.metal:80-107, which its matvec geometry
+ * sweep runs beside the organs): reads the nbytes of device memory at data
+ * (16-byte aligned, nbytes a multiple of 16) once with 16-byte loads, each
+ * of `workgroups` workgroups one contiguous slice, and writes the float sum
+ * of each slice's words to out[workgroups] (device).  Stream-ordered. */
+int hk_stream_control(hk_ctx* ctx, const void* data, size_t nbytes, float* out, uint32_t workgroups,
+                      hk_stream stream);
+
 /* ------------------------------------------------------------------ organs */
 
 /* One packed matrix in the reference's canonical byte layout (HOST memory).
@@ -436,7 +446,17 @@ typedef struct hk_moe_config {
     uint32_t topk_group;     /* noaux_tc: groups kept */
     int32_t norm_topk_prob;  /* noaux_tc: renormalise the selected scores (+1e-20) */
     float routed_scaling_factor; /* noaux_tc: factor on the routed weights */
+    float route_tie_eps;     /* softmax router: the HAWKING_DS_ROUTE_TIE_EPS window (route_tie_epsilon,
+                                moe.rs:8-14): a later probability replaces the best only when it is above
+                                it by more than this; 0 = strict '>' with the lowest index on exact ties */
+    int32_t stack_launch;    /* hk_moe_decode_stack: HK_STACK_PER_LAYER or HK_STACK_PERSISTENT */
 } hk_moe_config;
+
+/* How hk_moe_decode_stack runs a token (hk_moe_config.stack_launch). */
+#define HK_STACK_PER_LAYER 0  /* three stream-ordered launches per layer */
+#define HK_STACK_PERSISTENT 1 /* one persistent cooperative launch for every layer (the reference's one command
+                                 buffer per token, qwen80_mixed_hybrid_decode.rs:1962-2078) when its grid can
+                                 be resident at once, else the per-layer launches; the same bits either way */
 
 /* Host-side canonical weights of one layer (HOST pointers).
  * experts: n_experts*3 organ sources (gate, up, down per expert). */
@@ -486,18 +506,23 @@ int hk_moe_decode_layer(hk_ctx* ctx, hk_moe_model* model, uint32_t layer, const 
 /* All layers for one token: h_{l+1} = moe_layer_l(h_l) (forward_token's MoE
  * suffixes, model/qwen80_mixed_hybrid_decode.rs:4682-4736, without the
  * attention mixers).  ids/weights may be NULL or [n_layers*top_k].  Runs as
- * three launches per layer, or, with environment HK_MOE_PERSISTENT=1, as one
- * persistent cooperative launch (the reference's one command buffer per
- * token) when the model's grid fits the device at once (hidden <= 2048,
- * n_experts <= 512, intermediate <= 2048, top_k + shared <= 12); both give
- * the same bits.  A hand-off the persistent launch waited for too long sets
- * device status bit 4 (the output is then undefined). */
+ * three launches per layer (stack_launch = HK_STACK_PER_LAYER), or, with
+ * HK_STACK_PERSISTENT, as one persistent cooperative launch (the reference's
+ * one command buffer per token) when the model's grid fits the device at once
+ * (hidden <= 2048, n_experts <= 512, intermediate <= 2048, top_k + shared <=
+ * 12); both give the same bits.  A hand-off the persistent launch waited for
+ * too long sets device status bit 4: h_out, ids and weights of that call are
+ * then undefined (the next call, with a new tag, is unaffected). */
 int hk_moe_decode_stack(hk_ctx* ctx, hk_moe_model* model, const float* h_in, float* h_out,
                         int32_t* ids, float* weights, hk_stream stream);
 /* *persistent = 1 when hk_moe_decode_stack on this model runs as one
- * persistent launch (enabled and admitted), 0 when it uses per-layer launches.  Diagnostic with no
+ * persistent launch (selected and admitted), 0 when it uses per-layer launches.  Diagnostic with no
  * counterpart in the reference (its token is one command buffer). */
 int hk_moe_decode_stack_persistent(hk_ctx* ctx, hk_moe_model* model, int* persistent);
+/* Changes the model's hk_moe_config.stack_launch after creation (HK_STACK_PER_LAYER or
+ * HK_STACK_PERSISTENT); no reference counterpart.  Not to be called while a token of the
+ * model is in flight on another stream. */
+int hk_moe_model_set_stack_launch(hk_ctx* ctx, hk_moe_model* model, int32_t stack_launch);
 
 /* BackendMoe::moe_block (backend/mod.rs:509-521) on one layer of a model:
  * the routed (and optional shared) expert block for CALLER-supplied routes,
@@ -553,6 +578,7 @@ typedef struct hk_moe15_layer hk_moe15_layer;
 typedef struct hk_moe15_layer_src {
     uint32_t hidden, inter, shared_inter, n_experts, top_k;
     float eps;
+    float route_tie_eps;   /* as hk_moe_config.route_tie_eps (0 = strict '>') */
     const float* norm_w;
     const hk_organ* router;
     const hk_organ* shared_gate;

@@ -1175,7 +1175,7 @@ int hko_moe_layer_forward(const hko_moe_layer* L, const float* h, float* out, in
     if (L->shared && (rc = hko_mlp(&L->shared[0], &L->shared[1], &L->shared[2], xn, NULL, shared)) != HKO_OK)
         goto done;
     hko_gemv_f32(L->router_w, E, H, xn, logits);
-    if ((rc = hko_router_softmax_topk(logits, E, K, 0.0f, ids, wts)) != HKO_OK) goto done;
+    if ((rc = hko_router_softmax_topk(logits, E, K, L->tie_eps, ids, wts)) != HKO_OK) goto done;
     for (size_t r = 0; r < K; ++r) {
         const hko_organ* ex = L->experts + (size_t)ids[r] * 3;
         if ((rc = hko_mlp(&ex[0], &ex[1], &ex[2], xn, NULL, eout)) != HKO_OK) goto done;

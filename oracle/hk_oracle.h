@@ -208,6 +208,7 @@ typedef struct hko_moe_layer {
     const float* shared_gate_w; /* [hidden] or NULL (no sigmoid gate: weight 1) */
     const hko_organ* experts;   /* [n_experts * 3]: gate, up, down per expert */
     const hko_organ* shared;    /* [3] or NULL */
+    float tie_eps;              /* router tie window (route_tie_epsilon, src/moe.rs:8-14); 0 = strict */
 } hko_moe_layer;
 /* Full moe_suffix: out = h + sum_r w_r*mlp_r(xn) (route order) + g*shared(xn).
  * ids/weights/xn may be NULL. */

@@ -16,7 +16,9 @@ from dataclasses import dataclass
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "build", "libhk_oracle.so")
+# HKO_ORACLE_LIB selects another build of the same sources (the sanitizer
+# build that tests/test_sanitize.py runs the oracle tests against)
+LIB_PATH = os.environ.get("HKO_ORACLE_LIB") or os.path.join(_HERE, "build", "libhk_oracle.so")
 
 HKO_OK = 0
 
@@ -630,6 +632,7 @@ class _MoeLayer(C.Structure):
     _fields_ = [
         ("hidden", _sz), ("inter", _sz), ("n_experts", _sz), ("top_k", _sz), ("eps", C.c_float),
         ("norm_w", _p), ("router_w", _p), ("shared_gate_w", _p), ("experts", _p), ("shared", _p),
+        ("tie_eps", C.c_float),
     ]
 
 
@@ -639,7 +642,7 @@ class MoeLayer:
     (the oracle touches only the routed ids)."""
 
     def __init__(self, hidden, inter, n_experts, top_k, norm_w, router_w, experts,
-                 shared=None, shared_gate_w=None, eps=1e-6):
+                 shared=None, shared_gate_w=None, eps=1e-6, tie_eps=0.0):
         self.norm_w = np.ascontiguousarray(norm_w, np.float32)
         self.router_w = np.ascontiguousarray(router_w, np.float32)
         self.shared_gate_w = None if shared_gate_w is None else np.ascontiguousarray(shared_gate_w, np.float32)
@@ -658,7 +661,7 @@ class MoeLayer:
         self._sh = sh
         self.c = _MoeLayer(hidden, inter, n_experts, top_k, eps, _ptr(self.norm_w),
                            _ptr(self.router_w), _ptr(self.shared_gate_w),
-                           C.cast(arr, _p), C.cast(sh, _p) if sh is not None else None)
+                           C.cast(arr, _p), C.cast(sh, _p) if sh is not None else None, tie_eps)
         self.hidden, self.n_experts, self.top_k = hidden, n_experts, top_k
 
     def forward(self, h):

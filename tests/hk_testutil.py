@@ -62,7 +62,7 @@ def oracle_layer(oracle, seed, shape, layer, h):
     norm, router, gate = dense(oracle, seed, shape, layer)
     xn = oracle.rmsnorm_1p(h, norm, shape.eps)
     logits = oracle.gemv_f32(router, xn)
-    ids, _ = oracle.router_softmax_topk(logits, shape.top_k)
+    ids, _ = oracle.router_softmax_topk(logits, shape.top_k, getattr(shape, "route_tie_eps", 0.0))
     experts = [None] * shape.n_experts
     for e in ids.tolist():
         experts[e] = tuple(oracle_organ(oracle, seed, shape, layer, e, p) for p in range(3))
@@ -71,7 +71,7 @@ def oracle_layer(oracle, seed, shape, layer, h):
         shared = tuple(oracle_organ(oracle, seed, shape, layer, shape.n_experts, p) for p in range(3))
     L = oracle.MoeLayer(shape.hidden, shape.inter, shape.n_experts, shape.top_k, norm, router, experts,
                         shared=shared, shared_gate_w=gate if (shape.shared_gate and shape.shared_inter) else None,
-                        eps=shape.eps)
+                        eps=shape.eps, tie_eps=getattr(shape, "route_tie_eps", 0.0))
     out, ids2, w, xn2, logits2 = L.forward(h)
     assert np.array_equal(ids, ids2)
     return L, out, ids2, w, logits2
@@ -86,7 +86,7 @@ def oracle_layer_cached(oracle, seed, shape, layer, h, cache, pool=None):
     cache[("dense", layer)] = (norm, router, gate)
     xn = oracle.rmsnorm_1p(h, norm, shape.eps)
     logits = oracle.gemv_f32(router, xn)
-    ids, _ = oracle.router_softmax_topk(logits, shape.top_k)
+    ids, _ = oracle.router_softmax_topk(logits, shape.top_k, getattr(shape, "route_tie_eps", 0.0))
     want = [int(e) for e in ids] + ([shape.n_experts] if shape.shared_inter else [])
     todo = [(e, p) for e in want if (layer, e) not in cache for p in range(3)]
     make = lambda ep: oracle_organ(oracle, seed, shape, layer, ep[0], ep[1])
@@ -99,10 +99,24 @@ def oracle_layer_cached(oracle, seed, shape, layer, h, cache, pool=None):
     shared = cache[(layer, shape.n_experts)] if shape.shared_inter else None
     L = oracle.MoeLayer(shape.hidden, shape.inter, shape.n_experts, shape.top_k, norm, router, experts,
                         shared=shared, shared_gate_w=gate if (shape.shared_gate and shape.shared_inter) else None,
-                        eps=shape.eps)
+                        eps=shape.eps, tie_eps=getattr(shape, "route_tie_eps", 0.0))
     out, ids2, w, xn2, logits2 = L.forward(h)
     assert np.array_equal(ids, ids2)
     return L, out, ids2, w, logits2, xn2
+
+
+def tie_window_margin_ok(logits: np.ndarray, eps: float, margin: float = 1e-8) -> bool:
+    """Margin rule for the tie-window router: the selection depends only on
+    whether q_i - q_j exceeds eps for pairs of normalised probabilities
+    (q = softmax(logits), from the oracle's f32 logits), so every pairwise
+    difference must stay at least `margin` away from eps; the device's
+    logits differ from the oracle's by about 1e-7 relative, which moves a q
+    by far less than that."""
+    l = logits.astype(np.float64)
+    q = np.exp(l - l.max())
+    q /= q.sum()
+    d = q[:, None] - q[None, :]
+    return float(np.min(np.abs(d - eps))) >= margin
 
 
 def router_margin_ok(logits: np.ndarray, k: int, rel: float = 1e-4) -> bool:
@@ -174,3 +188,81 @@ def oracle_noaux(oracle, seed, shape, layer, x):
     out, ids2, w, logits2 = M.forward(x)
     assert np.array_equal(ids, ids2)
     return M, out, ids2, w, logits2
+
+
+# ---------------------------------------------------------------- synthetic mixed-1p5-v1 model
+def mixed15_weights(oracle, seed, d, layer, expert, proj):
+    """The draws of one tensor of hawking_amd.moe.synthetic_mixed15_layers
+    (the device's generator stream, regenerated by the oracle)."""
+    from hawking_amd.moe import mixed15_stream_id, mixed15_tensor
+    kind, rows, cols, group, sigma = mixed15_tensor(d, expert, proj)
+    key = oracle.stream_key(seed, mixed15_stream_id(layer, expert, proj))
+    return kind, oracle.normal(key, rows * cols, sigma).reshape(rows, cols)
+
+
+def mixed15_oracle_expert(oracle, seed, d, layer, expert):
+    """Routed expert `expert` of a synthetic mixed-1p5 layer as oracle organs:
+    (HGRAVB01 gate, HGRAVR02 up at the 2 % ratio, HGRAVS01 down)."""
+    from hawking_amd.moe import MIXED15_DOWN_LEFT, MIXED15_DOWN_RIGHT, MIXED15_GATE, MIXED15_UP
+    _, gw = mixed15_weights(oracle, seed, d, layer, expert, MIXED15_GATE)
+    _, uw = mixed15_weights(oracle, seed, d, layer, expert, MIXED15_UP)
+    _, lw = mixed15_weights(oracle, seed, d, layer, expert, MIXED15_DOWN_LEFT)
+    _, rw = mixed15_weights(oracle, seed, d, layer, expert, MIXED15_DOWN_RIGHT)
+    return oracle.Organ.binary(gw), oracle.Organ.rice_q1(uw, 0.02), oracle.Organ.low_rank(lw, rw)
+
+
+def mixed15_oracle_dense(oracle, seed, d, layer):
+    """(norm weight, decoded q8 router, decoded q8 shared gate row or None,
+    shared expert organs or None) of a synthetic mixed-1p5 layer.  The q8
+    router and shared gate reach the oracle as their decoded weights, which
+    is uniform_factor_matvec_f32's arithmetic."""
+    from hawking_amd.moe import (MIXED15_NORM, MIXED15_ROUTER, MIXED15_SHARED_DOWN, MIXED15_SHARED_GATE,
+                                 MIXED15_SHARED_GATE_PROJ, MIXED15_SHARED_UP, mixed15_stream_id)
+    H, E = d.hidden, d.n_experts
+    norm = oracle.normal(oracle.stream_key(seed, mixed15_stream_id(layer, E, MIXED15_NORM)), H, 0.02)
+    _, w = mixed15_weights(oracle, seed, d, layer, E, MIXED15_ROUTER)
+    ro = oracle.Organ.uniform8(w)
+    router = oracle.uniform_decode(ro.scales, ro.codes, E, H, 8, 64).reshape(E, H)
+    if not d.shared_inter:
+        return norm, router, None, None
+    _, w = mixed15_weights(oracle, seed, d, layer, E, MIXED15_SHARED_GATE)
+    so = oracle.Organ.uniform8(w)
+    sgate = oracle.uniform_decode(so.scales, so.codes, 1, H, 8, 64).reshape(H)
+    shared = tuple(oracle.Organ.uniform8(mixed15_weights(oracle, seed, d, layer, E, p)[1])
+                   for p in (MIXED15_SHARED_GATE_PROJ, MIXED15_SHARED_UP, MIXED15_SHARED_DOWN))
+    return norm, router, sgate, shared
+
+
+def mixed15_oracle_layer_cached(oracle, seed, d, layer, h, cache, pool=None, tie_eps=0.0):
+    """The oracle's moe_suffix of a synthetic mixed-1p5 layer on h, generating
+    only the routed experts (kept in `cache`, generated on `pool`).
+    Returns (layer_obj, out, ids, weights, logits)."""
+    if ("dense", layer) not in cache:
+        cache[("dense", layer)] = mixed15_oracle_dense(oracle, seed, d, layer)
+    norm, router, sgate, shared = cache[("dense", layer)]
+    logits = oracle.gemv_f32(router, oracle.rmsnorm_1p(h, norm, d.eps))
+    ids, _ = oracle.router_softmax_topk(logits, d.top_k, tie_eps)
+    todo = [int(e) for e in ids if (layer, int(e)) not in cache]
+    make = lambda e: mixed15_oracle_expert(oracle, seed, d, layer, e)
+    made = list(pool.map(make, todo)) if pool is not None else [make(e) for e in todo]
+    for e, t in zip(todo, made):
+        cache[(layer, e)] = t
+    experts = [None] * d.n_experts
+    for e in ids.tolist():
+        experts[e] = cache[(layer, e)]
+    L = oracle.MoeLayer(d.hidden, d.inter, d.n_experts, d.top_k, norm, router, experts, shared=shared,
+                        shared_gate_w=sgate, eps=d.eps, tie_eps=tie_eps)
+    out, ids2, w, _, logits2 = L.forward(h)
+    assert np.array_equal(ids, ids2)
+    return L, out, ids2, w, logits2
+
+
+def router_weights_f64(L, h, ids, eps=1e-6):
+    """The routed weights in FP64 (RMSNorm(1+w), the layer's router, softmax,
+    renormalised over the selection): the numeric authority for the weights."""
+    h64 = np.asarray(h, np.float64)
+    xn = h64 / np.sqrt(np.dot(h64, h64) / h64.size + eps) * (1.0 + L.norm_w.astype(np.float64))
+    lg = L.router_w.astype(np.float64) @ xn
+    p = np.exp(lg - lg.max())
+    sel = p[np.asarray(ids)] / p.sum()
+    return sel / sel.sum()

@@ -13,7 +13,12 @@ experts of each layer):
   * hk_moe_decode_stack's ids, weights and final state equal the 48
     chained single-layer calls bit for bit;
   * the final state within 2e-5 rel-L2 of the oracle's own 48-layer f32
-    chain and of the FP64 chain (same routes).
+    chain and of the FP64 chain (same routes);
+  * the persistent launch (stack_launch = HK_STACK_PERSISTENT, one
+    cooperative launch for the 48 layers) on the same token: every layer's
+    ids equal the oracle chain's, its weights within 1e-6 of the oracle's,
+    the final state within 2e-5 of the f32 and FP64 chains, and all of it
+    bit-identical to the per-layer launches.
 Router margin rule: the oracle's f64-sorted logits must keep the 10th/11th
 gap >= 1e-4 max|logit| at every layer; otherwise the input's seed advances
 (0xC4, 0xC5, ...) and the walk restarts.
@@ -94,11 +99,30 @@ def test_config4_48_layer_stack_layer_by_layer(ctx, oracle):
 
         fut64 = pool.submit(chain64)
         r = h0
+        chain_ids, chain_w = [], []
         for layer in range(N_LAYERS):
-            _, r, r_ids, _, _, _ = U.oracle_layer_cached(oracle, U.SEED, shape, layer, r, cache, pool)
+            _, r, r_ids, r_w, _, _ = U.oracle_layer_cached(oracle, U.SEED, shape, layer, r, cache, pool)
             assert r_ids.tolist() == sids[layer].tolist(), f"oracle chain route differs at layer {layer}"
+            chain_ids.append(r_ids.tolist())
+            chain_w.append(r_w)
         r64 = fut64.result()
     say("final state vs f32 chain / FP64 chain")
     assert oracle.relative_l2(out, r) < TOL
     assert oracle.relative_l2(out, r64) < TOL
     assert ctx.device_status() == 0
+
+    say("persistent launch of the same token vs the oracle chain")
+    m.set_stack_launch(1)
+    try:
+        assert m.stack_is_persistent(), "config 4 must be admitted as one persistent launch"
+        pout, pids, pw = m.forward_token(h0)
+    finally:
+        m.set_stack_launch(0)
+    assert ctx.device_status() == 0
+    for layer in range(N_LAYERS):
+        assert pids[layer].tolist() == chain_ids[layer], f"persistent route differs at layer {layer}"
+        assert np.max(np.abs(pw[layer] - chain_w[layer])) <= 1e-6, f"persistent weights at layer {layer}"
+    assert oracle.relative_l2(pout, r) < TOL
+    assert oracle.relative_l2(pout, r64) < TOL
+    assert np.array_equal(pids, sids) and np.array_equal(pw.view(np.uint32), sw.view(np.uint32))
+    assert np.array_equal(pout.view(np.uint32), out.view(np.uint32)), "persistent != per-layer launches"

@@ -243,6 +243,10 @@ VARIANTS = [
     ("q4-g128-no-shared", U.HK_Q4, 128, 256, 0, False),
     ("mixed-shared-no-gate", U.HK_MIXED, 128, 256, 256, False),
     ("mixed-inter384-narrow-shared", U.HK_MIXED, 128, 384, 128, True),
+    # routed and shared down organs with different numbers of 512-column steps
+    # (the down kernel reads each slot's copied step headers at its own stride)
+    ("mixed-inter512-shared1024", U.HK_MIXED, 128, 512, 1024, True),
+    ("mixed-inter1024-shared512", U.HK_MIXED, 128, 1024, 512, True),
 ]
 
 

@@ -1,9 +1,9 @@
 """The persistent decode (hk_moe_decode_stack as one cooperative launch with
-flag-tagged hand-offs, HK_MOE_PERSISTENT=1) against the per-layer launches: the same bits, layer
-ids and weights, over repeated calls (the tags advance), and the same status
-bits for a non-finite hidden state.  The per-layer path itself is checked
-against the oracle in test_gpu_moe.py / test_gpu_c4_stack.py."""
-import os
+flag-tagged hand-offs, stack_launch = HK_STACK_PERSISTENT) against the
+per-layer launches: the same bits, layer ids and weights, over repeated calls
+(the tags advance), and the same status bits for a non-finite hidden state.
+Both paths are checked against the oracle at config 4's full 48 layers in
+test_gpu_c4_stack.py."""
 import sys
 
 import numpy as np
@@ -35,21 +35,21 @@ SHAPES = [
 
 
 def run_mode(m, hd, persistent):
-    """One token with the persistent launch (HK_MOE_PERSISTENT=1) or the
-    per-layer launches (the default)."""
-    os.environ["HK_MOE_PERSISTENT"] = "1" if persistent else "0"
+    """One token with the persistent launch (HK_STACK_PERSISTENT) or the
+    per-layer launches (HK_STACK_PER_LAYER, the default)."""
+    m.set_stack_launch(1 if persistent else 0)
     try:
         return m.forward_token(hd)
     finally:
-        del os.environ["HK_MOE_PERSISTENT"]
+        m.set_stack_launch(0)
 
 
 def admitted(m):
-    os.environ["HK_MOE_PERSISTENT"] = "1"
+    m.set_stack_launch(1)
     try:
         return m.stack_is_persistent()
     finally:
-        del os.environ["HK_MOE_PERSISTENT"]
+        m.set_stack_launch(0)
 
 
 @pytest.mark.parametrize("label,n,H,I,SI,E,K,kind,group,gate", SHAPES)

@@ -67,6 +67,32 @@ def test_topk_desc_ties_lower_index_and_neg_inf(oracle):
     assert oracle.topk_desc(v, 7).tolist() == [1, 2, 5, 4, 0, 3, 6]
 
 
+def test_router_tie_window_known_answer(oracle):
+    """route_tie_epsilon (src/moe.rs:8-14) in source_qwen80_topk_router
+    (qwen80_complete_runtime.rs:5988-6000), derived by hand: probabilities
+    q = [a, a, .20, a, a, .205, a, .22, a, .215] (a = .16 / 6) and eps = .01.
+    Scanning left to right, a later q replaces the best only when it is above
+    it by more than eps:
+      route 0: 0 -> 2 (.20 - a > eps) -> 5 is within eps of .20 (kept 2)
+               -> 7 (.22 - .20 > eps); 9 is below .22           => 7
+      route 1: 0 -> 2 -> 9 (.215 - .20 = .015 > eps)              => 9
+      route 2: 0 -> 2; 5 (.005 above 2) is within eps            => 2
+      route 3: 0 -> 5 (the a's tie each other)                    => 5
+    The strict rule (eps = 0) orders by value instead: 7, 9, 5, 2."""
+    a = 0.16 / 6
+    q = np.array([a, a, 0.20, a, a, 0.205, a, 0.22, a, 0.215])
+    logits = np.log(q).astype(np.float32)
+    ids, w = oracle.router_softmax_topk(logits, 4, 0.01)
+    assert ids.tolist() == [7, 9, 2, 5]
+    sel = q[[7, 9, 2, 5]] / q[[7, 9, 2, 5]].sum()
+    assert np.max(np.abs(w - sel)) < 1e-6
+    ids0, _ = oracle.router_softmax_topk(logits, 4, 0.0)
+    assert ids0.tolist() == [7, 9, 5, 2]
+    # a window narrower than every gap is the strict rule
+    ids1, _ = oracle.router_softmax_topk(logits, 4, 1e-4)
+    assert ids1.tolist() == [7, 9, 5, 2]
+
+
 def test_router_weights_vs_f64_softmax(oracle):
     rng = np.random.default_rng(3)
     logits = (rng.standard_normal(512) * 0.5).astype(np.float32)
