@@ -171,24 +171,10 @@ def moe15_bench(ctx, steps, warmup, n_layers=48, H=2048, I=512, SI=512, E=512, K
     token: the canonical packed bytes of every organ the routes touch, the
     norm weights and the hidden state in and out."""
     from hawking_amd import organs
-    from hawking_amd.moe import Mixed15Layer, mixed15_decode_stack
+    from hawking_amd.moe import Mixed15Dims, mixed15_decode_stack, synthetic_mixed15_layers
     t0 = time.time()
-    layers, expert_bytes, dense_bytes = [], [], []
-    for l in range(n_layers):
-        def syn(kind, rows, cols, e, p, group, sigma=0.02):
-            sid = (0xC15 << 40) | (l << 24) | (e << 8) | p
-            return organs.SyntheticOrgan(ctx, kind, rows, cols, organs.stream_key(SEED, sid), 0, group=group,
-                                         sigma=sigma)
-        experts = [(syn(HK_BIN, I, H, e, 0, 128), syn(HK_BIN_RICE, I, H, e, 1, 128),
-                    (syn(HK_U3, H, rank, e, 2, 64, 0.05), syn(HK_U3, rank, I, e, 3, 64))) for e in range(E)]
-        router = syn(HK_Q8, E, H, E, 16, 64)
-        sgate = syn(HK_Q8, 1, H, E, 17, 64)
-        shared = (syn(HK_Q8, SI, H, E, 18, 64), syn(HK_Q8, SI, H, E, 19, 64), syn(HK_Q8, H, SI, E, 20, 64))
-        nw = np.random.default_rng(l).normal(0.0, 0.02, H).astype(np.float32)
-        layers.append(Mixed15Layer(ctx, nw, router, experts, K, shared=shared, shared_gate=sgate))
-        expert_bytes.append([t[0].packed_bytes + t[1].packed_bytes + t[2][0].packed_bytes + t[2][1].packed_bytes
-                             for t in experts])
-        dense_bytes.append(router.packed_bytes + sgate.packed_bytes + sum(o.packed_bytes for o in shared) + H * 4)
+    layers, expert_bytes, dense_bytes = synthetic_mixed15_layers(ctx, SEED, n_layers,
+                                                                 Mixed15Dims(H, I, SI, E, K, rank))
     ctx.synchronize()
     gen_s = time.time() - t0
     hs = ctx.empty((n_inputs, H))
@@ -213,6 +199,24 @@ def moe15_bench(ctx, steps, warmup, n_layers=48, H=2048, I=512, SI=512, E=512, K
             "gbps": round(tok_bytes / (ms * 1e-3) / 1e9, 1), "tokens_per_s": round(1e3 / ms, 1),
             "launches_per_layer": 4, "layers": n_layers, "device_status": status,
             "distinct_routes": int(np.unique(routes.reshape(-1, K), axis=0).shape[0]), "gen_seconds": round(gen_s, 2)}
+
+
+def stream_control(ctx, steps, warmup, nbytes=4 << 30, workgroup_counts=(1024, 2048, 4096, 8192)):
+    """The achievable-bandwidth control (hk_stream_control): one read of a
+    4 GiB buffer (16 x the MALL) per launch with 16-byte loads, at several
+    workgroup counts; the best is this box's read ceiling under the same
+    timing as the organ GEMVs."""
+    buf = ctx.empty(nbytes, np.uint8)
+    ctx.call("hk_memset", buf.ptr, 0x3C, nbytes, ctx.stream)
+    out = ctx.empty(max(workgroup_counts))
+    rates = {}
+    for wg in workgroup_counts:
+        ms = time_launches(ctx, lambda: ctx.call("hk_stream_control", buf.ptr, nbytes, out.ptr, wg, ctx.stream),
+                           steps, warmup)
+        rates[wg] = nbytes / (ms * 1e-3) / 1e9
+    best = max(rates, key=rates.get)
+    return {"gbps": round(rates[best], 1), "frac_hbm": round(rates[best] / HBM_PEAK_GBPS, 4), "workgroups": best,
+            "bytes": nbytes, "gbps_by_workgroups": {str(k): round(v, 1) for k, v in rates.items()}}
 
 
 def single_organ_us(ctx, steps=200):
@@ -575,6 +579,7 @@ def main():
     workloads = {name: (lambda n=name: streamed_extra(n)) for name in
                  ("binary_2048x512", "q4g32_512x2048", "mixed_512x2048", "q8g64_512x2048", "binary_rice_512x2048")}
     workloads.update({
+        "stream_control_read_4gib": lambda: stream_control(ctx, args.steps, args.warmup),
         "hgravs01_r160_2048x768": lambda: lowrank_streamed(ctx, args.steps, args.warmup),
         "terminal_head_q8_151936x2048": lambda: terminal_head_bench(ctx, tok_steps, args.warmup),
         "single_organ_binary_512x2048_us": lambda: round(single_organ_us(ctx), 2),
@@ -616,6 +621,10 @@ def main():
         for name, fn in list(workloads.items()) + ([] if args.no_moe else list(moe_workloads.items())):
             extra[name] = fn()
             log(name, extra[name])
+        ctrl = extra["stream_control_read_4gib"]["gbps"]
+        extra["frac_of_stream_control"] = {name: round(r["gbps"] / ctrl, 4) for name, r in
+                                           [(main_name, {"gbps": head["gbps"]})] + list(extra.items())
+                                           if isinstance(r, dict) and "gbps" in r and name != "stream_control_read_4gib"}
     cpu = None if (args.no_cpu or args.only_main) else cpu_baseline()
     if cpu:
         log("cpu", cpu)

@@ -20,7 +20,7 @@ from tests import hk_testutil as U
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-5
-HK_Q4, HK_BIN, HK_MIXED, HK_Q8 = U.HK_Q4, U.HK_BIN, U.HK_MIXED, 4
+HK_Q4, HK_BIN, HK_MIXED, HK_Q8, HK_U3, HK_BIN_RICE = U.HK_Q4, U.HK_BIN, U.HK_MIXED, 4, 5, 6
 
 
 def say(*a):
@@ -116,6 +116,19 @@ def _oracle_decode(oracle, kind, group, rows, cols, key, coin_key):
     if kind == HK_Q8:
         s, c = oracle.uniform_pack(w, rows, cols, 8, 64)
         return oracle.uniform_decode(s, c, rows, cols, 8, 64), s.nbytes + c.nbytes
+    if kind == HK_U3:
+        s, c = oracle.uniform_pack(w, rows, cols, 3, 64)
+        return oracle.uniform_decode(s, c, rows, cols, 3, 64), s.nbytes + c.nbytes
+    if kind == HK_BIN_RICE:
+        # base + (+-scale) at each outlier, in f32 (hk_decode_rows of an HGRAVR02 organ)
+        p = oracle.rice_q1_pack(w, rows, cols, 0.02)
+        d = oracle.bin_decode(p.bin_scales, p.bin_signs, rows, cols).reshape(-1).copy()
+        sc = oracle.f16_to_f32(p.res_scale)
+        bits = np.unpackbits(p.res_signs, bitorder="little")[:p.count]
+        np.add.at(d, p.indices.astype(np.int64), np.where(bits == 1, sc, -sc).astype(np.float32))
+        # canonical HGRAVR02 body: base, first_index (u32), Rice stream, f16 scale, sign bits
+        nbytes = p.bin_scales.nbytes + p.bin_signs.nbytes + 4 + p.rice.nbytes + 2 + p.res_signs.nbytes
+        return d, nbytes
     m = oracle.mixed_pack(w, oracle.mixed_coins(coin_key, rows * cols // 128))
     return oracle.mixed_decode(m), m.nbytes()
 
@@ -130,6 +143,10 @@ SYNTH = [
     ("mixed 2048x512", HK_MIXED, 128, 2048, 512),
     ("mixed ragged", HK_MIXED, 128, 33, 1152),
     ("q8 512x2048", HK_Q8, 64, 512, 2048),
+    # the mixed-1p5 model's HGRAVR02 up and HGRAVS01 factors (2 % outliers; flat 3-bit groups)
+    ("rice 512x2048", HK_BIN_RICE, 128, 512, 2048),
+    ("u3 2048x160", HK_U3, 64, 2048, 160),
+    ("u3 160x512", HK_U3, 64, 160, 512),
 ]
 
 
