@@ -618,10 +618,16 @@ __device__ __forceinline__ void fetch_mixed(const OrganView& o, const uint4& h, 
     f.V[r][5] = vb.y;
     f.V[r][6] = vb.z;
     f.V[r][7] = vb.w;
-    const uint8_t* sb = reinterpret_cast<const uint8_t*>(o.scales + soff);
-    const uint32_t sl = 2u * ((uint32_t)lane + below);
-    f.s0[r] = ldg(reinterpret_cast<const uint16_t*>(sb + sl));
-    f.s1[r] = ldg(reinterpret_cast<const uint16_t*>(sb + (sl + (isq2 ? 2u : 0u))));
+    // one aligned 4-byte load per lane: a Q2 lane's pair, or the word that
+    // holds a binary lane's scale (the step's Q2 pairs come first); a small
+    // load costs the memory pipeline as much as a 16-byte one, so two u16
+    // loads cost twice
+    const uint32_t nq2 = (uint32_t)__builtin_popcountll(mask), j = (uint32_t)lane - below;
+    const uint32_t* sw = reinterpret_cast<const uint32_t*>(o.scales + soff);
+    const uint32_t w = ldg(sw + (isq2 ? below : nq2 + (j >> 1)));
+    const uint16_t lo = (uint16_t)w, hi = (uint16_t)(w >> 16);
+    f.s0[r] = (isq2 || !(j & 1u)) ? lo : hi;
+    f.s1[r] = isq2 ? hi : f.s0[r];
     f.q2m[r] = mask;
 }
 

@@ -39,7 +39,8 @@ size_t tiled_bytes(int kind, int group, uint32_t rows, uint32_t cols, uint32_t n
     case HK_MIXED: {
         const size_t items = nt * S * 64, pad = items - (size_t)n_bin - n_q2;
         data = ((size_t)n_bin + pad) * 16 + (size_t)n_q2 * 32;
-        scales = ((size_t)n_bin + pad + 2 * (size_t)n_q2) * 2 + 16;
+        // each step's scales padded to whole 4-byte words (at most one u16 per step)
+        scales = ((size_t)n_bin + pad + 2 * (size_t)n_q2 + nt * S) * 2 + 16;
         hdr = nt * S * 16;
         packed = (n / 128 + 7) / 8 + (size_t)n_bin * 18 + (size_t)n_q2 * 36;
         break;
@@ -76,7 +77,7 @@ OrganView tiled_place(int kind, int group, uint32_t rows, uint32_t cols, uint32_
     } else if (kind == HK_MIXED) {
         const size_t items = nt * S * 64, pad = items - (size_t)n_bin - n_q2;
         data = ((size_t)n_bin + pad) * 16 + (size_t)n_q2 * 32;
-        scales = ((size_t)n_bin + pad + 2 * (size_t)n_q2) * 2 + 16;
+        scales = ((size_t)n_bin + pad + 2 * (size_t)n_q2 + nt * S) * 2 + 16;
         hdr = nt * S * 16;
     }
     uint8_t* p = base;
@@ -198,16 +199,17 @@ __device__ void repack_mixed_mask_body(const CanonView& src, const OrganView& ds
     }
 }
 
-// Pass 2 (one thread per organ): exclusive prefix of Q2 counts -> data /
-// scale offsets.
+// Pass 2 (one thread per organ): exclusive prefix of Q2 counts -> data
+// offsets; scale offsets advance by 64 + nq2 u16s rounded up to even.
 __device__ void repack_mixed_offsets_body(const OrganView& dst, const uint32_t* counts) {
     const uint32_t nb = dst.n_tiles * dst.steps;
-    uint32_t q2 = 0;
+    uint32_t q2 = 0, so = 0;
     for (uint32_t b = 0; b < nb; ++b) {
         uint4* h = const_cast<uint4*>(dst.hdr) + b;
         h->z = 16u * (64u * b + q2);
-        h->w = 64u * b + q2;
+        h->w = so;
         q2 += counts[b];
+        so += (64u + counts[b] + 1u) & ~1u;
     }
 }
 
@@ -221,11 +223,12 @@ __device__ void repack_mixed_items_body(const CanonView& src, const OrganView& d
         const uint32_t T = b / dst.steps, t = b % dst.steps, r = T * 16u + (l & 15u), g = 4u * t + (l >> 4);
         const uint4 h = dst.hdr[b];
         const uint64_t mask = (uint64_t)h.x | ((uint64_t)h.y << 32);
-        const uint32_t below = __popcll(mask & ((1ull << l) - 1ull));
+        const uint32_t below = __popcll(mask & ((1ull << l) - 1ull)), nq2 = __popcll(mask);
         uint8_t* item = const_cast<uint8_t*>(dst.data) + h.z + 16u * (l + below);
-        uint16_t* sc = const_cast<uint16_t*>(dst.scales) + h.w + l + below;
         bool valid;
         const bool q2 = canon_is_q2(src, r, g, &valid);
+        // Q2 pairs first, then the binary (and padding) lanes' scales
+        uint16_t* sc = const_cast<uint16_t*>(dst.scales) + h.w + (q2 ? 2u * below : 2u * nq2 + l - below);
         if (!valid) {
             *reinterpret_cast<uint4*>(item) = make_uint4(0, 0, 0, 0);
             sc[0] = 0;

@@ -18,8 +18,13 @@
 //         binary (16 B of signs, one f16 scale) or Q2 (32 B of 2-bit codes,
 //         two f16 scales for columns 0-63 and 64-127).  Per (tile, step) a
 //         16-byte header {q2mask.lo, q2mask.hi, data_off, scale_off}: item l
-//         starts at data_off + 16*(l + popcount(q2mask below l)) bytes and its
-//         scales at scale_off + (l + popcount(q2mask below l)) u16s.
+//         starts at data_off + 16*(l + popcount(q2mask below l)) bytes.  The
+//         step's scales start at u16 scale_off (even): first the Q2 items'
+//         pairs in lane order (Q2 lane l's pair at scale_off + 2 q, q =
+//         popcount(q2mask below l)), then one scale per binary lane (lane l at
+//         scale_off + 2 nq2 + l - q, nq2 = popcount(q2mask)), padded to whole
+//         4-byte words, so every lane reads its scales with one aligned 4-byte
+//         load (a binary lane takes the half of the word that holds its own).
 //         Q2 code order inside an item (so one shift pattern decodes both
 //         kinds): dword a (0..3) byte j holds, in 2-bit fields u = 0..3, the
 //         codes of columns 32a + 8j + 2u; dword 4+a byte j holds columns
@@ -102,10 +107,11 @@ __device__ inline float tiled_weight(const OrganView& o, uint32_t r, uint32_t c)
     }
     const uint4 h = o.hdr[(size_t)T * o.steps + t];
     const uint64_t mask = (uint64_t)h.x | ((uint64_t)h.y << 32);
-    const uint32_t below = __popcll(mask & ((1ull << l) - 1ull));
+    const uint32_t below = __popcll(mask & ((1ull << l) - 1ull)), nq2 = __popcll(mask);
     const uint8_t* item = o.data + h.z + 16u * (l + below);
-    const uint16_t* sc = o.scales + h.w + l + below;
-    if (!((mask >> l) & 1ull)) {
+    const bool q2 = (mask >> l) & 1ull;
+    const uint16_t* sc = o.scales + h.w + (q2 ? 2u * below : 2u * nq2 + l - below);
+    if (!q2) {
         const float s = f16_bits_to_f32(sc[0]);
         return ((item[i >> 3] >> (i & 7u)) & 1u) ? s : -s;
     }

@@ -122,6 +122,7 @@ def _check(ctx, oracle, layer, ref, h, K):
     (2048, 512, 512, 64, 10, 160),  # the artifact's Qwen3-Next shapes (r160 down), 64 experts
     (1024, 256, 256, 48, 16, 64),   # the largest top_k (one wave per slot in the down-left block)
     (512, 224, 128, 37, 6, 64),     # n_experts not a multiple of 4 (padded tile-start rows), a partial router tile
+    (512, 128, 128, 512, 10, 32),   # the largest n_experts the layer admits (the artifact's 512)
 ])
 def test_mixed15_layer_matches_oracle(ctx, oracle, H, I, SI, E, K, rank):
     say("mixed15 layer", H, I, SI, E, K, rank)

@@ -43,6 +43,57 @@ def ctx():
     return Context(0)
 
 
+def _oracle_dense_decode(oracle, o):
+    """Decoded weights of an oracle organ (rows x cols, f32)."""
+    if o.kind == 1:
+        return oracle.bin_decode(o.scales, o.codes, o.rows, o.cols)
+    if o.kind == 3:
+        return oracle.uniform_decode(o.scales, o.codes, o.rows, o.cols, 8, 64)
+    if o.kind == 5:
+        p = o.rice
+        d = oracle.bin_decode(p.bin_scales, p.bin_signs, p.rows, p.cols).reshape(-1).copy()
+        sc = oracle.f16_to_f32(p.res_scale)
+        bits = np.unpackbits(p.res_signs, bitorder="little")[:p.count]
+        np.add.at(d, p.indices.astype(np.int64), np.where(bits == 1, sc, -sc).astype(np.float32))
+        return d.reshape(p.rows, p.cols)
+    raise ValueError(o.kind)
+
+
+def _same_bits(got, want, what):
+    assert np.array_equal(np.asarray(got, np.float32).view(np.uint32),
+                          np.asarray(want, np.float32).reshape(np.shape(got)).view(np.uint32)), what
+
+
+def test_mixed15_synthetic_organs_decode_bit_exact(ctx, oracle):
+    """Every organ kind of the timed model, generated and packed on the device,
+    decodes bit for bit to the oracle's pack of the same draws: the router,
+    shared gate and shared expert (q8), and routed experts' HGRAVB01 gate,
+    HGRAVR02 up and HGRAVS01 factors (3-bit)."""
+    from hawking_amd.moe import Mixed15Dims, synthetic_mixed15_layers
+    d = Mixed15Dims(n_experts=16)
+    say("mixed-1p5 synthetic organs vs the oracle")
+    layers, _, _ = synthetic_mixed15_layers(ctx, U.SEED, 2, d)
+    for l in (0, 1):
+        router, experts, shared, sgate = layers[l]._keep
+        norm, router_dec, sgate_dec, oshared = U.mixed15_oracle_dense(oracle, U.SEED, d, l)
+        _same_bits(router.decode(), router_dec, f"router {l}")
+        _same_bits(sgate.decode().reshape(-1), sgate_dec, f"shared gate {l}")
+        for j in range(3):
+            _same_bits(shared[j].decode(), _oracle_dense_decode(oracle, oshared[j]), f"shared {j} {l}")
+        for e in (0, 7, 15):
+            og, ou, od = U.mixed15_oracle_expert(oracle, U.SEED, d, l, e)
+            g, u, (lf, rf) = experts[e]
+            _same_bits(g.decode(), _oracle_dense_decode(oracle, og), f"gate {l} {e}")
+            _same_bits(u.decode(), _oracle_dense_decode(oracle, ou), f"up {l} {e}")
+            _same_bits(lf.decode(), oracle.uniform_decode(od.scales, od.codes, d.hidden, d.rank, 3, 64),
+                       f"down left {l} {e}")
+            _same_bits(rf.decode(), oracle.uniform_decode(od.right[0], od.right[1], d.rank, d.inter, 3, 64),
+                       f"down right {l} {e}")
+        assert np.array_equal(layers[l]._norm, norm)
+    for layer in layers:
+        layer.free()
+
+
 def test_mixed15_token_512_experts_48_layers(ctx, oracle):
     from hawking_amd.moe import Mixed15Dims, mixed15_forward_token, synthetic_mixed15_layers
     d = Mixed15Dims()
