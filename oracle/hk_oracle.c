@@ -629,7 +629,9 @@ size_t hko_rice_q1_count(size_t n, double ratio) {
     return count;
 }
 
-static const float* g_sort_abs;
+/* qsort's comparator reads the magnitudes through this pointer; one per
+ * thread, so packs on several threads at once do not see each other's. */
+static _Thread_local const float* g_sort_abs;
 static int by_abs_desc_then_index(const void* a, const void* b) {
     uint32_t i = *(const uint32_t*)a, j = *(const uint32_t*)b;
     float x = g_sort_abs[i], y = g_sort_abs[j];

@@ -106,3 +106,17 @@ def test_reference_rice_cases(oracle):
     ref = dense.reshape(rows, cols) @ x.astype(np.float64)
     assert np.allclose(oracle.rice_q1_matvec_f64(p, x), ref, rtol=1e-12, atol=1e-12)
     assert np.linalg.norm(y - ref) / np.linalg.norm(ref) < 1e-6
+
+
+def test_rice_pack_is_thread_safe(oracle):
+    """Packs running on several threads at once (the GPU parity tests
+    generate experts on a thread pool) give the serial packs' bytes."""
+    import concurrent.futures as cf
+    ws = [oracle.normal(oracle.stream_key(0x7E5, i), 64 * 512, 0.02).reshape(64, 512) for i in range(16)]
+    serial = [oracle.rice_q1_pack(w, 64, 512, 0.02) for w in ws]
+    with cf.ThreadPoolExecutor(max_workers=8) as pool:
+        for _ in range(3):
+            par = list(pool.map(lambda w: oracle.rice_q1_pack(w, 64, 512, 0.02), ws))
+            for a, b in zip(serial, par):
+                assert np.array_equal(a.indices, b.indices) and np.array_equal(a.rice, b.rice)
+                assert np.array_equal(a.res_signs, b.res_signs) and a.res_scale == b.res_scale
