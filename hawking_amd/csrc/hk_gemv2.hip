@@ -564,7 +564,8 @@ static hipError_t launch_kind(const OrganView* organs, uint32_t n, const OrganVi
 // workgroup) by kind and size, from sweeps over the streamed workloads:
 // binary 4-tile groups over 16 tiles when the organ has >= 4 steps, else
 // 2-tile groups 5 deep over 32; Q4 and Q8 2 over 32; 3-bit factors 2 over 16,
-// or over 128 when narrow; mixed (large fragments) 1 over 32.
+// or over 128 when narrow; mixed (large fragments) 1 over 16 (1 over 32 and
+// 1 over 64 measured 1.3 % slower on 6,144 organs of 512 x 2048).
 // (build-time overrides for launch-shape sweeps)
 #ifndef HK_BIN_NARROW_R
 #define HK_BIN_NARROW_R 2
@@ -585,7 +586,7 @@ static hipError_t launch_kind(const OrganView* organs, uint32_t n, const OrganVi
 #ifndef HK_MIX_R
 #define HK_MIX_R 1
 #define HK_MIX_D 3
-#define HK_MIX_TPW 32
+#define HK_MIX_TPW 16
 #endif
 template <int KIND>
 static hipError_t launch_r(const OrganView* organs, uint32_t n, const OrganView& sh, const float* x, size_t xs,
