@@ -201,6 +201,22 @@ def moe15_bench(ctx, steps, warmup, n_layers=48, H=2048, I=512, SI=512, E=512, K
             "distinct_routes": int(np.unique(routes.reshape(-1, K), axis=0).shape[0]), "gen_seconds": round(gen_s, 2)}
 
 
+MALL_BYTES = 256 << 20  # MI355X Infinity Cache
+
+
+def token_cache_label(r):
+    """Whether a token's bytes can stay in the Infinity Cache between the
+    tokens that cycle over them: a layer's weights are read again only after
+    the whole token's other bytes went through."""
+    b = r["bytes_per_token"]
+    if b > MALL_BYTES:
+        r["cache"] = (f"MALL-cold ({b / 1e6:.0f} MB read per token, more than the 256 MB Infinity Cache, "
+                      f"before a layer's weights are read again)")
+    else:
+        r["cache"] = f"MALL-warm ({b / 1e6:.0f} MB read per token fits the 256 MB Infinity Cache)"
+    return r
+
+
 def stream_control(ctx, steps, warmup, nbytes=4 << 30, workgroup_counts=(1024, 2048, 4096, 8192)):
     """The achievable-bandwidth control (hk_stream_control): one read of a
     4 GiB buffer (16 x the MALL) per launch with 16-byte loads, at several
@@ -589,8 +605,9 @@ def main():
                                         cache="MALL-warm (one layer, 16 inputs: about 24 MB per token, "
                                               "all within the 256 MB Infinity Cache)"),
         "moe_layer_c3_q4_cold": lambda: moe_layer_cold_bench(ctx, tok_steps, args.warmup),
-        "moe_token_c4_mixed": lambda: rounded(moe_bench(ctx, c4, tok_steps, args.warmup)),
-        "moe15_token_c4_mixed_1p5_v1": lambda: moe15_bench(ctx, tok_steps, args.warmup, n_layers=args.moe_layers),
+        "moe_token_c4_mixed": lambda: token_cache_label(rounded(moe_bench(ctx, c4, tok_steps, args.warmup))),
+        "moe15_token_c4_mixed_1p5_v1": lambda: token_cache_label(
+            moe15_bench(ctx, tok_steps, args.warmup, n_layers=args.moe_layers)),
         "moe_batch_c5_dsv3": lambda: rounded(moe_batch_bench(ctx, max(args.steps, 10), args.warmup), 4),
     }
     if args.only:
