@@ -61,6 +61,9 @@ struct Layout {
 
 static int validate_shape(hk_ctx* ctx, int kind, int group, uint32_t rows, uint32_t cols) {
     if (rows == 0 || cols == 0) return set_error(ctx, HK_E_GEOMETRY, "organ rows and cols must be positive");
+    // the kernels address a tiled organ's sections with 32-bit offsets
+    if ((uint64_t)rows * cols > 0xC0000000ull)
+        return set_error(ctx, HK_E_GEOMETRY, "organ too large: rows * cols above 3 * 2^30 weights");
     switch (kind) {
     case HK_Q4:
         if (group != 32 && group != 64 && group != 128)

@@ -23,6 +23,36 @@ struct WaveItems {
     }
 };
 
+// A pipeline slot's walk over a wave's items: D items ahead at a time
+// without a division per item (D / steps and D % steps once), clamped at
+// the last item (past the end a slot re-reads it).  g = the slot's tile
+// group start, t = its step.
+template <int D>
+struct ItemStride {
+    uint32_t dq, dr, glast, tlast;
+    __device__ __forceinline__ void init(const WaveItems& W, uint32_t last) {
+        dq = (uint32_t)D / W.steps;
+        dr = (uint32_t)D % W.steps;
+        glast = W.g0 + (last / W.steps) * W.gstride;
+        tlast = last % W.steps;
+    }
+    // slot (g, t) from item nx - D to item nx (nx > last: the last item)
+    __device__ __forceinline__ void next(const WaveItems& W, uint32_t nx, uint32_t last, uint32_t* T, int R,
+                                         int* nvalid, uint32_t* t) const {
+        uint32_t g = T[0], s = *t + dr;
+        g += dq * W.gstride;
+        if (s >= W.steps) {
+            s -= W.steps;
+            g += W.gstride;
+        }
+        g = nx > last ? glast : g;
+        s = nx > last ? tlast : s;
+        *t = s;
+        for (int r = 0; r < R; ++r) T[r] = g + (uint32_t)r;
+        *nvalid = (int)min((uint32_t)R, W.t1 - g);
+    }
+};
+
 // Row totals of a finished group of R tiles into the workgroup's LDS row
 // buffer (unscaled; tiles r >= nvalid alias T[0] and are skipped).
 template <int R>
@@ -254,13 +284,15 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    ItemStride<D> adv;
+    adv.init(W, last);
     uint32_t it = 0;
     for (; it + D <= W.n; it += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             compute_step<KIND, R>(f[d], ts[d], A, SX, q, acc);
             if (ts[d] + 1 == o.steps) flush_group<R>(acc, T[d], nv[d], t0, lane, ysh);
-            W.at(min(it + D + d, last), T[d], R, &nv[d], &ts[d]);
+            adv.next(W, it + D + d, last, T[d], R, &nv[d], &ts[d]);
             if constexpr (KIND == HK_MIXED) {
                 // headers from LDS: the data loads wait for an LDS read, not
                 // for every load in flight before them
@@ -385,13 +417,15 @@ struct TileWalk {
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+        ItemStride<D> adv;
+        adv.init(W, last);
         uint32_t it = 0;
         for (; it + D <= W.n; it += D) {
 #pragma unroll
             for (int d = 0; d < D; ++d) {
                 compute_step<KIND, R>(f[d], ts[d], A, SX, q, acc);
                 if (ts[d] + 1 == o.steps) flush_group<R>(acc, T[d], nv[d], t0, lane, ysh);
-                W.at(min(it + D + d, last), T[d], R, &nv[d], &ts[d]);
+                adv.next(W, it + D + d, last, T[d], R, &nv[d], &ts[d]);
                 fetch_step<KIND, R>(o, T[d], nv[d], ts[d], lane, f[d]);
             }
         }
@@ -421,14 +455,26 @@ __host__ __device__ inline LowrankLds lowrank_lds(const OrganView& l, const Orga
     return L;
 }
 
+// (build-time overrides for launch-shape sweeps: tile groups and steps in
+// flight of the right and the left factor's walks)
+#ifndef HK_LR_RR
+#define HK_LR_RR 1
+#define HK_LR_RD 3
+#define HK_LR_LR 2
+#define HK_LR_LD 3
+#endif
+
 // HGRAVS01 pairs y_i = L_i (R_i x_i), one workgroup per pair: the right
 // factor's rows (mid, kept in LDS) and then the left factor's, whose first
 // weight steps are already in flight while mid is computed.  The arithmetic
 // is that of two gemv_tiled_kernel launches (mid rounded to f32, then its own
 // x image), so the result is the same bits.  mid_all (may be null) also
 // receives mid.
+#ifndef HK_LR_MINW
+#define HK_LR_MINW 1
+#endif
 template <int NC>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256, HK_LR_MINW)
 lowrank_kernel(const OrganView* __restrict__ lefts, const OrganView* __restrict__ rights, uint32_t n,
                const float* __restrict__ xall, size_t x_stride, float* __restrict__ mid_all, size_t mid_stride,
                float* __restrict__ yall, size_t y_stride, uint32_t* status) {
@@ -446,9 +492,9 @@ lowrank_kernel(const OrganView* __restrict__ lefts, const OrganView* __restrict_
 
     XChunks<NC> xc;
     load_x<NC>(BlockTeam{}, x, rv.cols, xc);
-    TileWalk<HK_U3, 1, 3> wr;
+    TileWalk<HK_U3, HK_LR_RR, HK_LR_RD> wr;
     wr.start(rv, 0, rv.n_tiles, wave, lane);
-    TileWalk<HK_U3, 2, 3> wl;
+    TileWalk<HK_U3, HK_LR_LR, HK_LR_LD> wl;
     wl.start(lv, 0, lv.n_tiles, wave, lane);
     // both x images with E = 0, scattered from each thread's chunks (the
     // two launches' images to the bit: the GEMV builds them the same way)

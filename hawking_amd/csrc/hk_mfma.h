@@ -636,23 +636,28 @@ __device__ __forceinline__ void fetch_mixed(const OrganView& o, const uint4& h, 
 template <int KIND, int R>
 __device__ __forceinline__ void fetch_one(const OrganView& o, uint32_t T, uint32_t t, int lane, Frag<KIND, R>& f,
                                           int r) {
+    // offsets in 32 bits (an organ's tiled sections are below 4 GiB, checked
+    // when it is created): a 64-bit product per address costs scalar
+    // instructions on every step
     if constexpr (KIND == HK_BIN || KIND == HK_Q4) {
-        f.v[r] = ldg(reinterpret_cast<const uint4*>(o.data + ((size_t)T * o.steps + t) * 1024u + 16u * lane));
-        f.s[r] = ldg(o.scales + ((size_t)T * o.steps + t) * 64u + lane);
+        const uint32_t st = T * o.steps + t;
+        f.v[r] = ldg(reinterpret_cast<const uint4*>(o.data + (st * 1024u + 16u * (uint32_t)lane)));
+        f.s[r] = ldg(o.scales + (st * 64u + (uint32_t)lane));
     } else if constexpr (KIND == HK_Q8) {
-        f.v[r] = ldg(reinterpret_cast<const uint4*>(o.data + ((size_t)T * o.steps + t) * 1024u + 16u * lane));
-        f.s[r] = ldg(o.scales + ((size_t)T * o.steps + t) * 16u + (lane & 15));
+        const uint32_t st = T * o.steps + t;
+        f.v[r] = ldg(reinterpret_cast<const uint4*>(o.data + (st * 1024u + 16u * (uint32_t)lane)));
+        f.s[r] = ldg(o.scales + (st * 16u + (uint32_t)(lane & 15)));
     } else if constexpr (KIND == HK_U3) {
         // the last step stores tail_q slots; lanes of absent slots re-read slot 0
         const bool tail = t + 1 == o.steps;
         const uint32_t nq = tail ? o.tail_q : 4u;
         const uint32_t l = (uint32_t)(lane >> 4) < nq ? (uint32_t)lane : (uint32_t)(lane & 15);
-        const uint8_t* base = o.data + (size_t)T * u3_tile_data(o.steps, o.tail_q) + 768u * t;
+        const uint8_t* base = o.data + (T * (uint32_t)u3_tile_data(o.steps, o.tail_q) + 768u * t);
         f.lo[r] = ldg(reinterpret_cast<const uint2*>(base + 8u * l));
         f.hi[r] = ldg(reinterpret_cast<const uint32_t*>(base + 128u * nq + 4u * l));
-        f.s[r] = ldg(o.scales + (size_t)T * u3_tile_scales(o.steps, o.tail_q) + 64u * t + l);
+        f.s[r] = ldg(o.scales + (T * (uint32_t)u3_tile_scales(o.steps, o.tail_q) + 64u * t + l));
     } else {
-        fetch_mixed<R>(o, ldg(o.hdr + (size_t)T * o.steps + t), lane, f, r);
+        fetch_mixed<R>(o, ldg(o.hdr + (T * o.steps + t)), lane, f, r);
     }
 }
 
