@@ -487,29 +487,38 @@ __device__ __forceinline__ void stage_images(uint8_t* lds, const uint8_t* src, u
 // Work items of a grouped kernel: (active expert a, tile group tg, member
 // groups [m_lo, m_hi) of TB tokens).  The shared expert (active entry 0) has
 // every token as a member, so each of its member groups is an item of its
-// own, listed first and tile-group-major (its weights are then re-read from
-// L2 / MALL by neighbouring items); a routed expert's item covers all of its
-// members (rarely more than one group).
+// own, listed first; a routed expert's item covers all of its members
+// (rarely more than one group).  Workgroup b runs on XCD b % 8 (dispatch is
+// round robin over the XCDs), so the shared expert's items are placed to put
+// every member group of a tile group on one XCD, in consecutive waves of the
+// dispatch: its weights are read from HBM once per tile group and the other
+// member groups find them in that XCD's L2.  Slots past the last tile group
+// (tile groups rounded up to a multiple of 8) are empty items.
+constexpr uint32_t MOE_BATCH_XCDS = 8;
+__host__ __device__ inline uint32_t moe_batch_items(uint32_t gpe, uint32_t ngs, uint32_t n_routed) {
+    return (gpe + MOE_BATCH_XCDS - 1u) / MOE_BATCH_XCDS * MOE_BATCH_XCDS * ngs + n_routed * gpe;
+}
 struct ItemMap {
-    uint32_t gpe, ngs, extra, n_items;
+    uint32_t gpe, ngs, nsh, n_items;
     __device__ ItemMap(const MoeBatchDims& d, uint32_t gpe_, uint32_t n_active, uint32_t TB) : gpe(gpe_) {
         ngs = d.SI ? (d.T + TB - 1) / TB : 0u;
-        extra = ngs > 1 ? gpe * (ngs - 1) : 0u;
-        n_items = extra + n_active * gpe;
+        nsh = moe_batch_items(gpe, ngs, 0u);
+        n_items = moe_batch_items(gpe, ngs, n_active - (ngs ? 1u : 0u));
     }
     __device__ void at(uint32_t item, uint32_t* a, uint32_t* tg, uint32_t* m_lo, uint32_t* m_hi) const {
-        if (item < extra) {
+        if (item < nsh) {
+            const uint32_t x = item % MOE_BATCH_XCDS, s = item / MOE_BATCH_XCDS;
             *a = 0;
-            *tg = item / (ngs - 1);
-            *m_lo = 1u + item % (ngs - 1);
+            *tg = x + MOE_BATCH_XCDS * (s / ngs);  // >= gpe: an empty slot
+            *m_lo = s % ngs;
             *m_hi = *m_lo + 1u;
             return;
         }
-        const uint32_t i = item - extra;
-        *a = i / gpe;
+        const uint32_t i = item - nsh;
+        *a = (ngs ? 1u : 0u) + i / gpe;
         *tg = i % gpe;
         *m_lo = 0;
-        *m_hi = (*a == 0 && ngs) ? 1u : 0xFFFFFFFFu;
+        *m_hi = 0xFFFFFFFFu;
     }
 };
 
@@ -686,17 +695,20 @@ static uint32_t tokens_per_group(uint32_t img_bytes, uint32_t cap, uint32_t budg
 hipError_t launch_moe_batch(const MoeBatchDims& d, const MoeLayerDev& L, const float* bias, const uint16_t* x_bf16,
                             float* y, const MoeBatchWs& ws, int32_t* ids_out, float* w_out, hipStream_t s) {
     const uint32_t pairs = d.T * d.K + (d.SI ? d.T : 0u);
-    const uint32_t max_active = min(d.E, d.T * d.K) + (d.SI ? 1u : 0u);
     // from sweeps of config 5: gate/up 8-tile items, one tile per wave, 6 steps
     // in flight; down 8-tile items, two tiles per wave, 4 steps in flight
     constexpr int GU_TPI = 8, GU_TPW = 1, GU_D = 6, DN_TPI = 8, DN_TPW = 2, DN_D = 4;
     const uint32_t gpe_gu = (n_tiles_for(max(d.I, d.SI)) + GU_TPI - 1) / GU_TPI;
     const uint32_t gpe_dn = (n_tiles_for(d.H) + DN_TPI - 1) / DN_TPI;
-    const uint32_t gu_items = (max_active + (d.SI ? d.T : 0u)) * gpe_gu, dn_items = (max_active + (d.SI ? d.T : 0u)) * gpe_dn;
     const uint32_t ximg = (uint32_t)moe_batch_img_bytes(d.H), aimg = (uint32_t)moe_batch_img_bytes(d.Imax);
     const uint32_t budget = image_lds_budget();
     const uint32_t tb_gu = tokens_per_group(ximg, 4u, budget), tb_dn = tokens_per_group(aimg, 4u, budget);
     if (tb_gu == 0 || tb_dn == 0) return hipErrorInvalidValue;
+    // the kernels' item counts (an upper bound: every active expert routed)
+    const uint32_t tbg = tb_gu >= 4 ? 4u : tb_gu >= 2 ? 2u : 1u, tbd = tb_dn >= 4 ? 4u : tb_dn >= 2 ? 2u : 1u;
+    const uint32_t n_routed = min(d.E, d.T * d.K);
+    const uint32_t gu_items = moe_batch_items(gpe_gu, d.SI ? (d.T + tbg - 1) / tbg : 0u, n_routed);
+    const uint32_t dn_items = moe_batch_items(gpe_dn, d.SI ? (d.T + tbd - 1) / tbd : 0u, n_routed);
     hipLaunchKernelGGL(moe_batch_xprep_kernel, dim3(d.T, (d.H + XPART_COLS - 1) / XPART_COLS), dim3(256),
                        (size_t)q4_stage_floats(d.H) * sizeof(float), s, d, x_bf16, ws);
     hipLaunchKernelGGL(moe_batch_router_kernel, dim3((d.E + RT_ROWS - 1) / RT_ROWS, d.S), dim3(256), 0, s, d, L.router_w,
