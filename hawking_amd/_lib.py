@@ -163,6 +163,7 @@ PROTOTYPES = {
     "hk_moe_decode_stack": (C.c_int, [_p, _p, _p, _p, _p, _p, _p]),
     "hk_moe_decode_stack_persistent": (C.c_int, [_p, _p, _p]),
     "hk_moe_model_set_stack_launch": (C.c_int, [_p, _p, _i32]),
+    "hk_moe_model_set_stall_polls": (C.c_int, [_p, _p, _u32]),
     "hk_moe_forward_batch": (C.c_int, [_p, _p, _u32, _p, _u32, _p, _p, _p, _p]),
     "hk_moe15_layer_create": (C.c_int, [_p, C.POINTER(Moe15LayerSrc), C.POINTER(_p)]),
     "hk_moe15_layer_free": (C.c_int, [_p, _p]),

@@ -1333,6 +1333,7 @@ struct hk_moe_model {
     size_t stack_bytes = 0;
     hk::StackArgs st{};  // the buffer pointers and strides (per-call fields unset)
     uint32_t tag = 1;
+    uint32_t stall_polls = HK_STALL_POLLS_DEFAULT;  // the persistent launch's bound on each wait
     int cu_count = 0;
 };
 
@@ -1938,7 +1939,14 @@ static hk::StackArgs stack_args(hk_ctx* ctx, hk_moe_model* m, const float* h_in,
     a.status = ctx->dev_status;
     a.gu_tiles = n_tiles_for(m->dims.has_shared ? std::max(m->dims.I, m->dims.SI) : m->dims.I);
     a.ng = a.gu_tiles * (m->dims.K + (m->dims.has_shared ? 1u : 0u));
+    a.spin_limit = m->stall_polls;
     return a;
+}
+
+extern "C" int hk_moe_model_set_stall_polls(hk_ctx* ctx, hk_moe_model* m, uint32_t polls) {
+    if (!ctx || !m) return HK_E_INVALID_ARG;
+    m->stall_polls = polls;
+    return HK_OK;
 }
 
 extern "C" int hk_moe_decode_stack_persistent(hk_ctx* ctx, hk_moe_model* m, int* persistent) {

@@ -262,9 +262,16 @@ __device__ __forceinline__ float group_max(float v) {
     }));
 }
 
+// A unit's exponent E_u is capped at UNIT_EXP_CAP above the image's: the
+// unit entries fold f_u = 2^-E_u into ALPHA (down to 2^-6 for a Q2 item's
+// half alpha), and 2^-6 * 2^-120 = 2^-126 is the smallest normal float.  A
+// unit whose max is below 2^-98 therefore keeps fewer than 24 bits: its
+// elements are quantized to 2^-120 (2^-121 worst-case error) instead.
+constexpr int UNIT_EXP_CAP = 120;
+
 // The x image: fixed-point x (E = 23 - exponent of max|x|; 0 for x = 0 or
 // non-finite x, which sets the flag), per unit of SXG columns E_u = 23 -
-// exponent of the unit's max (at most E + 100; E for an all-zero unit),
+// exponent of the unit's max (at most E + UNIT_EXP_CAP; E for an all-zero unit),
 // X = rint(x 2^E_u), and from it the A tiles and each unit's {ALPHA f_u,
 // BETA f_u sum X} with f_u = 2^(E - E_u), written to img
 // (x_lds_bytes<KIND>(steps) bytes, any address space).  Returns E.
@@ -322,7 +329,7 @@ __device__ int x_image(const Team& team, const XChunks<NC>& xc, const float* x, 
             const float mu = group_max<NL>(max_abs8(v));
             int eu = 0;
             if (mu > 0.0f) (void)frexpf(mu, &eu);
-            const int Eu = mu > 0.0f ? min(23 - eu, E + 100) : E;
+            const int Eu = mu > 0.0f ? min(23 - eu, E + UNIT_EXP_CAP) : E;
             const float fu = ldexpf(1.0f, E - Eu);
             float f[8];
             int32_t s = quantize8(v, Eu, f);
@@ -428,7 +435,7 @@ __device__ __forceinline__ bool image_chunk(uint32_t ch, float4 (&v)[2], uint8_t
     }
     int eu = 0;
     if (m > 0.0f) (void)frexpf(m, &eu);
-    const int Eu = m > 0.0f ? min(23 - eu, 100) : 0;
+    const int Eu = m > 0.0f ? min(23 - eu, UNIT_EXP_CAP) : 0;
     const float fu = ldexpf(1.0f, -Eu);
     float f[8];
     const int32_t s = group_sum<NL>(quantize8(v, Eu, f));
@@ -519,7 +526,7 @@ __device__ __forceinline__ void image_zero_blocks(uint32_t lane, uint8_t* tiles,
 // range's first unit on), in LDS or global memory: lane l takes chunks cb + l,
 // cb + l + 64, ...; each unit (SXG
 // columns = NL consecutive lanes) has E_u = 23 - exponent of its max (at most
-// 100, so f_u = 2^-E_u is a normal float; 0 for an all-zero unit), and every
+// UNIT_EXP_CAP, so ALPHA f_u is a normal float; 0 for an all-zero unit), and every
 // column's limbs of X = rint(x 2^E_u) are stored as bytes at their tile
 // positions (a_pos).  These are the bytes x_image makes, and its unit entries
 // divided by its 2^E (every scale a power of two times the same roundings),

@@ -104,6 +104,7 @@ struct StackArgs {
     uint32_t hrs, lrs, ars;
     uint32_t* abort;    // the tag of a launch whose wait ran out
     uint32_t ng, gu_tiles;
+    uint32_t spin_limit;  // polls a wait makes before the launch gives up (hk_moe_model_set_stall_polls)
 };
 size_t moe_stack_lds_bytes(int kind, const MoeDims& d);
 // Zeroes n 64-bit words on stream s with a kernel (graph-capture safe).
@@ -121,7 +122,10 @@ hipError_t launch_moe_layer(int kind, const MoeDims& d, const MoeLayerDev& L, co
 
 constexpr uint32_t MOE_BATCH_MAX_TOKENS = 64;
 constexpr uint32_t MOE_BATCH_MAX_EXPERTS = 512;
-constexpr uint32_t MOE_BATCH_ROUTER_COLS = 256;  // router columns per split-K workgroup
+#ifndef HK_BATCH_ROUTER_COLS
+#define HK_BATCH_ROUTER_COLS 256
+#endif
+constexpr uint32_t MOE_BATCH_ROUTER_COLS = HK_BATCH_ROUTER_COLS;  // router columns per split-K workgroup
 
 struct MoeBatchDims {
     uint32_t T;         // tokens

@@ -53,7 +53,6 @@ namespace hk {
 
 namespace {
 
-constexpr uint32_t SPIN_LIMIT = 1u << 16;  // polling rounds before a wait gives up (~tens of ms)
 constexpr int ROW_PRE = 8;                 // router row float4 per lane held in registers (2048 columns)
 // gate/up steps in flight (a mixed step of both organs is 24 registers, a Q4 step 10)
 template <int KIND>
@@ -110,7 +109,7 @@ __device__ uint32_t ll_wait(const uint64_t* p, const uint32_t (&idx)[N], uint32_
             return WAIT_OK;
         }
         if ((int32_t)(ab - a.tag) >= 0) return WAIT_ABORT;  // any wait of this launch gave up
-        if (spin >= SPIN_LIMIT) {
+        if (spin >= a.spin_limit) {
             __hip_atomic_store(abort, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             if (__lane_id() == 0) atomicOr(a.status, HK_DEVERR_STALL);
             return WAIT_ABORT;
@@ -142,7 +141,7 @@ __device__ uint32_t chunk_finish(const uint64_t* bp, uint64_t (&w)[8], uint32_t 
         }
         const uint32_t ab = __hip_atomic_load(a.abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         if ((int32_t)(ab - a.tag) >= 0) return WAIT_ABORT;
-        if (spin >= SPIN_LIMIT) {
+        if (spin >= a.spin_limit) {
             __hip_atomic_store(a.abort, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             if (__lane_id() == 0) atomicOr(a.status, HK_DEVERR_STALL);
             return WAIT_ABORT;

@@ -191,6 +191,10 @@ class MoeModel:
         self.ctx.call("hk_moe_model_set_stack_launch", self.h, int(mode))
         self.shape.stack_launch = int(mode)
 
+    def set_stall_polls(self, polls: int) -> None:
+        """The persistent launch's bound on each hand-off wait (hk_moe_model_set_stall_polls)."""
+        self.ctx.call("hk_moe_model_set_stall_polls", self.h, int(polls))
+
     def stack_is_persistent(self) -> bool:
         """Whether decode_stack runs as one persistent launch here (hk_moe_decode_stack_persistent)."""
         v = C.c_int(0)

@@ -523,6 +523,17 @@ int hk_moe_decode_stack_persistent(hk_ctx* ctx, hk_moe_model* model, int* persis
  * HK_STACK_PERSISTENT); no reference counterpart.  Not to be called while a token of the
  * model is in flight on another stream. */
 int hk_moe_model_set_stack_launch(hk_ctx* ctx, hk_moe_model* model, int32_t stack_launch);
+/* The persistent launch's bound on each hand-off wait: a wait that has polled
+ * `polls` times without its producer's words gives up, sets device status
+ * bit 4 (value 4, hk_check_device_status) and makes every other wait of that launch return,
+ * so the launch always ends; h_out, ids and weights of that call are then
+ * undefined and the next call (a new tag) is unaffected.  Default
+ * HK_STALL_POLLS_DEFAULT (tens of milliseconds); 0 gives up at the first
+ * wait that finds its words missing.  No reference counterpart (its command
+ * buffer has no hand-off waits).  Not to be called while a token of the model
+ * is in flight on another stream. */
+#define HK_STALL_POLLS_DEFAULT 65536u
+int hk_moe_model_set_stall_polls(hk_ctx* ctx, hk_moe_model* model, uint32_t polls);
 
 /* BackendMoe::moe_block (backend/mod.rs:509-521) on one layer of a model:
  * the routed (and optional shared) expert block for CALLER-supplied routes,

@@ -91,3 +91,33 @@ def test_persistent_stack_flags_nonfinite_then_recovers(ctx):
     rout, rids, rw = run_mode(m, h, False)
     assert ctx.device_status() == 0
     assert np.array_equal(out.view(np.uint32), rout.view(np.uint32))
+
+
+def test_persistent_stack_gives_up_and_recovers(ctx):
+    """The persistent launch's give-up path, forced from the host: with a
+    stall bound of 0 polls, the first wait that finds its producer's words
+    missing gives up (status bit 4) and every other wait of the launch
+    returns, so the launch drains (the call returns and the device answers);
+    the next call, with a new tag and the default bound, is bit-identical to
+    the per-layer launches."""
+    from hawking_amd.moe import MoeModel, MoeShape
+    say("persistent stack forced give-up")
+    shape = MoeShape(n_layers=4, hidden=2048, inter=512, shared_inter=512, n_experts=512, top_k=10,
+                     expert_kind=U.HK_MIXED, expert_group=128)
+    m = MoeModel(ctx, shape)
+    m.fill_synthetic(U.SEED + 4)
+    assert admitted(m)
+    h = np.random.default_rng(21).standard_normal(shape.hidden).astype(np.float32)
+    ctx.device_status()
+    m.set_stall_polls(0)
+    try:
+        run_mode(m, h, True)
+    finally:
+        m.set_stall_polls(65536)
+    assert ctx.device_status() & 4, "a wait gave up: status bit 4"
+    out, ids, w = run_mode(m, h, True)
+    assert ctx.device_status() == 0
+    rout, rids, rw = run_mode(m, h, False)
+    assert np.array_equal(ids, rids)
+    assert np.array_equal(w.view(np.uint32), rw.view(np.uint32))
+    assert np.array_equal(out.view(np.uint32), rout.view(np.uint32))
