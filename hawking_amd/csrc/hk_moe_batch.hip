@@ -388,21 +388,36 @@ __global__ void __launch_bounds__(1024) moe_batch_group_kernel(MoeBatchDims d, M
 
 // ------------------------------------------------------------------ grouped tile worker
 
+// Step t of weight tiles r < R (tile r of organ r's data/scales) into fr.
+template <int R>
+__device__ __forceinline__ void tiles_fetch(const uint8_t* const* base_d, const uint16_t* const* base_s, uint32_t t,
+                                            Frag<HK_Q4, R>& fr) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        fr.v[r] = ldg(reinterpret_cast<const uint4*>(base_d[r] + (size_t)t * 1024u));
+        fr.s[r] = ldg(base_s[r] + (size_t)t * 64u);
+    }
+}
+
+// The pipeline's first D steps (past the end they re-read the last): issued
+// before the member tokens' images are staged, so the staging's latency and
+// the weights' overlap.
+template <int R, int D>
+__device__ __forceinline__ void tiles_fetch_first(const uint8_t* const* base_d, const uint16_t* const* base_s,
+                                                  uint32_t S, Frag<HK_Q4, R> (&f)[D]) {
+#pragma unroll
+    for (int k = 0; k < D; ++k) tiles_fetch<R>(base_d, base_s, min((uint32_t)k, S - 1u), f[k]);
+}
+
 // acc[j][r] += this lane's partial dot of weight tile r (tile Tr[r] of organ
 // r's data/scales, S column steps) with member token j's x image in LDS
-// (img + j*img_bytes), over all S steps with a D-deep weight pipeline.
+// (img + j*img_bytes), over all S steps with a D-deep weight pipeline whose
+// first D steps are already in f (tiles_fetch_first).
 template <int R, int TB, int D>
 __device__ __forceinline__ void tiles_x_tokens(const uint8_t* const* base_d, const uint16_t* const* base_s, uint32_t S,
                                                const uint8_t* img, uint32_t img_bytes, uint32_t nm, uint32_t aoff,
-                                               int q, float (*acc)[R]) {
-    Frag<HK_Q4, R> f[D];
-    auto fetch = [&](uint32_t t, Frag<HK_Q4, R>& fr) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            fr.v[r] = ldg(reinterpret_cast<const uint4*>(base_d[r] + (size_t)t * 1024u));
-            fr.s[r] = ldg(base_s[r] + (size_t)t * 64u);
-        }
-    };
+                                               int q, float (*acc)[R], Frag<HK_Q4, R> (&f)[D]) {
+    auto fetch = [&](uint32_t t, Frag<HK_Q4, R>& fr) { tiles_fetch<R>(base_d, base_s, t, fr); };
     const float* SX0 = reinterpret_cast<const float*>(img + (size_t)S * 2u * A_TILE_STRIDE);
     auto consume = [&](const Frag<HK_Q4, R>& fr, uint32_t t) {
         v4i alo[TB], ahi[TB];
@@ -436,8 +451,6 @@ __device__ __forceinline__ void tiles_x_tokens(const uint8_t* const* base_d, con
     // branch-free pipeline (refetches past the end re-read the last step), so
     // each consume waits only for its own slot's loads
     const uint32_t last = S - 1u;
-#pragma unroll
-    for (int k = 0; k < D; ++k) fetch(min((uint32_t)k, last), f[k]);
     uint32_t it = 0;
     for (; it + D <= S; it += D) {
 #pragma unroll
@@ -566,12 +579,14 @@ moe_batch_gate_up_kernel(MoeBatchDims d, const OrganView* __restrict__ table, Mo
                 pair[j] = ws.members[ent.y + m0 + min((uint32_t)j, nm - 1u)];
                 tok[j] = pair_token(d, pair[j]);
             }
+            Frag<HK_Q4, 2 * TPW> f[D];
+            if (vw[0]) tiles_fetch_first<2 * TPW, D>(bd, bs, S, f);
             __syncthreads();
             stage_images<TB, 4>(lds, ws.ximg, ws.ximg_stride, tok, nm, img_bytes);
             __syncthreads();
             if (!vw[0]) continue;
             float acc[TB][2 * TPW] = {};
-            tiles_x_tokens<2 * TPW, TB, D>(bd, bs, S, lds, img_bytes, nm, aoff, q, acc);
+            tiles_x_tokens<2 * TPW, TB, D>(bd, bs, S, lds, img_bytes, nm, aoff, q, acc, f);
 #pragma unroll
             for (int j = 0; j < TB; ++j) {
                 if ((uint32_t)j >= nm) break;
@@ -641,12 +656,14 @@ moe_batch_down_kernel(MoeBatchDims d, const OrganView* __restrict__ table, MoeBa
             uint32_t pair[TB];
 #pragma unroll
             for (int j = 0; j < TB; ++j) pair[j] = ws.members[ent.y + m0 + min((uint32_t)j, nm - 1u)];
+            Frag<HK_Q4, TPW> f[D];
+            if (vw[0]) tiles_fetch_first<TPW, D>(bd, bs, S, f);
             __syncthreads();
             stage_images<TB, 2>(lds, ws.aimg, ws.aimg_stride, pair, nm, img_bytes);
             __syncthreads();
             if (!vw[0]) continue;
             float acc[TB][TPW] = {};
-            tiles_x_tokens<TPW, TB, D>(bd, bs, S, lds, img_bytes, nm, aoff, q, acc);
+            tiles_x_tokens<TPW, TB, D>(bd, bs, S, lds, img_bytes, nm, aoff, q, acc, f);
 #pragma unroll
             for (int j = 0; j < TB; ++j) {
                 if ((uint32_t)j >= nm) break;
