@@ -1369,7 +1369,6 @@ static int alloc_batch_ws(hk_ctx* ctx, hk_moe_model* m) {
     const size_t pairs = (size_t)T * K + (c.shared_inter ? T : 0);
     const size_t xs = align256(moe_batch_img_bytes(c.hidden)), as = align256(moe_batch_img_bytes(imax));
     const size_t sz[] = {
-        (size_t)T * c.hidden * 4,          // x32
         (size_t)T * xs,                    // ximg
         (size_t)T * 4,                     // ximg_e
         (size_t)S * T * E * 4,             // part
@@ -1394,20 +1393,19 @@ static int alloc_batch_ws(hk_ctx* ctx, hk_moe_model* m) {
         p += align256(sz[i]);
     }
     hk::MoeBatchWs& w = m->bws;
-    w.x32 = static_cast<float*>(ptr[0]);
-    w.ximg = static_cast<uint8_t*>(ptr[1]);
-    w.ximg_e = static_cast<int32_t*>(ptr[2]);
-    w.part = static_cast<float*>(ptr[3]);
-    w.ids = static_cast<int32_t*>(ptr[4]);
-    w.w = static_cast<float*>(ptr[5]);
-    w.order = static_cast<int32_t*>(ptr[6]);
-    w.active = static_cast<uint4*>(ptr[7]);
-    w.n_active = static_cast<uint32_t*>(ptr[8]);
-    w.members = static_cast<uint32_t*>(ptr[9]);
-    w.act = static_cast<float*>(ptr[10]);
-    w.aimg = static_cast<uint8_t*>(ptr[11]);
-    w.aimg_e = static_cast<int32_t*>(ptr[12]);
-    w.ybuf = static_cast<float*>(ptr[13]);
+    w.ximg = static_cast<uint8_t*>(ptr[0]);
+    w.ximg_e = static_cast<int32_t*>(ptr[1]);
+    w.part = static_cast<float*>(ptr[2]);
+    w.ids = static_cast<int32_t*>(ptr[3]);
+    w.w = static_cast<float*>(ptr[4]);
+    w.order = static_cast<int32_t*>(ptr[5]);
+    w.active = static_cast<uint4*>(ptr[6]);
+    w.n_active = static_cast<uint32_t*>(ptr[7]);
+    w.members = static_cast<uint32_t*>(ptr[8]);
+    w.act = static_cast<float*>(ptr[9]);
+    w.aimg = static_cast<uint8_t*>(ptr[10]);
+    w.aimg_e = static_cast<int32_t*>(ptr[11]);
+    w.ybuf = static_cast<float*>(ptr[12]);
     w.ximg_stride = (uint32_t)xs;
     w.aimg_stride = (uint32_t)as;
     w.status = ctx->dev_status;

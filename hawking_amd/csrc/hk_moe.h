@@ -123,7 +123,7 @@ hipError_t launch_moe_layer(int kind, const MoeDims& d, const MoeLayerDev& L, co
 constexpr uint32_t MOE_BATCH_MAX_TOKENS = 64;
 constexpr uint32_t MOE_BATCH_MAX_EXPERTS = 512;
 #ifndef HK_BATCH_ROUTER_COLS
-#define HK_BATCH_ROUTER_COLS 256
+#define HK_BATCH_ROUTER_COLS 512
 #endif
 constexpr uint32_t MOE_BATCH_ROUTER_COLS = HK_BATCH_ROUTER_COLS;  // router columns per split-K workgroup
 
@@ -142,7 +142,6 @@ struct MoeBatchDims {
 // token t is T*K + t.  active[a] = {expert, first member, members}; entry 0 is
 // the shared expert (if any), then the routed experts in ascending id.
 struct MoeBatchWs {
-    float* x32;          // [T x H]
     uint8_t* ximg;       // [T] x images of x (stride ximg_stride)
     int32_t* ximg_e;     // [T]
     float* part;         // [S x T x E] router partials

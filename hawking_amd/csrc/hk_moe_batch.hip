@@ -5,11 +5,11 @@
 // matrix-core engine of hk_mfma.h: every weight fetch serves all the member
 // tokens whose x images are in LDS).
 //
-//   1. xprep:    x (bf16) -> f32 rows and the fixed-point x image of each token
-//   2. router:   logits partials, split-K over 256-column slices (f32, router
-//                rows and x staged in LDS)
-//   3. route:    one wave per token: the noaux_tc route (gravity_glm.rs:447-500)
-//                on the DPP network
+//   1. xprep:    the fixed-point x image of each token (from its bf16 x)
+//   2. router:   logits partials, split-K over 512-column slices (f32 matrix
+//                cores, weights and bf16 x straight from global memory)
+//   3. route:    one block per token: the noaux_tc route (gravity_glm.rs:447-500)
+//                with ranks by counting in LDS
 //   4. group:    one block: the (token, slot) pairs grouped by expert (shared
 //                expert first, then ascending id) and each token's slots in
 //                ascending expert id
@@ -26,7 +26,9 @@
 
 namespace hk {
 
-constexpr uint32_t RT_ROWS = 32, RT_COLS = 128, RT_SLICE = MOE_BATCH_ROUTER_COLS;  // router tiling
+// router tiling: RT_WAVES waves of RT_WCOLS columns per split
+constexpr uint32_t RT_WAVES = 8, RT_WCOLS = 64, RT_SLICE = RT_WAVES * RT_WCOLS;
+static_assert(RT_SLICE == MOE_BATCH_ROUTER_COLS, "split width");
 
 size_t moe_batch_img_bytes(uint32_t cols) { return x_lds_bytes<HK_Q4>(n_steps_for(HK_Q4, cols)); }
 
@@ -113,11 +115,6 @@ __global__ void __launch_bounds__(256) moe_batch_xprep_kernel(MoeBatchDims d, co
                 float4* o = reinterpret_cast<float4*>(xs + 8u * k);
                 o[0] = make_float4(f[0], f[1], f[2], f[3]);
                 o[1] = make_float4(f[4], f[5], f[6], f[7]);
-                if (8u * k / XPART_COLS == part) {
-                    float4* g = reinterpret_cast<float4*>(ws.x32 + (size_t)t * d.H + 8u * k);
-                    g[0] = o[0];
-                    g[1] = o[1];
-                }
             }
         }
     }
@@ -130,92 +127,111 @@ __global__ void __launch_bounds__(256) moe_batch_xprep_kernel(MoeBatchDims d, co
     }
 }
 
-// ------------------------------------------------------------------ 2. router (split-K)
+// ------------------------------------------------------------------ 2. router (split-K, f32 matrix cores)
 
-// part[s][t][e] = sum over columns [256 s, 256 (s+1)) of W[e][k] x[t][k] for a
-// block of 32 router rows; thread (row r = tid / 8, tokens 4 (tid % 8) .. +3),
-// router rows and x staged in LDS 128 columns at a time (hidden % 128 == 0).
-// The inner loop reads 4 columns of its row and 4 x rows per step, 16 FMAs.
-__global__ void __launch_bounds__(256) moe_batch_router_kernel(MoeBatchDims d, const float* __restrict__ W,
-                                                               MoeBatchWs ws) {
-    __shared__ __align__(16) float wsh[RT_ROWS][RT_COLS + 4];
-    __shared__ __align__(16) float xsh[RT_COLS][32];
-    const uint32_t rr = threadIdx.x >> 3, tg = threadIdx.x & 7u;
-    const uint32_t r0 = blockIdx.x * RT_ROWS, s = blockIdx.y;
-    const uint32_t k0 = s * RT_SLICE, k1 = min(k0 + RT_SLICE, d.H);
+// part[s][t][e] = sum over the columns [RT_SLICE s, RT_SLICE (s + 1)) of
+// W[e][k] x[t][k], x read as bf16 (exact in f32).  A workgroup owns 16 router
+// rows and one slice; each of its RT_WAVES waves takes RT_WCOLS columns of it
+// and the waves' sums meet in LDS (in wave order).  A wave loads its weights
+// (16 rows) and its tokens' x (16 per token tile) straight into registers and
+// multiplies on v_mfma_f32_16x16x4_f32: in 32-column group g, lane l supplies
+// row / token l % 16 at columns 32 g + 8 (l / 16) + i, i < 8, the same map for
+// both operands (MFMA i of the group takes column offset i of every lane).
+__global__ void __launch_bounds__(64 * RT_WAVES) moe_batch_router_kernel(MoeBatchDims d, const float* __restrict__ W,
+                                                                        const uint16_t* __restrict__ xb, MoeBatchWs ws) {
+    constexpr uint32_t G = RT_WCOLS / 32u;
+    __shared__ float red[RT_WAVES][2][16][17];
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = threadIdx.x >> 6, li = (uint32_t)lane & 15u, lg = (uint32_t)lane >> 4;
+    const uint32_t r0 = blockIdx.x * 16u, s = blockIdx.y;
+    const uint32_t c0 = s * RT_SLICE + wave * RT_WCOLS;
+    const bool on = c0 < d.H;  // hidden % 128 == 0: a wave's columns are all in or all out
+    const uint32_t row = r0 + li;
+    float4 wv[G][2];
+#pragma unroll
+    for (uint32_t g = 0; g < G; ++g) {
+        const float* src = W + (size_t)row * d.H + c0 + 32u * g + 8u * lg;
+        const bool ok = on && row < d.E;
+        wv[g][0] = ok ? ldg(reinterpret_cast<const float4*>(src)) : make_float4(0.f, 0.f, 0.f, 0.f);
+        wv[g][1] = ok ? ldg(reinterpret_cast<const float4*>(src + 4)) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     for (uint32_t tb = 0; tb < d.T; tb += 32u) {
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
-        for (uint32_t kc = k0; kc < k1; kc += RT_COLS) {
-            const uint32_t kn = min(RT_COLS, k1 - kc);
-            // every thread's loads of the chunk (4 row pieces, 4 x pieces) in flight, then the stores
-            constexpr uint32_t NP = RT_ROWS * RT_COLS / 4u / 256u;
-            static_assert(NP * 256u == 32u * RT_COLS / 4u, "x and W chunks have the same piece count");
-            float4 wv[NP], xv[NP];
+        uint4 xv[2][G];
 #pragma unroll
-            for (uint32_t i = 0; i < NP; ++i) {
-                const uint32_t idx = threadIdx.x + 256u * i;
-                const uint32_t row = idx / (RT_COLS / 4u), k = 4u * (idx % (RT_COLS / 4u));
-                wv[i] = (r0 + row < d.E && k < kn) ? ldg(reinterpret_cast<const float4*>(W + (size_t)(r0 + row) * d.H + kc + k))
-                                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-                xv[i] = (tb + row < d.T && k < kn)
-                            ? ldg(reinterpret_cast<const float4*>(ws.x32 + (size_t)(tb + row) * d.H + kc + k))
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-            __syncthreads();
+        for (uint32_t tt = 0; tt < 2; ++tt) {
+            const uint32_t t = tb + 16u * tt + li;
 #pragma unroll
-            for (uint32_t i = 0; i < NP; ++i) {
-                const uint32_t idx = threadIdx.x + 256u * i;
-                const uint32_t row = idx / (RT_COLS / 4u), k = 4u * (idx % (RT_COLS / 4u));
-                *reinterpret_cast<float4*>(&wsh[row][k]) = wv[i];
-                xsh[k][row] = xv[i].x;
-                xsh[k + 1][row] = xv[i].y;
-                xsh[k + 2][row] = xv[i].z;
-                xsh[k + 3][row] = xv[i].w;
-            }
-            __syncthreads();
-#pragma unroll 4
-            for (uint32_t k = 0; k < kn; k += 4) {
-                const float4 w = *reinterpret_cast<const float4*>(&wsh[rr][k]);
-                const float wk[4] = {w.x, w.y, w.z, w.w};
+            for (uint32_t g = 0; g < G; ++g)
+                xv[tt][g] = (on && t < d.T)
+                                ? ldg(reinterpret_cast<const uint4*>(xb + (size_t)t * d.H + c0 + 32u * g + 8u * lg))
+                                : make_uint4(0u, 0u, 0u, 0u);
+        }
+        hk_f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-                for (uint32_t i = 0; i < 4; ++i) {
-                    const float4 x = *reinterpret_cast<const float4*>(&xsh[k + i][4u * tg]);
-                    acc[0] += wk[i] * x.x;
-                    acc[1] += wk[i] * x.y;
-                    acc[2] += wk[i] * x.z;
-                    acc[3] += wk[i] * x.w;
+        for (uint32_t g = 0; g < G; ++g) {
+            const float wk[8] = {wv[g][0].x, wv[g][0].y, wv[g][0].z, wv[g][0].w,
+                                 wv[g][1].x, wv[g][1].y, wv[g][1].z, wv[g][1].w};
+#pragma unroll
+            for (uint32_t tt = 0; tt < 2; ++tt) {
+                const uint32_t xw[4] = {xv[tt][g].x, xv[tt][g].y, xv[tt][g].z, xv[tt][g].w};
+#pragma unroll
+                for (uint32_t i = 0; i < 8; ++i) {
+                    const float xf = __builtin_bit_cast(float, (i & 1u) ? (xw[i >> 1] & 0xFFFF0000u) : (xw[i >> 1] << 16));
+                    acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(wk[i], xf, acc[tt], 0, 0, 0);
                 }
             }
         }
-        const uint32_t r = r0 + rr;
+        // lane l, register j holds row 4 (l / 16) + j, token l % 16 of its tile
+        __syncthreads();
 #pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) {
-            const uint32_t t = tb + 4u * tg + i;
-            if (r < d.E && t < d.T) ws.part[((size_t)s * d.T + t) * d.E + r] = acc[i];
+        for (uint32_t tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) red[wave][tt][4u * lg + j][li] = acc[tt][j];
+        __syncthreads();
+        for (uint32_t o = threadIdx.x; o < 2u * 16u * 16u; o += blockDim.x) {
+            const uint32_t tt = o >> 8, m = (o >> 4) & 15u, n = o & 15u;
+            float v = red[0][tt][m][n];
+#pragma unroll
+            for (uint32_t w = 1; w < RT_WAVES; ++w) v += red[w][tt][m][n];
+            const uint32_t e = r0 + m, t = tb + 16u * tt + n;
+            if (e < d.E && t < d.T) ws.part[((size_t)s * d.T + t) * d.E + e] = v;
         }
     }
 }
 
-// ------------------------------------------------------------------ 3. route (one wave per token)
+// ------------------------------------------------------------------ 3. route (one block per token)
 
 __device__ __forceinline__ float key_value(uint64_t k) {
     const uint32_t o = (uint32_t)(k >> 32);
     return __builtin_bit_cast(float, (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
 }
 
-// The block first sums each expert's split-K partials (in split order, every
-// load of a thread in flight at once) into LDS; one wave then selects.
-constexpr uint32_t MOE_ROUTER_MAX_SPLITS = 8192 / MOE_BATCH_ROUTER_COLS;
+// Experts i in [lo, hi) whose key is above k.
+__device__ __forceinline__ uint32_t keys_above(const uint64_t* keys, uint32_t lo, uint32_t hi, uint64_t k) {
+    uint32_t n = 0;
+#pragma unroll 8
+    for (uint32_t i = lo; i < hi; ++i) n += keys[i] > k ? 1u : 0u;
+    return n;
+}
 
+constexpr uint32_t MOE_ROUTER_MAX_SPLITS = (8192 + MOE_BATCH_ROUTER_COLS - 1) / MOE_BATCH_ROUTER_COLS;
+
+// The block sums each expert's split-K partials (in split order, every load
+// of a thread in flight at once) and ranks by counting: an expert's rank is
+// the number of keys above its own (keys are distinct: value desc, index asc),
+// so every selection below is the order-exact top-n.
 __global__ void __launch_bounds__(256) moe_batch_route_kernel(MoeBatchDims d, const float* __restrict__ bias,
                                                               MoeBatchWs ws, int32_t* ids_out, float* w_out) {
-    constexpr int NPL = MOE_BATCH_MAX_EXPERTS / 64;
-    __shared__ float lg[MOE_BATCH_MAX_EXPERTS];
+    __shared__ uint64_t key[MOE_BATCH_MAX_EXPERTS];
+    __shared__ float sc[MOE_BATCH_MAX_EXPERTS];
+    __shared__ float top2[64][2];
+    __shared__ uint64_t gkey[64];
+    __shared__ uint32_t chosen[64];
     __shared__ int32_t sel_i[16];
     __shared__ float sel_w[16];
-    const int lane = threadIdx.x & 63;
-    const uint32_t t = blockIdx.x, E = d.E, K = d.K, per = d.E / d.n_group;
-    for (uint32_t e = threadIdx.x; e < E; e += blockDim.x) {
+    const uint32_t t = blockIdx.x, E = d.E, K = d.K, per = d.E / d.n_group, tid = threadIdx.x;
+    uint32_t bad = 0;
+    for (uint32_t e = tid; e < E; e += blockDim.x) {
         float pv[MOE_ROUTER_MAX_SPLITS];
 #pragma unroll
         for (uint32_t s = 0; s < MOE_ROUTER_MAX_SPLITS; ++s)
@@ -224,90 +240,42 @@ __global__ void __launch_bounds__(256) moe_batch_route_kernel(MoeBatchDims d, co
 #pragma unroll
         for (uint32_t s = 0; s < MOE_ROUTER_MAX_SPLITS; ++s)
             if (s < d.S) l += pv[s];
-        lg[e] = l;
-    }
-    __syncthreads();
-    if (threadIdx.x >= 64) return;
-    float sc[NPL], cv[NPL];
-    uint32_t bad = 0;
-#pragma unroll
-    for (int j = 0; j < NPL; ++j) {
-        const uint32_t i = (uint32_t)lane + 64u * j;
-        sc[j] = 0.f;
-        cv[j] = -INFINITY;
-        if (i < E) {
-            const float l = lg[i];
-            if (!isfinite(l)) bad = 1;
-            sc[j] = 1.0f / (1.0f + expf(-l));
-            cv[j] = sc[j] + bias[i];
-        }
+        if (!isfinite(l)) bad = 1;
+        const float v = 1.0f / (1.0f + expf(-l));
+        sc[e] = v;
+        key[e] = order_key(v + bias[e], e);
     }
     if (bad) atomicOr(ws.status, HK_DEVERR_NONFINITE);
-    // group strength = sum of its best two corrected scores, in topk_desc order
-    uint64_t chosen = 1;
+    __syncthreads();
     if (d.topk_group < d.n_group) {
-        uint64_t gkey = 0;
-        for (uint32_t g = 0; g < d.n_group; ++g) {
-            uint64_t k1 = 0;
-#pragma unroll
-            for (int j = 0; j < NPL; ++j) {
-                const uint32_t i = (uint32_t)lane + 64u * j;
-                const uint64_t k = (i < E && i / per == g) ? order_key(cv[j], i) : 0ull;
-                k1 = k > k1 ? k : k1;
-            }
-            const uint64_t b0 = wave_max_key(k1);
-            float gs = -0.0f + key_value(b0);
-            if (per >= 2) {
-                uint64_t k2 = 0;
-#pragma unroll
-                for (int j = 0; j < NPL; ++j) {
-                    const uint32_t i = (uint32_t)lane + 64u * j;
-                    const uint64_t k = (i < E && i / per == g) ? order_key(cv[j], i) : 0ull;
-                    k2 = (k != b0 && k > k2) ? k : k2;
-                }
-                gs = gs + key_value(wave_max_key(k2));
-            }
-            if ((uint32_t)lane == g) gkey = order_key(gs, g);
+        // group strength = sum of its best two corrected scores, in topk_desc order
+        for (uint32_t e = tid; e < E; e += blockDim.x) {
+            const uint32_t g = e / per, rk = keys_above(key, g * per, g * per + per, key[e]);
+            if (rk < 2) top2[g][rk] = key_value(key[e]);
         }
-        chosen = 0;
-        for (uint32_t c = 0; c < d.topk_group; ++c) {
-            const uint64_t w = wave_max_key(gkey);
-            const uint32_t g = ~(uint32_t)w;
-            chosen |= 1ull << g;
-            if ((uint32_t)lane == g) gkey = 0;
+        __syncthreads();
+        if (tid < d.n_group) {
+            float gs = -0.0f + top2[tid][0];
+            if (per >= 2) gs = gs + top2[tid][1];
+            gkey[tid] = order_key(gs, tid);
         }
-    } else {
-        chosen = d.n_group >= 64 ? ~0ull : ((1ull << d.n_group) - 1ull);
+        __syncthreads();
+        if (tid < d.n_group) chosen[tid] = keys_above(gkey, 0, d.n_group, gkey[tid]) < d.topk_group ? 1u : 0u;
+        __syncthreads();
+        // only experts inside a chosen group compete (the others at -inf)
+        for (uint32_t e = tid; e < E; e += blockDim.x)
+            if (!chosen[e / per]) key[e] = order_key(-INFINITY, e);
+        __syncthreads();
     }
-    // only experts inside a chosen group compete (the others at -inf)
-    uint64_t key[NPL];
-    uint64_t best = 0;
-#pragma unroll
-    for (int j = 0; j < NPL; ++j) {
-        const uint32_t i = (uint32_t)lane + 64u * j;
-        key[j] = i < E ? order_key(((chosen >> (i / per)) & 1ull) ? cv[j] : -INFINITY, i) : 0ull;
-        best = key[j] > best ? key[j] : best;
-    }
-    for (uint32_t r = 0; r < K; ++r) {
-        const uint64_t w = wave_max_key(best);
-        const uint32_t id = ~(uint32_t)w;
-        if ((id & 63u) == (uint32_t)lane) {
-            float s_id = 0.f;
-            best = 0;
-#pragma unroll
-            for (int j = 0; j < NPL; ++j) {
-                if ((uint32_t)j == (id >> 6)) {
-                    s_id = sc[j];
-                    key[j] = 0;
-                }
-                best = key[j] > best ? key[j] : best;
-            }
-            sel_i[r] = (int32_t)id;
-            sel_w[r] = s_id;  // weights are the uncorrected scores
+    for (uint32_t e = tid; e < E; e += blockDim.x) {
+        const uint32_t rk = keys_above(key, 0, E, key[e]);
+        if (rk < K) {
+            sel_i[rk] = (int32_t)e;
+            sel_w[rk] = sc[e];  // weights are the uncorrected scores
         }
     }
-    wave_lds_sync();
-    if (lane == 0) {
+    __syncthreads();
+    if (tid == 0) {
         float total = -0.0f;
         for (uint32_t r = 0; r < K; ++r) total += sel_w[r];
         total = total + 1e-20f;
@@ -317,13 +285,13 @@ __global__ void __launch_bounds__(256) moe_batch_route_kernel(MoeBatchDims d, co
             sel_w[r] = v * d.scaling;
         }
     }
-    wave_lds_sync();
-    if ((uint32_t)lane < K) {
-        const uint32_t p = t * K + (uint32_t)lane;
-        ws.ids[p] = sel_i[lane];
-        ws.w[p] = sel_w[lane];
-        if (ids_out) ids_out[p] = sel_i[lane];
-        if (w_out) w_out[p] = sel_w[lane];
+    __syncthreads();
+    if (tid < K) {
+        const uint32_t p = t * K + tid;
+        ws.ids[p] = sel_i[tid];
+        ws.w[p] = sel_w[tid];
+        if (ids_out) ids_out[p] = sel_i[tid];
+        if (w_out) w_out[p] = sel_w[tid];
     }
 }
 
@@ -686,9 +654,17 @@ __global__ void __launch_bounds__(256) moe_batch_combine_kernel(MoeBatchDims d, 
     const uint32_t t = blockIdx.x, row = blockIdx.y * blockDim.x + threadIdx.x;
     if (row >= d.H) return;
     // routed = 0; routed += o * w over the experts in ascending id; routed += shared
+    // (every load in flight at once: top_k <= 16)
+    float v[17];
+#pragma unroll
+    for (uint32_t j = 0; j < 16; ++j)
+        v[j] = j < d.K ? ws.ybuf[(size_t)(t * d.K + (uint32_t)ws.order[t * d.K + j]) * d.H + row] : 0.0f;
+    v[16] = d.SI ? ws.ybuf[(size_t)(d.T * d.K + t) * d.H + row] : 0.0f;
     float acc = 0.0f;
-    for (uint32_t j = 0; j < d.K; ++j) acc += ws.ybuf[(size_t)(t * d.K + (uint32_t)ws.order[t * d.K + j]) * d.H + row];
-    if (d.SI) acc += ws.ybuf[(size_t)(d.T * d.K + t) * d.H + row];
+#pragma unroll
+    for (uint32_t j = 0; j < 16; ++j)
+        if (j < d.K) acc += v[j];
+    if (d.SI) acc += v[16];
     y[(size_t)t * d.H + row] = acc;
 }
 
@@ -731,8 +707,8 @@ hipError_t launch_moe_batch(const MoeBatchDims& d, const MoeLayerDev& L, const f
     const uint32_t dn_items = moe_batch_items(gpe_dn, d.SI ? (d.T + tbd - 1) / tbd : 0u, n_routed);
     hipLaunchKernelGGL(moe_batch_xprep_kernel, dim3(d.T, (d.H + XPART_COLS - 1) / XPART_COLS), dim3(256),
                        (size_t)q4_stage_floats(d.H) * sizeof(float), s, d, x_bf16, ws);
-    hipLaunchKernelGGL(moe_batch_router_kernel, dim3((d.E + RT_ROWS - 1) / RT_ROWS, d.S), dim3(256), 0, s, d, L.router_w,
-                       ws);
+    hipLaunchKernelGGL(moe_batch_router_kernel, dim3((d.E + 15) / 16, d.S), dim3(64 * RT_WAVES), 0, s, d, L.router_w,
+                       x_bf16, ws);
     hipLaunchKernelGGL(moe_batch_route_kernel, dim3(d.T), dim3(256), 0, s, d, bias, ws, ids_out, w_out);
     hipLaunchKernelGGL(moe_batch_group_kernel, dim3(1), dim3(1024), 0, s, d, ws);
     // one workgroup per item (the item count is an upper bound; the device
