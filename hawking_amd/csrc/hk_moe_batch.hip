@@ -7,7 +7,8 @@
 //
 //   1. xprep:    the fixed-point x image of each token (from its bf16 x)
 //   2. router:   logits partials, split-K over 512-column slices (f32 matrix
-//                cores, weights and bf16 x straight from global memory)
+//                cores, weights and bf16 x straight from global memory);
+//                steps 1 and 2 share one launch
 //   3. route:    one block per token: the noaux_tc route (gravity_glm.rs:447-500)
 //                with ranks by counting in LDS
 //   4. group:    one block: the (token, slot) pairs grouped by expert (shared
@@ -27,7 +28,7 @@
 namespace hk {
 
 // router tiling: RT_WAVES waves of RT_WCOLS columns per split
-constexpr uint32_t RT_WAVES = 8, RT_WCOLS = 64, RT_SLICE = RT_WAVES * RT_WCOLS;
+constexpr uint32_t RT_WAVES = 4, RT_WCOLS = 128, RT_SLICE = RT_WAVES * RT_WCOLS;
 static_assert(RT_SLICE == MOE_BATCH_ROUTER_COLS, "split width");
 
 size_t moe_batch_img_bytes(uint32_t cols) { return x_lds_bytes<HK_Q4>(n_steps_for(HK_Q4, cols)); }
@@ -86,11 +87,10 @@ __device__ int x_image_in_place(float* xs, uint32_t cols, uint8_t* img, float* r
                              tb + XPART_STEPS);
 }
 
-__global__ void __launch_bounds__(256) moe_batch_xprep_kernel(MoeBatchDims d, const uint16_t* __restrict__ xb,
-                                                              MoeBatchWs ws) {
-    extern __shared__ __align__(16) float xs[];  // [H rounded up to whole steps]
+// Token t's image part `part`; xs: LDS of q4_stage_floats(H) floats.
+__device__ __forceinline__ void xprep_block(const MoeBatchDims& d, const uint16_t* __restrict__ xb, const MoeBatchWs& ws,
+                                            uint32_t t, uint32_t part, float* xs) {
     __shared__ float red[4];
-    const uint32_t t = blockIdx.x, part = blockIdx.y;
     {
         // 8 bf16 per thread and piece, 4 pieces in flight (hidden <= 8192)
         const uint4* src = reinterpret_cast<const uint4*>(xb + (size_t)t * d.H);
@@ -137,13 +137,13 @@ __global__ void __launch_bounds__(256) moe_batch_xprep_kernel(MoeBatchDims d, co
 // multiplies on v_mfma_f32_16x16x4_f32: in 32-column group g, lane l supplies
 // row / token l % 16 at columns 32 g + 8 (l / 16) + i, i < 8, the same map for
 // both operands (MFMA i of the group takes column offset i of every lane).
-__global__ void __launch_bounds__(64 * RT_WAVES) moe_batch_router_kernel(MoeBatchDims d, const float* __restrict__ W,
-                                                                        const uint16_t* __restrict__ xb, MoeBatchWs ws) {
+__device__ __forceinline__ void router_block(const MoeBatchDims& d, const float* __restrict__ W,
+                                             const uint16_t* __restrict__ xb, const MoeBatchWs& ws, uint32_t bx, uint32_t s) {
     constexpr uint32_t G = RT_WCOLS / 32u;
     __shared__ float red[RT_WAVES][2][16][17];
     const int lane = threadIdx.x & 63;
     const uint32_t wave = threadIdx.x >> 6, li = (uint32_t)lane & 15u, lg = (uint32_t)lane >> 4;
-    const uint32_t r0 = blockIdx.x * 16u, s = blockIdx.y;
+    const uint32_t r0 = bx * 16u;
     const uint32_t c0 = s * RT_SLICE + wave * RT_WCOLS;
     const bool on = c0 < d.H;  // hidden % 128 == 0: a wave's columns are all in or all out
     const uint32_t row = r0 + li;
@@ -196,6 +196,21 @@ __global__ void __launch_bounds__(64 * RT_WAVES) moe_batch_router_kernel(MoeBatc
             const uint32_t e = r0 + m, t = tb + 16u * tt + n;
             if (e < d.E && t < d.T) ws.part[((size_t)s * d.T + t) * d.E + e] = v;
         }
+    }
+}
+
+// Steps 1 and 2 in one launch (they are independent): blocks [0, nr) are
+// router blocks (row tile b % rt, split b / rt), the rest x image blocks
+// (token i % T, part i / T).
+__global__ void __launch_bounds__(64 * RT_WAVES) moe_batch_prep_kernel(MoeBatchDims d, const uint16_t* __restrict__ xb,
+                                                                      const float* __restrict__ W, MoeBatchWs ws) {
+    extern __shared__ __align__(16) float xs[];  // [H rounded up to whole steps]
+    const uint32_t rt = (d.E + 15u) / 16u, nr = rt * d.S, b = blockIdx.x;
+    if (b < nr) {
+        router_block(d, W, xb, ws, b % rt, b / rt);
+    } else {
+        const uint32_t i = b - nr;
+        xprep_block(d, xb, ws, i % d.T, i / d.T, xs);
     }
 }
 
@@ -705,10 +720,9 @@ hipError_t launch_moe_batch(const MoeBatchDims& d, const MoeLayerDev& L, const f
     const uint32_t n_routed = min(d.E, d.T * d.K);
     const uint32_t gu_items = moe_batch_items(gpe_gu, d.SI ? (d.T + tbg - 1) / tbg : 0u, n_routed);
     const uint32_t dn_items = moe_batch_items(gpe_dn, d.SI ? (d.T + tbd - 1) / tbd : 0u, n_routed);
-    hipLaunchKernelGGL(moe_batch_xprep_kernel, dim3(d.T, (d.H + XPART_COLS - 1) / XPART_COLS), dim3(256),
-                       (size_t)q4_stage_floats(d.H) * sizeof(float), s, d, x_bf16, ws);
-    hipLaunchKernelGGL(moe_batch_router_kernel, dim3((d.E + 15) / 16, d.S), dim3(64 * RT_WAVES), 0, s, d, L.router_w,
-                       x_bf16, ws);
+    const uint32_t n_prep = (d.E + 15u) / 16u * d.S + d.T * ((d.H + XPART_COLS - 1) / XPART_COLS);
+    hipLaunchKernelGGL(moe_batch_prep_kernel, dim3(n_prep), dim3(64 * RT_WAVES), (size_t)q4_stage_floats(d.H) * sizeof(float),
+                       s, d, x_bf16, L.router_w, ws);
     hipLaunchKernelGGL(moe_batch_route_kernel, dim3(d.T), dim3(256), 0, s, d, bias, ws, ids_out, w_out);
     hipLaunchKernelGGL(moe_batch_group_kernel, dim3(1), dim3(1024), 0, s, d, ws);
     // one workgroup per item (the item count is an upper bound; the device
