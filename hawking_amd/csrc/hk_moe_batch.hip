@@ -704,8 +704,13 @@ hipError_t launch_moe_batch(const MoeBatchDims& d, const MoeLayerDev& L, const f
                             float* y, const MoeBatchWs& ws, int32_t* ids_out, float* w_out, hipStream_t s) {
     const uint32_t pairs = d.T * d.K + (d.SI ? d.T : 0u);
     // from sweeps of config 5: gate/up 8-tile items, one tile per wave, 6 steps
-    // in flight; down 8-tile items, two tiles per wave, 4 steps in flight
-    constexpr int GU_TPI = 8, GU_TPW = 1, GU_D = 6, DN_TPI = 8, DN_TPW = 2, DN_D = 4;
+    // in flight (5: same, 8: +0.7 %); down 8-tile items, two tiles per wave, 3
+    // steps in flight (4: +0.2 %, 6: +3 % with 201 VGPRs)
+#ifndef HK_BATCH_GU_D  // (build-time overrides for pipeline-depth sweeps)
+#define HK_BATCH_GU_D 6
+#define HK_BATCH_DN_D 3
+#endif
+    constexpr int GU_TPI = 8, GU_TPW = 1, GU_D = HK_BATCH_GU_D, DN_TPI = 8, DN_TPW = 2, DN_D = HK_BATCH_DN_D;
     const uint32_t gpe_gu = (n_tiles_for(max(d.I, d.SI)) + GU_TPI - 1) / GU_TPI;
     const uint32_t gpe_dn = (n_tiles_for(d.H) + DN_TPI - 1) / DN_TPI;
     const uint32_t ximg = (uint32_t)moe_batch_img_bytes(d.H), aimg = (uint32_t)moe_batch_img_bytes(d.Imax);
