@@ -704,20 +704,26 @@ hipError_t launch_moe_batch(const MoeBatchDims& d, const MoeLayerDev& L, const f
                             float* y, const MoeBatchWs& ws, int32_t* ids_out, float* w_out, hipStream_t s) {
     const uint32_t pairs = d.T * d.K + (d.SI ? d.T : 0u);
     // from sweeps of config 5: gate/up 8-tile items, one tile per wave, 6 steps
-    // in flight (5: same, 8: +0.7 %); down 8-tile items, two tiles per wave, 3
-    // steps in flight (4: +0.2 %, 6: +3 % with 201 VGPRs)
-#ifndef HK_BATCH_GU_D  // (build-time overrides for pipeline-depth sweeps)
+    // in flight (5: same, 8: +0.7 %; 4-tile items with two tokens a group and
+    // two workgroups a CU: +5.8 %, with four tokens: +20 %; 8-tile items with
+    // two tokens: +6.6 %); down 8-tile items, two tiles per wave, 3 steps in
+    // flight (4: +0.2 %, 6: +3 % with 201 VGPRs)
+#ifndef HK_BATCH_GU_D  // (build-time overrides for launch-shape sweeps)
 #define HK_BATCH_GU_D 6
 #define HK_BATCH_DN_D 3
 #endif
-    constexpr int GU_TPI = 8, GU_TPW = 1, GU_D = HK_BATCH_GU_D, DN_TPI = 8, DN_TPW = 2, DN_D = HK_BATCH_DN_D;
+#ifndef HK_BATCH_GU_TPI
+#define HK_BATCH_GU_TPI 8
+#define HK_BATCH_GU_TBMAX 4
+#endif
+    constexpr int GU_TPI = HK_BATCH_GU_TPI, GU_TPW = 1, GU_D = HK_BATCH_GU_D, DN_TPI = 8, DN_TPW = 2, DN_D = HK_BATCH_DN_D;
     const uint32_t gpe_gu = (n_tiles_for(max(d.I, d.SI)) + GU_TPI - 1) / GU_TPI;
     const uint32_t gpe_dn = (n_tiles_for(d.H) + DN_TPI - 1) / DN_TPI;
     const uint32_t ximg = (uint32_t)moe_batch_img_bytes(d.H), aimg = (uint32_t)moe_batch_img_bytes(d.Imax);
     const uint32_t budget = image_lds_budget();
     // 4 tokens per down group too: 8 (the activation images are small) took
     // 237 VGPRs and ran the down kernel 22 % slower
-    const uint32_t tb_gu = tokens_per_group(ximg, 4u, budget), tb_dn = tokens_per_group(aimg, 4u, budget);
+    const uint32_t tb_gu = tokens_per_group(ximg, HK_BATCH_GU_TBMAX, budget), tb_dn = tokens_per_group(aimg, 4u, budget);
     if (tb_gu == 0 || tb_dn == 0) return hipErrorInvalidValue;
     // the kernels' item counts (an upper bound: every active expert routed)
     const uint32_t tbg = tb_gu >= 4 ? 4u : tb_gu >= 2 ? 2u : 1u;
