@@ -466,7 +466,11 @@ __host__ __device__ inline LowrankLds lowrank_lds(const OrganView& l, const Orga
 
 // HGRAVS01 pairs y_i = L_i (R_i x_i), one workgroup per pair: the right
 // factor's rows (mid, kept in LDS) and then the left factor's, whose first
-// weight steps are already in flight while mid is computed.  The arithmetic
+// weight steps are issued as soon as the right factor's walk ends (in flight
+// while mid's x image is built).  Issued at the start instead, they hold
+// their registers through the right walk: 74 VGPRs and 6 workgroups per CU
+// against 56 and 8 (4,096 pairs then run in exactly two rounds; r160 pairs
+// 164 against 161 us).  The arithmetic
 // is that of two gemv_tiled_kernel launches (mid rounded to f32, then its own
 // x image), so the result is the same bits.  mid_all (may be null) also
 // receives mid.
@@ -495,7 +499,6 @@ lowrank_kernel(const OrganView* __restrict__ lefts, const OrganView* __restrict_
     TileWalk<HK_U3, HK_LR_RR, HK_LR_RD> wr;
     wr.start(rv, 0, rv.n_tiles, wave, lane);
     TileWalk<HK_U3, HK_LR_LR, HK_LR_LD> wl;
-    wl.start(lv, 0, lv.n_tiles, wave, lane);
     // both x images with E = 0, scattered from each thread's chunks (the
     // two launches' images to the bit: the GEMV builds them the same way)
     bool bad = false;
@@ -517,6 +520,7 @@ lowrank_kernel(const OrganView* __restrict__ lefts, const OrganView* __restrict_
         __syncthreads();
     }
     wr.run(rv, 0, lds + M.img_r, lane, mid);
+    wl.start(lv, 0, lv.n_tiles, wave, lane);
     __syncthreads();
     if (mid_all)
         for (uint32_t i = threadIdx.x; i < rv.rows; i += blockDim.x) mid_all[(size_t)oi * mid_stride + i] = mid[i];
