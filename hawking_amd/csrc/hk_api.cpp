@@ -614,6 +614,7 @@ struct hk_organ_set {
     ResView* res_dev = nullptr;  // HGRAVR02 sets: the residual table
     uint32_t res_pieces = 0;     // the most record pieces of any organ's apply part
     uint32_t res_pieces_256 = 0;  // the same for 256-row parts
+    uint32_t res8_pieces = 0, res8_pieces_256 = 0;  // the byte steps' (the fused GEMV's)
     uint32_t n = 0;
     OrganView first{};
 };
@@ -649,6 +650,8 @@ extern "C" int hk_organ_set_create(hk_ctx* ctx, const hk_organ* const* organs, u
             res[i] = organs[i]->res;
             set->res_pieces = std::max(set->res_pieces, organs[i]->res_pieces);
             set->res_pieces_256 = std::max(set->res_pieces_256, organs[i]->res_pieces_256);
+            set->res8_pieces = std::max(set->res8_pieces, organs[i]->res8_pieces);
+            set->res8_pieces_256 = std::max(set->res8_pieces_256, organs[i]->res8_pieces_256);
         }
         if (hipMalloc(&set->res_dev, n * sizeof(ResView)) != hipSuccess) {
             (void)hipFree(set->dev);
@@ -691,8 +694,8 @@ extern "C" int hk_gemv_set(hk_ctx* ctx, const hk_organ_set* set, const float* x,
     bool fused = false;
     if (set->res_dev)
         rc = check_hip(ctx,
-                       launch_gemv_rice(set->dev, set->res_dev, set->n, set->first, set->res_pieces_256,
-                                        set->res_pieces, x, x_stride, y, y_stride, st, &fused),
+                       launch_gemv_rice(set->dev, set->res_dev, set->n, set->first, set->res8_pieces_256,
+                                        set->res8_pieces, x, x_stride, y, y_stride, st, &fused),
                        "gemv_set launch");
     if (!rc && !fused)
         rc = check_hip(ctx, launch_gemv_tiled(set->dev, set->n, set->first, x, x_stride, y, y_stride, st),
@@ -895,6 +898,42 @@ static std::string rice_expand_csr(const uint8_t* rice, size_t len, uint32_t fir
     return "";
 }
 
+// The fused GEMV's byte steps (ResView) from the padded CSR: each real
+// record of a row (its padding, column cols, ends it) at table index
+// 3 col + sign, reached from the previous index (-1 at the row's start) in
+// steps of at most 255 through -0 entries (3c + 2); the row padded to 4 bytes
+// with steps onto the next -0 entries (at most 3 + 3 + 3 past the last real
+// index 3 cols - 2, inside the table's 3 cols + 8 entries); the stream padded
+// to 16 bytes.
+static void rice_step_records(const std::vector<uint32_t>& row_ptr, const std::vector<uint16_t>& recs, uint32_t rows,
+                              uint32_t cols, std::vector<uint32_t>& rp8, std::vector<uint8_t>& r8) {
+    rp8.assign((size_t)rows + 1, 0u);
+    r8.clear();
+    for (uint32_t r = 0; r < rows; ++r) {
+        int64_t v = -1;
+        const size_t start = r8.size();
+        for (uint32_t k = row_ptr[r]; k < row_ptr[r + 1]; ++k) {
+            const uint32_t u = recs[k];
+            if ((u >> 1) >= cols) break;
+            const int64_t t = 3 * (int64_t)(u >> 1) + (int64_t)(u & 1u);
+            while (t - v > 255) {
+                const int64_t z = v + 255 - (v + 253) % 3;  // the farthest -0 entry in reach (v + 253 >= 252)
+                r8.push_back((uint8_t)(z - v));
+                v = z;
+            }
+            r8.push_back((uint8_t)(t - v));
+            v = t;
+        }
+        while ((r8.size() - start) % 4u) {
+            const int64_t z = v + 1 + (3 - (v + 1 + 1) % 3) % 3;  // the nearest -0 entry past v (v + 2 >= 1)
+            r8.push_back((uint8_t)(z - v));
+            v = z;
+        }
+        rp8[r + 1] = (uint32_t)r8.size();
+    }
+    r8.resize((r8.size() + 15u) & ~(size_t)15, 0u);
+}
+
 // Bind of an HGRAVR02 body: base repack on the device, Rice expand + CSR.
 static int upload_rice(hk_ctx* ctx, const hk_rice_q1* s, hipStream_t st, hk_organ** out) {
     const size_t n = (size_t)s->rows * s->cols, count = s->outlier_count;
@@ -911,6 +950,9 @@ static int upload_rice(hk_ctx* ctx, const hk_rice_q1* s, hipStream_t st, hk_orga
     const std::string err = rice_expand_csr(rice.data(), rice.size(), s->first_index, s->rice_k, count, s->rows, s->cols,
                                             signs.data(), row_ptr, recs);
     if (!err.empty()) return set_error(ctx, HK_E_GEOMETRY, err);
+    std::vector<uint32_t> rp8;
+    std::vector<uint8_t> r8;
+    rice_step_records(row_ptr, recs, s->rows, s->cols, rp8, r8);
 
     const Layout L = layout_for(HK_BIN, 128, s->rows, s->cols, 0, 0);
     uint8_t* stage = nullptr;
@@ -933,7 +975,8 @@ static int upload_rice(hk_ctx* ctx, const hk_rice_q1* s, hipStream_t st, hk_orga
     if (!rc) rc = repack_into_organ(ctx, canon, 0, 0, st, &o);
     if (!rc) {
         const size_t a_rp = align256(row_ptr.size() * 4), a_rec = align256(recs.size() * 2);
-        if (hipMalloc(&o->res_mem, a_rp + a_rec + sizeof(ResView)) != hipSuccess) {
+        const size_t a_rp8 = align256(rp8.size() * 4), a_r8 = align256(r8.size());
+        if (hipMalloc(&o->res_mem, a_rp + a_rec + a_rp8 + a_r8 + sizeof(ResView)) != hipSuccess) {
             rc = set_error(ctx, HK_E_NOMEM, "residual allocation failed");
         } else {
             uint8_t* m = static_cast<uint8_t*>(o->res_mem);
@@ -943,11 +986,22 @@ static int upload_rice(hk_ctx* ctx, const hk_rice_q1* s, hipStream_t st, hk_orga
             o->res.cols = s->cols;
             o->res.scale = f16_to_f32_host(s->residual_scale_f16);
             o->res.count = row_ptr[s->rows];
+            o->res.row_ptr8 = reinterpret_cast<const uint32_t*>(m + a_rp + a_rec);
+            o->res.recs8 = m + a_rp + a_rec + a_rp8;
+            o->res.count8 = rp8[s->rows];
             o->res_pieces = rice_part_pieces(row_ptr.data(), s->rows, RICE_APPLY_ROWS);
             o->res_pieces_256 = rice_part_pieces(row_ptr.data(), s->rows, 256u);
-            ResView* rd = reinterpret_cast<ResView*>(m + a_rp + a_rec);
+            o->res8_pieces = rice_part_pieces8(rp8.data(), s->rows, 512u);
+            o->res8_pieces_256 = rice_part_pieces8(rp8.data(), s->rows, 256u);
+            ResView* rd = reinterpret_cast<ResView*>(m + a_rp + a_rec + a_rp8 + a_r8);
             rc = check_hip(ctx, hipMemcpy(m, row_ptr.data(), row_ptr.size() * 4, hipMemcpyHostToDevice), "row_ptr upload");
             if (!rc) rc = check_hip(ctx, hipMemcpy(m + a_rp, recs.data(), recs.size() * 2, hipMemcpyHostToDevice), "record upload");
+            if (!rc)
+                rc = check_hip(ctx, hipMemcpy(m + a_rp + a_rec, rp8.data(), rp8.size() * 4, hipMemcpyHostToDevice),
+                               "step row_ptr upload");
+            if (!rc)
+                rc = check_hip(ctx, hipMemcpy(m + a_rp + a_rec + a_rp8, r8.data(), r8.size(), hipMemcpyHostToDevice),
+                               "step record upload");
             if (!rc) rc = check_hip(ctx, hipMemcpy(rd, &o->res, sizeof(ResView), hipMemcpyHostToDevice), "residual upload");
             o->res_dev = rd;
         }

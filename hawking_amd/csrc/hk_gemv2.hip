@@ -165,7 +165,7 @@ constexpr int GEMV_RES_NP = 12;  // record pieces per thread (pieces <= 12 * 256
 template <int KIND, bool RES>
 __host__ __device__ inline size_t gemv_ysh_offset(uint32_t steps, uint32_t tpw, uint32_t cols, uint32_t pieces) {
     size_t off = gemv_hdr_offset<KIND>(steps) + (KIND == HK_MIXED ? (size_t)tpw * steps * sizeof(uint4) : 0);
-    if (RES) off = std::max(off, (rice_table_bytes(cols) + (size_t)pieces * 16u + 15u) & ~(size_t)15);
+    if (RES) off = std::max(off, (rice_table3_bytes(cols) + (size_t)pieces * 16u + 15u) & ~(size_t)15);
     return off;
 }
 
@@ -178,9 +178,10 @@ __host__ __device__ inline size_t gemv_ysh_offset(uint32_t steps, uint32_t tpw, 
 // RES (binary, at most 512 rows per workgroup): y = base + the HGRAVR02
 // residual, to the bit what rice_apply does after the plain GEMV.  The row
 // pointers load with the first weights; after the main loop the image's
-// LDS takes the signed product table (from the x chunks still in
-// registers) and the workgroup's record pieces (loaded in one round), and
-// each row's thread adds its products to the row total in index order.
+// LDS takes the product table of three entries per column (from the x
+// chunks still in registers) and the workgroup's byte-step record pieces
+// (loaded in one round), and each row's thread steps through its records,
+// adding its products to the row total in index order.
 template <int KIND, int R, int D, int NC, bool HEAD, bool RES = false>
 __global__ void __launch_bounds__(256)
 gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const float* __restrict__ xall,
@@ -244,12 +245,12 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const
     if constexpr (RES) {
         rv = ra.views[oi];
         const uint32_t r0 = t0 * 16u, r1 = min(t1 * 16u, o.rows);
-        rp0 = ldg(rv.row_ptr + r0) / 8u;
+        rp0 = ldg(rv.row_ptr8 + r0) / 16u;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const uint32_t row = min(r0 + threadIdx.x + 256u * (uint32_t)h, r1);
-            my0[h] = ldg(rv.row_ptr + row);
-            my1[h] = ldg(rv.row_ptr + min(row + 1u, r1));
+            my0[h] = ldg(rv.row_ptr8 + row);
+            my1[h] = ldg(rv.row_ptr8 + min(row + 1u, r1));
         }
     }
     if constexpr (HEAD) head_norm_chunks<NC>(xc, o.cols, ha, red);
@@ -317,13 +318,13 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const
     if constexpr (RES) {
         // the image is dead: its bytes take the residual's table and records
         const uint32_t np = (ra.pieces + 255u) / 256u;
-        const uint4* recs = reinterpret_cast<const uint4*>(rv.recs);
-        const uint32_t plast = (rv.count + 7u) / 8u - 1u;
+        const uint4* recs = reinterpret_cast<const uint4*>(rv.recs8);
+        const uint32_t plast = (rv.count8 + 15u) / 16u - 1u;
         uint4 rr[GEMV_RES_NP];
 #pragma unroll
         for (int j = 0; j < GEMV_RES_NP; ++j)
             if ((uint32_t)j < np) rr[j] = ldg(recs + min(rp0 + threadIdx.x + 256u * (uint32_t)j, plast));
-        float2* Tt = reinterpret_cast<float2*>(lds);
+        float* T3 = reinterpret_cast<float*>(lds);
         {
             const uint32_t c0 = 8u * threadIdx.x;
             if (c0 < o.cols) {
@@ -332,30 +333,36 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
                     const float p = rv.scale * xv[k];
-                    Tt[c0 + (uint32_t)k] = make_float2(-p, p);
+                    T3[3u * (c0 + (uint32_t)k)] = -p;
+                    T3[3u * (c0 + (uint32_t)k) + 1u] = p;
+                    T3[3u * (c0 + (uint32_t)k) + 2u] = -0.0f;
                 }
             }
         }
-        if (threadIdx.x == 0) Tt[o.cols] = make_float2(-0.0f, -0.0f);
-        uint4* Rr = reinterpret_cast<uint4*>(lds + rice_table_bytes(o.cols));
+        if (threadIdx.x < 8u) T3[3u * o.cols + threadIdx.x] = -0.0f;
+        uint4* Rr = reinterpret_cast<uint4*>(lds + rice_table3_bytes(o.cols));
 #pragma unroll
         for (int j = 0; j < GEMV_RES_NP; ++j)
             if ((uint32_t)j < np && threadIdx.x + 256u * (uint32_t)j < ra.pieces) Rr[threadIdx.x + 256u * j] = rr[j];
         __syncthreads();
-        const float* Tf = reinterpret_cast<const float*>(lds);
-        const uint2* R2 = reinterpret_cast<const uint2*>(Rr);
+        const uint32_t* R4 = reinterpret_cast<const uint32_t*>(Rr);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const uint32_t i = threadIdx.x + 256u * (uint32_t)h, row = t0 * 16u + i;
             if (i < nrows && row < o.rows) {
                 float acc = ldexpf(ysh[i], -E);
+                uint32_t v = 0xFFFFFFFFu;  // -1: a row's first step lands on its first index
 #pragma unroll 2
                 for (uint32_t e = my0[h]; e < my1[h]; e += 4u) {
-                    const uint2 w = R2[(e - 8u * rp0) / 4u];
-                    acc += Tf[w.x & 0xFFFFu];
-                    acc += Tf[w.x >> 16];
-                    acc += Tf[w.y & 0xFFFFu];
-                    acc += Tf[w.y >> 16];
+                    const uint32_t w = R4[(e - 16u * rp0) / 4u];
+                    v += w & 0xFFu;
+                    acc += T3[v];
+                    v += (w >> 8) & 0xFFu;
+                    acc += T3[v];
+                    v += (w >> 16) & 0xFFu;
+                    acc += T3[v];
+                    v += w >> 24;
+                    acc += T3[v];
                 }
                 y[row] = acc;
             }

@@ -301,12 +301,23 @@ hipError_t launch_repack_batch(int kind, const RepackJob* jobs_dev, uint32_t n, 
 // each row's records in index order and padded to a multiple of 4 with the
 // record cols << 1 (a column past the end: adds nothing); count (the padded
 // total) is a multiple of 4 and recs is readable to the next multiple of 8.
+//
+// The fused GEMV reads the same records as byte steps (row_ptr8, recs8,
+// count8; rice_step_records): a row's records index a table of three
+// entries per column (3c: -p, 3c + 1: +p, 3c + 2: -0; then 8 entries of -0
+// past the last column, rice_table3_bytes), each byte the step from the
+// previous index (a row starts at -1); a gap wider than one byte steps
+// through -0 entries, and rows are padded to 4 bytes with steps onto -0
+// entries.  Adding -0 changes no sum, so the totals are the CSR's to the bit.
 struct ResView {
     const uint32_t* row_ptr;
     const uint16_t* recs;
     uint32_t rows, cols;
     float scale;
     uint32_t count;
+    const uint32_t* row_ptr8;  // [rows + 1], byte offsets into recs8
+    const uint8_t* recs8;      // count8 bytes, readable to the next multiple of 16
+    uint32_t count8;
 };
 // status |= 16 if any of the n f16 values is not finite.
 hipError_t launch_f16_check(const uint16_t* v, size_t n, uint32_t* status, hipStream_t s);
@@ -321,6 +332,10 @@ constexpr uint32_t RICE_APPLY_ROWS = 512;
 // records' entry), 16-byte aligned.
 __host__ __device__ inline size_t rice_table_bytes(uint32_t cols) { return ((size_t)cols * 8u + 8u + 15u) & ~(size_t)15; }
 uint32_t rice_part_pieces(const uint32_t* row_ptr, uint32_t rows, uint32_t part_rows);
+// The byte-step records' table: 3 cols + 8 floats, 16-byte aligned.
+__host__ __device__ inline size_t rice_table3_bytes(uint32_t cols) { return ((size_t)cols * 12u + 32u + 15u) & ~(size_t)15; }
+// The most 16-byte pieces of byte-step records any part_rows-row part spans.
+uint32_t rice_part_pieces8(const uint32_t* row_ptr8, uint32_t rows, uint32_t part_rows);
 hipError_t launch_rice_apply(const ResView* res_dev, uint32_t n, uint32_t rows, uint32_t cols, uint32_t pieces,
                              const float* x, size_t x_stride, float* y, size_t y_stride, hipStream_t s);
 // Device packer (pack_binary_rice_q1): fills the canonical device buffers
@@ -378,6 +393,7 @@ struct hk_organ {
     const hk::ResView* res_dev = nullptr;
     uint32_t res_pieces = 0;   // rice_part_pieces of the residual (RICE_APPLY_ROWS-row parts)
     uint32_t res_pieces_256 = 0;  // the same for 256-row parts
+    uint32_t res8_pieces = 0, res8_pieces_256 = 0;  // rice_part_pieces8 of the byte steps, 512- and 256-row parts
     void* view_dev = nullptr;  // device copy of `view` for single-organ launches
     void* mem = nullptr;
     size_t alloc_bytes = 0;

@@ -140,6 +140,15 @@ uint32_t rice_part_pieces(const uint32_t* row_ptr, uint32_t rows, uint32_t part_
     return most;
 }
 
+uint32_t rice_part_pieces8(const uint32_t* row_ptr8, uint32_t rows, uint32_t part_rows) {
+    uint32_t most = 0;
+    for (uint32_t r0 = 0; r0 < rows; r0 += part_rows) {
+        const uint32_t r1 = std::min(r0 + part_rows, rows);
+        most = std::max(most, (row_ptr8[r1] + 15u) / 16u - row_ptr8[r0] / 16u);
+    }
+    return most;
+}
+
 hipError_t launch_rice_apply(const ResView* res_dev, uint32_t n, uint32_t rows, uint32_t cols, uint32_t pieces,
                              const float* x, size_t x_stride, float* y, size_t y_stride, hipStream_t s) {
     if (n == 0 || rows == 0) return hipSuccess;
