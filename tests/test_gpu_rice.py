@@ -192,6 +192,38 @@ def test_rice_organ_set_fused_matches_single(ctx, oracle, rows, cols, n):
         assert np.array_equal(y1[i], orgs[i].matvec(xs[i])), i
 
 
+def test_rice_fused_byte_steps_edge_rows(ctx, oracle):
+    """The fused GEMV's byte-step records (one byte per step through the
+    three-entry product table) at their edges: a row's first outlier at
+    column 0, gaps of 85, 86 and 2,047 columns (zero, one and 24 steps through
+    -0 entries), adjacent columns, a row ending at the last column (padding
+    steps past it), and rows without outliers.  512 organs of 512 x 2048 reach
+    the fused launch (16,384 row tiles); its sums must be the GEMV-then-apply
+    sums of each organ, bit for bit."""
+    rows, cols, n = 512, 2048, 512
+    pattern = [[0, 2047], [], [1, 86, 172, 173, 2046], list(range(100, 140))]
+    planted = []
+    for r in range(rows):
+        planted += [r * cols + c for c in pattern[r % 4]]
+    rng = np.random.default_rng(7)
+    w = (rng.standard_normal(rows * cols) * 1e-3).astype(np.float32)
+    w[planted] = np.where(rng.random(len(planted)) < 0.5, -1.0, 1.0).astype(np.float32)
+    ratio = len(planted) / (rows * cols)  # a power-of-two denominator: the count is exact
+    p = oracle.rice_q1_pack(w.reshape(rows, cols), rows, cols, ratio)
+    say("rice byte steps", rows, cols, n, "outliers", p.count)
+    assert p.count == len(planted) and set(p.indices.tolist()) == set(planted)
+    from hawking_amd.organs import OrganSet
+    orgs = [_organ(ctx, p) for _ in range(n)]
+    s = OrganSet(ctx, orgs)
+    xs = np.stack([oracle.normal(oracle.stream_key(U.SEED, (0xAC << 20) + i), cols, 1.0) for i in range(n)])
+    y = ctx.empty((n, rows))
+    s.gemv(ctx.to_device(xs), cols, y, rows)
+    yy = y.download()
+    for i in (0, 1, n // 2, n - 1):
+        assert np.array_equal(yy[i], orgs[i].matvec(xs[i])), i
+        assert oracle.relative_l2(yy[i], oracle.rice_q1_matvec(p, xs[i])) < TOL
+
+
 def test_rice_upload_rejects_bad_streams(ctx, oracle):
     from hawking_amd._lib import HK_E_GEOMETRY, HK_E_NONFINITE, HawkingError
     from hawking_amd.organs import RiceQ1Packed
