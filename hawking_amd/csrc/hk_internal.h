@@ -74,6 +74,13 @@ __device__ __forceinline__ T ldg(const T* p) {
 }
 typedef unsigned int hk_u32x4 __attribute__((ext_vector_type(4)));
 typedef float hk_f32x4 __attribute__((ext_vector_type(4)));
+// *(base + byte_off bytes): a 32-bit byte offset from a uniform base takes
+// the scalar-base load form (an element index scaled in 64 bits would cost a
+// 64-bit address per lane).
+template <class T>
+__device__ __forceinline__ T ldg_at(const T* base, uint32_t byte_off) {
+    return ldg(reinterpret_cast<const T*>(reinterpret_cast<const uint8_t*>(base) + byte_off));
+}
 __device__ __forceinline__ uint4 ldg(const uint4* p) {
     const hk_u32x4 v = *(const __attribute__((address_space(1))) hk_u32x4*)(p);
     return make_uint4(v.x, v.y, v.z, v.w);

@@ -659,10 +659,14 @@ __device__ __forceinline__ void fetch_one(const OrganView& o, uint32_t T, uint32
         const bool tail = t + 1 == o.steps;
         const uint32_t nq = tail ? o.tail_q : 4u;
         const uint32_t l = (uint32_t)(lane >> 4) < nq ? (uint32_t)lane : (uint32_t)(lane & 15);
-        const uint8_t* base = o.data + (T * (uint32_t)u3_tile_data(o.steps, o.tail_q) + 768u * t);
-        f.lo[r] = ldg(reinterpret_cast<const uint2*>(base + 8u * l));
-        f.hi[r] = ldg(reinterpret_cast<const uint32_t*>(base + 128u * nq + 4u * l));
-        f.s[r] = ldg(o.scales + (T * (uint32_t)u3_tile_scales(o.steps, o.tail_q) + 64u * t + l));
+        // the lane's 12 bytes (low fields, then high bits): one 12-byte load
+        const uint32_t* lw = reinterpret_cast<const uint32_t*>(o.data + (T * (uint32_t)u3_tile_data(o.steps, o.tail_q) +
+                                                                         768u * t + 12u * l));
+        f.lo[r] = make_uint2(ldg(lw), ldg(lw + 1));
+        f.hi[r] = ldg(lw + 2);
+        // (a 32-bit byte offset: the scalar-base form; measured neutral or
+        // slightly slower for the other kinds' scale loads, so only here)
+        f.s[r] = ldg_at(o.scales, 2u * (T * (uint32_t)u3_tile_scales(o.steps, o.tail_q) + 64u * t + l));
     } else {
         fetch_mixed<R>(o, ldg(o.hdr + (T * o.steps + t)), lane, f, r);
     }

@@ -167,8 +167,11 @@ __device__ void repack_u3_body(const CanonView& src, const OrganView& dst) {
             s = src.scales[e0 / 64u];
         }
         uint8_t* base = const_cast<uint8_t*>(dst.data) + (size_t)T * tile_data + 768u * t;
-        *reinterpret_cast<uint2*>(base + 8u * l) = make_uint2(lo0, lo1);
-        *reinterpret_cast<uint32_t*>(base + 128u * nq + 4u * l) = hi;
+        (void)nq;
+        uint32_t* lane_words = reinterpret_cast<uint32_t*>(base + 12u * l);
+        lane_words[0] = lo0;
+        lane_words[1] = lo1;
+        lane_words[2] = hi;
         const_cast<uint16_t*>(dst.scales)[(size_t)T * tile_sc + 64u * t + l] = s;
     }
 }

@@ -35,10 +35,10 @@
 //         scales: [tile][step][row] f16 (32 bytes per step: the four lanes of
 //         a row read one scale, no duplication).
 //   U3    step = 128 columns, 768 bytes: lane (n,q) holds row n, 32-column
-//         chunk 4t+q as 8 bytes of the codes' low 2-bit fields (column k of
-//         the chunk at bits 2(k%16) of dword k/16) at 8*l, then, after all
-//         lanes, 4 bytes of their high bits (column k at bit k) at
-//         128*nq + 4*l, where nq = 4 column slots per step.  The last step
+//         chunk 4t+q as 12 bytes at 12*l: two dwords of the codes' low 2-bit
+//         fields (column k of the chunk at bits 2(k%16) of dword k/16), then a
+//         dword of their high bits (column k at bit k), one 12-byte load a
+//         lane; nq = 4 column slots per step.  The last step
 //         stores only the tail_q slots that hold columns (nq = tail_q), so a
 //         narrow factor (cols = 160) carries no padded slots; lanes of absent
 //         slots read slot 0's bytes (the x image is zero there).  Value
@@ -87,8 +87,9 @@ __device__ inline float tiled_weight(const OrganView& o, uint32_t r, uint32_t c)
         const uint32_t t = c >> 7, q = (c >> 5) & 3u, k = c & 31u, l = n + 16u * q;
         const uint32_t nq = t + 1 == o.steps ? o.tail_q : 4u;
         const uint8_t* base = o.data + (size_t)T * u3_tile_data(o.steps, o.tail_q) + 768u * t;
-        const uint32_t lo = *reinterpret_cast<const uint32_t*>(base + 8u * l + 4u * (k >> 4));
-        const uint32_t hi = *reinterpret_cast<const uint32_t*>(base + 128u * nq + 4u * l);
+        (void)nq;
+        const uint32_t lo = *reinterpret_cast<const uint32_t*>(base + 12u * l + 4u * (k >> 4));
+        const uint32_t hi = *reinterpret_cast<const uint32_t*>(base + 12u * l + 8u);
         const uint32_t code = ((lo >> (2u * (k & 15u))) & 3u) + 4u * ((hi >> k) & 1u);
         const float s = f16_bits_to_f32(o.scales[(size_t)T * u3_tile_scales(o.steps, o.tail_q) + 64u * t + l]);
         return (float)((int)code - 3) * s;
