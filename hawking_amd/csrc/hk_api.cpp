@@ -1428,7 +1428,7 @@ static int alloc_batch_ws(hk_ctx* ctx, hk_moe_model* m) {
         (size_t)S * T * E * 4,             // part
         (size_t)T * K * 4,                 // ids
         (size_t)T * K * 4,                 // w
-        (size_t)T * K * 4,                 // order
+        (size_t)T * K * 4,                 // rank
         ((size_t)E + 1) * 16,              // active
         4,                                 // n_active
         pairs * 4,                         // members
@@ -1452,7 +1452,7 @@ static int alloc_batch_ws(hk_ctx* ctx, hk_moe_model* m) {
     w.part = static_cast<float*>(ptr[2]);
     w.ids = static_cast<int32_t*>(ptr[3]);
     w.w = static_cast<float*>(ptr[4]);
-    w.order = static_cast<int32_t*>(ptr[5]);
+    w.rank = static_cast<int32_t*>(ptr[5]);
     w.active = static_cast<uint4*>(ptr[6]);
     w.n_active = static_cast<uint32_t*>(ptr[7]);
     w.members = static_cast<uint32_t*>(ptr[8]);

@@ -147,14 +147,15 @@ struct MoeBatchWs {
     float* part;         // [S x T x E] router partials
     int32_t* ids;        // [T x K] route order
     float* w;            // [T x K]
-    int32_t* order;      // [T x K] slots of each token in ascending expert id
+    int32_t* rank;       // [T x K] each routed pair's position among its token's slots in ascending expert id
     uint4* active;       // [E + 1]
     uint32_t* n_active;  // [1]
     uint32_t* members;   // [T*K + T] pair ids, grouped by active expert
     float* act;          // [pairs x Imax]
     uint8_t* aimg;       // [pairs] x images of the activations (stride aimg_stride)
     int32_t* aimg_e;     // [pairs]
-    float* ybuf;         // [pairs x H] weighted expert outputs
+    float* ybuf;         // [pairs x H] weighted expert outputs: token t's routed ones at rows t K + rank
+                         // (ascending expert id), the shared expert's at T K + t
     uint32_t ximg_stride, aimg_stride;
     uint32_t* status;
 };

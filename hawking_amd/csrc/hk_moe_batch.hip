@@ -360,12 +360,14 @@ __global__ void __launch_bounds__(1024) moe_batch_group_kernel(MoeBatchDims d, M
     }
     if (has_shared)
         for (uint32_t t = threadIdx.x; t < d.T; t += blockDim.x) ws.members[t] = np + t;
-    // each token's slots in ascending expert id (ids of a token are distinct)
+    // each routed pair's position among its token's slots in ascending
+    // expert id (ids of a token are distinct): the down kernel stores the
+    // pair's output there, so the combine reads a token's outputs in order
     for (uint32_t p = threadIdx.x; p < np; p += blockDim.x) {
-        const uint32_t t = p / K, r = p % K;
+        const uint32_t t = p / K;
         uint32_t rank = 0;
         for (uint32_t j = 0; j < K; ++j) rank += sids[t * K + j] < sids[p] ? 1u : 0u;
-        ws.order[t * K + rank] = (int32_t)r;
+        ws.rank[p] = (int32_t)rank;
     }
 }
 
@@ -651,12 +653,15 @@ moe_batch_down_kernel(MoeBatchDims d, const OrganView* __restrict__ table, MoeBa
             for (int j = 0; j < TB; ++j) {
                 if ((uint32_t)j >= nm) break;
                 const int E = ws.aimg_e[pair[j]];
-                const float w = pair[j] < np ? ws.w[pair[j]] : 1.0f;
+                const bool routed = pair[j] < np;
+                const float w = routed ? ws.w[pair[j]] : 1.0f;
+                // a routed pair's output goes to its token's row of its rank in expert order
+                const uint32_t dst = routed ? pair[j] - pair[j] % d.K + (uint32_t)ws.rank[pair[j]] : pair[j];
 #pragma unroll
                 for (int h = 0; h < TPW; ++h) {
                     const float y = ldexpf(tile_row_sum(acc[j][h]), -E);
                     const uint32_t row = (Tb + h) * 16u + (uint32_t)(lane & 15);
-                    if (lane < 16 && vw[h] && row < d.H) ws.ybuf[(size_t)pair[j] * d.H + row] = y * w;
+                    if (lane < 16 && vw[h] && row < d.H) ws.ybuf[(size_t)dst * d.H + row] = y * w;
                 }
             }
         }
@@ -673,7 +678,7 @@ __global__ void __launch_bounds__(256) moe_batch_combine_kernel(MoeBatchDims d, 
     float v[17];
 #pragma unroll
     for (uint32_t j = 0; j < 16; ++j)
-        v[j] = j < d.K ? ws.ybuf[(size_t)(t * d.K + (uint32_t)ws.order[t * d.K + j]) * d.H + row] : 0.0f;
+        v[j] = j < d.K ? ws.ybuf[(size_t)(t * d.K + j) * d.H + row] : 0.0f;  // in expert order (the down kernel's rows)
     v[16] = d.SI ? ws.ybuf[(size_t)(d.T * d.K + t) * d.H + row] : 0.0f;
     float acc = 0.0f;
 #pragma unroll
