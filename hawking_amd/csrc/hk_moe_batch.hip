@@ -234,7 +234,11 @@ constexpr uint32_t MOE_ROUTER_MAX_SPLITS = (8192 + MOE_BATCH_ROUTER_COLS - 1) / 
 // The block sums each expert's split-K partials (in split order, every load
 // of a thread in flight at once) and ranks by counting: an expert's rank is
 // the number of keys above its own (keys are distinct: value desc, index asc),
-// so every selection below is the order-exact top-n.
+// so every selection below is the order-exact top-n.  The final top k counts
+// among candidates only: experts ranked below k inside their 64-expert range
+// (any expert above a top-k expert is itself top-k, so its rank inside its
+// range is below k too, and a candidate's rank among candidates is its rank
+// among all experts whenever either is below k).
 __global__ void __launch_bounds__(256) moe_batch_route_kernel(MoeBatchDims d, const float* __restrict__ bias,
                                                               MoeBatchWs ws, int32_t* ids_out, float* w_out) {
     __shared__ uint64_t key[MOE_BATCH_MAX_EXPERTS];
@@ -242,10 +246,14 @@ __global__ void __launch_bounds__(256) moe_batch_route_kernel(MoeBatchDims d, co
     __shared__ float top2[64][2];
     __shared__ uint64_t gkey[64];
     __shared__ uint32_t chosen[64];
+    __shared__ uint64_t ckey[MOE_BATCH_MAX_EXPERTS];
+    __shared__ uint16_t cand[MOE_BATCH_MAX_EXPERTS];
+    __shared__ uint32_t ncand;
     __shared__ int32_t sel_i[16];
     __shared__ float sel_w[16];
     const uint32_t t = blockIdx.x, E = d.E, K = d.K, per = d.E / d.n_group, tid = threadIdx.x;
     uint32_t bad = 0;
+    if (tid == 0) ncand = 0;
     for (uint32_t e = tid; e < E; e += blockDim.x) {
         float pv[MOE_ROUTER_MAX_SPLITS];
 #pragma unroll
@@ -283,10 +291,20 @@ __global__ void __launch_bounds__(256) moe_batch_route_kernel(MoeBatchDims d, co
         __syncthreads();
     }
     for (uint32_t e = tid; e < E; e += blockDim.x) {
-        const uint32_t rk = keys_above(key, 0, E, key[e]);
+        const uint32_t lo = e & ~63u;
+        if (keys_above(key, lo, min(lo + 64u, E), key[e]) < K) {
+            const uint32_t c = atomicAdd(&ncand, 1u);
+            cand[c] = (uint16_t)e;
+            ckey[c] = key[e];
+        }
+    }
+    __syncthreads();
+    const uint32_t nc = ncand;
+    for (uint32_t c = tid; c < nc; c += blockDim.x) {
+        const uint32_t rk = keys_above(ckey, 0, nc, ckey[c]);
         if (rk < K) {
-            sel_i[rk] = (int32_t)e;
-            sel_w[rk] = sc[e];  // weights are the uncorrected scores
+            sel_i[rk] = (int32_t)cand[c];
+            sel_w[rk] = sc[cand[c]];  // weights are the uncorrected scores
         }
     }
     __syncthreads();
