@@ -76,15 +76,15 @@ static uint32_t q4_stage_floats(uint32_t cols) { return n_steps_for(HK_Q4, cols)
 // ceil(cols / 512) blocks, each computing E from all of x.
 constexpr uint32_t XPART_COLS = 512, XPART_STEPS = XPART_COLS / 128u;
 
-// Steps [tb, tb + XPART_STEPS) of the Q4 x image of xs (LDS, >=
+// Steps [tb, tb + ns) of the Q4 x image of xs (LDS, >=
 // q4_stage_floats(cols) floats, those columns quantized in place) into img
 // (global), by the whole block.
-__device__ int x_image_in_place(float* xs, uint32_t cols, uint8_t* img, float* red, bool* bad, uint32_t tb) {
+__device__ int x_image_in_place(float* xs, uint32_t cols, uint8_t* img, float* red, bool* bad, uint32_t tb,
+                                uint32_t ns = XPART_STEPS) {
     const uint32_t S = n_steps_for(HK_Q4, cols);
     XChunks<1> xc;
     load_x<1>(BlockTeam{}, xs, cols, xc);
-    return x_image<HK_Q4, 1>(BlockTeam{}, xc, xs, cols, S, img, xs + tb * 128u, 8u * blockDim.x, red, bad, tb,
-                             tb + XPART_STEPS);
+    return x_image<HK_Q4, 1>(BlockTeam{}, xc, xs, cols, S, img, xs + tb * 128u, 8u * blockDim.x, red, bad, tb, tb + ns);
 }
 
 // Token t's image part `part`; xs: LDS of q4_stage_floats(H) floats.
@@ -617,7 +617,8 @@ __global__ void __launch_bounds__(256) moe_batch_act_image_kernel(MoeBatchDims d
                      threadIdx.x, blockDim.x);
     __syncthreads();
     bool bad = false;
-    const int E = x_image_in_place(xs, cols, ws.aimg + (size_t)p * ws.aimg_stride, red, &bad, blockIdx.y * XPART_STEPS);
+    const uint32_t ns = (n_steps_for(HK_Q4, d.Imax) + gridDim.y - 1u) / gridDim.y;  // steps per part
+    const int E = x_image_in_place(xs, cols, ws.aimg + (size_t)p * ws.aimg_stride, red, &bad, blockIdx.y * ns, ns);
     if (threadIdx.x == 0) {
         if (blockIdx.y == 0) ws.aimg_e[p] = E;
         if (bad) atomicOr(ws.status, HK_DEVERR_NONFINITE);
@@ -771,7 +772,10 @@ hipError_t launch_moe_batch(const MoeBatchDims& d, const MoeLayerDev& L, const f
         hipLaunchKernelGGL((moe_batch_gate_up_kernel<2, GU_D, GU_TPW, GU_TPI>), ggu, bgu, (size_t)2 * ximg, s, d, L.table, ws);
     else
         hipLaunchKernelGGL((moe_batch_gate_up_kernel<1, GU_D, GU_TPW, GU_TPI>), ggu, bgu, (size_t)ximg, s, d, L.table, ws);
-    hipLaunchKernelGGL(moe_batch_act_image_kernel, dim3(pairs, (d.Imax + XPART_COLS - 1) / XPART_COLS), dim3(256),
+#ifndef HK_BATCH_AIMG_COLS
+#define HK_BATCH_AIMG_COLS 2048  // activation image columns per block (512: +0.4 us; build-time override)
+#endif
+    hipLaunchKernelGGL(moe_batch_act_image_kernel, dim3(pairs, (d.Imax + HK_BATCH_AIMG_COLS - 1) / HK_BATCH_AIMG_COLS), dim3(256),
                        (size_t)q4_stage_floats(d.Imax) * sizeof(float), s, d, ws);
     if (tb_dn >= 4)
         hipLaunchKernelGGL((moe_batch_down_kernel<4, DN_D, DN_TPW, DN_TPI>), gdn, bdn, (size_t)4 * aimg, s, d, L.table, ws);
