@@ -228,7 +228,7 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             P.at(min((uint32_t)d, last), T[d], R, &nv[d], &ts[d]);
-            fetch_step<KIND, R>(o, T[d], nv[d], ts[d], lane, f[d]);
+            fetch_step<KIND, R, !HEAD>(o, T[d], nv[d], ts[d], lane, f[d]);
         }
     }
     if constexpr (KIND == HK_MIXED) {
@@ -303,7 +303,7 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const
                     fetch_mixed<R>(o, hsh[(Tr - t0) * o.steps + ts[d]], lane, f[d], r);
                 }
             } else {
-                fetch_step<KIND, R>(o, T[d], nv[d], ts[d], lane, f[d]);
+                fetch_step<KIND, R, !HEAD>(o, T[d], nv[d], ts[d], lane, f[d]);
             }
         }
     }
@@ -619,15 +619,32 @@ static hipError_t launch_kind(const OrganView* organs, uint32_t n, const OrganVi
 
 // Launch shape (R tiles per wave group, D steps in flight, tiles per
 // workgroup) by kind and size, from sweeps over the streamed workloads:
-// binary 4-tile groups over 16 tiles when the organ has >= 4 steps, else
-// 2-tile groups 5 deep over 32; Q4 and Q8 2 over 32; 3-bit factors 2 over 16,
-// or over 128 when narrow; mixed (large fragments) 1 over 16 (1 over 32 and
-// 1 over 64 measured 1.3 % slower on 6,144 organs of 512 x 2048).
+// binary 2-tile groups 5 deep, over 16 tiles when the organ has >= 4 steps
+// (also with the fused residual), else over 32; Q4 and Q8 2 over 32, 3 deep;
+// 3-bit factors 2 over 16, or over 128 when narrow; mixed (large fragments)
+// 1 over 16 (1 over 32 and 1 over 64 measured 1.3 % slower on 6,144 organs of
+// 512 x 2048).  With the weights' non-temporal loads (fetch_one) the wide
+// binary shape moved from 4-tile groups 3 deep (0.73 of 8 TB/s with the hint,
+// 0.756 without) to 2-tile groups 5 deep (0.78-0.80; 4 deep 0.70, 6 deep
+// 0.71, 4-tile groups 4 deep 0.56), and the fused residual's with it (0.69
+// -> 0.73).
 // (build-time overrides for launch-shape sweeps)
 #ifndef HK_BIN_NARROW_R
 #define HK_BIN_NARROW_R 2
 #define HK_BIN_NARROW_D 5
 #define HK_BIN_NARROW_TPW 32
+#endif
+#ifndef HK_BIN_WIDE_R
+#define HK_BIN_WIDE_R 2
+#define HK_BIN_WIDE_D 5
+#endif
+#ifndef HK_Q_R
+#define HK_Q_R 2
+#define HK_Q_D 3
+#endif
+#ifndef HK_RES_R
+#define HK_RES_R 2
+#define HK_RES_D 5
 #endif
 #ifndef HK_BIN_WIDE_TPW
 #define HK_BIN_WIDE_TPW 16
@@ -651,12 +668,13 @@ static hipError_t launch_r(const OrganView* organs, uint32_t n, const OrganView&
     const uint64_t tiles = (uint64_t)n * sh.n_tiles;
     if (tiles >= 16384) {
         if constexpr (KIND == HK_BIN) {
-            if (sh.steps >= 4) return launch_kind<KIND, 4, 3>(organs, n, sh, x, xs, y, ys, HK_BIN_WIDE_TPW, s);
+            if (sh.steps >= 4)
+                return launch_kind<KIND, HK_BIN_WIDE_R, HK_BIN_WIDE_D>(organs, n, sh, x, xs, y, ys, HK_BIN_WIDE_TPW, s);
             return launch_kind<KIND, HK_BIN_NARROW_R, HK_BIN_NARROW_D>(organs, n, sh, x, xs, y, ys, HK_BIN_NARROW_TPW, s);
         } else if constexpr (KIND == HK_U3) {
             return launch_kind<KIND, 2, 3>(organs, n, sh, x, xs, y, ys, gemv_max_tiles(KIND, sh.steps) == 128u ? 128 : 16, s);
         } else if constexpr (KIND == HK_Q4 || KIND == HK_Q8) {
-            return launch_kind<KIND, 2, 3>(organs, n, sh, x, xs, y, ys, HK_Q_TPW, s);
+            return launch_kind<KIND, HK_Q_R, HK_Q_D>(organs, n, sh, x, xs, y, ys, HK_Q_TPW, s);
         } else {
             return launch_kind<KIND, HK_MIX_R, HK_MIX_D>(organs, n, sh, x, xs, y, ys, HK_MIX_TPW, s);
         }
@@ -724,7 +742,9 @@ hipError_t launch_gemv_rice(const OrganView* organs_dev, const ResView* res_dev,
         return hipSuccess;
     const ResArgs ra{res_dev, pieces};
     *fused = true;
-    if (wide) return launch_kind<HK_BIN, 4, 3, false, true>(organs_dev, n, sh, x, x_stride, y, y_stride, tpw, s, {}, nullptr, ra);
+    if (wide)
+        return launch_kind<HK_BIN, HK_RES_R, HK_RES_D, false, true>(organs_dev, n, sh, x, x_stride, y, y_stride, tpw, s, {},
+                                                                   nullptr, ra);
     return launch_kind<HK_BIN, HK_BIN_NARROW_R, HK_BIN_NARROW_D, false, true>(organs_dev, n, sh, x, x_stride, y,
                                                                               y_stride, tpw, s, {}, nullptr, ra);
 }

