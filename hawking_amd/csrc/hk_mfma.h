@@ -647,8 +647,9 @@ __device__ __forceinline__ void fetch_mixed(const OrganView& o, const uint4& h, 
 // 0.78; the hint on the 2-byte scale loads, on the mixed kind's loads (its
 // binary lanes re-read their 16 bytes) or on the 3-bit kind's measured
 // slower, and so did the terminal head's q8 launch (its kernel runs NT =
-// false).
-template <int KIND, int R, bool NT = true>
+// false).  The default is off: the batch-1 MoE decode kernels, bound by
+// their latency chains, ran 1-2 % faster with ordinary loads.
+template <int KIND, int R, bool NT = false>
 __device__ __forceinline__ void fetch_one(const OrganView& o, uint32_t T, uint32_t t, int lane, Frag<KIND, R>& f,
                                           int r) {
     // offsets in 32 bits (an organ's tiled sections are below 4 GiB, checked
@@ -683,7 +684,7 @@ __device__ __forceinline__ void fetch_one(const OrganView& o, uint32_t T, uint32
 }
 
 // Issue the loads of step t for tiles T[0..R-1] (tiles r >= nvalid alias T[0]).
-template <int KIND, int R, bool NT = true>
+template <int KIND, int R, bool NT = false>
 __device__ __forceinline__ void fetch_step(const OrganView& o, const uint32_t* T, int nvalid, uint32_t t, int lane,
                                            Frag<KIND, R>& f) {
 #pragma unroll
