@@ -391,14 +391,30 @@ __global__ void __launch_bounds__(1024) moe_batch_group_kernel(MoeBatchDims d, M
 
 // ------------------------------------------------------------------ grouped tile worker
 
-// Step t of weight tiles r < R (tile r of organ r's data/scales) into fr.
+#ifndef HK_BATCH_NT
+#define HK_BATCH_NT 1
+#endif
+// Where the weight pipelines' fetches past an item's last step go (they stay
+// unconditional): a re-read of the last step under the non-temporal hint
+// would come from HBM again; this buffer stays in the caches.  Nothing
+// fetched from it is consumed.
+__device__ __align__(256) uint8_t g_batch_refetch_dummy[2048];
+
+// Step t of weight tiles r < R (tile r of organ r's data/scales, the lane's
+// 16 data bytes at base_d[r] + 1024 t) into fr; past: the same loads from the
+// refetch buffer.  The data loads carry the non-temporal hint (HK_BATCH_NT).
 template <int R>
 __device__ __forceinline__ void tiles_fetch(const uint8_t* const* base_d, const uint16_t* const* base_s, uint32_t t,
-                                            Frag<HK_Q4, R>& fr) {
+                                            Frag<HK_Q4, R>& fr, bool past = false) {
+    const uint32_t lane = threadIdx.x & 63u;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        fr.v[r] = ldg(reinterpret_cast<const uint4*>(base_d[r] + (size_t)t * 1024u));
-        fr.s[r] = ldg(base_s[r] + (size_t)t * 64u);
+        const uint4* pd = past ? reinterpret_cast<const uint4*>(g_batch_refetch_dummy + 16u * lane)
+                               : reinterpret_cast<const uint4*>(base_d[r] + (size_t)t * 1024u);
+        const uint16_t* ps = past ? reinterpret_cast<const uint16_t*>(g_batch_refetch_dummy + 1024u) + lane
+                                  : base_s[r] + (size_t)t * 64u;
+        fr.v[r] = HK_BATCH_NT ? ldg_nt(pd) : ldg(pd);
+        fr.s[r] = ldg(ps);
     }
 }
 
@@ -409,7 +425,7 @@ template <int R, int D>
 __device__ __forceinline__ void tiles_fetch_first(const uint8_t* const* base_d, const uint16_t* const* base_s,
                                                   uint32_t S, Frag<HK_Q4, R> (&f)[D]) {
 #pragma unroll
-    for (int k = 0; k < D; ++k) tiles_fetch<R>(base_d, base_s, min((uint32_t)k, S - 1u), f[k]);
+    for (int k = 0; k < D; ++k) tiles_fetch<R>(base_d, base_s, min((uint32_t)k, S - 1u), f[k], (uint32_t)k >= S);
 }
 
 // acc[j][r] += this lane's partial dot of weight tile r (tile Tr[r] of organ
@@ -420,7 +436,7 @@ template <int R, int TB, int D>
 __device__ __forceinline__ void tiles_x_tokens(const uint8_t* const* base_d, const uint16_t* const* base_s, uint32_t S,
                                                const uint8_t* img, uint32_t img_bytes, uint32_t nm, uint32_t aoff,
                                                int q, float (*acc)[R], Frag<HK_Q4, R> (&f)[D]) {
-    auto fetch = [&](uint32_t t, Frag<HK_Q4, R>& fr) { tiles_fetch<R>(base_d, base_s, t, fr); };
+    auto fetch = [&](uint32_t t, Frag<HK_Q4, R>& fr, bool past) { tiles_fetch<R>(base_d, base_s, t, fr, past); };
     const float* SX0 = reinterpret_cast<const float*>(img + (size_t)S * 2u * A_TILE_STRIDE);
     auto consume = [&](const Frag<HK_Q4, R>& fr, uint32_t t) {
         v4i alo[TB], ahi[TB];
@@ -459,7 +475,7 @@ __device__ __forceinline__ void tiles_x_tokens(const uint8_t* const* base_d, con
 #pragma unroll
         for (int k = 0; k < D; ++k) {
             consume(f[k], it + (uint32_t)k);
-            fetch(min(it + D + (uint32_t)k, last), f[k]);
+            fetch(min(it + D + (uint32_t)k, last), f[k], it + D + (uint32_t)k > last);
         }
     }
 #pragma unroll
