@@ -22,7 +22,9 @@ thread, timed on this host; "extra.cpu_baselines" times the oracle on the
 other configs the same way (c1 Q4 organ, c3 layer, c4 token from a sample of
 layers, c5 block from a sample of tokens) and the c2 organ on every host
 thread.  `--only NAME` runs one workload and prints its result (for
-profiler runs).
+profiler runs).  The headline and the decode tokens also carry per-call
+distributions (median, p10, p90 of 100 calls, each between its own pair of
+HIP events).
 
 roofline.traffic (HBM bytes per headline launch) is measured in the run:
 after the timed work, two child rocprofv3 --pmc passes (FETCH_SIZE, then
@@ -108,6 +110,24 @@ def time_launches(ctx, fn, steps: int, warmup: int, ramp_s: float | None = None)
     e1.record()
     ctx.synchronize()
     return e0.elapsed_ms(e1) / steps
+
+
+def launch_distribution(ctx, fn, reps: int = 100, warmup: int = 5) -> dict:
+    """Per-call times of `reps` back-to-back calls of fn(), each between its
+    own pair of HIP events on ctx.stream (one event between consecutive
+    calls): median, p10 and p90 in ms."""
+    for _ in range(warmup):
+        fn()
+    ev = [ctx.event() for _ in range(reps + 1)]
+    ctx.synchronize()
+    ev[0].record()
+    for i in range(reps):
+        fn()
+        ev[i + 1].record()
+    ctx.synchronize()
+    t = np.array([ev[i].elapsed_ms(ev[i + 1]) for i in range(reps)])
+    return {"reps": reps, "median_ms": round(float(np.median(t)), 5), "p10_ms": round(float(np.percentile(t, 10)), 5),
+            "p90_ms": round(float(np.percentile(t, 90)), 5)}
 
 
 def streamed(ctx, name, steps, warmup, n_organs=None):
@@ -198,6 +218,7 @@ def moe15_bench(ctx, steps, warmup, n_layers=48, H=2048, I=512, SI=512, E=512, K
     ctx.device_status()
     ms = time_launches(ctx, step, steps, warmup)
     status = ctx.device_status()
+    dist = launch_distribution(ctx, step, 100)
     routes = ids.download()
     per_tok = [sum(dense_bytes[l] + 2 * H * 4 + sum(expert_bytes[l][int(e)] for e in routes[t, l])
                    for l in range(n_layers)) for t in range(n_inputs)]
@@ -205,7 +226,9 @@ def moe15_bench(ctx, steps, warmup, n_layers=48, H=2048, I=512, SI=512, E=512, K
     return {"us_per_token": round(ms * 1e3, 2), "bytes_per_token": round(tok_bytes),
             "gbps": round(tok_bytes / (ms * 1e-3) / 1e9, 1), "tokens_per_s": round(1e3 / ms, 1),
             "launches_per_layer": 4, "layers": n_layers, "device_status": status,
-            "distinct_routes": int(np.unique(routes.reshape(-1, K), axis=0).shape[0]), "gen_seconds": round(gen_s, 2)}
+            "distinct_routes": int(np.unique(routes.reshape(-1, K), axis=0).shape[0]), "gen_seconds": round(gen_s, 2),
+            "per_call_us": {"median": round(dist["median_ms"] * 1e3, 2), "p10": round(dist["p10_ms"] * 1e3, 2),
+                            "p90": round(dist["p90_ms"] * 1e3, 2), "reps": dist["reps"]}}
 
 
 MALL_BYTES = 256 << 20  # MI355X Infinity Cache
@@ -274,6 +297,7 @@ def moe_bench(ctx, shape, steps, warmup, n_inputs=16):
         m.decode_stack_device(hs.offset(i * H), out, ids.offset(i * L * K), None)
 
     ms = time_launches(ctx, step, steps, warmup)
+    dist = launch_distribution(ctx, step, 100)
     # algorithmic bytes per token from the routes actually taken
     routes = ids.download()
     dev_bytes, dense_per_layer = m.model_bytes()
@@ -289,7 +313,9 @@ def moe_bench(ctx, shape, steps, warmup, n_inputs=16):
         per_tok.append(b)
     tok_bytes = float(np.mean(per_tok))
     return {"us_per_token": ms * 1e3, "bytes_per_token": tok_bytes, "gbps": tok_bytes / (ms * 1e-3) / 1e9,
-            "model_device_bytes": dev_bytes, "gen_seconds": round(gen_s, 2), "layers": L}
+            "model_device_bytes": dev_bytes, "gen_seconds": round(gen_s, 2), "layers": L,
+            "per_call_us": {"median": round(dist["median_ms"] * 1e3, 2), "p10": round(dist["p10_ms"] * 1e3, 2),
+                            "p90": round(dist["p90_ms"] * 1e3, 2), "reps": dist["reps"]}}
 
 
 def moe_layer_cold_bench(ctx, steps, warmup, n_layers=16, n_inputs=16):
@@ -712,6 +738,9 @@ def main():
     extra = {}
     rel = None
     if not args.only_main:
+        _, _, hrows, hcols, _ = WORKLOADS[main_name]
+        extra["headline_launch_distribution"] = launch_distribution(ctx, lambda: oset.gemv(x, hcols, y, hrows), 100)
+        log("headline per-launch", extra["headline_launch_distribution"])
         rel = spot_check(ctx, oset, x, y)
         log("spot-check rel_l2", rel)
         del oset, x, y
