@@ -11,9 +11,9 @@ the W warmup steps, then exactly K timed steps between HIP events.
 Also reported (the same JSON line, "extra"): Q4 (config 1), mixed, q8,
 HGRAVS01 low-rank and HGRAVR02 streamed GB/s, the binary down shape
 (2048x512), the terminal head, single-organ latency, the config-3 MoE layer,
-the config-4 48-layer mixed token and the mixed-1p5-v1 48-layer token (the
-reference's own codec triplet) in microseconds at batch 1, and the config-5
-batched block.
+the config-4 48-layer mixed token (per-layer launches, and as one persistent
+launch) and the mixed-1p5-v1 48-layer token (the reference's own codec
+triplet) in microseconds at batch 1, and the config-5 batched block.
 
 The CPU baseline is the oracle's serial restatement of
 binary_group_matvec_f32 (crates/hawking-core/src/model/qwen_complete_binary/
@@ -274,14 +274,20 @@ def single_organ_us(ctx, steps=200):
     return time_launches(ctx, lambda: o.matvec_device(x, y), steps, 20) * 1e3
 
 
-def moe_bench(ctx, shape, steps, warmup, n_inputs=16):
+def moe_bench(ctx, shape, steps, warmup, n_inputs=16, persistent=False):
     """Decode `steps` tokens cycling over n_inputs distinct hidden vectors
-    (distinct routings, so the MALL does not serve repeated experts)."""
+    (distinct routings, so the MALL does not serve repeated experts).
+    persistent: the token as one persistent launch (HK_STACK_PERSISTENT)
+    instead of the per-layer launches."""
     from hawking_amd.moe import MoeModel
     from hawking_amd.organs import stream_key
     t0 = time.time()
     m = MoeModel(ctx, shape)
     m.fill_synthetic(SEED)
+    if persistent:
+        m.set_stack_launch(1)
+        if not m.stack_is_persistent():
+            raise RuntimeError("the persistent launch is not admitted for this shape")
     ctx.synchronize()
     gen_s = time.time() - t0
     H, L, K = shape.hidden, shape.n_layers, shape.top_k
@@ -712,6 +718,8 @@ def main():
                                               "all within the 256 MB Infinity Cache)"),
         "moe_layer_c3_q4_cold": lambda: moe_layer_cold_bench(ctx, tok_steps, args.warmup),
         "moe_token_c4_mixed": lambda: token_cache_label(rounded(moe_bench(ctx, c4, tok_steps, args.warmup))),
+        "moe_token_c4_mixed_persistent": lambda: token_cache_label(
+            rounded(moe_bench(ctx, c4, tok_steps, args.warmup, persistent=True))),
         "moe15_token_c4_mixed_1p5_v1": lambda: token_cache_label(
             moe15_bench(ctx, tok_steps, args.warmup, n_layers=args.moe_layers)),
         "moe_batch_c5_dsv3": lambda: rounded(moe_batch_bench(ctx, max(args.steps, 10), args.warmup), 4),
