@@ -366,7 +366,6 @@ def _pmc_pass(counter: str, timeout_s: float):
     (--only-main, no ramp, 1 warm-up and 3 timed launches, after a 512 MiB
     device copy): the mean KiB per headline dispatch of `counter` and the KiB
     the copy read (FETCH_SIZE) or wrote (WRITE_SIZE).  Raises on failure."""
-    import csv
     import glob
     import shutil
     import signal
@@ -392,22 +391,31 @@ def _pmc_pass(counter: str, timeout_s: float):
         files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
         if not files:
             raise RuntimeError(f"{counter} pass wrote no counter file (exit {rc})")
-        per_dispatch = {}
-        for fn in files:
-            with open(fn, newline="") as f:
-                for row in csv.DictReader(f):
-                    if row.get("Counter_Name") != counter:
-                        continue
-                    key = (fn, row.get("Dispatch_Id"))
-                    name, v = per_dispatch.get(key, (row.get("Kernel_Name", ""), 0.0))
-                    per_dispatch[key] = (name, v + float(row["Counter_Value"]))
-        gemv = [v for name, v in per_dispatch.values() if "gemv_tiled_kernel" in name]
-        copies = [v for name, v in per_dispatch.values() if "copy" in name.lower()]
-        if len(gemv) < 3 or not copies:
-            raise RuntimeError(f"{counter} pass: {len(gemv)} headline and {len(copies)} copy dispatches (exit {rc})")
-        return sum(gemv) / len(gemv), max(copies)
+        return pmc_headline_and_copy(files, counter, f"exit {rc}")
     finally:
         shutil.rmtree(d, ignore_errors=True)
+
+
+def pmc_headline_and_copy(files, counter: str, note: str = ""):
+    """From rocprofv3 counter-collection CSV files: `counter` summed over its
+    dimensions per dispatch, then the mean over the headline GEMV's
+    dispatches (gemv_tiled_kernel, at least 3) and the largest copy
+    dispatch (the calibration copy).  Raises if either is missing."""
+    import csv
+    per_dispatch = {}
+    for fn in files:
+        with open(fn, newline="") as f:
+            for row in csv.DictReader(f):
+                if row.get("Counter_Name") != counter:
+                    continue
+                key = (fn, row.get("Dispatch_Id"))
+                name, v = per_dispatch.get(key, (row.get("Kernel_Name", ""), 0.0))
+                per_dispatch[key] = (name, v + float(row["Counter_Value"]))
+    gemv = [v for name, v in per_dispatch.values() if "gemv_tiled_kernel" in name]
+    copies = [v for name, v in per_dispatch.values() if "copy" in name.lower()]
+    if len(gemv) < 3 or not copies:
+        raise RuntimeError(f"{counter} pass: {len(gemv)} headline and {len(copies)} copy dispatches ({note})")
+    return sum(gemv) / len(gemv), max(copies)
 
 
 def live_traffic(timeout_s: float = 240.0):
