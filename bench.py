@@ -57,7 +57,7 @@ WORKLOADS = {
     "binary_512x2048": (HK_BIN, 128, 512, 2048, 8192),
     "binary_2048x512": (HK_BIN, 128, 2048, 512, 8192),
     "q4g32_512x2048": (HK_Q4, 32, 512, 2048, 2048),
-    "mixed_512x2048": (HK_MIXED, 128, 512, 2048, 6144),
+    "mixed_512x2048": (HK_MIXED, 128, 512, 2048, 8192),
     "q8g64_512x2048": (HK_Q8, 64, 512, 2048, 1024),
     "binary_rice_512x2048": (HK_BIN_RICE, 128, 512, 2048, 4096),
 }
