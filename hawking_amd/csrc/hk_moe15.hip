@@ -107,25 +107,32 @@ __device__ __forceinline__ float dot4(const float4& a, const float4& b) {
 // (8 columns each, k < M15_NC; hidden <= 8 * 256 * M15_NC).  h and w are
 // loaded once, unconditionally (index clamped, value dropped past H), so
 // every load is in flight before the block's one reduction.  Every thread
-// of the 256-thread block calls this.
+// of the 256-thread block calls this (xn_load, then xn_finish; a block
+// with weights to fetch issues them between the two, after h and w: vector
+// loads retire in issue order, so the norm then waits for h and w only).
 constexpr int M15_NC = 4;
 struct XnRegs {
     float4 v[M15_NC][2];
 };
-__device__ __forceinline__ void block_xn(const float* __restrict__ h, const float* __restrict__ w, uint32_t H,
-                                         float eps, float* red, XnRegs& x) {
+struct XnW {
+    float4 v[M15_NC][2];
+};
+__device__ __forceinline__ void xn_load(const float* __restrict__ h, const float* __restrict__ w, uint32_t H,
+                                        XnRegs& x, XnW& wv) {
     const uint32_t nch = H / 8u;
     const float4* h4 = reinterpret_cast<const float4*>(h);
     const float4* w4 = reinterpret_cast<const float4*>(w);
-    float4 wv[M15_NC][2];
 #pragma unroll
     for (int k = 0; k < M15_NC; ++k) {
         const uint32_t ch = min(threadIdx.x + 256u * (uint32_t)k, nch - 1u);
         x.v[k][0] = ldg(h4 + 2u * ch);
         x.v[k][1] = ldg(h4 + 2u * ch + 1u);
-        wv[k][0] = ldg(w4 + 2u * ch);
-        wv[k][1] = ldg(w4 + 2u * ch + 1u);
+        wv.v[k][0] = ldg(w4 + 2u * ch);
+        wv.v[k][1] = ldg(w4 + 2u * ch + 1u);
     }
+}
+__device__ __forceinline__ void xn_finish(uint32_t H, float eps, float* red, XnRegs& x, const XnW& wv) {
+    const uint32_t nch = H / 8u;
     float ss = 0.0f;
 #pragma unroll
     for (int k = 0; k < M15_NC; ++k)
@@ -135,10 +142,16 @@ __device__ __forceinline__ void block_xn(const float* __restrict__ h, const floa
     for (int k = 0; k < M15_NC; ++k)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const float4 v = x.v[k][j], g = wv[k][j];
+            const float4 v = x.v[k][j], g = wv.v[k][j];
             x.v[k][j] = make_float4(v.x * inv * (1.0f + g.x), v.y * inv * (1.0f + g.y), v.z * inv * (1.0f + g.z),
                                     v.w * inv * (1.0f + g.w));
         }
+}
+__device__ __forceinline__ void block_xn(const float* __restrict__ h, const float* __restrict__ w, uint32_t H,
+                                         float eps, float* red, XnRegs& x) {
+    XnW wv;
+    xn_load(h, w, H, x, wv);
+    xn_finish(H, eps, red, x, wv);
 }
 
 // The first D steps of [s0, s0 + n) of tile T of organs o[0..R-1].
@@ -208,8 +221,9 @@ __device__ __forceinline__ void wave_share(uint32_t S, uint32_t wave, uint32_t& 
 // the weights' first D steps per wave (a wave's whole share at H = 2048;
 // every route block runs one organ: router, shared gate, or one of the
 // shared expert's gate and up projections) are in flight while xn is formed
-// in registers and each thread scatters its chunks of the q8 x image (E = 0:
-// one exponent per 16-column unit, no block-wide maximum) into LDS.
+// in registers (h and w issued before the weights) and each thread scatters
+// its chunks of the q8 x image (E = 0: one exponent per 16-column unit, no
+// block-wide maximum) into LDS.
 template <int R, int D = 8 / R>
 __device__ __forceinline__ void q8_tile(const M15Dims& d, const M15Dev& L, const float* h, const OrganView (&o)[R],
                                         uint32_t T, uint8_t* lds, float* red, float* part, uint32_t* status,
@@ -219,13 +233,15 @@ __device__ __forceinline__ void q8_tile(const M15Dims& d, const M15Dev& L, const
     const uint32_t S = n_steps_for(HK_Q8, d.H), nch = d.H / 8u;
     uint32_t s0, n;
     wave_share(S, wave, s0, n);
+    XnRegs x;
+    XnW wv;
+    xn_load(h, L.norm_w, d.H, x, wv);
     Frag<HK_Q8, R> f[D];
     fetch_first<HK_Q8, R, D>(o, T, s0, n, lane, f);
     uint8_t* img = lds;
     float* sx = reinterpret_cast<float*>(img + (size_t)S * Kcfg<HK_Q8>::P * A_TILE_STRIDE);
     if (threadIdx.x < 64u) image_zero_blocks<HK_Q8>(threadIdx.x, img, S);
-    XnRegs x;
-    block_xn(h, L.norm_w, d.H, d.eps, red, x);
+    xn_finish(d.H, d.eps, red, x, wv);
     bool bad = false;
 #pragma unroll
     for (int k = 0; k < M15_NC; ++k) {
