@@ -122,9 +122,13 @@ __device__ __forceinline__ float block_sum_f(float v, float* red) {
 // xn = h * (1 / sqrt(mean(h^2) + eps)) * (1 + w) on this thread's register
 // chunks of h (source_qwen80_residual_rms_norm,
 // model/qwen80_complete_runtime.rs:6778-6797); every chunk of h must be in
-// registers (cols <= 8 * 256 * NC).
+// registers (cols <= 8 * 256 * NC), and gw holds the same chunks of w
+// (loaded with h, before the first weight steps: vector loads retire in
+// issue order, so a w load issued after them would hold the norm until the
+// weights land).
 template <int NC>
-__device__ __forceinline__ void head_norm_chunks(XChunks<NC>& xc, uint32_t cols, const HeadArgs& ha, float* red) {
+__device__ __forceinline__ void head_norm_chunks(XChunks<NC>& xc, const XChunks<NC>& gw, uint32_t cols,
+                                                 const HeadArgs& ha, float* red) {
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < NC; ++j)
@@ -141,7 +145,7 @@ __device__ __forceinline__ void head_norm_chunks(XChunks<NC>& xc, uint32_t cols,
         if (c0 < cols) {
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
-                const float4 g = ldg(reinterpret_cast<const float4*>(ha.norm_w + c0) + k);
+                const float4 g = gw.v[j][k];
                 float4& v = xc.v[j][k];
                 v = make_float4(v.x * inv * (1.0f + g.x), v.y * inv * (1.0f + g.y), v.z * inv * (1.0f + g.z),
                                 v.w * inv * (1.0f + g.w));
@@ -225,10 +229,13 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const
     W.n = W.g0 < t1 ? ((t1 - W.g0 + W.gstride - 1) / W.gstride) * o.steps : 0;
     const uint32_t last = W.n ? W.n - 1u : 0u;
 
-    // x first, then (mixed) this workgroup's step headers, then the first D
-    // steps' weight loads, all before the image build
+    // x (and for HEAD the norm weight) first, then (mixed) this workgroup's
+    // step headers, then the first D steps' weight loads, all before the
+    // image build
     XChunks<NC> xc;
     load_x<NC>(BlockTeam{}, x, o.cols, xc);
+    XChunks<HEAD ? NC : 1> gw;  // HEAD: the norm weight's chunks, with x
+    if constexpr (HEAD) load_x<NC>(BlockTeam{}, ha.norm_w, o.cols, gw);
     const uint32_t nh = (t1 - t0) * o.steps;
     uint4 hreg[GEMV_HDR_PER_THREAD];
     uint4* hsh = reinterpret_cast<uint4*>(lds + gemv_hdr_offset<KIND>(o.steps));
@@ -276,7 +283,7 @@ gemv_tiled_kernel(const OrganView* __restrict__ organs, uint32_t n_organs, const
             my1[h] = ldg(rv.row_ptr8 + min(row + 1u, r1));
         }
     }
-    if constexpr (HEAD) head_norm_chunks<NC>(xc, o.cols, ha, red);
+    if constexpr (HEAD) head_norm_chunks<NC>(xc, gw, o.cols, ha, red);
     // the x image with E = 0: every thread scatters its own chunks (no
     // block-wide maximum, no gather pass); a unit's chunks are consecutive
     // threads, active together
